@@ -1,0 +1,233 @@
+/*
+ * q8mi.h -- C-ABI of the MI355X-native Q8_0 matmul path (libq8mi.so).
+ *
+ * This is the drop-in boundary for the reference engine's matmul hot path.
+ * It replaces the libcuda driver FFI (apps/engine/src/cuda/sys.rs:54-137) and
+ * the matmul methods of the CUDA device runtime `Gpu`
+ * (apps/engine/src/cuda/mod.rs), which `Compute` (apps/engine/src/compute.rs)
+ * calls.  Every entry point below names the reference interface it stands in
+ * for; a Rust binding is a line-for-line `extern "C"` block over this header.
+ *
+ * Conventions (kept from the reference):
+ *  - Status codes: 0 is success (sys.rs:49 `SUCCESS`); non-zero is one of
+ *    Q8_ERR_*, and q8_last_error() holds the message the reference would have
+ *    put in `EngineError::Unsupported("cuda: <op> failed: <msg>")`
+ *    (cuda/mod.rs:2107-2115) -- here "hip: <op> failed: <msg>".
+ *  - Shape violations the reference `assert!`s (cuda/mod.rs:817-822,
+ *    1490-1500, 1562-1569) return Q8_ERR_INVALID instead of aborting, since a
+ *    panic cannot cross a C-ABI.  Nothing is launched in that case.
+ *  - Offsets (`x_offset`, `y_offset`, `bias_offset`) are in f32 elements, as
+ *    `shifted()` takes them (cuda/mod.rs:2092-2094).
+ *  - Device pointers are plain 64-bit integers (`DevicePtr`, sys.rs:44-47).
+ *  - One context owns one HIP stream; every launch and copy is ordered on it
+ *    (cuda/mod.rs:372-404).  Launches are asynchronous; q8_download and
+ *    q8_sync wait.  A context may be shared between threads: calls are
+ *    serialized by a mutex, as the reference's `Gpu` is `Send + Sync` over one
+ *    stream (cuda/mod.rs:1975-1979).
+ *  - The activations-and-weights data type is f32 in / f32 out, Q8_0 weights.
+ *
+ * Numerics (the reference CPU kernels are the oracle, apps/engine/src/quant.rs):
+ *  - n == 1: f32 activations, no quantization (tensor.rs:96-101).  Each block
+ *    is evaluated in the AVX2 order of dot_q8_0 (quant.rs:54-78); with option
+ *    "gemv.exact" = 1 (the default) the cross-block sum is also left-to-right,
+ *    so y is bit-identical to the reference's AVX2 path.
+ *  - n >= 2: activations are quantized to Q8_0 exactly as quantize_q8_0 does
+ *    (round half away from zero, saturating), then int8 x int8 per 32-block
+ *    on v_mfma_i32_32x32x32_i8 (exact int32), f32 scale d_w*s_x per block.
+ *    This follows the CPU semantics for every n >= 2 (tensor.rs:104-148), not
+ *    the reference GPU's f32 path for 2 <= n <= 7 (cuda/mod.rs:883-891).
+ */
+#ifndef Q8MI_H
+#define Q8MI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    Q8_OK = 0,
+    Q8_ERR_HIP = 1,           /* a HIP call failed */
+    Q8_ERR_INVALID = 2,       /* argument or shape error (the reference asserts) */
+    Q8_ERR_UNSUPPORTED = 3,   /* EngineError::Unsupported (e.g. n above the prompt limit) */
+    Q8_ERR_NO_DEVICE = 4,     /* no gfx950 device / code object does not load */
+    Q8_ERR_OUT_OF_MEMORY = 5, /* device allocation failed */
+};
+
+/* Largest prompt one matmul takes: MMA_TOKENS (cuda/mod.rs:115). */
+#define Q8_MAX_TOKENS 1024
+/* Matrices one grouped launch carries: MMA_GROUP_MAX (cuda/mod.rs:63). */
+#define Q8_GROUP_MAX_MEMBERS 4
+
+typedef uint64_t q8_dptr;
+typedef struct q8_ctx q8_ctx;
+typedef struct q8_weight q8_weight;
+
+/* Activations already quantized on the device: the reference's `Prepared`
+ * (cuda/mod.rs:119), a non-owning view into the context's activation
+ * workspace, valid until a later prepare needs a larger workspace. */
+typedef struct {
+    q8_dptr quants;
+    q8_dptr scales;
+    int n;
+    int k;
+} q8_prepared;
+
+/* One member of a grouped launch: `GroupEntry` (cuda/mod.rs:314-320). */
+typedef struct {
+    const q8_weight *weight;
+    q8_dptr y;
+    size_t y_offset;
+} q8_group_entry;
+
+/* Kernel variants a tactic can name. */
+enum { Q8_KERNEL_GEMV = 1, Q8_KERNEL_GEMM = 2 };
+
+/* The shape-keyed tactic chosen for one (n, out, k): the matmul counterpart
+ * of `Tactic`/`Choice` (apps/engine/src/tactics.rs:229-347). */
+typedef struct {
+    int kernel;          /* Q8_KERNEL_* */
+    int waves_per_tile;  /* GEMV: waves splitting one 32-row tile's blocks */
+    int pairs_per_wave;  /* GEMV: block pairs per wave */
+    int pairs_per_batch; /* GEMV: block pairs whose loads are issued together */
+    int exact;           /* GEMV: 1 = left-to-right block sum (bit-exact) */
+    int tt_per_wg;       /* GEMM: 32-token tiles (waves) per workgroup */
+    int smode;           /* GEMM: 1 = scale products on the matrix cores */
+    int xcd_remap;       /* GEMM: keep a row tile's workgroups on one XCD */
+    const char *name;    /* tactic name, e.g. "matmul.gemv_f32" */
+    const char *evidence;
+} q8_tactic;
+
+/* ---- status and build identity ---- */
+
+/* Human-readable name of a status code (sys.rs:140-151 error_message). */
+const char *q8_status_string(int status);
+/* Message of the last failed call on this thread (EngineError's text). */
+const char *q8_last_error(void);
+/* Build identity: arch, source and code-object sha256, hipcc version, kernel
+ * symbols (apps/engine/build.rs:53-61, apps/engine/src/manifest.rs:17-61). */
+const char *q8_build_info(void);
+
+/* ---- context: Gpu::open / Drop (cuda/mod.rs:363-522, 1981-1993) ---- */
+
+int q8_open(int device, q8_ctx **out);
+void q8_close(q8_ctx *ctx);
+int q8_device_name(q8_ctx *ctx, char *buf, size_t len);
+/* CU count, total and free bytes (cuDeviceGetAttribute / cuMemGetInfo,
+ * sys.rs:59-62; Gpu::free_bytes). */
+int q8_device_info(q8_ctx *ctx, int *cu_count, size_t *total_bytes, size_t *free_bytes);
+/* The context's HIP stream (hipStream_t), for callers that order their own
+ * work with this path's. */
+void *q8_stream(q8_ctx *ctx);
+/* Tuning/testing switches; value -1 restores the tactic table's choice.
+ * Names: "gemv.exact", "gemv.waves", "gemv.pairs", "gemm.smode",
+ * "gemm.tt_per_wg", "gemm.xcd_remap". */
+int q8_set_option(q8_ctx *ctx, const char *name, int value);
+
+/* ---- device memory: Gpu::alloc / upload / download (cuda/mod.rs:530-567) ---- */
+
+int q8_alloc(q8_ctx *ctx, size_t bytes, q8_dptr *out);
+int q8_free(q8_ctx *ctx, q8_dptr ptr);
+int q8_upload(q8_ctx *ctx, q8_dptr dst, const void *src, size_t bytes);
+int q8_download(q8_ctx *ctx, void *dst, q8_dptr src, size_t bytes);
+int q8_sync(q8_ctx *ctx);
+
+/* ---- weight residency: Gpu::quantized / reserve (cuda/mod.rs:1758-1790) ----
+ * Uploads GGUF Q8_0 bytes (`out` rows of k/32 blocks of 34 bytes) once and
+ * repacks them on the device into the tile layout; cached by the host
+ * identity (bytes, nbytes) exactly as `Weight::identity()` keys the
+ * reference's cache (tensor.rs:40-42).  The handle lives until q8_close or
+ * q8_weight_release. */
+int q8_weight_resident(q8_ctx *ctx, const void *gguf_bytes, size_t nbytes, int k, int out,
+                       const q8_weight **weight);
+int q8_weight_release(q8_ctx *ctx, const q8_weight *weight);
+int q8_weight_shape(const q8_weight *weight, int *k, int *out, size_t *device_bytes);
+/* Writes the resident weight back as GGUF bytes (inverse repack), so the
+ * device layout can be checked byte-exactly against the upload. */
+int q8_weight_export(q8_ctx *ctx, const q8_weight *weight, void *gguf_bytes, size_t nbytes);
+
+/* ---- the matmul entry points ---- */
+
+/* y[t*out + o] (+)= sum_i x[t*k + i] * W[o*k + i] for t < n.
+ * Gpu::matmul (cuda/mod.rs:803-892) / Compute::matmul, matmul_prepared,
+ * matmul_add (compute.rs:399-431, 537-581).  `prepared` may be NULL (the
+ * activations are then quantized here for n >= 2); `bias` != 0 adds
+ * bias[bias_offset + t*out + o] in the epilogue (the fused residual; it may
+ * alias y).  n == 1 takes the GEMV, n >= 2 the MFMA GEMM; n > Q8_MAX_TOKENS
+ * is Q8_ERR_UNSUPPORTED as in the reference. */
+int q8_matmul(q8_ctx *ctx, const q8_weight *weight, q8_dptr x, size_t x_offset, int n, q8_dptr y,
+              size_t y_offset, const q8_prepared *prepared, q8_dptr bias, size_t bias_offset);
+
+/* Quantize n rows of k f32 activations once for several matmuls:
+ * Gpu::prepare (cuda/mod.rs:1381-1410) / Compute::prepare (compute.rs:376-395). */
+int q8_prepare(q8_ctx *ctx, q8_dptr x, size_t x_offset, int n, int k, q8_prepared *out);
+
+/* quantize(silu(gate) * up) for the down projection without writing the f32
+ * product: Gpu::silu_mul_quantize (cuda/mod.rs:1449-1476) /
+ * Compute::silu_mul_prepare (compute.rs:993-1019).  gate and up are [n][k]. */
+int q8_silu_mul_prepare(q8_ctx *ctx, q8_dptr gate, q8_dptr up, int n, int k, q8_prepared *out);
+
+/* act[i] = silu(gate[i]) * up[i] for i < len: Gpu::silu_mul / Compute::silu_mul
+ * (compute.rs:931-953, ops.rs:33-35). */
+int q8_silu_mul(q8_ctx *ctx, q8_dptr act, q8_dptr gate, q8_dptr up, size_t len);
+
+/* Up to four n == 1 matmuls sharing x, one launch:
+ * Gpu::matmul_decode_group (cuda/mod.rs:1482-1543).  `bias` only for a
+ * single-member group, as in the reference. */
+int q8_matmul_decode_group(q8_ctx *ctx, const q8_group_entry *group, int count, q8_dptr x,
+                           size_t x_offset, int k, q8_dptr bias, size_t bias_offset);
+
+/* Up to four n >= 2 matmuls sharing prepared activations, one launch:
+ * Gpu::matmul_prompt_group (cuda/mod.rs:1549-1626) /
+ * Compute::matmul_prepared_group (compute.rs:437-472). */
+int q8_matmul_prompt_group(q8_ctx *ctx, const q8_group_entry *group, int count,
+                           const q8_prepared *prepared, int n, int k, q8_dptr bias,
+                           size_t bias_offset);
+
+/* The feed-forward gate/up pair with SiLU: act[t*ffn + i] =
+ * silu(gate(x)_i) * up(x)_i (model.rs:1170-1215 with compute.rs:937-953).
+ * n == 1: one fused launch (both GEMVs and the SiLU product in the epilogue).
+ * n >= 2: one grouped GEMM into workspace, then the product; if `prepared`
+ * is not NULL the product is also quantized into it for the down matmul. */
+int q8_gate_up_silu(q8_ctx *ctx, const q8_weight *gate, const q8_weight *up, q8_dptr x,
+                    size_t x_offset, int n, q8_dptr act, size_t act_offset, q8_prepared *prepared);
+
+/* lm_head GEMV on the last normed row plus the greedy argmax on the device:
+ * model.rs:806-832 + sampler.rs:167-175.  Writes the logits and returns the
+ * first index of the strictly greatest logit in *argmax (waits for it). */
+int q8_lm_head_argmax(q8_ctx *ctx, const q8_weight *weight, q8_dptr x, size_t x_offset,
+                      q8_dptr logits, size_t logits_offset, uint32_t *argmax);
+
+/* Greedy argmax of len f32 values on the device (sampler.rs:167-175). */
+int q8_argmax(q8_ctx *ctx, q8_dptr values, size_t offset, size_t len, uint32_t *argmax);
+
+/* ---- tactics: the shape-keyed plan (tactics.rs:229-347, for gfx950) ---- */
+
+/* The tactic a matmul of n tokens over an out x k weight would run. */
+int q8_plan(q8_ctx *ctx, int n, int out, int k, q8_tactic *tactic);
+/* Number of rows in the tactic table and row i of it, for the invariant
+ * checks the reference keeps (tactics.rs:453-501). */
+int q8_tactic_count(void);
+int q8_tactic_row(int i, q8_tactic *tactic, int *rank, int *maturity);
+
+/* ---- timing and graphs (cuEvent* / cuGraph*, sys.rs:76-123) ---- */
+
+int q8_event_create(q8_ctx *ctx, void **event);
+int q8_event_record(q8_ctx *ctx, void *event);
+/* Waits for `end`, then returns the milliseconds between the two. */
+int q8_event_elapsed_ms(void *start, void *end, float *ms);
+int q8_event_destroy(void *event);
+/* Capture the context's stream into a graph (cuStreamBeginCapture /
+ * cuStreamEndCapture / cuGraphInstantiate), then replay it. */
+int q8_graph_begin(q8_ctx *ctx);
+int q8_graph_end(q8_ctx *ctx, void **graph);
+int q8_graph_launch(q8_ctx *ctx, void *graph);
+int q8_graph_destroy(void *graph);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* Q8MI_H */

@@ -1,0 +1,142 @@
+/*
+ * q8_layout.h -- device data layout and kernel argument blocks, shared by the
+ * gfx950 kernels (q8_kernels.hip) and the host runtime (q8_runtime.cpp).
+ *
+ * Q8_0 block (GGUF, apps/engine/src/quant.rs:8-9): [f16 LE scale d][32 x i8 q],
+ * element value d*q.  A matrix is `rows x k`, row-major, k % 32 == 0.
+ *
+ * Device weight layout ("tile layout"), private to the residency cache exactly
+ * as the reference's repacked planes are (apps/engine/src/cuda/mod.rs:2072-2089):
+ *   rows are grouped in tiles of Q8_TILE_ROWS = 32 (the last tile zero-padded);
+ *   for tile g and block b the 32x32 quants form one 1024-byte "unit" laid out
+ *   in wave-lane order: lane L = 32*h + r (h = 0/1, r = row in tile) owns the
+ *   16 bytes at unit + 16*L, holding half h of row r's block in the permuted
+ *   element order Q8_PERM below;
+ *   quants:  unit(g, b) = quants + (g*nb + b) * 1024
+ *   scales:  f16 d of (row 32g+r, block b) at scales[(g*nb + b)*32 + r].
+ * One 64-lane dwordx4 load therefore fetches a whole unit, which is both the
+ * MFMA operand of v_mfma_i32_32x32x32_i8 and the GEMV's coalesced stream.
+ *
+ * Element permutation inside a block: byte p = 4*t + c of half h holds element
+ * 8*c + Q8_J[h][t].  Dword t of half h is thus the AVX2 lane j = Q8_J[h][t]
+ * across the four 8-wide chunks c (quant.rs:63-72), so one GPU lane can replay
+ * the reference's per-lane FMA chain, and halves h=0/h=1 hold lanes {0,4,1,5}
+ * and {2,6,3,7}: their pair sums are exactly the two halves of the reference's
+ * horizontal_sum (quant.rs:80-91).  Both MFMA operands use the same
+ * permutation, so the integer block dot is unchanged by it.
+ *
+ * Prepared activations (the quantized X of the prefill path, the reference's
+ * opaque `Prepared`, apps/engine/src/cuda/mod.rs:1381-1410) use the same
+ * lane-order units over tiles of Q8_TILE_TOKENS = 32 tokens:
+ *   quants: unit(tt, b) = xq + (tt*nb + b) * 1024, lane L = 32*h + (t % 32)
+ *   scales: f32 s of (token t, block b) at xs[((t/32)*nb + b)*32 + t%32]
+ * Padding tokens (t >= n in the last tile) are written as zero.
+ */
+#ifndef Q8_LAYOUT_H
+#define Q8_LAYOUT_H
+
+#include <stdint.h>
+
+#define Q8_BLOCK_ELEMS 32
+#define Q8_BLOCK_BYTES 34
+#define Q8_TILE_ROWS 32
+#define Q8_TILE_TOKENS 32
+#define Q8_UNIT_BYTES 1024
+#define Q8_GROUP_MAX 4 /* apps/engine/src/cuda/mod.rs:63 MMA_GROUP_MAX */
+
+/* Q8_J[h][t]: the AVX2 lane held by dword t of half h. */
+#define Q8_J_INIT {{0, 4, 1, 5}, {2, 6, 3, 7}}
+
+static inline int q8_perm_element(int h, int p) {
+    static const int J[2][4] = Q8_J_INIT;
+    return 8 * (p & 3) + J[h][p >> 2];
+}
+
+/* ---- kernel argument blocks (passed by value as the only kernel argument) ---- */
+
+typedef struct {
+    const uint8_t *src; /* GGUF Q8_0 bytes, rows * nb * 34 (inverse = 0) */
+    uint8_t *dst;       /* GGUF Q8_0 bytes written back (inverse = 1) */
+    uint8_t *quants;    /* tile layout quants */
+    uint16_t *scales;   /* tile layout scales */
+    int rows;
+    int nb;
+    int tiles;
+    int inverse; /* 0: GGUF -> tile layout; 1: tile layout -> GGUF (test hook) */
+} Q8RepackArgs;
+
+typedef struct {
+    const uint8_t *quants;
+    const uint16_t *scales;
+    float *y;          /* rows f32 (n = 1) */
+    const float *bias; /* residual added in the epilogue, or null */
+    int rows;
+    int tile_begin; /* first global tile index of this member */
+} Q8GemvMember;
+
+typedef struct {
+    Q8GemvMember m[Q8_GROUP_MAX];
+    int members;
+    int total_tiles;
+    const float *x; /* k f32 */
+    int nb;
+    int waves_per_tile;  /* W: waves splitting one tile's blocks */
+    int pairs_per_wave;  /* ceil(ceil(nb/2) / W) */
+    int silu_pair;       /* 1: m[0] = gate, m[1] = up; writes silu(g)*u to m[0].y */
+} Q8GemvArgs;
+
+typedef struct {
+    const float *x;    /* [n][k] f32 (mode 0) */
+    const float *gate; /* [n][k] f32 (mode 1) */
+    const float *up;   /* [n][k] f32 (mode 1) */
+    uint8_t *xq;       /* prepared quants */
+    float *xs;         /* prepared scales */
+    int n;
+    int nb;
+    int ttiles;
+    int mode; /* 0: quantize x; 1: quantize silu(gate) * up */
+} Q8QuantArgs;
+
+typedef struct {
+    const uint8_t *quants;
+    const uint16_t *scales;
+    float *y;          /* [n][rows] f32 */
+    const float *bias; /* [n][rows] residual, or null */
+    int rows;
+    int tile_begin; /* first global row tile of this member */
+} Q8GemmMember;
+
+typedef struct {
+    Q8GemmMember m[Q8_GROUP_MAX];
+    int members;
+    int total_rtiles;
+    const uint8_t *xq;
+    const float *xs;
+    int n;
+    int nb;
+    int ttiles;
+    int tt_per_wg;  /* waves per workgroup, one token tile each */
+    int tgroups;    /* ceil(ttiles / tt_per_wg) */
+    int nwg;        /* workgroups launched (total_rtiles * tgroups) */
+    int xcd_remap;  /* 1: map workgroups so one row tile's token groups share an XCD */
+} Q8GemmArgs;
+
+typedef struct {
+    const float *x;
+    float *act;
+    const float *gate;
+    const float *up;
+    long long len;
+} Q8EltArgs;
+
+typedef struct {
+    const float *values;
+    long long len;
+    float *part_value;     /* per-workgroup best value */
+    unsigned *part_index;  /* per-workgroup best index (UINT32_MAX = none) */
+    unsigned *result;      /* final index */
+    int parts;
+    int stage; /* 0: per-workgroup; 1: combine parts */
+} Q8ArgmaxArgs;
+
+#endif

@@ -1,0 +1,882 @@
+// q8_runtime.cpp -- host side of libq8mi.so: the C-ABI of include/q8mi.h over
+// the HIP runtime.
+//
+// Structure follows the reference's device runtime `Gpu`
+// (apps/engine/src/cuda/mod.rs): one context with one stream, a module loaded
+// from an embedded code object (cuModuleLoadData of embedded PTX,
+// cuda/mod.rs:406-411 -> hipModuleLoadData of an embedded gfx950 code object),
+// a weight residency cache keyed by the host slice identity
+// (cuda/mod.rs:1769-1790), a growing activation workspace for prepared
+// activations (cuda/mod.rs:1629-1645), and launches through
+// hipModuleLaunchKernel (cuda/mod.rs:1819-1902).  Before every launch the
+// operand spans are checked on the host against the allocations this context
+// made, so a wrong shape is an error here and never an out-of-bounds access on
+// the device.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/q8mi.h"
+#include "q8_layout.h"
+#include "q8_manifest.h"
+#include "q8_tactics.h"
+
+extern "C" const unsigned char q8_code_object[];
+extern "C" const unsigned char q8_code_object_end[];
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *op) {
+    return fail(e == hipErrorOutOfMemory ? Q8_ERR_OUT_OF_MEMORY : Q8_ERR_HIP, "hip: %s failed: %s", op,
+                hipGetErrorString(e));
+}
+
+#define HIP_TRY(call, op)                             \
+    do {                                              \
+        hipError_t e_ = (call);                       \
+        if (e_ != hipSuccess) return hip_fail(e_, op); \
+    } while (0)
+
+#define Q8_TRY(call)          \
+    do {                      \
+        int rc_ = (call);     \
+        if (rc_ != Q8_OK) return rc_; \
+    } while (0)
+
+enum Fn {
+    F_REPACK,
+    F_GEMV_2_0, F_GEMV_2_1, F_GEMV_3_0, F_GEMV_3_1, F_GEMV_5_0, F_GEMV_5_1, F_GEMV_9_0, F_GEMV_9_1,
+    F_QUANTIZE,
+    F_GEMM_S0, F_GEMM_S1,
+    F_ARGMAX,
+    F_SILU_MUL,
+    F_COUNT
+};
+
+const char *const kFnNames[F_COUNT] = {
+    "q8_repack",
+    "q8_gemv_pb2_e0", "q8_gemv_pb2_e1", "q8_gemv_pb3_e0", "q8_gemv_pb3_e1",
+    "q8_gemv_pb5_e0", "q8_gemv_pb5_e1", "q8_gemv_pb9_e0", "q8_gemv_pb9_e1",
+    "q8_quantize",
+    "q8_gemm_s0", "q8_gemm_s1",
+    "q8_argmax",
+    "q8_silu_mul",
+};
+
+constexpr int kArgmaxParts = 1024;
+constexpr size_t kAlign = 256;
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+long long ceil_div(long long a, long long b) { return (a + b - 1) / b; }
+
+}  // namespace
+
+struct q8_weight {
+    q8_ctx *ctx;
+    void *base;
+    uint8_t *quants;
+    uint16_t *scales;
+    int k, out, nb, tiles;
+    size_t device_bytes;
+    uintptr_t id_ptr;
+    size_t id_len;
+};
+
+struct q8_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipModule_t module = nullptr;
+    hipFunction_t fn[F_COUNT] = {};
+    std::recursive_mutex mu;
+    std::map<std::pair<uintptr_t, size_t>, q8_weight *> weights;
+    std::map<uintptr_t, size_t> allocs;  // buffers from q8_alloc, for span checks
+    void *act_ws = nullptr;              // prepared activations
+    size_t act_ws_bytes = 0;
+    void *tmp_ws = nullptr;              // gate/up f32 products of the n >= 2 FFN pair
+    size_t tmp_ws_bytes = 0;
+    void *argmax_ws = nullptr;           // per-workgroup partials + result
+    int cu_count = 0;
+    size_t total_mem = 0;
+    size_t max_lds = 0;
+    char name[256] = {};
+    std::map<std::string, int> options;
+};
+
+namespace {
+
+// [p, p + bytes) must lie inside one buffer this context allocated, when p is
+// one of ours; foreign pointers (a caller's own allocations) are not tracked.
+int check_span(q8_ctx *c, q8_dptr p, size_t bytes, const char *what) {
+    if (p == 0) return fail(Q8_ERR_INVALID, "%s: null device pointer", what);
+    auto it = c->allocs.upper_bound((uintptr_t)p);
+    if (it == c->allocs.begin()) return Q8_OK;
+    --it;
+    const uintptr_t base = it->first;
+    const size_t size = it->second;
+    if ((uintptr_t)p >= base + size) return Q8_OK;  // not inside a tracked buffer
+    if ((uintptr_t)p + bytes > base + size)
+        return fail(Q8_ERR_INVALID, "%s: %zu bytes at offset %zu overrun a %zu-byte buffer", what, bytes,
+                    (size_t)((uintptr_t)p - base), size);
+    return Q8_OK;
+}
+
+int option(q8_ctx *c, const char *name, int fallback) {
+    auto it = c->options.find(name);
+    return (it == c->options.end() || it->second < 0) ? fallback : it->second;
+}
+
+int launch(q8_ctx *c, Fn f, unsigned grid, unsigned block, unsigned lds, void *args, size_t args_size) {
+    if (grid == 0) return Q8_OK;
+    if (lds > c->max_lds)
+        return fail(Q8_ERR_UNSUPPORTED, "%s needs %u bytes of LDS, the device allows %zu", kFnNames[f], lds,
+                    c->max_lds);
+    (void)args_size;
+    void *params[] = {args};  // every kernel takes one argument block by value
+    HIP_TRY(hipModuleLaunchKernel(c->fn[f], grid, 1, 1, block, 1, 1, lds, c->stream, params, nullptr),
+            kFnNames[f]);
+    return Q8_OK;
+}
+
+int grow(q8_ctx *c, void **buf, size_t *have, size_t need, const char *what) {
+    if (*have >= need) return Q8_OK;
+    if (*buf) {
+        HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+        HIP_TRY(hipFree(*buf), "hipFree");
+        *buf = nullptr;
+        *have = 0;
+    }
+    const size_t bytes = align_up(need, 1 << 20);
+    HIP_TRY(hipMalloc(buf, bytes), what);
+    *have = bytes;
+    return Q8_OK;
+}
+
+q8_tactic plan(q8_ctx *c, int n, int out, int k) {
+    q8_tactic t{};
+    q8_tactics_choose(n, out, k, c->cu_count, &t);
+    if (t.kernel == Q8_KERNEL_GEMV) {
+        const int nb = k / 32;
+        const int npairs = (nb + 1) / 2;
+        t.exact = option(c, "gemv.exact", t.exact) ? 1 : 0;
+        const int w = option(c, "gemv.waves", -1);
+        if (w > 0) {
+            t.waves_per_tile = std::min(w, npairs);
+            t.pairs_per_wave = (int)ceil_div(npairs, t.waves_per_tile);
+            t.waves_per_tile = (int)ceil_div(npairs, t.pairs_per_wave);
+        }
+        const int pb = option(c, "gemv.pairs", -1);
+        if (pb > 0) t.pairs_per_batch = pb;
+    } else {
+        t.smode = option(c, "gemm.smode", t.smode) ? 1 : 0;
+        const int tpw = option(c, "gemm.tt_per_wg", -1);
+        if (tpw > 0) t.tt_per_wg = std::min(tpw, 4);
+        t.xcd_remap = option(c, "gemm.xcd_remap", t.xcd_remap) ? 1 : 0;
+    }
+    return t;
+}
+
+Fn gemv_fn(int pb, int exact) {
+    switch (pb) {
+        case 2: return exact ? F_GEMV_2_1 : F_GEMV_2_0;
+        case 3: return exact ? F_GEMV_3_1 : F_GEMV_3_0;
+        case 5: return exact ? F_GEMV_5_1 : F_GEMV_5_0;
+        default: return exact ? F_GEMV_9_1 : F_GEMV_9_0;
+    }
+}
+
+int valid_pb(int pb) { return pb == 2 || pb == 3 || pb == 5 || pb == 9; }
+
+// Re-split npairs block pairs over at most max_w waves (fused gate/up puts
+// two tiles' waves in one 512-thread workgroup).
+void fit_gemv_waves(q8_tactic *t, int npairs, int max_w) {
+    int w = std::min(max_w, npairs);
+    const int ppw = (int)ceil_div(npairs, w);
+    w = (int)ceil_div(npairs, ppw);
+    t->waves_per_tile = w;
+    t->pairs_per_wave = ppw;
+    t->pairs_per_batch = ppw <= 2 ? 2 : ppw <= 3 ? 3 : ppw <= 5 ? 5 : ppw <= 9 ? 9 : 5;
+}
+
+struct Member {
+    const q8_weight *w;
+    float *y;
+};
+
+// n = 1 over up to four weights sharing x; silu = 1 fuses silu(m0)*m1 into y of m0.
+int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const float *bias, int silu) {
+    const int nb = k / 32;
+    int rows_total = 0;
+    Q8GemvArgs a{};
+    a.members = count;
+    int tile = 0;
+    for (int i = 0; i < count; i++) {
+        a.m[i].quants = m[i].w->quants;
+        a.m[i].scales = m[i].w->scales;
+        a.m[i].y = m[i].y;
+        a.m[i].bias = (i == 0) ? bias : nullptr;
+        a.m[i].rows = m[i].w->out;
+        a.m[i].tile_begin = tile;
+        tile += m[i].w->tiles;
+        rows_total += m[i].w->out;
+    }
+    q8_tactic t = plan(c, 1, silu ? m[0].w->out : rows_total, k);
+    if (silu && t.waves_per_tile > 4) fit_gemv_waves(&t, (nb + 1) / 2, 4);
+    if (t.pairs_per_wave > 12)
+        return fail(Q8_ERR_UNSUPPORTED, "gemv: %d block pairs per wave exceeds the staging bound of 12",
+                    t.pairs_per_wave);
+    const int pb = valid_pb(t.pairs_per_batch) ? t.pairs_per_batch : 5;
+    a.total_tiles = silu ? m[0].w->tiles : tile;
+    a.x = reinterpret_cast<const float *>(x);
+    a.nb = nb;
+    a.waves_per_tile = t.waves_per_tile;
+    a.pairs_per_wave = t.pairs_per_wave;
+    a.silu_pair = silu;
+    const int slots = silu ? 2 : 1;
+    const int waves = t.waves_per_tile * slots;
+    if (waves * 64 > 512)
+        return fail(Q8_ERR_UNSUPPORTED, "gemv: %d waves per workgroup exceed the 512-thread launch bound", waves);
+    const unsigned lds = (unsigned)(nb * 32 * 4 + (t.exact ? slots * nb * 32 * 4 : waves * 32 * 4));
+    return launch(c, gemv_fn(pb, t.exact), (unsigned)a.total_tiles, (unsigned)(waves * 64), lds, &a, sizeof a);
+}
+
+int run_gemm(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n, const float *bias) {
+    const int k = p->k;
+    const int nb = k / 32;
+    Q8GemmArgs a{};
+    a.members = count;
+    int rt = 0, rows_total = 0;
+    for (int i = 0; i < count; i++) {
+        a.m[i].quants = m[i].w->quants;
+        a.m[i].scales = m[i].w->scales;
+        a.m[i].y = m[i].y;
+        a.m[i].bias = (i == 0) ? bias : nullptr;
+        a.m[i].rows = m[i].w->out;
+        a.m[i].tile_begin = rt;
+        rt += m[i].w->tiles;
+        rows_total += m[i].w->out;
+    }
+    const q8_tactic t = plan(c, n, rows_total, k);
+    a.total_rtiles = rt;
+    a.xq = reinterpret_cast<const uint8_t *>(p->quants);
+    a.xs = reinterpret_cast<const float *>(p->scales);
+    a.n = n;
+    a.nb = nb;
+    a.ttiles = (int)ceil_div(n, 32);
+    a.tt_per_wg = std::max(1, std::min(t.tt_per_wg, a.ttiles));
+    a.tgroups = (int)ceil_div(a.ttiles, a.tt_per_wg);
+    const long long nwg = (long long)rt * a.tgroups;
+    a.nwg = (int)nwg;
+    a.xcd_remap = (t.xcd_remap && nwg % 8 == 0) ? 1 : 0;
+    return launch(c, t.smode ? F_GEMM_S1 : F_GEMM_S0, (unsigned)nwg, (unsigned)(64 * a.tt_per_wg), 0, &a,
+                  sizeof a);
+}
+
+int prepare_into(q8_ctx *c, q8_dptr x, q8_dptr gate, q8_dptr up, int n, int k, q8_prepared *out) {
+    const int nb = k / 32;
+    const long long ttiles = ceil_div(n, 32);
+    const size_t qbytes = (size_t)ttiles * nb * Q8_UNIT_BYTES;
+    const size_t sbytes = (size_t)ttiles * nb * Q8_TILE_TOKENS * sizeof(float);
+    Q8_TRY(grow(c, &c->act_ws, &c->act_ws_bytes, align_up(qbytes, kAlign) + sbytes, "hipMalloc(activation)"));
+    Q8QuantArgs a{};
+    a.x = reinterpret_cast<const float *>(x);
+    a.gate = reinterpret_cast<const float *>(gate);
+    a.up = reinterpret_cast<const float *>(up);
+    a.xq = static_cast<uint8_t *>(c->act_ws);
+    a.xs = reinterpret_cast<float *>(static_cast<uint8_t *>(c->act_ws) + align_up(qbytes, kAlign));
+    a.n = n;
+    a.nb = nb;
+    a.ttiles = (int)ttiles;
+    a.mode = gate ? 1 : 0;
+    const long long threads = ttiles * Q8_TILE_TOKENS * nb * 8;
+    Q8_TRY(launch(c, F_QUANTIZE, (unsigned)ceil_div(threads, 256), 256, 0, &a, sizeof a));
+    out->quants = (q8_dptr)(uintptr_t)a.xq;
+    out->scales = (q8_dptr)(uintptr_t)a.xs;
+    out->n = n;
+    out->k = k;
+    return Q8_OK;
+}
+
+int check_k(int k) {
+    if (k <= 0 || k % 32 != 0) return fail(Q8_ERR_INVALID, "Q8_0 rows are whole 32-element blocks (k = %d)", k);
+    return Q8_OK;
+}
+
+int check_n(int n) {
+    if (n < 1) return fail(Q8_ERR_INVALID, "n must be at least 1 (got %d)", n);
+    if (n > Q8_MAX_TOKENS)
+        return fail(Q8_ERR_UNSUPPORTED, "prompt matmul holds %d tokens, got %d", Q8_MAX_TOKENS, n);
+    return Q8_OK;
+}
+
+int check_weight(q8_ctx *c, const q8_weight *w) {
+    if (!w || w->ctx != c) return fail(Q8_ERR_INVALID, "weight handle does not belong to this context");
+    return Q8_OK;
+}
+
+float *fptr(q8_dptr p, size_t off) { return p ? reinterpret_cast<float *>(p) + off : nullptr; }
+
+int argmax_into(q8_ctx *c, q8_dptr values, size_t len, uint32_t *out) {
+    if (len == 0) return fail(Q8_ERR_INVALID, "argmax of an empty vector");
+    if (len > 0xfffffffeULL) return fail(Q8_ERR_INVALID, "argmax length %zu exceeds u32 indices", len);
+    Q8_TRY(check_span(c, values, len * 4, "argmax values"));
+    uint8_t *ws = static_cast<uint8_t *>(c->argmax_ws);
+    Q8ArgmaxArgs a{};
+    a.values = reinterpret_cast<const float *>(values);
+    a.len = (long long)len;
+    a.part_value = reinterpret_cast<float *>(ws);
+    a.part_index = reinterpret_cast<unsigned *>(ws + kArgmaxParts * 4);
+    a.result = reinterpret_cast<unsigned *>(ws + kArgmaxParts * 8);
+    const int parts = (int)std::min<long long>(kArgmaxParts, std::max<long long>(1, ceil_div((long long)len, 4096)));
+    a.parts = parts;
+    a.stage = 0;
+    Q8_TRY(launch(c, F_ARGMAX, (unsigned)parts, 256, 0, &a, sizeof a));
+    a.stage = 1;
+    Q8_TRY(launch(c, F_ARGMAX, 1, 256, 0, &a, sizeof a));
+    uint32_t result = 0;
+    HIP_TRY(hipMemcpyAsync(&result, a.result, 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync(argmax)");
+    HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    *out = result;
+    return Q8_OK;
+}
+
+}  // namespace
+
+// ===========================================================================
+// C-ABI
+// ===========================================================================
+extern "C" {
+
+const char *q8_status_string(int status) {
+    switch (status) {
+        case Q8_OK: return "ok";
+        case Q8_ERR_HIP: return "HIP error";
+        case Q8_ERR_INVALID: return "invalid argument";
+        case Q8_ERR_UNSUPPORTED: return "unsupported";
+        case Q8_ERR_NO_DEVICE: return "no device";
+        case Q8_ERR_OUT_OF_MEMORY: return "out of device memory";
+        default: return "unknown status";
+    }
+}
+
+const char *q8_last_error(void) { return g_last_error.c_str(); }
+
+const char *q8_build_info(void) { return Q8_BUILD_INFO; }
+
+int q8_open(int device, q8_ctx **out) {
+    if (!out) return fail(Q8_ERR_INVALID, "q8_open: null output");
+    *out = nullptr;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count <= device || device < 0)
+        return fail(Q8_ERR_NO_DEVICE, "no HIP device %d (%d visible): %s", device, count,
+                    e == hipSuccess ? "out of range" : hipGetErrorString(e));
+    HIP_TRY(hipSetDevice(device), "hipSetDevice");
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(Q8_ERR_NO_DEVICE, "device %d is %s; this build carries gfx950 code only", device,
+                    prop.gcnArchName);
+    q8_ctx *c = new q8_ctx();
+    c->device = device;
+    c->cu_count = prop.multiProcessorCount;
+    c->total_mem = prop.totalGlobalMem;
+    c->max_lds = prop.sharedMemPerBlock;
+    std::snprintf(c->name, sizeof c->name, "%s (%s)", prop.name, prop.gcnArchName);
+    int rc = Q8_OK;
+    do {
+        hipError_t he = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+        if (he != hipSuccess) { rc = hip_fail(he, "hipStreamCreate"); break; }
+        he = hipModuleLoadData(&c->module, q8_code_object);
+        if (he != hipSuccess) { rc = fail(Q8_ERR_NO_DEVICE, "hip: hipModuleLoadData failed: %s", hipGetErrorString(he)); break; }
+        for (int i = 0; i < F_COUNT && rc == Q8_OK; i++) {
+            he = hipModuleGetFunction(&c->fn[i], c->module, kFnNames[i]);
+            if (he != hipSuccess)
+                rc = fail(Q8_ERR_NO_DEVICE, "hip: hipModuleGetFunction(%s) failed: %s", kFnNames[i],
+                          hipGetErrorString(he));
+        }
+        if (rc != Q8_OK) break;
+        he = hipMalloc(&c->argmax_ws, kArgmaxParts * 8 + 256);
+        if (he != hipSuccess) { rc = hip_fail(he, "hipMalloc(argmax)"); break; }
+    } while (0);
+    if (rc != Q8_OK) {
+        q8_close(c);
+        return rc;
+    }
+    *out = c;
+    return Q8_OK;
+}
+
+void q8_close(q8_ctx *c) {
+    if (!c) return;
+    hipSetDevice(c->device);
+    if (c->stream) hipStreamSynchronize(c->stream);
+    for (auto &kv : c->weights) {
+        hipFree(kv.second->base);
+        delete kv.second;
+    }
+    for (auto &kv : c->allocs) hipFree(reinterpret_cast<void *>(kv.first));
+    if (c->act_ws) hipFree(c->act_ws);
+    if (c->tmp_ws) hipFree(c->tmp_ws);
+    if (c->argmax_ws) hipFree(c->argmax_ws);
+    if (c->module) hipModuleUnload(c->module);
+    if (c->stream) hipStreamDestroy(c->stream);
+    delete c;
+}
+
+int q8_device_name(q8_ctx *c, char *buf, size_t len) {
+    if (!c || !buf || len == 0) return fail(Q8_ERR_INVALID, "q8_device_name: bad arguments");
+    std::snprintf(buf, len, "%s", c->name);
+    return Q8_OK;
+}
+
+int q8_device_info(q8_ctx *c, int *cu_count, size_t *total_bytes, size_t *free_bytes) {
+    if (!c) return fail(Q8_ERR_INVALID, "q8_device_info: null context");
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+    if (cu_count) *cu_count = c->cu_count;
+    size_t fr = 0, tot = 0;
+    HIP_TRY(hipMemGetInfo(&fr, &tot), "hipMemGetInfo");
+    if (total_bytes) *total_bytes = tot;
+    if (free_bytes) *free_bytes = fr;
+    return Q8_OK;
+}
+
+void *q8_stream(q8_ctx *c) { return c ? (void *)c->stream : nullptr; }
+
+int q8_set_option(q8_ctx *c, const char *name, int value) {
+    if (!c || !name) return fail(Q8_ERR_INVALID, "q8_set_option: bad arguments");
+    static const char *const known[] = {"gemv.exact", "gemv.waves", "gemv.pairs",
+                                        "gemm.smode", "gemm.tt_per_wg", "gemm.xcd_remap"};
+    bool ok = false;
+    for (const char *k : known) ok = ok || std::strcmp(k, name) == 0;
+    if (!ok) return fail(Q8_ERR_INVALID, "unknown option %s", name);
+    if (std::strcmp(name, "gemv.pairs") == 0 && value > 0 && !valid_pb(value))
+        return fail(Q8_ERR_INVALID, "gemv.pairs must be one of 2, 3, 5, 9");
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    c->options[name] = value;
+    return Q8_OK;
+}
+
+int q8_alloc(q8_ctx *c, size_t bytes, q8_dptr *out) {
+    if (!c || !out || bytes == 0) return fail(Q8_ERR_INVALID, "q8_alloc: bad arguments");
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+    void *p = nullptr;
+    HIP_TRY(hipMalloc(&p, bytes), "hipMalloc");
+    c->allocs[(uintptr_t)p] = bytes;
+    *out = (q8_dptr)(uintptr_t)p;
+    return Q8_OK;
+}
+
+int q8_free(q8_ctx *c, q8_dptr ptr) {
+    if (!c) return fail(Q8_ERR_INVALID, "q8_free: null context");
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    auto it = c->allocs.find((uintptr_t)ptr);
+    if (it == c->allocs.end()) return fail(Q8_ERR_INVALID, "q8_free: pointer was not allocated by this context");
+    HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    HIP_TRY(hipFree(reinterpret_cast<void *>(ptr)), "hipFree");
+    c->allocs.erase(it);
+    return Q8_OK;
+}
+
+int q8_upload(q8_ctx *c, q8_dptr dst, const void *src, size_t bytes) {
+    if (!c || (!src && bytes)) return fail(Q8_ERR_INVALID, "q8_upload: bad arguments");
+    if (bytes == 0) return Q8_OK;
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    Q8_TRY(check_span(c, dst, bytes, "upload"));
+    HIP_TRY(hipMemcpyAsync(reinterpret_cast<void *>(dst), src, bytes, hipMemcpyHostToDevice, c->stream),
+            "hipMemcpyAsync(H2D)");
+    HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return Q8_OK;
+}
+
+int q8_download(q8_ctx *c, void *dst, q8_dptr src, size_t bytes) {
+    if (!c || (!dst && bytes)) return fail(Q8_ERR_INVALID, "q8_download: bad arguments");
+    if (bytes == 0) return Q8_OK;
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    Q8_TRY(check_span(c, src, bytes, "download"));
+    HIP_TRY(hipMemcpyAsync(dst, reinterpret_cast<const void *>(src), bytes, hipMemcpyDeviceToHost, c->stream),
+            "hipMemcpyAsync(D2H)");
+    HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return Q8_OK;
+}
+
+int q8_sync(q8_ctx *c) {
+    if (!c) return fail(Q8_ERR_INVALID, "q8_sync: null context");
+    HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return Q8_OK;
+}
+
+int q8_weight_resident(q8_ctx *c, const void *bytes, size_t nbytes, int k, int out, const q8_weight **weight) {
+    if (!c || !bytes || !weight) return fail(Q8_ERR_INVALID, "q8_weight_resident: bad arguments");
+    Q8_TRY(check_k(k));
+    if (out <= 0) return fail(Q8_ERR_INVALID, "weight has %d rows", out);
+    const int nb = k / 32;
+    if (nbytes != (size_t)out * nb * Q8_BLOCK_BYTES)
+        return fail(Q8_ERR_INVALID, "weight byte length mismatch: %zu bytes for %d x %d Q8_0", nbytes, out, k);
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+    const auto key = std::make_pair((uintptr_t)bytes, nbytes);
+    auto it = c->weights.find(key);
+    if (it != c->weights.end()) {
+        if (it->second->k != k || it->second->out != out)
+            return fail(Q8_ERR_INVALID, "weight identity reused with another shape");
+        *weight = it->second;
+        return Q8_OK;
+    }
+    const int tiles = (int)ceil_div(out, Q8_TILE_ROWS);
+    const size_t qbytes = (size_t)tiles * nb * Q8_UNIT_BYTES;
+    const size_t sbytes = (size_t)tiles * nb * Q8_TILE_ROWS * 2;
+    const size_t total = align_up(qbytes, kAlign) + sbytes;
+    void *base = nullptr, *staging = nullptr;
+    HIP_TRY(hipMalloc(&base, total), "hipMalloc(weight)");
+    hipError_t e = hipMalloc(&staging, nbytes);
+    if (e != hipSuccess) {
+        hipFree(base);
+        return hip_fail(e, "hipMalloc(weight staging)");
+    }
+    Q8RepackArgs a{};
+    a.src = static_cast<const uint8_t *>(staging);
+    a.quants = static_cast<uint8_t *>(base);
+    a.scales = reinterpret_cast<uint16_t *>(static_cast<uint8_t *>(base) + align_up(qbytes, kAlign));
+    a.rows = out;
+    a.nb = nb;
+    a.tiles = tiles;
+    a.inverse = 0;
+    int rc = Q8_OK;
+    e = hipMemcpyAsync(staging, bytes, nbytes, hipMemcpyHostToDevice, c->stream);
+    if (e != hipSuccess) rc = hip_fail(e, "hipMemcpyAsync(weight)");
+    if (rc == Q8_OK) {
+        const long long threads = (long long)tiles * Q8_TILE_ROWS * nb;
+        rc = launch(c, F_REPACK, (unsigned)ceil_div(threads, 256), 256, 0, &a, sizeof a);
+    }
+    if (rc == Q8_OK) {
+        e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) rc = hip_fail(e, "hipStreamSynchronize");
+    }
+    hipFree(staging);
+    if (rc != Q8_OK) {
+        hipFree(base);
+        return rc;
+    }
+    q8_weight *w = new q8_weight{c, base, a.quants, a.scales, k, out, nb, tiles, total, (uintptr_t)bytes, nbytes};
+    c->weights[key] = w;
+    *weight = w;
+    return Q8_OK;
+}
+
+int q8_weight_release(q8_ctx *c, const q8_weight *w) {
+    if (!c) return fail(Q8_ERR_INVALID, "q8_weight_release: null context");
+    Q8_TRY(check_weight(c, w));
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    auto it = c->weights.find(std::make_pair(w->id_ptr, w->id_len));
+    if (it == c->weights.end() || it->second != w) return fail(Q8_ERR_INVALID, "weight is not resident");
+    HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    hipFree(w->base);
+    delete it->second;
+    c->weights.erase(it);
+    return Q8_OK;
+}
+
+int q8_weight_shape(const q8_weight *w, int *k, int *out, size_t *device_bytes) {
+    if (!w) return fail(Q8_ERR_INVALID, "q8_weight_shape: null weight");
+    if (k) *k = w->k;
+    if (out) *out = w->out;
+    if (device_bytes) *device_bytes = w->device_bytes;
+    return Q8_OK;
+}
+
+int q8_weight_export(q8_ctx *c, const q8_weight *w, void *dst, size_t nbytes) {
+    if (!c || !dst) return fail(Q8_ERR_INVALID, "q8_weight_export: bad arguments");
+    Q8_TRY(check_weight(c, w));
+    const size_t expect = (size_t)w->out * w->nb * Q8_BLOCK_BYTES;
+    if (nbytes != expect) return fail(Q8_ERR_INVALID, "export buffer holds %zu bytes, weight is %zu", nbytes, expect);
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    void *staging = nullptr;
+    HIP_TRY(hipMalloc(&staging, nbytes), "hipMalloc(export)");
+    Q8RepackArgs a{};
+    a.dst = static_cast<uint8_t *>(staging);
+    a.quants = w->quants;
+    a.scales = w->scales;
+    a.rows = w->out;
+    a.nb = w->nb;
+    a.tiles = w->tiles;
+    a.inverse = 1;
+    const long long threads = (long long)w->tiles * Q8_TILE_ROWS * w->nb;
+    int rc = launch(c, F_REPACK, (unsigned)ceil_div(threads, 256), 256, 0, &a, sizeof a);
+    if (rc == Q8_OK) {
+        hipError_t e = hipMemcpyAsync(dst, staging, nbytes, hipMemcpyDeviceToHost, c->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) rc = hip_fail(e, "hipMemcpyAsync(export)");
+    }
+    hipFree(staging);
+    return rc;
+}
+
+int q8_prepare(q8_ctx *c, q8_dptr x, size_t x_offset, int n, int k, q8_prepared *out) {
+    if (!c || !out) return fail(Q8_ERR_INVALID, "q8_prepare: bad arguments");
+    Q8_TRY(check_k(k));
+    Q8_TRY(check_n(n));
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    const q8_dptr xp = (q8_dptr)(uintptr_t)fptr(x, x_offset);
+    Q8_TRY(check_span(c, xp, (size_t)n * k * 4, "prepare x"));
+    return prepare_into(c, xp, 0, 0, n, k, out);
+}
+
+int q8_silu_mul_prepare(q8_ctx *c, q8_dptr gate, q8_dptr up, int n, int k, q8_prepared *out) {
+    if (!c || !out) return fail(Q8_ERR_INVALID, "q8_silu_mul_prepare: bad arguments");
+    Q8_TRY(check_k(k));
+    Q8_TRY(check_n(n));
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    Q8_TRY(check_span(c, gate, (size_t)n * k * 4, "silu gate"));
+    Q8_TRY(check_span(c, up, (size_t)n * k * 4, "silu up"));
+    return prepare_into(c, 0, gate, up, n, k, out);
+}
+
+int q8_silu_mul(q8_ctx *c, q8_dptr act, q8_dptr gate, q8_dptr up, size_t len) {
+    if (!c) return fail(Q8_ERR_INVALID, "q8_silu_mul: null context");
+    if (len == 0) return Q8_OK;
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    Q8_TRY(check_span(c, act, len * 4, "silu act"));
+    Q8_TRY(check_span(c, gate, len * 4, "silu gate"));
+    Q8_TRY(check_span(c, up, len * 4, "silu up"));
+    Q8EltArgs a{};
+    a.act = reinterpret_cast<float *>(act);
+    a.gate = reinterpret_cast<const float *>(gate);
+    a.up = reinterpret_cast<const float *>(up);
+    a.len = (long long)len;
+    return launch(c, F_SILU_MUL, (unsigned)ceil_div((long long)len, 256), 256, 0, &a, sizeof a);
+}
+
+int q8_matmul_decode_group(q8_ctx *c, const q8_group_entry *group, int count, q8_dptr x, size_t x_offset, int k,
+                           q8_dptr bias, size_t bias_offset) {
+    if (!c || !group) return fail(Q8_ERR_INVALID, "q8_matmul_decode_group: bad arguments");
+    if (count < 1 || count > Q8_GROUP_MAX)
+        return fail(Q8_ERR_INVALID, "decode matmul group holds one to four matrices (got %d)", count);
+    if (bias && count != 1) return fail(Q8_ERR_INVALID, "a residual add belongs to a single-matrix group");
+    Q8_TRY(check_k(k));
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    Member m[Q8_GROUP_MAX];
+    for (int i = 0; i < count; i++) {
+        Q8_TRY(check_weight(c, group[i].weight));
+        if (group[i].weight->k != k) return fail(Q8_ERR_INVALID, "group member %d has k = %d, not %d", i, group[i].weight->k, k);
+        m[i].w = group[i].weight;
+        m[i].y = fptr(group[i].y, group[i].y_offset);
+        Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)m[i].y, (size_t)m[i].w->out * 4, "decode y"));
+    }
+    const q8_dptr xp = (q8_dptr)(uintptr_t)fptr(x, x_offset);
+    Q8_TRY(check_span(c, xp, (size_t)k * 4, "decode x"));
+    const float *b = fptr(bias, bias_offset);
+    if (b) Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)b, (size_t)m[0].w->out * 4, "decode bias"));
+    return run_gemv(c, m, count, xp, k, b, 0);
+}
+
+int q8_matmul_prompt_group(q8_ctx *c, const q8_group_entry *group, int count, const q8_prepared *prepared, int n,
+                           int k, q8_dptr bias, size_t bias_offset) {
+    if (!c || !group || !prepared) return fail(Q8_ERR_INVALID, "q8_matmul_prompt_group: bad arguments");
+    if (count < 1 || count > Q8_GROUP_MAX)
+        return fail(Q8_ERR_INVALID, "prompt matmul group holds one to four matrices (got %d)", count);
+    if (bias && count != 1) return fail(Q8_ERR_INVALID, "a residual add belongs to a single-matrix group");
+    Q8_TRY(check_k(k));
+    Q8_TRY(check_n(n));
+    if (prepared->n != n || prepared->k != k)
+        return fail(Q8_ERR_INVALID, "prepared activations are %d x %d, the matmul wants %d x %d", prepared->n,
+                    prepared->k, n, k);
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    Member m[Q8_GROUP_MAX];
+    for (int i = 0; i < count; i++) {
+        Q8_TRY(check_weight(c, group[i].weight));
+        if (group[i].weight->k != k) return fail(Q8_ERR_INVALID, "group member %d has k = %d, not %d", i, group[i].weight->k, k);
+        m[i].w = group[i].weight;
+        m[i].y = fptr(group[i].y, group[i].y_offset);
+        Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)m[i].y, (size_t)n * m[i].w->out * 4, "prompt y"));
+    }
+    const float *b = fptr(bias, bias_offset);
+    if (b) Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)b, (size_t)n * m[0].w->out * 4, "prompt bias"));
+    return run_gemm(c, m, count, prepared, n, b);
+}
+
+int q8_matmul(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset, int n, q8_dptr y, size_t y_offset,
+              const q8_prepared *prepared, q8_dptr bias, size_t bias_offset) {
+    if (!c) return fail(Q8_ERR_INVALID, "q8_matmul: null context");
+    Q8_TRY(check_weight(c, w));
+    Q8_TRY(check_n(n));
+    q8_group_entry e{w, y, y_offset};
+    if (n == 1) return q8_matmul_decode_group(c, &e, 1, x, x_offset, w->k, bias, bias_offset);
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    q8_prepared own{};
+    if (!prepared) {
+        Q8_TRY(q8_prepare(c, x, x_offset, n, w->k, &own));
+        prepared = &own;
+    }
+    return q8_matmul_prompt_group(c, &e, 1, prepared, n, w->k, bias, bias_offset);
+}
+
+int q8_gate_up_silu(q8_ctx *c, const q8_weight *gate, const q8_weight *up, q8_dptr x, size_t x_offset, int n,
+                    q8_dptr act, size_t act_offset, q8_prepared *prepared) {
+    if (!c) return fail(Q8_ERR_INVALID, "q8_gate_up_silu: null context");
+    Q8_TRY(check_weight(c, gate));
+    Q8_TRY(check_weight(c, up));
+    Q8_TRY(check_n(n));
+    if (gate->k != up->k || gate->out != up->out)
+        return fail(Q8_ERR_INVALID, "gate is %d x %d but up is %d x %d", gate->out, gate->k, up->out, up->k);
+    const int k = gate->k, ffn = gate->out;
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    float *actp = fptr(act, act_offset);
+    Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)actp, (size_t)n * ffn * 4, "gate_up act"));
+    const q8_dptr xp = (q8_dptr)(uintptr_t)fptr(x, x_offset);
+    Q8_TRY(check_span(c, xp, (size_t)n * k * 4, "gate_up x"));
+    if (n == 1) {
+        q8_tactic t = plan(c, 1, ffn, k);
+        if (t.waves_per_tile > 4) fit_gemv_waves(&t, (k / 32 + 1) / 2, 4);
+        if (t.pairs_per_wave <= 12) {
+            Member m[2] = {{gate, actp}, {up, nullptr}};
+            Q8_TRY(run_gemv(c, m, 2, xp, k, nullptr, 1));
+            if (prepared) Q8_TRY(prepare_into(c, (q8_dptr)(uintptr_t)actp, 0, 0, 1, ffn, prepared));
+            return Q8_OK;
+        }
+    }
+    // gate and up products in f32 workspace, then the SiLU product.
+    const size_t one = align_up((size_t)n * ffn * 4, kAlign);
+    Q8_TRY(grow(c, &c->tmp_ws, &c->tmp_ws_bytes, 2 * one, "hipMalloc(ffn workspace)"));
+    float *g = static_cast<float *>(c->tmp_ws);
+    float *u = reinterpret_cast<float *>(static_cast<uint8_t *>(c->tmp_ws) + one);
+    Member m[2] = {{gate, g}, {up, u}};
+    if (n == 1) {
+        Q8_TRY(run_gemv(c, m, 2, xp, k, nullptr, 0));
+    } else {
+        q8_prepared px{};
+        Q8_TRY(prepare_into(c, xp, 0, 0, n, k, &px));
+        Q8_TRY(run_gemm(c, m, 2, &px, n, nullptr));
+    }
+    Q8EltArgs a{};
+    a.act = actp;
+    a.gate = g;
+    a.up = u;
+    a.len = (long long)n * ffn;
+    Q8_TRY(launch(c, F_SILU_MUL, (unsigned)ceil_div(a.len, 256), 256, 0, &a, sizeof a));
+    if (prepared) Q8_TRY(prepare_into(c, 0, (q8_dptr)(uintptr_t)g, (q8_dptr)(uintptr_t)u, n, ffn, prepared));
+    return Q8_OK;
+}
+
+int q8_lm_head_argmax(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset, q8_dptr logits,
+                      size_t logits_offset, uint32_t *argmax) {
+    if (!c || !argmax) return fail(Q8_ERR_INVALID, "q8_lm_head_argmax: bad arguments");
+    Q8_TRY(check_weight(c, w));
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    q8_group_entry e{w, logits, logits_offset};
+    Q8_TRY(q8_matmul_decode_group(c, &e, 1, x, x_offset, w->k, 0, 0));
+    return argmax_into(c, (q8_dptr)(uintptr_t)fptr(logits, logits_offset), (size_t)w->out, argmax);
+}
+
+int q8_argmax(q8_ctx *c, q8_dptr values, size_t offset, size_t len, uint32_t *argmax) {
+    if (!c || !argmax) return fail(Q8_ERR_INVALID, "q8_argmax: bad arguments");
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    return argmax_into(c, (q8_dptr)(uintptr_t)fptr(values, offset), len, argmax);
+}
+
+int q8_plan(q8_ctx *c, int n, int out, int k, q8_tactic *t) {
+    if (!t) return fail(Q8_ERR_INVALID, "q8_plan: null output");
+    Q8_TRY(check_k(k));
+    Q8_TRY(check_n(n));
+    if (out <= 0) return fail(Q8_ERR_INVALID, "q8_plan: %d rows", out);
+    if (c) {
+        std::lock_guard<std::recursive_mutex> lock(c->mu);
+        *t = plan(c, n, out, k);
+        return Q8_OK;
+    }
+    return q8_tactics_choose(n, out, k, 256, t);
+}
+
+int q8_tactic_count(void) { return q8_tactics_table_size(); }
+
+int q8_tactic_row(int i, q8_tactic *t, int *rank, int *maturity) {
+    if (i < 0 || i >= q8_tactics_table_size() || !t) return fail(Q8_ERR_INVALID, "q8_tactic_row: index %d", i);
+    const Q8TacticRow &row = q8_tactics_row(i);
+    *t = q8_tactic{};
+    t->kernel = row.kernel;
+    t->name = row.name;
+    t->evidence = row.evidence;
+    if (rank) *rank = row.rank;
+    if (maturity) *maturity = row.maturity;
+    return Q8_OK;
+}
+
+int q8_event_create(q8_ctx *c, void **ev) {
+    if (!c || !ev) return fail(Q8_ERR_INVALID, "q8_event_create: bad arguments");
+    hipEvent_t e;
+    HIP_TRY(hipEventCreate(&e), "hipEventCreate");
+    *ev = (void *)e;
+    return Q8_OK;
+}
+
+int q8_event_record(q8_ctx *c, void *ev) {
+    if (!c || !ev) return fail(Q8_ERR_INVALID, "q8_event_record: bad arguments");
+    HIP_TRY(hipEventRecord((hipEvent_t)ev, c->stream), "hipEventRecord");
+    return Q8_OK;
+}
+
+int q8_event_elapsed_ms(void *start, void *end, float *ms) {
+    if (!start || !end || !ms) return fail(Q8_ERR_INVALID, "q8_event_elapsed_ms: bad arguments");
+    HIP_TRY(hipEventSynchronize((hipEvent_t)end), "hipEventSynchronize");
+    HIP_TRY(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)end), "hipEventElapsedTime");
+    return Q8_OK;
+}
+
+int q8_event_destroy(void *ev) {
+    if (!ev) return Q8_OK;
+    HIP_TRY(hipEventDestroy((hipEvent_t)ev), "hipEventDestroy");
+    return Q8_OK;
+}
+
+int q8_graph_begin(q8_ctx *c) {
+    if (!c) return fail(Q8_ERR_INVALID, "q8_graph_begin: null context");
+    HIP_TRY(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    return Q8_OK;
+}
+
+int q8_graph_end(q8_ctx *c, void **graph) {
+    if (!c || !graph) return fail(Q8_ERR_INVALID, "q8_graph_end: bad arguments");
+    hipGraph_t g = nullptr;
+    HIP_TRY(hipStreamEndCapture(c->stream, &g), "hipStreamEndCapture");
+    hipGraphExec_t ge = nullptr;
+    hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    *graph = (void *)ge;
+    return Q8_OK;
+}
+
+int q8_graph_launch(q8_ctx *c, void *graph) {
+    if (!c || !graph) return fail(Q8_ERR_INVALID, "q8_graph_launch: bad arguments");
+    HIP_TRY(hipGraphLaunch((hipGraphExec_t)graph, c->stream), "hipGraphLaunch");
+    return Q8_OK;
+}
+
+int q8_graph_destroy(void *graph) {
+    if (!graph) return Q8_OK;
+    HIP_TRY(hipGraphExecDestroy((hipGraphExec_t)graph), "hipGraphExecDestroy");
+    return Q8_OK;
+}
+
+}  // extern "C"

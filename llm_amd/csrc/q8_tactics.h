@@ -1,0 +1,30 @@
+// q8_tactics.h -- the shape-keyed matmul tactic table for gfx950.
+//
+// The reference keeps its kernel choices in a ranked table of tactics with
+// guards, a maturity and a line of evidence (apps/engine/src/tactics.rs:118-181,
+// 229-347), but its matmul regime switch is hard-coded (cuda/mod.rs:803-892).
+// Here the matmul choice is such a table: each row guards a regime (n range)
+// and derives its launch parameters from (n, out, k).
+#ifndef Q8_TACTICS_H
+#define Q8_TACTICS_H
+
+#include "../../include/q8mi.h"
+
+enum { Q8_MATURITY_REJECTED = 0, Q8_MATURITY_EXPERIMENTAL = 1, Q8_MATURITY_MEASURED = 2 };
+
+struct Q8TacticRow {
+    const char *name;
+    int kernel;
+    int n_min, n_max;
+    int maturity;
+    int rank;
+    const char *evidence;
+};
+
+// Number of CUs the launch heuristics size for (MI355X: 256).
+int q8_tactics_table_size();
+const Q8TacticRow &q8_tactics_row(int i);
+// Resolve the tactic for one matmul; cu_count sizes the grid heuristics.
+int q8_tactics_choose(int n, int out, int k, int cu_count, q8_tactic *t);
+
+#endif

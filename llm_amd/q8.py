@@ -1,0 +1,451 @@
+"""Python binding of libq8mi.so (include/q8mi.h) -- the test/bench host side.
+
+``Gpu`` wraps the C-ABI one to one (it is what a Rust ``hip/sys.rs`` would
+declare).  ``Compute`` mirrors the matmul entry points of
+the reference engine's ``Compute`` (apps/engine/src/compute.rs:376-581,
+931-1019) over device ``Activation``s, so the parity tests read like the
+reference's own (apps/engine/tests/gpu_matmul.rs:57-65):
+
+    compute.upload(source, x)
+    compute.matmul(weight, source, 0, n, target, 0)
+    compute.download(target, result)
+
+There is no CPU fallback anywhere in this module: if the native library is
+missing or no gfx950 device opens, every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libq8mi.so")
+
+Q8_OK = 0
+Q8_ERR_HIP = 1
+Q8_ERR_INVALID = 2
+Q8_ERR_UNSUPPORTED = 3
+Q8_ERR_NO_DEVICE = 4
+Q8_ERR_OUT_OF_MEMORY = 5
+MAX_TOKENS = 1024
+GROUP_MAX = 4
+KERNEL_GEMV = 1
+KERNEL_GEMM = 2
+
+# Every function include/q8mi.h declares (the ABI test checks the header
+# against this list and the library's exports).
+EXPORTS = (
+    "q8_status_string", "q8_last_error", "q8_build_info",
+    "q8_open", "q8_close", "q8_device_name", "q8_device_info", "q8_stream", "q8_set_option",
+    "q8_alloc", "q8_free", "q8_upload", "q8_download", "q8_sync",
+    "q8_weight_resident", "q8_weight_release", "q8_weight_shape", "q8_weight_export",
+    "q8_matmul", "q8_prepare", "q8_silu_mul_prepare", "q8_silu_mul",
+    "q8_matmul_decode_group", "q8_matmul_prompt_group", "q8_gate_up_silu",
+    "q8_lm_head_argmax", "q8_argmax",
+    "q8_plan", "q8_tactic_count", "q8_tactic_row",
+    "q8_event_create", "q8_event_record", "q8_event_elapsed_ms", "q8_event_destroy",
+    "q8_graph_begin", "q8_graph_end", "q8_graph_launch", "q8_graph_destroy",
+)
+
+
+class Q8Error(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{message} [status {status}]")
+        self.status = status
+        self.message = message
+
+
+class Prepared(ctypes.Structure):
+    """q8_prepared: quantized activations (the reference's ``Prepared``)."""
+    _fields_ = [("quants", ctypes.c_uint64), ("scales", ctypes.c_uint64),
+                ("n", ctypes.c_int), ("k", ctypes.c_int)]
+
+
+class _GroupEntry(ctypes.Structure):
+    _fields_ = [("weight", ctypes.c_void_p), ("y", ctypes.c_uint64), ("y_offset", ctypes.c_size_t)]
+
+
+class Tactic(ctypes.Structure):
+    _fields_ = [("kernel", ctypes.c_int), ("waves_per_tile", ctypes.c_int),
+                ("pairs_per_wave", ctypes.c_int), ("pairs_per_batch", ctypes.c_int),
+                ("exact", ctypes.c_int), ("tt_per_wg", ctypes.c_int), ("smode", ctypes.c_int),
+                ("xcd_remap", ctypes.c_int), ("name", ctypes.c_char_p), ("evidence", ctypes.c_char_p)]
+
+    def as_dict(self) -> dict:
+        d = {f: getattr(self, f) for f, _ in self._fields_}
+        d["name"] = (self.name or b"").decode()
+        d["evidence"] = (self.evidence or b"").decode()
+        return d
+
+
+_lib = None
+
+
+def library_path() -> str:
+    return LIB_PATH
+
+
+def lib():
+    """Load libq8mi.so; raises if it was not built (no fallback)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m llm_amd.build` "
+                           "(the Q8_0 path has no CPU fallback)")
+    L = ctypes.CDLL(LIB_PATH)
+    c_int, c_size, u64, vp = ctypes.c_int, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_void_p
+    sig = {
+        "q8_status_string": (ctypes.c_char_p, [c_int]),
+        "q8_last_error": (ctypes.c_char_p, []),
+        "q8_build_info": (ctypes.c_char_p, []),
+        "q8_open": (c_int, [c_int, ctypes.POINTER(vp)]),
+        "q8_close": (None, [vp]),
+        "q8_device_name": (c_int, [vp, ctypes.c_char_p, c_size]),
+        "q8_device_info": (c_int, [vp, ctypes.POINTER(c_int), ctypes.POINTER(c_size), ctypes.POINTER(c_size)]),
+        "q8_stream": (vp, [vp]),
+        "q8_set_option": (c_int, [vp, ctypes.c_char_p, c_int]),
+        "q8_alloc": (c_int, [vp, c_size, ctypes.POINTER(u64)]),
+        "q8_free": (c_int, [vp, u64]),
+        "q8_upload": (c_int, [vp, u64, vp, c_size]),
+        "q8_download": (c_int, [vp, vp, u64, c_size]),
+        "q8_sync": (c_int, [vp]),
+        "q8_weight_resident": (c_int, [vp, vp, c_size, c_int, c_int, ctypes.POINTER(vp)]),
+        "q8_weight_release": (c_int, [vp, vp]),
+        "q8_weight_shape": (c_int, [vp, ctypes.POINTER(c_int), ctypes.POINTER(c_int), ctypes.POINTER(c_size)]),
+        "q8_weight_export": (c_int, [vp, vp, vp, c_size]),
+        "q8_matmul": (c_int, [vp, vp, u64, c_size, c_int, u64, c_size, ctypes.POINTER(Prepared), u64, c_size]),
+        "q8_prepare": (c_int, [vp, u64, c_size, c_int, c_int, ctypes.POINTER(Prepared)]),
+        "q8_silu_mul_prepare": (c_int, [vp, u64, u64, c_int, c_int, ctypes.POINTER(Prepared)]),
+        "q8_silu_mul": (c_int, [vp, u64, u64, u64, c_size]),
+        "q8_matmul_decode_group": (c_int, [vp, ctypes.POINTER(_GroupEntry), c_int, u64, c_size, c_int, u64, c_size]),
+        "q8_matmul_prompt_group": (c_int, [vp, ctypes.POINTER(_GroupEntry), c_int, ctypes.POINTER(Prepared),
+                                           c_int, c_int, u64, c_size]),
+        "q8_gate_up_silu": (c_int, [vp, vp, vp, u64, c_size, c_int, u64, c_size, ctypes.POINTER(Prepared)]),
+        "q8_lm_head_argmax": (c_int, [vp, vp, u64, c_size, u64, c_size, ctypes.POINTER(ctypes.c_uint32)]),
+        "q8_argmax": (c_int, [vp, u64, c_size, c_size, ctypes.POINTER(ctypes.c_uint32)]),
+        "q8_plan": (c_int, [vp, c_int, c_int, c_int, ctypes.POINTER(Tactic)]),
+        "q8_tactic_count": (c_int, []),
+        "q8_tactic_row": (c_int, [c_int, ctypes.POINTER(Tactic), ctypes.POINTER(c_int), ctypes.POINTER(c_int)]),
+        "q8_event_create": (c_int, [vp, ctypes.POINTER(vp)]),
+        "q8_event_record": (c_int, [vp, vp]),
+        "q8_event_elapsed_ms": (c_int, [vp, vp, ctypes.POINTER(ctypes.c_float)]),
+        "q8_event_destroy": (c_int, [vp]),
+        "q8_graph_begin": (c_int, [vp]),
+        "q8_graph_end": (c_int, [vp, ctypes.POINTER(vp)]),
+        "q8_graph_launch": (c_int, [vp, vp]),
+        "q8_graph_destroy": (c_int, [vp]),
+    }
+    assert set(sig) == set(EXPORTS)
+    for name, (res, args) in sig.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+    _lib = L
+    return L
+
+
+def _check(status: int):
+    if status != Q8_OK:
+        msg = lib().q8_last_error().decode(errors="replace")
+        raise Q8Error(status, msg or lib().q8_status_string(status).decode())
+
+
+def build_info() -> str:
+    return lib().q8_build_info().decode()
+
+
+def tactic_table() -> list[dict]:
+    out = []
+    for i in range(lib().q8_tactic_count()):
+        t, rank, maturity = Tactic(), ctypes.c_int(), ctypes.c_int()
+        _check(lib().q8_tactic_row(i, ctypes.byref(t), ctypes.byref(rank), ctypes.byref(maturity)))
+        d = t.as_dict()
+        d["rank"] = rank.value
+        d["maturity"] = maturity.value
+        out.append(d)
+    return out
+
+
+def plan(n: int, out: int, k: int, gpu: "Gpu | None" = None) -> dict:
+    t = Tactic()
+    _check(lib().q8_plan(gpu.handle if gpu else None, n, out, k, ctypes.byref(t)))
+    return t.as_dict()
+
+
+class DeviceBuffer:
+    """A q8_alloc'd device allocation (the reference's ``DeviceBuffer`` of f32,
+    cuda/mod.rs:123-182); ``len`` counts f32 elements."""
+
+    def __init__(self, gpu: "Gpu", nbytes: int):
+        self.gpu = gpu
+        self.nbytes = int(nbytes)
+        p = ctypes.c_uint64()
+        _check(lib().q8_alloc(gpu.handle, self.nbytes, ctypes.byref(p)))
+        self.ptr = p.value
+
+    def __len__(self):
+        return self.nbytes // 4
+
+    def free(self):
+        if self.ptr and self.gpu.handle:
+            _check(lib().q8_free(self.gpu.handle, self.ptr))
+        self.ptr = 0
+
+    def upload(self, values: np.ndarray, offset_bytes: int = 0):
+        a = np.ascontiguousarray(values)
+        assert offset_bytes + a.nbytes <= self.nbytes, "upload overruns the buffer"
+        _check(lib().q8_upload(self.gpu.handle, self.ptr + offset_bytes, a.ctypes.data, a.nbytes))
+
+    def download(self, dtype=np.float32, count: int | None = None, offset_bytes: int = 0) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        if count is None:
+            count = (self.nbytes - offset_bytes) // dtype.itemsize
+        out = np.empty(count, dtype=dtype)
+        assert offset_bytes + out.nbytes <= self.nbytes, "download overruns the buffer"
+        _check(lib().q8_download(self.gpu.handle, out.ctypes.data, self.ptr + offset_bytes, out.nbytes))
+        return out
+
+
+class Weight:
+    """A host Q8_0 matrix ``out x k`` (the reference's ``Weight``,
+    tensor.rs:15-51): GGUF bytes plus shape.  Its identity (address, length)
+    keys the device residency cache, so the bytes are kept alive here."""
+
+    def __init__(self, data: np.ndarray, k: int, out: int):
+        data = np.ascontiguousarray(data, dtype=np.uint8).reshape(-1)
+        if k % 32 != 0 or data.size != out * (k // 32) * 34:
+            raise ValueError("weight byte length mismatch")
+        self.data, self.k, self.out = data, int(k), int(out)
+
+    def identity(self):
+        return (self.data.ctypes.data, self.data.nbytes)
+
+
+class Gpu:
+    """The C-ABI context: Gpu::open / Drop (cuda/mod.rs:363-522, 1981-1993)."""
+
+    def __init__(self, device: int = 0):
+        h = ctypes.c_void_p()
+        _check(lib().q8_open(device, ctypes.byref(h)))
+        self.handle = h.value
+        self._resident = {}
+
+    def close(self):
+        if self.handle:
+            lib().q8_close(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @property
+    def name(self) -> str:
+        buf = ctypes.create_string_buffer(256)
+        _check(lib().q8_device_name(self.handle, buf, 256))
+        return buf.value.decode()
+
+    def info(self) -> dict:
+        cu, tot, fr = ctypes.c_int(), ctypes.c_size_t(), ctypes.c_size_t()
+        _check(lib().q8_device_info(self.handle, ctypes.byref(cu), ctypes.byref(tot), ctypes.byref(fr)))
+        return {"cu_count": cu.value, "total_bytes": tot.value, "free_bytes": fr.value}
+
+    def set_option(self, name: str, value: int):
+        _check(lib().q8_set_option(self.handle, name.encode(), int(value)))
+
+    def alloc(self, nbytes: int) -> DeviceBuffer:
+        return DeviceBuffer(self, nbytes)
+
+    def sync(self):
+        _check(lib().q8_sync(self.handle))
+
+    def resident(self, weight: Weight):
+        """Gpu::quantized: upload + repack once, cached by identity."""
+        h = ctypes.c_void_p()
+        _check(lib().q8_weight_resident(self.handle, weight.data.ctypes.data, weight.data.nbytes,
+                                        weight.k, weight.out, ctypes.byref(h)))
+        self._resident[weight.identity()] = weight  # keep the host bytes alive
+        return h.value
+
+    def release(self, weight: Weight):
+        h = self.resident(weight)
+        _check(lib().q8_weight_release(self.handle, h))
+        self._resident.pop(weight.identity(), None)
+
+    def export(self, weight: Weight) -> np.ndarray:
+        h = self.resident(weight)
+        out = np.empty(weight.data.nbytes, dtype=np.uint8)
+        _check(lib().q8_weight_export(self.handle, h, out.ctypes.data, out.nbytes))
+        return out
+
+    def matmul(self, weight: Weight, x: DeviceBuffer, x_offset: int, n: int, y: DeviceBuffer,
+               y_offset: int, prepared: Prepared | None = None, bias: DeviceBuffer | None = None,
+               bias_offset: int = 0):
+        h = self.resident(weight)
+        _check(lib().q8_matmul(self.handle, h, x.ptr, x_offset, n, y.ptr, y_offset,
+                               ctypes.byref(prepared) if prepared is not None else None,
+                               bias.ptr if bias is not None else 0, bias_offset))
+
+    def prepare(self, x: DeviceBuffer, x_offset: int, n: int, k: int) -> Prepared:
+        p = Prepared()
+        _check(lib().q8_prepare(self.handle, x.ptr, x_offset, n, k, ctypes.byref(p)))
+        return p
+
+    def silu_mul_prepare(self, gate: DeviceBuffer, up: DeviceBuffer, n: int, k: int) -> Prepared:
+        p = Prepared()
+        _check(lib().q8_silu_mul_prepare(self.handle, gate.ptr, up.ptr, n, k, ctypes.byref(p)))
+        return p
+
+    def silu_mul(self, act: DeviceBuffer, gate: DeviceBuffer, up: DeviceBuffer, length: int):
+        _check(lib().q8_silu_mul(self.handle, act.ptr, gate.ptr, up.ptr, length))
+
+    def _group(self, members):
+        arr = (_GroupEntry * len(members))()
+        for i, (w, y, y_off) in enumerate(members):
+            arr[i].weight = self.resident(w)
+            arr[i].y = y.ptr
+            arr[i].y_offset = y_off
+        return arr
+
+    def matmul_decode_group(self, members, x: DeviceBuffer, x_offset: int, k: int,
+                            bias: DeviceBuffer | None = None, bias_offset: int = 0):
+        arr = self._group(members)
+        _check(lib().q8_matmul_decode_group(self.handle, arr, len(members), x.ptr, x_offset, k,
+                                            bias.ptr if bias is not None else 0, bias_offset))
+
+    def matmul_prompt_group(self, members, prepared: Prepared, n: int, k: int,
+                            bias: DeviceBuffer | None = None, bias_offset: int = 0):
+        arr = self._group(members)
+        _check(lib().q8_matmul_prompt_group(self.handle, arr, len(members), ctypes.byref(prepared), n, k,
+                                            bias.ptr if bias is not None else 0, bias_offset))
+
+    def gate_up_silu(self, gate: Weight, up: Weight, x: DeviceBuffer, x_offset: int, n: int,
+                     act: DeviceBuffer, act_offset: int, want_prepared: bool = False):
+        p = Prepared()
+        _check(lib().q8_gate_up_silu(self.handle, self.resident(gate), self.resident(up), x.ptr, x_offset,
+                                     n, act.ptr, act_offset, ctypes.byref(p) if want_prepared else None))
+        return p if want_prepared else None
+
+    def lm_head_argmax(self, weight: Weight, x: DeviceBuffer, x_offset: int, logits: DeviceBuffer,
+                       logits_offset: int) -> int:
+        out = ctypes.c_uint32()
+        _check(lib().q8_lm_head_argmax(self.handle, self.resident(weight), x.ptr, x_offset, logits.ptr,
+                                       logits_offset, ctypes.byref(out)))
+        return int(out.value)
+
+    def argmax(self, values: DeviceBuffer, offset: int, length: int) -> int:
+        out = ctypes.c_uint32()
+        _check(lib().q8_argmax(self.handle, values.ptr, offset, length, ctypes.byref(out)))
+        return int(out.value)
+
+    def plan(self, n: int, out: int, k: int) -> dict:
+        return plan(n, out, k, self)
+
+    # ---- timing and graphs ----
+    def event(self):
+        e = ctypes.c_void_p()
+        _check(lib().q8_event_create(self.handle, ctypes.byref(e)))
+        return e.value
+
+    def record(self, event):
+        _check(lib().q8_event_record(self.handle, event))
+
+    @staticmethod
+    def elapsed_ms(start, end) -> float:
+        ms = ctypes.c_float()
+        _check(lib().q8_event_elapsed_ms(start, end, ctypes.byref(ms)))
+        return float(ms.value)
+
+    @staticmethod
+    def destroy_event(event):
+        _check(lib().q8_event_destroy(event))
+
+    def graph_begin(self):
+        _check(lib().q8_graph_begin(self.handle))
+
+    def graph_end(self):
+        g = ctypes.c_void_p()
+        _check(lib().q8_graph_end(self.handle, ctypes.byref(g)))
+        return g.value
+
+    def graph_launch(self, graph):
+        _check(lib().q8_graph_launch(self.handle, graph))
+
+    @staticmethod
+    def graph_destroy(graph):
+        _check(lib().q8_graph_destroy(graph))
+
+
+@dataclass
+class GroupMember:
+    """compute.rs:62-66: one matmul of a group sharing its activations."""
+    weight: Weight
+    out: DeviceBuffer
+    out_offset: int = 0
+
+
+class Compute:
+    """The matmul surface of the reference's ``Compute`` on the device
+    (compute.rs:376-581, 931-1019).  Activations are device buffers of f32;
+    offsets and lengths are in f32 elements, as in the reference."""
+
+    # Below this many tokens the reference's prepare is a no-op (tactics.rs:194);
+    # here every n >= 2 runs the quantized GEMM, so preparing pays from n = 2.
+    prepare_min_tokens = 2
+
+    def __init__(self, gpu: Gpu):
+        self.gpu = gpu
+
+    def device_name(self) -> str:
+        return self.gpu.name
+
+    def alloc(self, length: int) -> DeviceBuffer:
+        return self.gpu.alloc(4 * int(length))
+
+    def upload(self, buf: DeviceBuffer, values: np.ndarray):
+        buf.upload(np.ascontiguousarray(values, dtype=np.float32))
+
+    def download(self, buf: DeviceBuffer, out: np.ndarray):
+        out[...] = buf.download(np.float32, out.size).reshape(out.shape)
+
+    def prepare(self, x, x_offset, n, k):
+        if n < self.prepare_min_tokens:
+            return None
+        return self.gpu.prepare(x, x_offset, n, k)
+
+    def matmul(self, weight, x, x_offset, n, y, y_offset):
+        self.gpu.matmul(weight, x, x_offset, n, y, y_offset)
+
+    def matmul_prepared(self, weight, x, x_offset, prepared, n, y, y_offset):
+        self.gpu.matmul(weight, x, x_offset, n, y, y_offset, prepared=prepared)
+
+    def matmul_prepared_group(self, members, x, x_offset, prepared, n):
+        """compute.rs:437-472: one launch for up to four matrices."""
+        k = members[0].weight.k
+        entries = [(m.weight, m.out, m.out_offset) for m in members]
+        if n == 1:
+            self.gpu.matmul_decode_group(entries, x, x_offset, k)
+        else:
+            if prepared is None:
+                prepared = self.gpu.prepare(x, x_offset, n, k)
+            self.gpu.matmul_prompt_group(entries, prepared, n, k)
+
+    def matmul_add(self, weight, x, x_offset, prepared, n, y, y_offset, temp=None):
+        """compute.rs:537-581: y += W x with the residual in the epilogue."""
+        self.gpu.matmul(weight, x, x_offset, n, y, y_offset, prepared=prepared, bias=y, bias_offset=y_offset)
+
+    def silu_mul(self, act, gate, up, length):
+        self.gpu.silu_mul(act, gate, up, length)
+
+    def silu_mul_prepare(self, act, gate, up, n, k):
+        """compute.rs:993-1019."""
+        if n < self.prepare_min_tokens:
+            self.gpu.silu_mul(act, gate, up, n * k)
+            return None
+        return self.gpu.silu_mul_prepare(gate, up, n, k)

@@ -1,0 +1,121 @@
+"""CPU checks of the C-ABI library: it loads, exports exactly what
+include/q8mi.h declares, carries its build identity, and its host logic (the
+tactic table, argument validation before any device work) behaves."""
+import json
+import os
+import re
+import subprocess
+
+import pytest
+
+import llm_amd
+from llm_amd import q8
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "q8mi.h")
+
+
+def header_functions() -> set[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(q8_[a-z0-9_]+)\s*\(", text))
+
+
+def library_exports() -> set[str]:
+    out = subprocess.run(["nm", "-D", "--defined-only", q8.library_path()], stdout=subprocess.PIPE,
+                         text=True, check=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if " T " in line}
+
+
+def test_library_loads():
+    assert q8.lib() is not None
+
+
+def test_every_declared_function_is_exported():
+    declared = header_functions()
+    exported = library_exports()
+    assert declared, "no declarations parsed from the header"
+    missing = declared - exported
+    assert not missing, f"declared but not exported: {sorted(missing)}"
+    extra = {s for s in exported if s.startswith("q8_")} - declared
+    assert not extra, f"exported but not declared: {sorted(extra)}"
+    assert declared == set(q8.EXPORTS)
+
+
+def test_build_identity_names_its_artifact():
+    info = json.loads(llm_amd.build_info())
+    assert info["arch"] == "gfx950"
+    assert len(info["code_object_sha256"]) == 64
+    assert len(info["kernel_source_sha256"]) == 64
+    for k in ("q8_repack", "q8_quantize", "q8_gemm_s1", "q8_gemv_pb5_e1", "q8_argmax", "q8_silu_mul"):
+        assert k in info["kernels"]
+    assert "-ffp-contract=off" in info["hipcc_flags"]
+
+
+def test_status_strings():
+    L = q8.lib()
+    for code in range(6):
+        assert L.q8_status_string(code).decode()
+    assert L.q8_status_string(0).decode() == "ok"
+
+
+def test_open_without_a_device_fails_cleanly():
+    if os.path.exists("/dev/kfd"):
+        pytest.skip("a GPU driver is present")
+    with pytest.raises(q8.Q8Error) as err:
+        q8.Gpu(0)
+    assert err.value.status == q8.Q8_ERR_NO_DEVICE
+
+
+# ---- tactic table invariants (the reference's, tactics.rs:453-501) ----
+
+def test_tactic_table_invariants():
+    rows = llm_amd.tactic_table()
+    assert rows
+    for row in rows:
+        assert len(row["evidence"]) > 40, row["name"]
+        if row["maturity"] != 0:
+            assert row["rank"] > 0, row["name"]
+    names = [r["name"] for r in rows]
+    assert len(names) == len(set(names))
+
+
+@pytest.mark.parametrize("n,out,k", [(1, 5760, 2304), (1, 122880, 2304), (1, 2304, 5760), (1, 4, 32),
+                                     (1, 33, 96), (2, 64, 64), (8, 5760, 2304), (64, 5760, 2304),
+                                     (512, 11520, 2304), (1024, 2304, 5760)])
+def test_plan_never_selects_a_rejected_tactic(n, out, k):
+    rejected = {r["name"] for r in llm_amd.tactic_table() if r["maturity"] == 0}
+    t = llm_amd.plan(n, out, k)
+    assert t["name"] not in rejected
+    if n == 1:
+        assert t["kernel"] == q8.KERNEL_GEMV
+        nb = k // 32
+        npairs = (nb + 1) // 2
+        assert 1 <= t["pairs_per_wave"] <= 12
+        assert t["waves_per_tile"] * t["pairs_per_wave"] >= npairs
+        assert (t["waves_per_tile"] - 1) * t["pairs_per_wave"] < npairs  # no empty wave
+        assert t["waves_per_tile"] * 64 <= 512
+        assert t["pairs_per_batch"] in (2, 3, 5, 9)
+    else:
+        assert t["kernel"] == q8.KERNEL_GEMM
+        assert 1 <= t["tt_per_wg"] <= 4
+
+
+def test_plan_rejects_bad_shapes():
+    with pytest.raises(q8.Q8Error) as e:
+        llm_amd.plan(1, 10, 33)
+    assert e.value.status == q8.Q8_ERR_INVALID
+    with pytest.raises(q8.Q8Error) as e:
+        llm_amd.plan(1025, 10, 32)
+    assert e.value.status == q8.Q8_ERR_UNSUPPORTED
+    with pytest.raises(q8.Q8Error) as e:
+        llm_amd.plan(0, 10, 32)
+    assert e.value.status == q8.Q8_ERR_INVALID
+
+
+def test_weight_view_checks_its_byte_length():
+    import numpy as np
+    with pytest.raises(ValueError):
+        q8.Weight(np.zeros(33, np.uint8), 32, 1)
+    w = q8.Weight(np.zeros(68, np.uint8), 32, 2)
+    assert w.identity()[1] == 68

@@ -1,0 +1,553 @@
+"""GPU parity of the HIP Q8_0 path against the CPU oracle, through the C-ABI.
+
+Bars:
+  * integer/byte work bit-exact: the device weight layout (round trip), the
+    quantized activations (q and scales), the int32 block dot;
+  * f32 outputs within |d| <= 2e-6 + 1e-5*|ref| (TOL_ABS, TOL_REL below);
+  * n = 1 with gemv.exact = 1: bit-identical to the reference's AVX2 order
+    when the host oracle takes that order (it does on AVX2+FMA hosts);
+  * lm_head: identical argmax.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from llm_amd import q8
+
+pytestmark = pytest.mark.gpu
+
+TOL_ABS = 2e-6
+TOL_REL = 1e-5
+SEED = 0x5EED
+J = [[0, 4, 1, 5], [2, 6, 3, 7]]
+
+
+def assert_close(got, ref, what):
+    got = np.asarray(got, np.float32)
+    ref = np.asarray(ref, np.float32)
+    assert got.shape == ref.shape, f"{what}: shape {got.shape} vs {ref.shape}"
+    d = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+    bound = TOL_ABS + TOL_REL * np.abs(ref.astype(np.float64))
+    bad = ~(d <= bound)
+    if bad.any():
+        i = int(np.flatnonzero(bad.reshape(-1))[0])
+        raise AssertionError(f"{what}: {int(bad.sum())} of {bad.size} outside tolerance; max|d| = "
+                             f"{float(np.nanmax(d)):.3e}; first at {i}: got {got.reshape(-1)[i]!r} "
+                             f"ref {ref.reshape(-1)[i]!r}")
+
+
+def assert_bits(got, ref, what):
+    got = np.ascontiguousarray(got, np.float32)
+    ref = np.ascontiguousarray(ref, np.float32)
+    diff = got.view(np.uint32) != ref.view(np.uint32)
+    if diff.any():
+        i = int(np.flatnonzero(diff.reshape(-1))[0])
+        raise AssertionError(f"{what}: {int(diff.sum())} of {diff.size} not bit-identical; first at {i}: "
+                             f"got {got.reshape(-1)[i]!r} ref {ref.reshape(-1)[i]!r}")
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    g = q8.Gpu(0)
+    print(f"\ndevice: {g.name}", flush=True)
+    yield g
+    g.close()
+
+
+@pytest.fixture(autouse=True)
+def default_options(gpu):
+    yield
+    for name in ("gemv.exact", "gemv.waves", "gemv.pairs", "gemm.smode", "gemm.tt_per_wg", "gemm.xcd_remap"):
+        gpu.set_option(name, -1)
+
+
+def rng(i=0):
+    return np.random.default_rng(SEED + i)
+
+
+def weight(r, out, k, **kw):
+    return q8.Weight(oracle.make_q8_weight(r, out, k, **kw), k, out)
+
+
+def run_matmul(gpu, w, x, n, bias=None):
+    k, out = w.k, w.out
+    xb = gpu.alloc(4 * n * k)
+    yb = gpu.alloc(4 * n * out)
+    xb.upload(x.astype(np.float32))
+    bb = None
+    if bias is not None:
+        yb.upload(bias.astype(np.float32))
+        bb = yb
+    gpu.matmul(w, xb, 0, n, yb, 0, bias=bb)
+    y = yb.download(np.float32, n * out).reshape(n, out)
+    xb.free()
+    yb.free()
+    return y
+
+
+def unpack_prepared(gpu, p, n, k):
+    """Download a prepared buffer and undo the lane-order layout
+    (llm_amd/csrc/q8_layout.h) into [n][k] int8 and [n][k/32] f32."""
+    nb = k // 32
+    tt = (n + 31) // 32
+    qraw = np.empty(tt * nb * 1024, np.uint8)
+    sraw = np.empty(tt * nb * 32, np.float32)
+    q8._check(q8.lib().q8_download(gpu.handle, qraw.ctypes.data, p.quants, qraw.nbytes))
+    q8._check(q8.lib().q8_download(gpu.handle, sraw.ctypes.data, p.scales, sraw.nbytes))
+    qv = qraw.view(np.int8).reshape(tt, nb, 2, 32, 16)
+    out = np.zeros((tt, 32, nb, 32), np.int8)
+    for h in range(2):
+        for pp in range(16):
+            e = 8 * (pp % 4) + J[h][pp // 4]
+            out[:, :, :, e] = qv[:, :, h, :, pp].transpose(0, 2, 1)
+    q = out.reshape(tt * 32, nb * 32)
+    s = sraw.reshape(tt, nb, 32).transpose(0, 2, 1).reshape(tt * 32, nb)
+    return q, s
+
+
+# ---------------------------------------------------------------------------
+# weight residency: the device tile layout is a byte-exact re-arrangement
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("out,k", [(1, 32), (4, 64), (33, 96), (100, 2304), (2304, 5760), (5760, 2304)])
+def test_weight_layout_round_trips_byte_exact(gpu, out, k):
+    w = weight(rng(1), out, k)
+    back = gpu.export(w)
+    assert np.array_equal(back, w.data)
+    gpu.release(w)
+
+
+def test_weight_cache_is_keyed_by_identity(gpu):
+    w = weight(rng(2), 64, 64)
+    a = gpu.resident(w)
+    b = gpu.resident(w)
+    assert a == b
+    w2 = q8.Weight(w.data.copy(), 64, 64)
+    assert gpu.resident(w2) != a
+    gpu.release(w)
+    gpu.release(w2)
+
+
+# ---------------------------------------------------------------------------
+# n = 1 GEMV (tensor.rs:96-101)
+# ---------------------------------------------------------------------------
+
+def test_gemv_configs0_matches_the_reference_bit_for_bit(gpu):
+    """W 5760 x 2304, x ~ N(0,1), y f32[5760]."""
+    r = rng(10)
+    w = weight(r, 5760, 2304)
+    x = r.standard_normal(2304, dtype=np.float32)
+    ref = oracle.matmul(w.data, 2304, 5760, x, 1).reshape(-1)
+    got = run_matmul(gpu, w, x, 1).reshape(-1)
+    assert_close(got, ref, "gemv configs[0]")
+    if oracle.simd_path() == "avx2+fma":
+        assert_bits(got, ref, "gemv configs[0] (AVX2 order)")
+    gpu.release(w)
+
+
+@pytest.mark.parametrize("out,k", [(1, 32), (4, 32), (33, 96), (64, 64), (100, 1056), (257, 2304),
+                                   (2304, 5760), (96, 224)])
+@pytest.mark.parametrize("exact", [1, 0])
+def test_gemv_shapes(gpu, out, k, exact):
+    gpu.set_option("gemv.exact", exact)
+    r = rng(11 + out + k)
+    w = weight(r, out, k)
+    x = r.standard_normal(k, dtype=np.float32)
+    ref = oracle.matmul(w.data, k, out, x, 1).reshape(-1)
+    got = run_matmul(gpu, w, x, 1).reshape(-1)
+    assert_close(got, ref, f"gemv {out}x{k} exact={exact}")
+    if exact and oracle.simd_path() == "avx2+fma":
+        assert_bits(got, ref, f"gemv {out}x{k}")
+    gpu.release(w)
+
+
+@pytest.mark.parametrize("waves,pairs", [(1, 9), (2, 5), (3, 3), (4, 2), (6, 2), (8, 5)])
+def test_gemv_launch_shapes_agree(gpu, waves, pairs):
+    """Every (waves per tile, pairs per batch) split gives the same bits."""
+    gpu.set_option("gemv.waves", waves)
+    gpu.set_option("gemv.pairs", pairs)
+    r = rng(12)
+    w = weight(r, 320, 768)
+    x = r.standard_normal(768, dtype=np.float32)
+    ref = oracle.matmul(w.data, 768, 320, x, 1).reshape(-1)
+    got = run_matmul(gpu, w, x, 1).reshape(-1)
+    if oracle.simd_path() == "avx2+fma":
+        assert_bits(got, ref, f"gemv waves={waves} pairs={pairs}")
+    else:
+        assert_close(got, ref, f"gemv waves={waves} pairs={pairs}")
+    gpu.release(w)
+
+
+def test_gemv_subnormal_and_special_scales(gpu):
+    r = rng(13)
+    out, k = 64, 256
+    blocks = out * k // 32
+    scales = np.abs(r.standard_normal(blocks)).astype(np.float32) * 1e-6  # all f16 subnormal
+    scales[::7] = 0.0
+    scales[1::11] = 6e-8  # the smallest subnormal
+    w = weight(r, out, k, scales=scales)
+    x = r.standard_normal(k, dtype=np.float32)
+    ref = oracle.matmul(w.data, k, out, x, 1).reshape(-1)
+    got = run_matmul(gpu, w, x, 1).reshape(-1)
+    assert_close(got, ref, "gemv subnormal scales")
+    if oracle.simd_path() == "avx2+fma":
+        assert_bits(got, ref, "gemv subnormal scales")
+    gpu.release(w)
+
+
+def test_gemv_residual_epilogue_is_matmul_add(gpu):
+    """compute.rs:537-581: y += W x, the add fused in the epilogue."""
+    r = rng(14)
+    w = weight(r, 2304, 2304)
+    x = r.standard_normal(2304, dtype=np.float32)
+    y0 = r.standard_normal(2304, dtype=np.float32)
+    ref = y0 + oracle.matmul(w.data, 2304, 2304, x, 1).reshape(-1)
+    got = run_matmul(gpu, w, x, 1, bias=y0).reshape(-1)
+    assert_close(got, ref, "gemv residual")
+    if oracle.simd_path() == "avx2+fma":
+        assert_bits(got, ref, "gemv residual")
+    gpu.release(w)
+
+
+def test_decode_group_matches_separate_matmuls(gpu):
+    """cuda/mod.rs:1482-1543: QKV-like group sharing x in one launch."""
+    r = rng(15)
+    k = 2304
+    ws = [weight(r, o, k) for o in (2304, 512, 768)]
+    x = r.standard_normal(k, dtype=np.float32)
+    xb = gpu.alloc(4 * k)
+    xb.upload(x)
+    ys = [gpu.alloc(4 * (w.out + 8)) for w in ws]
+    gpu.matmul_decode_group([(w, y, 8) for w, y in zip(ws, ys)], xb, 0, k)
+    for w, y in zip(ws, ys):
+        got = y.download(np.float32, w.out, offset_bytes=32)
+        ref = oracle.matmul(w.data, k, w.out, x, 1).reshape(-1)
+        assert_close(got, ref, f"group member {w.out}")
+        if oracle.simd_path() == "avx2+fma":
+            assert_bits(got, ref, f"group member {w.out}")
+        gpu.release(w)
+        y.free()
+    xb.free()
+
+
+# ---------------------------------------------------------------------------
+# activation quantization (quant.rs:98-121), byte-exact
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n,k", [(1, 32), (2, 64), (31, 2304), (33, 2304), (65, 5760)])
+def test_quantized_activations_are_bit_exact(gpu, n, k):
+    r = rng(20 + n)
+    x = oracle.make_activations(r, n, k, outlier_rate=0.01)
+    x[0, :32] = 0.0                                   # all-zero block
+    if k >= 64:
+        x[0, 32:64] = np.arange(32, dtype=np.float32) - 16.0
+        x[0, 32] = 127.0                              # inverse exactly 1: ties
+        x[0, 33:37] = [2.5, -2.5, 0.5, -0.5]
+    if n > 1:
+        x[1, 5] = np.nan                              # ignored by the peak, q = 0
+        x[1, 40 % k] = np.inf if k > 40 else x[1, 40 % k]
+    xb = gpu.alloc(4 * n * k)
+    xb.upload(x)
+    p = gpu.prepare(xb, 0, n, k)
+    q, s = unpack_prepared(gpu, p, n, k)
+    for t in range(n):
+        rq, rs = oracle.quantize_q8_0(x[t])
+        assert np.array_equal(q[t], rq), f"token {t}: quants differ"
+        assert np.array_equal(s[t].view(np.uint32), rs.view(np.uint32)), f"token {t}: scales differ"
+    tt = (n + 31) // 32
+    assert not q[n:tt * 32].any() and not s[n:tt * 32].any(), "padding tokens must be zero"
+    xb.free()
+
+
+# ---------------------------------------------------------------------------
+# n >= 2 MFMA GEMM (tensor.rs:104-148)
+# ---------------------------------------------------------------------------
+
+def exact_problem(r, out, k, n):
+    """Power-of-two scales, one per weight row and one per token, and
+    activations whose block peak is exactly 127 * s_x, so d_w*s_x is a power
+    of two, every quantized value is the integer itself, and (with k <= 1024,
+    |sum| < 2^24) every f32 step is exact: y must equal the integer sum."""
+    assert k <= 1024
+    nb = k // 32
+    qw = r.integers(-127, 128, size=(out, nb, 32))
+    ew = r.integers(-12, 0, size=out)
+    raw = np.zeros((out, nb, 34), np.uint8)
+    d16 = np.repeat((2.0 ** ew)[:, None], nb, axis=1).astype(np.float16)
+    raw[:, :, 0:2] = d16.view(np.uint8).reshape(out, nb, 2)
+    raw[:, :, 2:] = qw.astype(np.int8).view(np.uint8)
+    qx = r.integers(-127, 128, size=(n, nb, 32))
+    qx[:, :, 0] = 127
+    ex = r.integers(-6, 1, size=n)
+    x = (qx * (2.0 ** ex)[:, None, None]).reshape(n, k).astype(np.float32)
+    isum = np.einsum("onk,tnk->to", qw.astype(np.int64), qx.astype(np.int64))
+    y = isum.astype(np.float64) * (2.0 ** ew)[None, :] * (2.0 ** ex)[:, None]
+    return q8.Weight(raw.reshape(-1), k, out), x, y.astype(np.float32)
+
+
+@pytest.mark.parametrize("n,k", [(2, 32), (5, 64), (33, 96), (64, 1024)])
+@pytest.mark.parametrize("smode", [1, 0])
+def test_gemm_int32_block_dot_is_exact(gpu, n, k, smode):
+    gpu.set_option("gemm.smode", smode)
+    r = rng(30 + n)
+    w, x, y = exact_problem(r, 40, k, n)
+    got = run_matmul(gpu, w, x, n)
+    assert_bits(got, y, f"exact gemm n={n} k={k}")
+    gpu.release(w)
+
+
+@pytest.mark.parametrize("n", [2, 7, 8, 9, 33, 64, 65, 128, 129, 172, 193, 512, 1024])
+def test_gemm_matches_the_reference(gpu, n):
+    r = rng(40 + n)
+    out, k = 392, 2304
+    w = weight(r, out, k)
+    x = oracle.make_activations(r, n, k, outlier_rate=0.01)
+    ref = oracle.matmul(w.data, k, out, x, n)
+    got = run_matmul(gpu, w, x, n)
+    assert_close(got, ref, f"gemm n={n}")
+    gpu.release(w)
+
+
+@pytest.mark.parametrize("n", [8, 64])
+def test_gemm_configs1(gpu, n):
+    """same W as configs[0], X [n, 2304] N(0,1) with ~1% +-20."""
+    r = rng(50 + n)
+    w = weight(r, 5760, 2304)
+    x = oracle.make_activations(r, n, 2304, outlier_rate=0.01)
+    ref = oracle.matmul(w.data, 2304, 5760, x, n)
+    got = run_matmul(gpu, w, x, n)
+    assert_close(got, ref, f"configs[1] n={n}")
+    gpu.release(w)
+
+
+@pytest.mark.parametrize("smode,tpw,remap", [(0, 1, 0), (0, 4, 1), (1, 2, 0), (1, 3, 1)])
+def test_gemm_variants_agree(gpu, smode, tpw, remap):
+    gpu.set_option("gemm.smode", smode)
+    gpu.set_option("gemm.tt_per_wg", tpw)
+    gpu.set_option("gemm.xcd_remap", remap)
+    r = rng(60)
+    n, out, k = 200, 256, 5760
+    w = weight(r, out, k)
+    x = oracle.make_activations(r, n, k, outlier_rate=0.01)
+    ref = oracle.matmul(w.data, k, out, x, n)
+    got = run_matmul(gpu, w, x, n)
+    assert_close(got, ref, f"gemm smode={smode} tpw={tpw} remap={remap}")
+    gpu.release(w)
+
+
+def test_gemm_residual_and_prompt_group(gpu):
+    r = rng(61)
+    n, k = 96, 2304
+    ws = [weight(r, o, k) for o in (256, 128, 320)]
+    x = oracle.make_activations(r, n, k, outlier_rate=0.01)
+    xb = gpu.alloc(4 * n * k)
+    xb.upload(x)
+    p = gpu.prepare(xb, 0, n, k)
+    ys = [gpu.alloc(4 * n * w.out) for w in ws]
+    gpu.matmul_prompt_group([(w, y, 0) for w, y in zip(ws, ys)], p, n, k)
+    for w, y in zip(ws, ys):
+        ref = oracle.matmul(w.data, k, w.out, x, n)
+        assert_close(y.download(np.float32, n * w.out).reshape(n, w.out), ref, f"prompt group {w.out}")
+    # residual: y += W x on the first member
+    y0 = r.standard_normal((n, ws[0].out), dtype=np.float32)
+    ys[0].upload(y0)
+    gpu.matmul(ws[0], xb, 0, n, ys[0], 0, prepared=p, bias=ys[0])
+    ref = y0 + oracle.matmul(ws[0].data, k, ws[0].out, x, n)
+    assert_close(ys[0].download(np.float32, n * ws[0].out).reshape(n, -1), ref, "prompt residual")
+    for w, y in zip(ws, ys):
+        gpu.release(w)
+        y.free()
+    xb.free()
+
+
+def test_reference_gpu_vs_cpu_protocol(gpu):
+    """gpu_matmul.rs:32-80 on synthetic weights of attn_q / ffn_down shape:
+    x = 0.5 sin(0.017 i + n), n in {1, 8, 65, 128, 129, 172, 193},
+    max|d| <= 1e-3 * max(max|y|, 1); plus this build's tighter bar."""
+    r = rng(70)
+    for out, k in ((2304, 2304), (2304, 5760)):
+        w = weight(r, out, k)
+        for n in (1, 8, 65, 128, 129, 172, 193):
+            x = (np.sin(np.arange(n * k, dtype=np.float32) * np.float32(0.017) + np.float32(n))
+                 * np.float32(0.5)).astype(np.float32)
+            ref = oracle.matmul(w.data, k, out, x, n)
+            got = run_matmul(gpu, w, x, n)
+            md = float(np.max(np.abs(got - ref)))
+            scale = float(np.max(np.abs(ref)))
+            print(f"{out}x{k} n={n}: max|d| = {md:.3e} (values up to {scale:.3f})", flush=True)
+            assert md <= 1e-3 * max(scale, 1.0)
+            assert_close(got, ref, f"protocol {out}x{k} n={n}")
+        gpu.release(w)
+
+
+# ---------------------------------------------------------------------------
+# gate/up + SiLU, silu_mul_prepare, lm_head argmax
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n", [1, 3, 64])
+def test_gate_up_silu(gpu, n):
+    r = rng(80 + n)
+    k, ffn = 2304, 5760
+    gw, uw = weight(r, ffn, k), weight(r, ffn, k)
+    x = oracle.make_activations(r, n, k)
+    xb = gpu.alloc(4 * n * k)
+    xb.upload(x)
+    act = gpu.alloc(4 * n * ffn)
+    gpu.gate_up_silu(gw, uw, xb, 0, n, act, 0)
+    g = oracle.matmul(gw.data, k, ffn, x, n)
+    u = oracle.matmul(uw.data, k, ffn, x, n)
+    ref = oracle.silu_mul(g, u).reshape(n, ffn)
+    got = act.download(np.float32, n * ffn).reshape(n, ffn)
+    assert_close(got, ref, f"gate_up_silu n={n}")
+    for b in (xb, act):
+        b.free()
+    gpu.release(gw)
+    gpu.release(uw)
+
+
+def test_silu_mul_and_its_quantization(gpu):
+    r = rng(90)
+    n, k = 40, 5760
+    g = (r.standard_normal((n, k)) * 3).astype(np.float32)
+    u = r.standard_normal((n, k)).astype(np.float32)
+    gb, ub, ab = gpu.alloc(4 * n * k), gpu.alloc(4 * n * k), gpu.alloc(4 * n * k)
+    gb.upload(g)
+    ub.upload(u)
+    gpu.silu_mul(ab, gb, ub, n * k)
+    act_ref = oracle.silu_mul(g, u).reshape(n, k)
+    act = ab.download(np.float32, n * k).reshape(n, k)
+    assert_close(act, act_ref, "silu_mul")
+    ulp = np.abs(act.view(np.int32).astype(np.int64) - act_ref.view(np.int32).astype(np.int64))
+    assert int(ulp.max()) <= 2, f"silu_mul differs by {int(ulp.max())} ulp"
+    p = gpu.silu_mul_prepare(gb, ub, n, k)
+    q, s = unpack_prepared(gpu, p, n, k)
+    for t in range(n):
+        # quantize exactly what the device computed: bit-exact
+        rq, rs = oracle.quantize_q8_0(act[t])
+        assert np.array_equal(q[t], rq) and np.array_equal(s[t], rs), f"token {t}"
+    for b in (gb, ub, ab):
+        b.free()
+
+
+def test_lm_head_argmax(gpu):
+    """lm_head 122880 x 2304 with the greedy argmax."""
+    r = rng(100)
+    vocab, k = 122880, 2304
+    w = weight(r, vocab, k)
+    x = r.standard_normal(k, dtype=np.float32)
+    ref = oracle.matmul(w.data, k, vocab, x, 1).reshape(-1)
+    xb, lb = gpu.alloc(4 * k), gpu.alloc(4 * vocab)
+    xb.upload(x)
+    best = gpu.lm_head_argmax(w, xb, 0, lb, 0)
+    got = lb.download(np.float32, vocab)
+    assert_close(got, ref, "lm_head logits")
+    if oracle.simd_path() == "avx2+fma":
+        assert_bits(got, ref, "lm_head logits")
+    assert best == oracle.argmax(ref)
+    top2 = np.sort(ref)[-2:]
+    print(f"argmax {best}, top-2 gap {float(top2[1] - top2[0]):.3e}", flush=True)
+    xb.free()
+    lb.free()
+    gpu.release(w)
+
+
+@pytest.mark.parametrize("values,expect", [
+    ([1, 3, 3, 2], 1), ([-1, -1], 0), ([0, float("nan"), 5, 5], 2), ([float("nan"), 1, 9], 0),
+    ([-0.0, 0.0], 0), ([float("-inf"), float("-inf")], 0), ([1, float("inf"), float("inf")], 1),
+])
+def test_argmax_semantics(gpu, values, expect):
+    v = np.array(values, np.float32)
+    b = gpu.alloc(4 * v.size)
+    b.upload(v)
+    assert gpu.argmax(b, 0, v.size) == expect == oracle.argmax(v)
+    b.free()
+
+
+def test_argmax_large_with_ties_across_workgroups(gpu):
+    r = rng(101)
+    v = r.standard_normal(1_000_003).astype(np.float32)
+    v[[123_456, 654_321, 999_999]] = 50.0
+    b = gpu.alloc(4 * v.size)
+    b.upload(v)
+    assert gpu.argmax(b, 0, v.size) == 123_456 == oracle.argmax(v)
+    b.free()
+
+
+# ---------------------------------------------------------------------------
+# error paths: rejected on the host, nothing launched
+# ---------------------------------------------------------------------------
+
+def test_errors_are_reported_not_launched(gpu):
+    r = rng(110)
+    w = weight(r, 64, 64)
+    xb = gpu.alloc(4 * 64 * 2000)
+    small = gpu.alloc(4 * 10)
+    with pytest.raises(q8.Q8Error) as e:
+        gpu.matmul(w, xb, 0, 1025, xb, 0)
+    assert e.value.status == q8.Q8_ERR_UNSUPPORTED
+    with pytest.raises(q8.Q8Error) as e:
+        gpu.matmul(w, xb, 0, 1, small, 0)            # y too small
+    assert e.value.status == q8.Q8_ERR_INVALID
+    with pytest.raises(q8.Q8Error) as e:
+        gpu.matmul(w, small, 0, 2, xb, 0)            # x too small
+    assert e.value.status == q8.Q8_ERR_INVALID
+    with pytest.raises(q8.Q8Error) as e:
+        gpu.matmul_decode_group([(w, xb, 0)] * 5, xb, 0, 64)
+    assert e.value.status == q8.Q8_ERR_INVALID
+    with pytest.raises(q8.Q8Error) as e:
+        gpu.matmul_decode_group([(w, xb, 0), (w, xb, 64)], xb, 0, 64, bias=xb)
+    assert e.value.status == q8.Q8_ERR_INVALID
+    p = gpu.prepare(xb, 0, 4, 64)
+    with pytest.raises(q8.Q8Error) as e:
+        gpu.matmul(w, xb, 0, 5, xb, 4096, prepared=p)  # prepared for another n
+    assert e.value.status == q8.Q8_ERR_INVALID
+    raw = np.zeros(34 * 3, np.uint8)
+    import ctypes
+    h = ctypes.c_void_p()
+    assert q8.lib().q8_weight_resident(gpu.handle, raw.ctypes.data, 100, 96, 1,
+                                       ctypes.byref(h)) == q8.Q8_ERR_INVALID
+    assert q8.lib().q8_weight_resident(gpu.handle, raw.ctypes.data, raw.nbytes, 95, 1,
+                                       ctypes.byref(h)) == q8.Q8_ERR_INVALID
+    gpu.sync()
+    xb.free()
+    small.free()
+    gpu.release(w)
+
+
+# ---------------------------------------------------------------------------
+# graph capture: replays match eager results (no memset nodes are recorded)
+# ---------------------------------------------------------------------------
+
+def test_graph_replay_matches_eager(gpu):
+    r = rng(120)
+    k, out, n = 2304, 640, 48
+    w = weight(r, out, k)
+    x1 = r.standard_normal(k, dtype=np.float32)
+    xn = oracle.make_activations(r, n, k)
+    b1, bn = gpu.alloc(4 * k), gpu.alloc(4 * n * k)
+    y1, yn = gpu.alloc(4 * out), gpu.alloc(4 * n * out)
+    b1.upload(x1)
+    bn.upload(xn)
+    gpu.matmul(w, b1, 0, 1, y1, 0)
+    gpu.matmul(w, bn, 0, n, yn, 0)
+    e1 = y1.download(np.float32, out)
+    en = yn.download(np.float32, n * out)
+    gpu.graph_begin()
+    gpu.matmul(w, b1, 0, 1, y1, 0)
+    gpu.matmul(w, bn, 0, n, yn, 0)
+    graph = gpu.graph_end()
+    try:
+        for i in range(3):
+            y1.upload(np.zeros(out, np.float32))
+            yn.upload(np.zeros(n * out, np.float32))
+            gpu.graph_launch(graph)
+            gpu.sync()
+            assert_bits(y1.download(np.float32, out), e1, f"replay {i} gemv")
+            assert_bits(yn.download(np.float32, n * out), en, f"replay {i} gemm")
+    finally:
+        gpu.graph_destroy(graph)
+    for b in (b1, bn, y1, yn):
+        b.free()
+    gpu.release(w)
