@@ -232,6 +232,20 @@ def bench_decode_layer(gpu, reps, rng):
     return layer, head
 
 
+CALIBRATION_BYTES = 64 << 20
+
+
+def calibration_copy(gpu, reps=3):
+    """A plain q8_copy of CALIBRATION_BYTES, the known-size kernel the
+    rocprofv3 FETCH_SIZE / WRITE_SIZE counters are scaled against."""
+    src, dst = gpu.alloc(CALIBRATION_BYTES), gpu.alloc(CALIBRATION_BYTES)
+    for _ in range(reps):
+        gpu.copy(dst, src, CALIBRATION_BYTES)
+    gpu.sync()
+    src.free()
+    dst.free()
+
+
 def cpu_baseline(seconds: float = 10.0):
     """The oracle (C restatement of tensor::matmul, rayon-style row split) on
     this host's cores: configs[0] GEMV for ~`seconds` of wall time."""
@@ -266,6 +280,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--skip-extras", action="store_true")
+    ap.add_argument("--skip-gemm", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus "
@@ -276,9 +291,10 @@ def main():
     rng = np.random.default_rng(0x5EED)
     gpu = q8.Gpu(0)
     log(f"device {gpu.name}")
+    calibration_copy(gpu)
     m, k = 5760, 2304
     gemv = bench_gemv_rotating(gpu, m, k, args.steps, args.warmup, rng, "configs[0] GEMV")
-    gemm = bench_layer_n512(gpu, 20, rng)
+    gemm = bench_layer_n512(gpu, 20, rng) if not args.skip_gemm else {"tops": 0.0, "frac": 0.0, "us": 0.0, "ops": 0}
     extras = {}
     if not args.skip_extras:
         extras["configs1_n8"] = bench_gemm_rotating(gpu, m, k, 8, 5, rng, "configs[1] n=8")
@@ -286,7 +302,7 @@ def main():
         layer, head = bench_decode_layer(gpu, 50, rng)
         extras["configs2_decode_layer"] = layer
         extras["configs2_lm_head"] = head
-    cpu = cpu_baseline(args.cpu_seconds)
+    cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
     gpu.close()
 
     value = gemv["gbs"]

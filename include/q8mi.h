@@ -96,6 +96,8 @@ typedef struct {
     int tt_per_wg;       /* GEMM: 32-token tiles (waves) per workgroup */
     int smode;           /* GEMM: 1 = scale products on the matrix cores */
     int xcd_remap;       /* GEMM: keep a row tile's workgroups on one XCD */
+    int kslices;         /* workgroups splitting one output tile's blocks (1 = none) */
+    int kwaves;          /* GEMM: waves splitting the blocks inside a workgroup */
     const char *name;    /* tactic name, e.g. "matmul.gemv_f32" */
     const char *evidence;
 } q8_tactic;
@@ -122,8 +124,9 @@ int q8_device_info(q8_ctx *ctx, int *cu_count, size_t *total_bytes, size_t *free
  * work with this path's. */
 void *q8_stream(q8_ctx *ctx);
 /* Tuning/testing switches; value -1 restores the tactic table's choice.
- * Names: "gemv.exact", "gemv.waves", "gemv.pairs", "gemm.smode",
- * "gemm.tt_per_wg", "gemm.xcd_remap". */
+ * Names: "gemv.exact", "gemv.waves", "gemv.pairs", "gemv.slices",
+ * "gemm.smode", "gemm.tt_per_wg", "gemm.xcd_remap", "gemm.kwaves",
+ * "gemm.slices". */
 int q8_set_option(q8_ctx *ctx, const char *name, int value);
 
 /* ---- device memory: Gpu::alloc / upload / download (cuda/mod.rs:530-567) ---- */
@@ -189,8 +192,10 @@ int q8_matmul_prompt_group(q8_ctx *ctx, const q8_group_entry *group, int count,
 /* The feed-forward gate/up pair with SiLU: act[t*ffn + i] =
  * silu(gate(x)_i) * up(x)_i (model.rs:1170-1215 with compute.rs:937-953).
  * n == 1: one fused launch (both GEMVs and the SiLU product in the epilogue).
- * n >= 2: one grouped GEMM into workspace, then the product; if `prepared`
- * is not NULL the product is also quantized into it for the down matmul. */
+ * n >= 2: one grouped GEMM into workspace, then the product: written to
+ * `act` in f32 when `prepared` is NULL, otherwise quantized straight into
+ * `prepared` for the down matmul and not written in f32 (as
+ * Compute::silu_mul_prepare does, compute.rs:993-1019). */
 int q8_gate_up_silu(q8_ctx *ctx, const q8_weight *gate, const q8_weight *up, q8_dptr x,
                     size_t x_offset, int n, q8_dptr act, size_t act_offset, q8_prepared *prepared);
 
@@ -199,6 +204,11 @@ int q8_gate_up_silu(q8_ctx *ctx, const q8_weight *gate, const q8_weight *up, q8_
  * first index of the strictly greatest logit in *argmax (waits for it). */
 int q8_lm_head_argmax(q8_ctx *ctx, const q8_weight *weight, q8_dptr x, size_t x_offset,
                       q8_dptr logits, size_t logits_offset, uint32_t *argmax);
+
+/* Device-to-device copy (bytes, pointers 16-byte aligned): the reference's
+ * copy_f32 kernel (gpu.cu:422-435, cuda/mod.rs:1008-1030); also the plain
+ * streaming kernel the HBM counters are calibrated with. */
+int q8_copy_device(q8_ctx *ctx, q8_dptr dst, q8_dptr src, size_t bytes);
 
 /* Greedy argmax of len f32 values on the device (sampler.rs:167-175). */
 int q8_argmax(q8_ctx *ctx, q8_dptr values, size_t offset, size_t len, uint32_t *argmax);

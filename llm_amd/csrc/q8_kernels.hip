@@ -30,17 +30,12 @@ typedef float f32x32 __attribute__((ext_vector_type(32)));
 // AVX2 lane held by dword t of half h (see q8_layout.h): J = {{0,4,1,5},{2,6,3,7}}.
 static __device__ __forceinline__ int perm_lane(int h, int t) { return ((t & 1) << 2) + (t >> 1) + (h << 1); }
 
-// Exact f16 -> f32 (subnormals included; about 30% of the benchmark scales are
-// f16 subnormals).  Integer decode, so it does not depend on the FP16 denormal
-// mode of the wave.
+// Exact f16 -> f32, subnormals included (about 30% of the benchmark scales are
+// f16 subnormals).  v_cvt_f32_f16 is exact when the wave keeps f16 denormals,
+// which every kernel here does (amdhsa_float_denorm_mode_16_64 = 3, HIP's
+// default without -ffast-math / denormal flushing).
 static __device__ __forceinline__ float f16_to_f32(unsigned h) {
-    const unsigned sign = (h & 0x8000u) << 16;
-    const unsigned e = (h >> 10) & 0x1fu;
-    const unsigned m = h & 0x3ffu;
-    float sub = __uint_as_float(sign | __float_as_uint((float)m * 5.9604644775390625e-8f));
-    unsigned bits = e == 0x1fu ? (sign | 0x7f800000u | (m ? (0x400000u | (m << 13)) : 0u))
-                               : (sign | ((e + 112u) << 23) | (m << 13));
-    return e == 0 ? sub : __uint_as_float(bits);
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)h);
 }
 
 // Rust `f32 as i8`: saturating, NaN -> 0.
@@ -62,14 +57,14 @@ static __device__ __forceinline__ float silu_f32(float v) {
 // Repack: GGUF Q8_0 rows <-> tile layout.  One thread per (row slot, block).
 // ---------------------------------------------------------------------------
 extern "C" __global__ __launch_bounds__(256) void q8_repack(Q8RepackArgs a) {
-    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;  // < 2^31: the host checks
     const int nb = a.nb;
-    const long long total = (long long)a.tiles * Q8_TILE_ROWS * nb;
+    const int total = a.tiles * Q8_TILE_ROWS * nb;
     if (idx >= total) return;
-    const int b = (int)(idx % nb);
-    const long long row = idx / nb;
-    const long long g = row / Q8_TILE_ROWS;
-    const int r = (int)(row % Q8_TILE_ROWS);
+    const int row = idx / nb;
+    const int b = idx - row * nb;
+    const int g = row / Q8_TILE_ROWS;
+    const int r = row % Q8_TILE_ROWS;
     uint8_t *unit = a.quants + (size_t)(g * nb + b) * Q8_UNIT_BYTES;
     uint16_t *sp = a.scales + (size_t)(g * nb + b) * Q8_TILE_ROWS + r;
     if (!a.inverse) {
@@ -154,24 +149,44 @@ static __device__ __forceinline__ float half_partial(i32x4 q, const f32x4 *xh) {
 // 64 * Q8_GEMV_STAGE / 16 = 12 block pairs (the host's tactic keeps to it).
 #define Q8_GEMV_STAGE 3
 
+// Sum of `count` values at stride 32 floats, left to right, with the loads of
+// eight values issued before their adds (the order of the adds is unchanged).
+static __device__ __forceinline__ float chain_sum(const float *v, int count) {
+    float acc = 0.0f;
+    int b = 0;
+    for (; b + 8 <= count; b += 8) {
+        float t[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) t[u] = v[(b + u) * 32];
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc = acc + t[u];
+    }
+    for (; b < count; b++) acc = acc + v[b * 32];
+    return acc;
+}
+
 template <int PB, int EXACT>
 static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
     extern __shared__ __attribute__((aligned(16))) float smem[];
+    __shared__ int last_flag;
     const int nb = a.nb;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform, in an SGPR
     const int W = a.waves_per_tile;
     const int h = lane >> 5;
     const int r = lane & 31;
     const int slot = wave / W;  // member slot within the workgroup (silu mode: 0 gate, 1 up)
     const int nslots = (blockDim.x >> 6) / W;
+    const int S = a.kslices;
+    const int slice = blockIdx.x % S;
+    const int gtile = blockIdx.x / S;  // global tile index (over the group's members)
 
     int mi, tile;
     if (a.silu_pair) {
         mi = slot;
-        tile = blockIdx.x;
+        tile = gtile;
     } else {
-        tile = blockIdx.x;
+        tile = gtile;
         mi = 0;
 #pragma unroll
         for (int i = 1; i < Q8_GROUP_MAX; i++)
@@ -181,14 +196,19 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
     const Q8GemvMember mem = a.m[mi];
     const int w = wave - slot * W;
     const int npairs = (nb + 1) >> 1;
-    const int p_begin = w * a.pairs_per_wave;
-    const int p_end = min(npairs, p_begin + a.pairs_per_wave);
+    const int s_begin = slice * a.pairs_per_slice;
+    const int s_end = min(npairs, s_begin + a.pairs_per_slice);
+    const int p_begin = s_begin + w * a.pairs_per_wave;
+    const int p_end = min(s_end, p_begin + a.pairs_per_wave);
     const int p_last = max(p_end - 1, 0);
     const uint8_t *qbase = mem.quants + (size_t)tile * nb * Q8_UNIT_BYTES + lane * 16;
     const uint16_t *sbase = mem.scales + (size_t)tile * nb * Q8_TILE_ROWS + r;
 
-    float *xs = smem;                // nb * 32 floats, permuted
-    float *vbuf = smem + nb * 32;    // EXACT: [nslots][nb][32]; else [waves][32]
+    float *xs = smem;               // nb * 32 floats, permuted
+    float *vbuf = smem + nb * 32;   // EXACT, one slice: [nslots][nb][32]; else [waves][32]
+    // Cross-workgroup scratch (S > 1): EXACT [slots][tiles][nb][32] block values,
+    // else [slots][tiles][S][32] per-slice row sums.
+    float *gbuf = a.scratch;
 
     // Loads are unconditional at clamped, in-bounds addresses (no exec-mask
     // branches, so nothing waits between them); validity is applied after.
@@ -212,19 +232,19 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
     // block ranges (in silu mode the gate and up waves write identical values
     // to the same range), so only a wave-level fence is needed.
     {
-        const int s_begin = 16 * p_begin;
-        const int s_end = min(16 * p_end, nb * 8);
+        const int st_begin = 16 * p_begin;
+        const int st_end = min(16 * p_end, nb * 8);
         f32x4 v[Q8_GEMV_STAGE];
 #pragma unroll
         for (int u = 0; u < Q8_GEMV_STAGE; u++) {
-            const int i = min(s_begin + lane + 64 * u, nb * 8 - 1);
+            const int i = min(st_begin + lane + 64 * u, nb * 8 - 1);
             const float *xb = a.x + (i >> 3) * 32 + perm_lane((i >> 2) & 1, i & 3);
             v[u] = (f32x4){xb[0], xb[8], xb[16], xb[24]};
         }
 #pragma unroll
         for (int u = 0; u < Q8_GEMV_STAGE; u++) {
-            const int i = s_begin + lane + 64 * u;
-            if (i < s_end) ((f32x4 *)xs)[i] = v[u];
+            const int i = st_begin + lane + 64 * u;
+            if (i < st_end) ((f32x4 *)xs)[i] = v[u];
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -253,7 +273,12 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
             const int blk = b0 + h;
             const bool ok = pair_ok && blk < nb;
             if (EXACT) {
-                if (ok) vbuf[(slot * nb + blk) * 32 + r] = v;
+                if (ok) {
+                    if (S == 1)
+                        vbuf[(slot * nb + blk) * 32 + r] = v;
+                    else
+                        gbuf[((size_t)(slot * a.total_tiles + gtile) * nb + blk) * 32 + r] = v;
+                }
             } else {
                 total = ok ? total + v : total;
             }
@@ -269,20 +294,46 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
         if (lane < 32) vbuf[wave * 32 + r] = row_part;
     }
     __syncthreads();
+
+    if (S > 1) {
+        // This slice's share of the tile: EXACT wrote block values to gbuf
+        // above; otherwise the first wave of each slot sums its waves here.
+        if (!EXACT && w == 0 && lane < 32) {
+            float acc = 0.0f;
+            for (int ww = 0; ww < W; ww++) acc = acc + vbuf[(slot * W + ww) * 32 + r];
+            gbuf[((size_t)(slot * a.total_tiles + gtile) * S + slice) * 32 + r] = acc;
+        }
+        // The last workgroup of the tile to arrive finishes it.
+        __threadfence();
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const unsigned old = atomicAdd(&a.counters[gtile], 1u);
+            last_flag = (old == (unsigned)(S - 1));
+        }
+        __syncthreads();
+        if (!last_flag) return;
+        __threadfence();
+        if (threadIdx.x == 0) a.counters[gtile] = 0u;  // ready for the next launch
+    }
     if (wave != 0 || lane >= 32) return;
 
     float sums[2] = {0.0f, 0.0f};
 #pragma unroll
-    for (int s = 0; s < 2; s++) {
-        if (s < nslots) {
-            float acc = 0.0f;
-            if (EXACT) {
-                const float *vb = vbuf + (size_t)s * nb * 32 + r;
-                for (int b = 0; b < nb; b++) acc = acc + vb[b * 32];
+    for (int sl = 0; sl < 2; sl++) {
+        if (sl < nslots) {
+            float acc;
+            if (S == 1) {
+                if (EXACT) {
+                    acc = chain_sum(vbuf + (size_t)sl * nb * 32 + r, nb);
+                } else {
+                    acc = 0.0f;
+                    for (int ww = 0; ww < W; ww++) acc = acc + vbuf[(sl * W + ww) * 32 + r];
+                }
             } else {
-                for (int ww = 0; ww < W; ww++) acc = acc + vbuf[(s * W + ww) * 32 + r];
+                const size_t base = (size_t)(sl * a.total_tiles + gtile);
+                acc = EXACT ? chain_sum(gbuf + base * nb * 32 + r, nb) : chain_sum(gbuf + base * S * 32 + r, S);
             }
-            sums[s] = acc;
+            sums[sl] = acc;
         }
     }
     const int row = tile * Q8_TILE_ROWS + r;
@@ -297,67 +348,93 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
     }
 }
 
-#define Q8_GEMV_KERNEL(PB, EXACT)                                                                  \
-    extern "C" __global__ __launch_bounds__(512) void q8_gemv_pb##PB##_e##EXACT(Q8GemvArgs a) { \
-        gemv_body<PB, EXACT>(a);                                                                   \
+// Batches of up to five pairs fit 1024-thread workgroups (<= 128 VGPRs); the
+// nine-pair batch keeps 512 threads.
+#define Q8_GEMV_KERNEL(PB, EXACT, THREADS)                                                              \
+    extern "C" __global__ __launch_bounds__(THREADS) void q8_gemv_pb##PB##_e##EXACT(Q8GemvArgs a) { \
+        gemv_body<PB, EXACT>(a);                                                                        \
     }
-Q8_GEMV_KERNEL(2, 0)
-Q8_GEMV_KERNEL(2, 1)
-Q8_GEMV_KERNEL(3, 0)
-Q8_GEMV_KERNEL(3, 1)
-Q8_GEMV_KERNEL(5, 0)
-Q8_GEMV_KERNEL(5, 1)
-Q8_GEMV_KERNEL(9, 0)
-Q8_GEMV_KERNEL(9, 1)
+Q8_GEMV_KERNEL(2, 0, 1024)
+Q8_GEMV_KERNEL(2, 1, 1024)
+Q8_GEMV_KERNEL(3, 0, 1024)
+Q8_GEMV_KERNEL(3, 1, 1024)
+Q8_GEMV_KERNEL(5, 0, 1024)
+Q8_GEMV_KERNEL(5, 1, 1024)
+Q8_GEMV_KERNEL(9, 0, 512)
+Q8_GEMV_KERNEL(9, 1, 512)
 
 // ---------------------------------------------------------------------------
 // Activation quantization (quant.rs:98-121), into the prepared tile layout.
-// Eight lanes per (token, block): lane (h, t) reads the four elements of AVX2
-// lane J[h][t] and writes them as one dword of the permuted block.
+// One wave per (32-token tile, block) unit: lane L = 32h + t owns half h of
+// token t's block, i.e. AVX2 lanes J[h][0..3] across the four chunks -- as
+// eight float2 loads (elements 8c + {j, j+1}) -- and writes it as one 16-byte
+// store, so the wave's stores are one contiguous 1 KB unit.  The block peak
+// is the max of the two halves' peaks (one v_permlane32_swap).
 // ---------------------------------------------------------------------------
 extern "C" __global__ __launch_bounds__(256) void q8_quantize(Q8QuantArgs a) {
-    const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    const long long unit = gid >> 3;
-    const int l8 = threadIdx.x & 7;
+    const int lane = threadIdx.x & 63;
+    const int unit = blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nb = a.nb;
-    const long long units = (long long)a.ttiles * Q8_TILE_TOKENS * nb;
-    if (unit >= units) return;  // uniform across the 8 lanes of a unit
-    const int b = (int)(unit % nb);
-    const int t = (int)(unit / nb);
-    const int h = l8 >> 2;
-    const int tq = l8 & 3;
-    const int j = perm_lane(h, tq);
-    const long long k = (long long)nb * 32;
-    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (unit >= a.ttiles * nb) return;  // whole waves
+    const int tt = unit / nb;
+    const int b = unit - tt * nb;
+    const int h = lane >> 5;
+    const int tl = lane & 31;
+    const int t = tt * Q8_TILE_TOKENS + tl;
+    // v[2i], v[2i+1] = elements 8*(i>>1)... laid out per dword: dword q holds
+    // elements 8c + J[h][q] for c = 0..3; J[h] = {2h, 4+2h, 1+2h, 5+2h}, so the
+    // pairs (2h, 2h+1) and (4+2h, 5+2h) of each chunk c cover all four dwords.
+    float e[4][4];  // e[q][c]
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) e[q][c] = 0.0f;
     if (t < a.n) {
-        const long long base = (long long)t * k + b * 32 + j;
-        if (a.mode == 0) {
+        const size_t base = (size_t)t * nb * 32 + (size_t)b * 32 + 2 * h;
 #pragma unroll
-            for (int c = 0; c < 4; c++) v[c] = a.x[base + 8 * c];
-        } else {
-#pragma unroll
-            for (int c = 0; c < 4; c++) v[c] = silu_f32(a.gate[base + 8 * c]) * a.up[base + 8 * c];
+        for (int c = 0; c < 4; c++) {
+            // chunk c: elements 8c + 2h, 8c + 2h + 1 (dwords 0, 2) and 8c + 4 + 2h, +1 (dwords 1, 3)
+            float2 lo, hi;
+            if (a.mode == 0) {
+                lo = *(const float2 *)(a.x + base + 8 * c);
+                hi = *(const float2 *)(a.x + base + 8 * c + 4);
+            } else {
+                const float2 g0 = *(const float2 *)(a.gate + base + 8 * c);
+                const float2 u0 = *(const float2 *)(a.up + base + 8 * c);
+                const float2 g1 = *(const float2 *)(a.gate + base + 8 * c + 4);
+                const float2 u1 = *(const float2 *)(a.up + base + 8 * c + 4);
+                lo = make_float2(silu_f32(g0.x) * u0.x, silu_f32(g0.y) * u0.y);
+                hi = make_float2(silu_f32(g1.x) * u1.x, silu_f32(g1.y) * u1.y);
+            }
+            e[0][c] = lo.x;  // J[h][0] = 2h
+            e[2][c] = lo.y;  // J[h][2] = 2h + 1
+            e[1][c] = hi.x;  // J[h][1] = 4 + 2h
+            e[3][c] = hi.y;  // J[h][3] = 5 + 2h
         }
     }
     float peak = 0.0f;
 #pragma unroll
-    for (int c = 0; c < 4; c++) peak = fmaxf(peak, fabsf(v[c]));
-    peak = fmaxf(peak, __shfl_xor(peak, 1, 8));
-    peak = fmaxf(peak, __shfl_xor(peak, 2, 8));
-    peak = fmaxf(peak, __shfl_xor(peak, 4, 8));
+    for (int q = 0; q < 4; q++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) peak = fmaxf(peak, fabsf(e[q][c]));
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(peak), __float_as_uint(peak), false, false);
+    peak = fmaxf(peak, __uint_as_float(h ? sw[0] : sw[1]));
     const float scale = peak / 127.0f;
     const float inverse = peak > 0.0f ? 127.0f / peak : 0.0f;
-    unsigned packed = 0;
+    i32x4 packed;
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-        const float prod = v[c] * inverse;
-        packed |= ((unsigned)sat_i8(roundf(prod)) & 0xffu) << (8 * c);
+    for (int q = 0; q < 4; q++) {
+        unsigned w = 0;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float prod = e[q][c] * inverse;
+            w |= ((unsigned)sat_i8(roundf(prod)) & 0xffu) << (8 * c);
+        }
+        packed[q] = (int)w;
     }
-    const int tt = t / Q8_TILE_TOKENS;
-    const int tl = t % Q8_TILE_TOKENS;
     const size_t u = (size_t)tt * nb + b;
-    *(unsigned *)(a.xq + u * Q8_UNIT_BYTES + h * 512 + tl * 16 + tq * 4) = packed;
-    if (l8 == 0) a.xs[u * Q8_TILE_TOKENS + tl] = scale;
+    *(i32x4 *)(a.xq + u * Q8_UNIT_BYTES + lane * 16) = packed;
+    if (h == 0) a.xs[u * Q8_TILE_TOKENS + tl] = scale;
 }
 
 // ---------------------------------------------------------------------------
@@ -385,17 +462,26 @@ struct GemmPair {
 
 template <int SMODE>
 static __device__ __forceinline__ void gemm_body(const Q8GemmArgs &a) {
+    extern __shared__ __attribute__((aligned(16))) float gsm[];  // [kwaves-1][tt_per_wg][64][16] partials
+    __shared__ int last_flag;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform, in an SGPR
+    const int TT = a.tt_per_wg;
+    const int tw = wave % TT;  // token tile within the workgroup
+    const int kw = wave / TT;  // K-split wave
+    const int S = a.kslices;
     int wg = blockIdx.x;
     if (a.xcd_remap) {
         const int per = a.nwg >> 3;
         wg = (wg & 7) * per + (wg >> 3);
     }
-    const int rt = wg / a.tgroups;
-    const int tg = wg - rt * a.tgroups;
-    const int tt = tg * a.tt_per_wg + wave;
-    if (tt >= a.ttiles) return;
+    // workgroup -> (row tile, token group, K slice); slices of one tile are adjacent
+    const int slice = wg % S;
+    const int rtg = wg / S;
+    const int rt = rtg / a.tgroups;
+    const int tg = rtg - rt * a.tgroups;
+    const int tt = tg * TT + tw;
+    const bool live = tt < a.ttiles;  // padding waves still meet every barrier
     int mi = 0;
 #pragma unroll
     for (int i = 1; i < Q8_GROUP_MAX; i++)
@@ -405,10 +491,18 @@ static __device__ __forceinline__ void gemm_body(const Q8GemmArgs &a) {
     const int nb = a.nb;
     const int h = lane >> 5;
     const int r = lane & 31;
+    const int ttc = min(tt, a.ttiles - 1);  // clamped, always a valid tile to address
     const uint8_t *wq = mem.quants + (size_t)g * nb * Q8_UNIT_BYTES + lane * 16;
     const uint16_t *wsc = mem.scales + (size_t)g * nb * Q8_TILE_ROWS;
-    const uint8_t *xq = a.xq + (size_t)tt * nb * Q8_UNIT_BYTES + lane * 16;
-    const float *xsc = a.xs + (size_t)tt * nb * Q8_TILE_TOKENS;
+    const uint8_t *xq = a.xq + (size_t)ttc * nb * Q8_UNIT_BYTES + lane * 16;
+    const float *xsc = a.xs + (size_t)ttc * nb * Q8_TILE_TOKENS;
+
+    // this wave's block pairs: slice range split over the kw waves
+    const int npairs = (nb + 1) >> 1;
+    const int s_begin = slice * a.pairs_per_slice;
+    const int s_end = min(npairs, s_begin + a.pairs_per_slice);
+    const int p_begin = s_begin + kw * a.pairs_per_wave;
+    const int p_end = live ? min(s_end, p_begin + a.pairs_per_wave) : p_begin;
 
     f32x16 acc;
 #pragma unroll
@@ -424,12 +518,12 @@ static __device__ __forceinline__ void gemm_body(const Q8GemmArgs &a) {
         if (SMODE == 1) {
             // lanes 0-31 carry block b and lanes 32-63 block b+1: the two blocks
             // of the outer-product MFMA, d_w * s_x in the accumulator layout.
-            const f32x32 s = __builtin_amdgcn_mfma_f32_32x32x1f32(q.sx, f16_to_f32(q.dw), fzero, 0, 0, 0);
+            const f32x32 sc = __builtin_amdgcn_mfma_f32_32x32x1f32(q.sx, f16_to_f32(q.dw), fzero, 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < 16; i++) acc[i] = __builtin_fmaf((float)i0[i], s[i], acc[i]);
+            for (int i = 0; i < 16; i++) acc[i] = __builtin_fmaf((float)i0[i], sc[i], acc[i]);
             if (two) {
 #pragma unroll
-                for (int i = 0; i < 16; i++) acc[i] = __builtin_fmaf((float)i1[i], s[16 + i], acc[i]);
+                for (int i = 0; i < 16; i++) acc[i] = __builtin_fmaf((float)i1[i], sc[16 + i], acc[i]);
             }
         } else {
             // lane owns row r and tokens 8(i/4) + 4h + (i%4) of the tile
@@ -456,28 +550,103 @@ static __device__ __forceinline__ void gemm_body(const Q8GemmArgs &a) {
             }
         }
     };
-    // Loads at clamped, always in-bounds block indices: no exec-mask branches.
-    auto load_pair = [&](int b) {
+    // Full pairs walk the unit streams by pointer; the odd last block of an
+    // odd nb (its pair's second block absent) is handled after the loop.
+    const int full_end = min(p_end, nb >> 1);  // pairs whose two blocks both exist
+    auto load_pair = [&](int b, bool two) {
         GemmPair q;
-        const int b1 = min(b + 1, nb - 1);
-        const int bs = min(b + h, nb - 1);
+        const int b1 = two ? b + 1 : b;
+        const int bs = two ? b + h : b;
         q.x0 = *(const i32x4 *)(xq + (size_t)b * Q8_UNIT_BYTES);
         q.w0 = *(const i32x4 *)(wq + (size_t)b * Q8_UNIT_BYTES);
         q.x1 = *(const i32x4 *)(xq + (size_t)b1 * Q8_UNIT_BYTES);
         q.w1 = *(const i32x4 *)(wq + (size_t)b1 * Q8_UNIT_BYTES);
         q.sx = xsc[(size_t)bs * Q8_TILE_TOKENS + r];
         q.dw = wsc[(size_t)bs * Q8_TILE_ROWS + r];
+        if (!two && h) {  // the absent block contributes 0 * 0
+            q.sx = 0.0f;
+            q.dw = 0u;
+        }
         return q;
     };
 
-    const int npairs = (nb + 1) >> 1;
-    GemmPair cur = load_pair(0);
-    for (int p = 0; p < npairs; p++) {
-        const int b = 2 * p;
-        const GemmPair nxt = load_pair(2 * min(p + 1, npairs - 1));
-        pair_step(cur, b, b + 1 < nb);
-        cur = nxt;
+    if (p_begin < full_end) {
+        GemmPair cur = load_pair(2 * p_begin, true);
+        for (int p = p_begin; p < full_end; p++) {
+            if (SMODE == 1) {
+                // Matrix-core work of this pair first (the scale products, whose
+                // result the epilogue needs last-issued-first-ready, then the two
+                // block dots), then the next pair's loads, then the VALU epilogue
+                // while those loads are in flight.  sched_barrier keeps the
+                // compiler from sinking the loads next to their use.
+                const f32x32 sc = __builtin_amdgcn_mfma_f32_32x32x1f32(cur.sx, f16_to_f32(cur.dw), fzero, 0, 0, 0);
+                const i32x16 i0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.x0, cur.w0, izero, 0, 0, 0);
+                const i32x16 i1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.x1, cur.w1, izero, 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                cur = load_pair(2 * min(p + 1, full_end - 1), true);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < 16; i++) acc[i] = __builtin_fmaf((float)i0[i], sc[i], acc[i]);
+#pragma unroll
+                for (int i = 0; i < 16; i++) acc[i] = __builtin_fmaf((float)i1[i], sc[16 + i], acc[i]);
+            } else {
+                const GemmPair nxt = load_pair(2 * min(p + 1, full_end - 1), true);
+                pair_step(cur, 2 * p, true);
+                cur = nxt;
+            }
+        }
     }
+    if (full_end < p_end) {  // odd nb: the last pair holds one block
+        const GemmPair q = load_pair(2 * full_end, false);
+        pair_step(q, 2 * full_end, false);
+    }
+
+    const int KW = (blockDim.x >> 6) / TT;
+    if (KW > 1) {
+        // reduce the K-split waves in a fixed order: kw = 0 adds 1, 2, ...
+        if (kw > 0) {
+            float *dst = gsm + ((size_t)((kw - 1) * TT + tw) * 64 + lane) * 16;
+#pragma unroll
+            for (int i = 0; i < 16; i += 4) *(f32x4 *)(dst + i) = (f32x4){acc[i], acc[i + 1], acc[i + 2], acc[i + 3]};
+        }
+        __syncthreads();
+        if (kw == 0) {
+            for (int k2 = 1; k2 < KW; k2++) {
+                const float *src = gsm + ((size_t)((k2 - 1) * TT + tw) * 64 + lane) * 16;
+#pragma unroll
+                for (int i = 0; i < 16; i++) acc[i] = acc[i] + src[i];
+            }
+        }
+    }
+    if (S > 1) {
+        // per-slice partial tiles in scratch; the tile group's last workgroup sums them in slice order
+        float *part = a.scratch + ((size_t)((rt * a.ttiles + ttc) * S + slice) * 64 + lane) * 16;
+        if (kw == 0 && live) {
+#pragma unroll
+            for (int i = 0; i < 16; i += 4) *(f32x4 *)(part + i) = (f32x4){acc[i], acc[i + 1], acc[i + 2], acc[i + 3]};
+        }
+        __threadfence();
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const unsigned old = atomicAdd(&a.counters[rtg], 1u);
+            last_flag = (old == (unsigned)(S - 1));
+        }
+        __syncthreads();
+        if (!last_flag) return;
+        __threadfence();
+        if (threadIdx.x == 0) a.counters[rtg] = 0u;
+        if (kw == 0 && live) {
+            const float *base = a.scratch + ((size_t)((rt * a.ttiles + ttc) * S) * 64 + lane) * 16;
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[i] = 0.0f;
+            for (int sl = 0; sl < S; sl++) {
+                const float *src = base + (size_t)sl * 64 * 16;
+#pragma unroll
+                for (int i = 0; i < 16; i++) acc[i] = acc[i] + src[i];
+            }
+        }
+    }
+    if (kw != 0 || !live) return;
 
     const int o = g * Q8_TILE_ROWS + r;
     if (o >= mem.rows) return;
@@ -491,8 +660,8 @@ static __device__ __forceinline__ void gemm_body(const Q8GemmArgs &a) {
     }
 }
 
-extern "C" __global__ __launch_bounds__(256) void q8_gemm_s0(Q8GemmArgs a) { gemm_body<0>(a); }
-extern "C" __global__ __launch_bounds__(256) void q8_gemm_s1(Q8GemmArgs a) { gemm_body<1>(a); }
+extern "C" __global__ __launch_bounds__(1024) void q8_gemm_s0(Q8GemmArgs a) { gemm_body<0>(a); }
+extern "C" __global__ __launch_bounds__(1024) void q8_gemm_s1(Q8GemmArgs a) { gemm_body<1>(a); }
 
 // ---------------------------------------------------------------------------
 // Greedy argmax (sampler.rs:167-175): the first index whose value is strictly
@@ -557,6 +726,18 @@ extern "C" __global__ __launch_bounds__(256) void q8_argmax(Q8ArgmaxArgs a) {
             a.result[0] = (first != first || best == 0xffffffffu) ? 0u : best;
         }
     }
+}
+
+// Device-to-device copy of `bytes` (a multiple of 16) with dwordx4 loads and
+// stores: the counterpart of the reference's copy_f32 (gpu.cu:422-435), and the
+// plain streaming kernel of known size that the HBM traffic counters are
+// calibrated against.
+extern "C" __global__ __launch_bounds__(256) void q8_copy(Q8CopyArgs a) {
+    const long long n16 = a.bytes >> 4;
+    const long long stride = (long long)a.blocks * blockDim.x;
+    const i32x4 *src = (const i32x4 *)a.src;
+    i32x4 *dst = (i32x4 *)a.dst;
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
 }
 
 // act[i] = silu(gate[i]) * up[i]   (compute.rs:940-944)

@@ -83,6 +83,10 @@ typedef struct {
     int waves_per_tile;  /* W: waves splitting one tile's blocks */
     int pairs_per_wave;  /* ceil(ceil(nb/2) / W) */
     int silu_pair;       /* 1: m[0] = gate, m[1] = up; writes silu(g)*u to m[0].y */
+    int kslices;         /* S: workgroups splitting one tile's block pairs */
+    int pairs_per_slice; /* ceil(ceil(nb/2) / S) */
+    float *scratch;      /* S > 1: partial results shared between a tile's workgroups */
+    unsigned *counters;  /* S > 1: arrivals per tile, zero between launches */
 } Q8GemvArgs;
 
 typedef struct {
@@ -117,8 +121,13 @@ typedef struct {
     int ttiles;
     int tt_per_wg;  /* waves per workgroup, one token tile each */
     int tgroups;    /* ceil(ttiles / tt_per_wg) */
-    int nwg;        /* workgroups launched (total_rtiles * tgroups) */
+    int nwg;        /* workgroups launched (total_rtiles * tgroups * kslices) */
     int xcd_remap;  /* 1: map workgroups so one row tile's token groups share an XCD */
+    int kslices;          /* S: workgroups splitting the block pairs of one output tile group */
+    int pairs_per_slice;  /* ceil(ceil(nb/2) / S) */
+    int pairs_per_wave;   /* ceil(pairs_per_slice / kwaves) */
+    float *scratch;       /* S > 1: [rtiles][ttiles][S][64][16] partial tiles */
+    unsigned *counters;   /* S > 1: arrivals per (row tile, token group), zero between launches */
 } Q8GemmArgs;
 
 typedef struct {
@@ -128,6 +137,13 @@ typedef struct {
     const float *up;
     long long len;
 } Q8EltArgs;
+
+typedef struct {
+    const uint8_t *src;
+    uint8_t *dst;
+    long long bytes;
+    int blocks; /* workgroups launched */
+} Q8CopyArgs;
 
 typedef struct {
     const float *values;

@@ -70,6 +70,7 @@ enum Fn {
     F_GEMM_S0, F_GEMM_S1,
     F_ARGMAX,
     F_SILU_MUL,
+    F_COPY,
     F_COUNT
 };
 
@@ -81,9 +82,15 @@ const char *const kFnNames[F_COUNT] = {
     "q8_gemm_s0", "q8_gemm_s1",
     "q8_argmax",
     "q8_silu_mul",
+    "q8_copy",
 };
 
 constexpr int kArgmaxParts = 1024;
+// Split-K scratch, allocated once at open: 32 MiB of partial results and
+// 65536 arrival counters (zeroed once; each launch's last workgroup re-zeroes
+// the counters it used, so no memset is ever recorded into a graph).
+constexpr size_t kSplitBytes = 32u << 20;
+constexpr int kCounters = 65536;
 constexpr size_t kAlign = 256;
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
@@ -115,6 +122,8 @@ struct q8_ctx {
     void *tmp_ws = nullptr;              // gate/up f32 products of the n >= 2 FFN pair
     size_t tmp_ws_bytes = 0;
     void *argmax_ws = nullptr;           // per-workgroup partials + result
+    float *split_ws = nullptr;           // partial results of split-K workgroups
+    unsigned *counters = nullptr;        // split-K arrival counters (kernels reset them to 0)
     int cu_count = 0;
     size_t total_mem = 0;
     size_t max_lds = 0;
@@ -171,26 +180,49 @@ int grow(q8_ctx *c, void **buf, size_t *have, size_t need, const char *what) {
     return Q8_OK;
 }
 
-q8_tactic plan(q8_ctx *c, int n, int out, int k) {
+q8_tactic plan(q8_ctx *c, int n, int out, int k, int slots = 1) {
     q8_tactic t{};
     q8_tactics_choose(n, out, k, c->cu_count, &t);
     if (t.kernel == Q8_KERNEL_GEMV) {
+        if (slots != 1) q8_gemv_shape(out, k, c->cu_count, slots, &t);
         const int nb = k / 32;
         const int npairs = (nb + 1) / 2;
         t.exact = option(c, "gemv.exact", t.exact) ? 1 : 0;
+        const int sl = option(c, "gemv.slices", -1);
+        if (sl > 0) t.kslices = std::min(sl, npairs);
+        const int pps = (int)ceil_div(npairs, t.kslices);
+        t.kslices = (int)ceil_div(npairs, pps);
         const int w = option(c, "gemv.waves", -1);
-        if (w > 0) {
-            t.waves_per_tile = std::min(w, npairs);
-            t.pairs_per_wave = (int)ceil_div(npairs, t.waves_per_tile);
-            t.waves_per_tile = (int)ceil_div(npairs, t.pairs_per_wave);
+        if (w > 0 || sl > 0) {
+            int ww = w > 0 ? std::min(w, pps) : std::min(t.waves_per_tile, pps);
+            t.pairs_per_wave = (int)ceil_div(pps, ww);
+            t.waves_per_tile = (int)ceil_div(pps, t.pairs_per_wave);
         }
         const int pb = option(c, "gemv.pairs", -1);
         if (pb > 0) t.pairs_per_batch = pb;
     } else {
         t.smode = option(c, "gemm.smode", t.smode) ? 1 : 0;
-        const int tpw = option(c, "gemm.tt_per_wg", -1);
-        if (tpw > 0) t.tt_per_wg = std::min(tpw, 4);
         t.xcd_remap = option(c, "gemm.xcd_remap", t.xcd_remap) ? 1 : 0;
+        const int tpw = option(c, "gemm.tt_per_wg", -1);
+        const int kw = option(c, "gemm.kwaves", -1);
+        const int sl = option(c, "gemm.slices", -1);
+        if (tpw > 0 || kw > 0 || sl > 0) {
+            const int npairs = (k / 32 + 1) / 2;
+            const int ttiles = (int)ceil_div(n, 32);
+            int tt = tpw > 0 ? std::min(tpw, 4) : t.tt_per_wg;
+            tt = std::max(1, std::min(tt, ttiles));
+            int kws = kw > 0 ? kw : t.kwaves;
+            kws = std::max(1, std::min(kws, 16 / tt));
+            int s = sl > 0 ? sl : t.kslices;
+            s = std::max(1, std::min(s, npairs));
+            const int pps = (int)ceil_div(npairs, s);
+            s = (int)ceil_div(npairs, pps);
+            const int ppw = (int)ceil_div(pps, kws);
+            t.tt_per_wg = tt;
+            t.kslices = s;
+            t.pairs_per_wave = ppw;
+            t.kwaves = (int)ceil_div(pps, ppw);
+        }
     }
     return t;
 }
@@ -205,17 +237,6 @@ Fn gemv_fn(int pb, int exact) {
 }
 
 int valid_pb(int pb) { return pb == 2 || pb == 3 || pb == 5 || pb == 9; }
-
-// Re-split npairs block pairs over at most max_w waves (fused gate/up puts
-// two tiles' waves in one 512-thread workgroup).
-void fit_gemv_waves(q8_tactic *t, int npairs, int max_w) {
-    int w = std::min(max_w, npairs);
-    const int ppw = (int)ceil_div(npairs, w);
-    w = (int)ceil_div(npairs, ppw);
-    t->waves_per_tile = w;
-    t->pairs_per_wave = ppw;
-    t->pairs_per_batch = ppw <= 2 ? 2 : ppw <= 3 ? 3 : ppw <= 5 ? 5 : ppw <= 9 ? 9 : 5;
-}
 
 struct Member {
     const q8_weight *w;
@@ -239,8 +260,8 @@ int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const floa
         tile += m[i].w->tiles;
         rows_total += m[i].w->out;
     }
-    q8_tactic t = plan(c, 1, silu ? m[0].w->out : rows_total, k);
-    if (silu && t.waves_per_tile > 4) fit_gemv_waves(&t, (nb + 1) / 2, 4);
+    const int slots = silu ? 2 : 1;
+    const q8_tactic t = plan(c, 1, silu ? m[0].w->out : rows_total, k, slots);
     if (t.pairs_per_wave > 12)
         return fail(Q8_ERR_UNSUPPORTED, "gemv: %d block pairs per wave exceeds the staging bound of 12",
                     t.pairs_per_wave);
@@ -251,12 +272,26 @@ int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const floa
     a.waves_per_tile = t.waves_per_tile;
     a.pairs_per_wave = t.pairs_per_wave;
     a.silu_pair = silu;
-    const int slots = silu ? 2 : 1;
+    a.kslices = t.kslices;
+    a.pairs_per_slice = (int)ceil_div((nb + 1) / 2, t.kslices);
+    a.scratch = c->split_ws;
+    a.counters = c->counters;
     const int waves = t.waves_per_tile * slots;
-    if (waves * 64 > 512)
-        return fail(Q8_ERR_UNSUPPORTED, "gemv: %d waves per workgroup exceed the 512-thread launch bound", waves);
-    const unsigned lds = (unsigned)(nb * 32 * 4 + (t.exact ? slots * nb * 32 * 4 : waves * 32 * 4));
-    return launch(c, gemv_fn(pb, t.exact), (unsigned)a.total_tiles, (unsigned)(waves * 64), lds, &a, sizeof a);
+    const int max_threads = pb == 9 ? 512 : 1024;
+    if (waves * 64 > max_threads)
+        return fail(Q8_ERR_UNSUPPORTED, "gemv: %d waves per workgroup exceed the %d-thread launch bound", waves,
+                    max_threads);
+    if (t.kslices > 1) {
+        const size_t need = (size_t)slots * a.total_tiles * (t.exact ? nb : t.kslices) * 32 * sizeof(float);
+        if (need > kSplitBytes || a.total_tiles > kCounters)
+            return fail(Q8_ERR_UNSUPPORTED, "gemv: split-K needs %zu bytes of scratch for %d tiles", need,
+                        a.total_tiles);
+    }
+    const long long grid = (long long)a.total_tiles * t.kslices;
+    if (grid > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "gemv: grid of %lld workgroups", grid);
+    const unsigned lds =
+        (unsigned)(nb * 32 * 4 + ((t.exact && t.kslices == 1) ? slots * nb * 32 * 4 : waves * 32 * 4));
+    return launch(c, gemv_fn(pb, t.exact), (unsigned)grid, (unsigned)(waves * 64), lds, &a, sizeof a);
 }
 
 int run_gemm(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n, const float *bias) {
@@ -284,11 +319,26 @@ int run_gemm(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n,
     a.ttiles = (int)ceil_div(n, 32);
     a.tt_per_wg = std::max(1, std::min(t.tt_per_wg, a.ttiles));
     a.tgroups = (int)ceil_div(a.ttiles, a.tt_per_wg);
-    const long long nwg = (long long)rt * a.tgroups;
+    a.kslices = std::max(1, t.kslices);
+    a.pairs_per_slice = (int)ceil_div((nb + 1) / 2, a.kslices);
+    a.pairs_per_wave = std::max(1, t.pairs_per_wave);
+    const int kwaves = std::max(1, t.kwaves);
+    a.scratch = c->split_ws;
+    a.counters = c->counters;
+    const long long groups = (long long)rt * a.tgroups;
+    if (a.kslices > 1) {
+        const size_t need = (size_t)rt * a.ttiles * a.kslices * 64 * 16 * sizeof(float);
+        if (need > kSplitBytes || groups > kCounters)
+            return fail(Q8_ERR_UNSUPPORTED, "gemm: split-K needs %zu bytes of scratch", need);
+    }
+    const long long nwg = groups * a.kslices;
+    if (nwg > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "gemm: grid of %lld workgroups", nwg);
     a.nwg = (int)nwg;
     a.xcd_remap = (t.xcd_remap && nwg % 8 == 0) ? 1 : 0;
-    return launch(c, t.smode ? F_GEMM_S1 : F_GEMM_S0, (unsigned)nwg, (unsigned)(64 * a.tt_per_wg), 0, &a,
-                  sizeof a);
+    const int threads = 64 * a.tt_per_wg * kwaves;
+    if (threads > 1024) return fail(Q8_ERR_UNSUPPORTED, "gemm: %d threads per workgroup", threads);
+    const unsigned lds = (unsigned)((kwaves - 1) * a.tt_per_wg * 64 * 16 * sizeof(float));
+    return launch(c, t.smode ? F_GEMM_S1 : F_GEMM_S0, (unsigned)nwg, (unsigned)threads, lds, &a, sizeof a);
 }
 
 int prepare_into(q8_ctx *c, q8_dptr x, q8_dptr gate, q8_dptr up, int n, int k, q8_prepared *out) {
@@ -307,8 +357,9 @@ int prepare_into(q8_ctx *c, q8_dptr x, q8_dptr gate, q8_dptr up, int n, int k, q
     a.nb = nb;
     a.ttiles = (int)ttiles;
     a.mode = gate ? 1 : 0;
-    const long long threads = ttiles * Q8_TILE_TOKENS * nb * 8;
-    Q8_TRY(launch(c, F_QUANTIZE, (unsigned)ceil_div(threads, 256), 256, 0, &a, sizeof a));
+    const long long units = ttiles * nb;  // one wave per (token tile, block) unit, four per workgroup
+    if (units > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "prepare: %lld units", units);
+    Q8_TRY(launch(c, F_QUANTIZE, (unsigned)ceil_div(units, 4), 256, 0, &a, sizeof a));
     out->quants = (q8_dptr)(uintptr_t)a.xq;
     out->scales = (q8_dptr)(uintptr_t)a.xs;
     out->n = n;
@@ -417,6 +468,13 @@ int q8_open(int device, q8_ctx **out) {
         if (rc != Q8_OK) break;
         he = hipMalloc(&c->argmax_ws, kArgmaxParts * 8 + 256);
         if (he != hipSuccess) { rc = hip_fail(he, "hipMalloc(argmax)"); break; }
+        he = hipMalloc((void **)&c->split_ws, kSplitBytes);
+        if (he != hipSuccess) { rc = hip_fail(he, "hipMalloc(split scratch)"); break; }
+        he = hipMalloc((void **)&c->counters, kCounters * sizeof(unsigned));
+        if (he != hipSuccess) { rc = hip_fail(he, "hipMalloc(counters)"); break; }
+        he = hipMemset(c->counters, 0, kCounters * sizeof(unsigned));
+        if (he == hipSuccess) he = hipDeviceSynchronize();
+        if (he != hipSuccess) { rc = hip_fail(he, "hipMemset(counters)"); break; }
     } while (0);
     if (rc != Q8_OK) {
         q8_close(c);
@@ -438,6 +496,8 @@ void q8_close(q8_ctx *c) {
     if (c->act_ws) hipFree(c->act_ws);
     if (c->tmp_ws) hipFree(c->tmp_ws);
     if (c->argmax_ws) hipFree(c->argmax_ws);
+    if (c->split_ws) hipFree(c->split_ws);
+    if (c->counters) hipFree(c->counters);
     if (c->module) hipModuleUnload(c->module);
     if (c->stream) hipStreamDestroy(c->stream);
     delete c;
@@ -465,8 +525,9 @@ void *q8_stream(q8_ctx *c) { return c ? (void *)c->stream : nullptr; }
 
 int q8_set_option(q8_ctx *c, const char *name, int value) {
     if (!c || !name) return fail(Q8_ERR_INVALID, "q8_set_option: bad arguments");
-    static const char *const known[] = {"gemv.exact", "gemv.waves", "gemv.pairs",
-                                        "gemm.smode", "gemm.tt_per_wg", "gemm.xcd_remap"};
+    static const char *const known[] = {"gemv.exact",  "gemv.waves",     "gemv.pairs",
+                                        "gemv.slices", "gemm.smode",     "gemm.tt_per_wg",
+                                        "gemm.xcd_remap", "gemm.kwaves", "gemm.slices"};
     bool ok = false;
     for (const char *k : known) ok = ok || std::strcmp(k, name) == 0;
     if (!ok) return fail(Q8_ERR_INVALID, "unknown option %s", name);
@@ -568,7 +629,8 @@ int q8_weight_resident(q8_ctx *c, const void *bytes, size_t nbytes, int k, int o
     if (e != hipSuccess) rc = hip_fail(e, "hipMemcpyAsync(weight)");
     if (rc == Q8_OK) {
         const long long threads = (long long)tiles * Q8_TILE_ROWS * nb;
-        rc = launch(c, F_REPACK, (unsigned)ceil_div(threads, 256), 256, 0, &a, sizeof a);
+        if (threads > 0x7fffffffLL) rc = fail(Q8_ERR_UNSUPPORTED, "weight of %lld blocks is too large", threads);
+        if (rc == Q8_OK) rc = launch(c, F_REPACK, (unsigned)ceil_div(threads, 256), 256, 0, &a, sizeof a);
     }
     if (rc == Q8_OK) {
         e = hipStreamSynchronize(c->stream);
@@ -747,9 +809,8 @@ int q8_gate_up_silu(q8_ctx *c, const q8_weight *gate, const q8_weight *up, q8_dp
     const q8_dptr xp = (q8_dptr)(uintptr_t)fptr(x, x_offset);
     Q8_TRY(check_span(c, xp, (size_t)n * k * 4, "gate_up x"));
     if (n == 1) {
-        q8_tactic t = plan(c, 1, ffn, k);
-        if (t.waves_per_tile > 4) fit_gemv_waves(&t, (k / 32 + 1) / 2, 4);
-        if (t.pairs_per_wave <= 12) {
+        const q8_tactic t = plan(c, 1, ffn, k, 2);
+        if (t.pairs_per_wave <= 12 && t.waves_per_tile <= 8) {
             Member m[2] = {{gate, actp}, {up, nullptr}};
             Q8_TRY(run_gemv(c, m, 2, xp, k, nullptr, 1));
             if (prepared) Q8_TRY(prepare_into(c, (q8_dptr)(uintptr_t)actp, 0, 0, 1, ffn, prepared));
@@ -769,14 +830,33 @@ int q8_gate_up_silu(q8_ctx *c, const q8_weight *gate, const q8_weight *up, q8_dp
         Q8_TRY(prepare_into(c, xp, 0, 0, n, k, &px));
         Q8_TRY(run_gemm(c, m, 2, &px, n, nullptr));
     }
+    if (prepared) {
+        // compute.rs:993-1019: the product goes straight to Q8_0 for the down
+        // matmul and is never written in f32
+        return prepare_into(c, 0, (q8_dptr)(uintptr_t)g, (q8_dptr)(uintptr_t)u, n, ffn, prepared);
+    }
     Q8EltArgs a{};
     a.act = actp;
     a.gate = g;
     a.up = u;
     a.len = (long long)n * ffn;
-    Q8_TRY(launch(c, F_SILU_MUL, (unsigned)ceil_div(a.len, 256), 256, 0, &a, sizeof a));
-    if (prepared) Q8_TRY(prepare_into(c, 0, (q8_dptr)(uintptr_t)g, (q8_dptr)(uintptr_t)u, n, ffn, prepared));
-    return Q8_OK;
+    return launch(c, F_SILU_MUL, (unsigned)ceil_div(a.len, 256), 256, 0, &a, sizeof a);
+}
+
+int q8_copy_device(q8_ctx *c, q8_dptr dst, q8_dptr src, size_t bytes) {
+    if (!c) return fail(Q8_ERR_INVALID, "q8_copy_device: null context");
+    if (bytes == 0) return Q8_OK;
+    if (bytes % 16 != 0 || dst % 16 != 0 || src % 16 != 0)
+        return fail(Q8_ERR_INVALID, "q8_copy_device: pointers and size must be 16-byte multiples");
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    Q8_TRY(check_span(c, dst, bytes, "copy dst"));
+    Q8_TRY(check_span(c, src, bytes, "copy src"));
+    Q8CopyArgs a{};
+    a.src = reinterpret_cast<const uint8_t *>(src);
+    a.dst = reinterpret_cast<uint8_t *>(dst);
+    a.bytes = (long long)bytes;
+    a.blocks = (int)std::min<long long>(ceil_div((long long)(bytes / 16), 256), 8LL * c->cu_count);
+    return launch(c, F_COPY, (unsigned)a.blocks, 256, 0, &a, sizeof a);
 }
 
 int q8_lm_head_argmax(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset, q8_dptr logits,

@@ -23,35 +23,73 @@ constexpr int kCount = sizeof(kRows) / sizeof(kRows[0]);
 
 int ceil_div(long long a, long long b) { return (int)((a + b - 1) / b); }
 
-// GEMV launch shape: enough waves to cover every SIMD about twice, each wave
-// taking a contiguous run of block pairs (at most 12, the LDS staging bound),
-// with the first batch of loads covering the whole run when it is short.
-void gemv_shape(int out, int k, int cu_count, q8_tactic *t) {
+int pairs_per_batch(int ppw) { return ppw <= 2 ? 2 : ppw <= 3 ? 3 : ppw <= 5 ? 5 : 3; }
+
+}  // namespace
+
+// GEMV launch shape: one workgroup per 32-row tile (two for the fused
+// gate/up pair), its block pairs split over W waves.  Large matrices (two or
+// more tiles per CU) take four waves of up to nine pairs; smaller ones take
+// waves of about three pairs, up to 16 waves, so the whole matrix is in
+// flight at once.  Splitting a tile's blocks over several workgroups (kslices)
+// needs an agent-scope release per workgroup, which on gfx950 writes back the
+// XCD's L2; measured slower, so it is never chosen here (option "gemv.slices").
+void q8_gemv_shape(int out, int k, int cu_count, int slots, q8_tactic *t) {
     const int nb = k / 32;
     const int tiles = ceil_div(out, 32);
     const int npairs = ceil_div(nb, 2);
-    const long long target_waves = 2LL * 4 * std::max(cu_count, 1);
-    int w = (int)std::min<long long>(8, std::max<long long>(1, (target_waves + tiles - 1) / tiles));
-    w = std::max(w, ceil_div(npairs, 12));
-    w = std::min(w, npairs);
+    const int cus = std::max(cu_count, 1);
+    const int max_w = 16 / slots;
+    int w;
+    if (tiles >= 2 * cus)
+        w = std::min(std::min(4, max_w), npairs);
+    else
+        w = std::min(max_w, std::max(1, ceil_div(npairs, 3)));
     int ppw = ceil_div(npairs, w);
+    if (ppw > 12) ppw = 12;  // LDS staging bound of a wave
     w = ceil_div(npairs, ppw);
-    int pb = ppw <= 2 ? 2 : ppw <= 3 ? 3 : ppw <= 5 ? 5 : ppw <= 9 ? 9 : 5;
+    int s = 1;
+    if (w > max_w) {  // K too long for one workgroup: split it
+        s = ceil_div(w, max_w);
+        const int pps = ceil_div(npairs, s);
+        s = ceil_div(npairs, pps);
+        w = ceil_div(pps, ppw);
+    }
+    t->kslices = s;
     t->waves_per_tile = w;
     t->pairs_per_wave = ppw;
-    t->pairs_per_batch = pb;
+    t->pairs_per_batch = pairs_per_batch(ppw);
+    if (w * slots > 8 && t->pairs_per_batch == 9) t->pairs_per_batch = 5;
     t->exact = 1;
 }
 
-void gemm_shape(int n, int out, int /*k*/, int /*cu_count*/, q8_tactic *t) {
+// GEMM launch shape.  Waves own 32-token x 32-row output tiles, four token
+// tiles per workgroup.  When that leaves fewer than about two waves per SIMD,
+// the block pairs are also split over up to 16/TT waves of the workgroup,
+// reduced in LDS in a fixed order.
+void q8_gemm_shape(int n, int out, int k, int cu_count, q8_tactic *t) {
+    const int nb = k / 32;
+    const int npairs = ceil_div(nb, 2);
     const int ttiles = ceil_div(n, 32);
-    (void)out;
-    t->tt_per_wg = std::min(4, ttiles);
+    const int rtiles = ceil_div(out, 32);
+    const long long base = (long long)rtiles * ttiles;  // one wave per output tile
+    // about eight waves per SIMD: each wave's loop is bound by its own load and
+    // matrix-core latency, so more waves (K split) beat fewer, longer ones
+    // (n = 512 down, 2304 x 5760: 35 us at 8 K-waves vs 46 us at one)
+    const long long target = 32LL * std::max(cu_count, 1);
+    int f = (int)std::max<long long>(1, (target + base - 1) / base);
+    f = std::min(f, std::max(1, npairs / 3));
+    const int tt = f > 1 ? std::min(2, ttiles) : std::min(4, ttiles);
+    int kw = std::min(f, 16 / tt);
+    const int ppw = ceil_div(npairs, kw);
+    kw = ceil_div(npairs, ppw);
+    t->tt_per_wg = tt;
+    t->kwaves = kw;
+    t->kslices = 1;
+    t->pairs_per_wave = ppw;
     t->smode = 1;
     t->xcd_remap = 1;
 }
-
-}  // namespace
 
 int q8_tactics_table_size() { return kCount; }
 
@@ -71,8 +109,8 @@ int q8_tactics_choose(int n, int out, int k, int cu_count, q8_tactic *t) {
     t->name = best->name;
     t->evidence = best->evidence;
     if (best->kernel == Q8_KERNEL_GEMV)
-        gemv_shape(out, k, cu_count, t);
+        q8_gemv_shape(out, k, cu_count, 1, t);
     else
-        gemm_shape(n, out, k, cu_count, t);
+        q8_gemm_shape(n, out, k, cu_count, t);
     return Q8_OK;
 }

@@ -21,10 +21,12 @@ struct Q8TacticRow {
     const char *evidence;
 };
 
-// Number of CUs the launch heuristics size for (MI355X: 256).
 int q8_tactics_table_size();
 const Q8TacticRow &q8_tactics_row(int i);
 // Resolve the tactic for one matmul; cu_count sizes the grid heuristics.
 int q8_tactics_choose(int n, int out, int k, int cu_count, q8_tactic *t);
+// Launch shapes (slots = member tiles per GEMV workgroup: 2 for fused gate/up).
+void q8_gemv_shape(int out, int k, int cu_count, int slots, q8_tactic *t);
+void q8_gemm_shape(int n, int out, int k, int cu_count, q8_tactic *t);
 
 #endif

@@ -44,7 +44,7 @@ EXPORTS = (
     "q8_weight_resident", "q8_weight_release", "q8_weight_shape", "q8_weight_export",
     "q8_matmul", "q8_prepare", "q8_silu_mul_prepare", "q8_silu_mul",
     "q8_matmul_decode_group", "q8_matmul_prompt_group", "q8_gate_up_silu",
-    "q8_lm_head_argmax", "q8_argmax",
+    "q8_lm_head_argmax", "q8_argmax", "q8_copy_device",
     "q8_plan", "q8_tactic_count", "q8_tactic_row",
     "q8_event_create", "q8_event_record", "q8_event_elapsed_ms", "q8_event_destroy",
     "q8_graph_begin", "q8_graph_end", "q8_graph_launch", "q8_graph_destroy",
@@ -72,7 +72,8 @@ class Tactic(ctypes.Structure):
     _fields_ = [("kernel", ctypes.c_int), ("waves_per_tile", ctypes.c_int),
                 ("pairs_per_wave", ctypes.c_int), ("pairs_per_batch", ctypes.c_int),
                 ("exact", ctypes.c_int), ("tt_per_wg", ctypes.c_int), ("smode", ctypes.c_int),
-                ("xcd_remap", ctypes.c_int), ("name", ctypes.c_char_p), ("evidence", ctypes.c_char_p)]
+                ("xcd_remap", ctypes.c_int), ("kslices", ctypes.c_int), ("kwaves", ctypes.c_int),
+                ("name", ctypes.c_char_p), ("evidence", ctypes.c_char_p)]
 
     def as_dict(self) -> dict:
         d = {f: getattr(self, f) for f, _ in self._fields_}
@@ -127,6 +128,7 @@ def lib():
         "q8_gate_up_silu": (c_int, [vp, vp, vp, u64, c_size, c_int, u64, c_size, ctypes.POINTER(Prepared)]),
         "q8_lm_head_argmax": (c_int, [vp, vp, u64, c_size, u64, c_size, ctypes.POINTER(ctypes.c_uint32)]),
         "q8_argmax": (c_int, [vp, u64, c_size, c_size, ctypes.POINTER(ctypes.c_uint32)]),
+        "q8_copy_device": (c_int, [vp, u64, u64, c_size]),
         "q8_plan": (c_int, [vp, c_int, c_int, c_int, ctypes.POINTER(Tactic)]),
         "q8_tactic_count": (c_int, []),
         "q8_tactic_row": (c_int, [c_int, ctypes.POINTER(Tactic), ctypes.POINTER(c_int), ctypes.POINTER(c_int)]),
@@ -343,6 +345,9 @@ class Gpu:
         out = ctypes.c_uint32()
         _check(lib().q8_argmax(self.handle, values.ptr, offset, length, ctypes.byref(out)))
         return int(out.value)
+
+    def copy(self, dst: DeviceBuffer, src: DeviceBuffer, nbytes: int):
+        _check(lib().q8_copy_device(self.handle, dst.ptr, src.ptr, nbytes))
 
     def plan(self, n: int, out: int, k: int) -> dict:
         return plan(n, out, k, self)

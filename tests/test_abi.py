@@ -81,8 +81,9 @@ def test_tactic_table_invariants():
 
 
 @pytest.mark.parametrize("n,out,k", [(1, 5760, 2304), (1, 122880, 2304), (1, 2304, 5760), (1, 4, 32),
-                                     (1, 33, 96), (2, 64, 64), (8, 5760, 2304), (64, 5760, 2304),
-                                     (512, 11520, 2304), (1024, 2304, 5760)])
+                                     (1, 33, 96), (1, 100, 11520), (1, 8000, 16384), (2, 64, 64),
+                                     (8, 5760, 2304), (64, 5760, 2304), (512, 11520, 2304), (512, 2304, 5760),
+                                     (1024, 2304, 5760)])
 def test_plan_never_selects_a_rejected_tactic(n, out, k):
     rejected = {r["name"] for r in llm_amd.tactic_table() if r["maturity"] == 0}
     t = llm_amd.plan(n, out, k)
@@ -92,13 +93,19 @@ def test_plan_never_selects_a_rejected_tactic(n, out, k):
         nb = k // 32
         npairs = (nb + 1) // 2
         assert 1 <= t["pairs_per_wave"] <= 12
-        assert t["waves_per_tile"] * t["pairs_per_wave"] >= npairs
-        assert (t["waves_per_tile"] - 1) * t["pairs_per_wave"] < npairs  # no empty wave
-        assert t["waves_per_tile"] * 64 <= 512
+        assert t["waves_per_tile"] * 64 <= (512 if t["pairs_per_batch"] == 9 else 1024)
         assert t["pairs_per_batch"] in (2, 3, 5, 9)
+        s = t["kslices"]
+        pps = -(-npairs // s)
+        assert 1 <= s <= npairs and (s - 1) * pps < npairs  # no empty slice
+        assert t["waves_per_tile"] * t["pairs_per_wave"] >= pps
     else:
         assert t["kernel"] == q8.KERNEL_GEMM
         assert 1 <= t["tt_per_wg"] <= 4
+        assert t["tt_per_wg"] * t["kwaves"] * 64 <= 1024
+        npairs = (k // 32 + 1) // 2
+        pps = -(-npairs // t["kslices"])
+        assert t["kwaves"] * t["pairs_per_wave"] >= pps
 
 
 def test_plan_rejects_bad_shapes():
