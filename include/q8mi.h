@@ -93,7 +93,8 @@ typedef struct {
     int pairs_per_wave;  /* GEMV: block pairs per wave */
     int pairs_per_batch; /* GEMV: block pairs whose loads are issued together */
     int exact;           /* GEMV: 1 = left-to-right block sum (bit-exact) */
-    int tt_per_wg;       /* GEMM: 32-token tiles (waves) per workgroup */
+    int tpw;             /* GEMM: 32-token tiles per wave (1, 2 or 4) */
+    int twaves;          /* GEMM: waves along the tokens per workgroup */
     int smode;           /* GEMM: 1 = scale products on the matrix cores */
     int xcd_remap;       /* GEMM: keep a row tile's workgroups on one XCD */
     int kslices;         /* workgroups splitting one output tile's blocks (1 = none) */
@@ -125,7 +126,7 @@ int q8_device_info(q8_ctx *ctx, int *cu_count, size_t *total_bytes, size_t *free
 void *q8_stream(q8_ctx *ctx);
 /* Tuning/testing switches; value -1 restores the tactic table's choice.
  * Names: "gemv.exact", "gemv.waves", "gemv.pairs", "gemv.slices",
- * "gemm.smode", "gemm.tt_per_wg", "gemm.xcd_remap", "gemm.kwaves",
+ * "gemm.smode", "gemm.tpw", "gemm.twaves", "gemm.xcd_remap", "gemm.kwaves",
  * "gemm.slices". */
 int q8_set_option(q8_ctx *ctx, const char *name, int value);
 

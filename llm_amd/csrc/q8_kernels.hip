@@ -440,35 +440,40 @@ extern "C" __global__ __launch_bounds__(256) void q8_quantize(Q8QuantArgs a) {
 // ---------------------------------------------------------------------------
 // GEMM, n >= 2 (tensor.rs:104-148 -> quant.rs:156-181).
 //
-// One wave computes a 32-token x 32-row output tile with
-// v_mfma_i32_32x32x32_i8: one instruction is exactly one Q8_0 block, so its
-// int32 result is the reference's exact block dot Σ q_w q_x.  A = activations
-// (tokens), B = weights (rows), so each lane owns one output row and its
-// stores are row-contiguous.  The per-block f32 scale product d_w * s_x is
-// either
-//   SMODE 1: one v_mfma_f32_32x32x1_2b_f32 outer product per block pair,
-//            landing in the accumulator's register layout, or
-//   SMODE 0: VALU multiplies from the lanes' 16 token scales;
+// v_mfma_i32_32x32x32_i8 is exactly one Q8_0 block per instruction, so its
+// int32 result is the reference's exact block dot sum q_w q_x.  A =
+// activations (tokens), B = weights (rows): each lane owns one output row and
+// its stores are row-contiguous.  The per-block f32 scale d_w * s_x is
+//   SMODE 1: one v_mfma_f32_32x32x1_2b_f32 outer product per block pair, which
+//            lands in the accumulator's register layout, or
+//   SMODE 0: VALU multiplies of the lane's row scale by its 16 token scales;
 // then acc = fma(float(I_b), d_w*s_x, acc) block by block, as the reference's
-// AVX2 lanes do.  Workgroup = tt_per_wg waves over consecutive token tiles of
-// one row tile, so they share its weight stream through L1.
+// AVX2 lanes accumulate.
+//
+// A wave owns TPW token tiles x one 32-row tile: the weight stream and its
+// scale are loaded once for TPW tiles, and the TPW independent MFMA chains
+// keep the wave busy while one of them waits.  A workgroup holds twaves such
+// waves along the tokens times kwaves along K; the K-split waves are reduced
+// in LDS in a fixed order, and optional K slices across workgroups by the
+// last workgroup to arrive.
 // ---------------------------------------------------------------------------
-// Operands of one block pair for one wave (SMODE 1: one scale per lane).
-struct GemmPair {
-    i32x4 x0, w0, x1, w1;
-    float sx;
+template <int TPW>
+struct GemmOps {
+    i32x4 w0, w1;
     unsigned dw;
+    i32x4 x0[TPW], x1[TPW];
+    float sx[TPW];
 };
 
-template <int SMODE>
+template <int SMODE, int TPW>
 static __device__ __forceinline__ void gemm_body(const Q8GemmArgs &a) {
-    extern __shared__ __attribute__((aligned(16))) float gsm[];  // [kwaves-1][tt_per_wg][64][16] partials
+    extern __shared__ __attribute__((aligned(16))) float gsm[];  // [kwaves-1][twaves][TPW][64][16]
     __shared__ int last_flag;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform, in an SGPR
-    const int TT = a.tt_per_wg;
-    const int tw = wave % TT;  // token tile within the workgroup
-    const int kw = wave / TT;  // K-split wave
+    const int TW = a.twaves;
+    const int tw = wave % TW;  // token-tile group of this wave
+    const int kw = wave / TW;  // K-split wave
     const int S = a.kslices;
     int wg = blockIdx.x;
     if (a.xcd_remap) {
@@ -480,8 +485,8 @@ static __device__ __forceinline__ void gemm_body(const Q8GemmArgs &a) {
     const int rtg = wg / S;
     const int rt = rtg / a.tgroups;
     const int tg = rtg - rt * a.tgroups;
-    const int tt = tg * TT + tw;
-    const bool live = tt < a.ttiles;  // padding waves still meet every barrier
+    const int tt0 = (tg * TW + tw) * TPW;               // first token tile of this wave
+    const int ntl = max(0, min(TPW, a.ttiles - tt0));   // live token tiles (wave-uniform)
     int mi = 0;
 #pragma unroll
     for (int i = 1; i < Q8_GROUP_MAX; i++)
@@ -491,139 +496,171 @@ static __device__ __forceinline__ void gemm_body(const Q8GemmArgs &a) {
     const int nb = a.nb;
     const int h = lane >> 5;
     const int r = lane & 31;
-    const int ttc = min(tt, a.ttiles - 1);  // clamped, always a valid tile to address
-    const uint8_t *wq = mem.quants + (size_t)g * nb * Q8_UNIT_BYTES + lane * 16;
+    // Stream bases are wave-uniform (SGPRs); a lane adds only its constant
+    // offset, so loads need no per-block VALU address arithmetic.
+    const uint8_t *wq = mem.quants + (size_t)g * nb * Q8_UNIT_BYTES;
     const uint16_t *wsc = mem.scales + (size_t)g * nb * Q8_TILE_ROWS;
-    const uint8_t *xq = a.xq + (size_t)ttc * nb * Q8_UNIT_BYTES + lane * 16;
-    const float *xsc = a.xs + (size_t)ttc * nb * Q8_TILE_TOKENS;
+    const uint8_t *xq[TPW];
+    const float *xsc[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; t++) {
+        const int ttc = min(tt0 + t, a.ttiles - 1);  // clamped: always a valid tile to address
+        xq[t] = a.xq + (size_t)ttc * nb * Q8_UNIT_BYTES;
+        xsc[t] = a.xs + (size_t)ttc * nb * Q8_TILE_TOKENS;
+    }
+    const int lo = lane * 16;
 
     // this wave's block pairs: slice range split over the kw waves
     const int npairs = (nb + 1) >> 1;
     const int s_begin = slice * a.pairs_per_slice;
     const int s_end = min(npairs, s_begin + a.pairs_per_slice);
     const int p_begin = s_begin + kw * a.pairs_per_wave;
-    const int p_end = live ? min(s_end, p_begin + a.pairs_per_wave) : p_begin;
+    const int p_end = ntl > 0 ? min(s_end, p_begin + a.pairs_per_wave) : p_begin;
+    const int full_end = min(p_end, nb >> 1);  // pairs whose two blocks both exist
 
-    f32x16 acc;
+    f32x16 acc[TPW];
 #pragma unroll
-    for (int i = 0; i < 16; i++) acc[i] = 0.0f;
+    for (int t = 0; t < TPW; t++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[t][i] = 0.0f;
     const i32x16 izero = {};
     const f32x32 fzero = {};
 
-    // One block pair: int32 block dots on the matrix cores, then the f32
-    // scale epilogue, block b before block b+1 (the reference's order).
-    auto pair_step = [&](const GemmPair &q, int b, bool two) {
-        const i32x16 i0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(q.x0, q.w0, izero, 0, 0, 0);
-        const i32x16 i1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(q.x1, q.w1, izero, 0, 0, 0);
+    // Loads of the full pair (b, b+1): lane L's scale slot (b + h, r) is
+    // element b*32 + L of the scale stream.
+    auto load_full = [&](GemmOps<TPW> &q, int b) {
+        const size_t u0 = (size_t)b * Q8_UNIT_BYTES;
+        q.w0 = *(const i32x4 *)(wq + u0 + lo);
+        q.w1 = *(const i32x4 *)(wq + u0 + Q8_UNIT_BYTES + lo);
+        q.dw = wsc[(size_t)b * Q8_TILE_ROWS + lane];
+#pragma unroll
+        for (int t = 0; t < TPW; t++) {
+            q.x0[t] = *(const i32x4 *)(xq[t] + u0 + lo);
+            q.x1[t] = *(const i32x4 *)(xq[t] + u0 + Q8_UNIT_BYTES + lo);
+            q.sx[t] = xsc[t][(size_t)b * Q8_TILE_TOKENS + lane];
+        }
+    };
+    // The odd last block of an odd nb: the absent block repeats block b with
+    // zero scales, so it adds 0 * 0.
+    auto load_last = [&](GemmOps<TPW> &q, int b) {
+        const size_t u0 = (size_t)b * Q8_UNIT_BYTES;
+        q.w0 = *(const i32x4 *)(wq + u0 + lo);
+        q.w1 = q.w0;
+        q.dw = h ? 0u : (unsigned)wsc[(size_t)b * Q8_TILE_ROWS + r];
+#pragma unroll
+        for (int t = 0; t < TPW; t++) {
+            q.x0[t] = *(const i32x4 *)(xq[t] + u0 + lo);
+            q.x1[t] = q.x0[t];
+            q.sx[t] = h ? 0.0f : xsc[t][(size_t)b * Q8_TILE_TOKENS + r];
+        }
+    };
+    // One block pair of one token tile: the scale products first (the
+    // longest MFMA), then the two block dots, then block b's and block b+1's
+    // epilogues in that order.
+    auto step = [&](const GemmOps<TPW> &q, int t, int b, bool two) {
         if (SMODE == 1) {
             // lanes 0-31 carry block b and lanes 32-63 block b+1: the two blocks
             // of the outer-product MFMA, d_w * s_x in the accumulator layout.
-            const f32x32 sc = __builtin_amdgcn_mfma_f32_32x32x1f32(q.sx, f16_to_f32(q.dw), fzero, 0, 0, 0);
+            const f32x32 sc = __builtin_amdgcn_mfma_f32_32x32x1f32(q.sx[t], f16_to_f32(q.dw), fzero, 0, 0, 0);
+            const i32x16 i0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(q.x0[t], q.w0, izero, 0, 0, 0);
+            const i32x16 i1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(q.x1[t], q.w1, izero, 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < 16; i++) acc[i] = __builtin_fmaf((float)i0[i], sc[i], acc[i]);
+            for (int i = 0; i < 16; i++) acc[t][i] = __builtin_fmaf((float)i0[i], sc[i], acc[t][i]);
             if (two) {
 #pragma unroll
-                for (int i = 0; i < 16; i++) acc[i] = __builtin_fmaf((float)i1[i], sc[16 + i], acc[i]);
+                for (int i = 0; i < 16; i++) acc[t][i] = __builtin_fmaf((float)i1[i], sc[16 + i], acc[t][i]);
             }
         } else {
+            const i32x16 i0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(q.x0[t], q.w0, izero, 0, 0, 0);
+            const i32x16 i1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(q.x1[t], q.w1, izero, 0, 0, 0);
             // lane owns row r and tokens 8(i/4) + 4h + (i%4) of the tile
             const int b1 = two ? b + 1 : b;
             const float dw0 = f16_to_f32(wsc[(size_t)b * Q8_TILE_ROWS + r]);
             const float dw1 = f16_to_f32(wsc[(size_t)b1 * Q8_TILE_ROWS + r]);
-            f32x4 s0[4], s1[4];
-#pragma unroll
-            for (int qq = 0; qq < 4; qq++) {
-                s0[qq] = *(const f32x4 *)(xsc + (size_t)b * Q8_TILE_TOKENS + 8 * qq + 4 * h);
-                s1[qq] = *(const f32x4 *)(xsc + (size_t)b1 * Q8_TILE_TOKENS + 8 * qq + 4 * h);
-            }
+            const float *xs0 = xsc[t] + (size_t)b * Q8_TILE_TOKENS + 4 * h;
+            const float *xs1 = xsc[t] + (size_t)b1 * Q8_TILE_TOKENS + 4 * h;
 #pragma unroll
             for (int i = 0; i < 16; i++) {
-                const float c0 = dw0 * s0[i >> 2][i & 3];
-                acc[i] = __builtin_fmaf((float)i0[i], c0, acc[i]);
+                const float c0 = dw0 * xs0[8 * (i >> 2) + (i & 3)];
+                acc[t][i] = __builtin_fmaf((float)i0[i], c0, acc[t][i]);
             }
             if (two) {
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
-                    const float c1 = dw1 * s1[i >> 2][i & 3];
-                    acc[i] = __builtin_fmaf((float)i1[i], c1, acc[i]);
+                    const float c1 = dw1 * xs1[8 * (i >> 2) + (i & 3)];
+                    acc[t][i] = __builtin_fmaf((float)i1[i], c1, acc[t][i]);
                 }
             }
         }
     };
-    // Full pairs walk the unit streams by pointer; the odd last block of an
-    // odd nb (its pair's second block absent) is handled after the loop.
-    const int full_end = min(p_end, nb >> 1);  // pairs whose two blocks both exist
-    auto load_pair = [&](int b, bool two) {
-        GemmPair q;
-        const int b1 = two ? b + 1 : b;
-        const int bs = two ? b + h : b;
-        q.x0 = *(const i32x4 *)(xq + (size_t)b * Q8_UNIT_BYTES);
-        q.w0 = *(const i32x4 *)(wq + (size_t)b * Q8_UNIT_BYTES);
-        q.x1 = *(const i32x4 *)(xq + (size_t)b1 * Q8_UNIT_BYTES);
-        q.w1 = *(const i32x4 *)(wq + (size_t)b1 * Q8_UNIT_BYTES);
-        q.sx = xsc[(size_t)bs * Q8_TILE_TOKENS + r];
-        q.dw = wsc[(size_t)bs * Q8_TILE_ROWS + r];
-        if (!two && h) {  // the absent block contributes 0 * 0
-            q.sx = 0.0f;
-            q.dw = 0u;
-        }
-        return q;
-    };
 
+    // Full pairs, two per iteration with ping-pong operand sets (no register
+    // copies); each set's loads are issued one pair ahead of its use, and
+    // sched_barrier keeps the compiler from sinking them next to their use.
     if (p_begin < full_end) {
-        GemmPair cur = load_pair(2 * p_begin, true);
-        for (int p = p_begin; p < full_end; p++) {
-            if (SMODE == 1) {
-                // Matrix-core work of this pair first (the scale products, whose
-                // result the epilogue needs last-issued-first-ready, then the two
-                // block dots), then the next pair's loads, then the VALU epilogue
-                // while those loads are in flight.  sched_barrier keeps the
-                // compiler from sinking the loads next to their use.
-                const f32x32 sc = __builtin_amdgcn_mfma_f32_32x32x1f32(cur.sx, f16_to_f32(cur.dw), fzero, 0, 0, 0);
-                const i32x16 i0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.x0, cur.w0, izero, 0, 0, 0);
-                const i32x16 i1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.x1, cur.w1, izero, 0, 0, 0);
-                __builtin_amdgcn_sched_barrier(0);
-                cur = load_pair(2 * min(p + 1, full_end - 1), true);
-                __builtin_amdgcn_sched_barrier(0);
+        GemmOps<TPW> qa, qb;
+        load_full(qa, 2 * p_begin);
+        int p = p_begin;
+        for (; p + 1 < full_end; p += 2) {
+            load_full(qb, 2 * (p + 1));
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int i = 0; i < 16; i++) acc[i] = __builtin_fmaf((float)i0[i], sc[i], acc[i]);
+            for (int t = 0; t < TPW; t++) step(qa, t, 2 * p, true);
+            __builtin_amdgcn_sched_barrier(0);
+            load_full(qa, 2 * min(p + 2, full_end - 1));
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int i = 0; i < 16; i++) acc[i] = __builtin_fmaf((float)i1[i], sc[16 + i], acc[i]);
-            } else {
-                const GemmPair nxt = load_pair(2 * min(p + 1, full_end - 1), true);
-                pair_step(cur, 2 * p, true);
-                cur = nxt;
-            }
+            for (int t = 0; t < TPW; t++) step(qb, t, 2 * (p + 1), true);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (p < full_end) {
+#pragma unroll
+            for (int t = 0; t < TPW; t++) step(qa, t, 2 * p, true);
         }
     }
     if (full_end < p_end) {  // odd nb: the last pair holds one block
-        const GemmPair q = load_pair(2 * full_end, false);
-        pair_step(q, 2 * full_end, false);
+        GemmOps<TPW> q;
+        load_last(q, 2 * full_end);
+#pragma unroll
+        for (int t = 0; t < TPW; t++) step(q, t, 2 * full_end, false);
     }
 
-    const int KW = (blockDim.x >> 6) / TT;
+    const int KW = (blockDim.x >> 6) / TW;
     if (KW > 1) {
         // reduce the K-split waves in a fixed order: kw = 0 adds 1, 2, ...
         if (kw > 0) {
-            float *dst = gsm + ((size_t)((kw - 1) * TT + tw) * 64 + lane) * 16;
 #pragma unroll
-            for (int i = 0; i < 16; i += 4) *(f32x4 *)(dst + i) = (f32x4){acc[i], acc[i + 1], acc[i + 2], acc[i + 3]};
+            for (int t = 0; t < TPW; t++) {
+                float *dst = gsm + ((size_t)(((kw - 1) * TW + tw) * TPW + t) * 64 + lane) * 16;
+#pragma unroll
+                for (int i = 0; i < 16; i += 4)
+                    *(f32x4 *)(dst + i) = (f32x4){acc[t][i], acc[t][i + 1], acc[t][i + 2], acc[t][i + 3]};
+            }
         }
         __syncthreads();
         if (kw == 0) {
             for (int k2 = 1; k2 < KW; k2++) {
-                const float *src = gsm + ((size_t)((k2 - 1) * TT + tw) * 64 + lane) * 16;
 #pragma unroll
-                for (int i = 0; i < 16; i++) acc[i] = acc[i] + src[i];
+                for (int t = 0; t < TPW; t++) {
+                    const float *src = gsm + ((size_t)(((k2 - 1) * TW + tw) * TPW + t) * 64 + lane) * 16;
+#pragma unroll
+                    for (int i = 0; i < 16; i++) acc[t][i] = acc[t][i] + src[i];
+                }
             }
         }
     }
     if (S > 1) {
         // per-slice partial tiles in scratch; the tile group's last workgroup sums them in slice order
-        float *part = a.scratch + ((size_t)((rt * a.ttiles + ttc) * S + slice) * 64 + lane) * 16;
-        if (kw == 0 && live) {
+        if (kw == 0) {
 #pragma unroll
-            for (int i = 0; i < 16; i += 4) *(f32x4 *)(part + i) = (f32x4){acc[i], acc[i + 1], acc[i + 2], acc[i + 3]};
+            for (int t = 0; t < TPW; t++) {
+                if (t < ntl) {
+                    float *part = a.scratch + ((size_t)(((size_t)rt * a.ttiles + tt0 + t) * S + slice) * 64 + lane) * 16;
+#pragma unroll
+                    for (int i = 0; i < 16; i += 4)
+                        *(f32x4 *)(part + i) = (f32x4){acc[t][i], acc[t][i + 1], acc[t][i + 2], acc[t][i + 3]};
+                }
+            }
         }
         __threadfence();
         __syncthreads();
@@ -635,33 +672,45 @@ static __device__ __forceinline__ void gemm_body(const Q8GemmArgs &a) {
         if (!last_flag) return;
         __threadfence();
         if (threadIdx.x == 0) a.counters[rtg] = 0u;
-        if (kw == 0 && live) {
-            const float *base = a.scratch + ((size_t)((rt * a.ttiles + ttc) * S) * 64 + lane) * 16;
+        if (kw == 0) {
 #pragma unroll
-            for (int i = 0; i < 16; i++) acc[i] = 0.0f;
-            for (int sl = 0; sl < S; sl++) {
-                const float *src = base + (size_t)sl * 64 * 16;
+            for (int t = 0; t < TPW; t++) {
+                if (t < ntl) {
+                    const float *base = a.scratch + ((size_t)(((size_t)rt * a.ttiles + tt0 + t) * S) * 64 + lane) * 16;
 #pragma unroll
-                for (int i = 0; i < 16; i++) acc[i] = acc[i] + src[i];
+                    for (int i = 0; i < 16; i++) acc[t][i] = 0.0f;
+                    for (int sl = 0; sl < S; sl++) {
+                        const float *src = base + (size_t)sl * 64 * 16;
+#pragma unroll
+                        for (int i = 0; i < 16; i++) acc[t][i] = acc[t][i] + src[i];
+                    }
+                }
             }
         }
     }
-    if (kw != 0 || !live) return;
+    if (kw != 0) return;
 
     const int o = g * Q8_TILE_ROWS + r;
     if (o >= mem.rows) return;
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const int t = tt * Q8_TILE_TOKENS + 8 * (i >> 2) + 4 * h + (i & 3);
-        if (t < a.n) {
-            const size_t idx = (size_t)t * mem.rows + o;
-            mem.y[idx] = mem.bias ? acc[i] + mem.bias[idx] : acc[i];
+    for (int t = 0; t < TPW; t++) {
+        if (t < ntl) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int tok = (tt0 + t) * Q8_TILE_TOKENS + 8 * (i >> 2) + 4 * h + (i & 3);
+                if (tok < a.n) {
+                    const size_t idx = (size_t)tok * mem.rows + o;
+                    mem.y[idx] = mem.bias ? acc[t][i] + mem.bias[idx] : acc[t][i];
+                }
+            }
         }
     }
 }
 
-extern "C" __global__ __launch_bounds__(1024) void q8_gemm_s0(Q8GemmArgs a) { gemm_body<0>(a); }
-extern "C" __global__ __launch_bounds__(1024) void q8_gemm_s1(Q8GemmArgs a) { gemm_body<1>(a); }
+extern "C" __global__ __launch_bounds__(1024) void q8_gemm_s0_t1(Q8GemmArgs a) { gemm_body<0, 1>(a); }
+extern "C" __global__ __launch_bounds__(1024) void q8_gemm_s1_t1(Q8GemmArgs a) { gemm_body<1, 1>(a); }
+extern "C" __global__ __launch_bounds__(512) void q8_gemm_s1_t2(Q8GemmArgs a) { gemm_body<1, 2>(a); }
+extern "C" __global__ __launch_bounds__(512) void q8_gemm_s1_t4(Q8GemmArgs a) { gemm_body<1, 4>(a); }
 
 // ---------------------------------------------------------------------------
 // Greedy argmax (sampler.rs:167-175): the first index whose value is strictly

@@ -119,8 +119,8 @@ typedef struct {
     int n;
     int nb;
     int ttiles;
-    int tt_per_wg;  /* waves per workgroup, one token tile each */
-    int tgroups;    /* ceil(ttiles / tt_per_wg) */
+    int twaves;     /* waves along the tokens per workgroup (each TPW token tiles) */
+    int tgroups;    /* ceil(ttiles / (twaves * TPW)) */
     int nwg;        /* workgroups launched (total_rtiles * tgroups * kslices) */
     int xcd_remap;  /* 1: map workgroups so one row tile's token groups share an XCD */
     int kslices;          /* S: workgroups splitting the block pairs of one output tile group */

@@ -67,7 +67,7 @@ enum Fn {
     F_REPACK,
     F_GEMV_2_0, F_GEMV_2_1, F_GEMV_3_0, F_GEMV_3_1, F_GEMV_5_0, F_GEMV_5_1, F_GEMV_9_0, F_GEMV_9_1,
     F_QUANTIZE,
-    F_GEMM_S0, F_GEMM_S1,
+    F_GEMM_S0_T1, F_GEMM_S1_T1, F_GEMM_S1_T2, F_GEMM_S1_T4,
     F_ARGMAX,
     F_SILU_MUL,
     F_COPY,
@@ -79,7 +79,7 @@ const char *const kFnNames[F_COUNT] = {
     "q8_gemv_pb2_e0", "q8_gemv_pb2_e1", "q8_gemv_pb3_e0", "q8_gemv_pb3_e1",
     "q8_gemv_pb5_e0", "q8_gemv_pb5_e1", "q8_gemv_pb9_e0", "q8_gemv_pb9_e1",
     "q8_quantize",
-    "q8_gemm_s0", "q8_gemm_s1",
+    "q8_gemm_s0_t1", "q8_gemm_s1_t1", "q8_gemm_s1_t2", "q8_gemm_s1_t4",
     "q8_argmax",
     "q8_silu_mul",
     "q8_copy",
@@ -203,22 +203,27 @@ q8_tactic plan(q8_ctx *c, int n, int out, int k, int slots = 1) {
     } else {
         t.smode = option(c, "gemm.smode", t.smode) ? 1 : 0;
         t.xcd_remap = option(c, "gemm.xcd_remap", t.xcd_remap) ? 1 : 0;
-        const int tpw = option(c, "gemm.tt_per_wg", -1);
+        const int tpw = option(c, "gemm.tpw", -1);
+        const int tw = option(c, "gemm.twaves", -1);
         const int kw = option(c, "gemm.kwaves", -1);
         const int sl = option(c, "gemm.slices", -1);
-        if (tpw > 0 || kw > 0 || sl > 0) {
+        if (tpw > 0) t.tpw = (tpw >= 4) ? 4 : (tpw >= 2 ? 2 : 1);
+        if (!t.smode) t.tpw = 1;  // the VALU-scale variant is built for one token tile per wave
+        if (tpw > 0 || tw > 0 || kw > 0 || sl > 0 || !t.smode) {
             const int npairs = (k / 32 + 1) / 2;
             const int ttiles = (int)ceil_div(n, 32);
-            int tt = tpw > 0 ? std::min(tpw, 4) : t.tt_per_wg;
-            tt = std::max(1, std::min(tt, ttiles));
+            const int groups = (int)ceil_div(ttiles, t.tpw);
+            const int max_threads = t.tpw == 1 ? 1024 : 512;
+            int twv = tw > 0 ? tw : t.twaves;
+            twv = std::max(1, std::min(twv, std::min(groups, max_threads / 64)));
             int kws = kw > 0 ? kw : t.kwaves;
-            kws = std::max(1, std::min(kws, 16 / tt));
+            kws = std::max(1, std::min(kws, max_threads / 64 / twv));
             int s = sl > 0 ? sl : t.kslices;
             s = std::max(1, std::min(s, npairs));
             const int pps = (int)ceil_div(npairs, s);
             s = (int)ceil_div(npairs, pps);
             const int ppw = (int)ceil_div(pps, kws);
-            t.tt_per_wg = tt;
+            t.twaves = twv;
             t.kslices = s;
             t.pairs_per_wave = ppw;
             t.kwaves = (int)ceil_div(pps, ppw);
@@ -317,8 +322,9 @@ int run_gemm(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n,
     a.n = n;
     a.nb = nb;
     a.ttiles = (int)ceil_div(n, 32);
-    a.tt_per_wg = std::max(1, std::min(t.tt_per_wg, a.ttiles));
-    a.tgroups = (int)ceil_div(a.ttiles, a.tt_per_wg);
+    const int tpw = t.tpw > 0 ? t.tpw : 1;
+    a.twaves = std::max(1, t.twaves);
+    a.tgroups = (int)ceil_div(a.ttiles, (long long)a.twaves * tpw);
     a.kslices = std::max(1, t.kslices);
     a.pairs_per_slice = (int)ceil_div((nb + 1) / 2, a.kslices);
     a.pairs_per_wave = std::max(1, t.pairs_per_wave);
@@ -335,10 +341,12 @@ int run_gemm(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n,
     if (nwg > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "gemm: grid of %lld workgroups", nwg);
     a.nwg = (int)nwg;
     a.xcd_remap = (t.xcd_remap && nwg % 8 == 0) ? 1 : 0;
-    const int threads = 64 * a.tt_per_wg * kwaves;
-    if (threads > 1024) return fail(Q8_ERR_UNSUPPORTED, "gemm: %d threads per workgroup", threads);
-    const unsigned lds = (unsigned)((kwaves - 1) * a.tt_per_wg * 64 * 16 * sizeof(float));
-    return launch(c, t.smode ? F_GEMM_S1 : F_GEMM_S0, (unsigned)nwg, (unsigned)threads, lds, &a, sizeof a);
+    const int threads = 64 * a.twaves * kwaves;
+    const int max_threads = tpw == 1 ? 1024 : 512;
+    if (threads > max_threads) return fail(Q8_ERR_UNSUPPORTED, "gemm: %d threads per workgroup", threads);
+    const unsigned lds = (unsigned)((kwaves - 1) * a.twaves * tpw * 64 * 16 * sizeof(float));
+    const Fn f = !t.smode ? F_GEMM_S0_T1 : tpw == 4 ? F_GEMM_S1_T4 : tpw == 2 ? F_GEMM_S1_T2 : F_GEMM_S1_T1;
+    return launch(c, f, (unsigned)nwg, (unsigned)threads, lds, &a, sizeof a);
 }
 
 int prepare_into(q8_ctx *c, q8_dptr x, q8_dptr gate, q8_dptr up, int n, int k, q8_prepared *out) {
@@ -525,9 +533,9 @@ void *q8_stream(q8_ctx *c) { return c ? (void *)c->stream : nullptr; }
 
 int q8_set_option(q8_ctx *c, const char *name, int value) {
     if (!c || !name) return fail(Q8_ERR_INVALID, "q8_set_option: bad arguments");
-    static const char *const known[] = {"gemv.exact",  "gemv.waves",     "gemv.pairs",
-                                        "gemv.slices", "gemm.smode",     "gemm.tt_per_wg",
-                                        "gemm.xcd_remap", "gemm.kwaves", "gemm.slices"};
+    static const char *const known[] = {"gemv.exact", "gemv.waves",  "gemv.pairs",     "gemv.slices",
+                                        "gemm.smode", "gemm.tpw",    "gemm.twaves",    "gemm.xcd_remap",
+                                        "gemm.kwaves", "gemm.slices"};
     bool ok = false;
     for (const char *k : known) ok = ok || std::strcmp(k, name) == 0;
     if (!ok) return fail(Q8_ERR_INVALID, "unknown option %s", name);

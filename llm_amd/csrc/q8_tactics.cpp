@@ -63,27 +63,30 @@ void q8_gemv_shape(int out, int k, int cu_count, int slots, q8_tactic *t) {
     t->exact = 1;
 }
 
-// GEMM launch shape.  Waves own 32-token x 32-row output tiles, four token
-// tiles per workgroup.  When that leaves fewer than about two waves per SIMD,
-// the block pairs are also split over up to 16/TT waves of the workgroup,
-// reduced in LDS in a fixed order.
+// GEMM launch shape.  A wave owns TPW token tiles of one 32-row tile.  Two
+// tiles per wave share the weight stream and measured best for wide matrices
+// (n = 512: gate|up 11520 rows 51 us, QKV 6912 rows 37.5 us); one tile per
+// wave with the block pairs split over eight waves of a workgroup (reduced in
+// LDS in a fixed order) measured best for the 2304-row projections (O 18.6 us,
+// down 33 us) and for small n.  Four tiles per wave needs ~240 VGPRs (two
+// waves per SIMD) and measured slower everywhere; it stays an option.
 void q8_gemm_shape(int n, int out, int k, int cu_count, q8_tactic *t) {
     const int nb = k / 32;
     const int npairs = ceil_div(nb, 2);
     const int ttiles = ceil_div(n, 32);
     const int rtiles = ceil_div(out, 32);
-    const long long base = (long long)rtiles * ttiles;  // one wave per output tile
-    // about eight waves per SIMD: each wave's loop is bound by its own load and
-    // matrix-core latency, so more waves (K split) beat fewer, longer ones
-    // (n = 512 down, 2304 x 5760: 35 us at 8 K-waves vs 46 us at one)
-    const long long target = 32LL * std::max(cu_count, 1);
-    int f = (int)std::max<long long>(1, (target + base - 1) / base);
-    f = std::min(f, std::max(1, npairs / 3));
-    const int tt = f > 1 ? std::min(2, ttiles) : std::min(4, ttiles);
-    int kw = std::min(f, 16 / tt);
+    const int cus = std::max(cu_count, 1);
+    const int tpw = (rtiles >= 200 && ttiles >= 2) ? 2 : 1;
+    const int groups = ceil_div(ttiles, tpw);
+    const long long base = (long long)rtiles * groups;  // waves without a K split
+    const long long target = (tpw == 1 ? 36LL : 11LL) * cus;  // 9216 / 2816 waves on 256 CUs
+    int kw = (int)std::max<long long>(1, (target + base - 1) / base);
+    kw = std::min(kw, std::max(1, npairs / 3));
+    kw = std::min(kw, 8);
     const int ppw = ceil_div(npairs, kw);
     kw = ceil_div(npairs, ppw);
-    t->tt_per_wg = tt;
+    t->tpw = tpw;
+    t->twaves = 1;
     t->kwaves = kw;
     t->kslices = 1;
     t->pairs_per_wave = ppw;

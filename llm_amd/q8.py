@@ -71,7 +71,8 @@ class _GroupEntry(ctypes.Structure):
 class Tactic(ctypes.Structure):
     _fields_ = [("kernel", ctypes.c_int), ("waves_per_tile", ctypes.c_int),
                 ("pairs_per_wave", ctypes.c_int), ("pairs_per_batch", ctypes.c_int),
-                ("exact", ctypes.c_int), ("tt_per_wg", ctypes.c_int), ("smode", ctypes.c_int),
+                ("exact", ctypes.c_int), ("tpw", ctypes.c_int), ("twaves", ctypes.c_int),
+                ("smode", ctypes.c_int),
                 ("xcd_remap", ctypes.c_int), ("kslices", ctypes.c_int), ("kwaves", ctypes.c_int),
                 ("name", ctypes.c_char_p), ("evidence", ctypes.c_char_p)]
 

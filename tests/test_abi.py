@@ -47,7 +47,7 @@ def test_build_identity_names_its_artifact():
     assert info["arch"] == "gfx950"
     assert len(info["code_object_sha256"]) == 64
     assert len(info["kernel_source_sha256"]) == 64
-    for k in ("q8_repack", "q8_quantize", "q8_gemm_s1", "q8_gemv_pb5_e1", "q8_argmax", "q8_silu_mul"):
+    for k in ("q8_repack", "q8_quantize", "q8_gemm_s1_t4", "q8_gemv_pb5_e1", "q8_argmax", "q8_silu_mul"):
         assert k in info["kernels"]
     assert "-ffp-contract=off" in info["hipcc_flags"]
 
@@ -101,8 +101,8 @@ def test_plan_never_selects_a_rejected_tactic(n, out, k):
         assert t["waves_per_tile"] * t["pairs_per_wave"] >= pps
     else:
         assert t["kernel"] == q8.KERNEL_GEMM
-        assert 1 <= t["tt_per_wg"] <= 4
-        assert t["tt_per_wg"] * t["kwaves"] * 64 <= 1024
+        assert t["tpw"] in (1, 2, 4)
+        assert t["twaves"] * t["kwaves"] * 64 <= (1024 if t["tpw"] == 1 else 512)
         npairs = (k // 32 + 1) // 2
         pps = -(-npairs // t["kslices"])
         assert t["kwaves"] * t["pairs_per_wave"] >= pps

@@ -22,7 +22,7 @@ TOL_ABS = 2e-6
 TOL_REL = 1e-5
 SEED = 0x5EED
 J = [[0, 4, 1, 5], [2, 6, 3, 7]]
-OPTIONS = ("gemv.exact", "gemv.waves", "gemv.pairs", "gemv.slices", "gemm.smode", "gemm.tt_per_wg",
+OPTIONS = ("gemv.exact", "gemv.waves", "gemv.pairs", "gemv.slices", "gemm.smode", "gemm.tpw", "gemm.twaves",
            "gemm.xcd_remap", "gemm.kwaves", "gemm.slices")
 
 
@@ -371,12 +371,14 @@ def test_gemm_configs1(gpu, n):
     gpu.release(w)
 
 
-@pytest.mark.parametrize("smode,tpw,remap,kwaves,slices", [
-    (0, 1, 0, 1, 1), (0, 4, 1, 1, 1), (1, 2, 0, 1, 1), (1, 3, 1, 1, 1), (1, 1, 1, 8, 1), (1, 2, 0, 3, 1),
-    (1, 4, 1, 2, 4), (1, 1, 0, 1, 7), (0, 2, 1, 4, 3), (1, 1, 1, 6, 15), (1, 3, 0, 2, 2)])
-def test_gemm_variants_agree(gpu, smode, tpw, remap, kwaves, slices):
+@pytest.mark.parametrize("smode,tpw,twaves,remap,kwaves,slices", [
+    (0, 1, 1, 0, 1, 1), (0, 1, 4, 1, 1, 1), (1, 1, 2, 0, 1, 1), (1, 1, 3, 1, 1, 1), (1, 1, 1, 1, 8, 1),
+    (1, 2, 2, 0, 3, 1), (1, 2, 1, 1, 2, 4), (1, 4, 1, 0, 1, 7), (1, 4, 2, 1, 4, 1), (1, 4, 1, 1, 8, 3),
+    (0, 1, 2, 1, 4, 3), (1, 1, 1, 1, 6, 15), (1, 2, 3, 0, 2, 2), (1, 4, 2, 0, 1, 1)])
+def test_gemm_variants_agree(gpu, smode, tpw, twaves, remap, kwaves, slices):
     gpu.set_option("gemm.smode", smode)
-    gpu.set_option("gemm.tt_per_wg", tpw)
+    gpu.set_option("gemm.tpw", tpw)
+    gpu.set_option("gemm.twaves", twaves)
     gpu.set_option("gemm.xcd_remap", remap)
     gpu.set_option("gemm.kwaves", kwaves)
     gpu.set_option("gemm.slices", slices)
@@ -387,7 +389,7 @@ def test_gemm_variants_agree(gpu, smode, tpw, remap, kwaves, slices):
     ref = oracle.matmul(w.data, k, out, x, n)
     got = run_matmul(gpu, w, x, n)
     assert_parity(got, ref, exact_matmul(w.data, k, out, x, n),
-                  f"gemm smode={smode} tpw={tpw} remap={remap} kwaves={kwaves} slices={slices}")
+                  f"gemm smode={smode} tpw={tpw} twaves={twaves} remap={remap} kwaves={kwaves} slices={slices}")
     gpu.release(w)
 
 
