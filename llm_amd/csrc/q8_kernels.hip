@@ -165,6 +165,35 @@ static __device__ __forceinline__ float chain_sum(const float *v, int count) {
     return acc;
 }
 
+// Left-to-right sum of row[0..count) (16-byte aligned, zero from count up to
+// the next multiple of four), read as float4s eight at a time ahead of their
+// adds.  The zeros change nothing: the sum starts at +0.0, so it is never
+// -0.0, and x + (+0.0) == x for every other x.
+static __device__ __forceinline__ float chain_row(const float *row, int count) {
+    const f32x4 *r4 = (const f32x4 *)row;
+    const int nq = (count + 3) >> 2;
+    float acc = 0.0f;
+    int q0 = 0;
+    for (; q0 + 8 <= nq; q0 += 8) {
+        f32x4 t[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) t[u] = r4[q0 + u];
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc = (((acc + t[u].x) + t[u].y) + t[u].z) + t[u].w;
+    }
+    if (q0 < nq) {
+        f32x4 t[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) t[u] = r4[min(q0 + u, nq - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const float next = (((acc + t[u].x) + t[u].y) + t[u].z) + t[u].w;
+            acc = q0 + u < nq ? next : acc;
+        }
+    }
+    return acc;
+}
+
 template <int PB, int EXACT>
 static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
     extern __shared__ __attribute__((aligned(16))) float smem[];
@@ -204,14 +233,41 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
     const uint8_t *qbase = mem.quants + (size_t)tile * nb * Q8_UNIT_BYTES + lane * 16;
     const uint16_t *sbase = mem.scales + (size_t)tile * nb * Q8_TILE_ROWS + r;
 
+    const int vrow = Q8_GEMV_VROW(nb);
     float *xs = smem;               // nb * 32 floats, permuted
-    float *vbuf = smem + nb * 32;   // EXACT, one slice: [nslots][nb][32]; else [waves][32]
+    float *vbuf = smem + nb * 32;   // EXACT, one slice: [nslots][32][vrow]; else [waves][32]
     // Cross-workgroup scratch (S > 1): EXACT [slots][tiles][nb][32] block values,
     // else [slots][tiles][S][32] per-slice row sums.
     float *gbuf = a.scratch;
 
-    // Loads are unconditional at clamped, in-bounds addresses (no exec-mask
-    // branches, so nothing waits between them); validity is applied after.
+    // Exact mode: zero each row's tail up to a multiple of four blocks (read
+    // by the final sum as whole float4s).
+    if (EXACT && S == 1 && w == 0 && lane < 32) {
+        for (int b = nb; b < ((nb + 3) & ~3); b++) vbuf[(slot * 32 + r) * vrow + b] = 0.0f;
+    }
+
+    // Stores that have nothing to write go to this pad (after the exact-mode
+    // block values or the wave sums), so no store sits in an exec branch.
+    float *pad = vbuf + ((EXACT && S == 1) ? nslots * 32 * vrow : (blockDim.x >> 6) * 32);
+
+    // This wave's range of x, issued first as natural-order float4s (LLVM
+    // merges the four dword loads into one dwordx4, which gfx950 allows at
+    // 4-byte alignment), so waiting for x does not wait for the weight
+    // stream issued after it.
+    const int st_begin = 16 * p_begin;  // float4 index: eight per block
+    const int st_end = min(16 * p_end, nb * 8);
+    f32x4 xv[Q8_GEMV_STAGE];
+#pragma unroll
+    for (int u = 0; u < Q8_GEMV_STAGE; u++) {
+        const int i = min(st_begin + lane + 64 * u, nb * 8 - 1);
+        const float *xp = a.x + 4 * i;
+        xv[u] = (f32x4){xp[0], xp[1], xp[2], xp[3]};
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // Weight loads are unconditional at clamped, in-bounds addresses (no
+    // exec-mask branches, so nothing waits between them); validity is applied
+    // after.
     i32x4 qa[PB], qb[PB];
     unsigned dd[PB];
 #define Q8_GEMV_LOAD_BATCH(P0)                                                        \
@@ -224,36 +280,33 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
         qb[i] = *(const i32x4 *)(qbase + (size_t)b1 * Q8_UNIT_BYTES);                 \
         dd[i] = (unsigned)sbase[(size_t)bs * Q8_TILE_ROWS];                           \
     }
-    if (p_begin < p_end) { Q8_GEMV_LOAD_BATCH(p_begin) }
+    Q8_GEMV_LOAD_BATCH(p_begin)
+    __builtin_amdgcn_sched_barrier(0);
 
-    // Stage this wave's blocks of x into LDS, permuted: float4 slot i holds
-    // x[b*32 + 8c + J[hh][t]] for c = 0..3 (b = i/8, hh = (i/4)%2, t = i%4).
-    // Every gather is issued before the first store; waves stage disjoint
+    // Stage x into LDS, permuted: float4 slot s = 8b + 4hh + t holds
+    // x[32b + 8c + J[hh][t]] in component c.  Natural float4 i holds elements
+    // 8c + j0 .. 8c + j0 + 3 of block i/8 (c = (i%8)/2, j0 = 4(i%2)); element
+    // j0 + e lands in half e/2, dword (i%2) + 2(e%2).  Waves stage disjoint
     // block ranges (in silu mode the gate and up waves write identical values
     // to the same range), so only a wave-level fence is needed.
-    {
-        const int st_begin = 16 * p_begin;
-        const int st_end = min(16 * p_end, nb * 8);
-        f32x4 v[Q8_GEMV_STAGE];
 #pragma unroll
-        for (int u = 0; u < Q8_GEMV_STAGE; u++) {
-            const int i = min(st_begin + lane + 64 * u, nb * 8 - 1);
-            const float *xb = a.x + (i >> 3) * 32 + perm_lane((i >> 2) & 1, i & 3);
-            v[u] = (f32x4){xb[0], xb[8], xb[16], xb[24]};
-        }
-#pragma unroll
-        for (int u = 0; u < Q8_GEMV_STAGE; u++) {
-            const int i = st_begin + lane + 64 * u;
-            if (i < st_end) ((f32x4 *)xs)[i] = v[u];
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int u = 0; u < Q8_GEMV_STAGE; u++) {
+        const int i = st_begin + lane + 64 * u;
+        float *d = i < st_end ? xs + (i >> 3) * 32 + ((i & 7) >> 1) + 4 * (i & 1) : pad;
+        d[0] = xv[u].x;
+        d[8] = xv[u].y;
+        d[16] = xv[u].z;
+        d[24] = xv[u].w;
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
+    // One batch of PB pairs.  The first batch runs as straight-line code
+    // outside any loop, so each pair waits only for its own loads (a loop
+    // back-edge would make the compiler wait for the whole batch first).
     float total = 0.0f;
-    for (int p0 = p_begin; p0 < p_end; p0 += PB) {
-        if (p0 != p_begin) { Q8_GEMV_LOAD_BATCH(p0) }
+    auto process = [&](int p0) {
 #pragma unroll
         for (int i = 0; i < PB; i++) {
             const int p = min(p0 + i, p_last);
@@ -273,16 +326,20 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
             const int blk = b0 + h;
             const bool ok = pair_ok && blk < nb;
             if (EXACT) {
-                if (ok) {
-                    if (S == 1)
-                        vbuf[(slot * nb + blk) * 32 + r] = v;
-                    else
-                        gbuf[((size_t)(slot * a.total_tiles + gtile) * nb + blk) * 32 + r] = v;
+                if (S == 1) {
+                    *(ok ? vbuf + (slot * 32 + r) * vrow + blk : pad) = v;
+                } else if (ok) {
+                    gbuf[((size_t)(slot * a.total_tiles + gtile) * nb + blk) * 32 + r] = v;
                 }
             } else {
                 total = ok ? total + v : total;
             }
         }
+    };
+    process(p_begin);
+    for (int p0 = p_begin + PB; p0 < p_end; p0 += PB) {
+        Q8_GEMV_LOAD_BATCH(p0)
+        process(p0);
     }
 #undef Q8_GEMV_LOAD_BATCH
 
@@ -324,7 +381,7 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
             float acc;
             if (S == 1) {
                 if (EXACT) {
-                    acc = chain_sum(vbuf + (size_t)sl * nb * 32 + r, nb);
+                    acc = chain_row(vbuf + (size_t)(sl * 32 + r) * vrow, nb);
                 } else {
                     acc = 0.0f;
                     for (int ww = 0; ww < W; ww++) acc = acc + vbuf[(sl * W + ww) * 32 + r];

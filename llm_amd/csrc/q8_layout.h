@@ -52,6 +52,13 @@ static inline int q8_perm_element(int h, int p) {
     return 8 * (p & 3) + J[h][p >> 2];
 }
 
+/* GEMV exact mode parks each row's block values in LDS row-major, rows
+ * Q8_GEMV_VROW(nb) floats apart: a multiple of four (16-byte reads) plus four,
+ * so eight consecutive rows start in distinct bank groups. */
+#define Q8_GEMV_VROW(nb) ((((nb) + 3) & ~3) + 4)
+/* LDS floats after the GEMV's staging areas that absorb stores with nothing to write. */
+#define Q8_GEMV_PAD_FLOATS 32
+
 /* ---- kernel argument blocks (passed by value as the only kernel argument) ---- */
 
 typedef struct {

@@ -295,7 +295,8 @@ int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const floa
     const long long grid = (long long)a.total_tiles * t.kslices;
     if (grid > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "gemv: grid of %lld workgroups", grid);
     const unsigned lds =
-        (unsigned)(nb * 32 * 4 + ((t.exact && t.kslices == 1) ? slots * nb * 32 * 4 : waves * 32 * 4));
+        (unsigned)(nb * 32 * 4 + ((t.exact && t.kslices == 1) ? slots * 32 * Q8_GEMV_VROW(nb) * 4 : waves * 32 * 4) +
+                   Q8_GEMV_PAD_FLOATS * 4);
     return launch(c, gemv_fn(pb, t.exact), (unsigned)grid, (unsigned)(waves * 64), lds, &a, sizeof a);
 }
 

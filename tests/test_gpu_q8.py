@@ -260,6 +260,27 @@ def test_gemv_residual_epilogue_is_matmul_add(gpu):
     gpu.release(w)
 
 
+@pytest.mark.parametrize("x_off", [1, 2, 3, 4])
+def test_gemv_x_offsets_of_any_alignment(gpu, x_off):
+    """Offsets are in f32 elements (compute.rs:421-431); x at a 4-, 8- or
+    12-byte offset takes the kernel's dword path, 16 bytes its dwordx4 path."""
+    r = rng(16 + x_off)
+    out, k = 96, 2304
+    w = weight(r, out, k)
+    x = r.standard_normal(k, dtype=np.float32)
+    xb, yb = gpu.alloc(4 * (k + x_off)), gpu.alloc(4 * out)
+    xb.upload(np.concatenate([np.full(x_off, np.nan, np.float32), x]))
+    gpu.matmul(w, xb, x_off, 1, yb, 0)
+    got = yb.download(np.float32, out)
+    ref = oracle.matmul(w.data, k, out, x, 1).reshape(-1)
+    assert_close(got, ref, f"gemv x_off={x_off}")
+    if oracle.simd_path() == "avx2+fma":
+        assert_bits(got, ref, f"gemv x_off={x_off}")
+    xb.free()
+    yb.free()
+    gpu.release(w)
+
+
 def test_decode_group_matches_separate_matmuls(gpu):
     """cuda/mod.rs:1482-1543: QKV-like group sharing x in one launch."""
     r = rng(15)
