@@ -113,6 +113,51 @@ def bench_gemv_rotating(gpu, m, k, steps, warmup, rng, label):
             "total_ms": ms_total}
 
 
+def bench_gemv_hot(gpu, m, k, rng, steps=2000):
+    """The same GEMV on one weight copy (14 MB, resident in the 256 MB
+    Infinity Cache after the first launch): the MALL-hot figure."""
+    w = make_weight(rng, m, k)
+    gpu.resident(w)
+    xb, yb = gpu.alloc(4 * k), gpu.alloc(4 * m)
+    xb.upload(rng.standard_normal(k, dtype=np.float32))
+
+    def rec():
+        for _ in range(steps):
+            gpu.matmul(w, xb, 0, 1, yb, 0)
+    ms = timed_graph(gpu, rec, 1, 1) / steps
+    gbs = gemv_bytes(m, k) / (ms * 1e-3) / 1e9
+    log(f"configs[0] GEMV MALL-hot: {ms * 1e3:.2f} us/step, {gbs:.0f} GB/s")
+    gpu.release(w)
+    xb.free()
+    yb.free()
+    return round(gbs, 1)
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "q8_gemv_configs0_traffic.md")
+
+
+def traffic_from_profile():
+    """HBM bytes per configs[0] GEMV launch from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary, if it was measured on the code object
+    loaded now (its sha256 is recorded in the summary); otherwise None."""
+    from llm_amd import q8
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None
+    fields = {}
+    for line in text.splitlines():
+        if line.startswith("- ") and ": " in line:
+            key, val = line[2:].split(": ", 1)
+            fields[key.strip("` ")] = val.strip("` ")
+    if fields.get("code_object_sha256") != json.loads(q8.build_info())["code_object_sha256"]:
+        return None
+    try:
+        return int(fields["traffic_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
+
+
 def bench_gemm_rotating(gpu, m, k, n, reps, rng, label):
     """n tokens over rotating weight copies, quantization included."""
     import oracle
@@ -140,6 +185,18 @@ def bench_gemm_rotating(gpu, m, k, n, reps, rng, label):
     xb.free()
     yb.free()
     return {"us": ms * 1e3, "gbs": gbs, "tops": tops, "bytes": per}
+
+
+def own_prepared(gpu, prep, n, k):
+    """Copy a prepared operand (quants then f32 scales, lane-order units of
+    32 tokens) into a buffer we own; returns (Prepared, buffer)."""
+    from llm_amd import q8
+    units = (n + 31) // 32 * (k // 32)
+    qbytes, sbytes = units * 1024, units * 32 * 4
+    buf = gpu.alloc(qbytes + sbytes)
+    q8._check(q8.lib().q8_copy_device(gpu.handle, buf.ptr, prep.quants, qbytes))
+    q8._check(q8.lib().q8_copy_device(gpu.handle, buf.ptr + qbytes, prep.scales, sbytes))
+    return q8.Prepared(buf.ptr, buf.ptr + qbytes, n, k), buf
 
 
 def bench_layer_n512(gpu, reps, rng, n=512):
@@ -178,12 +235,39 @@ def bench_layer_n512(gpu, reps, rng, n=512):
     total_ops = sum(ops.values())
     tops = total_ops / (ms * 1e-3) / 1e12
     log(f"n={n} layer set: {ms * 1e3:.1f} us, {tops:.1f} TOPS ({tops / INT8_PEAK_TOPS * 100:.1f}% of int8 peak)")
+
+    # the same work piece by piece (each its own graph): quantization alone and
+    # each projection on already-prepared activations
+    gu = gpu.alloc(4 * n * 2 * ffn)
+    # A Prepared points into the library's one activation workspace (valid
+    # until the next prepare, as the reference's); keep copies in buffers of
+    # our own so both operands stay valid side by side.
+    p, pbuf = own_prepared(gpu, gpu.prepare(xb, 0, n, hid), n, hid)
+    pf, pfbuf = own_prepared(gpu, gpu.prepare(act, 0, n, ffn), n, ffn)
+    pieces = {
+        "quantize_x": lambda: gpu.prepare(xb, 0, n, hid),
+        "quantize_act": lambda: gpu.prepare(act, 0, n, ffn),
+        "qkv": lambda: gpu.matmul_prompt_group([(wq, qkv, 0), (wk, qkv, n * hid), (wv, qkv, 2 * n * hid)],
+                                               p, n, hid),
+        "o": lambda: gpu.matmul(wo, qkv, 0, n, hb, 0, prepared=p),
+        "gate_up": lambda: gpu.matmul_prompt_group([(wg, gu, 0), (wu, gu, n * ffn)], p, n, hid),
+        "gate_up_silu": lambda: gpu.gate_up_silu(wg, wu, hb, 0, n, act, 0, want_prepared=True),
+        "down": lambda: gpu.matmul(wd, act, 0, n, hb, 0, prepared=pf),
+    }
+    piece_us = {}
+    per_graph = 10  # one graph launch costs more than a kernel: record each piece 10 times per graph
+
+    def repeat(fn):
+        return lambda: [fn() for _ in range(per_graph)]
+    for name, fn in pieces.items():
+        piece_us[name] = round(timed_graph(gpu, repeat(fn), reps, 3) / per_graph * 1e3, 2)
+    log("n=512 pieces (us): " + ", ".join(f"{k} {v}" for k, v in piece_us.items()))
     for w in (wq, wk, wv, wo, wg, wu, wd):
         gpu.release(w)
-    for b in (xb, qkv, hb, act):
+    for b in (xb, qkv, hb, act, gu, pbuf, pfbuf):
         b.free()
     return {"us": ms * 1e3, "tops": tops, "ops": total_ops, "frac": tops / INT8_PEAK_TOPS,
-            "ops_by_projection": ops}
+            "ops_by_projection": ops, "quantize_us": piece_us["quantize_x"], "projections_us": piece_us}
 
 
 def bench_decode_layer(gpu, reps, rng):
@@ -279,9 +363,14 @@ def main():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--skip-extras", action="store_true")
-    ap.add_argument("--skip-gemm", action="store_true")
+    ap.add_argument("--sections", default="all",
+                    help="comma list of gemv,gemm,extras,cpu (default all); a profiler run names one so "
+                         "each kernel's average covers one workload")
     args = ap.parse_args()
+    sections = {"gemv", "gemm", "extras", "cpu"} if args.sections == "all" else set(args.sections.split(","))
+    unknown = sections - {"gemv", "gemm", "extras", "cpu"}
+    if unknown:
+        ap.error(f"unknown sections {sorted(unknown)}")
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus "
               f"{args.gpus}); the sharding design is described in DESIGN.md", file=sys.stderr)
@@ -293,27 +382,32 @@ def main():
     log(f"device {gpu.name}")
     calibration_copy(gpu)
     m, k = 5760, 2304
-    gemv = bench_gemv_rotating(gpu, m, k, args.steps, args.warmup, rng, "configs[0] GEMV")
-    gemm = bench_layer_n512(gpu, 20, rng) if not args.skip_gemm else {"tops": 0.0, "frac": 0.0, "us": 0.0, "ops": 0}
+    gemv = {"gbs": None, "us_per_step": None, "bytes_per_step": gemv_bytes(m, k), "copies": None}
+    if "gemv" in sections:
+        gemv = bench_gemv_rotating(gpu, m, k, args.steps, args.warmup, rng, "configs[0] GEMV")
+    gemm = {"tops": None, "frac": None, "us": None, "ops": None}
+    if "gemm" in sections:
+        gemm = bench_layer_n512(gpu, 20, rng)
     extras = {}
-    if not args.skip_extras:
+    if "extras" in sections:
+        gemv["mall_hot"] = bench_gemv_hot(gpu, m, k, rng)
         extras["configs1_n8"] = bench_gemm_rotating(gpu, m, k, 8, 5, rng, "configs[1] n=8")
         extras["configs1_n64"] = bench_gemm_rotating(gpu, m, k, 64, 5, rng, "configs[1] n=64")
         layer, head = bench_decode_layer(gpu, 50, rng)
         extras["configs2_decode_layer"] = layer
         extras["configs2_lm_head"] = head
-    cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
+    cpu = cpu_baseline(args.cpu_seconds) if "cpu" in sections and args.cpu_seconds > 0 else None
     gpu.close()
 
     value = gemv["gbs"]
     line = {
         "metric": METRIC,
-        "value": round(value, 1),
+        "value": round(value, 1) if value is not None else None,
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": gemv["us_per_step"] / 1e3,
+        "ms_per_step": gemv["us_per_step"] / 1e3 if gemv["us_per_step"] is not None else None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -322,12 +416,19 @@ def main():
         "config": {"workload": "configs[0] Q8_0 GEMV n=1, W 5760x2304, MALL-cold (rotating copies); "
                                "plus configs[3] n=512 layer projections",
                    "M": m, "K": k, "n": 1, "rotating_copies": gemv["copies"]},
-        "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "q8_gemv (configs[0])", "bytes_per_launch": gemv["bytes_per_step"]},
-        "gemm_n512": {"value": round(gemm["tops"], 2), "unit": "TOPS", "peak": INT8_PEAK_TOPS,
-                      "frac": round(gemm["frac"], 4), "us_per_layer": round(gemm["us"], 2),
-                      "ops_per_layer": gemm["ops"]},
+        "roofline": {"bound": "hbm", "achieved": round(value, 1) if value is not None else None,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBS, 4) if value is not None else None,
+                     "traffic": traffic_from_profile(),
+                     "kernel": "q8_gemv (configs[0])", "bytes_per_launch": gemv["bytes_per_step"],
+                     "mall_hot_gbs": gemv.get("mall_hot")},
+        "gemm_n512": {"value": round(gemm["tops"], 2) if gemm["tops"] is not None else None, "unit": "TOPS",
+                      "peak": INT8_PEAK_TOPS,
+                      "frac": round(gemm["frac"], 4) if gemm["frac"] is not None else None,
+                      "us_per_layer": round(gemm["us"], 2) if gemm["us"] is not None else None,
+                      "ops_per_layer": gemm["ops"],
+                      "quantize_us": gemm.get("quantize_us"),
+                      "projections_us": gemm.get("projections_us")},
         "extras": extras,
         "cpu_baseline": cpu,
     }

@@ -461,7 +461,10 @@ int q8_open(int device, q8_ctx **out) {
     c->cu_count = prop.multiProcessorCount;
     c->total_mem = prop.totalGlobalMem;
     c->max_lds = prop.sharedMemPerBlock;
-    std::snprintf(c->name, sizeof c->name, "%s (%s)", prop.name, prop.gcnArchName);
+    char market[256] = {0};
+    if (hipDeviceGetName(market, sizeof market - 1, device) != hipSuccess || market[0] == 0)
+        std::snprintf(market, sizeof market, "%s", prop.name[0] ? prop.name : "AMD Instinct");
+    std::snprintf(c->name, sizeof c->name, "%s (%s, %d CUs)", market, prop.gcnArchName, c->cu_count);
     int rc = Q8_OK;
     do {
         hipError_t he = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
