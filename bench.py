@@ -188,15 +188,14 @@ def bench_gemm_rotating(gpu, m, k, n, reps, rng, label):
 
 
 def own_prepared(gpu, prep, n, k):
-    """Copy a prepared operand (quants then f32 scales, lane-order units of
-    32 tokens) into a buffer we own; returns (Prepared, buffer)."""
+    """Copy a prepared operand (quants in either format, then f32 scales) into
+    a buffer we own; returns (Prepared, buffer)."""
     from llm_amd import q8
-    units = (n + 31) // 32 * (k // 32)
-    qbytes, sbytes = units * 1024, units * 32 * 4
+    qbytes, sbytes = prep.quant_bytes(), prep.scale_bytes()
     buf = gpu.alloc(qbytes + sbytes)
     q8._check(q8.lib().q8_copy_device(gpu.handle, buf.ptr, prep.quants, qbytes))
     q8._check(q8.lib().q8_copy_device(gpu.handle, buf.ptr + qbytes, prep.scales, sbytes))
-    return q8.Prepared(buf.ptr, buf.ptr + qbytes, n, k), buf
+    return q8.Prepared(buf.ptr, buf.ptr + qbytes, n, k, prep.format), buf
 
 
 def bench_layer_n512(gpu, reps, rng, n=512):

@@ -67,12 +67,17 @@ typedef struct q8_weight q8_weight;
 
 /* Activations already quantized on the device: the reference's `Prepared`
  * (cuda/mod.rs:119), a non-owning view into the context's activation
- * workspace, valid until a later prepare needs a larger workspace. */
+ * workspace, valid until a later prepare needs a larger workspace.  `format`
+ * says how the quants are stored: Q8_PREPARED_I8 as int8 units (1 KB per
+ * 32 tokens x 32 elements), Q8_PREPARED_F16 as the same integers in f16 units
+ * (2 KB), read by the f16-MFMA GEMM; q8_prepare picks it from n. */
+enum { Q8_PREPARED_I8 = 0, Q8_PREPARED_F16 = 1 };
 typedef struct {
     q8_dptr quants;
     q8_dptr scales;
     int n;
     int k;
+    int format;
 } q8_prepared;
 
 /* One member of a grouped launch: `GroupEntry` (cuda/mod.rs:314-320). */
@@ -83,7 +88,7 @@ typedef struct {
 } q8_group_entry;
 
 /* Kernel variants a tactic can name. */
-enum { Q8_KERNEL_GEMV = 1, Q8_KERNEL_GEMM = 2 };
+enum { Q8_KERNEL_GEMV = 1, Q8_KERNEL_GEMM = 2, Q8_KERNEL_GEMM_F16 = 3 };
 
 /* The shape-keyed tactic chosen for one (n, out, k): the matmul counterpart
  * of `Tactic`/`Choice` (apps/engine/src/tactics.rs:229-347). */
@@ -99,6 +104,7 @@ typedef struct {
     int xcd_remap;       /* GEMM: keep a row tile's workgroups on one XCD */
     int kslices;         /* workgroups splitting one output tile's blocks (1 = none) */
     int kwaves;          /* GEMM: waves splitting the blocks inside a workgroup */
+    int rwaves;          /* f16 GEMM: row-tile waves per workgroup sharing staged activations */
     const char *name;    /* tactic name, e.g. "matmul.gemv_f32" */
     const char *evidence;
 } q8_tactic;
@@ -127,7 +133,9 @@ void *q8_stream(q8_ctx *ctx);
 /* Tuning/testing switches; value -1 restores the tactic table's choice.
  * Names: "gemv.exact", "gemv.waves", "gemv.pairs", "gemv.slices",
  * "gemm.smode", "gemm.tpw", "gemm.twaves", "gemm.xcd_remap", "gemm.kwaves",
- * "gemm.slices". */
+ * "gemm.slices", "gemm.rwaves", "gemm.f16" (0: int8 prepared activations and
+ * the int8-MFMA GEMM for every n; 1: f16 and the f16-MFMA GEMM for every
+ * n >= 2). */
 int q8_set_option(q8_ctx *ctx, const char *name, int value);
 
 /* ---- device memory: Gpu::alloc / upload / download (cuda/mod.rs:530-567) ---- */

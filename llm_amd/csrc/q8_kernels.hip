@@ -38,6 +38,22 @@ static __device__ __forceinline__ float f16_to_f32(unsigned h) {
     return (float)__builtin_bit_cast(_Float16, (unsigned short)h);
 }
 
+// Eight int8 (two dwords, byte order kept) -> eight f16 (four dwords), exact:
+// bytes biased to q + 128, placed under the f16 exponent of 1024 (0x64xx is
+// 1024 + byte), then one packed f16 subtraction of 1152 per two values.
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+static __device__ __forceinline__ unsigned f16_pair(unsigned biased, unsigned sel) {
+    const unsigned bits = __builtin_amdgcn_perm(0x64646464u, biased, sel);
+    const f16x2 v = __builtin_bit_cast(f16x2, bits) - (f16x2){(_Float16)1152.0f, (_Float16)1152.0f};
+    return __builtin_bit_cast(unsigned, v);
+}
+static __device__ __forceinline__ i32x4 i8x4_to_f16x4(int d0, int d1) {
+    const unsigned u0 = (unsigned)d0 ^ 0x80808080u, u1 = (unsigned)d1 ^ 0x80808080u;
+    return (i32x4){(int)f16_pair(u0, 0x04010400u), (int)f16_pair(u0, 0x04030402u),
+                   (int)f16_pair(u1, 0x04010400u), (int)f16_pair(u1, 0x04030402u)};
+}
+
 // Rust `f32 as i8`: saturating, NaN -> 0.
 static __device__ __forceinline__ int sat_i8(float v) {
     if (v != v) return 0;
@@ -490,7 +506,14 @@ extern "C" __global__ __launch_bounds__(256) void q8_quantize(Q8QuantArgs a) {
         packed[q] = (int)w;
     }
     const size_t u = (size_t)tt * nb + b;
-    *(i32x4 *)(a.xq + u * Q8_UNIT_BYTES + lane * 16) = packed;
+    if (a.f16) {
+        // the same values as f16, bytes 0-7 to the unit's first half, 8-15 to its second
+        uint8_t *dst = a.xq + u * Q8_UNIT_F16_BYTES + lane * 16;
+        *(i32x4 *)dst = i8x4_to_f16x4(packed[0], packed[1]);
+        *(i32x4 *)(dst + 1024) = i8x4_to_f16x4(packed[2], packed[3]);
+    } else {
+        *(i32x4 *)(a.xq + u * Q8_UNIT_BYTES + lane * 16) = packed;
+    }
     if (h == 0) a.xs[u * Q8_TILE_TOKENS + tl] = scale;
 }
 
@@ -763,6 +786,252 @@ static __device__ __forceinline__ void gemm_body(const Q8GemmArgs &a) {
         }
     }
 }
+
+// ---------------------------------------------------------------------------
+// GEMM on the f16 MFMA, n >= 2, same arithmetic as above.
+//
+// Q8_0 quants are integers |q| <= 127, exact in f16; two
+// v_mfma_f32_32x32x16_f16 over a block's 32 elements give the int32 block dot
+// exactly (every partial sum is an integer below 2^24), already as f32.  The
+// 16 v_cvt_f32_i32 per output tile and block of the int8 path disappear; the
+// scale products and the fma epilogue are unchanged, so the results are the
+// int8 kernel's bit for bit.  Per 32 x 32 tile and block: 96 MFMA cycles (two
+// f16 dots, half a scale-product MFMA) against 16 fma + the weight conversion
+// on the VALU, instead of 128 VALU cycles.
+//
+// A workgroup is RW row-tile waves x KW K-split waves; all waves cover the
+// same TPW token tiles.  Per block pair the RW waves of a K group bring the
+// activations (f16 units and scales) into LDS once, and each wave its own two
+// weight units and their scales, all with global_load_lds (LDS written
+// without passing through registers), into a ring of Q8_GEMM_H_STAGES
+// buffers: the loads for pair i + STAGES - 1 are issued while pair i is
+// computed.  Every wave converts only its own weight units to f16 (once for
+// its TPW token tiles).  The K groups are reduced in LDS in a fixed order, as
+// in the int8 kernel.
+//
+// Synchronisation is explicit: the loop issues no vector-memory load other
+// than these, the same number per wave per pair, so "this wave's loads of pair
+// i + 1 have landed" is s_waitcnt vmcnt(N) with a constant N, followed by
+// s_barrier.  (The compiler's __syncthreads, and its waits for register loads,
+// would wait for every load in flight, prefetches included.)  All waves run
+// the same number of iterations; pairs past a wave's range use a zero weight
+// scale and add nothing (their loads are clamped to valid addresses).
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// s_waitcnt with vmcnt = n (0..63) and the other counters left free (gfx9 encoding)
+#define Q8_VMCNT_IMM(n) ((((n)&15) | (7 << 4) | (15 << 8) | ((((n) >> 4) & 3) << 14)))
+
+template <int TPW, int RW>
+static __device__ __forceinline__ void gemm_h_body(const Q8GemmArgs &a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t hsm[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int KW = (blockDim.x >> 6) / RW;
+    const int rw = wave % RW;
+    const int kw = wave / RW;
+    int wg = blockIdx.x;
+    if (a.xcd_remap) {
+        const int per = a.nwg >> 3;
+        wg = (wg & 7) * per + (wg >> 3);
+    }
+    const int rg = wg / a.tgroups;
+    const int tg = wg - rg * a.tgroups;
+    const int rt = rg * RW + rw;                       // global row tile (may be past the end)
+    const bool row_live = rt < a.total_rtiles;
+    const int rtc = min(rt, a.total_rtiles - 1);
+    const int tt0 = tg * TPW;
+    int mi = 0;
+#pragma unroll
+    for (int i = 1; i < Q8_GROUP_MAX; i++)
+        if (i < a.members && rtc >= a.m[i].tile_begin) mi = i;
+    const Q8GemmMember mem = a.m[mi];
+    const int g = rtc - mem.tile_begin;
+    const int nb = a.nb;
+    const int h = lane >> 5;
+    const int r = lane & 31;
+    const uint8_t *wq = mem.quants + (size_t)g * nb * Q8_UNIT_BYTES + lane * 16;
+    const uint16_t *wsc = mem.scales + (size_t)g * nb * Q8_TILE_ROWS;
+
+    const int npairs = (nb + 1) >> 1;
+    const int ppw = a.pairs_per_wave;
+    const int p_begin = kw * ppw;
+    const int p_end = min(npairs, p_begin + ppw);
+
+    // LDS per K group: STAGES buffers of [TPW][2 blocks][2048 B f16 unit],
+    // SCALE_SLOTS f32 scale slots ([TPW][2][32] used; RW > TPW waves fill the
+    // rest), then per wave its two weight units and 64 f16 weight scales.
+    constexpr int GLANES = RW * 64;
+    constexpr int ACT_BYTES = TPW * 2 * Q8_UNIT_F16_BYTES;
+    constexpr int SCALE_SLOTS = (TPW * 64 > GLANES ? TPW * 64 : GLANES);
+    constexpr int W_OFF = ACT_BYTES + SCALE_SLOTS * 4;
+    constexpr int W_BYTES = 2 * Q8_UNIT_BYTES + 256;
+    constexpr int BUF_BYTES = W_OFF + RW * W_BYTES;
+    static_assert(BUF_BYTES == Q8_GEMM_H_BUF_BYTES(TPW, RW), "host and kernel LDS layouts agree");
+    constexpr int MAXC = TPW * 256 / GLANES;             // 16-byte chunks per lane per pair
+    constexpr int MAXS = (TPW * 64 + GLANES - 1) / GLANES;  // scales per lane per pair
+    static_assert(TPW * 256 % GLANES == 0, "whole chunks per lane");
+    constexpr int SG = MAXC + MAXS + 3;                  // loads per lane per pair (+ w0, w1, d_w)
+    // at the end of iteration i: loads issued after pair i+1's
+    constexpr int AFTER = (Q8_GEMM_H_STAGES - 2) * SG;
+    uint8_t *kbase = hsm + (size_t)kw * Q8_GEMM_H_STAGES * BUF_BYTES;
+    const int wig = wave - kw * RW;  // this wave within its K group
+    const int wbase = wig * 64;
+
+    // stage pair p into ring buffer `buf`: every lane issues exactly SG loads
+    auto stage = [&](int p, int buf) {
+        const int pc = min(p, npairs - 1);
+        uint8_t *base = kbase + buf * BUF_BYTES;
+        {
+            // this wave's weight units (lane L's 16 bytes at 16L) and the pair's 64 f16
+            // scales as dwords: lane L < 32 brings scales 2L, 2L+1 (block b0 + L/16, rows
+            // 2(L%16), +1), lanes >= 32 repeat lanes L-32 into the upper, unread half
+            const int b0 = 2 * pc;
+            const int b1 = min(b0 + 1, nb - 1);
+            const int i = lane & 31;
+            const int bs = min(b0 + (i >> 4), nb - 1);
+            uint8_t *wl = base + W_OFF + wig * W_BYTES;
+            __builtin_amdgcn_global_load_lds(wq + (size_t)b0 * Q8_UNIT_BYTES, (lds_void_t *)wl, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(wq + (size_t)b1 * Q8_UNIT_BYTES, (lds_void_t *)(wl + Q8_UNIT_BYTES), 16,
+                                             0, 0);
+            __builtin_amdgcn_global_load_lds(wsc + (size_t)bs * Q8_TILE_ROWS + 2 * (i & 15),
+                                             (lds_void_t *)(wl + 2 * Q8_UNIT_BYTES), 4, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < MAXC; i++) {
+            const int c = wbase + i * GLANES + lane;
+            const int j = c >> 8, bb = (c >> 7) & 1;
+            const int tt = min(tt0 + j, a.ttiles - 1);
+            const int b = min(2 * pc + bb, nb - 1);
+            __builtin_amdgcn_global_load_lds(a.xq + ((size_t)tt * nb + b) * Q8_UNIT_F16_BYTES + (c & 127) * 16,
+                                             (lds_void_t *)(base + (wbase + i * GLANES) * 16), 16, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < MAXS; i++) {
+            const int s = min(wbase + i * GLANES + lane, SCALE_SLOTS - 1);
+            const int j = min(s >> 6, TPW - 1), bb = (s >> 5) & 1;
+            const int tt = min(tt0 + j, a.ttiles - 1);
+            const int b = min(2 * pc + bb, nb - 1);
+            __builtin_amdgcn_global_load_lds(a.xs + ((size_t)tt * nb + b) * Q8_TILE_TOKENS + (s & 31),
+                                             (lds_void_t *)(base + ACT_BYTES + (wbase + i * GLANES) * 4), 4, 0, 0);
+        }
+    };
+
+    f32x16 acc[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; t++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[t][i] = 0.0f;
+    const f32x16 fz16 = {};
+    const f32x32 fz32 = {};
+
+    // prologue: pairs 0 .. STAGES-2 staged; wait for pair 0
+#pragma unroll
+    for (int s = 0; s < Q8_GEMM_H_STAGES - 1; s++) stage(p_begin + s, s);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(Q8_VMCNT_IMM((Q8_GEMM_H_STAGES - 2) * SG));
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+
+    for (int it = 0; it < ppw; it++) {
+        const int cur = it % Q8_GEMM_H_STAGES;
+        // ring slot of pair it+STAGES-1 was last read in iteration it-1 (barrier since)
+        stage(p_begin + it + Q8_GEMM_H_STAGES - 1, (it + Q8_GEMM_H_STAGES - 1) % Q8_GEMM_H_STAGES);
+        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t *base = kbase + cur * BUF_BYTES;
+        // this pair's weights to f16 (lane L: bytes 0-7 for the first MFMA, 8-15 for the second)
+        const uint8_t *wl = base + W_OFF + wig * W_BYTES;
+        const i32x4 w0 = *(const i32x4 *)(wl + lane * 16);
+        const i32x4 w1 = *(const i32x4 *)(wl + Q8_UNIT_BYTES + lane * 16);
+        const unsigned dwb = *(const uint16_t *)(wl + 2 * Q8_UNIT_BYTES + lane * 2);
+        const int p = p_begin + it;
+        const bool dwv = p < p_end && 2 * p + h < nb;
+        const i32x4 wa0 = i8x4_to_f16x4(w0.x, w0.y), wa1 = i8x4_to_f16x4(w0.z, w0.w);
+        const i32x4 wb0 = i8x4_to_f16x4(w1.x, w1.y), wb1 = i8x4_to_f16x4(w1.z, w1.w);
+        const float dwf = dwv ? f16_to_f32(dwb) : 0.0f;
+#pragma unroll
+        for (int t = 0; t < TPW; t++) {
+            const uint8_t *u0 = base + (t * 2) * Q8_UNIT_F16_BYTES + lane * 16;
+            const uint8_t *u1 = u0 + Q8_UNIT_F16_BYTES;
+            const i32x4 x00 = *(const i32x4 *)u0, x01 = *(const i32x4 *)(u0 + 1024);
+            const i32x4 x10 = *(const i32x4 *)u1, x11 = *(const i32x4 *)(u1 + 1024);
+            const float sx = ((const float *)(base + ACT_BYTES))[t * 64 + lane];
+            const f32x32 sc = __builtin_amdgcn_mfma_f32_32x32x1f32(sx, dwf, fz32, 0, 0, 0);
+            f32x16 d0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, x00),
+                                                               __builtin_bit_cast(f16x8, wa0), fz16, 0, 0, 0);
+            d0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, x01),
+                                                        __builtin_bit_cast(f16x8, wa1), d0, 0, 0, 0);
+            f32x16 d1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, x10),
+                                                               __builtin_bit_cast(f16x8, wb0), fz16, 0, 0, 0);
+            d1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, x11),
+                                                        __builtin_bit_cast(f16x8, wb1), d1, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[t][i] = __builtin_fmaf(d0[i], sc[i], acc[t][i]);
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[t][i] = __builtin_fmaf(d1[i], sc[16 + i], acc[t][i]);
+        }
+        // pair it+1 staged by every wave of the K group (and this pair's LDS reads done)
+        __builtin_amdgcn_s_waitcnt(Q8_VMCNT_IMM(AFTER));
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_barrier();
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    }
+    // drain every prefetch (they write LDS) before the LDS is reused below
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    if (KW > 1) {
+        // reduce the K groups in a fixed order (kw = 0 adds 1, 2, ...), through the staging LDS
+        float *red = (float *)hsm;  // [KW-1][RW][TPW][64][16]
+        if (kw > 0) {
+#pragma unroll
+            for (int t = 0; t < TPW; t++) {
+                float *dst = red + ((size_t)(((kw - 1) * RW + rw) * TPW + t) * 64 + lane) * 16;
+#pragma unroll
+                for (int i = 0; i < 16; i += 4)
+                    *(f32x4 *)(dst + i) = (f32x4){acc[t][i], acc[t][i + 1], acc[t][i + 2], acc[t][i + 3]};
+            }
+        }
+        __syncthreads();
+        if (kw == 0) {
+            for (int k2 = 1; k2 < KW; k2++) {
+#pragma unroll
+                for (int t = 0; t < TPW; t++) {
+                    const float *src = red + ((size_t)(((k2 - 1) * RW + rw) * TPW + t) * 64 + lane) * 16;
+#pragma unroll
+                    for (int i = 0; i < 16; i++) acc[t][i] = acc[t][i] + src[i];
+                }
+            }
+        }
+    }
+    if (kw != 0 || !row_live) return;
+    const int o = g * Q8_TILE_ROWS + r;
+    if (o >= mem.rows) return;
+#pragma unroll
+    for (int t = 0; t < TPW; t++) {
+        if (tt0 + t < a.ttiles) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int tok = (tt0 + t) * Q8_TILE_TOKENS + 8 * (i >> 2) + 4 * h + (i & 3);
+                if (tok < a.n) {
+                    const size_t idx = (size_t)tok * mem.rows + o;
+                    mem.y[idx] = mem.bias ? acc[t][i] + mem.bias[idx] : acc[t][i];
+                }
+            }
+        }
+    }
+}
+
+// q8_gemm_h_t<TPW>_r<RW>: up to 512 threads (RW x KW waves).
+#define Q8_GEMM_H(TPW, RW)                                                                             \
+    extern "C" __global__ __launch_bounds__(512) void q8_gemm_h_t##TPW##_r##RW(Q8GemmArgs a) { \
+        gemm_h_body<TPW, RW>(a);                                                                       \
+    }
+Q8_GEMM_H(1, 4)
+Q8_GEMM_H(2, 2)
+Q8_GEMM_H(2, 4)
 
 extern "C" __global__ __launch_bounds__(1024) void q8_gemm_s0_t1(Q8GemmArgs a) { gemm_body<0, 1>(a); }
 extern "C" __global__ __launch_bounds__(1024) void q8_gemm_s1_t1(Q8GemmArgs a) { gemm_body<1, 1>(a); }

@@ -42,6 +42,17 @@
 #define Q8_TILE_ROWS 32
 #define Q8_TILE_TOKENS 32
 #define Q8_UNIT_BYTES 1024
+/* f16 form of a prepared activation unit: the same 16 values per lane as f16,
+ * split in two 1 KB halves: half u holds, at 16*L, lane L's bytes 8u..8u+7
+ * of the int8 unit as eight f16 (exact: |q| <= 127). */
+#define Q8_UNIT_F16_BYTES 2048
+
+/* f16-MFMA GEMM LDS: per K group, Q8_GEMM_H_STAGES ring buffers of
+ * [TPW][2 blocks] f16 activation units, max(TPW, RW) * 64 f32 activation
+ * scale slots, and per row wave two int8 weight units + 256 bytes of scales. */
+#define Q8_GEMM_H_STAGES 3
+#define Q8_GEMM_H_BUF_BYTES(tpw, rw) \
+    ((tpw) * 2 * Q8_UNIT_F16_BYTES + ((tpw) > (rw) ? (tpw) : (rw)) * 64 * 4 + (rw) * (2 * Q8_UNIT_BYTES + 256))
 #define Q8_GROUP_MAX 4 /* apps/engine/src/cuda/mod.rs:63 MMA_GROUP_MAX */
 
 /* Q8_J[h][t]: the AVX2 lane held by dword t of half h. */
@@ -106,6 +117,7 @@ typedef struct {
     int nb;
     int ttiles;
     int mode; /* 0: quantize x; 1: quantize silu(gate) * up */
+    int f16;  /* 1: write the quants as f16 units (Q8_UNIT_F16_BYTES) for the f16-MFMA GEMM */
 } Q8QuantArgs;
 
 typedef struct {
@@ -135,6 +147,7 @@ typedef struct {
     int pairs_per_wave;   /* ceil(pairs_per_slice / kwaves) */
     float *scratch;       /* S > 1: [rtiles][ttiles][S][64][16] partial tiles */
     unsigned *counters;   /* S > 1: arrivals per (row tile, token group), zero between launches */
+    int rwaves;           /* f16 GEMM: row-tile waves per workgroup sharing the LDS-staged activations */
 } Q8GemmArgs;
 
 typedef struct {

@@ -68,6 +68,7 @@ enum Fn {
     F_GEMV_2_0, F_GEMV_2_1, F_GEMV_3_0, F_GEMV_3_1, F_GEMV_5_0, F_GEMV_5_1, F_GEMV_9_0, F_GEMV_9_1,
     F_QUANTIZE,
     F_GEMM_S0_T1, F_GEMM_S1_T1, F_GEMM_S1_T2, F_GEMM_S1_T4,
+    F_GEMM_H_T1_R4, F_GEMM_H_T2_R2, F_GEMM_H_T2_R4,
     F_ARGMAX,
     F_SILU_MUL,
     F_COPY,
@@ -80,6 +81,7 @@ const char *const kFnNames[F_COUNT] = {
     "q8_gemv_pb5_e0", "q8_gemv_pb5_e1", "q8_gemv_pb9_e0", "q8_gemv_pb9_e1",
     "q8_quantize",
     "q8_gemm_s0_t1", "q8_gemm_s1_t1", "q8_gemm_s1_t2", "q8_gemm_s1_t4",
+    "q8_gemm_h_t1_r4", "q8_gemm_h_t2_r2", "q8_gemm_h_t2_r4",
     "q8_argmax",
     "q8_silu_mul",
     "q8_copy",
@@ -180,9 +182,43 @@ int grow(q8_ctx *c, void **buf, size_t *have, size_t need, const char *what) {
     return Q8_OK;
 }
 
-q8_tactic plan(q8_ctx *c, int n, int out, int k, int slots = 1) {
+// Prepared-activation format for n tokens: the tactic table's choice, or the
+// "gemm.f16" option (0: always int8, 1: f16 whenever n >= 2).
+int prepared_format(q8_ctx *c, int n) {
+    const int f = option(c, "gemm.f16", -1);
+    if (f == 0 || n < 2) return Q8_PREPARED_I8;
+    if (f == 1) return Q8_PREPARED_F16;
+    return q8_tactics_prepared_format(n);
+}
+
+// fmt >= 0: a GEMM plan for prepared activations of that format (the kernel
+// family follows the operand's format).
+q8_tactic plan(q8_ctx *c, int n, int out, int k, int slots = 1, int fmt = -1) {
     q8_tactic t{};
     q8_tactics_choose(n, out, k, c->cu_count, &t);
+    if (fmt == Q8_PREPARED_F16 && t.kernel != Q8_KERNEL_GEMM_F16)
+        q8_tactics_for_kernel(Q8_KERNEL_GEMM_F16, n, out, k, c->cu_count, &t);
+    else if (fmt == Q8_PREPARED_I8 && t.kernel != Q8_KERNEL_GEMM)
+        q8_tactics_for_kernel(Q8_KERNEL_GEMM, n, out, k, c->cu_count, &t);
+    if (t.kernel == Q8_KERNEL_GEMM_F16) {
+        const int npairs = (k / 32 + 1) / 2;
+        const int ttiles = (int)ceil_div(n, 32);
+        const int tpw = option(c, "gemm.tpw", -1);
+        const int rw = option(c, "gemm.rwaves", -1);
+        const int kw = option(c, "gemm.kwaves", -1);
+        t.xcd_remap = option(c, "gemm.xcd_remap", t.xcd_remap) ? 1 : 0;
+        if (tpw > 0) t.tpw = (tpw >= 2 && ttiles >= 2) ? 2 : 1;
+        if (rw > 0) t.rwaves = rw >= 4 ? 4 : 2;
+        if (t.tpw == 1) t.rwaves = 4;  // built variants: t1_r4, t2_r2, t2_r4
+        if (tpw > 0 || rw > 0 || kw > 0) {
+            int kws = kw > 0 ? kw : t.kwaves;
+            const int lds_kw = (int)(c->max_lds / ((size_t)Q8_GEMM_H_STAGES * Q8_GEMM_H_BUF_BYTES(t.tpw, t.rwaves)));
+            kws = std::max(1, std::min(std::min(std::min(kws, 8 / t.rwaves), npairs), lds_kw));
+            t.pairs_per_wave = (int)ceil_div(npairs, kws);
+            t.kwaves = (int)ceil_div(npairs, t.pairs_per_wave);
+        }
+        return t;
+    }
     if (t.kernel == Q8_KERNEL_GEMV) {
         if (slots != 1) q8_gemv_shape(out, k, c->cu_count, slots, &t);
         const int nb = k / 32;
@@ -300,7 +336,11 @@ int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const floa
     return launch(c, gemv_fn(pb, t.exact), (unsigned)grid, (unsigned)(waves * 64), lds, &a, sizeof a);
 }
 
+int run_gemm_h(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n, const float *bias);
+
 int run_gemm(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n, const float *bias) {
+    if (p->format == Q8_PREPARED_F16) return run_gemm_h(c, m, count, p, n, bias);
+    if (p->format != Q8_PREPARED_I8) return fail(Q8_ERR_INVALID, "prepared activations: unknown format %d", p->format);
     const int k = p->k;
     const int nb = k / 32;
     Q8GemmArgs a{};
@@ -316,7 +356,7 @@ int run_gemm(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n,
         rt += m[i].w->tiles;
         rows_total += m[i].w->out;
     }
-    const q8_tactic t = plan(c, n, rows_total, k);
+    const q8_tactic t = plan(c, n, rows_total, k, 1, Q8_PREPARED_I8);
     a.total_rtiles = rt;
     a.xq = reinterpret_cast<const uint8_t *>(p->quants);
     a.xs = reinterpret_cast<const float *>(p->scales);
@@ -350,10 +390,59 @@ int run_gemm(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n,
     return launch(c, f, (unsigned)nwg, (unsigned)threads, lds, &a, sizeof a);
 }
 
+// The f16-MFMA GEMM (gemm_h_body): RW row-tile waves x KW K groups per
+// workgroup over TPW token tiles, activations staged in LDS per K group.
+int run_gemm_h(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n, const float *bias) {
+    const int k = p->k;
+    const int nb = k / 32;
+    Q8GemmArgs a{};
+    a.members = count;
+    int rt = 0, rows_total = 0;
+    for (int i = 0; i < count; i++) {
+        a.m[i].quants = m[i].w->quants;
+        a.m[i].scales = m[i].w->scales;
+        a.m[i].y = m[i].y;
+        a.m[i].bias = (i == 0) ? bias : nullptr;
+        a.m[i].rows = m[i].w->out;
+        a.m[i].tile_begin = rt;
+        rt += m[i].w->tiles;
+        rows_total += m[i].w->out;
+    }
+    const q8_tactic t = plan(c, n, rows_total, k, 1, Q8_PREPARED_F16);
+    const int tpw = t.tpw == 2 ? 2 : 1;
+    const int rw = tpw == 1 ? 4 : (t.rwaves >= 4 ? 4 : 2);
+    const int kw = std::max(1, t.kwaves);
+    if (rw * kw > 8) return fail(Q8_ERR_UNSUPPORTED, "gemm_h: %d x %d waves per workgroup", rw, kw);
+    a.total_rtiles = rt;
+    a.xq = reinterpret_cast<const uint8_t *>(p->quants);
+    a.xs = reinterpret_cast<const float *>(p->scales);
+    a.n = n;
+    a.nb = nb;
+    a.ttiles = (int)ceil_div(n, 32);
+    a.twaves = 1;
+    a.rwaves = rw;
+    a.tgroups = (int)ceil_div(a.ttiles, tpw);
+    a.kslices = 1;
+    a.pairs_per_slice = (nb + 1) / 2;
+    a.pairs_per_wave = std::max(1, t.pairs_per_wave);
+    if ((long long)a.pairs_per_wave * kw < (nb + 1) / 2)
+        return fail(Q8_ERR_UNSUPPORTED, "gemm_h: %d K waves x %d pairs miss blocks", kw, a.pairs_per_wave);
+    const long long nwg = ceil_div(rt, rw) * (long long)a.tgroups;
+    if (nwg > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "gemm_h: grid of %lld workgroups", nwg);
+    a.nwg = (int)nwg;
+    a.xcd_remap = (t.xcd_remap && nwg % 8 == 0) ? 1 : 0;
+    const size_t stage = (size_t)kw * Q8_GEMM_H_STAGES * Q8_GEMM_H_BUF_BYTES(tpw, rw);
+    const size_t reduce = (size_t)(kw - 1) * rw * tpw * 64 * 16 * sizeof(float);
+    const unsigned lds = (unsigned)std::max(stage, reduce);
+    const Fn f = tpw == 1 ? F_GEMM_H_T1_R4 : rw == 4 ? F_GEMM_H_T2_R4 : F_GEMM_H_T2_R2;
+    return launch(c, f, (unsigned)nwg, (unsigned)(64 * rw * kw), lds, &a, sizeof a);
+}
+
 int prepare_into(q8_ctx *c, q8_dptr x, q8_dptr gate, q8_dptr up, int n, int k, q8_prepared *out) {
     const int nb = k / 32;
     const long long ttiles = ceil_div(n, 32);
-    const size_t qbytes = (size_t)ttiles * nb * Q8_UNIT_BYTES;
+    const int fmt = prepared_format(c, n);
+    const size_t qbytes = (size_t)ttiles * nb * (fmt == Q8_PREPARED_F16 ? Q8_UNIT_F16_BYTES : Q8_UNIT_BYTES);
     const size_t sbytes = (size_t)ttiles * nb * Q8_TILE_TOKENS * sizeof(float);
     Q8_TRY(grow(c, &c->act_ws, &c->act_ws_bytes, align_up(qbytes, kAlign) + sbytes, "hipMalloc(activation)"));
     Q8QuantArgs a{};
@@ -366,6 +455,7 @@ int prepare_into(q8_ctx *c, q8_dptr x, q8_dptr gate, q8_dptr up, int n, int k, q
     a.nb = nb;
     a.ttiles = (int)ttiles;
     a.mode = gate ? 1 : 0;
+    a.f16 = fmt == Q8_PREPARED_F16 ? 1 : 0;
     const long long units = ttiles * nb;  // one wave per (token tile, block) unit, four per workgroup
     if (units > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "prepare: %lld units", units);
     Q8_TRY(launch(c, F_QUANTIZE, (unsigned)ceil_div(units, 4), 256, 0, &a, sizeof a));
@@ -373,6 +463,7 @@ int prepare_into(q8_ctx *c, q8_dptr x, q8_dptr gate, q8_dptr up, int n, int k, q
     out->scales = (q8_dptr)(uintptr_t)a.xs;
     out->n = n;
     out->k = k;
+    out->format = fmt;
     return Q8_OK;
 }
 
@@ -464,7 +555,8 @@ int q8_open(int device, q8_ctx **out) {
     char market[256] = {0};
     if (hipDeviceGetName(market, sizeof market - 1, device) != hipSuccess || market[0] == 0)
         std::snprintf(market, sizeof market, "%s", prop.name[0] ? prop.name : "AMD Instinct");
-    std::snprintf(c->name, sizeof c->name, "%s (%s, %d CUs)", market, prop.gcnArchName, c->cu_count);
+    std::snprintf(c->name, sizeof c->name, "%s (%s, %d CUs, %zu KB LDS per workgroup)", market, prop.gcnArchName,
+                  c->cu_count, c->max_lds / 1024);
     int rc = Q8_OK;
     do {
         hipError_t he = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
@@ -539,7 +631,7 @@ int q8_set_option(q8_ctx *c, const char *name, int value) {
     if (!c || !name) return fail(Q8_ERR_INVALID, "q8_set_option: bad arguments");
     static const char *const known[] = {"gemv.exact", "gemv.waves",  "gemv.pairs",     "gemv.slices",
                                         "gemm.smode", "gemm.tpw",    "gemm.twaves",    "gemm.xcd_remap",
-                                        "gemm.kwaves", "gemm.slices"};
+                                        "gemm.kwaves", "gemm.slices", "gemm.rwaves",    "gemm.f16"};
     bool ok = false;
     for (const char *k : known) ok = ok || std::strcmp(k, name) == 0;
     if (!ok) return fail(Q8_ERR_INVALID, "unknown option %s", name);
@@ -893,8 +985,10 @@ int q8_plan(q8_ctx *c, int n, int out, int k, q8_tactic *t) {
     Q8_TRY(check_n(n));
     if (out <= 0) return fail(Q8_ERR_INVALID, "q8_plan: %d rows", out);
     if (c) {
+        // with a context: the plan q8_matmul runs, options and the prepared
+        // format for n included
         std::lock_guard<std::recursive_mutex> lock(c->mu);
-        *t = plan(c, n, out, k);
+        *t = n == 1 ? plan(c, n, out, k) : plan(c, n, out, k, 1, prepared_format(c, n));
         return Q8_OK;
     }
     return q8_tactics_choose(n, out, k, 256, t);

@@ -1,7 +1,9 @@
 // q8_tactics.cpp -- see q8_tactics.h.
 #include "q8_tactics.h"
+#include "q8_layout.h"
 
 #include <algorithm>
+#include <cmath>
 
 namespace {
 
@@ -12,6 +14,12 @@ const Q8TacticRow kRows[] = {
     {"matmul.gemm_mfma_i8", Q8_KERNEL_GEMM, 2, Q8_MAX_TOKENS, Q8_MATURITY_MEASURED, 10,
      "n >= 2 quantizes activations (tensor.rs:104-125); v_mfma_i32_32x32x32_i8 is one Q8_0 block "
      "per instruction, exact int32, scale products on v_mfma_f32_32x32x1_2b_f32"},
+    {"matmul.gemm_mfma_f16", Q8_KERNEL_GEMM_F16, 2, Q8_MAX_TOKENS, Q8_MATURITY_EXPERIMENTAL, 5,
+     "quants are integers |q| <= 127, exact in f16: two v_mfma_f32_32x32x16_f16 give each block's int32 "
+     "dot already in f32, removing the 16 v_cvt_f32_i32 per 32x32 tile and block that bound the int8 "
+     "path on the VALU; bit-identical to the int8 kernel.  Measured slower so far (gate|up n=512 70 us "
+     "vs 50 us): one wave per row tile reads 2 KB of f16 activations per block-tile from LDS, about "
+     "150 B/clk per CU at the MFMA rate, above the LDS bandwidth; option gemm.f16 = 1 selects it"},
     {"matmul.gemm_f32_small_n", Q8_KERNEL_GEMM, 2, 7, Q8_MATURITY_REJECTED, 0,
      "the reference GPU's f32-activation path for 2 <= n <= 7 (cuda/mod.rs:883-891) disagrees with "
      "the CPU kernels that define parity, which quantize for every n >= 2"},
@@ -94,6 +102,76 @@ void q8_gemm_shape(int n, int out, int k, int cu_count, q8_tactic *t) {
     t->xcd_remap = 1;
 }
 
+// f16 GEMM launch shape: TPW token tiles per wave (2 when there are two or
+// more), RW row-tile waves sharing the LDS-staged activations, KW K-split
+// waves, RW * KW <= 8.  The GEMM kernel runs two waves per SIMD (about 210
+// VGPRs), so the chip holds 2 * 4 * cu_count waves at once; the search takes
+// the (RW, KW) whose last round of waves is fullest, discounted for the fixed
+// per-wave cost (about two block pairs of prologue, drain and K reduction).
+void q8_gemm_h_shape(int n, int out, int k, int cu_count, q8_tactic *t) {
+    const int nb = k / 32;
+    const int npairs = ceil_div(nb, 2);
+    const int ttiles = ceil_div(n, 32);
+    const int rtiles = ceil_div(out, 32);
+    const double cap = 2.0 * 4.0 * std::max(cu_count, 1);
+    const int tpw = ttiles >= 2 ? 2 : 1;
+    double best = -1.0;
+    int best_rw = 4, best_kw = 1;
+    for (int rw : {2, 4}) {
+        if (tpw == 1 && rw != 4) continue;  // built variants: t1_r4, t2_r2, t2_r4
+        for (int kw = 1; rw * kw <= 8 && kw <= npairs; kw++) {
+            // LDS: KW K groups x the staging ring, within 64 KB
+            const long long lds = (long long)kw * Q8_GEMM_H_STAGES * Q8_GEMM_H_BUF_BYTES(tpw, rw);
+            if (lds > 65536) continue;
+            const int ppw = ceil_div(npairs, kw);
+            if (ceil_div(npairs, ppw) != kw) continue;  // no K wave without pairs
+            const double waves = (double)ceil_div(rtiles, rw) * ceil_div(ttiles, tpw) * rw * kw;
+            const double rounds = waves / cap;
+            const double fill = rounds / std::ceil(rounds);
+            const double live = (double)rtiles / (ceil_div(rtiles, rw) * rw);  // row waves past the end idle
+            const double score = fill * live * ppw / (ppw + 2.0);
+            if (score > best + 1e-9) {
+                best = score;
+                best_rw = rw;
+                best_kw = kw;
+            }
+        }
+    }
+    t->tpw = tpw;
+    t->rwaves = best_rw;
+    t->kwaves = best_kw;
+    t->pairs_per_wave = ceil_div(npairs, best_kw);
+    t->twaves = 1;
+    t->kslices = 1;
+    t->smode = 1;
+    t->xcd_remap = 1;
+}
+
+int q8_tactics_for_kernel(int kernel, int n, int out, int k, int cu_count, q8_tactic *t) {
+    for (int i = 0; i < kCount; i++) {
+        const Q8TacticRow &row = kRows[i];
+        if (row.kernel != kernel || row.maturity == Q8_MATURITY_REJECTED) continue;
+        *t = q8_tactic{};
+        t->kernel = kernel;
+        t->name = row.name;
+        t->evidence = row.evidence;
+        if (kernel == Q8_KERNEL_GEMV)
+            q8_gemv_shape(out, k, cu_count, 1, t);
+        else if (kernel == Q8_KERNEL_GEMM_F16)
+            q8_gemm_h_shape(n, out, k, cu_count, t);
+        else
+            q8_gemm_shape(n, out, k, cu_count, t);
+        return Q8_OK;
+    }
+    return Q8_ERR_UNSUPPORTED;
+}
+
+int q8_tactics_prepared_format(int n) {
+    q8_tactic t{};
+    if (q8_tactics_choose(n, 32, 32, 1, &t) != Q8_OK) return Q8_PREPARED_I8;
+    return t.kernel == Q8_KERNEL_GEMM_F16 ? Q8_PREPARED_F16 : Q8_PREPARED_I8;
+}
+
 int q8_tactics_table_size() { return kCount; }
 
 const Q8TacticRow &q8_tactics_row(int i) { return kRows[i]; }
@@ -113,6 +191,8 @@ int q8_tactics_choose(int n, int out, int k, int cu_count, q8_tactic *t) {
     t->evidence = best->evidence;
     if (best->kernel == Q8_KERNEL_GEMV)
         q8_gemv_shape(out, k, cu_count, 1, t);
+    else if (best->kernel == Q8_KERNEL_GEMM_F16)
+        q8_gemm_h_shape(n, out, k, cu_count, t);
     else
         q8_gemm_shape(n, out, k, cu_count, t);
     return Q8_OK;

@@ -28,5 +28,11 @@ int q8_tactics_choose(int n, int out, int k, int cu_count, q8_tactic *t);
 // Launch shapes (slots = member tiles per GEMV workgroup: 2 for fused gate/up).
 void q8_gemv_shape(int out, int k, int cu_count, int slots, q8_tactic *t);
 void q8_gemm_shape(int n, int out, int k, int cu_count, q8_tactic *t);
+void q8_gemm_h_shape(int n, int out, int k, int cu_count, q8_tactic *t);
+/* The prepared-activation format the table's choice for n consumes
+ * (Q8_PREPARED_I8 or Q8_PREPARED_F16): it depends on n only. */
+int q8_tactics_prepared_format(int n);
+/* The first non-rejected row of `kernel` and its launch shape for (n, out, k). */
+int q8_tactics_for_kernel(int kernel, int n, int out, int k, int cu_count, q8_tactic *t);
 
 #endif

@@ -32,6 +32,8 @@ Q8_ERR_NO_DEVICE = 4
 Q8_ERR_OUT_OF_MEMORY = 5
 MAX_TOKENS = 1024
 GROUP_MAX = 4
+KERNEL_GEMV, KERNEL_GEMM, KERNEL_GEMM_F16 = 1, 2, 3
+PREPARED_I8, PREPARED_F16 = 0, 1
 KERNEL_GEMV = 1
 KERNEL_GEMM = 2
 
@@ -61,7 +63,16 @@ class Q8Error(RuntimeError):
 class Prepared(ctypes.Structure):
     """q8_prepared: quantized activations (the reference's ``Prepared``)."""
     _fields_ = [("quants", ctypes.c_uint64), ("scales", ctypes.c_uint64),
-                ("n", ctypes.c_int), ("k", ctypes.c_int)]
+                ("n", ctypes.c_int), ("k", ctypes.c_int), ("format", ctypes.c_int)]
+
+    def quant_bytes(self) -> int:
+        """Bytes of the quant plane: one unit per (32 tokens, block), 1 KB
+        as int8 (PREPARED_I8) or 2 KB as f16 (PREPARED_F16)."""
+        units = (self.n + 31) // 32 * (self.k // 32)
+        return units * (2048 if self.format == PREPARED_F16 else 1024)
+
+    def scale_bytes(self) -> int:
+        return (self.n + 31) // 32 * (self.k // 32) * 32 * 4
 
 
 class _GroupEntry(ctypes.Structure):
@@ -74,7 +85,7 @@ class Tactic(ctypes.Structure):
                 ("exact", ctypes.c_int), ("tpw", ctypes.c_int), ("twaves", ctypes.c_int),
                 ("smode", ctypes.c_int),
                 ("xcd_remap", ctypes.c_int), ("kslices", ctypes.c_int), ("kwaves", ctypes.c_int),
-                ("name", ctypes.c_char_p), ("evidence", ctypes.c_char_p)]
+                ("rwaves", ctypes.c_int), ("name", ctypes.c_char_p), ("evidence", ctypes.c_char_p)]
 
     def as_dict(self) -> dict:
         d = {f: getattr(self, f) for f, _ in self._fields_}

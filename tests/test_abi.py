@@ -99,6 +99,14 @@ def test_plan_never_selects_a_rejected_tactic(n, out, k):
         pps = -(-npairs // s)
         assert 1 <= s <= npairs and (s - 1) * pps < npairs  # no empty slice
         assert t["waves_per_tile"] * t["pairs_per_wave"] >= pps
+    elif t["kernel"] == q8.KERNEL_GEMM_F16:
+        # f16-MFMA family: built variants t1_r4, t2_r2, t2_r4; <= 512 threads
+        assert n >= 2
+        assert (t["tpw"], t["rwaves"]) in ((1, 4), (2, 2), (2, 4))
+        assert t["rwaves"] * t["kwaves"] <= 8
+        npairs = (k // 32 + 1) // 2
+        assert t["kwaves"] * t["pairs_per_wave"] >= npairs
+        assert (t["kwaves"] - 1) * t["pairs_per_wave"] < npairs  # no K wave without pairs
     else:
         assert t["kernel"] == q8.KERNEL_GEMM
         assert t["tpw"] in (1, 2, 4)

@@ -23,7 +23,7 @@ TOL_REL = 1e-5
 SEED = 0x5EED
 J = [[0, 4, 1, 5], [2, 6, 3, 7]]
 OPTIONS = ("gemv.exact", "gemv.waves", "gemv.pairs", "gemv.slices", "gemm.smode", "gemm.tpw", "gemm.twaves",
-           "gemm.xcd_remap", "gemm.kwaves", "gemm.slices")
+           "gemm.xcd_remap", "gemm.kwaves", "gemm.slices", "gemm.rwaves", "gemm.f16")
 
 
 def assert_close(got, ref, what):
@@ -133,13 +133,23 @@ def run_matmul(gpu, w, x, n, bias=None):
 
 def unpack_prepared(gpu, p, n, k):
     """Download a prepared buffer and undo the lane-order layout
-    (llm_amd/csrc/q8_layout.h) into [n][k] int8 and [n][k/32] f32."""
+    (llm_amd/csrc/q8_layout.h) into [n][k] int8 and [n][k/32] f32.  The f16
+    format holds the same integers as f16: unit half u, lane L = bytes
+    8u..8u+7 of lane L's 16-byte int8 slot."""
     nb = k // 32
     tt = (n + 31) // 32
-    qraw = np.empty(tt * nb * 1024, np.uint8)
     sraw = np.empty(tt * nb * 32, np.float32)
-    q8._check(q8.lib().q8_download(gpu.handle, qraw.ctypes.data, p.quants, qraw.nbytes))
     q8._check(q8.lib().q8_download(gpu.handle, sraw.ctypes.data, p.scales, sraw.nbytes))
+    if p.format == q8.PREPARED_F16:
+        hraw = np.empty(tt * nb * 1024, np.float16)
+        q8._check(q8.lib().q8_download(gpu.handle, hraw.ctypes.data, p.quants, hraw.nbytes))
+        hv = hraw.astype(np.float32).reshape(tt, nb, 2, 64, 8)          # [tt][b][u][lane][8]
+        assert np.array_equal(hv, np.round(hv)) and np.abs(hv).max(initial=0) <= 127, "f16 quants are integers"
+        qraw = hv.transpose(0, 1, 3, 2, 4).reshape(tt, nb, 64, 16).astype(np.int8).view(np.uint8).reshape(-1)
+    else:
+        assert p.format == q8.PREPARED_I8
+        qraw = np.empty(tt * nb * 1024, np.uint8)
+        q8._check(q8.lib().q8_download(gpu.handle, qraw.ctypes.data, p.quants, qraw.nbytes))
     qv = qraw.view(np.int8).reshape(tt, nb, 2, 32, 16)
     out = np.zeros((tt, 32, nb, 32), np.int8)
     for h in range(2):
@@ -306,8 +316,12 @@ def test_decode_group_matches_separate_matmuls(gpu):
 # activation quantization (quant.rs:98-121), byte-exact
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("n,k", [(1, 32), (2, 64), (31, 2304), (33, 2304), (65, 5760)])
-def test_quantized_activations_are_bit_exact(gpu, n, k):
+@pytest.mark.parametrize("n,k", [(1, 32), (2, 64), (31, 2304), (33, 2304), (65, 5760), (130, 2304)])
+@pytest.mark.parametrize("f16", [-1, 0, 1])
+def test_quantized_activations_are_bit_exact(gpu, n, k, f16):
+    """Both prepared formats (int8 units, and the same integers as f16 for
+    the f16-MFMA GEMM) hold the reference's quantize_q8_0 bit for bit."""
+    gpu.set_option("gemm.f16", f16)
     r = rng(20 + n)
     x = oracle.make_activations(r, n, k, outlier_rate=0.01)
     x[0, :32] = 0.0                                   # all-zero block
@@ -321,6 +335,12 @@ def test_quantized_activations_are_bit_exact(gpu, n, k):
     xb = gpu.alloc(4 * n * k)
     xb.upload(x)
     p = gpu.prepare(xb, 0, n, k)
+    planned_f16 = n >= 2 and gpu.plan(n, 64, k)["kernel"] == q8.KERNEL_GEMM_F16
+    assert p.format == (q8.PREPARED_F16 if planned_f16 else q8.PREPARED_I8)
+    if f16 == 1:
+        assert planned_f16 == (n >= 2)
+    if f16 == 0:
+        assert not planned_f16
     q, s = unpack_prepared(gpu, p, n, k)
     for t in range(n):
         rq, rs = oracle.quantize_q8_0(x[t])
@@ -357,10 +377,11 @@ def exact_problem(r, out, k, n):
     return q8.Weight(raw.reshape(-1), k, out), x, y.astype(np.float32)
 
 
-@pytest.mark.parametrize("n,k", [(2, 32), (5, 64), (33, 96), (64, 1024)])
-@pytest.mark.parametrize("smode", [1, 0])
-def test_gemm_int32_block_dot_is_exact(gpu, n, k, smode):
-    gpu.set_option("gemm.smode", smode)
+@pytest.mark.parametrize("n,k", [(2, 32), (5, 64), (33, 96), (64, 1024), (160, 1024)])
+@pytest.mark.parametrize("path", ["i8_smode1", "i8_smode0", "f16"])
+def test_gemm_int32_block_dot_is_exact(gpu, n, k, path):
+    gpu.set_option("gemm.f16", 1 if path == "f16" else 0)
+    gpu.set_option("gemm.smode", 0 if path == "i8_smode0" else 1)
     r = rng(30 + n)
     w, x, y = exact_problem(r, 40, k, n)
     got = run_matmul(gpu, w, x, n)
@@ -397,6 +418,7 @@ def test_gemm_configs1(gpu, n):
     (1, 2, 2, 0, 3, 1), (1, 2, 1, 1, 2, 4), (1, 4, 1, 0, 1, 7), (1, 4, 2, 1, 4, 1), (1, 4, 1, 1, 8, 3),
     (0, 1, 2, 1, 4, 3), (1, 1, 1, 1, 6, 15), (1, 2, 3, 0, 2, 2), (1, 4, 2, 0, 1, 1)])
 def test_gemm_variants_agree(gpu, smode, tpw, twaves, remap, kwaves, slices):
+    gpu.set_option("gemm.f16", 0)  # the int8-MFMA family's launch variants
     gpu.set_option("gemm.smode", smode)
     gpu.set_option("gemm.tpw", tpw)
     gpu.set_option("gemm.twaves", twaves)
@@ -411,6 +433,38 @@ def test_gemm_variants_agree(gpu, smode, tpw, twaves, remap, kwaves, slices):
     got = run_matmul(gpu, w, x, n)
     assert_parity(got, ref, exact_matmul(w.data, k, out, x, n),
                   f"gemm smode={smode} tpw={tpw} twaves={twaves} remap={remap} kwaves={kwaves} slices={slices}")
+    gpu.release(w)
+
+
+@pytest.mark.parametrize("n,out,k", [(200, 256, 5760), (64, 96, 2304), (512, 320, 2304), (33, 40, 96),
+                                     (130, 64, 32)])
+@pytest.mark.parametrize("tpw,rwaves,kwaves", [(2, 4, 1), (2, 2, 1), (2, 2, 3), (2, 4, 2), (1, 4, 2), (2, 2, 4)])
+def test_gemm_f16_equals_int8_bit_for_bit(gpu, n, out, k, tpw, rwaves, kwaves):
+    """The f16-MFMA GEMM computes each block's integer dot exactly and then
+    the int8 kernel's arithmetic in its order, so with the same K split the
+    two families agree to the bit (and both meet the reference bar)."""
+    r = rng(61 + n + out)
+    w = weight(r, out, k)
+    x = oracle.make_activations(r, n, k, outlier_rate=0.01)
+    gpu.set_option("gemm.f16", 1)
+    gpu.set_option("gemm.tpw", tpw)
+    gpu.set_option("gemm.rwaves", rwaves)
+    gpu.set_option("gemm.kwaves", kwaves)
+    t = gpu.plan(n, out, k)
+    assert t["kernel"] == q8.KERNEL_GEMM_F16
+    kw = t["kwaves"]                              # the K split the runtime settles on (LDS, pairs)
+    got = run_matmul(gpu, w, x, n)
+    gpu.set_option("gemm.f16", 0)
+    gpu.set_option("gemm.tpw", 1)
+    gpu.set_option("gemm.twaves", 1)
+    gpu.set_option("gemm.slices", 1)
+    gpu.set_option("gemm.kwaves", kw)
+    assert gpu.plan(n, out, k)["kwaves"] == kw
+    want = run_matmul(gpu, w, x, n)
+    what = f"f16 gemm n={n} out={out} k={k} tpw={tpw} rwaves={rwaves} kwaves={kw}"
+    assert_bits(got, want, what)
+    ref = oracle.matmul(w.data, k, out, x, n)
+    assert_parity(got, ref, exact_matmul(w.data, k, out, x, n), what)
     gpu.release(w)
 
 
@@ -468,10 +522,10 @@ def test_reference_gpu_vs_cpu_protocol(gpu):
 # gate/up + SiLU, silu_mul_prepare, lm_head argmax
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("n", [1, 3, 64])
-def test_gate_up_silu(gpu, n):
+@pytest.mark.parametrize("n,ffn", [(1, 5760), (3, 5760), (64, 5760), (130, 640)])
+def test_gate_up_silu(gpu, n, ffn):
     r = rng(80 + n)
-    k, ffn = 2304, 5760
+    k = 2304
     gw, uw = weight(r, ffn, k), weight(r, ffn, k)
     x = oracle.make_activations(r, n, k)
     xb = gpu.alloc(4 * n * k)
@@ -493,9 +547,9 @@ def test_gate_up_silu(gpu, n):
     gpu.release(uw)
 
 
-def test_silu_mul_and_its_quantization(gpu):
-    r = rng(90)
-    n, k = 40, 5760
+@pytest.mark.parametrize("n,k", [(40, 5760), (130, 1024)])
+def test_silu_mul_and_its_quantization(gpu, n, k):
+    r = rng(90 + n)
     g = (r.standard_normal((n, k)) * 3).astype(np.float32)
     u = r.standard_normal((n, k)).astype(np.float32)
     gb, ub, ab = gpu.alloc(4 * n * k), gpu.alloc(4 * n * k), gpu.alloc(4 * n * k)
