@@ -238,6 +238,7 @@ def bench_layer_n512(gpu, reps, rng, n=512):
     # the same work piece by piece (each its own graph): quantization alone and
     # each projection on already-prepared activations
     gu = gpu.alloc(4 * n * 2 * ffn)
+    norm_w = (1.0 + 0.1 * rng.standard_normal(hid)).astype(np.float32)  # the fused rmsnorm -> Q8_0 prologue
     # A Prepared points into the library's one activation workspace (valid
     # until the next prepare, as the reference's); keep copies in buffers of
     # our own so both operands stay valid side by side.
@@ -246,6 +247,7 @@ def bench_layer_n512(gpu, reps, rng, n=512):
     pieces = {
         "quantize_x": lambda: gpu.prepare(xb, 0, n, hid),
         "quantize_act": lambda: gpu.prepare(act, 0, n, ffn),
+        "norm_prepare_x": lambda: gpu.norm_prepare(xb, 0, norm_w, 1e-6, n),
         "qkv": lambda: gpu.matmul_prompt_group([(wq, qkv, 0), (wk, qkv, n * hid), (wv, qkv, 2 * n * hid)],
                                                p, n, hid),
         "o": lambda: gpu.matmul(wo, qkv, 0, n, hb, 0, prepared=p),

@@ -181,6 +181,19 @@ int q8_prepare(q8_ctx *ctx, q8_dptr x, size_t x_offset, int n, int k, q8_prepare
  * Compute::silu_mul_prepare (compute.rs:993-1019).  gate and up are [n][k]. */
 int q8_silu_mul_prepare(q8_ctx *ctx, q8_dptr gate, q8_dptr up, int n, int k, q8_prepared *out);
 
+/* RMSNorm rows (ops.rs:5-30; Compute::rmsnorm -> Gpu::rmsnorm_rows,
+ * compute.rs:584-614): out[t][i] = (x[t][i] * s_t) * weight[i], s_t =
+ * 1 / sqrt(mean_t(x^2) + eps), the squares summed in f64.  `weight` is a host
+ * f32[k] made resident on first use and cached by (pointer, length), as
+ * Gpu::plain does; k % 32 == 0. */
+int q8_rmsnorm(q8_ctx *ctx, q8_dptr x, size_t x_offset, const float *weight, int k, float eps, int rows, q8_dptr out,
+               size_t out_offset);
+/* prepare(rmsnorm(x)) in one pass, the f32 norm never written
+ * (Gpu::rmsnorm_prepare, cuda/mod.rs:1414-1445; Compute::norm_prepare,
+ * compute.rs:959-984, whose below-threshold f32 branch is q8_rmsnorm).
+ * The result is a view into the activation workspace like q8_prepare's. */
+int q8_norm_prepare(q8_ctx *ctx, q8_dptr x, size_t x_offset, const float *weight, int k, float eps, int rows,
+                    q8_prepared *out);
 /* act[i] = silu(gate[i]) * up[i] for i < len: Gpu::silu_mul / Compute::silu_mul
  * (compute.rs:931-953, ops.rs:33-35). */
 int q8_silu_mul(q8_ctx *ctx, q8_dptr act, q8_dptr gate, q8_dptr up, size_t len);

@@ -17,6 +17,8 @@
 //                   matrices, residual epilogue               (gpu.cu q8_matmul_mma 907-1212)
 //   q8_argmax       greedy argmax over the lm_head logits      (sampler.rs:167-175, on device)
 //   q8_silu_mul     act = silu(gate) * up                      (gpu.cu silu_mul 410-418)
+//   q8_rmsnorm      RMSNorm rows, optionally quantized to prepared Q8_0
+//                                                              (gpu.cu rmsnorm_rows, rmsnorm_quantize_rows 351-407)
 #include <hip/hip_runtime.h>
 
 #include "q8_layout.h"
@@ -438,6 +440,47 @@ Q8_GEMV_KERNEL(9, 1, 512)
 
 // ---------------------------------------------------------------------------
 // Activation quantization (quant.rs:98-121), into the prepared tile layout.
+//
+// e[q][c] is half h of one token's block: element 8c + J[h][q].  half_peak is
+// the max |e| of the half (f32::max ignores NaN, as fmaxf does); quant_store
+// quantizes with the block's peak (both halves) and writes the half as lane
+// slot `slot` (= 32h + token % 32) of prepared unit `u` (int8 or f16 form),
+// and, when `write_scale`, the block's f32 scale.
+static __device__ __forceinline__ float half_peak(const float (&e)[4][4]) {
+    float peak = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) peak = fmaxf(peak, fabsf(e[q][c]));
+    return peak;
+}
+
+static __device__ __forceinline__ void quant_store(const float (&e)[4][4], float peak, uint8_t *xq, float *xs,
+                                                   size_t u, int slot, bool write_scale, int f16) {
+    const float scale = peak / 127.0f;
+    const float inverse = peak > 0.0f ? 127.0f / peak : 0.0f;
+    i32x4 packed;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        unsigned w = 0;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float prod = e[q][c] * inverse;
+            w |= ((unsigned)sat_i8(roundf(prod)) & 0xffu) << (8 * c);
+        }
+        packed[q] = (int)w;
+    }
+    if (f16) {
+        // the same values as f16, bytes 0-7 to the unit's first half, 8-15 to its second
+        uint8_t *dst = xq + u * Q8_UNIT_F16_BYTES + slot * 16;
+        *(i32x4 *)dst = i8x4_to_f16x4(packed[0], packed[1]);
+        *(i32x4 *)(dst + 1024) = i8x4_to_f16x4(packed[2], packed[3]);
+    } else {
+        *(i32x4 *)(xq + u * Q8_UNIT_BYTES + slot * 16) = packed;
+    }
+    if (write_scale) xs[u * Q8_TILE_TOKENS + (slot & 31)] = scale;
+}
+
 // One wave per (32-token tile, block) unit: lane L = 32h + t owns half h of
 // token t's block, i.e. AVX2 lanes J[h][0..3] across the four chunks -- as
 // eight float2 loads (elements 8c + {j, j+1}) -- and writes it as one 16-byte
@@ -485,36 +528,10 @@ extern "C" __global__ __launch_bounds__(256) void q8_quantize(Q8QuantArgs a) {
             e[3][c] = hi.y;  // J[h][3] = 5 + 2h
         }
     }
-    float peak = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 4; q++)
-#pragma unroll
-        for (int c = 0; c < 4; c++) peak = fmaxf(peak, fabsf(e[q][c]));
+    float peak = half_peak(e);
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(peak), __float_as_uint(peak), false, false);
     peak = fmaxf(peak, __uint_as_float(h ? sw[0] : sw[1]));
-    const float scale = peak / 127.0f;
-    const float inverse = peak > 0.0f ? 127.0f / peak : 0.0f;
-    i32x4 packed;
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-        unsigned w = 0;
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const float prod = e[q][c] * inverse;
-            w |= ((unsigned)sat_i8(roundf(prod)) & 0xffu) << (8 * c);
-        }
-        packed[q] = (int)w;
-    }
-    const size_t u = (size_t)tt * nb + b;
-    if (a.f16) {
-        // the same values as f16, bytes 0-7 to the unit's first half, 8-15 to its second
-        uint8_t *dst = a.xq + u * Q8_UNIT_F16_BYTES + lane * 16;
-        *(i32x4 *)dst = i8x4_to_f16x4(packed[0], packed[1]);
-        *(i32x4 *)(dst + 1024) = i8x4_to_f16x4(packed[2], packed[3]);
-    } else {
-        *(i32x4 *)(a.xq + u * Q8_UNIT_BYTES + lane * 16) = packed;
-    }
-    if (h == 0) a.xs[u * Q8_TILE_TOKENS + tl] = scale;
+    quant_store(e, peak, a.xq, a.xs, (size_t)tt * nb + b, lane, h == 0, a.f16);
 }
 
 // ---------------------------------------------------------------------------
@@ -1116,6 +1133,77 @@ extern "C" __global__ __launch_bounds__(256) void q8_copy(Q8CopyArgs a) {
 }
 
 // act[i] = silu(gate[i]) * up[i]   (compute.rs:940-944)
+// ---------------------------------------------------------------------------
+// RMSNorm (ops.rs:5-30), as f32 rows and/or straight into prepared Q8_0
+// activations (compute.rs:959-984 norm_prepare; gpu.cu rmsnorm_quantize_rows
+// 351-407).  One wave per token row, four rows per workgroup.
+//
+// The row's squares are taken in f32 and summed in f64 (ggml's choice, kept
+// by the reference), here as per-lane partial sums reduced across the wave;
+// the reference adds them left to right.  Both are f64 sums of the same f32
+// terms, within n * 2^-53 of each other, so the f32 mean square they round to
+// differs only when the exact value lies that close to an f32 rounding
+// boundary.  Then scale = 1 / sqrt(mean_square + eps) in f32 (correctly
+// rounded sqrt and division) and each value is (x * scale) * w.
+//
+// Quantization: lane L handles half L%2 of blocks L/2, L/2 + 32, ...; the
+// block peak meets its partner half through one xor-1 shuffle.  Rows from n
+// up to the token-tile boundary are written as zeros.
+// ---------------------------------------------------------------------------
+extern "C" __global__ __launch_bounds__(256) void q8_rmsnorm(Q8NormArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (t >= a.rows_launched) return;  // whole waves
+    const int k = a.k;
+    const bool live = t < a.n;
+    const float *xr = a.x + (size_t)min(t, a.n - 1) * k;
+    double ss = 0.0;
+    for (int i = lane * 4; i < k; i += 256) {
+        const float v0 = xr[i], v1 = xr[i + 1], v2 = xr[i + 2], v3 = xr[i + 3];
+        ss += (double)(v0 * v0);
+        ss += (double)(v1 * v1);
+        ss += (double)(v2 * v2);
+        ss += (double)(v3 * v3);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    const float mean_square = (float)(ss / (double)k);
+    const float scale = 1.0f / sqrtf(mean_square + a.eps);
+
+    if (a.out && live) {
+        float *orow = a.out + (size_t)t * k;
+        for (int i = lane * 4; i < k; i += 256) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) orow[i + j] = (xr[i + j] * scale) * a.w[i + j];
+        }
+    }
+    if (a.xq) {
+        const int nb = k / 32;
+        const int h = lane & 1;
+        const int tt = t >> 5;
+        for (int b0 = 0; b0 < nb; b0 += 32) {
+            const int b = min(b0 + (lane >> 1), nb - 1);  // clamped: every lane joins the shuffle
+            const size_t base = (size_t)b * 32 + 2 * h;
+            float e[4][4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                // chunk c: elements 8c + 2h, +1 (dwords 0, 2) and 8c + 4 + 2h, +1 (dwords 1, 3)
+                const size_t i0 = base + 8 * c, i1 = base + 8 * c + 4;
+                const float x00 = (xr[i0] * scale) * a.w[i0], x01 = (xr[i0 + 1] * scale) * a.w[i0 + 1];
+                const float x10 = (xr[i1] * scale) * a.w[i1], x11 = (xr[i1 + 1] * scale) * a.w[i1 + 1];
+                e[0][c] = live ? x00 : 0.0f;  // J[h][0] = 2h
+                e[2][c] = live ? x01 : 0.0f;  // J[h][2] = 2h + 1
+                e[1][c] = live ? x10 : 0.0f;  // J[h][1] = 4 + 2h
+                e[3][c] = live ? x11 : 0.0f;  // J[h][3] = 5 + 2h
+            }
+            float peak = half_peak(e);
+            peak = fmaxf(peak, __shfl_xor(peak, 1));
+            if (b0 + (lane >> 1) < nb)
+                quant_store(e, peak, a.xq, a.xs, (size_t)tt * nb + b, 32 * h + (t & 31), h == 0, a.f16);
+        }
+    }
+}
+
 extern "C" __global__ __launch_bounds__(256) void q8_silu_mul(Q8EltArgs a) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < a.len) a.act[i] = silu_f32(a.gate[i]) * a.up[i];

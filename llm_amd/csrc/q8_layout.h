@@ -159,6 +159,19 @@ typedef struct {
 } Q8EltArgs;
 
 typedef struct {
+    const float *x;    /* [n][k] f32 rows */
+    const float *w;    /* [k] norm weight */
+    float *out;        /* [n][k] f32 norm, or null */
+    uint8_t *xq;       /* prepared quants (format by f16), or null */
+    float *xs;         /* prepared scales */
+    int n;
+    int rows_launched; /* n, or the token-tile boundary when quantizing (padding rows zero) */
+    int k;
+    int f16;
+    float eps;
+} Q8NormArgs;
+
+typedef struct {
     const uint8_t *src;
     uint8_t *dst;
     long long bytes;

@@ -69,6 +69,7 @@ enum Fn {
     F_QUANTIZE,
     F_GEMM_S0_T1, F_GEMM_S1_T1, F_GEMM_S1_T2, F_GEMM_S1_T4,
     F_GEMM_H_T1_R4, F_GEMM_H_T2_R2, F_GEMM_H_T2_R4,
+    F_RMSNORM,
     F_ARGMAX,
     F_SILU_MUL,
     F_COPY,
@@ -82,6 +83,7 @@ const char *const kFnNames[F_COUNT] = {
     "q8_quantize",
     "q8_gemm_s0_t1", "q8_gemm_s1_t1", "q8_gemm_s1_t2", "q8_gemm_s1_t4",
     "q8_gemm_h_t1_r4", "q8_gemm_h_t2_r2", "q8_gemm_h_t2_r4",
+    "q8_rmsnorm",
     "q8_argmax",
     "q8_silu_mul",
     "q8_copy",
@@ -118,6 +120,7 @@ struct q8_ctx {
     hipFunction_t fn[F_COUNT] = {};
     std::recursive_mutex mu;
     std::map<std::pair<uintptr_t, size_t>, q8_weight *> weights;
+    std::map<std::pair<uintptr_t, size_t>, float *> vectors;  // resident f32 norm weights, by host identity
     std::map<uintptr_t, size_t> allocs;  // buffers from q8_alloc, for span checks
     void *act_ws = nullptr;              // prepared activations
     size_t act_ws_bytes = 0;
@@ -467,6 +470,58 @@ int prepare_into(q8_ctx *c, q8_dptr x, q8_dptr gate, q8_dptr up, int n, int k, q
     return Q8_OK;
 }
 
+// Gpu::plain (cuda/mod.rs, used by rmsnorm_prepare 1414-1445): an f32 vector
+// copied to the device once, keyed by the host slice's identity (ptr, len).
+int vector_resident(q8_ctx *c, const float *host, size_t len, float **out) {
+    const auto key = std::make_pair((uintptr_t)host, len);
+    auto it = c->vectors.find(key);
+    if (it != c->vectors.end()) {
+        *out = it->second;
+        return Q8_OK;
+    }
+    float *dev = nullptr;
+    HIP_TRY(hipMalloc(reinterpret_cast<void **>(&dev), len * sizeof(float)), "hipMalloc(norm weight)");
+    hipError_t e = hipMemcpyAsync(dev, host, len * sizeof(float), hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+        hipFree(dev);
+        return hip_fail(e, "upload(norm weight)");
+    }
+    c->vectors[key] = dev;
+    *out = dev;
+    return Q8_OK;
+}
+
+// q8_rmsnorm kernel: f32 rows into `out` and/or prepared Q8_0 into `p`.
+int run_rmsnorm(q8_ctx *c, const float *x, int rows, int k, const float *w, float eps, float *out, q8_prepared *p) {
+    Q8NormArgs a{};
+    a.x = x;
+    a.w = w;
+    a.out = out;
+    a.n = rows;
+    a.rows_launched = rows;
+    a.k = k;
+    a.eps = eps;
+    if (p) {
+        const int nb = k / 32;
+        const long long ttiles = ceil_div(rows, 32);
+        const int fmt = prepared_format(c, rows);
+        const size_t qbytes = (size_t)ttiles * nb * (fmt == Q8_PREPARED_F16 ? Q8_UNIT_F16_BYTES : Q8_UNIT_BYTES);
+        const size_t sbytes = (size_t)ttiles * nb * Q8_TILE_TOKENS * sizeof(float);
+        Q8_TRY(grow(c, &c->act_ws, &c->act_ws_bytes, align_up(qbytes, kAlign) + sbytes, "hipMalloc(activation)"));
+        a.xq = static_cast<uint8_t *>(c->act_ws);
+        a.xs = reinterpret_cast<float *>(static_cast<uint8_t *>(c->act_ws) + align_up(qbytes, kAlign));
+        a.f16 = fmt == Q8_PREPARED_F16 ? 1 : 0;
+        a.rows_launched = (int)(ttiles * 32);
+        p->quants = (q8_dptr)(uintptr_t)a.xq;
+        p->scales = (q8_dptr)(uintptr_t)a.xs;
+        p->n = rows;
+        p->k = k;
+        p->format = fmt;
+    }
+    return launch(c, F_RMSNORM, (unsigned)ceil_div(a.rows_launched, 4), 256, 0, &a, sizeof a);
+}
+
 int check_k(int k) {
     if (k <= 0 || k % 32 != 0) return fail(Q8_ERR_INVALID, "Q8_0 rows are whole 32-element blocks (k = %d)", k);
     return Q8_OK;
@@ -596,6 +651,7 @@ void q8_close(q8_ctx *c) {
         hipFree(kv.second->base);
         delete kv.second;
     }
+    for (auto &kv : c->vectors) hipFree(kv.second);
     for (auto &kv : c->allocs) hipFree(reinterpret_cast<void *>(kv.first));
     if (c->act_ws) hipFree(c->act_ws);
     if (c->tmp_ws) hipFree(c->tmp_ws);
@@ -945,6 +1001,34 @@ int q8_gate_up_silu(q8_ctx *c, const q8_weight *gate, const q8_weight *up, q8_dp
     a.up = u;
     a.len = (long long)n * ffn;
     return launch(c, F_SILU_MUL, (unsigned)ceil_div(a.len, 256), 256, 0, &a, sizeof a);
+}
+
+int q8_rmsnorm(q8_ctx *c, q8_dptr x, size_t x_offset, const float *weight, int k, float eps, int rows, q8_dptr out,
+               size_t out_offset) {
+    if (!c || !weight) return fail(Q8_ERR_INVALID, "q8_rmsnorm: bad arguments");
+    Q8_TRY(check_k(k));
+    if (rows < 1) return fail(Q8_ERR_INVALID, "q8_rmsnorm: %d rows", rows);
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    const float *xp = fptr(x, x_offset);
+    float *op = fptr(out, out_offset);
+    Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)xp, (size_t)rows * k * 4, "rmsnorm x"));
+    Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)op, (size_t)rows * k * 4, "rmsnorm out"));
+    float *w = nullptr;
+    Q8_TRY(vector_resident(c, weight, (size_t)k, &w));
+    return run_rmsnorm(c, xp, rows, k, w, eps, op, nullptr);
+}
+
+int q8_norm_prepare(q8_ctx *c, q8_dptr x, size_t x_offset, const float *weight, int k, float eps, int rows,
+                    q8_prepared *prepared) {
+    if (!c || !weight || !prepared) return fail(Q8_ERR_INVALID, "q8_norm_prepare: bad arguments");
+    Q8_TRY(check_k(k));
+    Q8_TRY(check_n(rows));
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    const float *xp = fptr(x, x_offset);
+    Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)xp, (size_t)rows * k * 4, "norm_prepare x"));
+    float *w = nullptr;
+    Q8_TRY(vector_resident(c, weight, (size_t)k, &w));
+    return run_rmsnorm(c, xp, rows, k, w, eps, nullptr, prepared);
 }
 
 int q8_copy_device(q8_ctx *c, q8_dptr dst, q8_dptr src, size_t bytes) {

@@ -44,7 +44,7 @@ EXPORTS = (
     "q8_open", "q8_close", "q8_device_name", "q8_device_info", "q8_stream", "q8_set_option",
     "q8_alloc", "q8_free", "q8_upload", "q8_download", "q8_sync",
     "q8_weight_resident", "q8_weight_release", "q8_weight_shape", "q8_weight_export",
-    "q8_matmul", "q8_prepare", "q8_silu_mul_prepare", "q8_silu_mul",
+    "q8_matmul", "q8_prepare", "q8_silu_mul_prepare", "q8_rmsnorm", "q8_norm_prepare", "q8_silu_mul",
     "q8_matmul_decode_group", "q8_matmul_prompt_group", "q8_gate_up_silu",
     "q8_lm_head_argmax", "q8_argmax", "q8_copy_device",
     "q8_plan", "q8_tactic_count", "q8_tactic_row",
@@ -134,6 +134,8 @@ def lib():
         "q8_prepare": (c_int, [vp, u64, c_size, c_int, c_int, ctypes.POINTER(Prepared)]),
         "q8_silu_mul_prepare": (c_int, [vp, u64, u64, c_int, c_int, ctypes.POINTER(Prepared)]),
         "q8_silu_mul": (c_int, [vp, u64, u64, u64, c_size]),
+        "q8_rmsnorm": (c_int, [vp, u64, c_size, vp, c_int, ctypes.c_float, c_int, u64, c_size]),
+        "q8_norm_prepare": (c_int, [vp, u64, c_size, vp, c_int, ctypes.c_float, c_int, ctypes.POINTER(Prepared)]),
         "q8_matmul_decode_group": (c_int, [vp, ctypes.POINTER(_GroupEntry), c_int, u64, c_size, c_int, u64, c_size]),
         "q8_matmul_prompt_group": (c_int, [vp, ctypes.POINTER(_GroupEntry), c_int, ctypes.POINTER(Prepared),
                                            c_int, c_int, u64, c_size]),
@@ -247,6 +249,7 @@ class Gpu:
         _check(lib().q8_open(device, ctypes.byref(h)))
         self.handle = h.value
         self._resident = {}
+        self._pinned = {}  # norm weights made resident by host identity
 
     def close(self):
         if self.handle:
@@ -314,6 +317,32 @@ class Gpu:
     def silu_mul_prepare(self, gate: DeviceBuffer, up: DeviceBuffer, n: int, k: int) -> Prepared:
         p = Prepared()
         _check(lib().q8_silu_mul_prepare(self.handle, gate.ptr, up.ptr, n, k, ctypes.byref(p)))
+        return p
+
+    def _norm_weight(self, weight: np.ndarray) -> np.ndarray:
+        """The library makes a norm weight resident by its host identity
+        (pointer, length), as the reference's Gpu::plain does for its mmap'd
+        slices.  The array is pinned here for the context's lifetime, so its
+        address cannot be reused by another array while the copy is cached;
+        its contents must not change."""
+        if not (isinstance(weight, np.ndarray) and weight.dtype == np.float32 and weight.flags.c_contiguous):
+            raise TypeError("norm weight must be a C-contiguous float32 numpy array")
+        self._pinned.setdefault((weight.ctypes.data, weight.size), weight)
+        return weight
+
+    def rmsnorm(self, x: DeviceBuffer, x_offset: int, weight: np.ndarray, eps: float, rows: int,
+                out: DeviceBuffer, out_offset: int = 0):
+        """Gpu::rmsnorm_rows (compute.rs:584-614): f32 RMSNorm of `rows` rows."""
+        w = self._norm_weight(weight)
+        _check(lib().q8_rmsnorm(self.handle, x.ptr, x_offset, w.ctypes.data, w.size, float(eps), rows, out.ptr,
+                                out_offset))
+
+    def norm_prepare(self, x: DeviceBuffer, x_offset: int, weight: np.ndarray, eps: float, rows: int) -> Prepared:
+        """Gpu::rmsnorm_prepare (cuda/mod.rs:1414-1445): quantize(rmsnorm(x))."""
+        w = self._norm_weight(weight)
+        p = Prepared()
+        _check(lib().q8_norm_prepare(self.handle, x.ptr, x_offset, w.ctypes.data, w.size, float(eps), rows,
+                                     ctypes.byref(p)))
         return p
 
     def silu_mul(self, act: DeviceBuffer, gate: DeviceBuffer, up: DeviceBuffer, length: int):
@@ -459,6 +488,18 @@ class Compute:
 
     def silu_mul(self, act, gate, up, length):
         self.gpu.silu_mul(act, gate, up, length)
+
+    def rmsnorm(self, x, x_offset, weight, eps, rows, out, out_offset):
+        """compute.rs:584-614."""
+        self.gpu.rmsnorm(x, x_offset, weight, eps, rows, out, out_offset)
+
+    def norm_prepare(self, x, x_offset, weight, eps, rows, out, out_offset):
+        """compute.rs:959-984: quantized rmsnorm rows, or below the threshold
+        the f32 norm written to `out` and no prepared buffer."""
+        if rows < self.prepare_min_tokens:
+            self.gpu.rmsnorm(x, x_offset, weight, eps, rows, out, out_offset)
+            return None
+        return self.gpu.norm_prepare(x, x_offset, weight, eps, rows)
 
     def silu_mul_prepare(self, act, gate, up, n, k):
         """compute.rs:993-1019."""

@@ -571,6 +571,90 @@ def test_silu_mul_and_its_quantization(gpu, n, k):
         b.free()
 
 
+# ---------------------------------------------------------------------------
+# RMSNorm and the fused norm -> Q8_0 prepare (ops.rs:5-30, compute.rs:584-614, 959-984)
+# ---------------------------------------------------------------------------
+
+EPS = 1e-6  # configs[4]'s RMSNorm epsilon
+
+
+def norm_rows(r, rows, k):
+    x = (r.standard_normal((rows, k)) * 3.0).astype(np.float32)
+    x[0, :] = 0.0                                     # all-zero row: scale = 1 / sqrt(eps)
+    if rows > 2:
+        x[2, :] *= 1e4                                # large row
+        x[2, 7] = -3e5
+    if rows > 3:
+        x[3, :] *= 1e-5                               # tiny row (the eps term dominates)
+    w = (1.0 + 0.1 * r.standard_normal(k)).astype(np.float32)
+    return x, w
+
+
+@pytest.mark.parametrize("rows,k", [(1, 2304), (3, 32), (5, 5760), (40, 2304), (67, 64)])
+def test_rmsnorm_rows_match_the_reference_bit_for_bit(gpu, rows, k):
+    """f32 squares summed in f64, then 1 / sqrt(ms + eps) and (x * s) * w in
+    f32; the device's f64 sum is a tree, the reference's left to right, which
+    round to the same f32 mean square unless it lies within ~1e-12 of an f32
+    rounding boundary -- not the case on these seeded rows."""
+    r = rng(100 + rows + k)
+    x, w = norm_rows(r, rows, k)
+    xb, ob = gpu.alloc(4 * rows * k), gpu.alloc(4 * rows * k)
+    xb.upload(x)
+    gpu.rmsnorm(xb, 0, w, EPS, rows, ob, 0)
+    got = ob.download(np.float32, rows * k).reshape(rows, k)
+    ref = np.stack([oracle.rmsnorm(x[t], w, EPS) for t in range(rows)])
+    assert_bits(got, ref, f"rmsnorm {rows}x{k}")
+    xb.free()
+    ob.free()
+
+
+@pytest.mark.parametrize("rows,k", [(1, 2304), (2, 64), (33, 2304), (130, 5760), (512, 2304)])
+@pytest.mark.parametrize("f16", [-1, 1])
+def test_norm_prepare_is_quantize_of_rmsnorm(gpu, rows, k, f16):
+    """Gpu::rmsnorm_prepare: the quantized bytes and scales are the
+    reference's quantize_q8_0(rmsnorm(x)) exactly, padding tokens zero."""
+    gpu.set_option("gemm.f16", f16)
+    r = rng(110 + rows + k)
+    x, w = norm_rows(r, rows, k)
+    xb = gpu.alloc(4 * rows * k)
+    xb.upload(x)
+    p = gpu.norm_prepare(xb, 0, w, EPS, rows)
+    assert p.n == rows and p.k == k
+    q, sc = unpack_prepared(gpu, p, rows, k)
+    for t in range(rows):
+        rq, rs = oracle.quantize_q8_0(oracle.rmsnorm(x[t], w, EPS))
+        assert np.array_equal(q[t], rq), f"token {t}: quants differ"
+        assert np.array_equal(sc[t].view(np.uint32), rs.view(np.uint32)), f"token {t}: scales differ"
+    tt = (rows + 31) // 32
+    assert not q[rows:tt * 32].any() and not sc[rows:tt * 32].any(), "padding tokens must be zero"
+    xb.free()
+
+
+def test_norm_prepare_feeds_the_gemm_and_compute_threshold(gpu):
+    """The layer's norm -> QKV chain (model.rs:887-954): norm_prepare's
+    operand through the GEMM equals the reference's matmul of the normed rows;
+    Compute.norm_prepare below prepare_min_tokens writes the f32 norm instead."""
+    r = rng(120)
+    n, k, out = 96, 2304, 320
+    x, wn = norm_rows(r, n, k)
+    wm = weight(r, out, k)
+    xb, yb = gpu.alloc(4 * n * k), gpu.alloc(4 * n * out)
+    xb.upload(x)
+    p = gpu.norm_prepare(xb, 0, wn, EPS, n)
+    gpu.matmul(wm, xb, 0, n, yb, 0, prepared=p)
+    got = yb.download(np.float32, n * out).reshape(n, out)
+    normed = np.stack([oracle.rmsnorm(x[t], wn, EPS) for t in range(n)])
+    ref = oracle.matmul(wm.data, k, out, normed, n)
+    assert_parity(got, ref, exact_matmul(wm.data, k, out, normed, n), "norm_prepare -> gemm")
+    comp = q8.Compute(gpu)
+    ob = gpu.alloc(4 * k)
+    assert comp.norm_prepare(xb, k, wn, EPS, 1, ob, 0) is None
+    assert_bits(ob.download(np.float32, k), oracle.rmsnorm(x[1], wn, EPS), "Compute.norm_prepare n=1")
+    for b in (xb, yb, ob):
+        b.free()
+    gpu.release(wm)
+
+
 def test_lm_head_argmax(gpu):
     """lm_head 122880 x 2304 with the greedy argmax."""
     r = rng(100)
