@@ -105,6 +105,7 @@ typedef struct {
     int kslices;         /* workgroups splitting one output tile's blocks (1 = none) */
     int kwaves;          /* GEMM: waves splitting the blocks inside a workgroup */
     int rwaves;          /* f16 GEMM: row-tile waves per workgroup sharing staged activations */
+    int pipe;            /* int8 GEMM: 1 = software-pipelined kernel (MFMAs one item ahead) */
     const char *name;    /* tactic name, e.g. "matmul.gemv_f32" */
     const char *evidence;
 } q8_tactic;
@@ -133,7 +134,7 @@ void *q8_stream(q8_ctx *ctx);
 /* Tuning/testing switches; value -1 restores the tactic table's choice.
  * Names: "gemv.exact", "gemv.waves", "gemv.pairs", "gemv.slices",
  * "gemm.smode", "gemm.tpw", "gemm.twaves", "gemm.xcd_remap", "gemm.kwaves",
- * "gemm.slices", "gemm.rwaves", "gemm.f16" (0: int8 prepared activations and
+ * "gemm.slices", "gemm.rwaves", "gemm.pipe", "gemm.f16" (0: int8 prepared activations and
  * the int8-MFMA GEMM for every n; 1: f16 and the f16-MFMA GEMM for every
  * n >= 2). */
 int q8_set_option(q8_ctx *ctx, const char *name, int value);

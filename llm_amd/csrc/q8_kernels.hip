@@ -535,6 +535,37 @@ extern "C" __global__ __launch_bounds__(256) void q8_quantize(Q8QuantArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// GEMM epilogue shared by the GEMM kernels: lane (h, r) of a wave holds row o
+// = 32g + r of TPW 32 x 32 output tiles, tokens 8(i/4) + 4h + (i%4) of each.
+// The residual (bias) values are loaded first, all 16 per tile at clamped
+// addresses, so their loads are in flight together; then the stores.
+// ---------------------------------------------------------------------------
+template <int TPW>
+static __device__ __forceinline__ void store_tiles(const Q8GemmArgs &a, const Q8GemmMember &mem,
+                                                   const f32x16 (&acc)[TPW], int tt0, int o, int h) {
+    if (o >= mem.rows) return;
+#pragma unroll
+    for (int t = 0; t < TPW; t++) {
+        if (tt0 + t >= a.ttiles) continue;
+        float add[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) add[i] = 0.0f;
+        if (mem.bias) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int tok = min((tt0 + t) * Q8_TILE_TOKENS + 8 * (i >> 2) + 4 * h + (i & 3), a.n - 1);
+                add[i] = mem.bias[(size_t)tok * mem.rows + o];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int tok = (tt0 + t) * Q8_TILE_TOKENS + 8 * (i >> 2) + 4 * h + (i & 3);
+            if (tok < a.n) mem.y[(size_t)tok * mem.rows + o] = mem.bias ? acc[t][i] + add[i] : acc[t][i];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // GEMM, n >= 2 (tensor.rs:104-148 -> quant.rs:156-181).
 //
 // v_mfma_i32_32x32x32_i8 is exactly one Q8_0 block per instruction, so its
@@ -787,21 +818,7 @@ static __device__ __forceinline__ void gemm_body(const Q8GemmArgs &a) {
     }
     if (kw != 0) return;
 
-    const int o = g * Q8_TILE_ROWS + r;
-    if (o >= mem.rows) return;
-#pragma unroll
-    for (int t = 0; t < TPW; t++) {
-        if (t < ntl) {
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int tok = (tt0 + t) * Q8_TILE_TOKENS + 8 * (i >> 2) + 4 * h + (i & 3);
-                if (tok < a.n) {
-                    const size_t idx = (size_t)tok * mem.rows + o;
-                    mem.y[idx] = mem.bias ? acc[t][i] + mem.bias[idx] : acc[t][i];
-                }
-            }
-        }
-    }
+    store_tiles<TPW>(a, mem, acc, tt0, g * Q8_TILE_ROWS + r, h);
 }
 
 // ---------------------------------------------------------------------------
@@ -839,9 +856,10 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // s_waitcnt with vmcnt = n (0..63) and the other counters left free (gfx9 encoding)
 #define Q8_VMCNT_IMM(n) ((((n)&15) | (7 << 4) | (15 << 8) | ((((n) >> 4) & 3) << 14)))
 
-template <int TPW, int RW>
+template <int TPW, int RW, bool I8 = false>
 static __device__ __forceinline__ void gemm_h_body(const Q8GemmArgs &a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t hsm[];
+    constexpr int UNIT = I8 ? Q8_UNIT_BYTES : Q8_UNIT_F16_BYTES;  // activation unit in LDS and HBM
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int KW = (blockDim.x >> 6) / RW;
@@ -879,15 +897,16 @@ static __device__ __forceinline__ void gemm_h_body(const Q8GemmArgs &a) {
     // SCALE_SLOTS f32 scale slots ([TPW][2][32] used; RW > TPW waves fill the
     // rest), then per wave its two weight units and 64 f16 weight scales.
     constexpr int GLANES = RW * 64;
-    constexpr int ACT_BYTES = TPW * 2 * Q8_UNIT_F16_BYTES;
+    constexpr int ACT_BYTES = TPW * 2 * UNIT;
     constexpr int SCALE_SLOTS = (TPW * 64 > GLANES ? TPW * 64 : GLANES);
     constexpr int W_OFF = ACT_BYTES + SCALE_SLOTS * 4;
     constexpr int W_BYTES = 2 * Q8_UNIT_BYTES + 256;
     constexpr int BUF_BYTES = W_OFF + RW * W_BYTES;
-    static_assert(BUF_BYTES == Q8_GEMM_H_BUF_BYTES(TPW, RW), "host and kernel LDS layouts agree");
-    constexpr int MAXC = TPW * 256 / GLANES;             // 16-byte chunks per lane per pair
+    static_assert(BUF_BYTES == Q8_GEMM_STAGED_BUF_BYTES(TPW, RW, UNIT), "host and kernel LDS layouts agree");
+    constexpr int CPU_ = UNIT / 16;                      // 16-byte chunks per unit
+    constexpr int MAXC = TPW * 2 * CPU_ / GLANES;        // 16-byte chunks per lane per pair
     constexpr int MAXS = (TPW * 64 + GLANES - 1) / GLANES;  // scales per lane per pair
-    static_assert(TPW * 256 % GLANES == 0, "whole chunks per lane");
+    static_assert(TPW * 2 * CPU_ % GLANES == 0, "whole chunks per lane");
     constexpr int SG = MAXC + MAXS + 3;                  // loads per lane per pair (+ w0, w1, d_w)
     // at the end of iteration i: loads issued after pair i+1's
     constexpr int AFTER = (Q8_GEMM_H_STAGES - 2) * SG;
@@ -917,10 +936,10 @@ static __device__ __forceinline__ void gemm_h_body(const Q8GemmArgs &a) {
 #pragma unroll
         for (int i = 0; i < MAXC; i++) {
             const int c = wbase + i * GLANES + lane;
-            const int j = c >> 8, bb = (c >> 7) & 1;
+            const int j = c / (2 * CPU_), bb = (c / CPU_) & 1;
             const int tt = min(tt0 + j, a.ttiles - 1);
             const int b = min(2 * pc + bb, nb - 1);
-            __builtin_amdgcn_global_load_lds(a.xq + ((size_t)tt * nb + b) * Q8_UNIT_F16_BYTES + (c & 127) * 16,
+            __builtin_amdgcn_global_load_lds(a.xq + ((size_t)tt * nb + b) * UNIT + (c % CPU_) * 16,
                                              (lds_void_t *)(base + (wbase + i * GLANES) * 16), 16, 0, 0);
         }
 #pragma unroll
@@ -957,36 +976,54 @@ static __device__ __forceinline__ void gemm_h_body(const Q8GemmArgs &a) {
         stage(p_begin + it + Q8_GEMM_H_STAGES - 1, (it + Q8_GEMM_H_STAGES - 1) % Q8_GEMM_H_STAGES);
         __builtin_amdgcn_sched_barrier(0);
         const uint8_t *base = kbase + cur * BUF_BYTES;
-        // this pair's weights to f16 (lane L: bytes 0-7 for the first MFMA, 8-15 for the second)
         const uint8_t *wl = base + W_OFF + wig * W_BYTES;
         const i32x4 w0 = *(const i32x4 *)(wl + lane * 16);
         const i32x4 w1 = *(const i32x4 *)(wl + Q8_UNIT_BYTES + lane * 16);
         const unsigned dwb = *(const uint16_t *)(wl + 2 * Q8_UNIT_BYTES + lane * 2);
         const int p = p_begin + it;
         const bool dwv = p < p_end && 2 * p + h < nb;
-        const i32x4 wa0 = i8x4_to_f16x4(w0.x, w0.y), wa1 = i8x4_to_f16x4(w0.z, w0.w);
-        const i32x4 wb0 = i8x4_to_f16x4(w1.x, w1.y), wb1 = i8x4_to_f16x4(w1.z, w1.w);
         const float dwf = dwv ? f16_to_f32(dwb) : 0.0f;
+        if constexpr (I8) {
+            // int8 units: one v_mfma_i32_32x32x32_i8 per block, then convert + fma
+            const i32x16 iz = {};
 #pragma unroll
-        for (int t = 0; t < TPW; t++) {
-            const uint8_t *u0 = base + (t * 2) * Q8_UNIT_F16_BYTES + lane * 16;
-            const uint8_t *u1 = u0 + Q8_UNIT_F16_BYTES;
-            const i32x4 x00 = *(const i32x4 *)u0, x01 = *(const i32x4 *)(u0 + 1024);
-            const i32x4 x10 = *(const i32x4 *)u1, x11 = *(const i32x4 *)(u1 + 1024);
-            const float sx = ((const float *)(base + ACT_BYTES))[t * 64 + lane];
-            const f32x32 sc = __builtin_amdgcn_mfma_f32_32x32x1f32(sx, dwf, fz32, 0, 0, 0);
-            f32x16 d0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, x00),
-                                                               __builtin_bit_cast(f16x8, wa0), fz16, 0, 0, 0);
-            d0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, x01),
-                                                        __builtin_bit_cast(f16x8, wa1), d0, 0, 0, 0);
-            f32x16 d1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, x10),
-                                                               __builtin_bit_cast(f16x8, wb0), fz16, 0, 0, 0);
-            d1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, x11),
-                                                        __builtin_bit_cast(f16x8, wb1), d1, 0, 0, 0);
+            for (int t = 0; t < TPW; t++) {
+                const uint8_t *u0 = base + (t * 2) * UNIT + lane * 16;
+                const i32x4 x0 = *(const i32x4 *)u0, x1 = *(const i32x4 *)(u0 + UNIT);
+                const float sx = ((const float *)(base + ACT_BYTES))[t * 64 + lane];
+                const f32x32 sc = __builtin_amdgcn_mfma_f32_32x32x1f32(sx, dwf, fz32, 0, 0, 0);
+                const i32x16 i0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(x0, w0, iz, 0, 0, 0);
+                const i32x16 i1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(x1, w1, iz, 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < 16; i++) acc[t][i] = __builtin_fmaf(d0[i], sc[i], acc[t][i]);
+                for (int i = 0; i < 16; i++) acc[t][i] = __builtin_fmaf((float)i0[i], sc[i], acc[t][i]);
 #pragma unroll
-            for (int i = 0; i < 16; i++) acc[t][i] = __builtin_fmaf(d1[i], sc[16 + i], acc[t][i]);
+                for (int i = 0; i < 16; i++) acc[t][i] = __builtin_fmaf((float)i1[i], sc[16 + i], acc[t][i]);
+            }
+        } else {
+            // this pair's weights to f16 (lane L: bytes 0-7 for the first MFMA, 8-15 for the second)
+            const i32x4 wa0 = i8x4_to_f16x4(w0.x, w0.y), wa1 = i8x4_to_f16x4(w0.z, w0.w);
+            const i32x4 wb0 = i8x4_to_f16x4(w1.x, w1.y), wb1 = i8x4_to_f16x4(w1.z, w1.w);
+#pragma unroll
+            for (int t = 0; t < TPW; t++) {
+                const uint8_t *u0 = base + (t * 2) * UNIT + lane * 16;
+                const uint8_t *u1 = u0 + UNIT;
+                const i32x4 x00 = *(const i32x4 *)u0, x01 = *(const i32x4 *)(u0 + 1024);
+                const i32x4 x10 = *(const i32x4 *)u1, x11 = *(const i32x4 *)(u1 + 1024);
+                const float sx = ((const float *)(base + ACT_BYTES))[t * 64 + lane];
+                const f32x32 sc = __builtin_amdgcn_mfma_f32_32x32x1f32(sx, dwf, fz32, 0, 0, 0);
+                f32x16 d0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, x00),
+                                                                   __builtin_bit_cast(f16x8, wa0), fz16, 0, 0, 0);
+                d0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, x01),
+                                                            __builtin_bit_cast(f16x8, wa1), d0, 0, 0, 0);
+                f32x16 d1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, x10),
+                                                                   __builtin_bit_cast(f16x8, wb0), fz16, 0, 0, 0);
+                d1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, x11),
+                                                            __builtin_bit_cast(f16x8, wb1), d1, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 16; i++) acc[t][i] = __builtin_fmaf(d0[i], sc[i], acc[t][i]);
+#pragma unroll
+                for (int i = 0; i < 16; i++) acc[t][i] = __builtin_fmaf(d1[i], sc[16 + i], acc[t][i]);
+            }
         }
         // pair it+1 staged by every wave of the K group (and this pair's LDS reads done)
         __builtin_amdgcn_s_waitcnt(Q8_VMCNT_IMM(AFTER));
@@ -1024,21 +1061,7 @@ static __device__ __forceinline__ void gemm_h_body(const Q8GemmArgs &a) {
         }
     }
     if (kw != 0 || !row_live) return;
-    const int o = g * Q8_TILE_ROWS + r;
-    if (o >= mem.rows) return;
-#pragma unroll
-    for (int t = 0; t < TPW; t++) {
-        if (tt0 + t < a.ttiles) {
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int tok = (tt0 + t) * Q8_TILE_TOKENS + 8 * (i >> 2) + 4 * h + (i & 3);
-                if (tok < a.n) {
-                    const size_t idx = (size_t)tok * mem.rows + o;
-                    mem.y[idx] = mem.bias ? acc[t][i] + mem.bias[idx] : acc[t][i];
-                }
-            }
-        }
-    }
+    store_tiles<TPW>(a, mem, acc, tt0, g * Q8_TILE_ROWS + r, h);
 }
 
 // q8_gemm_h_t<TPW>_r<RW>: up to 512 threads (RW x KW waves).
@@ -1049,6 +1072,207 @@ static __device__ __forceinline__ void gemm_h_body(const Q8GemmArgs &a) {
 Q8_GEMM_H(1, 4)
 Q8_GEMM_H(2, 2)
 Q8_GEMM_H(2, 4)
+
+// q8_gemm_l_t<TPW>_r<RW>: the same staging with int8 activation units and the int8 MFMA.
+#define Q8_GEMM_L(TPW, RW)                                                                             \
+    extern "C" __global__ __launch_bounds__(512) void q8_gemm_l_t##TPW##_r##RW(Q8GemmArgs a) { \
+        gemm_h_body<TPW, RW, true>(a);                                                                 \
+    }
+Q8_GEMM_L(1, 2)
+Q8_GEMM_L(2, 2)
+Q8_GEMM_L(2, 4)
+
+// ---------------------------------------------------------------------------
+// The int8 GEMM, software-pipelined.  Same arithmetic and order as gemm_body
+// (SMODE 1), so the results are bit-identical; only the schedule differs.
+//
+// Work items are (block pair, token tile).  Each item's three MFMAs (the
+// scale products and the two block dots) are issued one item ahead of the
+// previous item's convert + fma epilogue, into the other of two result
+// buffers, so a wave always has VALU work that does not wait on its own
+// MFMAs; operand loads run two pairs ahead (ping-pong operand sets).  The
+// two result buffers cost ~130 VGPRs, so these kernels run two waves per
+// SIMD.  A wave rounds its pair count up to even; the extra pair, and the
+// absent second block of an odd nb, get zero scales (fma(I, 0, acc) == acc:
+// I is an exact integer and acc is never -0).  K-split waves reduce in LDS
+// as in gemm_body; no split across workgroups.
+// ---------------------------------------------------------------------------
+template <int TPW>
+struct PipeOps {
+    i32x4 w0, w1;
+    unsigned dw;
+    i32x4 x0[TPW], x1[TPW];
+    float sx[TPW];
+};
+
+struct PipeRes {
+    f32x32 sc;
+    i32x16 i0, i1;
+};
+
+template <int TPW>
+static __device__ __forceinline__ void gemm_p_body(const Q8GemmArgs &a) {
+    extern __shared__ __attribute__((aligned(16))) float psm[];  // [kwaves-1][twaves][TPW][64][16]
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int TW = a.twaves;
+    const int tw = wave % TW;
+    const int kw = wave / TW;
+    int wg = blockIdx.x;
+    if (a.xcd_remap) {
+        const int per = a.nwg >> 3;
+        wg = (wg & 7) * per + (wg >> 3);
+    }
+    const int rt = wg / a.tgroups;
+    const int tg = wg - rt * a.tgroups;
+    const int tt0 = (tg * TW + tw) * TPW;
+    const int ntl = max(0, min(TPW, a.ttiles - tt0));
+    int mi = 0;
+#pragma unroll
+    for (int i = 1; i < Q8_GROUP_MAX; i++)
+        if (i < a.members && rt >= a.m[i].tile_begin) mi = i;
+    const Q8GemmMember mem = a.m[mi];
+    const int g = rt - mem.tile_begin;
+    const int nb = a.nb;
+    const int h = lane >> 5;
+    const int r = lane & 31;
+    const uint8_t *wq = mem.quants + (size_t)g * nb * Q8_UNIT_BYTES;
+    const uint16_t *wsc = mem.scales + (size_t)g * nb * Q8_TILE_ROWS;
+    const uint8_t *xq[TPW];
+    const float *xsc[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; t++) {
+        const int ttc = min(tt0 + t, a.ttiles - 1);
+        xq[t] = a.xq + (size_t)ttc * nb * Q8_UNIT_BYTES;
+        xsc[t] = a.xs + (size_t)ttc * nb * Q8_TILE_TOKENS;
+    }
+    const int lo = lane * 16;
+    const int npairs = (nb + 1) >> 1;
+    const int p_begin = kw * a.pairs_per_wave;
+    const int p_end = ntl > 0 ? min(npairs, p_begin + a.pairs_per_wave) : p_begin;
+    const int nsteps = (max(p_end - p_begin, 0) + 1) & ~1;  // even: pairs come in (A, B) couples
+
+    f32x16 acc[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; t++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[t][i] = 0.0f;
+    const i32x16 izero = {};
+    const f32x32 fzero = {};
+
+    // operands of pair p at clamped, valid addresses; validity is applied when issued
+    auto load = [&](PipeOps<TPW> &q, int p) {
+        const int pc = min(p, npairs - 1);
+        const int b0 = 2 * pc;
+        const int b1 = min(b0 + 1, nb - 1);
+        const int bs = min(b0 + h, nb - 1);
+        q.w0 = *(const i32x4 *)(wq + (size_t)b0 * Q8_UNIT_BYTES + lo);
+        q.w1 = *(const i32x4 *)(wq + (size_t)b1 * Q8_UNIT_BYTES + lo);
+        q.dw = wsc[(size_t)bs * Q8_TILE_ROWS + r];
+#pragma unroll
+        for (int t = 0; t < TPW; t++) {
+            q.x0[t] = *(const i32x4 *)(xq[t] + (size_t)b0 * Q8_UNIT_BYTES + lo);
+            q.x1[t] = *(const i32x4 *)(xq[t] + (size_t)b1 * Q8_UNIT_BYTES + lo);
+            q.sx[t] = xsc[t][(size_t)bs * Q8_TILE_TOKENS + r];
+        }
+    };
+    // the three MFMAs of item (pair p, tile t); lanes 0-31 carry block 2p, 32-63 block 2p+1
+    auto issue = [&](const PipeOps<TPW> &q, int t, int p, PipeRes &res) {
+        const bool v = p < p_end && 2 * min(p, npairs - 1) + h < nb;
+        const float dwf = v ? f16_to_f32(q.dw) : 0.0f;
+        const float sx = v ? q.sx[t] : 0.0f;
+        res.sc = __builtin_amdgcn_mfma_f32_32x32x1f32(sx, dwf, fzero, 0, 0, 0);
+        res.i0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(q.x0[t], q.w0, izero, 0, 0, 0);
+        res.i1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(q.x1[t], q.w1, izero, 0, 0, 0);
+    };
+    auto epi = [&](const PipeRes &res, int t) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[t][i] = __builtin_fmaf((float)res.i0[i], res.sc[i], acc[t][i]);
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[t][i] = __builtin_fmaf((float)res.i1[i], res.sc[16 + i], acc[t][i]);
+    };
+
+    if (nsteps > 0) {
+        PipeOps<TPW> qa, qb;
+        PipeRes r0, r1;
+        load(qa, p_begin);
+        load(qb, p_begin + 1);
+        if constexpr (TPW == 1) {
+            // items = pairs; pair p in (qa, r0), pair p + 1 in (qb, r1)
+            for (int s = 0; s < nsteps; s += 2) {
+                const int p = p_begin + s;
+                issue(qa, 0, p, r0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (s > 0) epi(r1, 0);  // pair p - 1
+                __builtin_amdgcn_sched_barrier(0);
+                load(qa, p + 2);
+                __builtin_amdgcn_sched_barrier(0);
+                issue(qb, 0, p + 1, r1);
+                __builtin_amdgcn_sched_barrier(0);
+                epi(r0, 0);  // pair p
+                __builtin_amdgcn_sched_barrier(0);
+                load(qb, p + 3);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            epi(r1, 0);
+        } else {
+            // items (p, 0), (p, 1), (p + 1, 0), (p + 1, 1): results alternate r0 / r1
+            for (int s = 0; s < nsteps; s += 2) {
+                const int p = p_begin + s;
+                issue(qa, 0, p, r0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (s > 0) epi(r1, 1);  // (p - 1, 1)
+                __builtin_amdgcn_sched_barrier(0);
+                issue(qa, 1, p, r1);
+                __builtin_amdgcn_sched_barrier(0);
+                load(qa, p + 2);
+                __builtin_amdgcn_sched_barrier(0);
+                epi(r0, 0);  // (p, 0)
+                __builtin_amdgcn_sched_barrier(0);
+                issue(qb, 0, p + 1, r0);
+                __builtin_amdgcn_sched_barrier(0);
+                epi(r1, 1);  // (p, 1)
+                __builtin_amdgcn_sched_barrier(0);
+                issue(qb, 1, p + 1, r1);
+                __builtin_amdgcn_sched_barrier(0);
+                load(qb, p + 3);
+                __builtin_amdgcn_sched_barrier(0);
+                epi(r0, 0);  // (p + 1, 0)
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            epi(r1, 1);
+        }
+    }
+
+    const int KW = (blockDim.x >> 6) / TW;
+    if (KW > 1) {
+        if (kw > 0) {
+#pragma unroll
+            for (int t = 0; t < TPW; t++) {
+                float *dst = psm + ((size_t)(((kw - 1) * TW + tw) * TPW + t) * 64 + lane) * 16;
+#pragma unroll
+                for (int i = 0; i < 16; i += 4)
+                    *(f32x4 *)(dst + i) = (f32x4){acc[t][i], acc[t][i + 1], acc[t][i + 2], acc[t][i + 3]};
+            }
+        }
+        __syncthreads();
+        if (kw == 0) {
+            for (int k2 = 1; k2 < KW; k2++) {
+#pragma unroll
+                for (int t = 0; t < TPW; t++) {
+                    const float *src = psm + ((size_t)(((k2 - 1) * TW + tw) * TPW + t) * 64 + lane) * 16;
+#pragma unroll
+                    for (int i = 0; i < 16; i++) acc[t][i] = acc[t][i] + src[i];
+                }
+            }
+        }
+    }
+    if (kw != 0) return;
+    store_tiles<TPW>(a, mem, acc, tt0, g * Q8_TILE_ROWS + r, h);
+}
+
+extern "C" __global__ __launch_bounds__(512) void q8_gemm_p_t1(Q8GemmArgs a) { gemm_p_body<1>(a); }
+extern "C" __global__ __launch_bounds__(512) void q8_gemm_p_t2(Q8GemmArgs a) { gemm_p_body<2>(a); }
 
 extern "C" __global__ __launch_bounds__(1024) void q8_gemm_s0_t1(Q8GemmArgs a) { gemm_body<0, 1>(a); }
 extern "C" __global__ __launch_bounds__(1024) void q8_gemm_s1_t1(Q8GemmArgs a) { gemm_body<1, 1>(a); }

@@ -51,8 +51,11 @@
  * [TPW][2 blocks] f16 activation units, max(TPW, RW) * 64 f32 activation
  * scale slots, and per row wave two int8 weight units + 256 bytes of scales. */
 #define Q8_GEMM_H_STAGES 3
-#define Q8_GEMM_H_BUF_BYTES(tpw, rw) \
-    ((tpw) * 2 * Q8_UNIT_F16_BYTES + ((tpw) > (rw) ? (tpw) : (rw)) * 64 * 4 + (rw) * (2 * Q8_UNIT_BYTES + 256))
+#define Q8_GEMM_STAGED_BUF_BYTES(tpw, rw, unit) \
+    ((tpw) * 2 * (unit) + ((tpw) > (rw) ? (tpw) : (rw)) * 64 * 4 + (rw) * (2 * Q8_UNIT_BYTES + 256))
+#define Q8_GEMM_H_BUF_BYTES(tpw, rw) Q8_GEMM_STAGED_BUF_BYTES(tpw, rw, Q8_UNIT_F16_BYTES)
+/* The int8-MFMA variant of the staged GEMM (q8_gemm_l): int8 activation units. */
+#define Q8_GEMM_L_BUF_BYTES(tpw, rw) Q8_GEMM_STAGED_BUF_BYTES(tpw, rw, Q8_UNIT_BYTES)
 #define Q8_GROUP_MAX 4 /* apps/engine/src/cuda/mod.rs:63 MMA_GROUP_MAX */
 
 /* Q8_J[h][t]: the AVX2 lane held by dword t of half h. */

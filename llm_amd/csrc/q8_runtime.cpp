@@ -69,6 +69,8 @@ enum Fn {
     F_QUANTIZE,
     F_GEMM_S0_T1, F_GEMM_S1_T1, F_GEMM_S1_T2, F_GEMM_S1_T4,
     F_GEMM_H_T1_R4, F_GEMM_H_T2_R2, F_GEMM_H_T2_R4,
+    F_GEMM_P_T1, F_GEMM_P_T2,
+    F_GEMM_L_T1_R2, F_GEMM_L_T2_R2, F_GEMM_L_T2_R4,
     F_RMSNORM,
     F_ARGMAX,
     F_SILU_MUL,
@@ -83,6 +85,8 @@ const char *const kFnNames[F_COUNT] = {
     "q8_quantize",
     "q8_gemm_s0_t1", "q8_gemm_s1_t1", "q8_gemm_s1_t2", "q8_gemm_s1_t4",
     "q8_gemm_h_t1_r4", "q8_gemm_h_t2_r2", "q8_gemm_h_t2_r4",
+    "q8_gemm_p_t1", "q8_gemm_p_t2",
+    "q8_gemm_l_t1_r2", "q8_gemm_l_t2_r2", "q8_gemm_l_t2_r4",
     "q8_rmsnorm",
     "q8_argmax",
     "q8_silu_mul",
@@ -242,17 +246,44 @@ q8_tactic plan(q8_ctx *c, int n, int out, int k, int slots = 1, int fmt = -1) {
     } else {
         t.smode = option(c, "gemm.smode", t.smode) ? 1 : 0;
         t.xcd_remap = option(c, "gemm.xcd_remap", t.xcd_remap) ? 1 : 0;
+        t.pipe = option(c, "gemm.pipe", t.pipe) ? 1 : 0;
+        if (option(c, "gemm.lds", t.rwaves > 0 ? 1 : 0)) {
+            // the int8 units staged in LDS (q8_gemm_l): its own launch shape
+            q8_tactic l = t;
+            q8_gemm_staged_shape(n, out, k, c->cu_count, 1, &l);
+            const int tpw = option(c, "gemm.tpw", -1);
+            const int rw = option(c, "gemm.rwaves", -1);
+            const int kw = option(c, "gemm.kwaves", -1);
+            const int ttiles = (int)ceil_div(n, 32);
+            const int npairs = (k / 32 + 1) / 2;
+            if (tpw > 0) l.tpw = (tpw >= 2 && ttiles >= 2) ? 2 : 1;
+            if (rw > 0) l.rwaves = rw >= 4 ? 4 : 2;
+            if (l.tpw == 1) l.rwaves = 2;  // built variants: t1_r2, t2_r2, t2_r4
+            if (tpw > 0 || rw > 0 || kw > 0) {
+                int kws = kw > 0 ? kw : l.kwaves;
+                const int lds_kw = (int)(c->max_lds / ((size_t)Q8_GEMM_H_STAGES * Q8_GEMM_L_BUF_BYTES(l.tpw, l.rwaves)));
+                kws = std::max(1, std::min(std::min(std::min(kws, 8 / l.rwaves), npairs), lds_kw));
+                l.pairs_per_wave = (int)ceil_div(npairs, kws);
+                l.kwaves = (int)ceil_div(npairs, l.pairs_per_wave);
+            }
+            l.pipe = 0;
+            l.kslices = 1;
+            return l;
+        }
+        t.rwaves = 0;
         const int tpw = option(c, "gemm.tpw", -1);
         const int tw = option(c, "gemm.twaves", -1);
         const int kw = option(c, "gemm.kwaves", -1);
-        const int sl = option(c, "gemm.slices", -1);
+        int sl = option(c, "gemm.slices", -1);
         if (tpw > 0) t.tpw = (tpw >= 4) ? 4 : (tpw >= 2 ? 2 : 1);
         if (!t.smode) t.tpw = 1;  // the VALU-scale variant is built for one token tile per wave
-        if (tpw > 0 || tw > 0 || kw > 0 || sl > 0 || !t.smode) {
+        if (t.pipe && t.tpw == 4) t.tpw = 2;  // the pipelined kernel is built for one or two
+        if (tpw > 0 || tw > 0 || kw > 0 || sl > 0 || !t.smode || t.pipe) {
             const int npairs = (k / 32 + 1) / 2;
             const int ttiles = (int)ceil_div(n, 32);
             const int groups = (int)ceil_div(ttiles, t.tpw);
-            const int max_threads = t.tpw == 1 ? 1024 : 512;
+            const int max_threads = (t.tpw == 1 && !t.pipe) ? 1024 : 512;
+            if (t.pipe) sl = 1;
             int twv = tw > 0 ? tw : t.twaves;
             twv = std::max(1, std::min(twv, std::min(groups, max_threads / 64)));
             int kws = kw > 0 ? kw : t.kwaves;
@@ -344,6 +375,12 @@ int run_gemm_h(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int 
 int run_gemm(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n, const float *bias) {
     if (p->format == Q8_PREPARED_F16) return run_gemm_h(c, m, count, p, n, bias);
     if (p->format != Q8_PREPARED_I8) return fail(Q8_ERR_INVALID, "prepared activations: unknown format %d", p->format);
+    {
+        int rows_total = 0;
+        for (int i = 0; i < count; i++) rows_total += m[i].w->out;
+        const q8_tactic t = plan(c, n, rows_total, p->k, 1, Q8_PREPARED_I8);
+        if (t.rwaves > 0) return run_gemm_h(c, m, count, p, n, bias);
+    }
     const int k = p->k;
     const int nb = k / 32;
     Q8GemmArgs a{};
@@ -386,15 +423,19 @@ int run_gemm(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n,
     a.nwg = (int)nwg;
     a.xcd_remap = (t.xcd_remap && nwg % 8 == 0) ? 1 : 0;
     const int threads = 64 * a.twaves * kwaves;
-    const int max_threads = tpw == 1 ? 1024 : 512;
+    const bool pipe = t.pipe && t.smode && a.kslices == 1 && tpw <= 2;
+    const int max_threads = (tpw == 1 && !pipe) ? 1024 : 512;
     if (threads > max_threads) return fail(Q8_ERR_UNSUPPORTED, "gemm: %d threads per workgroup", threads);
     const unsigned lds = (unsigned)((kwaves - 1) * a.twaves * tpw * 64 * 16 * sizeof(float));
-    const Fn f = !t.smode ? F_GEMM_S0_T1 : tpw == 4 ? F_GEMM_S1_T4 : tpw == 2 ? F_GEMM_S1_T2 : F_GEMM_S1_T1;
+    const Fn f = pipe ? (tpw == 2 ? F_GEMM_P_T2 : F_GEMM_P_T1)
+                      : !t.smode ? F_GEMM_S0_T1 : tpw == 4 ? F_GEMM_S1_T4 : tpw == 2 ? F_GEMM_S1_T2 : F_GEMM_S1_T1;
     return launch(c, f, (unsigned)nwg, (unsigned)threads, lds, &a, sizeof a);
 }
 
-// The f16-MFMA GEMM (gemm_h_body): RW row-tile waves x KW K groups per
-// workgroup over TPW token tiles, activations staged in LDS per K group.
+// The staged GEMMs (gemm_h_body): RW row-tile waves x KW K groups per
+// workgroup over TPW token tiles, activations staged in LDS per K group;
+// f16 units on the f16 MFMA (q8_gemm_h) or int8 units on the int8 MFMA
+// (q8_gemm_l), by the prepared format.
 int run_gemm_h(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n, const float *bias) {
     const int k = p->k;
     const int nb = k / 32;
@@ -411,9 +452,10 @@ int run_gemm_h(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int 
         rt += m[i].w->tiles;
         rows_total += m[i].w->out;
     }
-    const q8_tactic t = plan(c, n, rows_total, k, 1, Q8_PREPARED_F16);
+    const bool i8 = p->format == Q8_PREPARED_I8;
+    const q8_tactic t = plan(c, n, rows_total, k, 1, p->format);
     const int tpw = t.tpw == 2 ? 2 : 1;
-    const int rw = tpw == 1 ? 4 : (t.rwaves >= 4 ? 4 : 2);
+    const int rw = tpw == 1 ? (i8 ? 2 : 4) : (t.rwaves >= 4 ? 4 : 2);
     const int kw = std::max(1, t.kwaves);
     if (rw * kw > 8) return fail(Q8_ERR_UNSUPPORTED, "gemm_h: %d x %d waves per workgroup", rw, kw);
     a.total_rtiles = rt;
@@ -434,10 +476,12 @@ int run_gemm_h(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int 
     if (nwg > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "gemm_h: grid of %lld workgroups", nwg);
     a.nwg = (int)nwg;
     a.xcd_remap = (t.xcd_remap && nwg % 8 == 0) ? 1 : 0;
-    const size_t stage = (size_t)kw * Q8_GEMM_H_STAGES * Q8_GEMM_H_BUF_BYTES(tpw, rw);
+    const size_t stage =
+        (size_t)kw * Q8_GEMM_H_STAGES * (i8 ? Q8_GEMM_L_BUF_BYTES(tpw, rw) : Q8_GEMM_H_BUF_BYTES(tpw, rw));
     const size_t reduce = (size_t)(kw - 1) * rw * tpw * 64 * 16 * sizeof(float);
     const unsigned lds = (unsigned)std::max(stage, reduce);
-    const Fn f = tpw == 1 ? F_GEMM_H_T1_R4 : rw == 4 ? F_GEMM_H_T2_R4 : F_GEMM_H_T2_R2;
+    const Fn f = i8 ? (tpw == 1 ? F_GEMM_L_T1_R2 : rw == 4 ? F_GEMM_L_T2_R4 : F_GEMM_L_T2_R2)
+                    : (tpw == 1 ? F_GEMM_H_T1_R4 : rw == 4 ? F_GEMM_H_T2_R4 : F_GEMM_H_T2_R2);
     return launch(c, f, (unsigned)nwg, (unsigned)(64 * rw * kw), lds, &a, sizeof a);
 }
 
@@ -687,7 +731,8 @@ int q8_set_option(q8_ctx *c, const char *name, int value) {
     if (!c || !name) return fail(Q8_ERR_INVALID, "q8_set_option: bad arguments");
     static const char *const known[] = {"gemv.exact", "gemv.waves",  "gemv.pairs",     "gemv.slices",
                                         "gemm.smode", "gemm.tpw",    "gemm.twaves",    "gemm.xcd_remap",
-                                        "gemm.kwaves", "gemm.slices", "gemm.rwaves",    "gemm.f16"};
+                                        "gemm.kwaves", "gemm.slices", "gemm.rwaves",    "gemm.f16",
+                                        "gemm.pipe",  "gemm.lds"};
     bool ok = false;
     for (const char *k : known) ok = ok || std::strcmp(k, name) == 0;
     if (!ok) return fail(Q8_ERR_INVALID, "unknown option %s", name);

@@ -20,6 +20,13 @@ const Q8TacticRow kRows[] = {
      "path on the VALU; bit-identical to the int8 kernel.  Measured slower so far (gate|up n=512 70 us "
      "vs 50 us): one wave per row tile reads 2 KB of f16 activations per block-tile from LDS, about "
      "150 B/clk per CU at the MFMA rate, above the LDS bandwidth; option gemm.f16 = 1 selects it"},
+    {"matmul.gemm_mfma_i8_pipelined", Q8_KERNEL_GEMM, 2, Q8_MAX_TOKENS, Q8_MATURITY_REJECTED, 0,
+     "each item's MFMAs issued one item ahead of the previous epilogue (option gemm.pipe): two result "
+     "buffers cost ~130 VGPRs, two waves per SIMD instead of three; gate|up n=512 57 us vs 51 us"},
+    {"matmul.gemm_mfma_i8_lds_staged", Q8_KERNEL_GEMM, 2, Q8_MAX_TOKENS, Q8_MATURITY_REJECTED, 0,
+     "int8 activations staged once per workgroup in LDS with global_load_lds and shared by row-tile "
+     "waves (option gemm.lds), cutting L2 reads (the plain kernel keeps the L2 79% busy): one "
+     "workgroup barrier per block pair costs more; gate|up n=512 56 us vs 51 us"},
     {"matmul.gemm_f32_small_n", Q8_KERNEL_GEMM, 2, 7, Q8_MATURITY_REJECTED, 0,
      "the reference GPU's f32-activation path for 2 <= n <= 7 (cuda/mod.rs:883-891) disagrees with "
      "the CPU kernels that define parity, which quantize for every n >= 2"},
@@ -109,6 +116,10 @@ void q8_gemm_shape(int n, int out, int k, int cu_count, q8_tactic *t) {
 // the (RW, KW) whose last round of waves is fullest, discounted for the fixed
 // per-wave cost (about two block pairs of prologue, drain and K reduction).
 void q8_gemm_h_shape(int n, int out, int k, int cu_count, q8_tactic *t) {
+    q8_gemm_staged_shape(n, out, k, cu_count, 0, t);
+}
+
+void q8_gemm_staged_shape(int n, int out, int k, int cu_count, int i8, q8_tactic *t) {
     const int nb = k / 32;
     const int npairs = ceil_div(nb, 2);
     const int ttiles = ceil_div(n, 32);
@@ -116,12 +127,13 @@ void q8_gemm_h_shape(int n, int out, int k, int cu_count, q8_tactic *t) {
     const double cap = 2.0 * 4.0 * std::max(cu_count, 1);
     const int tpw = ttiles >= 2 ? 2 : 1;
     double best = -1.0;
-    int best_rw = 4, best_kw = 1;
+    int best_rw = (tpw == 1 && i8) ? 2 : 4, best_kw = 1;
     for (int rw : {2, 4}) {
-        if (tpw == 1 && rw != 4) continue;  // built variants: t1_r4, t2_r2, t2_r4
+        if (tpw == 1 && rw != (i8 ? 2 : 4)) continue;  // built: f16 t1_r4, t2_r2, t2_r4; int8 t1_r2, t2_r2, t2_r4
         for (int kw = 1; rw * kw <= 8 && kw <= npairs; kw++) {
             // LDS: KW K groups x the staging ring, within 64 KB
-            const long long lds = (long long)kw * Q8_GEMM_H_STAGES * Q8_GEMM_H_BUF_BYTES(tpw, rw);
+            const long long lds =
+                (long long)kw * Q8_GEMM_H_STAGES * (i8 ? Q8_GEMM_L_BUF_BYTES(tpw, rw) : Q8_GEMM_H_BUF_BYTES(tpw, rw));
             if (lds > 65536) continue;
             const int ppw = ceil_div(npairs, kw);
             if (ceil_div(npairs, ppw) != kw) continue;  // no K wave without pairs

@@ -29,6 +29,8 @@ int q8_tactics_choose(int n, int out, int k, int cu_count, q8_tactic *t);
 void q8_gemv_shape(int out, int k, int cu_count, int slots, q8_tactic *t);
 void q8_gemm_shape(int n, int out, int k, int cu_count, q8_tactic *t);
 void q8_gemm_h_shape(int n, int out, int k, int cu_count, q8_tactic *t);
+/* Staged GEMM launch shape (RW, KW, TPW) for f16 (i8 = 0) or int8 (i8 = 1) activation units. */
+void q8_gemm_staged_shape(int n, int out, int k, int cu_count, int i8, q8_tactic *t);
 /* The prepared-activation format the table's choice for n consumes
  * (Q8_PREPARED_I8 or Q8_PREPARED_F16): it depends on n only. */
 int q8_tactics_prepared_format(int n);

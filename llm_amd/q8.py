@@ -85,7 +85,8 @@ class Tactic(ctypes.Structure):
                 ("exact", ctypes.c_int), ("tpw", ctypes.c_int), ("twaves", ctypes.c_int),
                 ("smode", ctypes.c_int),
                 ("xcd_remap", ctypes.c_int), ("kslices", ctypes.c_int), ("kwaves", ctypes.c_int),
-                ("rwaves", ctypes.c_int), ("name", ctypes.c_char_p), ("evidence", ctypes.c_char_p)]
+                ("rwaves", ctypes.c_int), ("pipe", ctypes.c_int),
+                ("name", ctypes.c_char_p), ("evidence", ctypes.c_char_p)]
 
     def as_dict(self) -> dict:
         d = {f: getattr(self, f) for f, _ in self._fields_}
