@@ -183,6 +183,30 @@ static __device__ __forceinline__ float chain_sum(const float *v, int count) {
     return acc;
 }
 
+// Cross-workgroup partials: agent-scope (all XCDs) relaxed atomic stores and
+// loads, i.e. global_store/global_load with sc1.
+static __device__ __forceinline__ void store_agent(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+static __device__ __forceinline__ float load_agent(const float *p) {
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// chain_sum over cross-workgroup partials (agent-scope loads).
+static __device__ __forceinline__ float chain_sum_agent(const float *v, int count) {
+    float acc = 0.0f;
+    int b = 0;
+    for (; b + 8 <= count; b += 8) {
+        float t[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) t[u] = load_agent(v + (b + u) * 32);
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc = acc + t[u];
+    }
+    for (; b < count; b++) acc = acc + load_agent(v + b * 32);
+    return acc;
+}
+
 // Left-to-right sum of row[0..count) (16-byte aligned, zero from count up to
 // the next multiple of four), read as float4s eight at a time ahead of their
 // adds.  The zeros change nothing: the sum starts at +0.0, so it is never
@@ -347,7 +371,7 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
                 if (S == 1) {
                     *(ok ? vbuf + (slot * 32 + r) * vrow + blk : pad) = v;
                 } else if (ok) {
-                    gbuf[((size_t)(slot * a.total_tiles + gtile) * nb + blk) * 32 + r] = v;
+                    store_agent(gbuf + ((size_t)(slot * a.total_tiles + gtile) * nb + blk) * 32 + r, v);
                 }
             } else {
                 total = ok ? total + v : total;
@@ -376,10 +400,14 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
         if (!EXACT && w == 0 && lane < 32) {
             float acc = 0.0f;
             for (int ww = 0; ww < W; ww++) acc = acc + vbuf[(slot * W + ww) * 32 + r];
-            gbuf[((size_t)(slot * a.total_tiles + gtile) * S + slice) * 32 + r] = acc;
+            store_agent(gbuf + ((size_t)(slot * a.total_tiles + gtile) * S + slice) * 32 + r, acc);
         }
-        // The last workgroup of the tile to arrive finishes it.
-        __threadfence();
+        // The last workgroup of the tile to arrive finishes it.  The partials
+        // travel as agent-scope atomic stores and loads (coherent across the
+        // XCDs' L2s without writing back or invalidating whole caches, which
+        // __threadfence does); each wave waits for its stores to complete
+        // before the workgroup's arrival is counted.
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         if (threadIdx.x == 0) {
             const unsigned old = atomicAdd(&a.counters[gtile], 1u);
@@ -387,8 +415,7 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
         }
         __syncthreads();
         if (!last_flag) return;
-        __threadfence();
-        if (threadIdx.x == 0) a.counters[gtile] = 0u;  // ready for the next launch
+        if (threadIdx.x == 0) __hip_atomic_store(&a.counters[gtile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (wave != 0 || lane >= 32) return;
 
@@ -406,7 +433,8 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
                 }
             } else {
                 const size_t base = (size_t)(sl * a.total_tiles + gtile);
-                acc = EXACT ? chain_sum(gbuf + base * nb * 32 + r, nb) : chain_sum(gbuf + base * S * 32 + r, S);
+                acc = EXACT ? chain_sum_agent(gbuf + base * nb * 32 + r, nb)
+                            : chain_sum_agent(gbuf + base * S * 32 + r, S);
             }
             sums[sl] = acc;
         }
