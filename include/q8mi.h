@@ -54,6 +54,9 @@ enum {
     Q8_ERR_UNSUPPORTED = 3,   /* EngineError::Unsupported (e.g. n above the prompt limit) */
     Q8_ERR_NO_DEVICE = 4,     /* no gfx950 device / code object does not load */
     Q8_ERR_OUT_OF_MEMORY = 5, /* device allocation failed */
+    Q8_ERR_FORMAT = 6,        /* EngineError::Format: malformed GGUF (include/q8gguf.h) */
+    Q8_ERR_MISSING = 7,       /* EngineError::MissingTensor / MissingMetadata */
+    Q8_ERR_IO = 8,            /* EngineError::Io: the file cannot be opened or mapped */
 };
 
 /* Largest prompt one matmul takes: MMA_TOKENS (cuda/mod.rs:115). */
@@ -235,6 +238,18 @@ int q8_copy_device(q8_ctx *ctx, q8_dptr dst, q8_dptr src, size_t bytes);
 
 /* Greedy argmax of len f32 values on the device (sampler.rs:167-175). */
 int q8_argmax(q8_ctx *ctx, q8_dptr values, size_t offset, size_t len, uint32_t *argmax);
+
+/* Embedding lookup: the rows of `weight` (k = embedding width, out = vocabulary)
+ * named by the host token ids, dequantized (d * q, as dequant_q8_0,
+ * quant.rs:184-203) into out[out_offset + t*k ...] for t < n, in one launch
+ * over the resident device copy.  Replaces Gpu::embeddings (cuda/mod.rs:
+ * 1690-1716, kernel embedding_rows gpu.cu:1754-1766) with the vocabulary check
+ * of the caller (model.rs:741-751): an id >= out is Q8_ERR_INVALID and nothing
+ * is launched.  The ids are copied to a device buffer of the context and the
+ * call waits for that copy (cuda/mod.rs:540-552), so `tokens` may be reused on
+ * return. */
+int q8_embeddings(q8_ctx *ctx, const q8_weight *weight, const uint32_t *tokens, size_t n, q8_dptr out,
+                  size_t out_offset);
 
 /* ---- tactics: the shape-keyed plan (tactics.rs:229-347, for gfx950) ---- */
 

@@ -1,0 +1,11 @@
+// q8_internal.h -- declarations shared by the host sources of libq8mi.so.
+// Nothing here is part of the C-ABI (hidden, C++ linkage).
+#ifndef Q8_INTERNAL_H
+#define Q8_INTERNAL_H
+
+namespace q8i {
+// Record `fmt` as the calling thread's q8_last_error() message; returns code.
+__attribute__((visibility("hidden"), format(printf, 2, 3))) int set_error(int code, const char *fmt, ...);
+}  // namespace q8i
+
+#endif

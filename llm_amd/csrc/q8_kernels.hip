@@ -1384,7 +1384,39 @@ extern "C" __global__ __launch_bounds__(256) void q8_copy(Q8CopyArgs a) {
     for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
 }
 
-// act[i] = silu(gate[i]) * up[i]   (compute.rs:940-944)
+// ---------------------------------------------------------------------------
+// Embedding rows out of the resident tile layout (gpu.cu embedding_rows
+// 1754-1766; dequant_q8_0, quant.rs:184-203): out[t][32b + e] = d * q, one f32
+// product, as the reference computes it.
+//
+// One thread per (token, block, half h): its 16-byte lane segment of the unit
+// holds, in dword j, elements 8c + Q8_J[h][j] for bytes c = 0..3.  Dwords 0
+// and 2 carry AVX2 lanes 2h and 2h+1, dwords 1 and 3 lanes 4+2h and 5+2h, so
+// each chunk c yields two adjacent f32 pairs.
+// ---------------------------------------------------------------------------
+extern "C" __global__ __launch_bounds__(256) void q8_embed(Q8EmbedArgs a) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;  // < 2^31: the host checks
+    const int per_token = a.nb * 2;
+    if (idx >= a.n * per_token) return;
+    const int t = idx / per_token;
+    const int rem = idx - t * per_token;
+    const int b = rem >> 1;
+    const int h = rem & 1;
+    const unsigned row = a.tokens[t];
+    const size_t unit = (size_t)(row / Q8_TILE_ROWS) * a.nb + b;
+    const unsigned r = row % Q8_TILE_ROWS;
+    const i32x4 q = *(const i32x4 *)(a.quants + unit * Q8_UNIT_BYTES + 16 * (32 * h + r));
+    const float d = f16_to_f32(a.scales[unit * Q8_TILE_ROWS + r]);
+    float *o = a.out + (size_t)t * a.nb * Q8_BLOCK_ELEMS + b * Q8_BLOCK_ELEMS + 2 * h;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const float2 lo = {d * (float)(signed char)(q[0] >> (8 * c)), d * (float)(signed char)(q[2] >> (8 * c))};
+        const float2 hi = {d * (float)(signed char)(q[1] >> (8 * c)), d * (float)(signed char)(q[3] >> (8 * c))};
+        *(float2 *)(o + 8 * c) = lo;
+        *(float2 *)(o + 8 * c + 4) = hi;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // RMSNorm (ops.rs:5-30), as f32 rows and/or straight into prepared Q8_0
 // activations (compute.rs:959-984 norm_prepare; gpu.cu rmsnorm_quantize_rows

@@ -87,6 +87,15 @@ typedef struct {
 } Q8RepackArgs;
 
 typedef struct {
+    const uint8_t *quants;   /* resident weight, tile layout */
+    const uint16_t *scales;
+    const uint32_t *tokens;  /* n row ids, each < the weight's rows (checked on the host) */
+    float *out;              /* n rows of nb*32 f32 */
+    int n;
+    int nb;
+} Q8EmbedArgs;
+
+typedef struct {
     const uint8_t *quants;
     const uint16_t *scales;
     float *y;          /* rows f32 (n = 1) */

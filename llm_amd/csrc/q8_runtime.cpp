@@ -25,6 +25,7 @@
 #include <vector>
 
 #include "../../include/q8mi.h"
+#include "q8_internal.h"
 #include "q8_layout.h"
 #include "q8_manifest.h"
 #include "q8_tactics.h"
@@ -75,6 +76,7 @@ enum Fn {
     F_ARGMAX,
     F_SILU_MUL,
     F_COPY,
+    F_EMBED,
     F_COUNT
 };
 
@@ -91,6 +93,7 @@ const char *const kFnNames[F_COUNT] = {
     "q8_argmax",
     "q8_silu_mul",
     "q8_copy",
+    "q8_embed",
 };
 
 constexpr int kArgmaxParts = 1024;
@@ -133,6 +136,8 @@ struct q8_ctx {
     void *argmax_ws = nullptr;           // per-workgroup partials + result
     float *split_ws = nullptr;           // partial results of split-K workgroups
     unsigned *counters = nullptr;        // split-K arrival counters (kernels reset them to 0)
+    void *token_ws = nullptr;            // token ids of the embedding lookup
+    size_t token_ws_bytes = 0;
     int cu_count = 0;
     size_t total_mem = 0;
     size_t max_lds = 0;
@@ -611,6 +616,18 @@ int argmax_into(q8_ctx *c, q8_dptr values, size_t len, uint32_t *out) {
 
 }  // namespace
 
+namespace q8i {
+int set_error(int code, const char *fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+}  // namespace q8i
+
 // ===========================================================================
 // C-ABI
 // ===========================================================================
@@ -624,6 +641,9 @@ const char *q8_status_string(int status) {
         case Q8_ERR_UNSUPPORTED: return "unsupported";
         case Q8_ERR_NO_DEVICE: return "no device";
         case Q8_ERR_OUT_OF_MEMORY: return "out of device memory";
+        case Q8_ERR_FORMAT: return "malformed gguf";
+        case Q8_ERR_MISSING: return "missing tensor or metadata key";
+        case Q8_ERR_IO: return "io error";
         default: return "unknown status";
     }
 }
@@ -702,6 +722,7 @@ void q8_close(q8_ctx *c) {
     if (c->argmax_ws) hipFree(c->argmax_ws);
     if (c->split_ws) hipFree(c->split_ws);
     if (c->counters) hipFree(c->counters);
+    if (c->token_ws) hipFree(c->token_ws);
     if (c->module) hipModuleUnload(c->module);
     if (c->stream) hipStreamDestroy(c->stream);
     delete c;
@@ -1100,6 +1121,32 @@ int q8_lm_head_argmax(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset,
     q8_group_entry e{w, logits, logits_offset};
     Q8_TRY(q8_matmul_decode_group(c, &e, 1, x, x_offset, w->k, 0, 0));
     return argmax_into(c, (q8_dptr)(uintptr_t)fptr(logits, logits_offset), (size_t)w->out, argmax);
+}
+
+int q8_embeddings(q8_ctx *c, const q8_weight *w, const uint32_t *tokens, size_t n, q8_dptr out,
+                  size_t out_offset) {
+    if (!c) return fail(Q8_ERR_INVALID, "q8_embeddings: null context");
+    Q8_TRY(check_weight(c, w));
+    if (n == 0) return Q8_OK;
+    if (!tokens) return fail(Q8_ERR_INVALID, "q8_embeddings: null token ids");
+    for (size_t i = 0; i < n; i++)
+        if (tokens[i] >= (uint32_t)w->out) return fail(Q8_ERR_INVALID, "token %u outside vocabulary", tokens[i]);
+    const long long threads = (long long)n * w->nb * 2;
+    if (threads > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "embedding of %zu tokens is too large", n);
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    Q8_TRY(check_span(c, out, ((size_t)out_offset + n * (size_t)w->k) * sizeof(float), "embedding output"));
+    Q8_TRY(grow(c, &c->token_ws, &c->token_ws_bytes, n * sizeof(uint32_t), "hipMalloc(token ids)"));
+    HIP_TRY(hipMemcpyAsync(c->token_ws, tokens, n * sizeof(uint32_t), hipMemcpyHostToDevice, c->stream),
+            "hipMemcpyAsync(token ids)");
+    HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    Q8EmbedArgs a{};
+    a.quants = w->quants;
+    a.scales = w->scales;
+    a.tokens = static_cast<const uint32_t *>(c->token_ws);
+    a.out = fptr(out, out_offset);
+    a.n = (int)n;
+    a.nb = w->nb;
+    return launch(c, F_EMBED, (unsigned)ceil_div(threads, 256), 256, 0, &a, sizeof a);
 }
 
 int q8_argmax(q8_ctx *c, q8_dptr values, size_t offset, size_t len, uint32_t *argmax) {

@@ -30,15 +30,16 @@ Q8_ERR_INVALID = 2
 Q8_ERR_UNSUPPORTED = 3
 Q8_ERR_NO_DEVICE = 4
 Q8_ERR_OUT_OF_MEMORY = 5
+Q8_ERR_FORMAT = 6
+Q8_ERR_MISSING = 7
+Q8_ERR_IO = 8
 MAX_TOKENS = 1024
 GROUP_MAX = 4
 KERNEL_GEMV, KERNEL_GEMM, KERNEL_GEMM_F16 = 1, 2, 3
 PREPARED_I8, PREPARED_F16 = 0, 1
-KERNEL_GEMV = 1
-KERNEL_GEMM = 2
 
-# Every function include/q8mi.h declares (the ABI test checks the header
-# against this list and the library's exports).
+# Every function include/q8mi.h and include/q8gguf.h declare (the ABI test
+# checks the headers against this list and the library's exports).
 EXPORTS = (
     "q8_status_string", "q8_last_error", "q8_build_info",
     "q8_open", "q8_close", "q8_device_name", "q8_device_info", "q8_stream", "q8_set_option",
@@ -46,10 +47,14 @@ EXPORTS = (
     "q8_weight_resident", "q8_weight_release", "q8_weight_shape", "q8_weight_export",
     "q8_matmul", "q8_prepare", "q8_silu_mul_prepare", "q8_rmsnorm", "q8_norm_prepare", "q8_silu_mul",
     "q8_matmul_decode_group", "q8_matmul_prompt_group", "q8_gate_up_silu",
-    "q8_lm_head_argmax", "q8_argmax", "q8_copy_device",
+    "q8_lm_head_argmax", "q8_argmax", "q8_copy_device", "q8_embeddings",
     "q8_plan", "q8_tactic_count", "q8_tactic_row",
     "q8_event_create", "q8_event_record", "q8_event_elapsed_ms", "q8_event_destroy",
     "q8_graph_begin", "q8_graph_end", "q8_graph_launch", "q8_graph_destroy",
+    "q8_gguf_open", "q8_gguf_close", "q8_gguf_layout", "q8_gguf_tensor_count", "q8_gguf_tensor_at",
+    "q8_gguf_tensor", "q8_gguf_meta_count", "q8_gguf_meta_key_at", "q8_gguf_meta_type", "q8_gguf_meta_u64",
+    "q8_gguf_meta_f32", "q8_gguf_meta_bool", "q8_gguf_meta_str", "q8_gguf_has_key_prefix",
+    "q8_gguf_meta_i32_array", "q8_gguf_meta_f32_array", "q8_gguf_meta_str_array", "q8_gguf_weight",
 )
 
 
@@ -73,6 +78,14 @@ class Prepared(ctypes.Structure):
 
     def scale_bytes(self) -> int:
         return (self.n + 31) // 32 * (self.k // 32) * 32 * 4
+
+
+class GgufTensorInfo(ctypes.Structure):
+    """q8_gguf_tensor_info (include/q8gguf.h)."""
+    _fields_ = [("name", ctypes.c_char_p), ("name_len", ctypes.c_uint64), ("n_dims", ctypes.c_uint32),
+                ("dims", ctypes.POINTER(ctypes.c_uint64)), ("dtype", ctypes.c_uint32),
+                ("offset", ctypes.c_uint64), ("byte_len", ctypes.c_uint64), ("elements", ctypes.c_uint64),
+                ("data", ctypes.c_void_p)]
 
 
 class _GroupEntry(ctypes.Structure):
@@ -144,6 +157,7 @@ def lib():
         "q8_lm_head_argmax": (c_int, [vp, vp, u64, c_size, u64, c_size, ctypes.POINTER(ctypes.c_uint32)]),
         "q8_argmax": (c_int, [vp, u64, c_size, c_size, ctypes.POINTER(ctypes.c_uint32)]),
         "q8_copy_device": (c_int, [vp, u64, u64, c_size]),
+        "q8_embeddings": (c_int, [vp, vp, ctypes.POINTER(ctypes.c_uint32), c_size, u64, c_size]),
         "q8_plan": (c_int, [vp, c_int, c_int, c_int, ctypes.POINTER(Tactic)]),
         "q8_tactic_count": (c_int, []),
         "q8_tactic_row": (c_int, [c_int, ctypes.POINTER(Tactic), ctypes.POINTER(c_int), ctypes.POINTER(c_int)]),
@@ -155,6 +169,27 @@ def lib():
         "q8_graph_end": (c_int, [vp, ctypes.POINTER(vp)]),
         "q8_graph_launch": (c_int, [vp, vp]),
         "q8_graph_destroy": (c_int, [vp]),
+        "q8_gguf_open": (c_int, [ctypes.c_char_p, ctypes.POINTER(vp)]),
+        "q8_gguf_close": (None, [vp]),
+        "q8_gguf_layout": (c_int, [vp, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(u64), ctypes.POINTER(u64),
+                                   ctypes.POINTER(u64)]),
+        "q8_gguf_tensor_count": (c_int, [vp, ctypes.POINTER(u64)]),
+        "q8_gguf_tensor_at": (c_int, [vp, u64, ctypes.POINTER(GgufTensorInfo)]),
+        "q8_gguf_tensor": (c_int, [vp, ctypes.c_char_p, ctypes.POINTER(GgufTensorInfo)]),
+        "q8_gguf_meta_count": (c_int, [vp, ctypes.POINTER(u64)]),
+        "q8_gguf_meta_key_at": (c_int, [vp, u64, ctypes.POINTER(ctypes.c_char_p)]),
+        "q8_gguf_meta_type": (c_int, [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint32),
+                                      ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(u64)]),
+        "q8_gguf_meta_u64": (c_int, [vp, ctypes.c_char_p, ctypes.POINTER(u64)]),
+        "q8_gguf_meta_f32": (c_int, [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_float)]),
+        "q8_gguf_meta_bool": (c_int, [vp, ctypes.c_char_p, ctypes.POINTER(c_int)]),
+        "q8_gguf_meta_str": (c_int, [vp, ctypes.c_char_p, ctypes.POINTER(vp), ctypes.POINTER(u64)]),
+        "q8_gguf_has_key_prefix": (c_int, [vp, ctypes.c_char_p]),
+        "q8_gguf_meta_i32_array": (c_int, [vp, ctypes.c_char_p, vp, u64, ctypes.POINTER(u64)]),
+        "q8_gguf_meta_f32_array": (c_int, [vp, ctypes.c_char_p, vp, u64, ctypes.POINTER(u64)]),
+        "q8_gguf_meta_str_array": (c_int, [vp, ctypes.c_char_p, ctypes.POINTER(vp), ctypes.POINTER(u64), u64,
+                                           ctypes.POINTER(u64)]),
+        "q8_gguf_weight": (c_int, [vp, vp, ctypes.c_char_p, c_int, c_int, ctypes.POINTER(vp)]),
     }
     assert set(sig) == set(EXPORTS)
     for name, (res, args) in sig.items():
@@ -383,6 +418,27 @@ class Gpu:
                                        logits_offset, ctypes.byref(out)))
         return int(out.value)
 
+    def embeddings(self, weight: Weight, tokens, out: DeviceBuffer, out_offset: int = 0):
+        """Gpu::embeddings (cuda/mod.rs:1690-1716): rows `tokens` of the
+        resident weight, dequantized into out[out_offset:]."""
+        ids = np.ascontiguousarray(np.asarray(tokens, dtype=np.int64))
+        if ids.size and (ids.min() < 0 or ids.max() > 0xFFFFFFFF):
+            raise Q8Error(Q8_ERR_INVALID, "token ids are u32")
+        ids = ids.astype(np.uint32)
+        _check(lib().q8_embeddings(self.handle, self.resident(weight),
+                                   ids.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), ids.size, out.ptr,
+                                   out_offset))
+
+    def gguf_weight(self, gguf, name: str, k: int, out: int):
+        """q8_gguf_weight: the shape-checked Q8_0 tensor of an open GgufFile
+        made resident straight from the map.  The file is kept open while the
+        context may use the weight."""
+        h = ctypes.c_void_p()
+        _check(lib().q8_gguf_weight(self.handle, gguf.handle, name.encode(), k, out, ctypes.byref(h)))
+        info = gguf.tensor(name)
+        self._resident[(gguf.data_address(name), info.byte_len)] = gguf
+        return h.value
+
     def argmax(self, values: DeviceBuffer, offset: int, length: int) -> int:
         out = ctypes.c_uint32()
         _check(lib().q8_argmax(self.handle, values.ptr, offset, length, ctypes.byref(out)))
@@ -489,6 +545,10 @@ class Compute:
 
     def silu_mul(self, act, gate, up, length):
         self.gpu.silu_mul(act, gate, up, length)
+
+    def embeddings(self, weight, tokens, out, out_offset):
+        """compute.rs:346-371 (device branch): the embedding rows of `tokens`."""
+        self.gpu.embeddings(weight, tokens, out, out_offset)
 
     def rmsnorm(self, x, x_offset, weight, eps, rows, out, out_offset):
         """compute.rs:584-614."""
