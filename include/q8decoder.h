@@ -1,0 +1,118 @@
+/*
+ * q8decoder.h -- the decoder around the Q8_0 matmul path of libq8mi.so: the
+ * support operations a llama-style decoder step needs beside the matmuls
+ * (rotary embedding into an f16 KV cache, attention, device-side token
+ * feedback) and a synthetic decoder that runs them with the matmuls in situ.
+ *
+ * Positions are read from device memory (an int the caller allocates with
+ * q8_alloc), so a captured step replays at any position, as the reference's
+ * captured decode steps do (model.rs:676-731: "only the position changes, and
+ * the kernels read that from device memory").
+ */
+#ifndef Q8DECODER_H
+#define Q8DECODER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "q8mi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- support operations ---- */
+
+/* Rotary embedding and KV append: Compute::rope_append (compute.rs:743-797),
+ * kernel rope_append (gpu.cu:525-581) with the host path's semantics
+ * (ops.rs:152-166 rotation of consecutive pairs, kv_append copying every
+ * dimension).  q [n][n_head][head_dim] is rotated in place; k [n][n_kv][head_dim]
+ * rotated and v [n][n_kv*head_dim] copied are rounded to f16 into the caches
+ * (f16 [capacity][n_kv*head_dim]) at rows *position + t.  Pairs i < n_rot/2
+ * rotate by position * base^(-2i/n_rot); the others are copied.  Rows at or
+ * beyond `capacity` are not written (the caller checks the context first). */
+int q8_rope_append(q8_ctx *ctx, q8_dptr q, size_t q_offset, q8_dptr k, size_t k_offset, q8_dptr v,
+                   size_t v_offset, q8_dptr kcache, q8_dptr vcache, int n, int n_head, int n_kv, int head_dim,
+                   int n_rot, float base, int capacity, q8_dptr position);
+
+/* Causal attention of n query rows at cache positions *position + t, each
+ * seeing cache rows 0 ..= its own position: Compute::attend (compute.rs,
+ * attend_host 1075-1126 semantics: scores = dot(q, k) * scale, softmax, sum of
+ * weighted values), with f16 keys and values as the reference's device cache.
+ * n == 1 runs the split decode kernel (attention_split + attention_combine,
+ * gpu.cu:649-762) over `splits` workgroups per head; n > 1 the tiled prefill
+ * kernel (`splits` ignored).  head_dim must be 64; n_head a multiple of n_kv. */
+int q8_attention(q8_ctx *ctx, q8_dptr q, size_t q_offset, q8_dptr kcache, q8_dptr vcache, q8_dptr out,
+                 size_t out_offset, int n, int n_head, int n_kv, int head_dim, int capacity, float scale,
+                 q8_dptr position, int splits);
+
+/* q8_embeddings with the token ids already in device memory (u32), so the
+ * lookup can sit inside a captured step.  An id >= the vocabulary yields a
+ * zero row (the host-side check of q8_embeddings cannot run here). */
+int q8_embeddings_device(q8_ctx *ctx, const q8_weight *weight, q8_dptr tokens, size_t n, q8_dptr out,
+                         size_t out_offset);
+
+/* q8_argmax writing the index to device memory (u32 at `result`) instead of
+ * returning it: the greedy token fed back to the next step on the device. */
+int q8_argmax_device(q8_ctx *ctx, q8_dptr values, size_t offset, size_t len, q8_dptr result);
+
+/* *position += by, on the device (the end of a captured step). */
+int q8_advance_position(q8_ctx *ctx, q8_dptr position, int by);
+
+/* A random-init out x k Q8_0 weight generated on the device from `seed`
+ * (quants uniform in [-127, 127], scales f16(|N(0, scale_std)| / 127)),
+ * owned by the context until q8_weight_release or q8_close.  No counterpart in
+ * the reference, whose weights always come from a GGUF; q8_weight_export reads
+ * it back for the CPU checks. */
+int q8_weight_synthetic(q8_ctx *ctx, int k, int out, uint64_t seed, float scale_std, const q8_weight **weight);
+
+/* ---- the synthetic decoder ---- */
+
+typedef struct q8_decoder q8_decoder;
+
+/* Geometry of a dense llama-style decoder (Config, model.rs:20-180): separate
+ * q, k, v projections, SiLU-gated feed-forward, RMSNorm before each block,
+ * token embedding tied to the output projection (model.rs:519-524). */
+typedef struct {
+    int n_layer, n_embd, n_ff, n_head, n_head_kv, head_dim, n_rot, n_vocab;
+    int capacity;   /* KV cache positions */
+    int max_batch;  /* most tokens one forward takes (<= Q8_MAX_TOKENS) */
+    float eps, rope_base;
+} q8_decoder_config;
+
+enum { Q8_DEC_Q = 0, Q8_DEC_K, Q8_DEC_V, Q8_DEC_O, Q8_DEC_GATE, Q8_DEC_UP, Q8_DEC_DOWN };
+
+/* Random-init weights on the device (q8_weight_synthetic, one seed per
+ * matrix), norm weights near 1, an f16 KV cache of `capacity` positions. */
+int q8_decoder_create_synthetic(q8_ctx *ctx, const q8_decoder_config *config, uint64_t seed, q8_decoder **out);
+void q8_decoder_destroy(q8_decoder *dec);
+/* Empty the cache: the next forward starts at position 0 (KvCache::reset). */
+int q8_decoder_reset(q8_decoder *dec);
+int q8_decoder_position(const q8_decoder *dec, int *position);
+
+/* Model::forward (model.rs:652-673) for n prompt tokens at the current
+ * position, then the greedy choice (sampler.rs:167-175) on the last row's
+ * logits: *next is the argmax.  The pass is captured into a graph keyed by n
+ * the second time that n runs and replayed after that.  Errors: an id outside
+ * the vocabulary (Q8_ERR_INVALID), a full context (Q8_ERR_UNSUPPORTED). */
+int q8_decoder_forward(q8_decoder *dec, const uint32_t *tokens, int n, uint32_t *next);
+
+/* `steps` greedy decode steps (Model::forward_decode, model.rs:682-731): each
+ * step feeds the previous argmax, which stays on the device, and the steps run
+ * as replays of one captured graph (keyed by the attention split count) with
+ * no host round trip between them.  out[i] receives the token step i chose. */
+int q8_decoder_generate(q8_decoder *dec, int steps, uint32_t *out);
+
+/* The logits of the last forward or step (n_vocab f32, waits). */
+int q8_decoder_logits(q8_decoder *dec, float *host, size_t len);
+/* Weights for the CPU checks: layer < 0 is the tied embedding / output
+ * matrix; `which` is Q8_DEC_*.  Norms: which 0 attention, 1 feed-forward;
+ * layer < 0 the output norm (host pointer of n_embd floats). */
+int q8_decoder_weight(const q8_decoder *dec, int layer, int which, const q8_weight **weight);
+int q8_decoder_norm(const q8_decoder *dec, int layer, int which, const float **weight);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* Q8DECODER_H */

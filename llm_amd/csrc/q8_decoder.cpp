@@ -1,0 +1,350 @@
+// q8_decoder.cpp -- the synthetic decoder of include/q8decoder.h, written
+// against the library's own C-ABI the way the reference's Model is written
+// against Compute (apps/engine/src/model.rs:652-1235): one pass per forward,
+// every projection through the Q8_0 matmul entry points.
+//
+// A pass (Model::body, model.rs:755-826) per layer:
+//   attention: norm (f32 rows for one token, straight to prepared Q8_0 for a
+//              prompt), q/k/v as one grouped matmul, rope + f16 KV append,
+//              attention, output projection with the residual in its epilogue;
+//   feed-forward: norm, gate/up (one fused GEMV + SiLU for one token; grouped
+//              GEMM, then silu(gate)*up quantized for the down projection for
+//              a prompt), down projection with the residual;
+// then the output norm of the last row, the lm_head GEMV (the tied embedding)
+// and the greedy argmax, written to the token slot the next step embeds.
+//
+// Graphs: a pass of shape (n, attention splits) runs eagerly the first time
+// (it grows the context's workspaces and makes the norm weights resident) and
+// is captured into a graph the next time; replays read the position from
+// device memory.  A captured graph is dropped when the context reallocates a
+// workspace (its pointers would be stale).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <utility>
+#include <vector>
+
+#include "../../include/q8decoder.h"
+#include "q8_internal.h"
+#include "q8_layout.h"
+
+namespace {
+
+using q8i::set_error;
+
+#define DEC_TRY(call)                 \
+    do {                              \
+        int rc_ = (call);             \
+        if (rc_ != Q8_OK) return rc_; \
+    } while (0)
+
+unsigned long long mix(unsigned long long z) {
+    z += 0x9e3779b97f4a7c15ull;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+// Norm weights near one: 1 + 0.05 * (u - 0.5), u uniform from the seed.
+std::vector<float> norm_weights(unsigned long long seed, int n) {
+    std::vector<float> w(n);
+    for (int i = 0; i < n; i++) {
+        const double u = (double)(mix(seed + (unsigned long long)i) >> 11) * (1.0 / 9007199254740992.0);
+        w[i] = (float)(1.0 + 0.05 * (u - 0.5));
+    }
+    return w;
+}
+
+struct Layer {
+    const q8_weight *w[7] = {};
+    std::vector<float> attn_norm, ffn_norm;
+    q8_dptr kcache = 0, vcache = 0;
+};
+
+}  // namespace
+
+struct q8_decoder {
+    q8_ctx *c = nullptr;
+    q8_decoder_config cfg{};
+    std::vector<Layer> layers;
+    const q8_weight *embd = nullptr;
+    std::vector<float> output_norm;
+    q8_dptr x = 0, normed = 0, q = 0, k = 0, v = 0, attn = 0, gate = 0, up = 0, act = 0, logits = 0;
+    q8_dptr pos = 0, tokens = 0;
+    int position = 0;  // host mirror of *pos
+    std::map<std::pair<int, int>, void *> graphs;
+    std::map<std::pair<int, int>, int> runs;  // eager runs per shape
+    unsigned long long generation = 0;
+    uint32_t *pinned = nullptr;  // generate(): tokens read back without a wait per step
+    int pinned_len = 0;
+    std::vector<q8_dptr> buffers;
+
+    int alloc(size_t bytes, q8_dptr *p) {
+        DEC_TRY(q8_alloc(c, bytes, p));
+        buffers.push_back(*p);
+        return Q8_OK;
+    }
+    void drop_graphs() {
+        for (auto &g : graphs) q8_graph_destroy(g.second);
+        graphs.clear();
+    }
+    int splits_for(int visible) const {
+        // about 64 positions per decode workgroup, at most 16 per head
+        int s = (visible + 63) / 64;
+        return s < 1 ? 1 : s > 16 ? 16 : s;
+    }
+    int body(int n, int splits);
+    int run(int n, int splits);
+    void sync_generation() {
+        const unsigned long long now = q8i::workspace_generation(c);
+        if (now != generation) {
+            drop_graphs();
+            generation = now;
+        }
+    }
+};
+
+namespace {
+
+int check_config(const q8_decoder_config &g) {
+    if (g.n_layer < 1 || g.n_embd < 32 || g.n_embd % 32 || g.n_ff < 32 || g.n_ff % 32 || g.n_head < 1 ||
+        g.n_head_kv < 1 || g.n_head % g.n_head_kv || g.head_dim != Q8_ATTN_HEAD_DIM ||
+        g.n_head * g.head_dim != g.n_embd || g.n_rot < 0 || g.n_rot > g.head_dim || g.n_rot % 2 || g.n_vocab < 1 ||
+        g.capacity < 1 || g.max_batch < 1 || g.max_batch > Q8_MAX_TOKENS || !(g.eps > 0.0f))
+        return set_error(Q8_ERR_INVALID,
+                         "decoder config: layers %d, embd %d, ff %d, heads %d/%d x %d, rot %d, vocab %d, capacity %d, "
+                         "batch %d (head_dim must be 64, heads x head_dim = embd, dims multiples of 32)",
+                         g.n_layer, g.n_embd, g.n_ff, g.n_head, g.n_head_kv, g.head_dim, g.n_rot, g.n_vocab, g.capacity,
+                         g.max_batch);
+    return Q8_OK;
+}
+
+}  // namespace
+
+// One pass of n tokens at the device position (Model::body, model.rs:755-826).
+int q8_decoder::body(int n, int splits) {
+    const q8_decoder_config &g = cfg;
+    const int E = g.n_embd;
+    const float scale = 1.0f / std::sqrt((float)g.head_dim);
+    DEC_TRY(q8_embeddings_device(c, embd, tokens, (size_t)n, x, 0));
+    for (Layer &L : layers) {
+        // attention block (dense_attention, model.rs:869-1043)
+        q8_group_entry qkv[3] = {{L.w[Q8_DEC_Q], q, 0}, {L.w[Q8_DEC_K], k, 0}, {L.w[Q8_DEC_V], v, 0}};
+        if (n == 1) {
+            DEC_TRY(q8_rmsnorm(c, x, 0, L.attn_norm.data(), E, g.eps, 1, normed, 0));
+            DEC_TRY(q8_matmul_decode_group(c, qkv, 3, normed, 0, E, 0, 0));
+        } else {
+            q8_prepared p{};
+            DEC_TRY(q8_norm_prepare(c, x, 0, L.attn_norm.data(), E, g.eps, n, &p));
+            DEC_TRY(q8_matmul_prompt_group(c, qkv, 3, &p, n, E, 0, 0));
+        }
+        DEC_TRY(q8_rope_append(c, q, 0, k, 0, v, 0, L.kcache, L.vcache, n, g.n_head, g.n_head_kv, g.head_dim, g.n_rot,
+                               g.rope_base, g.capacity, pos));
+        DEC_TRY(q8_attention(c, q, 0, L.kcache, L.vcache, attn, 0, n, g.n_head, g.n_head_kv, g.head_dim, g.capacity,
+                             scale, pos, splits));
+        DEC_TRY(q8_matmul(c, L.w[Q8_DEC_O], attn, 0, n, x, 0, nullptr, x, 0));
+        // feed-forward block (feed_forward, model.rs:1162-1235)
+        if (n == 1) {
+            DEC_TRY(q8_rmsnorm(c, x, 0, L.ffn_norm.data(), E, g.eps, 1, normed, 0));
+            DEC_TRY(q8_gate_up_silu(c, L.w[Q8_DEC_GATE], L.w[Q8_DEC_UP], normed, 0, 1, act, 0, nullptr));
+            DEC_TRY(q8_matmul(c, L.w[Q8_DEC_DOWN], act, 0, 1, x, 0, nullptr, x, 0));
+        } else {
+            q8_prepared p{};
+            DEC_TRY(q8_norm_prepare(c, x, 0, L.ffn_norm.data(), E, g.eps, n, &p));
+            q8_group_entry gu[2] = {{L.w[Q8_DEC_GATE], gate, 0}, {L.w[Q8_DEC_UP], up, 0}};
+            DEC_TRY(q8_matmul_prompt_group(c, gu, 2, &p, n, E, 0, 0));
+            q8_prepared pd{};
+            DEC_TRY(q8_silu_mul_prepare(c, gate, up, n, g.n_ff, &pd));
+            DEC_TRY(q8_matmul(c, L.w[Q8_DEC_DOWN], act, 0, n, x, 0, &pd, x, 0));
+        }
+    }
+    // output norm of the last row, lm_head, greedy choice into the token slot
+    DEC_TRY(q8_rmsnorm(c, x, (size_t)(n - 1) * E, output_norm.data(), E, g.eps, 1, normed, 0));
+    DEC_TRY(q8_matmul(c, embd, normed, 0, 1, logits, 0, nullptr, 0, 0));
+    DEC_TRY(q8_argmax_device(c, logits, 0, (size_t)g.n_vocab, tokens));
+    return q8_advance_position(c, pos, n);
+}
+
+// A pass, through its graph once the shape has run eagerly.
+int q8_decoder::run(int n, int splits) {
+    const auto key = std::make_pair(n, splits);
+    sync_generation();
+    auto it = graphs.find(key);
+    if (it != graphs.end()) return q8_graph_launch(c, it->second);
+    if (runs[key]++ == 0) {
+        const int rc = body(n, splits);
+        sync_generation();  // the eager run may have grown workspaces under older graphs
+        return rc;
+    }
+    DEC_TRY(q8_graph_begin(c));
+    const int rc = body(n, splits);
+    void *graph = nullptr;
+    const int rc_end = q8_graph_end(c, &graph);
+    if (rc != Q8_OK) {
+        q8_graph_destroy(graph);
+        return rc;
+    }
+    DEC_TRY(rc_end);
+    if (q8i::workspace_generation(c) != generation) {  // cannot happen after an eager run; never replay stale
+        q8_graph_destroy(graph);
+        return set_error(Q8_ERR_HIP, "decoder: a workspace grew during capture");
+    }
+    graphs[key] = graph;
+    return q8_graph_launch(c, graph);
+}
+
+extern "C" {
+
+int q8_decoder_create_synthetic(q8_ctx *c, const q8_decoder_config *config, uint64_t seed, q8_decoder **out) {
+    if (!c || !config || !out) return set_error(Q8_ERR_INVALID, "q8_decoder_create_synthetic: bad arguments");
+    *out = nullptr;
+    DEC_TRY(check_config(*config));
+    q8_decoder *d = new q8_decoder;
+    d->c = c;
+    d->cfg = *config;
+    const q8_decoder_config &g = d->cfg;
+    const int E = g.n_embd, kv_dim = g.n_head_kv * g.head_dim, B = g.max_batch;
+    const float std_w = 0.02f;
+    auto fail = [&](int rc) {
+        q8_decoder_destroy(d);
+        return rc;
+    };
+    int rc = q8_weight_synthetic(c, E, g.n_vocab, mix(seed), std_w, &d->embd);
+    if (rc) return fail(rc);
+    d->output_norm = norm_weights(mix(seed ^ 0x6f75747075746e6full), E);
+    d->layers.resize(g.n_layer);
+    for (int l = 0; l < g.n_layer; l++) {
+        Layer &L = d->layers[l];
+        const int dims[7][2] = {{E, g.n_head * g.head_dim}, {E, kv_dim},  {E, kv_dim}, {g.n_head * g.head_dim, E},
+                                {E, g.n_ff},                {E, g.n_ff}, {g.n_ff, E}};
+        for (int i = 0; i < 7; i++) {
+            rc = q8_weight_synthetic(c, dims[i][0], dims[i][1], mix(seed + 1000003ull * (l + 1) + i), std_w, &L.w[i]);
+            if (rc) return fail(rc);
+        }
+        L.attn_norm = norm_weights(mix(seed + 7919ull * (l + 1)), E);
+        L.ffn_norm = norm_weights(mix(seed + 104729ull * (l + 1)), E);
+        const size_t cache = (size_t)g.capacity * kv_dim * 2;
+        if ((rc = d->alloc(cache, &L.kcache)) || (rc = d->alloc(cache, &L.vcache))) return fail(rc);
+    }
+    const size_t f = sizeof(float);
+    if ((rc = d->alloc((size_t)B * E * f, &d->x)) || (rc = d->alloc((size_t)B * E * f, &d->normed)) ||
+        (rc = d->alloc((size_t)B * g.n_head * g.head_dim * f, &d->q)) ||
+        (rc = d->alloc((size_t)B * kv_dim * f, &d->k)) || (rc = d->alloc((size_t)B * kv_dim * f, &d->v)) ||
+        (rc = d->alloc((size_t)B * g.n_head * g.head_dim * f, &d->attn)) ||
+        (rc = d->alloc((size_t)B * g.n_ff * f, &d->gate)) || (rc = d->alloc((size_t)B * g.n_ff * f, &d->up)) ||
+        (rc = d->alloc((size_t)B * g.n_ff * f, &d->act)) || (rc = d->alloc((size_t)g.n_vocab * f, &d->logits)) ||
+        (rc = d->alloc(256, &d->pos)) || (rc = d->alloc((size_t)B * 4, &d->tokens)))
+        return fail(rc);
+    if ((rc = q8_decoder_reset(d))) return fail(rc);
+    *out = d;
+    return Q8_OK;
+}
+
+void q8_decoder_destroy(q8_decoder *d) {
+    if (!d) return;
+    q8_sync(d->c);
+    d->drop_graphs();
+    for (Layer &L : d->layers)
+        for (const q8_weight *w : L.w)
+            if (w) q8_weight_release(d->c, w);
+    if (d->embd) q8_weight_release(d->c, d->embd);
+    for (q8_dptr p : d->buffers) q8_free(d->c, p);
+    if (d->pinned) (void)hipHostFree(d->pinned);
+    delete d;
+}
+
+int q8_decoder_reset(q8_decoder *d) {
+    if (!d) return set_error(Q8_ERR_INVALID, "q8_decoder_reset: null decoder");
+    const int zero[2] = {0, 0};
+    DEC_TRY(q8_upload(d->c, d->pos, zero, sizeof zero));
+    d->position = 0;
+    return Q8_OK;
+}
+
+int q8_decoder_position(const q8_decoder *d, int *position) {
+    if (!d || !position) return set_error(Q8_ERR_INVALID, "q8_decoder_position: bad arguments");
+    *position = d->position;
+    return Q8_OK;
+}
+
+int q8_decoder_forward(q8_decoder *d, const uint32_t *tokens, int n, uint32_t *next) {
+    if (!d || !tokens || !next) return set_error(Q8_ERR_INVALID, "q8_decoder_forward: bad arguments");
+    if (n < 1) return set_error(Q8_ERR_INVALID, "empty prompt");
+    if (n > d->cfg.max_batch)
+        return set_error(Q8_ERR_UNSUPPORTED, "forward of %d tokens exceeds the decoder's batch of %d", n,
+                         d->cfg.max_batch);
+    if (d->position + n > d->cfg.capacity)
+        return set_error(Q8_ERR_UNSUPPORTED, "context full: %d of %d tokens used", d->position + n, d->cfg.capacity);
+    for (int i = 0; i < n; i++)
+        if (tokens[i] >= (uint32_t)d->cfg.n_vocab) return set_error(Q8_ERR_INVALID, "token %u outside vocabulary", tokens[i]);
+    DEC_TRY(q8_upload(d->c, d->tokens, tokens, (size_t)n * 4));
+    DEC_TRY(d->run(n, d->splits_for(d->position + n)));
+    DEC_TRY(q8_download(d->c, next, d->tokens, 4));
+    d->position += n;
+    return Q8_OK;
+}
+
+int q8_decoder_generate(q8_decoder *d, int steps, uint32_t *out) {
+    if (!d || (!out && steps > 0)) return set_error(Q8_ERR_INVALID, "q8_decoder_generate: bad arguments");
+    if (steps <= 0) return Q8_OK;
+    if (d->position < 1) return set_error(Q8_ERR_INVALID, "generate needs a forward first (no token to feed)");
+    if (d->position + steps > d->cfg.capacity)
+        return set_error(Q8_ERR_UNSUPPORTED, "context full: %d of %d tokens used", d->position + steps,
+                         d->cfg.capacity);
+    if (d->pinned_len < steps) {
+        if (d->pinned) (void)hipHostFree(d->pinned);
+        d->pinned = nullptr;
+        d->pinned_len = 0;
+        if (hipHostMalloc((void **)&d->pinned, (size_t)steps * 4, 0) != hipSuccess)
+            return set_error(Q8_ERR_OUT_OF_MEMORY, "hipHostMalloc(%d tokens)", steps);
+        d->pinned_len = steps;
+    }
+    // one split count for the whole run, sized for its last step
+    const int splits = d->splits_for(d->position + steps);
+    hipStream_t stream = (hipStream_t)q8_stream(d->c);
+    for (int i = 0; i < steps; i++) {
+        DEC_TRY(d->run(1, splits));
+        if (hipMemcpyAsync(d->pinned + i, (const void *)(uintptr_t)d->tokens, 4, hipMemcpyDeviceToHost, stream) !=
+            hipSuccess)
+            return set_error(Q8_ERR_HIP, "hip: hipMemcpyAsync(token) failed");
+    }
+    DEC_TRY(q8_sync(d->c));
+    std::memcpy(out, d->pinned, (size_t)steps * 4);
+    d->position += steps;
+    return Q8_OK;
+}
+
+int q8_decoder_logits(q8_decoder *d, float *host, size_t len) {
+    if (!d || !host) return set_error(Q8_ERR_INVALID, "q8_decoder_logits: bad arguments");
+    if (len != (size_t)d->cfg.n_vocab)
+        return set_error(Q8_ERR_INVALID, "logits hold %d values, %zu asked", d->cfg.n_vocab, len);
+    return q8_download(d->c, host, d->logits, len * 4);
+}
+
+int q8_decoder_weight(const q8_decoder *d, int layer, int which, const q8_weight **weight) {
+    if (!d || !weight) return set_error(Q8_ERR_INVALID, "q8_decoder_weight: bad arguments");
+    if (layer < 0) {
+        *weight = d->embd;
+        return Q8_OK;
+    }
+    if (layer >= (int)d->layers.size() || which < 0 || which > Q8_DEC_DOWN)
+        return set_error(Q8_ERR_INVALID, "decoder weight (%d, %d) out of range", layer, which);
+    *weight = d->layers[layer].w[which];
+    return Q8_OK;
+}
+
+int q8_decoder_norm(const q8_decoder *d, int layer, int which, const float **weight) {
+    if (!d || !weight) return set_error(Q8_ERR_INVALID, "q8_decoder_norm: bad arguments");
+    if (layer < 0) {
+        *weight = d->output_norm.data();
+        return Q8_OK;
+    }
+    if (layer >= (int)d->layers.size() || which < 0 || which > 1)
+        return set_error(Q8_ERR_INVALID, "decoder norm (%d, %d) out of range", layer, which);
+    *weight = which == 0 ? d->layers[layer].attn_norm.data() : d->layers[layer].ffn_norm.data();
+    return Q8_OK;
+}
+
+}  // extern "C"

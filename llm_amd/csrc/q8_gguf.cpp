@@ -83,7 +83,7 @@ struct Reader {
     }
     template <typename T>
     int get(T *v) {
-        const uint8_t *p;
+        const uint8_t *p = nullptr;
         if (int rc = take(sizeof(T), &p)) return rc;
         std::memcpy(v, p, sizeof(T));  // x86-64 and the file are both little-endian
         return Q8_OK;
@@ -96,7 +96,7 @@ struct Reader {
         return Q8_OK;
     }
     int str(std::string *s) {
-        const uint8_t *p;
+        const uint8_t *p = nullptr;
         uint64_t len;
         if (int rc = str(&p, &len)) return rc;
         s->assign(reinterpret_cast<const char *>(p), len);
@@ -139,7 +139,7 @@ int skip_array(Reader &r, uint32_t elem_type, uint64_t len, int depth) {
     }
     for (uint64_t i = 0; i < len; i++) {
         if (elem_type == 8) {
-            const uint8_t *p;
+            const uint8_t *p = nullptr;
             uint64_t n;
             if (int rc = r.str(&p, &n)) return rc;
         } else {
@@ -507,7 +507,7 @@ int q8_gguf_meta_str_array(const q8_gguf *g, const char *key, const char **ptrs,
     if (n && (!ptrs || !lens)) return set_error(Q8_ERR_INVALID, "gguf: null output");
     Reader r{g->map, g->size, m->data_offset};
     for (uint64_t i = 0; i < n; i++) {
-        const uint8_t *p;
+        const uint8_t *p = nullptr;
         uint64_t l;
         if (int rc = r.str(&p, &l)) return rc;  // validated at open; kept checked
         ptrs[i] = reinterpret_cast<const char *>(p);

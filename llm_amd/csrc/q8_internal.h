@@ -3,9 +3,14 @@
 #ifndef Q8_INTERNAL_H
 #define Q8_INTERNAL_H
 
+struct q8_ctx;
+
 namespace q8i {
 // Record `fmt` as the calling thread's q8_last_error() message; returns code.
 __attribute__((visibility("hidden"), format(printf, 2, 3))) int set_error(int code, const char *fmt, ...);
+// Changes whenever the context reallocates a workspace; a graph captured
+// before the change holds freed pointers.
+__attribute__((visibility("hidden"))) unsigned long long workspace_generation(const q8_ctx *c);
 }  // namespace q8i
 
 #endif

@@ -1402,11 +1402,14 @@ extern "C" __global__ __launch_bounds__(256) void q8_embed(Q8EmbedArgs a) {
     const int rem = idx - t * per_token;
     const int b = rem >> 1;
     const int h = rem & 1;
-    const unsigned row = a.tokens[t];
+    unsigned row = a.tokens[t];
+    const bool valid = row < (unsigned)a.rows;  // ids from device memory are not host-checked
+    row = valid ? row : 0u;
     const size_t unit = (size_t)(row / Q8_TILE_ROWS) * a.nb + b;
     const unsigned r = row % Q8_TILE_ROWS;
-    const i32x4 q = *(const i32x4 *)(a.quants + unit * Q8_UNIT_BYTES + 16 * (32 * h + r));
-    const float d = f16_to_f32(a.scales[unit * Q8_TILE_ROWS + r]);
+    i32x4 q = *(const i32x4 *)(a.quants + unit * Q8_UNIT_BYTES + 16 * (32 * h + r));
+    const float d = valid ? f16_to_f32(a.scales[unit * Q8_TILE_ROWS + r]) : 0.0f;
+    if (!valid) q = i32x4{0, 0, 0, 0};
     float *o = a.out + (size_t)t * a.nb * Q8_BLOCK_ELEMS + b * Q8_BLOCK_ELEMS + 2 * h;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
@@ -1492,3 +1495,5 @@ extern "C" __global__ __launch_bounds__(256) void q8_silu_mul(Q8EltArgs a) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < a.len) a.act[i] = silu_f32(a.gate[i]) * a.up[i];
 }
+
+#include "q8_attn.hip"

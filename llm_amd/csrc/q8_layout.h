@@ -89,10 +89,11 @@ typedef struct {
 typedef struct {
     const uint8_t *quants;   /* resident weight, tile layout */
     const uint16_t *scales;
-    const uint32_t *tokens;  /* n row ids, each < the weight's rows (checked on the host) */
+    const uint32_t *tokens;  /* n row ids; an id >= rows yields a zero row */
     float *out;              /* n rows of nb*32 f32 */
     int n;
     int nb;
+    int rows;
 } Q8EmbedArgs;
 
 typedef struct {
@@ -199,5 +200,57 @@ typedef struct {
     int parts;
     int stage; /* 0: per-workgroup; 1: combine parts */
 } Q8ArgmaxArgs;
+
+/* ---- decoder support: rotary embedding, f16 KV cache, attention ----
+ * KV cache layout (one layer): f16 [capacity][n_kv * head_dim], position-major,
+ * as the reference's device cache (gpu.cu kv_append 506-519). */
+#define Q8_ATTN_HEAD_DIM 64 /* the head width the attention kernels are built for */
+#define Q8_ATTN_TILE 64     /* prefill: queries and keys per tile */
+
+typedef struct {
+    float *q;            /* [n][n_head][head_dim] f32, rotated in place */
+    const float *k;      /* [n][n_kv][head_dim] f32 */
+    const float *v;      /* [n][n_kv * head_dim] f32 */
+    uint16_t *kcache;    /* f16 cache */
+    uint16_t *vcache;
+    const int *position; /* device: cache position of the first of the n tokens */
+    const float *freq;   /* n_rot / 2 rotation frequencies base^(-2i/n_rot), computed on the host */
+    int n, n_head, n_kv, head_dim, n_rot, capacity;
+} Q8RopeArgs;
+
+typedef struct {
+    const float *q;         /* [n_head][head_dim] (one token) */
+    const uint16_t *kcache;
+    const uint16_t *vcache;
+    float *part_acc;        /* [n_head][splits][head_dim] unnormalised sums */
+    float *part_max;        /* [n_head][splits] */
+    float *part_sum;        /* [n_head][splits] */
+    float *out;             /* [n_head][head_dim]: written directly when splits == 1 */
+    const int *position;    /* device: the token's cache position; it sees position + 1 keys */
+    int n_head, n_kv, splits, capacity;
+    float scale;
+} Q8AttnDecodeArgs;
+
+typedef struct {
+    const float *q;         /* [n][n_head][head_dim] rotated queries */
+    const uint16_t *kcache;
+    const uint16_t *vcache;
+    float *out;             /* [n][n_head][head_dim] */
+    const int *position;    /* device: cache position of query 0 */
+    int n, n_head, n_kv, capacity, qtiles;
+    float scale;
+} Q8AttnPrefillArgs;
+
+typedef struct {
+    uint8_t *dst;           /* GGUF Q8_0 blocks */
+    long long blocks;
+    unsigned long long seed;
+    float scale_std;        /* d = f16(|N(0, scale_std)| / 127) */
+} Q8SynthArgs;
+
+typedef struct {
+    int *position;          /* device: advanced by `advance` */
+    int advance;
+} Q8AdvanceArgs;
 
 #endif

@@ -15,6 +15,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -24,6 +25,7 @@
 #include <string>
 #include <vector>
 
+#include "../../include/q8decoder.h"
 #include "../../include/q8mi.h"
 #include "q8_internal.h"
 #include "q8_layout.h"
@@ -77,6 +79,7 @@ enum Fn {
     F_SILU_MUL,
     F_COPY,
     F_EMBED,
+    F_ROPE, F_ATTN_DECODE, F_ATTN_COMBINE, F_ATTN_PREFILL, F_SYNTH, F_ADVANCE,
     F_COUNT
 };
 
@@ -94,6 +97,7 @@ const char *const kFnNames[F_COUNT] = {
     "q8_silu_mul",
     "q8_copy",
     "q8_embed",
+    "q8_rope_append", "q8_attn_decode", "q8_attn_combine", "q8_attn_prefill", "q8_synth", "q8_advance",
 };
 
 constexpr int kArgmaxParts = 1024;
@@ -128,6 +132,7 @@ struct q8_ctx {
     std::recursive_mutex mu;
     std::map<std::pair<uintptr_t, size_t>, q8_weight *> weights;
     std::map<std::pair<uintptr_t, size_t>, float *> vectors;  // resident f32 norm weights, by host identity
+    std::map<std::pair<int, uint32_t>, float *> rope_freq;    // rotation frequencies by (n_rot, bits of base)
     std::map<uintptr_t, size_t> allocs;  // buffers from q8_alloc, for span checks
     void *act_ws = nullptr;              // prepared activations
     size_t act_ws_bytes = 0;
@@ -138,6 +143,10 @@ struct q8_ctx {
     unsigned *counters = nullptr;        // split-K arrival counters (kernels reset them to 0)
     void *token_ws = nullptr;            // token ids of the embedding lookup
     size_t token_ws_bytes = 0;
+    void *attn_ws = nullptr;             // decode attention partials (acc, max, sum per head and split)
+    size_t attn_ws_bytes = 0;
+    std::vector<q8_weight *> owned;      // weights generated on the device (no host identity)
+    unsigned long long ws_generation = 0; // bumped whenever a workspace is reallocated
     int cu_count = 0;
     size_t total_mem = 0;
     size_t max_lds = 0;
@@ -188,6 +197,7 @@ int grow(q8_ctx *c, void **buf, size_t *have, size_t need, const char *what) {
         *buf = nullptr;
         *have = 0;
     }
+    c->ws_generation++;  // graphs captured over the old buffer must not be replayed
     const size_t bytes = align_up(need, 1 << 20);
     HIP_TRY(hipMalloc(buf, bytes), what);
     *have = bytes;
@@ -617,6 +627,8 @@ int argmax_into(q8_ctx *c, q8_dptr values, size_t len, uint32_t *out) {
 }  // namespace
 
 namespace q8i {
+unsigned long long workspace_generation(const q8_ctx *c) { return c->ws_generation; }
+
 int set_error(int code, const char *fmt, ...) {
     char buf[1024];
     va_list ap;
@@ -716,6 +728,7 @@ void q8_close(q8_ctx *c) {
         delete kv.second;
     }
     for (auto &kv : c->vectors) hipFree(kv.second);
+    for (auto &kv : c->rope_freq) hipFree(kv.second);
     for (auto &kv : c->allocs) hipFree(reinterpret_cast<void *>(kv.first));
     if (c->act_ws) hipFree(c->act_ws);
     if (c->tmp_ws) hipFree(c->tmp_ws);
@@ -723,6 +736,11 @@ void q8_close(q8_ctx *c) {
     if (c->split_ws) hipFree(c->split_ws);
     if (c->counters) hipFree(c->counters);
     if (c->token_ws) hipFree(c->token_ws);
+    if (c->attn_ws) hipFree(c->attn_ws);
+    for (q8_weight *w : c->owned) {
+        hipFree(w->base);
+        delete w;
+    }
     if (c->module) hipModuleUnload(c->module);
     if (c->stream) hipStreamDestroy(c->stream);
     delete c;
@@ -877,6 +895,14 @@ int q8_weight_release(q8_ctx *c, const q8_weight *w) {
     if (!c) return fail(Q8_ERR_INVALID, "q8_weight_release: null context");
     Q8_TRY(check_weight(c, w));
     std::lock_guard<std::recursive_mutex> lock(c->mu);
+    auto own = std::find(c->owned.begin(), c->owned.end(), w);
+    if (own != c->owned.end()) {  // generated on the device
+        HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+        hipFree(w->base);
+        delete *own;
+        c->owned.erase(own);
+        return Q8_OK;
+    }
     auto it = c->weights.find(std::make_pair(w->id_ptr, w->id_len));
     if (it == c->weights.end() || it->second != w) return fail(Q8_ERR_INVALID, "weight is not resident");
     HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
@@ -1139,14 +1165,221 @@ int q8_embeddings(q8_ctx *c, const q8_weight *w, const uint32_t *tokens, size_t 
     HIP_TRY(hipMemcpyAsync(c->token_ws, tokens, n * sizeof(uint32_t), hipMemcpyHostToDevice, c->stream),
             "hipMemcpyAsync(token ids)");
     HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return q8_embeddings_device(c, w, (q8_dptr)(uintptr_t)c->token_ws, n, out, out_offset);
+}
+
+int q8_embeddings_device(q8_ctx *c, const q8_weight *w, q8_dptr tokens, size_t n, q8_dptr out, size_t out_offset) {
+    if (!c) return fail(Q8_ERR_INVALID, "q8_embeddings_device: null context");
+    Q8_TRY(check_weight(c, w));
+    if (n == 0) return Q8_OK;
+    const long long threads = (long long)n * w->nb * 2;
+    if (threads > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "embedding of %zu tokens is too large", n);
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    Q8_TRY(check_span(c, tokens, n * sizeof(uint32_t), "embedding token ids"));
+    Q8_TRY(check_span(c, out, ((size_t)out_offset + n * (size_t)w->k) * sizeof(float), "embedding output"));
     Q8EmbedArgs a{};
     a.quants = w->quants;
     a.scales = w->scales;
-    a.tokens = static_cast<const uint32_t *>(c->token_ws);
+    a.tokens = reinterpret_cast<const uint32_t *>(tokens);
     a.out = fptr(out, out_offset);
     a.n = (int)n;
     a.nb = w->nb;
+    a.rows = w->out;
     return launch(c, F_EMBED, (unsigned)ceil_div(threads, 256), 256, 0, &a, sizeof a);
+}
+
+int q8_argmax_device(q8_ctx *c, q8_dptr values, size_t offset, size_t len, q8_dptr result) {
+    if (!c) return fail(Q8_ERR_INVALID, "q8_argmax_device: null context");
+    if (len == 0) return fail(Q8_ERR_INVALID, "argmax of an empty vector");
+    if (len > 0xfffffffeULL) return fail(Q8_ERR_INVALID, "argmax length %zu exceeds u32 indices", len);
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    const q8_dptr v = (q8_dptr)(uintptr_t)fptr(values, offset);
+    Q8_TRY(check_span(c, v, len * 4, "argmax values"));
+    Q8_TRY(check_span(c, result, 4, "argmax result"));
+    uint8_t *ws = static_cast<uint8_t *>(c->argmax_ws);
+    Q8ArgmaxArgs a{};
+    a.values = reinterpret_cast<const float *>(v);
+    a.len = (long long)len;
+    a.part_value = reinterpret_cast<float *>(ws);
+    a.part_index = reinterpret_cast<unsigned *>(ws + kArgmaxParts * 4);
+    a.result = reinterpret_cast<unsigned *>(result);
+    a.parts = (int)std::min<long long>(kArgmaxParts, std::max<long long>(1, ceil_div((long long)len, 4096)));
+    a.stage = 0;
+    Q8_TRY(launch(c, F_ARGMAX, (unsigned)a.parts, 256, 0, &a, sizeof a));
+    a.stage = 1;
+    return launch(c, F_ARGMAX, 1, 256, 0, &a, sizeof a);
+}
+
+int q8_rope_append(q8_ctx *c, q8_dptr q, size_t q_offset, q8_dptr k, size_t k_offset, q8_dptr v, size_t v_offset,
+                   q8_dptr kcache, q8_dptr vcache, int n, int n_head, int n_kv, int head_dim, int n_rot, float base,
+                   int capacity, q8_dptr position) {
+    if (!c) return fail(Q8_ERR_INVALID, "q8_rope_append: null context");
+    if (n < 1 || n_head < 1 || n_kv < 1 || n_head % n_kv || head_dim < 2 || head_dim % 2 || n_rot < 0 ||
+        n_rot > head_dim || n_rot % 2 || capacity < 1)
+        return fail(Q8_ERR_INVALID, "rope_append: bad geometry (n %d, heads %d/%d, head_dim %d, n_rot %d)", n, n_head,
+                    n_kv, head_dim, n_rot);
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    const size_t kv_dim = (size_t)n_kv * head_dim;
+    Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)fptr(q, q_offset), (size_t)n * n_head * head_dim * 4, "rope q"));
+    Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)fptr(k, k_offset), (size_t)n * kv_dim * 4, "rope k"));
+    Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)fptr(v, v_offset), (size_t)n * kv_dim * 4, "rope v"));
+    Q8_TRY(check_span(c, kcache, (size_t)capacity * kv_dim * 2, "key cache"));
+    Q8_TRY(check_span(c, vcache, (size_t)capacity * kv_dim * 2, "value cache"));
+    Q8_TRY(check_span(c, position, 4, "position"));
+    // RopeTable::new (ops.rs:121-131): frequency = base.powf(-2.0 * pair / n_rot)
+    // in f32, from the C library's powf as the reference's table is; uploaded
+    // once per (n_rot, base) and kept (never inside a capture: the eager pass
+    // of a shape runs first).
+    uint32_t base_bits;
+    std::memcpy(&base_bits, &base, 4);
+    const auto fkey = std::make_pair(n_rot, base_bits);
+    auto fit = c->rope_freq.find(fkey);
+    if (fit == c->rope_freq.end()) {
+        std::vector<float> table(std::max(1, n_rot / 2));
+        for (int i = 0; i < n_rot / 2; i++) table[i] = powf(base, (-2.0f * (float)i) / (float)n_rot);
+        float *dev = nullptr;
+        HIP_TRY(hipMalloc(reinterpret_cast<void **>(&dev), table.size() * 4), "hipMalloc(rope table)");
+        hipError_t e = hipMemcpyAsync(dev, table.data(), table.size() * 4, hipMemcpyHostToDevice, c->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) {
+            hipFree(dev);
+            return hip_fail(e, "upload(rope table)");
+        }
+        fit = c->rope_freq.emplace(fkey, dev).first;
+    }
+    Q8RopeArgs a{};
+    a.freq = fit->second;
+    a.q = fptr(q, q_offset);
+    a.k = fptr(k, k_offset);
+    a.v = fptr(v, v_offset);
+    a.kcache = reinterpret_cast<uint16_t *>(kcache);
+    a.vcache = reinterpret_cast<uint16_t *>(vcache);
+    a.position = reinterpret_cast<const int *>(position);
+    a.n = n;
+    a.n_head = n_head;
+    a.n_kv = n_kv;
+    a.head_dim = head_dim;
+    a.n_rot = n_rot;
+    a.capacity = capacity;
+    const long long items = (long long)n * (n_head + 2 * n_kv) * (head_dim / 2);
+    const unsigned grid = (unsigned)std::min<long long>(ceil_div(items, 256), 4096);
+    return launch(c, F_ROPE, grid, 256, 0, &a, sizeof a);
+}
+
+int q8_attention(q8_ctx *c, q8_dptr q, size_t q_offset, q8_dptr kcache, q8_dptr vcache, q8_dptr out,
+                 size_t out_offset, int n, int n_head, int n_kv, int head_dim, int capacity, float scale,
+                 q8_dptr position, int splits) {
+    if (!c) return fail(Q8_ERR_INVALID, "q8_attention: null context");
+    if (head_dim != Q8_ATTN_HEAD_DIM)
+        return fail(Q8_ERR_UNSUPPORTED, "attention kernels are built for head_dim %d, got %d", Q8_ATTN_HEAD_DIM,
+                    head_dim);
+    if (n < 1 || n_head < 1 || n_kv < 1 || n_head % n_kv || capacity < 1)
+        return fail(Q8_ERR_INVALID, "attention: bad geometry (n %d, heads %d/%d, capacity %d)", n, n_head, n_kv,
+                    capacity);
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    const size_t kv_dim = (size_t)n_kv * head_dim;
+    const q8_dptr qp = (q8_dptr)(uintptr_t)fptr(q, q_offset);
+    const q8_dptr op = (q8_dptr)(uintptr_t)fptr(out, out_offset);
+    Q8_TRY(check_span(c, qp, (size_t)n * n_head * head_dim * 4, "attention q"));
+    Q8_TRY(check_span(c, op, (size_t)n * n_head * head_dim * 4, "attention out"));
+    Q8_TRY(check_span(c, kcache, (size_t)capacity * kv_dim * 2, "key cache"));
+    Q8_TRY(check_span(c, vcache, (size_t)capacity * kv_dim * 2, "value cache"));
+    Q8_TRY(check_span(c, position, 4, "position"));
+    if (n == 1) {
+        if (splits < 1 || splits > 1024 || splits > capacity)
+            return fail(Q8_ERR_INVALID, "attention: %d splits for capacity %d", splits, capacity);
+        const size_t per = (size_t)ceil_div(capacity, splits);
+        const size_t lds = per * 4;
+        const size_t parts = (size_t)n_head * splits;
+        if (splits > 1)
+            Q8_TRY(grow(c, &c->attn_ws, &c->attn_ws_bytes, parts * (head_dim + 2) * 4, "hipMalloc(attention)"));
+        Q8AttnDecodeArgs a{};
+        a.q = reinterpret_cast<const float *>(qp);
+        a.kcache = reinterpret_cast<const uint16_t *>(kcache);
+        a.vcache = reinterpret_cast<const uint16_t *>(vcache);
+        a.part_acc = static_cast<float *>(c->attn_ws);
+        a.part_max = a.part_acc ? a.part_acc + parts * head_dim : nullptr;
+        a.part_sum = a.part_max ? a.part_max + parts : nullptr;
+        a.out = reinterpret_cast<float *>(op);
+        a.position = reinterpret_cast<const int *>(position);
+        a.n_head = n_head;
+        a.n_kv = n_kv;
+        a.splits = splits;
+        a.capacity = capacity;
+        a.scale = scale;
+        Q8_TRY(launch(c, F_ATTN_DECODE, (unsigned)parts, 256, (unsigned)lds, &a, sizeof a));
+        if (splits == 1) return Q8_OK;
+        return launch(c, F_ATTN_COMBINE, (unsigned)n_head, 64, 0, &a, sizeof a);
+    }
+    Q8AttnPrefillArgs a{};
+    a.q = reinterpret_cast<const float *>(qp);
+    a.kcache = reinterpret_cast<const uint16_t *>(kcache);
+    a.vcache = reinterpret_cast<const uint16_t *>(vcache);
+    a.out = reinterpret_cast<float *>(op);
+    a.position = reinterpret_cast<const int *>(position);
+    a.n = n;
+    a.n_head = n_head;
+    a.n_kv = n_kv;
+    a.capacity = capacity;
+    a.qtiles = (int)ceil_div(n, Q8_ATTN_TILE);
+    a.scale = scale;
+    const unsigned lds = 4 * Q8_ATTN_TILE * Q8_ATTN_HEAD_DIM * 4;
+    return launch(c, F_ATTN_PREFILL, (unsigned)(n_head * a.qtiles), 256, lds, &a, sizeof a);
+}
+
+int q8_advance_position(q8_ctx *c, q8_dptr position, int by) {
+    if (!c) return fail(Q8_ERR_INVALID, "q8_advance_position: null context");
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    Q8_TRY(check_span(c, position, 4, "position"));
+    Q8AdvanceArgs a{reinterpret_cast<int *>(position), by};
+    return launch(c, F_ADVANCE, 1, 64, 0, &a, sizeof a);
+}
+
+int q8_weight_synthetic(q8_ctx *c, int k, int out, uint64_t seed, float scale_std, const q8_weight **weight) {
+    if (!c || !weight) return fail(Q8_ERR_INVALID, "q8_weight_synthetic: bad arguments");
+    Q8_TRY(check_k(k));
+    if (out <= 0) return fail(Q8_ERR_INVALID, "weight has %d rows", out);
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+    const int nb = k / 32;
+    const int tiles = (int)ceil_div(out, Q8_TILE_ROWS);
+    const size_t nbytes = (size_t)out * nb * Q8_BLOCK_BYTES;
+    const size_t qbytes = (size_t)tiles * nb * Q8_UNIT_BYTES;
+    const size_t sbytes = (size_t)tiles * nb * Q8_TILE_ROWS * 2;
+    const size_t total = align_up(qbytes, kAlign) + sbytes;
+    const long long threads = (long long)tiles * Q8_TILE_ROWS * nb;
+    if (threads > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "weight of %lld blocks is too large", threads);
+    void *base = nullptr, *staging = nullptr;
+    HIP_TRY(hipMalloc(&base, total), "hipMalloc(weight)");
+    hipError_t e = hipMalloc(&staging, nbytes);
+    if (e != hipSuccess) {
+        hipFree(base);
+        return hip_fail(e, "hipMalloc(weight staging)");
+    }
+    Q8SynthArgs sa{static_cast<uint8_t *>(staging), (long long)out * nb, seed, scale_std};
+    Q8RepackArgs a{};
+    a.src = static_cast<const uint8_t *>(staging);
+    a.quants = static_cast<uint8_t *>(base);
+    a.scales = reinterpret_cast<uint16_t *>(static_cast<uint8_t *>(base) + align_up(qbytes, kAlign));
+    a.rows = out;
+    a.nb = nb;
+    a.tiles = tiles;
+    a.inverse = 0;
+    int rc = launch(c, F_SYNTH, (unsigned)std::min<long long>(ceil_div(sa.blocks, 256), 65536), 256, 0, &sa, sizeof sa);
+    if (rc == Q8_OK) rc = launch(c, F_REPACK, (unsigned)ceil_div(threads, 256), 256, 0, &a, sizeof a);
+    if (rc == Q8_OK) {
+        e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) rc = hip_fail(e, "hipStreamSynchronize");
+    }
+    hipFree(staging);
+    if (rc != Q8_OK) {
+        hipFree(base);
+        return rc;
+    }
+    q8_weight *w = new q8_weight{c, base, a.quants, a.scales, k, out, nb, tiles, total, 0, 0};
+    c->owned.push_back(w);
+    *weight = w;
+    return Q8_OK;
 }
 
 int q8_argmax(q8_ctx *c, q8_dptr values, size_t offset, size_t len, uint32_t *argmax) {

@@ -38,8 +38,8 @@ GROUP_MAX = 4
 KERNEL_GEMV, KERNEL_GEMM, KERNEL_GEMM_F16 = 1, 2, 3
 PREPARED_I8, PREPARED_F16 = 0, 1
 
-# Every function include/q8mi.h and include/q8gguf.h declare (the ABI test
-# checks the headers against this list and the library's exports).
+# Every function include/*.h declare (the ABI test checks the headers against
+# this list and the library's exports).
 EXPORTS = (
     "q8_status_string", "q8_last_error", "q8_build_info",
     "q8_open", "q8_close", "q8_device_name", "q8_device_info", "q8_stream", "q8_set_option",
@@ -55,6 +55,10 @@ EXPORTS = (
     "q8_gguf_tensor", "q8_gguf_meta_count", "q8_gguf_meta_key_at", "q8_gguf_meta_type", "q8_gguf_meta_u64",
     "q8_gguf_meta_f32", "q8_gguf_meta_bool", "q8_gguf_meta_str", "q8_gguf_has_key_prefix",
     "q8_gguf_meta_i32_array", "q8_gguf_meta_f32_array", "q8_gguf_meta_str_array", "q8_gguf_weight",
+    "q8_rope_append", "q8_attention", "q8_embeddings_device", "q8_argmax_device", "q8_advance_position",
+    "q8_weight_synthetic", "q8_decoder_create_synthetic", "q8_decoder_destroy", "q8_decoder_reset",
+    "q8_decoder_position", "q8_decoder_forward", "q8_decoder_generate", "q8_decoder_logits", "q8_decoder_weight",
+    "q8_decoder_norm",
 )
 
 
@@ -86,6 +90,13 @@ class GgufTensorInfo(ctypes.Structure):
                 ("dims", ctypes.POINTER(ctypes.c_uint64)), ("dtype", ctypes.c_uint32),
                 ("offset", ctypes.c_uint64), ("byte_len", ctypes.c_uint64), ("elements", ctypes.c_uint64),
                 ("data", ctypes.c_void_p)]
+
+
+class DecoderConfig(ctypes.Structure):
+    """q8_decoder_config (include/q8decoder.h)."""
+    _fields_ = [(f, ctypes.c_int) for f in ("n_layer", "n_embd", "n_ff", "n_head", "n_head_kv", "head_dim",
+                                            "n_rot", "n_vocab", "capacity", "max_batch")] + \
+               [("eps", ctypes.c_float), ("rope_base", ctypes.c_float)]
 
 
 class _GroupEntry(ctypes.Structure):
@@ -190,6 +201,23 @@ def lib():
         "q8_gguf_meta_str_array": (c_int, [vp, ctypes.c_char_p, ctypes.POINTER(vp), ctypes.POINTER(u64), u64,
                                            ctypes.POINTER(u64)]),
         "q8_gguf_weight": (c_int, [vp, vp, ctypes.c_char_p, c_int, c_int, ctypes.POINTER(vp)]),
+        "q8_rope_append": (c_int, [vp, u64, c_size, u64, c_size, u64, c_size, u64, u64, c_int, c_int, c_int, c_int,
+                                   c_int, ctypes.c_float, c_int, u64]),
+        "q8_attention": (c_int, [vp, u64, c_size, u64, u64, u64, c_size, c_int, c_int, c_int, c_int, c_int,
+                                 ctypes.c_float, u64, c_int]),
+        "q8_embeddings_device": (c_int, [vp, vp, u64, c_size, u64, c_size]),
+        "q8_argmax_device": (c_int, [vp, u64, c_size, c_size, u64]),
+        "q8_advance_position": (c_int, [vp, u64, c_int]),
+        "q8_weight_synthetic": (c_int, [vp, c_int, c_int, u64, ctypes.c_float, ctypes.POINTER(vp)]),
+        "q8_decoder_create_synthetic": (c_int, [vp, ctypes.POINTER(DecoderConfig), u64, ctypes.POINTER(vp)]),
+        "q8_decoder_destroy": (None, [vp]),
+        "q8_decoder_reset": (c_int, [vp]),
+        "q8_decoder_position": (c_int, [vp, ctypes.POINTER(c_int)]),
+        "q8_decoder_forward": (c_int, [vp, ctypes.POINTER(ctypes.c_uint32), c_int, ctypes.POINTER(ctypes.c_uint32)]),
+        "q8_decoder_generate": (c_int, [vp, c_int, ctypes.POINTER(ctypes.c_uint32)]),
+        "q8_decoder_logits": (c_int, [vp, ctypes.POINTER(ctypes.c_float), c_size]),
+        "q8_decoder_weight": (c_int, [vp, c_int, c_int, ctypes.POINTER(vp)]),
+        "q8_decoder_norm": (c_int, [vp, c_int, c_int, ctypes.POINTER(ctypes.POINTER(ctypes.c_float))]),
     }
     assert set(sig) == set(EXPORTS)
     for name, (res, args) in sig.items():
@@ -277,6 +305,18 @@ class Weight:
         return (self.data.ctypes.data, self.data.nbytes)
 
 
+class DeviceWeight:
+    """A weight that lives only on the device (q8_weight_synthetic, or a
+    decoder's): the C-ABI handle plus its shape.  Accepted wherever a
+    ``Weight`` is; ``Gpu.export`` reads its GGUF bytes back."""
+
+    def __init__(self, handle: int, k: int, out: int):
+        self.handle, self.k, self.out = handle, int(k), int(out)
+
+    def nbytes(self) -> int:
+        return self.out * (self.k // 32) * 34
+
+
 class Gpu:
     """The C-ABI context: Gpu::open / Drop (cuda/mod.rs:363-522, 1981-1993)."""
 
@@ -320,6 +360,8 @@ class Gpu:
 
     def resident(self, weight: Weight):
         """Gpu::quantized: upload + repack once, cached by identity."""
+        if isinstance(weight, DeviceWeight):
+            return weight.handle
         h = ctypes.c_void_p()
         _check(lib().q8_weight_resident(self.handle, weight.data.ctypes.data, weight.data.nbytes,
                                         weight.k, weight.out, ctypes.byref(h)))
@@ -333,7 +375,7 @@ class Gpu:
 
     def export(self, weight: Weight) -> np.ndarray:
         h = self.resident(weight)
-        out = np.empty(weight.data.nbytes, dtype=np.uint8)
+        out = np.empty(weight.nbytes() if isinstance(weight, DeviceWeight) else weight.data.nbytes, dtype=np.uint8)
         _check(lib().q8_weight_export(self.handle, h, out.ctypes.data, out.nbytes))
         return out
 
@@ -438,6 +480,36 @@ class Gpu:
         info = gguf.tensor(name)
         self._resident[(gguf.data_address(name), info.byte_len)] = gguf
         return h.value
+
+    def weight_synthetic(self, k: int, out: int, seed: int, scale_std: float = 0.02) -> DeviceWeight:
+        h = ctypes.c_void_p()
+        _check(lib().q8_weight_synthetic(self.handle, k, out, seed, scale_std, ctypes.byref(h)))
+        return DeviceWeight(h.value, k, out)
+
+    def release_device(self, weight: DeviceWeight):
+        _check(lib().q8_weight_release(self.handle, weight.handle))
+
+    def rope_append(self, q: DeviceBuffer, k: DeviceBuffer, v: DeviceBuffer, kcache: DeviceBuffer,
+                    vcache: DeviceBuffer, n: int, n_head: int, n_kv: int, head_dim: int, n_rot: int, base: float,
+                    capacity: int, position: DeviceBuffer, q_offset=0, k_offset=0, v_offset=0):
+        _check(lib().q8_rope_append(self.handle, q.ptr, q_offset, k.ptr, k_offset, v.ptr, v_offset, kcache.ptr,
+                                    vcache.ptr, n, n_head, n_kv, head_dim, n_rot, float(base), capacity,
+                                    position.ptr))
+
+    def attention(self, q: DeviceBuffer, kcache: DeviceBuffer, vcache: DeviceBuffer, out: DeviceBuffer, n: int,
+                  n_head: int, n_kv: int, head_dim: int, capacity: int, scale: float, position: DeviceBuffer,
+                  splits: int = 1, q_offset=0, out_offset=0):
+        _check(lib().q8_attention(self.handle, q.ptr, q_offset, kcache.ptr, vcache.ptr, out.ptr, out_offset, n,
+                                  n_head, n_kv, head_dim, capacity, float(scale), position.ptr, splits))
+
+    def embeddings_device(self, weight, tokens: DeviceBuffer, n: int, out: DeviceBuffer, out_offset: int = 0):
+        _check(lib().q8_embeddings_device(self.handle, self.resident(weight), tokens.ptr, n, out.ptr, out_offset))
+
+    def argmax_device(self, values: DeviceBuffer, offset: int, length: int, result: DeviceBuffer):
+        _check(lib().q8_argmax_device(self.handle, values.ptr, offset, length, result.ptr))
+
+    def advance_position(self, position: DeviceBuffer, by: int):
+        _check(lib().q8_advance_position(self.handle, position.ptr, by))
 
     def argmax(self, values: DeviceBuffer, offset: int, length: int) -> int:
         out = ctypes.c_uint32()

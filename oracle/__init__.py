@@ -28,6 +28,15 @@ How each function is pinned (and where the pin lives):
   reference relies on (``tensor.rs:127-148``).
 * ``silu`` / ``rmsnorm`` / ``argmax`` -- ``ops.rs``'s hand values
   (``apps/engine/tests/ops.rs``) and closed forms.
+* ``rope`` -- closed forms: position 0 is the identity, each pair keeps its
+  norm, rotations compose (angle(p) = p * angle(1) within f32 rounding), pairs
+  past ``n_rot`` are untouched, and a hand-computed pair; ``tests/test_oracle.py``.
+* ``attention`` -- closed forms: one visible key returns its value, equal keys
+  return the mean of the values, a key far above the rest returns its value,
+  shifting every score changes nothing, and later keys never change earlier
+  rows (causality); ``tests/test_oracle.py``.  It computes the exact (f64)
+  value of the reference's formula; the device is held to the f32 bar against
+  it rather than to one f32 summation order.
 """
 from __future__ import annotations
 
@@ -230,3 +239,65 @@ def make_activations(rng: np.random.Generator, n: int, k: int,
         signs = np.where(rng.random((n, k)) < 0.5, -outlier, outlier).astype(np.float32)
         x = np.where(mask, signs, x).astype(np.float32)
     return np.ascontiguousarray(x)
+
+
+# ---------------------------------------------------------------------------
+# Decoder support: rotary embedding, f16 KV cache, attention (numpy).
+# ---------------------------------------------------------------------------
+
+def rope(x: np.ndarray, start: int, n_rot: int, base: float) -> np.ndarray:
+    """RopeTable::new + apply (apps/engine/src/ops.rs:120-166) for rows at
+    positions start, start+1, ...: ``x`` is [n, heads, head_dim] f32; pair i of
+    every head (dims 2i, 2i+1) for i < n_rot/2 rotates by
+    angle = position * base.powf(-2 * i / n_rot), all in f32 and without
+    contraction (low*cos - high*sin, low*sin + high*cos); other dims are kept.
+    powf, cos and sin are the correctly rounded values of their f32 operands."""
+    x = np.array(x, dtype=np.float32, copy=True)
+    n = x.shape[0]
+    half = n_rot // 2
+    if half == 0:
+        return x
+    pair = np.arange(half, dtype=np.float32)
+    exponent = (np.float32(-2.0) * pair) / np.float32(n_rot)
+    # f32::powf is the C library's powf, correctly rounded here; numpy's float32
+    # power is not (it is an ulp off at base 1e4, exponent -1/32), so take the
+    # f64 power of the same f32 operands and round once
+    freq = np.power(np.float64(np.float32(base)), exponent.astype(np.float64)).astype(np.float32)
+    pos = (np.arange(n, dtype=np.float32) + np.float32(start)).astype(np.float32)
+    angle = (pos[:, None] * freq[None, :]).astype(np.float32)          # [n, half]
+    cos = np.cos(angle.astype(np.float64)).astype(np.float32)[:, None, :]
+    sin = np.sin(angle.astype(np.float64)).astype(np.float32)[:, None, :]
+    low = x[:, :, 0:2 * half:2].copy()
+    high = x[:, :, 1:2 * half:2].copy()
+    x[:, :, 0:2 * half:2] = (low * cos).astype(np.float32) - (high * sin).astype(np.float32)
+    x[:, :, 1:2 * half:2] = (low * sin).astype(np.float32) + (high * cos).astype(np.float32)
+    return x
+
+
+def to_f16(x: np.ndarray) -> np.ndarray:
+    """The device cache's f32 -> f16 narrowing, nearest even (gpu.cu:506-519)."""
+    return np.asarray(x, dtype=np.float32).astype(np.float16)
+
+
+def attention(q: np.ndarray, keys: np.ndarray, values: np.ndarray, start: int, scale: float) -> np.ndarray:
+    """attend_host (apps/engine/src/compute.rs:1075-1126): q [n, n_head, hd]
+    for tokens at positions start + t, keys/values [L, n_kv, hd] (the cache,
+    L >= start + n); token t sees positions 0 ..= start + t.  Query head h uses
+    kv head h // (n_head / n_kv).  scores = dot(q, k) * scale, softmax with the
+    max subtracted, output = sum of weight * value.  Computed in f64 (the exact
+    value of that formula on the given inputs), returned as f32."""
+    q = np.asarray(q, dtype=np.float64)
+    keys = np.asarray(keys, dtype=np.float64)
+    values = np.asarray(values, dtype=np.float64)
+    n, n_head, hd = q.shape
+    n_kv = keys.shape[1]
+    group = n_head // n_kv
+    out = np.zeros((n, n_head, hd))
+    for t in range(n):
+        vis = start + t + 1
+        for h in range(n_head):
+            kv = h // group
+            s = keys[:vis, kv, :] @ q[t, h] * float(scale)
+            w = np.exp(s - s.max())
+            out[t, h] = (w / w.sum()) @ values[:vis, kv, :]
+    return out.astype(np.float32)

@@ -1,0 +1,311 @@
+"""GPU tests of the decoder support kernels and the synthetic decoder, through
+the C-ABI (include/q8decoder.h), against the CPU oracle.
+
+Bars:
+  * rope_append: rotated q within 2e-6 + 1e-5|ref| of oracle.rope (device
+    powf/sincosf vs correctly rounded host values); the f16 value cache
+    bit-exact (a pure narrowing); the f16 key cache equal to the narrowed
+    oracle keys except where the f32 rotation differs in its last bit at an
+    f16 rounding boundary (at most one f16 ulp, on at most 1% of elements);
+    rows outside [position, position + n) and at or past capacity untouched;
+  * attention (decode with 1..7 splits, prefill tiles): within 2e-6 + 1e-5|ref|
+    of the exact value of the reference formula over the same f16 cache;
+  * embeddings/argmax/advance on device memory: bit-exact / exact;
+  * the decoder: logits of a prompt and of greedy decode steps against the
+    oracle's composition of the reference ops on the same (exported) weights,
+    within a whole-model tolerance (1e-3 relative to the logit scale: f16
+    cache rounding and int8 activation rounding both flip on last-bit
+    differences), identical greedy tokens wherever the oracle's top-2 gap
+    exceeds that tolerance, and bit-identical replays of the captured graphs.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from llm_amd import decoder as dm
+from llm_amd import q8
+from test_gpu_q8 import assert_bits, assert_close
+
+pytestmark = pytest.mark.gpu
+SEED = 0x5EED
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    g = q8.Gpu(0)
+    yield g
+    g.close()
+
+
+def f16_buffer(gpu, rows, kv_dim, fill=np.float16(-7.0)):
+    host = np.full(rows * kv_dim, fill, np.float16)
+    b = gpu.alloc(host.nbytes)
+    b.upload(host)
+    return b
+
+
+def read_f16(buf, rows, kv_dim):
+    return buf.download(np.uint16, rows * kv_dim).view(np.float16).reshape(rows, kv_dim)
+
+
+def int_buffer(gpu, value):
+    b = gpu.alloc(256)
+    b.upload(np.array([value, 0], np.int32))
+    return b
+
+
+@pytest.mark.parametrize("n,n_head,n_kv,n_rot,position,capacity", [(5, 4, 2, 64, 7, 32), (1, 36, 36, 64, 511, 1024),
+                                                                   (40, 4, 4, 32, 3, 64), (6, 2, 1, 64, 30, 32)])
+def test_rope_append_matches_the_oracle(gpu, n, n_head, n_kv, n_rot, position, capacity):
+    """The last case runs past the capacity: rows from there on are not
+    written (and their queries not rotated: the host reports the full context
+    before such a call)."""
+    r = np.random.default_rng(SEED + n)
+    hd, base = 64, 10000.0
+    kv_dim = n_kv * hd
+    q = r.standard_normal((n, n_head, hd)).astype(np.float32)
+    k = r.standard_normal((n, n_kv, hd)).astype(np.float32)
+    v = r.standard_normal((n, n_kv, hd)).astype(np.float32)
+    qb, kb, vb = (gpu.alloc(a.nbytes) for a in (q, k, v))
+    qb.upload(q)
+    kb.upload(k)
+    vb.upload(v)
+    extra = 8  # rows past capacity that must stay untouched
+    kc, vc = f16_buffer(gpu, capacity + extra, kv_dim), f16_buffer(gpu, capacity + extra, kv_dim)
+    pos = int_buffer(gpu, position)
+    print(f"\nrope n={n} heads={n_head}/{n_kv} rot={n_rot} pos={position}", flush=True)
+    gpu.rope_append(qb, kb, vb, kc, vc, n, n_head, n_kv, hd, n_rot, base, capacity, pos)
+    gpu.sync()
+    q_ref = oracle.rope(q, position, n_rot, base)
+    k_ref = oracle.to_f16(oracle.rope(k, position, n_rot, base)).reshape(n, kv_dim)
+    v_ref = oracle.to_f16(v).reshape(n, kv_dim)
+    live = min(n, capacity - position)
+    assert_close(qb.download(np.float32, q.size).reshape(q.shape)[:live], q_ref[:live], "rotated q")
+    kg, vg = read_f16(kc, capacity + extra, kv_dim), read_f16(vc, capacity + extra, kv_dim)
+    rows = slice(position, position + live)
+    assert np.array_equal(vg[rows].view(np.uint16), v_ref[:live].view(np.uint16)), "value cache not bit-exact"
+    diff = kg[rows].view(np.uint16).astype(np.int32) - k_ref[:live].view(np.uint16).astype(np.int32)
+    assert np.abs(diff).max() <= 1 and (diff != 0).mean() <= 0.01, f"key cache: {int((diff != 0).sum())} differ"
+    untouched = np.ones(capacity + extra, bool)
+    untouched[rows] = False
+    assert (kg[untouched] == np.float16(-7.0)).all() and (vg[untouched] == np.float16(-7.0)).all()
+
+
+def cache_pair(gpu, r, L, capacity, n_kv, hd=64):
+    k = oracle.to_f16(r.standard_normal((capacity, n_kv, hd)))
+    v = oracle.to_f16(r.standard_normal((capacity, n_kv, hd)))
+    kc, vc = gpu.alloc(k.nbytes), gpu.alloc(v.nbytes)
+    kc.upload(k.view(np.uint16))
+    vc.upload(v.view(np.uint16))
+    return k.astype(np.float32), v.astype(np.float32), kc, vc
+
+
+@pytest.mark.parametrize("visible,splits,n_head,n_kv", [(1, 1, 4, 2), (200, 1, 4, 2), (200, 3, 4, 4), (200, 7, 8, 2),
+                                                        (640, 10, 36, 36), (4096, 16, 4, 1)])
+def test_decode_attention_matches_the_oracle(gpu, visible, splits, n_head, n_kv):
+    r = np.random.default_rng(SEED + visible + splits)
+    capacity = max(visible, 256)
+    kf, vf, kc, vc = cache_pair(gpu, r, visible, capacity, n_kv)
+    q = (r.standard_normal((1, n_head, 64)) * 2).astype(np.float32)
+    qb, out = gpu.alloc(q.nbytes), gpu.alloc(q.nbytes)
+    qb.upload(q)
+    pos = int_buffer(gpu, visible - 1)
+    print(f"\ndecode attention visible={visible} splits={splits} heads={n_head}/{n_kv}", flush=True)
+    gpu.attention(qb, kc, vc, out, 1, n_head, n_kv, 64, capacity, 0.125, pos, splits)
+    got = out.download(np.float32, q.size).reshape(q.shape)
+    assert_close(got, oracle.attention(q, kf, vf, visible - 1, 0.125), f"decode attention L={visible} s={splits}")
+
+
+@pytest.mark.parametrize("n,start,n_head,n_kv", [(2, 0, 4, 2), (64, 0, 4, 4), (100, 0, 2, 1), (130, 37, 4, 2),
+                                                 (512, 0, 36, 36)])
+def test_prefill_attention_matches_the_oracle(gpu, n, start, n_head, n_kv):
+    r = np.random.default_rng(SEED + n + start)
+    capacity = start + n + 16
+    kf, vf, kc, vc = cache_pair(gpu, r, start + n, capacity, n_kv)
+    q = (r.standard_normal((n, n_head, 64)) * 2).astype(np.float32)
+    qb, out = gpu.alloc(q.nbytes), gpu.alloc(q.nbytes)
+    qb.upload(q)
+    pos = int_buffer(gpu, start)
+    print(f"\nprefill attention n={n} start={start} heads={n_head}/{n_kv}", flush=True)
+    gpu.attention(qb, kc, vc, out, n, n_head, n_kv, 64, capacity, 0.125, pos)
+    got = out.download(np.float32, q.size).reshape(q.shape)
+    ref = oracle.attention(q, kf, vf, start, 0.125) if n <= 130 else None
+    if ref is None:  # the large case: check a sample of rows against the oracle
+        rows = [0, 1, 63, 64, 255, 511]
+        ref = np.stack([oracle.attention(q[t:t + 1], kf, vf, start + t, 0.125)[0] for t in rows])
+        got = got[rows]
+    assert_close(got, ref, f"prefill attention n={n} start={start}")
+
+
+def test_device_token_ops(gpu):
+    r = np.random.default_rng(SEED)
+    data = oracle.make_q8_weight(r, 300, 96)
+    w = q8.Weight(data, 96, 300)
+    ids = np.array([5, 299, 0, 1000], np.uint32)  # 1000: outside the vocabulary -> zero row
+    tb = gpu.alloc(16)
+    tb.upload(ids)
+    out = gpu.alloc(4 * 4 * 96)
+    gpu.embeddings_device(w, tb, 4, out, 0)
+    got = out.download(np.float32, 4 * 96).reshape(4, 96)
+    rows = data.reshape(300, -1)
+    for i, t in enumerate(ids[:3]):
+        assert_bits(got[i], oracle.dequant_q8_0(rows[t], 96), f"row {t}")
+    assert (got[3].view(np.uint32) == 0).all()
+    vals = r.standard_normal(5000).astype(np.float32)
+    vb = gpu.alloc(vals.nbytes)
+    vb.upload(vals)
+    gpu.argmax_device(vb, 0, vals.size, tb)
+    pos = int_buffer(gpu, 10)
+    gpu.advance_position(pos, 7)
+    gpu.advance_position(pos, 1)
+    assert int(tb.download(np.uint32, 1)[0]) == oracle.argmax(vals)
+    assert int(pos.download(np.int32, 1)[0]) == 18
+
+
+def test_synthetic_weights_are_valid_q8_0_and_seeded(gpu):
+    a = gpu.weight_synthetic(2304, 96, seed=7)
+    b = gpu.weight_synthetic(2304, 96, seed=7)
+    c = gpu.weight_synthetic(2304, 96, seed=8)
+    ea, eb, ec = gpu.export(a), gpu.export(b), gpu.export(c)
+    assert np.array_equal(ea, eb) and not np.array_equal(ea, ec)
+    blk = ea.reshape(-1, 34)
+    qv = blk[:, 2:].view(np.int8)
+    d = blk[:, :2].copy().view(np.float16).astype(np.float32)
+    assert qv.min() >= -127 and qv.max() <= 127 and abs(float(qv.mean())) < 1.0
+    assert (d >= 0).all() and np.isfinite(d).all() and 0.5e-4 < float(np.median(d)) < 2e-4
+    x = np.random.default_rng(SEED).standard_normal(2304).astype(np.float32)
+    xb, yb = gpu.alloc(x.nbytes), gpu.alloc(96 * 4)
+    xb.upload(x)
+    gpu.matmul(a, xb, 0, 1, yb, 0)
+    assert_close(yb.download(np.float32, 96), oracle.matmul(ea, 2304, 96, x, 1)[0], "GEMV on a synthetic weight")
+    for w in (a, b, c):
+        gpu.release_device(w)
+
+
+# ---- the decoder against the oracle's composition of the reference ops ----
+
+def small_config():
+    return dm.config(n_layer=2, n_embd=256, n_ff=512, n_head=4, n_head_kv=2, head_dim=64, n_vocab=1000,
+                     capacity=96, max_batch=80)
+
+
+class OracleDecoder:
+    """Model::body (model.rs:755-826) composed from the oracle's restatements of
+    the reference ops, over the decoder's exported weights."""
+
+    def __init__(self, gpu, dec):
+        c = self.cfg = dec.cfg
+        self.embd = gpu.export(dec.weight(-1))
+        self.w = {(l, i): gpu.export(dec.weight(l, i)) for l in range(c.n_layer) for i in range(7)}
+        self.norms = {(l, i): dec.norm(l, i) for l in range(c.n_layer) for i in range(2)}
+        self.out_norm = dec.norm(-1)
+        kv_dim = c.n_head_kv * c.head_dim
+        self.kc = [np.zeros((c.capacity, c.n_head_kv, c.head_dim), np.float32) for _ in range(c.n_layer)]
+        self.vc = [np.zeros((c.capacity, c.n_head_kv, c.head_dim), np.float32) for _ in range(c.n_layer)]
+        self.kv_dim = kv_dim
+        self.pos = 0
+
+    def mm(self, data, k, out, x):
+        x = np.asarray(x, np.float32)
+        return oracle.matmul(data, k, out, x.reshape(-1), x.shape[0]).reshape(x.shape[0], out)
+
+    def norm_rows(self, x, w):
+        return np.stack([oracle.rmsnorm(row, w, self.cfg.eps) for row in x])
+
+    def forward(self, tokens):
+        c, E = self.cfg, self.cfg.n_embd
+        n = len(tokens)
+        rows = self.embd.reshape(c.n_vocab, -1)
+        x = np.stack([oracle.dequant_q8_0(rows[t], E) for t in tokens]).astype(np.float32)
+        H, KV, hd = c.n_head, c.n_head_kv, c.head_dim
+        for l in range(c.n_layer):
+            h = self.norm_rows(x, self.norms[(l, 0)])
+            q = self.mm(self.w[(l, dm.Q)], E, H * hd, h).reshape(n, H, hd)
+            k = self.mm(self.w[(l, dm.K)], E, KV * hd, h).reshape(n, KV, hd)
+            v = self.mm(self.w[(l, dm.V)], E, KV * hd, h).reshape(n, KV, hd)
+            q = oracle.rope(q, self.pos, c.n_rot, c.rope_base)
+            k = oracle.rope(k, self.pos, c.n_rot, c.rope_base)
+            self.kc[l][self.pos:self.pos + n] = oracle.to_f16(k).astype(np.float32)
+            self.vc[l][self.pos:self.pos + n] = oracle.to_f16(v).astype(np.float32)
+            a = oracle.attention(q, self.kc[l], self.vc[l], self.pos, 1.0 / np.sqrt(np.float32(hd)))
+            x = (x + self.mm(self.w[(l, dm.O)], H * hd, E, a.reshape(n, -1))).astype(np.float32)
+            h = self.norm_rows(x, self.norms[(l, 1)])
+            g = self.mm(self.w[(l, dm.GATE)], E, c.n_ff, h)
+            u = self.mm(self.w[(l, dm.UP)], E, c.n_ff, h)
+            act = oracle.silu_mul(g, u).reshape(n, c.n_ff)
+            x = (x + self.mm(self.w[(l, dm.DOWN)], c.n_ff, E, act)).astype(np.float32)
+        self.pos += n
+        last = oracle.rmsnorm(x[-1], self.out_norm, c.eps)
+        return self.mm(self.embd, E, c.n_vocab, last[None])[0]
+
+
+def check_logits(got, ref, what):
+    tol = 1e-3 * float(np.abs(ref).max())
+    d = np.abs(got.astype(np.float64) - ref)
+    assert d.max() <= tol, f"{what}: max |d| {d.max():.3e} > {tol:.3e}"
+    top2 = np.sort(ref)[-2:]
+    if top2[1] - top2[0] > 2 * tol:
+        assert int(np.argmax(got)) == oracle.argmax(ref), f"{what}: greedy token differs"
+
+
+def test_decoder_prompt_and_decode_steps_match_the_oracle(gpu):
+    dec = dm.Decoder(gpu, small_config(), seed=11)
+    try:
+        ref = OracleDecoder(gpu, dec)
+        prompt = np.random.default_rng(SEED).integers(0, 1000, 70).astype(np.uint32)
+        print("\ndecoder prompt of 70", flush=True)
+        nxt = dec.forward(prompt)
+        ref_logits = ref.forward(prompt)
+        got = dec.logits()
+        check_logits(got, ref_logits, "prompt logits")
+        assert nxt == int(np.argmax(got))
+        steps = dec.generate(4)  # eager step, then captured replays
+        assert dec.position == 74
+        feed = [nxt] + [int(t) for t in steps[:-1]]
+        for i, tok in enumerate(feed):
+            logits = ref.forward([tok])
+            top2 = np.sort(logits)[-2:]
+            if top2[1] - top2[0] > 2e-3 * np.abs(logits).max():
+                assert int(steps[i]) == oracle.argmax(logits), f"decode step {i}"
+        check_logits(dec.logits(), logits, "last decode step logits")
+    finally:
+        dec.close()
+
+
+def test_decoder_graph_replays_are_bit_identical(gpu):
+    dec = dm.Decoder(gpu, small_config(), seed=12)
+    try:
+        prompt = np.arange(1, 41, dtype=np.uint32)
+        runs = []
+        for _ in range(3):  # eager, capture + replay, replay
+            dec.reset()
+            first = dec.forward(prompt)
+            toks = dec.generate(6)
+            runs.append((first, toks.copy(), dec.logits()))
+        for first, toks, logits in runs[1:]:
+            assert first == runs[0][0] and np.array_equal(toks, runs[0][1])
+            assert_bits(logits, runs[0][2], "replayed logits")
+    finally:
+        dec.close()
+
+
+def test_decoder_errors(gpu):
+    dec = dm.Decoder(gpu, small_config(), seed=13)
+    try:
+        with pytest.raises(q8.Q8Error) as e:
+            dec.forward([1, 1000])
+        assert e.value.status == q8.Q8_ERR_INVALID and "outside vocabulary" in e.value.message
+        with pytest.raises(q8.Q8Error) as e:
+            dec.forward([])
+        assert e.value.status == q8.Q8_ERR_INVALID
+        with pytest.raises(q8.Q8Error) as e:
+            dec.generate(1)  # nothing to feed yet
+        assert e.value.status == q8.Q8_ERR_INVALID
+        dec.forward(np.zeros(80, np.uint32))
+        with pytest.raises(q8.Q8Error) as e:
+            dec.generate(17)  # 80 + 17 > capacity 96
+        assert e.value.status == q8.Q8_ERR_UNSUPPORTED and "context full" in e.value.message
+        assert dec.position == 80
+        assert len(dec.generate(16)) == 16 and dec.position == 96
+    finally:
+        dec.close()

@@ -327,3 +327,98 @@ def test_argmax_takes_the_first_strictly_greatest():
     assert oracle.argmax(np.array([-1, -1], np.float32)) == 0
     assert oracle.argmax(np.array([0, np.nan, 5, 5], np.float32)) == 2
     assert oracle.argmax(np.array([np.nan, 1, 9], np.float32)) == 0
+
+
+# ---- rope (ops.rs:120-166) ----
+
+def test_rope_position_zero_is_identity_and_pairs_keep_their_norm():
+    rng = np.random.default_rng(RNG_SEED)
+    x = rng.standard_normal((5, 3, 64)).astype(np.float32)
+    y = oracle.rope(x, 0, 64, 10000.0)
+    assert np.array_equal(y[0], x[0])  # angle 0: cos 1, sin 0 exactly
+    norm_x = np.hypot(x[..., 0::2].astype(np.float64), x[..., 1::2])
+    norm_y = np.hypot(y[..., 0::2].astype(np.float64), y[..., 1::2])
+    assert np.allclose(norm_x, norm_y, rtol=1e-6, atol=1e-7)
+
+
+def test_rope_hand_value_and_partial_rotation():
+    # pair 0 rotates by exactly `position` radians (base^0 = 1); pair 1 of a
+    # 4-dim rotary span by position * base^(-1/2)
+    x = np.zeros((1, 1, 8), np.float32)
+    x[0, 0, :] = [1, 0, 0, 1, 5, 6, 7, 8]
+    y = oracle.rope(x, 3, 4, 100.0)
+    assert np.allclose(y[0, 0, 0:2], [np.cos(3.0), np.sin(3.0)], atol=1e-6)
+    a = 3.0 * 100.0 ** -0.5
+    assert np.allclose(y[0, 0, 2:4], [-np.sin(a), np.cos(a)], atol=1e-6)
+    assert np.array_equal(y[0, 0, 4:], x[0, 0, 4:])  # past n_rot: untouched
+
+
+def test_rope_rotations_compose():
+    rng = np.random.default_rng(RNG_SEED + 1)
+    x = rng.standard_normal((1, 2, 64)).astype(np.float32)
+    once = oracle.rope(x, 7, 64, 10000.0)
+    # rotating position 3 then by 4 more equals position 7, to f32 rounding
+    twice = oracle.rope(oracle.rope(x, 3, 64, 10000.0), 4, 64, 10000.0)
+    assert np.allclose(once, twice, atol=2e-5)
+    with pytest.raises(AssertionError):  # a sign slip in the rotation fails this
+        bad = x.copy()
+        bad[..., 1::2] *= -1
+        assert np.allclose(oracle.rope(bad, 7, 64, 10000.0), once, atol=2e-5)
+
+
+# ---- attention (compute.rs:1075-1126) ----
+
+def test_attention_single_key_returns_its_value():
+    rng = np.random.default_rng(RNG_SEED + 2)
+    q = rng.standard_normal((1, 4, 64)).astype(np.float32)
+    k = rng.standard_normal((1, 2, 64)).astype(np.float32)
+    v = rng.standard_normal((1, 2, 64)).astype(np.float32)
+    out = oracle.attention(q, k, v, 0, 0.125)
+    for h in range(4):
+        assert np.allclose(out[0, h], v[0, h // 2], atol=1e-7)
+
+
+def test_attention_equal_keys_average_and_dominant_key_wins():
+    rng = np.random.default_rng(RNG_SEED + 3)
+    L = 9
+    q = rng.standard_normal((1, 1, 64)).astype(np.float32)
+    k = np.repeat(rng.standard_normal((1, 1, 64)).astype(np.float32), L, axis=0)
+    v = rng.standard_normal((L, 1, 64)).astype(np.float32)
+    out = oracle.attention(q, k, v, L - 1, 0.125)
+    assert np.allclose(out[0, 0], v[:, 0].astype(np.float64).mean(axis=0), atol=1e-6)
+    k2 = rng.standard_normal((L, 1, 64)).astype(np.float32) * 0.01
+    k2[4, 0] = q[0, 0] * 100.0  # score ~ 100 * |q|^2 * 0.125 above the rest
+    out2 = oracle.attention(q, k2, v, L - 1, 0.125)
+    assert np.allclose(out2[0, 0], v[4, 0], atol=1e-6)
+
+
+def test_attention_is_causal_and_convex():
+    rng = np.random.default_rng(RNG_SEED + 4)
+    n, L = 6, 6
+    q = rng.standard_normal((n, 2, 64)).astype(np.float32)
+    k = rng.standard_normal((L, 2, 64)).astype(np.float32)
+    v = rng.standard_normal((L, 2, 64)).astype(np.float32)
+    full = oracle.attention(q, k, v, 0, 0.125)
+    for t in range(n):  # row t only sees keys 0..t
+        part = oracle.attention(q[t:t + 1], k[:t + 1], v[:t + 1], t, 0.125)
+        assert np.allclose(full[t], part[0], atol=1e-6)
+    # a larger scale sharpens but the row still sums the same values convexly
+    sharp = oracle.attention(q, k, v, 0, 10.0)
+    lo, hi = v.min(axis=0), v.max(axis=0)
+    assert np.all(sharp >= lo[None] - 1e-5) and np.all(sharp <= hi[None] + 1e-5)
+
+
+def test_rope_frequency_is_the_correctly_rounded_powf():
+    # the frequency of pair 1 at base 1e4 over 64 dims: 10000^(-1/32) =
+    # 0.74989420933..., whose nearest f32 is 0.7498942 (numpy's float32 power
+    # returns the next one up, 0.74989426; a position of 511 turns that ulp
+    # into a 3e-5 error in the rotated value)
+    import math
+    exact = math.exp(-math.log(10000.0) / 32)
+    nearest = np.float32(exact)
+    assert abs(float(nearest) - exact) < abs(float(np.nextafter(nearest, np.float32(1))) - exact)
+    x = np.zeros((512, 1, 64), np.float32)
+    x[:, 0, 2] = 1.0
+    y = oracle.rope(x, 0, 64, 10000.0)
+    angle = np.float32(511) * nearest
+    assert y[511, 0, 2] == np.float32(np.cos(np.float64(angle)))
