@@ -14,6 +14,10 @@ Also reported (own fixed repetition counts, graphs, events):
               quantization, in int8 TOPS (2*M*N*K) vs the 5.0 POPS dense peak;
   extras      configs[1] n = 8 / 64 (GB/s), configs[2] decode layer set and
               the 122880 x 2304 lm_head GEMV + argmax (GB/s, us);
+  decoder     configs[4]: the 42-layer synthetic decoder (hidden 2304, FFN
+              5760, 36 heads x 64, vocab 122880, f16 KV cache of 4096) with
+              random-init Q8_0 weights generated on the device: a 512-token
+              prefill of random ids, then 128 greedy decode steps (tok/s);
   cpu_baseline the oracle's C restatement of the reference rayon CPU path
               (oracle/q8_oracle.c) on this host's cores, on a bounded sample.
 
@@ -317,6 +321,57 @@ def bench_decode_layer(gpu, reps, rng):
     return layer, head
 
 
+def bench_decoder(gpu, rng, prompt=512, steps=128, reps=3):
+    """prefill `prompt` random ids, then `steps` greedy decode
+    steps, on the 42-layer synthetic decoder.  Each phase runs once untimed
+    (the eager pass, then the capture of its graph) before the timed runs;
+    times are host wall-clock around the calls (which end in a wait), the
+    median of `reps`."""
+    from llm_amd import decoder as dm
+    cfg = dm.config(n_layer=42, n_embd=2304, n_ff=5760, n_head=36, n_head_kv=36, head_dim=64, n_vocab=122880,
+                    capacity=4096, max_batch=prompt)
+    t0 = time.perf_counter()
+    dec = dm.Decoder(gpu, cfg, seed=0x5EED)
+    log(f"decoder: 42 layers generated on the device in {time.perf_counter() - t0:.1f} s")
+    ids = rng.integers(0, cfg.n_vocab, prompt).astype(np.uint32)
+    try:
+        for _ in range(2):  # eager pass, then capture
+            dec.reset()
+            dec.forward(ids)
+            dec.generate(steps)
+        pre, gen = [], []
+        tokens = None
+        for _ in range(reps):
+            dec.reset()
+            t0 = time.perf_counter()
+            first = dec.forward(ids)
+            pre.append(time.perf_counter() - t0)
+            t0 = time.perf_counter()
+            toks = dec.generate(steps)
+            gen.append(time.perf_counter() - t0)
+            cur = [first] + toks.tolist()
+            assert tokens is None or tokens == cur, "greedy tokens differ between identical runs"
+            tokens = cur
+    finally:
+        dec.close()
+    t_pre, t_gen = float(np.median(pre)), float(np.median(gen))
+    layer_w = (2304 * 3 * 2304 + 2304 * 2304 + 2 * 5760 * 2304 + 2304 * 5760) // 32 * 34
+    head_w = 122880 * 2304 // 32 * 34
+    per_token = 42 * layer_w + head_w
+    out = {"prefill_tokens": prompt, "prefill_ms": round(t_pre * 1e3, 2),
+           "prefill_tok_s": round(prompt / t_pre, 1),
+           "decode_steps": steps, "decode_ms_per_token": round(t_gen / steps * 1e3, 3),
+           "decode_tok_s": round(steps / t_gen, 1),
+           "decode_weight_bytes_per_token": per_token,
+           "decode_weight_gbs": round(per_token * steps / t_gen / 1e9, 1),
+           "decode_floor_ms_per_token_at_8tbs": round(per_token / 8e12 * 1e3, 3),
+           "first_tokens": tokens[:8]}
+    log(f"decoder: prefill {prompt} in {t_pre * 1e3:.1f} ms ({out['prefill_tok_s']} tok/s); decode "
+        f"{out['decode_ms_per_token']} ms/token ({out['decode_tok_s']} tok/s, {out['decode_weight_gbs']} GB/s of "
+        f"weights)")
+    return out
+
+
 CALIBRATION_BYTES = 64 << 20
 
 
@@ -365,11 +420,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--sections", default="all",
-                    help="comma list of gemv,gemm,extras,cpu (default all); a profiler run names one so "
-                         "each kernel's average covers one workload")
+                    help="comma list of gemv,gemm,extras,decoder,cpu (default all); a profiler run names "
+                         "one so each kernel's average covers one workload")
     args = ap.parse_args()
-    sections = {"gemv", "gemm", "extras", "cpu"} if args.sections == "all" else set(args.sections.split(","))
-    unknown = sections - {"gemv", "gemm", "extras", "cpu"}
+    known = {"gemv", "gemm", "extras", "decoder", "cpu"}
+    sections = set(known) if args.sections == "all" else set(args.sections.split(","))
+    unknown = sections - known
     if unknown:
         ap.error(f"unknown sections {sorted(unknown)}")
     if args.gpus != 1:
@@ -397,6 +453,7 @@ def main():
         layer, head = bench_decode_layer(gpu, 50, rng)
         extras["configs2_decode_layer"] = layer
         extras["configs2_lm_head"] = head
+    decoder = bench_decoder(gpu, rng) if "decoder" in sections else None
     cpu = cpu_baseline(args.cpu_seconds) if "cpu" in sections and args.cpu_seconds > 0 else None
     gpu.close()
 
@@ -431,6 +488,7 @@ def main():
                       "quantize_us": gemm.get("quantize_us"),
                       "projections_us": gemm.get("projections_us")},
         "extras": extras,
+        "decoder_configs4": decoder,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -4,9 +4,9 @@
 //   q8_rope_append   rotary embedding of q and k, k and v narrowed to the f16
 //                    KV cache                     (gpu.cu rope_append 525-581, ops.rs:152-166)
 //   q8_attn_decode   one token against the cache, positions split over
-//   q8_attn_combine  workgroups, then combined    (gpu.cu attention_split 649-733, combine 735-762)
-//   q8_attn_prefill  causal attention of n tokens, 64 x 64 tiles, online softmax
-//                                                 (compute.rs attend_host 1075-1126)
+//                    workgroups, combined by the last (gpu.cu attention_split 649-733, combine 735-762)
+//   q8_attn_prefill  causal attention of n tokens on f16 MFMA (split operands),
+//                    online softmax               (compute.rs attend_host 1075-1126)
 //   q8_synth         seeded synthetic Q8_0 blocks for the benchmark decoder
 //   q8_advance       the position a captured step reads, moved on the device
 //
@@ -78,16 +78,22 @@ extern "C" __global__ __launch_bounds__(256) void q8_rope_append(Q8RopeArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Decode attention for one token: workgroup (head, split) of 256 threads takes
-// positions [begin, end) of the position + 1 visible ones.
-//   scores: a thread per position, dot(q, k) over the 64 dims in order (q from
-//           LDS, broadcast), then * scale (the reference's dot * scale);
+// Decode attention for one token: workgroup (head, split) of 16 waves takes
+// positions [begin, end) of the position + 1 visible ones.  Rows are read
+// whole and coalesced, and every load of a pass is issued before it waits:
+//   scores: 8 lanes per key row (16 bytes = 8 dims each), 128 rows per pass;
+//           the 8 partial dots (dims in order, q from LDS) meet by xor
+//           shuffles, then * scale (the reference's dot * scale);
 //   softmax: workgroup max, exp(s - max) in LDS, workgroup sum;
-//   values: lane = dimension, the four waves take every fourth position.
-// splits == 1 writes acc / sum; otherwise the unnormalised (acc, max, sum) go
-// to the partials and q8_attn_combine rescales them by exp(max_s - max), the
-// same arithmetic as one softmax summed in another order (gpu.cu:735-762).
-// Dynamic LDS: ceil(capacity / splits) floats of weights.
+//   values: 16 lanes per value row (8 bytes = 4 dims each), 64 rows per pass;
+//           the 64 row slots are summed by xor shuffles inside a wave and in
+//           LDS across the waves, in a fixed order.
+// splits == 1 (contexts up to 2K positions) writes acc / sum.  Otherwise each
+// workgroup stores its unnormalised (acc, max, sum) with agent-scope atomic
+// stores and the last workgroup of the head to arrive (an arrival counter,
+// reset by it) rescales them by exp(max_s - max) and writes the row: the same
+// arithmetic as one softmax summed in another order (gpu.cu attention_combine
+// 735-762), in one launch.  Dynamic LDS: ceil(capacity / splits) floats.
 // ---------------------------------------------------------------------------
 static __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -100,12 +106,18 @@ static __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-extern "C" __global__ __launch_bounds__(256) void q8_attn_decode(Q8AttnDecodeArgs a) {
-    extern __shared__ __attribute__((aligned(16))) float wsm[];
-    __shared__ __attribute__((aligned(16))) float qs[Q8_ATTN_HEAD_DIM];
-    __shared__ float red[8];
-    __shared__ float part[4][Q8_ATTN_HEAD_DIM];
+#define Q8_ATTN_DEC_WAVES 16
+#define Q8_ATTN_KPASS 4  /* key rows per thread-group loaded before the dots: 4 x 128 rows */
+#define Q8_ATTN_VPASS 4  /* value rows per lane group loaded before the sums: 4 x 64 rows */
+extern "C" __global__ __launch_bounds__(64 * Q8_ATTN_DEC_WAVES) void q8_attn_decode(Q8AttnDecodeArgs a) {
+    constexpr int W = Q8_ATTN_DEC_WAVES;
+    constexpr int T = 64 * W;
     constexpr int HD = Q8_ATTN_HEAD_DIM;
+    extern __shared__ __attribute__((aligned(16))) float wsm[];
+    __shared__ __attribute__((aligned(16))) float qs[HD];
+    __shared__ float red[2 * W];
+    __shared__ __attribute__((aligned(16))) float part[W][HD];
+    __shared__ int last_flag;
     const int head = blockIdx.x / a.splits;
     const int split = blockIdx.x - head * a.splits;
     const int kvh = head / (a.n_head / a.n_kv);
@@ -120,228 +132,342 @@ extern "C" __global__ __launch_bounds__(256) void q8_attn_decode(Q8AttnDecodeArg
     if (tid < HD) qs[tid] = a.q[(size_t)head * HD + tid];
     __syncthreads();
 
+    // scores: thread -> row slot tid / 8 (128 per pass), dims 8 (tid % 8) .. +7
+    const int kc = tid & 7;
+    const f32x4 q0 = *(const f32x4 *)(qs + 8 * kc);
+    const f32x4 q1 = *(const f32x4 *)(qs + 8 * kc + 4);
+    const uint16_t *kbase = a.kcache + kvh * HD + 8 * kc;
     float mx = -INFINITY;
-    for (int p = begin + tid; p < end; p += 256) {
-        const uint16_t *kr = a.kcache + (size_t)p * kv_dim + kvh * HD;
-        float dot = 0.0f;
+    for (int p0 = begin + (tid >> 3); p0 < end; p0 += (T / 8) * Q8_ATTN_KPASS) {
+        i32x4 u[Q8_ATTN_KPASS];
 #pragma unroll
-        for (int c = 0; c < HD / 8; c++) {
-            const i32x4 u = *(const i32x4 *)(kr + 8 * c);
-            const f32x4 q0 = *(const f32x4 *)(qs + 8 * c);
-            const f32x4 q1 = *(const f32x4 *)(qs + 8 * c + 4);
-            dot = __builtin_fmaf(q0[0], f16_to_f32((unsigned)u[0] & 0xffffu), dot);
-            dot = __builtin_fmaf(q0[1], f16_to_f32((unsigned)u[0] >> 16), dot);
-            dot = __builtin_fmaf(q0[2], f16_to_f32((unsigned)u[1] & 0xffffu), dot);
-            dot = __builtin_fmaf(q0[3], f16_to_f32((unsigned)u[1] >> 16), dot);
-            dot = __builtin_fmaf(q1[0], f16_to_f32((unsigned)u[2] & 0xffffu), dot);
-            dot = __builtin_fmaf(q1[1], f16_to_f32((unsigned)u[2] >> 16), dot);
-            dot = __builtin_fmaf(q1[2], f16_to_f32((unsigned)u[3] & 0xffffu), dot);
-            dot = __builtin_fmaf(q1[3], f16_to_f32((unsigned)u[3] >> 16), dot);
+        for (int j = 0; j < Q8_ATTN_KPASS; j++) {
+            const int p = min(p0 + (T / 8) * j, end - 1);  // clamped in-bounds; the score is not kept past end
+            u[j] = *(const i32x4 *)(kbase + (size_t)p * kv_dim);
         }
-        const float s = dot * a.scale;
-        wsm[p - begin] = s;
-        mx = fmaxf(mx, s);
+#pragma unroll
+        for (int j = 0; j < Q8_ATTN_KPASS; j++) {
+            float dot = 0.0f;
+            dot = __builtin_fmaf(q0[0], f16_to_f32((unsigned)u[j][0] & 0xffffu), dot);
+            dot = __builtin_fmaf(q0[1], f16_to_f32((unsigned)u[j][0] >> 16), dot);
+            dot = __builtin_fmaf(q0[2], f16_to_f32((unsigned)u[j][1] & 0xffffu), dot);
+            dot = __builtin_fmaf(q0[3], f16_to_f32((unsigned)u[j][1] >> 16), dot);
+            dot = __builtin_fmaf(q1[0], f16_to_f32((unsigned)u[j][2] & 0xffffu), dot);
+            dot = __builtin_fmaf(q1[1], f16_to_f32((unsigned)u[j][2] >> 16), dot);
+            dot = __builtin_fmaf(q1[2], f16_to_f32((unsigned)u[j][3] & 0xffffu), dot);
+            dot = __builtin_fmaf(q1[3], f16_to_f32((unsigned)u[j][3] >> 16), dot);
+            dot += __shfl_xor(dot, 1);
+            dot += __shfl_xor(dot, 2);
+            dot += __shfl_xor(dot, 4);
+            const int p = p0 + (T / 8) * j;
+            if (p < end) {
+                const float s = dot * a.scale;
+                if (kc == 0) wsm[p - begin] = s;
+                mx = fmaxf(mx, s);
+            }
+        }
     }
     mx = wave_max(mx);
     if (lane == 0) red[wave] = mx;
     __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    mx = red[0];
+#pragma unroll
+    for (int w = 1; w < W; w++) mx = fmaxf(mx, red[w]);
     float sum = 0.0f;
-    for (int p = begin + tid; p < end; p += 256) {
+    for (int p = begin + tid; p < end; p += T) {
         const float e = expf(wsm[p - begin] - mx);
         wsm[p - begin] = e;
         sum += e;
     }
     sum = wave_sum(sum);
-    if (lane == 0) red[4 + wave] = sum;
+    if (lane == 0) red[W + wave] = sum;
     __syncthreads();  // weights and partial sums complete
-    sum = (red[4] + red[5]) + (red[6] + red[7]);
+    sum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; w++) sum += red[W + w];
 
-    float acc = 0.0f;
-    const uint16_t *vcol = a.vcache + kvh * HD + lane;
-    for (int p = begin + wave; p < end; p += 4)
-        acc = __builtin_fmaf(wsm[p - begin], f16_to_f32(vcol[(size_t)p * kv_dim]), acc);
-    part[wave][lane] = acc;
-    __syncthreads();
-    if (wave == 0) {
-        const float tot = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
-        if (a.splits == 1) {
-            a.out[(size_t)head * HD + lane] = tot / sum;
-        } else {
-            const size_t slot = (size_t)head * a.splits + split;
-            a.part_acc[slot * HD + lane] = tot;
-            if (lane == 0) {
-                a.part_max[slot] = mx;
-                a.part_sum[slot] = sum;
+    // values: thread -> row slot tid / 16 (64 per pass), dims 4 (tid % 16) .. +3
+    const int vg = tid & 15;
+    const uint16_t *vbase = a.vcache + kvh * HD + 4 * vg;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int p0 = begin + (tid >> 4); p0 < end; p0 += (T / 16) * Q8_ATTN_VPASS) {
+        unsigned long long u[Q8_ATTN_VPASS];
+#pragma unroll
+        for (int j = 0; j < Q8_ATTN_VPASS; j++) {
+            const int p = min(p0 + (T / 16) * j, end - 1);
+            u[j] = *(const unsigned long long *)(vbase + (size_t)p * kv_dim);
+        }
+#pragma unroll
+        for (int j = 0; j < Q8_ATTN_VPASS; j++) {
+            const int p = p0 + (T / 16) * j;
+            if (p < end) {
+                const float w = wsm[p - begin];
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    acc[e] = __builtin_fmaf(w, f16_to_f32((unsigned)(u[j] >> (16 * e)) & 0xffffu), acc[e]);
             }
         }
     }
-}
-
-extern "C" __global__ __launch_bounds__(64) void q8_attn_combine(Q8AttnDecodeArgs a) {
-    constexpr int HD = Q8_ATTN_HEAD_DIM;
-    const int head = blockIdx.x;
-    const int d = threadIdx.x;
+    // the four row slots of a wave (lanes vg, vg+16, vg+32, vg+48), then the waves
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        acc[e] += __shfl_xor(acc[e], 16);
+        acc[e] += __shfl_xor(acc[e], 32);
+    }
+    if (lane < 16) {
+        const f32x4 v4 = {acc[0], acc[1], acc[2], acc[3]};
+        *(f32x4 *)(&part[wave][4 * vg]) = v4;
+    }
+    __syncthreads();
+    if (wave != 0) {
+        if (a.splits == 1) return;
+    }
+    float tot = 0.0f;
+    if (wave == 0) {
+#pragma unroll
+        for (int w = 0; w < W; w++) tot += part[w][lane];
+    }
+    if (a.splits == 1) {
+        a.out[(size_t)head * HD + lane] = tot / sum;
+        return;
+    }
     const size_t base = (size_t)head * a.splits;
+    if (wave == 0) {
+        store_agent(a.part_acc + (base + split) * HD + lane, tot);
+        if (lane == 0) {
+            store_agent(a.part_max + base + split, mx);
+            store_agent(a.part_sum + base + split, sum);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned old = atomicAdd(&a.counters[head], 1u);
+        last_flag = (old == (unsigned)(a.splits - 1));
+    }
+    __syncthreads();
+    if (!last_flag) return;
+    if (tid == 0) __hip_atomic_store(&a.counters[head], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (wave != 0) return;
     float gmax = -INFINITY;
-    for (int s = 0; s < a.splits; s++) gmax = fmaxf(gmax, a.part_max[base + s]);
+    for (int s = 0; s < a.splits; s++) gmax = fmaxf(gmax, load_agent(a.part_max + base + s));
     float num = 0.0f, den = 0.0f;
     for (int s = 0; s < a.splits; s++) {
-        const float f = expf(a.part_max[base + s] - gmax);  // an empty split has max -inf: f = 0
-        den += a.part_sum[base + s] * f;
-        num += a.part_acc[(base + s) * HD + d] * f;
+        const float f = expf(load_agent(a.part_max + base + s) - gmax);  // an empty split has max -inf: f = 0
+        den += load_agent(a.part_sum + base + s) * f;
+        num += load_agent(a.part_acc + (base + s) * HD + lane) * f;
     }
-    a.out[(size_t)head * HD + d] = num / den;
+    a.out[(size_t)head * HD + lane] = num / den;
 }
 
 // ---------------------------------------------------------------------------
 // Prefill attention: n query tokens at cache positions start .. start+n-1, each
-// seeing keys 0 .. its own position (causal).  Workgroup = (head, 64-query
-// tile), 256 threads; thread (qi, kj) = (tid / 16, tid % 16) owns queries
-// 4qi..4qi+3 and, per 64-key tile, keys 4kj..4kj+3 of the scores and dims
-// 4kj..4kj+3 of the output.  LDS: Q^T and K^T ([dim][row], so a thread's four
-// rows are one 16-byte read), V and P^T, 64 KB.  Online softmax per query row
-// (running max and sum across key tiles, the 16 lanes of a row meeting by
-// xor shuffles), f32 throughout with f16 keys and values widened exactly.
-// Heavier (later) query tiles are launched first.
+// seeing keys 0 .. its own position (causal), on v_mfma_f32_32x32x16_f16.
+//
+// Workgroup = (head, 32 queries), two waves splitting the 64-key tiles (wave w
+// takes tiles w, w+2, ...), combined through LDS at the end.  Per tile a wave
+// computes S^T = K Q^T (keys x queries) and O^T += V^T P^T (dims x queries),
+// so a lane always holds one query (lane % 32): its scores, its running max
+// and sum, and its output accumulators, and the softmax needs no transpose.
+// f32 operands enter the MFMA exactly as two f16 parts (x = hi + lo, hi =
+// f16(x), lo = f16(x - hi), ~22 significant bits; products of f16 are exact
+// in f32): q for the scores, the probabilities for the values; keys and
+// values are the f16 cache itself.  Accumulation is f32.  Element k of an
+// MFMA operand sits in lane-half k / 8, slot k % 8, for A and B alike; D[m][n]
+// has n = lane % 32, m = 8(v/4) + 4(lane/32) + v%4.  Keys past the last
+// visible one read as zero values and -inf scores.  Heavier (later) query
+// tiles are launched first.
 // ---------------------------------------------------------------------------
-extern "C" __global__ __launch_bounds__(256) void q8_attn_prefill(Q8AttnPrefillArgs a) {
-    extern __shared__ __attribute__((aligned(16))) float psm_attn[];
+#define Q8_ATTN_VT_STRIDE 72  /* f16 per V^T row in LDS: 64 keys + 8 of padding, 144 B (16-byte rows) */
+
+static __device__ __forceinline__ void split_f16(const float *x, f16x8 &hi, f16x8 &lo) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const _Float16 h = (_Float16)x[i];
+        hi[i] = h;
+        lo[i] = (_Float16)(x[i] - (float)h);
+    }
+}
+
+extern "C" __global__ __launch_bounds__(128) void q8_attn_prefill(Q8AttnPrefillArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t vt_all[2][Q8_ATTN_HEAD_DIM * Q8_ATTN_VT_STRIDE];
+    __shared__ float xm[64], xl[64];
+    __shared__ __attribute__((aligned(16))) float xo[64][33];
     constexpr int HD = Q8_ATTN_HEAD_DIM;
-    constexpr int T = Q8_ATTN_TILE;
-    float *Qt = psm_attn;            // [HD][T]
-    float *Kt = Qt + HD * T;         // [HD][T]
-    float *Vs = Kt + HD * T;         // [T][HD]
-    float *Pt = Vs + T * HD;         // [T][T]  (key, query)
     const int head = blockIdx.x / a.qtiles;
     const int qt = a.qtiles - 1 - (blockIdx.x - head * a.qtiles);
     const int kvh = head / (a.n_head / a.n_kv);
     const int kv_dim = a.n_kv * HD;
     const int start = *a.position;
-    const int t0 = qt * T;
     const int tid = threadIdx.x;
-    const int qi = tid >> 4;
-    const int kj = tid & 15;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int h = lane >> 5;
+    const int r = lane & 31;
+    uint16_t *vt = vt_all[wave];
+    const int qrow = qt * 32 + r;  // this lane's query
+    const int qa = start + qrow;   // its cache position
+    const bool qlive = qrow < a.n;
+
+    // Q^T operand, d-step s: q[qrow][16s + 8h .. +7] as f16 hi/lo
+    f16x8 qhi[4], qlo[4];
     {
-        const int i = tid >> 2, qq = tid & 3;
-        const int t = t0 + i;
-        f32x4 v[4] = {};
-        if (t < a.n) {
-            const f32x4 *src = (const f32x4 *)(a.q + ((size_t)t * a.n_head + head) * HD + 16 * qq);
+        const float *src = a.q + ((size_t)min(qrow, a.n - 1) * a.n_head + head) * HD + 8 * h;
 #pragma unroll
-            for (int u = 0; u < 4; u++) v[u] = src[u];
+        for (int s = 0; s < 4; s++) {
+            f32x4 u0 = *(const f32x4 *)(src + 16 * s), u1 = *(const f32x4 *)(src + 16 * s + 4);
+            float x[8] = {u0[0], u0[1], u0[2], u0[3], u1[0], u1[1], u1[2], u1[3]};
+            if (!qlive)
+#pragma unroll
+                for (int i = 0; i < 8; i++) x[i] = 0.0f;
+            split_f16(x, qhi[s], qlo[s]);
         }
-#pragma unroll
-        for (int e = 0; e < 16; e++) Qt[(16 * qq + e) * T + i] = v[e >> 2][e & 3];
     }
-    float m[4], l[4], o[4][4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        m[r] = -INFINITY;
-        l[r] = 0.0f;
-#pragma unroll
-        for (int c = 0; c < 4; c++) o[r][c] = 0.0f;
-    }
-    const int last_q = min(t0 + T - 1, a.n - 1);
+    float m = -INFINITY, l = 0.0f;
+    f32x16 o[2] = {};
+    const f32x16 zero16 = {};
+    const int last_q = min(qt * 32 + 31, a.n - 1);
     const int kend = min(start + last_q + 1, a.capacity);  // keys [0, kend)
-    for (int p0 = 0; p0 < kend; p0 += T) {
-        __syncthreads();  // the previous tile's readers are done (and Qt is complete)
+    const int ntiles = (kend + 63) >> 6;
+    for (int t = wave; t < ntiles; t += 2) {
+        const int p0 = t * 64;
+        // K operand rows (keys p0 + 32kt + r), d-slices 16s + 8h: loads issued first
+        i32x4 kk[2][4];
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++) {
+            const int key = min(p0 + 32 * kt + r, a.capacity - 1);
+            const uint16_t *krow = a.kcache + (size_t)key * kv_dim + kvh * HD + 8 * h;
+#pragma unroll
+            for (int s = 0; s < 4; s++) kk[kt][s] = *(const i32x4 *)(krow + 16 * s);
+        }
+        // V^T tile (wave-private): lane -> dims 2(lane%32), +1 and keys 16(lane/32) .. +15 and +32
         {
-            const int j = tid >> 2, qq = tid & 3;
-            const int p = p0 + j;
-            i32x4 kw[2] = {}, vw[2] = {};
-            if (p < kend) {
-                const i32x4 *ks = (const i32x4 *)(a.kcache + (size_t)p * kv_dim + kvh * HD + 16 * qq);
-                const i32x4 *vsrc = (const i32x4 *)(a.vcache + (size_t)p * kv_dim + kvh * HD + 16 * qq);
-                kw[0] = ks[0];
-                kw[1] = ks[1];
-                vw[0] = vsrc[0];
-                vw[1] = vsrc[1];
-            }
+            const int dp = lane & 31;
 #pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const unsigned bits = ((unsigned)kw[e >> 3][(e >> 1) & 3] >> (16 * (e & 1))) & 0xffffu;
-                Kt[(16 * qq + e) * T + j] = f16_to_f32(bits);
-            }
+            for (int half_keys = 0; half_keys < 2; half_keys++) {
+                const int kb = 32 * half_keys + 16 * h;
+                unsigned w[16];
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                f32x4 w;
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const int f = 4 * u + e;
-                    w[e] = f16_to_f32(((unsigned)vw[f >> 3][(f >> 1) & 3] >> (16 * (f & 1))) & 0xffffu);
+                for (int i = 0; i < 16; i++) {
+                    const int key = p0 + kb + i;
+                    w[i] = key < kend ? *(const unsigned *)(a.vcache + (size_t)key * kv_dim + kvh * HD + 2 * dp) : 0u;
                 }
-                *(f32x4 *)(Vs + j * HD + 16 * qq + 4 * u) = w;
+                i32x4 r0[2], r1[2];
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    r0[j >> 2][j & 3] = (int)__builtin_amdgcn_perm(w[2 * j + 1], w[2 * j], 0x05040100u);
+                    r1[j >> 2][j & 3] = (int)__builtin_amdgcn_perm(w[2 * j + 1], w[2 * j], 0x07060302u);
+                }
+                i32x4 *d0 = (i32x4 *)(vt + (2 * dp) * Q8_ATTN_VT_STRIDE + kb);
+                i32x4 *d1 = (i32x4 *)(vt + (2 * dp + 1) * Q8_ATTN_VT_STRIDE + kb);
+                d0[0] = r0[0];
+                d0[1] = r0[1];
+                d1[0] = r1[0];
+                d1[1] = r1[1];
             }
         }
-        __syncthreads();
-        float s[4][4];
+        // S^T: keys x queries
+        f32x16 st[2];
 #pragma unroll
-        for (int r = 0; r < 4; r++)
+        for (int kt = 0; kt < 2; kt++) {
+            f32x16 acc = zero16;
 #pragma unroll
-            for (int c = 0; c < 4; c++) s[r][c] = 0.0f;
-#pragma unroll 8
-        for (int d = 0; d < HD; d++) {
-            const f32x4 qv = *(const f32x4 *)(Qt + d * T + 4 * qi);
-            const f32x4 kv = *(const f32x4 *)(Kt + d * T + 4 * kj);
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-#pragma unroll
-                for (int c = 0; c < 4; c++) s[r][c] = __builtin_fmaf(qv[r], kv[c], s[r][c]);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int qa = start + t0 + 4 * qi + r;
-            float tm = -INFINITY;
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const int p = p0 + 4 * kj + c;
-                s[r][c] = (p <= qa) ? s[r][c] * a.scale : -INFINITY;
-                tm = fmaxf(tm, s[r][c]);
+            for (int s = 0; s < 4; s++) {
+                const f16x8 kv = __builtin_bit_cast(f16x8, kk[kt][s]);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kv, qhi[s], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kv, qlo[s], acc, 0, 0, 0);
             }
+            st[kt] = acc;
+        }
+        // scale, causal mask, online softmax for query qrow
+        float tm = -INFINITY;
 #pragma unroll
-            for (int sh = 1; sh < 16; sh <<= 1) tm = fmaxf(tm, __shfl_xor(tm, sh));
-            // key 0 is in the first tile and visible to every query, so m is
-            // finite from the first tile on and mn never -inf
-            const float mn = fmaxf(m[r], tm);
-            const float corr = expf(m[r] - mn);
-            float rs = 0.0f;
+        for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-            for (int c = 0; c < 4; c++) {
-                s[r][c] = expf(s[r][c] - mn);
-                rs += s[r][c];
+            for (int v = 0; v < 16; v++) {
+                const int p = p0 + 32 * kt + 8 * (v >> 2) + 4 * h + (v & 3);
+                const float sc = (p <= qa) ? st[kt][v] * a.scale : -INFINITY;
+                st[kt][v] = sc;
+                tm = fmaxf(tm, sc);
             }
+        tm = fmaxf(tm, __shfl_xor(tm, 32));
+        const float mn = fmaxf(m, tm);
+        // a wave's first tile may be all masked for its queries only if it is
+        // not tile 0; then m and mn stay -inf: no weight and no rescale
+        const float corr = (mn == -INFINITY) ? 1.0f : expf(m - mn);
+        float rs = 0.0f;
 #pragma unroll
-            for (int sh = 1; sh < 16; sh <<= 1) rs += __shfl_xor(rs, sh);
-            l[r] = l[r] * corr + rs;
-            m[r] = mn;
+        for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-            for (int c = 0; c < 4; c++) o[r][c] *= corr;
+            for (int v = 0; v < 16; v++) {
+                const float e = (mn == -INFINITY) ? 0.0f : expf(st[kt][v] - mn);
+                st[kt][v] = e;
+                rs += e;
+            }
+        rs += __shfl_xor(rs, 32);
+        l = l * corr + rs;
+        m = mn;
+#pragma unroll
+        for (int dt = 0; dt < 2; dt++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) o[dt][v] *= corr;
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's V^T stores are done
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_wave_barrier();
+        // O^T += V^T P^T over four 16-key steps
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            float pv[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) pv[i] = st[j >> 1][8 * (j & 1) + i];
+            f16x8 phi, plo;
+            split_f16(pv, phi, plo);
+#pragma unroll
+            for (int dt = 0; dt < 2; dt++) {
+                const uint16_t *row = vt + (32 * dt + r) * Q8_ATTN_VT_STRIDE + 16 * j + 4 * h;
+                const uint2 lo4 = *(const uint2 *)row;
+                const uint2 hi4 = *(const uint2 *)(row + 8);
+                const i32x4 va = {(int)lo4.x, (int)lo4.y, (int)hi4.x, (int)hi4.y};
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, va), phi, o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, va), plo, o[dt], 0, 0, 0);
+            }
         }
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const f32x4 pc = {s[0][c], s[1][c], s[2][c], s[3][c]};
-            *(f32x4 *)(Pt + (4 * kj + c) * T + 4 * qi) = pc;
-        }
-        __syncthreads();
-#pragma unroll 8
-        for (int k = 0; k < T; k++) {
-            const f32x4 pv = *(const f32x4 *)(Pt + k * T + 4 * qi);
-            const f32x4 vv = *(const f32x4 *)(Vs + k * HD + 4 * kj);
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-#pragma unroll
-                for (int c = 0; c < 4; c++) o[r][c] = __builtin_fmaf(pv[r], vv[c], o[r][c]);
-        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // the tile's V^T reads are done before the next tile overwrites it
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_wave_barrier();
     }
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int t = t0 + 4 * qi + r;
-        if (t < a.n) {
-            const f32x4 res = {o[r][0] / l[r], o[r][1] / l[r], o[r][2] / l[r], o[r][3] / l[r]};
-            *(f32x4 *)(a.out + ((size_t)t * a.n_head + head) * HD + 4 * kj) = res;
+    // combine the two waves' partial softmax states (wave 1 -> LDS -> wave 0)
+    if (wave == 1) {
+        if (h == 0) {
+            xm[r] = m;
+            xl[r] = l;
         }
+#pragma unroll
+        for (int dt = 0; dt < 2; dt++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) xo[32 * dt + 8 * (v >> 2) + 4 * h + (v & 3)][r] = o[dt][v];
     }
+    __syncthreads();
+    if (wave == 1 || !qlive) return;
+    const float m1 = xm[r], l1 = xl[r];
+    const float mt = fmaxf(m, m1);  // finite: key 0 is in tile 0 (wave 0) and visible to every query
+    const float c0 = expf(m - mt);
+    const float c1 = (m1 == -INFINITY) ? 0.0f : expf(m1 - mt);
+    const float lt = l * c0 + l1 * c1;
+    float *orow = a.out + ((size_t)qrow * a.n_head + head) * HD;
+#pragma unroll
+    for (int dt = 0; dt < 2; dt++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            f32x4 res;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int v = 4 * g + e;
+                const int d = 32 * dt + 8 * g + 4 * h + e;
+                res[e] = (o[dt][v] * c0 + xo[d][r] * c1) / lt;
+            }
+            *(f32x4 *)(orow + 32 * dt + 8 * g + 4 * h) = res;
+        }
 }
 
 // ---------------------------------------------------------------------------

@@ -91,9 +91,9 @@ struct q8_decoder {
         graphs.clear();
     }
     int splits_for(int visible) const {
-        // about 64 positions per decode workgroup, at most 16 per head
-        int s = (visible + 63) / 64;
-        return s < 1 ? 1 : s > 16 ? 16 : s;
+        // one 16-wave workgroup per head up to 2048 visible positions (no
+        // cross-workgroup combine); beyond, about 1024 positions per workgroup
+        return visible <= 2048 ? 1 : (visible + 1023) / 1024;
     }
     int body(int n, int splits);
     int run(int n, int splits);

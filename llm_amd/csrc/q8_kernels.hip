@@ -1491,6 +1491,56 @@ extern "C" __global__ __launch_bounds__(256) void q8_rmsnorm(Q8NormArgs a) {
     }
 }
 
+// RMSNorm of single rows to f32 (the decode step's norms): a 256-thread
+// workgroup per row.  Each thread loads its float4s of x and w once, up front
+// (k <= 256 * 4 * Q8_NORM_ROW_VEC), adds its squares in f64, the waves meet in
+// LDS in a fixed order, and the row is scaled from registers: one memory round
+// trip where the wave-per-row kernel above makes one per 256 elements.  The f64
+// sum is the same set of f32 terms as there, in another order.
+#define Q8_NORM_ROW_VEC 8
+extern "C" __global__ __launch_bounds__(256) void q8_rmsnorm_row(Q8NormArgs a) {
+    __shared__ double part[4];
+    const int tid = threadIdx.x;
+    const int k = a.k;
+    const int nv = k >> 2;
+    const f32x4 *xr = (const f32x4 *)(a.x + (size_t)blockIdx.x * k);
+    const f32x4 *wr = (const f32x4 *)a.w;
+    f32x4 xv[Q8_NORM_ROW_VEC], wv[Q8_NORM_ROW_VEC];
+#pragma unroll
+    for (int j = 0; j < Q8_NORM_ROW_VEC; j++) {
+        const int i = tid + 256 * j;
+        const int ic = min(i, nv - 1);  // clamped in-bounds address; the value is unused past nv
+        xv[j] = xr[ic];
+        wv[j] = wr[ic];
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < Q8_NORM_ROW_VEC; j++) {
+        if (tid + 256 * j < nv) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) ss += (double)(xv[j][e] * xv[j][e]);
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    if ((tid & 63) == 0) part[tid >> 6] = ss;
+    __syncthreads();
+    const double total = (part[0] + part[1]) + (part[2] + part[3]);
+    const float mean_square = (float)(total / (double)k);
+    const float scale = 1.0f / sqrtf(mean_square + a.eps);
+    f32x4 *orow = (f32x4 *)(a.out + (size_t)blockIdx.x * k);
+#pragma unroll
+    for (int j = 0; j < Q8_NORM_ROW_VEC; j++) {
+        const int i = tid + 256 * j;
+        if (i < nv) {
+            f32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = (xv[j][e] * scale) * wv[j][e];
+            orow[i] = o;
+        }
+    }
+}
+
 extern "C" __global__ __launch_bounds__(256) void q8_silu_mul(Q8EltArgs a) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < a.len) a.act[i] = silu_f32(a.gate[i]) * a.up[i];

@@ -225,7 +225,8 @@ typedef struct {
     float *part_acc;        /* [n_head][splits][head_dim] unnormalised sums */
     float *part_max;        /* [n_head][splits] */
     float *part_sum;        /* [n_head][splits] */
-    float *out;             /* [n_head][head_dim]: written directly when splits == 1 */
+    float *out;             /* [n_head][head_dim] */
+    unsigned *counters;     /* splits > 1: arrivals per head, zero between launches */
     const int *position;    /* device: the token's cache position; it sees position + 1 keys */
     int n_head, n_kv, splits, capacity;
     float scale;

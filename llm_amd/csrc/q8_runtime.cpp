@@ -74,12 +74,12 @@ enum Fn {
     F_GEMM_H_T1_R4, F_GEMM_H_T2_R2, F_GEMM_H_T2_R4,
     F_GEMM_P_T1, F_GEMM_P_T2,
     F_GEMM_L_T1_R2, F_GEMM_L_T2_R2, F_GEMM_L_T2_R4,
-    F_RMSNORM,
+    F_RMSNORM, F_RMSNORM_ROW,
     F_ARGMAX,
     F_SILU_MUL,
     F_COPY,
     F_EMBED,
-    F_ROPE, F_ATTN_DECODE, F_ATTN_COMBINE, F_ATTN_PREFILL, F_SYNTH, F_ADVANCE,
+    F_ROPE, F_ATTN_DECODE, F_ATTN_PREFILL, F_SYNTH, F_ADVANCE,
     F_COUNT
 };
 
@@ -92,12 +92,12 @@ const char *const kFnNames[F_COUNT] = {
     "q8_gemm_h_t1_r4", "q8_gemm_h_t2_r2", "q8_gemm_h_t2_r4",
     "q8_gemm_p_t1", "q8_gemm_p_t2",
     "q8_gemm_l_t1_r2", "q8_gemm_l_t2_r2", "q8_gemm_l_t2_r4",
-    "q8_rmsnorm",
+    "q8_rmsnorm", "q8_rmsnorm_row",
     "q8_argmax",
     "q8_silu_mul",
     "q8_copy",
     "q8_embed",
-    "q8_rope_append", "q8_attn_decode", "q8_attn_combine", "q8_attn_prefill", "q8_synth", "q8_advance",
+    "q8_rope_append", "q8_attn_decode", "q8_attn_prefill", "q8_synth", "q8_advance",
 };
 
 constexpr int kArgmaxParts = 1024;
@@ -106,6 +106,10 @@ constexpr int kArgmaxParts = 1024;
 // the counters it used, so no memset is ever recorded into a graph).
 constexpr size_t kSplitBytes = 32u << 20;
 constexpr int kCounters = 65536;
+// Decode attention's per-head arrival counters live at the top of the same
+// array (the matmul split-K paths index from the bottom; launches on the one
+// stream never overlap, and each resets what it used).
+constexpr int kAttnCounterBase = 61440;
 constexpr size_t kAlign = 256;
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
@@ -578,6 +582,9 @@ int run_rmsnorm(q8_ctx *c, const float *x, int rows, int k, const float *w, floa
         p->k = k;
         p->format = fmt;
     }
+    // f32 rows only (the decode step's norms): a workgroup per row, the row
+    // loaded once (k <= 8192, four floats per thread per step)
+    if (!p && k <= 256 * 4 * 8) return launch(c, F_RMSNORM_ROW, (unsigned)rows, 256, 0, &a, sizeof a);
     return launch(c, F_RMSNORM, (unsigned)ceil_div(a.rows_launched, 4), 256, 0, &a, sizeof a);
 }
 
@@ -1288,6 +1295,9 @@ int q8_attention(q8_ctx *c, q8_dptr q, size_t q_offset, q8_dptr kcache, q8_dptr 
     if (n == 1) {
         if (splits < 1 || splits > 1024 || splits > capacity)
             return fail(Q8_ERR_INVALID, "attention: %d splits for capacity %d", splits, capacity);
+        if (n_head > kCounters - kAttnCounterBase)
+            return fail(Q8_ERR_UNSUPPORTED, "attention: %d heads exceed the %d arrival counters", n_head,
+                        kCounters - kAttnCounterBase);
         const size_t per = (size_t)ceil_div(capacity, splits);
         const size_t lds = per * 4;
         const size_t parts = (size_t)n_head * splits;
@@ -1301,15 +1311,14 @@ int q8_attention(q8_ctx *c, q8_dptr q, size_t q_offset, q8_dptr kcache, q8_dptr 
         a.part_max = a.part_acc ? a.part_acc + parts * head_dim : nullptr;
         a.part_sum = a.part_max ? a.part_max + parts : nullptr;
         a.out = reinterpret_cast<float *>(op);
+        a.counters = c->counters + kAttnCounterBase;
         a.position = reinterpret_cast<const int *>(position);
         a.n_head = n_head;
         a.n_kv = n_kv;
         a.splits = splits;
         a.capacity = capacity;
         a.scale = scale;
-        Q8_TRY(launch(c, F_ATTN_DECODE, (unsigned)parts, 256, (unsigned)lds, &a, sizeof a));
-        if (splits == 1) return Q8_OK;
-        return launch(c, F_ATTN_COMBINE, (unsigned)n_head, 64, 0, &a, sizeof a);
+        return launch(c, F_ATTN_DECODE, (unsigned)parts, 1024, (unsigned)lds, &a, sizeof a);
     }
     Q8AttnPrefillArgs a{};
     a.q = reinterpret_cast<const float *>(qp);
@@ -1321,10 +1330,9 @@ int q8_attention(q8_ctx *c, q8_dptr q, size_t q_offset, q8_dptr kcache, q8_dptr 
     a.n_head = n_head;
     a.n_kv = n_kv;
     a.capacity = capacity;
-    a.qtiles = (int)ceil_div(n, Q8_ATTN_TILE);
+    a.qtiles = (int)ceil_div(n, 32);
     a.scale = scale;
-    const unsigned lds = 4 * Q8_ATTN_TILE * Q8_ATTN_HEAD_DIM * 4;
-    return launch(c, F_ATTN_PREFILL, (unsigned)(n_head * a.qtiles), 256, lds, &a, sizeof a);
+    return launch(c, F_ATTN_PREFILL, (unsigned)(n_head * a.qtiles), 128, 0, &a, sizeof a);
 }
 
 int q8_advance_position(q8_ctx *c, q8_dptr position, int by) {
