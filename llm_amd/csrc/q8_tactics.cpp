@@ -86,22 +86,31 @@ void q8_gemv_shape(int out, int k, int cu_count, int slots, q8_tactic *t) {
 // down 33 us) and for small n.  Four tiles per wave needs ~240 VGPRs (two
 // waves per SIMD) and measured slower everywhere; it stays an option.
 void q8_gemm_shape(int n, int out, int k, int cu_count, q8_tactic *t) {
+    // Measured on gfx950 (n = 8 ... 1024, M = 2304 ... 11 520, K = 2304 / 5760):
+    // a wave costs a fixed prologue (first loads) and K reduction, so it wants
+    // at least ~9 block pairs of work, and the launch wants ~18 waves per CU
+    // (4.5 per SIMD) to hide the MFMA -> convert -> fma chain of each wave.
+    // Very tall matrices (gate|up, 360 row tiles) already have enough waves
+    // with two token tiles per wave and the full K; matrices of >= 128 row
+    // tiles pair two token-tile waves in a workgroup, which then share the
+    // weight units in L1.
     const int nb = k / 32;
     const int npairs = ceil_div(nb, 2);
     const int ttiles = ceil_div(n, 32);
     const int rtiles = ceil_div(out, 32);
     const int cus = std::max(cu_count, 1);
-    const int tpw = (rtiles >= 200 && ttiles >= 2) ? 2 : 1;
+    const int tpw = (rtiles >= 300 && ttiles >= 2) ? 2 : 1;
     const int groups = ceil_div(ttiles, tpw);
     const long long base = (long long)rtiles * groups;  // waves without a K split
-    const long long target = (tpw == 1 ? 36LL : 11LL) * cus;  // 9216 / 2816 waves on 256 CUs
+    const long long target = (tpw == 1 ? 18LL : 11LL) * cus;  // 4608 / 2816 waves on 256 CUs
     int kw = (int)std::max<long long>(1, (target + base - 1) / base);
-    kw = std::min(kw, std::max(1, npairs / 3));
+    kw = std::min(kw, std::max(1, npairs / 9));
     kw = std::min(kw, 8);
     const int ppw = ceil_div(npairs, kw);
     kw = ceil_div(npairs, ppw);
+    const int tw = (tpw == 1 && rtiles >= 128 && groups >= 2 && kw <= 8) ? 2 : 1;
     t->tpw = tpw;
-    t->twaves = 1;
+    t->twaves = tw;
     t->kwaves = kw;
     t->kslices = 1;
     t->pairs_per_wave = ppw;
