@@ -218,12 +218,23 @@ int q8_matmul_prompt_group(q8_ctx *ctx, const q8_group_entry *group, int count,
 /* The feed-forward gate/up pair with SiLU: act[t*ffn + i] =
  * silu(gate(x)_i) * up(x)_i (model.rs:1170-1215 with compute.rs:937-953).
  * n == 1: one fused launch (both GEMVs and the SiLU product in the epilogue).
- * n >= 2: one grouped GEMM into workspace, then the product: written to
- * `act` in f32 when `prepared` is NULL, otherwise quantized straight into
- * `prepared` for the down matmul and not written in f32 (as
- * Compute::silu_mul_prepare does, compute.rs:993-1019). */
+ * n >= 2: with `prepared`, the product goes to prepared Q8_0 for the down
+ * matmul and is never written in f32 (as Compute::silu_mul_prepare does,
+ * compute.rs:993-1019): x is quantized, then one gate/up GEMM whose epilogue
+ * quantizes silu(gate) * up (see q8_gate_up_silu_prepared).  Without it, one
+ * grouped GEMM into workspace, then the f32 product into `act`. */
 int q8_gate_up_silu(q8_ctx *ctx, const q8_weight *gate, const q8_weight *up, q8_dptr x,
                     size_t x_offset, int n, q8_dptr act, size_t act_offset, q8_prepared *prepared);
+
+/* The prompt form of the feed-forward pair on activations already prepared
+ * (by q8_norm_prepare or q8_prepare): Compute::matmul_prepared_group over
+ * gate and up (compute.rs:437-472) followed by silu_mul_prepare
+ * (compute.rs:993-1019), returning silu(gate) * up as prepared Q8_0 for the
+ * down matmul.  One launch for int8 prepared input (the GEMM's epilogue
+ * quantizes the product; bytes equal quantize_q8_0 of the f32 product); the
+ * output lives in a second workspace, so `x` stays valid.  n >= 2. */
+int q8_gate_up_silu_prepared(q8_ctx *ctx, const q8_weight *gate, const q8_weight *up, const q8_prepared *x,
+                             q8_prepared *out);
 
 /* lm_head GEMV on the last normed row plus the greedy argmax on the device:
  * model.rs:806-832 + sampler.rs:167-175.  Writes the logits and returns the

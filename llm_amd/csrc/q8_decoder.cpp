@@ -7,9 +7,9 @@
 //   attention: norm (f32 rows for one token, straight to prepared Q8_0 for a
 //              prompt), q/k/v as one grouped matmul, rope + f16 KV append,
 //              attention, output projection with the residual in its epilogue;
-//   feed-forward: norm, gate/up (one fused GEMV + SiLU for one token; grouped
-//              GEMM, then silu(gate)*up quantized for the down projection for
-//              a prompt), down projection with the residual;
+//   feed-forward: norm, gate/up (one fused GEMV + SiLU for one token; for a
+//              prompt one GEMM whose epilogue quantizes silu(gate)*up for the
+//              down projection), down projection with the residual;
 // then the output norm of the last row, the lm_head GEMV (the tied embedding)
 // and the greedy argmax, written to the token slot the next step embeds.
 //
@@ -153,10 +153,8 @@ int q8_decoder::body(int n, int splits) {
         } else {
             q8_prepared p{};
             DEC_TRY(q8_norm_prepare(c, x, 0, L.ffn_norm.data(), E, g.eps, n, &p));
-            q8_group_entry gu[2] = {{L.w[Q8_DEC_GATE], gate, 0}, {L.w[Q8_DEC_UP], up, 0}};
-            DEC_TRY(q8_matmul_prompt_group(c, gu, 2, &p, n, E, 0, 0));
             q8_prepared pd{};
-            DEC_TRY(q8_silu_mul_prepare(c, gate, up, n, g.n_ff, &pd));
+            DEC_TRY(q8_gate_up_silu_prepared(c, L.w[Q8_DEC_GATE], L.w[Q8_DEC_UP], &p, &pd));
             DEC_TRY(q8_matmul(c, L.w[Q8_DEC_DOWN], act, 0, n, x, 0, &pd, x, 0));
         }
     }

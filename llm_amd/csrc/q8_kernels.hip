@@ -850,6 +850,183 @@ static __device__ __forceinline__ void gemm_body(const Q8GemmArgs &a) {
 }
 
 // ---------------------------------------------------------------------------
+// Gate/up GEMM with silu(gate) * up quantized straight to prepared Q8_0 for the
+// down projection (Compute::silu_mul_prepare after matmul_prepared_group,
+// compute.rs:993-1019 and 437-472; gpu.cu silu_mul_quantize_rows 812-853).
+//
+// Members m[0] = gate and m[1] = up, same shape.  A workgroup owns gate row
+// tile g, the up row tile g and one token tile; its KW waves split the block
+// pairs.  A wave runs the int8 GEMM's per-block arithmetic (int32 block dot on
+// v_mfma_i32_32x32x32_i8, d_w * s_x from the outer-product MFMA, fma) on both
+// weight streams with one activation stream, so gate and up are exactly the
+// values the plain GEMM stores.  After the fixed-order K reduction, wave 0
+// forms v = silu(g) * u for its 32 features x 32 tokens: feature block g of
+// every token, one Q8_0 block each.  The tile goes through LDS from the MFMA
+// layout (lane = feature, 16 tokens) to the prepared lane order (lane =
+// token half, elements 8c + J[h][q]) and is quantized by quant_store, the
+// quantizer's own code: the bytes equal q8_quantize of silu(gate) * up.
+// LDS: max((KW - 1) * 2 accumulator sets, the 32 x 33 transpose).
+// ---------------------------------------------------------------------------
+struct SiluOps {
+    i32x4 w0, w1, u0, u1;
+    unsigned dw, du;
+    i32x4 x0, x1;
+    float sx;
+};
+
+extern "C" __global__ __launch_bounds__(512) void q8_gemm_silu(Q8GemmArgs a) {
+    extern __shared__ __attribute__((aligned(16))) float ssm[];
+    const int lane = threadIdx.x & 63;
+    const int kw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int KW = blockDim.x >> 6;
+    int wg = blockIdx.x;
+    if (a.xcd_remap) {
+        const int per = a.nwg >> 3;
+        wg = (wg & 7) * per + (wg >> 3);
+    }
+    const int g = wg / a.ttiles;   // gate (and up) row tile = output feature block
+    const int tt = wg - g * a.ttiles;
+    const Q8GemmMember gm = a.m[0], um = a.m[1];
+    const int nb = a.nb;
+    const int h = lane >> 5;
+    const int r = lane & 31;
+    const uint8_t *wq = gm.quants + (size_t)g * nb * Q8_UNIT_BYTES;
+    const uint16_t *wsc = gm.scales + (size_t)g * nb * Q8_TILE_ROWS;
+    const uint8_t *uq = um.quants + (size_t)g * nb * Q8_UNIT_BYTES;
+    const uint16_t *usc = um.scales + (size_t)g * nb * Q8_TILE_ROWS;
+    const uint8_t *xq = a.xq + (size_t)tt * nb * Q8_UNIT_BYTES;
+    const float *xsc = a.xs + (size_t)tt * nb * Q8_TILE_TOKENS;
+    const int lo = lane * 16;
+    const int npairs = (nb + 1) >> 1;
+    const int p_begin = kw * a.pairs_per_wave;
+    const int p_end = min(npairs, p_begin + a.pairs_per_wave);
+    const int full_end = min(p_end, nb >> 1);
+
+    f32x16 ag = {}, au = {};
+    const i32x16 izero = {};
+    const f32x32 fzero = {};
+    auto load_full = [&](SiluOps &q, int b) {
+        const size_t u0 = (size_t)b * Q8_UNIT_BYTES;
+        q.w0 = *(const i32x4 *)(wq + u0 + lo);
+        q.w1 = *(const i32x4 *)(wq + u0 + Q8_UNIT_BYTES + lo);
+        q.u0 = *(const i32x4 *)(uq + u0 + lo);
+        q.u1 = *(const i32x4 *)(uq + u0 + Q8_UNIT_BYTES + lo);
+        q.dw = wsc[(size_t)b * Q8_TILE_ROWS + lane];
+        q.du = usc[(size_t)b * Q8_TILE_ROWS + lane];
+        q.x0 = *(const i32x4 *)(xq + u0 + lo);
+        q.x1 = *(const i32x4 *)(xq + u0 + Q8_UNIT_BYTES + lo);
+        q.sx = xsc[(size_t)b * Q8_TILE_TOKENS + lane];
+    };
+    // the odd last block of an odd nb: the absent block repeats block b with zero scales
+    auto load_last = [&](SiluOps &q, int b) {
+        const size_t u0 = (size_t)b * Q8_UNIT_BYTES;
+        q.w0 = *(const i32x4 *)(wq + u0 + lo);
+        q.w1 = q.w0;
+        q.u0 = *(const i32x4 *)(uq + u0 + lo);
+        q.u1 = q.u0;
+        q.dw = h ? 0u : (unsigned)wsc[(size_t)b * Q8_TILE_ROWS + r];
+        q.du = h ? 0u : (unsigned)usc[(size_t)b * Q8_TILE_ROWS + r];
+        q.x0 = *(const i32x4 *)(xq + u0 + lo);
+        q.x1 = q.x0;
+        q.sx = h ? 0.0f : xsc[(size_t)b * Q8_TILE_TOKENS + r];
+    };
+    auto step = [&](const SiluOps &q, bool two) {
+        {
+            const f32x32 sc = __builtin_amdgcn_mfma_f32_32x32x1f32(q.sx, f16_to_f32(q.dw), fzero, 0, 0, 0);
+            const i32x16 i0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(q.x0, q.w0, izero, 0, 0, 0);
+            const i32x16 i1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(q.x1, q.w1, izero, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 16; i++) ag[i] = __builtin_fmaf((float)i0[i], sc[i], ag[i]);
+            if (two) {
+#pragma unroll
+                for (int i = 0; i < 16; i++) ag[i] = __builtin_fmaf((float)i1[i], sc[16 + i], ag[i]);
+            }
+        }
+        {
+            const f32x32 sc = __builtin_amdgcn_mfma_f32_32x32x1f32(q.sx, f16_to_f32(q.du), fzero, 0, 0, 0);
+            const i32x16 i0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(q.x0, q.u0, izero, 0, 0, 0);
+            const i32x16 i1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(q.x1, q.u1, izero, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 16; i++) au[i] = __builtin_fmaf((float)i0[i], sc[i], au[i]);
+            if (two) {
+#pragma unroll
+                for (int i = 0; i < 16; i++) au[i] = __builtin_fmaf((float)i1[i], sc[16 + i], au[i]);
+            }
+        }
+    };
+    if (p_begin < full_end) {
+        SiluOps qa, qb;
+        load_full(qa, 2 * p_begin);
+        int p = p_begin;
+        for (; p + 1 < full_end; p += 2) {
+            load_full(qb, 2 * (p + 1));
+            __builtin_amdgcn_sched_barrier(0);
+            step(qa, true);
+            __builtin_amdgcn_sched_barrier(0);
+            load_full(qa, 2 * min(p + 2, full_end - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            step(qb, true);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (p < full_end) step(qa, true);
+    }
+    if (full_end < p_end) {
+        SiluOps q;
+        load_last(q, 2 * full_end);
+        step(q, false);
+    }
+
+    if (KW > 1) {
+        // reduce the K-split waves in a fixed order: kw = 0 adds 1, 2, ...
+        if (kw > 0) {
+            float *dg = ssm + ((size_t)((kw - 1) * 2 + 0) * 64 + lane) * 16;
+            float *du = ssm + ((size_t)((kw - 1) * 2 + 1) * 64 + lane) * 16;
+#pragma unroll
+            for (int i = 0; i < 16; i += 4) {
+                *(f32x4 *)(dg + i) = (f32x4){ag[i], ag[i + 1], ag[i + 2], ag[i + 3]};
+                *(f32x4 *)(du + i) = (f32x4){au[i], au[i + 1], au[i + 2], au[i + 3]};
+            }
+        }
+        __syncthreads();
+        if (kw != 0) return;
+        for (int k2 = 1; k2 < KW; k2++) {
+            const float *sg = ssm + ((size_t)((k2 - 1) * 2 + 0) * 64 + lane) * 16;
+            const float *su = ssm + ((size_t)((k2 - 1) * 2 + 1) * 64 + lane) * 16;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                ag[i] = ag[i] + sg[i];
+                au[i] = au[i] + su[i];
+            }
+        }
+        // every wave > 0 has returned; wave 0's reads above complete before its
+        // transpose stores below (one wave's LDS operations stay in order)
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    }
+    // v = silu(gate) * up: lane (h, r) holds feature r of tokens 8(i/4) + 4h + i%4
+    float *tr = ssm;  // [32 tokens][33]
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int tok = 8 * (i >> 2) + 4 * h + (i & 3);
+        tr[tok * 33 + r] = silu_f32(ag[i]) * au[i];
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_wave_barrier();
+    // prepared order: lane (h, t = r) takes half h of token t's block: e[q][c] = element 8c + J[h][q]
+    float e[4][4];
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) e[q][c] = tr[r * 33 + 8 * c + perm_lane(h, q)];
+    float peak = half_peak(e);
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(peak), __float_as_uint(peak), false, false);
+    peak = fmaxf(peak, __uint_as_float(h ? sw[0] : sw[1]));
+    const int nbo = gm.rows / Q8_BLOCK_ELEMS;  // blocks per token of the down projection's input
+    quant_store(e, peak, a.oq, a.os, (size_t)tt * nbo + g, lane, h == 0, a.of16);
+}
+
+// ---------------------------------------------------------------------------
 // GEMM on the f16 MFMA, n >= 2, same arithmetic as above.
 //
 // Q8_0 quants are integers |q| <= 127, exact in f16; two

@@ -161,6 +161,9 @@ typedef struct {
     float *scratch;       /* S > 1: [rtiles][ttiles][S][64][16] partial tiles */
     unsigned *counters;   /* S > 1: arrivals per (row tile, token group), zero between launches */
     int rwaves;           /* f16 GEMM: row-tile waves per workgroup sharing the LDS-staged activations */
+    uint8_t *oq;          /* q8_gemm_silu: prepared Q8_0 output of silu(gate) * up (quants) */
+    float *os;            /* q8_gemm_silu: its scales */
+    int of16;             /* q8_gemm_silu: 1 = f16 prepared units */
 } Q8GemmArgs;
 
 typedef struct {

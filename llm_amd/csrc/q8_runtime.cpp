@@ -74,6 +74,7 @@ enum Fn {
     F_GEMM_H_T1_R4, F_GEMM_H_T2_R2, F_GEMM_H_T2_R4,
     F_GEMM_P_T1, F_GEMM_P_T2,
     F_GEMM_L_T1_R2, F_GEMM_L_T2_R2, F_GEMM_L_T2_R4,
+    F_GEMM_SILU,
     F_RMSNORM, F_RMSNORM_ROW,
     F_ARGMAX,
     F_SILU_MUL,
@@ -92,6 +93,7 @@ const char *const kFnNames[F_COUNT] = {
     "q8_gemm_h_t1_r4", "q8_gemm_h_t2_r2", "q8_gemm_h_t2_r4",
     "q8_gemm_p_t1", "q8_gemm_p_t2",
     "q8_gemm_l_t1_r2", "q8_gemm_l_t2_r2", "q8_gemm_l_t2_r4",
+    "q8_gemm_silu",
     "q8_rmsnorm", "q8_rmsnorm_row",
     "q8_argmax",
     "q8_silu_mul",
@@ -142,6 +144,8 @@ struct q8_ctx {
     size_t act_ws_bytes = 0;
     void *tmp_ws = nullptr;              // gate/up f32 products of the n >= 2 FFN pair
     size_t tmp_ws_bytes = 0;
+    void *act2_ws = nullptr;             // prepared silu(gate) * up written by the fused gate/up GEMM
+    size_t act2_ws_bytes = 0;
     void *argmax_ws = nullptr;           // per-workgroup partials + result
     float *split_ws = nullptr;           // partial results of split-K workgroups
     unsigned *counters = nullptr;        // split-K arrival counters (kernels reset them to 0)
@@ -390,6 +394,59 @@ int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const floa
 }
 
 int run_gemm_h(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n, const float *bias);
+
+// Gate/up GEMM whose epilogue writes silu(gate) * up as prepared Q8_0
+// (q8_gemm_silu) into the second activation workspace: the input stays
+// readable in the first.  int8 prepared input only.
+int run_gemm_silu(q8_ctx *c, const q8_weight *gate, const q8_weight *up, const q8_prepared *p, int n,
+                  q8_prepared *out) {
+    const int k = p->k, nb = k / 32, ffn = gate->out, nbo = ffn / 32;
+    const long long ttiles = ceil_div(n, 32);
+    const int fmt = prepared_format(c, n);
+    const size_t qbytes = (size_t)ttiles * nbo * (fmt == Q8_PREPARED_F16 ? Q8_UNIT_F16_BYTES : Q8_UNIT_BYTES);
+    const size_t sbytes = (size_t)ttiles * nbo * Q8_TILE_TOKENS * sizeof(float);
+    Q8_TRY(grow(c, &c->act2_ws, &c->act2_ws_bytes, align_up(qbytes, kAlign) + sbytes, "hipMalloc(activation 2)"));
+    Q8GemmArgs a{};
+    a.members = 2;
+    a.m[0] = {gate->quants, gate->scales, nullptr, nullptr, ffn, 0};
+    a.m[1] = {up->quants, up->scales, nullptr, nullptr, ffn, gate->tiles};
+    a.total_rtiles = gate->tiles;
+    a.xq = reinterpret_cast<const uint8_t *>(p->quants);
+    a.xs = reinterpret_cast<const float *>(p->scales);
+    a.n = n;
+    a.nb = nb;
+    a.ttiles = (int)ttiles;
+    a.twaves = 1;
+    a.tgroups = (int)ttiles;
+    a.kslices = 1;
+    const int npairs = (nb + 1) / 2;
+    a.pairs_per_slice = npairs;
+    // the int8 GEMM's rule (>= 18 waves per CU, >= 9 block pairs per wave)
+    const long long base = (long long)gate->tiles * ttiles;
+    int kw = (int)std::max<long long>(1, ceil_div(18LL * std::max(c->cu_count, 1), base));
+    kw = std::min(std::min(kw, 8), std::max(1, npairs / 9));
+    const int kw_opt = option(c, "gemm.kwaves", -1);
+    if (kw_opt > 0) kw = std::min(kw_opt, 8);
+    kw = std::min(kw, npairs);
+    const int ppw = (int)ceil_div(npairs, kw);
+    kw = (int)ceil_div(npairs, ppw);
+    a.pairs_per_wave = ppw;
+    const long long nwg = base;
+    if (nwg > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "gemm_silu: grid of %lld workgroups", nwg);
+    a.nwg = (int)nwg;
+    a.xcd_remap = nwg % 8 == 0 ? 1 : 0;
+    a.oq = static_cast<uint8_t *>(c->act2_ws);
+    a.os = reinterpret_cast<float *>(static_cast<uint8_t *>(c->act2_ws) + align_up(qbytes, kAlign));
+    a.of16 = fmt == Q8_PREPARED_F16 ? 1 : 0;
+    const unsigned lds = (unsigned)std::max<size_t>((size_t)(kw - 1) * 2 * 64 * 16 * sizeof(float), 32 * 33 * sizeof(float));
+    Q8_TRY(launch(c, F_GEMM_SILU, (unsigned)nwg, (unsigned)(64 * kw), lds, &a, sizeof a));
+    out->quants = (q8_dptr)(uintptr_t)a.oq;
+    out->scales = (q8_dptr)(uintptr_t)a.os;
+    out->n = n;
+    out->k = ffn;
+    out->format = fmt;
+    return Q8_OK;
+}
 
 int run_gemm(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n, const float *bias) {
     if (p->format == Q8_PREPARED_F16) return run_gemm_h(c, m, count, p, n, bias);
@@ -739,6 +796,7 @@ void q8_close(q8_ctx *c) {
     for (auto &kv : c->allocs) hipFree(reinterpret_cast<void *>(kv.first));
     if (c->act_ws) hipFree(c->act_ws);
     if (c->tmp_ws) hipFree(c->tmp_ws);
+    if (c->act2_ws) hipFree(c->act2_ws);
     if (c->argmax_ws) hipFree(c->argmax_ws);
     if (c->split_ws) hipFree(c->split_ws);
     if (c->counters) hipFree(c->counters);
@@ -778,7 +836,7 @@ int q8_set_option(q8_ctx *c, const char *name, int value) {
     static const char *const known[] = {"gemv.exact", "gemv.waves",  "gemv.pairs",     "gemv.slices",
                                         "gemm.smode", "gemm.tpw",    "gemm.twaves",    "gemm.xcd_remap",
                                         "gemm.kwaves", "gemm.slices", "gemm.rwaves",    "gemm.f16",
-                                        "gemm.pipe",  "gemm.lds"};
+                                        "gemm.pipe",  "gemm.lds",      "gemm.silu"};
     bool ok = false;
     for (const char *k : known) ok = ok || std::strcmp(k, name) == 0;
     if (!ok) return fail(Q8_ERR_INVALID, "unknown option %s", name);
@@ -1076,6 +1134,11 @@ int q8_gate_up_silu(q8_ctx *c, const q8_weight *gate, const q8_weight *up, q8_dp
             return Q8_OK;
         }
     }
+    if (n >= 2 && prepared && ffn % 32 == 0 && option(c, "gemm.silu", 1)) {
+        q8_prepared px{};
+        Q8_TRY(prepare_into(c, xp, 0, 0, n, k, &px));
+        if (px.format == Q8_PREPARED_I8) return run_gemm_silu(c, gate, up, &px, n, prepared);
+    }
     // gate and up products in f32 workspace, then the SiLU product.
     const size_t one = align_up((size_t)n * ffn * 4, kAlign);
     Q8_TRY(grow(c, &c->tmp_ws, &c->tmp_ws_bytes, 2 * one, "hipMalloc(ffn workspace)"));
@@ -1100,6 +1163,29 @@ int q8_gate_up_silu(q8_ctx *c, const q8_weight *gate, const q8_weight *up, q8_dp
     a.up = u;
     a.len = (long long)n * ffn;
     return launch(c, F_SILU_MUL, (unsigned)ceil_div(a.len, 256), 256, 0, &a, sizeof a);
+}
+
+int q8_gate_up_silu_prepared(q8_ctx *c, const q8_weight *gate, const q8_weight *up, const q8_prepared *x,
+                             q8_prepared *out) {
+    if (!c || !x || !out) return fail(Q8_ERR_INVALID, "q8_gate_up_silu_prepared: bad arguments");
+    Q8_TRY(check_weight(c, gate));
+    Q8_TRY(check_weight(c, up));
+    Q8_TRY(check_n(x->n));
+    if (gate->k != up->k || gate->out != up->out)
+        return fail(Q8_ERR_INVALID, "gate is %d x %d but up is %d x %d", gate->out, gate->k, up->out, up->k);
+    if (x->k != gate->k) return fail(Q8_ERR_INVALID, "prepared activations have k = %d, weights %d", x->k, gate->k);
+    if (x->n < 2) return fail(Q8_ERR_INVALID, "prepared activations are for n >= 2 (got %d)", x->n);
+    Q8_TRY(check_k(gate->out));
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    const int n = x->n, ffn = gate->out;
+    if (x->format == Q8_PREPARED_I8 && option(c, "gemm.silu", 1)) return run_gemm_silu(c, gate, up, x, n, out);
+    const size_t one = align_up((size_t)n * ffn * 4, kAlign);
+    Q8_TRY(grow(c, &c->tmp_ws, &c->tmp_ws_bytes, 2 * one, "hipMalloc(ffn workspace)"));
+    float *g = static_cast<float *>(c->tmp_ws);
+    float *u = reinterpret_cast<float *>(static_cast<uint8_t *>(c->tmp_ws) + one);
+    Member m[2] = {{gate, g}, {up, u}};
+    Q8_TRY(run_gemm(c, m, 2, x, n, nullptr));
+    return prepare_into(c, 0, (q8_dptr)(uintptr_t)g, (q8_dptr)(uintptr_t)u, n, ffn, out);
 }
 
 int q8_rmsnorm(q8_ctx *c, q8_dptr x, size_t x_offset, const float *weight, int k, float eps, int rows, q8_dptr out,

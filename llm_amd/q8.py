@@ -46,7 +46,7 @@ EXPORTS = (
     "q8_alloc", "q8_free", "q8_upload", "q8_download", "q8_sync",
     "q8_weight_resident", "q8_weight_release", "q8_weight_shape", "q8_weight_export",
     "q8_matmul", "q8_prepare", "q8_silu_mul_prepare", "q8_rmsnorm", "q8_norm_prepare", "q8_silu_mul",
-    "q8_matmul_decode_group", "q8_matmul_prompt_group", "q8_gate_up_silu",
+    "q8_matmul_decode_group", "q8_matmul_prompt_group", "q8_gate_up_silu", "q8_gate_up_silu_prepared",
     "q8_lm_head_argmax", "q8_argmax", "q8_copy_device", "q8_embeddings",
     "q8_plan", "q8_tactic_count", "q8_tactic_row",
     "q8_event_create", "q8_event_record", "q8_event_elapsed_ms", "q8_event_destroy",
@@ -165,6 +165,7 @@ def lib():
         "q8_matmul_prompt_group": (c_int, [vp, ctypes.POINTER(_GroupEntry), c_int, ctypes.POINTER(Prepared),
                                            c_int, c_int, u64, c_size]),
         "q8_gate_up_silu": (c_int, [vp, vp, vp, u64, c_size, c_int, u64, c_size, ctypes.POINTER(Prepared)]),
+        "q8_gate_up_silu_prepared": (c_int, [vp, vp, vp, ctypes.POINTER(Prepared), ctypes.POINTER(Prepared)]),
         "q8_lm_head_argmax": (c_int, [vp, vp, u64, c_size, u64, c_size, ctypes.POINTER(ctypes.c_uint32)]),
         "q8_argmax": (c_int, [vp, u64, c_size, c_size, ctypes.POINTER(ctypes.c_uint32)]),
         "q8_copy_device": (c_int, [vp, u64, u64, c_size]),
@@ -452,6 +453,13 @@ class Gpu:
         _check(lib().q8_gate_up_silu(self.handle, self.resident(gate), self.resident(up), x.ptr, x_offset,
                                      n, act.ptr, act_offset, ctypes.byref(p) if want_prepared else None))
         return p if want_prepared else None
+
+    def gate_up_silu_prepared(self, gate: Weight, up: Weight, prepared: Prepared) -> Prepared:
+        """matmul_prepared_group(gate, up) + silu_mul_prepare on prepared x (n >= 2)."""
+        out = Prepared()
+        _check(lib().q8_gate_up_silu_prepared(self.handle, self.resident(gate), self.resident(up),
+                                              ctypes.byref(prepared), ctypes.byref(out)))
+        return out
 
     def lm_head_argmax(self, weight: Weight, x: DeviceBuffer, x_offset: int, logits: DeviceBuffer,
                        logits_offset: int) -> int:

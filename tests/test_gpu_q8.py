@@ -23,7 +23,8 @@ TOL_REL = 1e-5
 SEED = 0x5EED
 J = [[0, 4, 1, 5], [2, 6, 3, 7]]
 OPTIONS = ("gemv.exact", "gemv.waves", "gemv.pairs", "gemv.slices", "gemm.smode", "gemm.tpw", "gemm.twaves",
-           "gemm.xcd_remap", "gemm.kwaves", "gemm.slices", "gemm.rwaves", "gemm.f16", "gemm.pipe", "gemm.lds")
+           "gemm.xcd_remap", "gemm.kwaves", "gemm.slices", "gemm.rwaves", "gemm.f16", "gemm.pipe", "gemm.lds",
+           "gemm.silu")
 
 
 def assert_close(got, ref, what):
@@ -605,6 +606,58 @@ def test_gate_up_silu(gpu, n, ffn):
     else:
         ge, ue = exact_matmul(gw.data, k, ffn, x, n), exact_matmul(uw.data, k, ffn, x, n)
         assert_parity(got, ref, ge / (1.0 + np.exp(-ge)) * ue, f"gate_up_silu n={n}")
+    for b in (xb, act):
+        b.free()
+    gpu.release(gw)
+    gpu.release(uw)
+
+
+@pytest.mark.parametrize("n,ffn,k", [(2, 640, 2304), (33, 96, 96), (130, 5760, 2304), (512, 320, 5760),
+                                     (64, 64, 32)])
+@pytest.mark.parametrize("kw", [1, 2, 3, 8])
+@pytest.mark.parametrize("entry", ["x", "prepared", "prepared_f16_out"])
+def test_gate_up_silu_fused_epilogue_equals_unfused(gpu, n, ffn, k, kw, entry):
+    """q8_gemm_silu (gate and up accumulated by one wave, silu(g) * u
+    quantized to Q8_0 in the epilogue) writes the same prepared bytes as the
+    int8 GEMM into f32 workspace followed by the SiLU-product quantization,
+    at the same K split; odd block counts and an f16 output plane included."""
+    r = rng(95 + n + ffn + k)
+    gw, uw = weight(r, ffn, k), weight(r, ffn, k)
+    x = oracle.make_activations(r, n, k, outlier_rate=0.01)
+    xb = gpu.alloc(4 * n * k)
+    xb.upload(x)
+    act = gpu.alloc(4 * n * ffn)
+    for name, value in (("gemm.f16", 0), ("gemm.tpw", 1), ("gemm.twaves", 1), ("gemm.slices", 1),
+                        ("gemm.pipe", 0), ("gemm.lds", 0), ("gemm.kwaves", kw)):
+        gpu.set_option(name, value)
+
+    def run(fused):
+        gpu.set_option("gemm.silu", fused)
+        if entry == "x":
+            p = gpu.gate_up_silu(gw, uw, xb, 0, n, act, 0, want_prepared=True)
+        else:
+            gpu.set_option("gemm.f16", 0)
+            px = gpu.prepare(xb, 0, n, k)
+            assert px.format == q8.PREPARED_I8
+            if entry == "prepared_f16_out":
+                gpu.set_option("gemm.f16", 1)   # int8 input, f16 output plane
+            p = gpu.gate_up_silu_prepared(gw, uw, px)
+        want_fmt = q8.PREPARED_F16 if entry == "prepared_f16_out" else q8.PREPARED_I8
+        assert p.format == want_fmt and p.n == n and p.k == ffn
+        return unpack_prepared(gpu, p, n, ffn)
+
+    q1, s1 = run(1)
+    q0, s0 = run(0)
+    what = f"gate_up_silu fused n={n} ffn={ffn} k={k} kw={kw} {entry}"
+    assert np.array_equal(s1, s0), f"{what}: scales differ"
+    assert np.array_equal(q1, q0), f"{what}: {int((q1 != q0).sum())} quants differ"
+    # and the bytes quantize the reference's product
+    g = oracle.matmul(gw.data, k, ffn, x, n)
+    u = oracle.matmul(uw.data, k, ffn, x, n)
+    ref = oracle.silu_mul(g, u).reshape(n, ffn)
+    deq = q1[:n].astype(np.float32).reshape(n, ffn // 32, 32) * s1[:n, :, None]
+    bound = 0.5 * s1[:n, :, None] * 1.001 + 1e-4 * np.abs(ref.reshape(n, ffn // 32, 32)) + 1e-5
+    assert np.all(np.abs(deq - ref.reshape(n, ffn // 32, 32)) <= bound), what
     for b in (xb, act):
         b.free()
     gpu.release(gw)
