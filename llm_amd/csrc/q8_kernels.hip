@@ -236,44 +236,96 @@ static __device__ __forceinline__ float chain_row(const float *row, int count) {
     return acc;
 }
 
-template <int PB, int EXACT>
+// ONE: a launch over one matrix (members == 1, no SiLU pair), whose fields
+// are read at static offsets with no selection.
+template <int PB, int EXACT, int ONE>
 static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
     extern __shared__ __attribute__((aligned(16))) float smem[];
     __shared__ int last_flag;
+    // The prologue up to the first weight load is one basic block: every
+    // argument is read at a static offset and the member is chosen with
+    // selects, so the kernel-argument loads issue in one round (each
+    // dependent round, e.g. a member indexed by a loaded value, delays the
+    // weight stream by a scalar-cache miss).
     const int nb = a.nb;
+    const int W = a.waves_per_tile;
+    const int S = a.kslices;
+    const int silu = ONE ? 0 : a.silu_pair;
+    const int members = ONE ? 1 : a.members;
+    const int ppw = a.pairs_per_wave;
+    const int pps = a.pairs_per_slice;
+    const float *xg = a.x;
+    const unsigned long long slice_magic = a.slice_magic;
+    // Every member's fields are read unconditionally and selected
+    // arithmetically below: a short-circuit condition would become a branch,
+    // and the loads after it a second round.
+    constexpr int NM = ONE ? 1 : Q8_GROUP_MAX;
+    const uint8_t *q_[Q8_GROUP_MAX];
+    const uint16_t *sc_[Q8_GROUP_MAX];
+    float *y_[Q8_GROUP_MAX];
+    const float *bias_[Q8_GROUP_MAX];
+    int rows_[Q8_GROUP_MAX], tb_[Q8_GROUP_MAX];
+#pragma unroll
+    for (int i = 0; i < NM; i++) {
+        q_[i] = a.m[i].quants;
+        sc_[i] = a.m[i].scales;
+        y_[i] = a.m[i].y;
+        bias_[i] = a.m[i].bias;
+        rows_[i] = a.m[i].rows;
+        tb_[i] = a.m[i].tile_begin;
+    }
+    if (ONE) {
+        // Everything the kernel reads, waited for together before any
+        // arithmetic (an asm is a scheduling boundary): left to itself the
+        // scheduler loads the matrix pointers in a second round.
+        asm volatile("" ::"s"(q_[0]), "s"(sc_[0]), "s"(y_[0]), "s"(bias_[0]), "s"(rows_[0]), "s"(xg), "s"(nb),
+                     "s"(W), "s"(S), "s"(ppw), "s"(pps), "s"(slice_magic));
+    }
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform, in an SGPR
-    const int W = a.waves_per_tile;
     const int h = lane >> 5;
     const int r = lane & 31;
-    const int slot = wave / W;  // member slot within the workgroup (silu mode: 0 gate, 1 up)
-    const int nslots = (blockDim.x >> 6) / W;
-    const int S = a.kslices;
-    const int slice = blockIdx.x % S;
-    const int gtile = blockIdx.x / S;  // global tile index (over the group's members)
+    // member slot within the workgroup: silu mode has two (0 gate, 1 up) of
+    // W waves each, every other launch one
+    const int slot = (silu && wave >= W) ? 1 : 0;
+    const int nslots = silu ? 2 : 1;
+    // global tile index (over the group's members) and K slice without a
+    // division: exact while workgroups * S < 2^32 (the host checks it)
+    const int gtile = (int)(((unsigned long long)blockIdx.x * slice_magic) >> 32);
+    const int slice = (int)blockIdx.x - gtile * S;
 
-    int mi, tile;
-    if (a.silu_pair) {
-        mi = slot;
-        tile = gtile;
-    } else {
-        tile = gtile;
-        mi = 0;
+    // silu mode: member = slot; otherwise the number of later members whose
+    // tiles begin at or before gtile (tile_begin ascends).
+    int by_tile = 0;
 #pragma unroll
-        for (int i = 1; i < Q8_GROUP_MAX; i++)
-            if (i < a.members && tile >= a.m[i].tile_begin) mi = i;
-        tile -= a.m[mi].tile_begin;
+    for (int i = 1; i < NM; i++) by_tile += (int)(i < members) & (int)(gtile >= tb_[i]);
+    const int mi = silu ? slot : by_tile;
+    const uint8_t *mq = q_[0];
+    const uint16_t *msc = sc_[0];
+    float *my = y_[0];
+    const float *mbias = bias_[0];
+    int mrows = rows_[0];
+    int mtb = tb_[0];
+#pragma unroll
+    for (int i = 1; i < NM; i++) {
+        const bool take = mi == i;
+        mq = take ? q_[i] : mq;
+        msc = take ? sc_[i] : msc;
+        my = take ? y_[i] : my;
+        mbias = take ? bias_[i] : mbias;
+        mrows = take ? rows_[i] : mrows;
+        mtb = take ? tb_[i] : mtb;
     }
-    const Q8GemvMember mem = a.m[mi];
+    const int tile = (ONE || silu) ? gtile : gtile - mtb;
     const int w = wave - slot * W;
     const int npairs = (nb + 1) >> 1;
-    const int s_begin = slice * a.pairs_per_slice;
-    const int s_end = min(npairs, s_begin + a.pairs_per_slice);
-    const int p_begin = s_begin + w * a.pairs_per_wave;
-    const int p_end = min(s_end, p_begin + a.pairs_per_wave);
+    const int s_begin = slice * pps;
+    const int s_end = min(npairs, s_begin + pps);
+    const int p_begin = s_begin + w * ppw;
+    const int p_end = min(s_end, p_begin + ppw);
     const int p_last = max(p_end - 1, 0);
-    const uint8_t *qbase = mem.quants + (size_t)tile * nb * Q8_UNIT_BYTES + lane * 16;
-    const uint16_t *sbase = mem.scales + (size_t)tile * nb * Q8_TILE_ROWS + r;
+    const uint8_t *qbase = mq + (size_t)tile * nb * Q8_UNIT_BYTES + lane * 16;
+    const uint16_t *sbase = msc + (size_t)tile * nb * Q8_TILE_ROWS + r;
 
     const int vrow = Q8_GEMV_VROW(nb);
     float *xs = smem;               // nb * 32 floats, permuted
@@ -282,27 +334,20 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
     // else [slots][tiles][S][32] per-slice row sums.
     float *gbuf = a.scratch;
 
-    // Exact mode: zero each row's tail up to a multiple of four blocks (read
-    // by the final sum as whole float4s).
-    if (EXACT && S == 1 && w == 0 && lane < 32) {
-        for (int b = nb; b < ((nb + 3) & ~3); b++) vbuf[(slot * 32 + r) * vrow + b] = 0.0f;
-    }
-
-    // Stores that have nothing to write go to this pad (after the exact-mode
-    // block values or the wave sums), so no store sits in an exec branch.
-    float *pad = vbuf + ((EXACT && S == 1) ? nslots * 32 * vrow : (blockDim.x >> 6) * 32);
-
     // This wave's range of x, issued first as natural-order float4s (LLVM
     // merges the four dword loads into one dwordx4, which gfx950 allows at
     // 4-byte alignment), so waiting for x does not wait for the weight
-    // stream issued after it.
+    // stream issued after it.  Lanes past the range's end re-read its last
+    // float4, so a wave asks L2 for no line outside its own range.
     const int st_begin = 16 * p_begin;  // float4 index: eight per block
     const int st_end = min(16 * p_end, nb * 8);
+    const int st_count = st_end - st_begin;  // <= 0 for a wave without pairs
+    const int st_clamp = max(st_end - 1, 0);
     f32x4 xv[Q8_GEMV_STAGE];
 #pragma unroll
     for (int u = 0; u < Q8_GEMV_STAGE; u++) {
-        const int i = min(st_begin + lane + 64 * u, nb * 8 - 1);
-        const float *xp = a.x + 4 * i;
+        const int i = min(st_begin + lane + 64 * u, st_clamp);
+        const float *xp = xg + 4 * i;
         xv[u] = (f32x4){xp[0], xp[1], xp[2], xp[3]};
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -325,6 +370,16 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
     Q8_GEMV_LOAD_BATCH(p_begin)
     __builtin_amdgcn_sched_barrier(0);
 
+    // Stores that have nothing to write go to this pad (after the exact-mode
+    // block values or the wave sums), so no store sits in an exec branch.
+    float *pad = vbuf + ((EXACT && S == 1) ? nslots * 32 * vrow : nslots * W * 32);
+
+    // Exact mode: zero each row's tail up to a multiple of four blocks (read
+    // by the final sum as whole float4s, after the workgroup barrier).
+    if (EXACT && S == 1 && w == 0 && lane < 32) {
+        for (int b = nb; b < ((nb + 3) & ~3); b++) vbuf[(slot * 32 + r) * vrow + b] = 0.0f;
+    }
+
     // Stage x into LDS, permuted: float4 slot s = 8b + 4hh + t holds
     // x[32b + 8c + J[hh][t]] in component c.  Natural float4 i holds elements
     // 8c + j0 .. 8c + j0 + 3 of block i/8 (c = (i%8)/2, j0 = 4(i%2)); element
@@ -333,12 +388,14 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
     // to the same range), so only a wave-level fence is needed.
 #pragma unroll
     for (int u = 0; u < Q8_GEMV_STAGE; u++) {
-        const int i = st_begin + lane + 64 * u;
-        float *d = i < st_end ? xs + (i >> 3) * 32 + ((i & 7) >> 1) + 4 * (i & 1) : pad;
-        d[0] = xv[u].x;
-        d[8] = xv[u].y;
-        d[16] = xv[u].z;
-        d[24] = xv[u].w;
+        if (64 * u < st_count) {
+            const int i = st_begin + lane + 64 * u;
+            float *d = i < st_end ? xs + (i >> 3) * 32 + ((i & 7) >> 1) + 4 * (i & 1) : pad;
+            d[0] = xv[u].x;
+            d[8] = xv[u].y;
+            d[16] = xv[u].z;
+            d[24] = xv[u].w;
+        }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -440,22 +497,26 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
         }
     }
     const int row = tile * Q8_TILE_ROWS + r;
-    if (a.silu_pair) {
-        if (row < a.m[0].rows) {
+    if (silu) {
+        // m[0] (gate) carries the output: in silu mode slot 0 is wave 0's
+        if (row < mrows) {
             const float act = silu_f32(sums[0]) * sums[1];
-            a.m[0].y[row] = act;
+            my[row] = act;
         }
-    } else if (row < mem.rows) {
-        const float out = mem.bias ? sums[0] + mem.bias[row] : sums[0];
-        mem.y[row] = out;
+    } else if (row < mrows) {
+        const float out = mbias ? sums[0] + mbias[row] : sums[0];
+        my[row] = out;
     }
 }
 
 // Batches of up to five pairs fit 1024-thread workgroups (<= 128 VGPRs); the
 // nine-pair batch keeps 512 threads.
-#define Q8_GEMV_KERNEL(PB, EXACT, THREADS)                                                              \
-    extern "C" __global__ __launch_bounds__(THREADS) void q8_gemv_pb##PB##_e##EXACT(Q8GemvArgs a) { \
-        gemv_body<PB, EXACT>(a);                                                                        \
+#define Q8_GEMV_KERNEL(PB, EXACT, THREADS)                                                               \
+    extern "C" __global__ __launch_bounds__(THREADS) void q8_gemv_pb##PB##_e##EXACT(Q8GemvArgs a) {  \
+        gemv_body<PB, EXACT, 0>(a);                                                                      \
+    }                                                                                                    \
+    extern "C" __global__ __launch_bounds__(THREADS) void q8_gemv1_pb##PB##_e##EXACT(Q8GemvArgs a) { \
+        gemv_body<PB, EXACT, 1>(a);                                                                      \
     }
 Q8_GEMV_KERNEL(2, 0, 1024)
 Q8_GEMV_KERNEL(2, 1, 1024)

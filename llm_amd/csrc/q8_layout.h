@@ -118,6 +118,7 @@ typedef struct {
     int pairs_per_slice; /* ceil(ceil(nb/2) / S) */
     float *scratch;      /* S > 1: partial results shared between a tile's workgroups */
     unsigned *counters;  /* S > 1: arrivals per tile, zero between launches */
+    unsigned long long slice_magic; /* ceil(2^32 / S): workgroup / S = (workgroup * magic) >> 32 */
 } Q8GemvArgs;
 
 typedef struct {

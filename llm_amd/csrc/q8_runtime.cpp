@@ -69,6 +69,7 @@ int hip_fail(hipError_t e, const char *op) {
 enum Fn {
     F_REPACK,
     F_GEMV_2_0, F_GEMV_2_1, F_GEMV_3_0, F_GEMV_3_1, F_GEMV_5_0, F_GEMV_5_1, F_GEMV_9_0, F_GEMV_9_1,
+    F_GEMV1_2_0, F_GEMV1_2_1, F_GEMV1_3_0, F_GEMV1_3_1, F_GEMV1_5_0, F_GEMV1_5_1, F_GEMV1_9_0, F_GEMV1_9_1,
     F_QUANTIZE,
     F_GEMM_S0_T1, F_GEMM_S1_T1, F_GEMM_S1_T2, F_GEMM_S1_T4,
     F_GEMM_H_T1_R4, F_GEMM_H_T2_R2, F_GEMM_H_T2_R4,
@@ -88,6 +89,8 @@ const char *const kFnNames[F_COUNT] = {
     "q8_repack",
     "q8_gemv_pb2_e0", "q8_gemv_pb2_e1", "q8_gemv_pb3_e0", "q8_gemv_pb3_e1",
     "q8_gemv_pb5_e0", "q8_gemv_pb5_e1", "q8_gemv_pb9_e0", "q8_gemv_pb9_e1",
+    "q8_gemv1_pb2_e0", "q8_gemv1_pb2_e1", "q8_gemv1_pb3_e0", "q8_gemv1_pb3_e1",
+    "q8_gemv1_pb5_e0", "q8_gemv1_pb5_e1", "q8_gemv1_pb9_e0", "q8_gemv1_pb9_e1",
     "q8_quantize",
     "q8_gemm_s0_t1", "q8_gemm_s1_t1", "q8_gemm_s1_t2", "q8_gemm_s1_t4",
     "q8_gemm_h_t1_r4", "q8_gemm_h_t2_r2", "q8_gemm_h_t2_r4",
@@ -325,13 +328,11 @@ q8_tactic plan(q8_ctx *c, int n, int out, int k, int slots = 1, int fmt = -1) {
     return t;
 }
 
-Fn gemv_fn(int pb, int exact) {
-    switch (pb) {
-        case 2: return exact ? F_GEMV_2_1 : F_GEMV_2_0;
-        case 3: return exact ? F_GEMV_3_1 : F_GEMV_3_0;
-        case 5: return exact ? F_GEMV_5_1 : F_GEMV_5_0;
-        default: return exact ? F_GEMV_9_1 : F_GEMV_9_0;
-    }
+// one: a launch over a single matrix (q8_gemv1_*, no member selection).
+Fn gemv_fn(int pb, int exact, bool one) {
+    const int base = one ? F_GEMV1_2_0 : F_GEMV_2_0;
+    const int i = pb == 2 ? 0 : pb == 3 ? 1 : pb == 5 ? 2 : 3;
+    return (Fn)(base + 2 * i + (exact ? 1 : 0));
 }
 
 int valid_pb(int pb) { return pb == 2 || pb == 3 || pb == 5 || pb == 9; }
@@ -371,6 +372,7 @@ int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const floa
     a.pairs_per_wave = t.pairs_per_wave;
     a.silu_pair = silu;
     a.kslices = t.kslices;
+    a.slice_magic = ((1ULL << 32) + (unsigned long long)t.kslices - 1) / (unsigned long long)t.kslices;
     a.pairs_per_slice = (int)ceil_div((nb + 1) / 2, t.kslices);
     a.scratch = c->split_ws;
     a.counters = c->counters;
@@ -387,10 +389,14 @@ int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const floa
     }
     const long long grid = (long long)a.total_tiles * t.kslices;
     if (grid > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "gemv: grid of %lld workgroups", grid);
+    // the kernel divides workgroup indices by S with slice_magic: exact below 2^32
+    if ((unsigned long long)grid * (unsigned long long)t.kslices >= (1ULL << 32))
+        return fail(Q8_ERR_UNSUPPORTED, "gemv: %lld workgroups in %d K slices", grid, t.kslices);
     const unsigned lds =
         (unsigned)(nb * 32 * 4 + ((t.exact && t.kslices == 1) ? slots * 32 * Q8_GEMV_VROW(nb) * 4 : waves * 32 * 4) +
                    Q8_GEMV_PAD_FLOATS * 4);
-    return launch(c, gemv_fn(pb, t.exact), (unsigned)grid, (unsigned)(waves * 64), lds, &a, sizeof a);
+    return launch(c, gemv_fn(pb, t.exact, count == 1 && !silu), (unsigned)grid, (unsigned)(waves * 64), lds, &a,
+                  sizeof a);
 }
 
 int run_gemm_h(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n, const float *bias);
@@ -421,9 +427,11 @@ int run_gemm_silu(q8_ctx *c, const q8_weight *gate, const q8_weight *up, const q
     a.kslices = 1;
     const int npairs = (nb + 1) / 2;
     a.pairs_per_slice = npairs;
-    // the int8 GEMM's rule (>= 18 waves per CU, >= 9 block pairs per wave)
+    // >= 11 waves per CU (each wave carries a gate and an up tile, as the
+    // paired-token-tile GEMM), >= 9 block pairs per wave; measured over
+    // n = 32..1024 at 5760 x 2304
     const long long base = (long long)gate->tiles * ttiles;
-    int kw = (int)std::max<long long>(1, ceil_div(18LL * std::max(c->cu_count, 1), base));
+    int kw = (int)std::max<long long>(1, ceil_div(11LL * std::max(c->cu_count, 1), base));
     kw = std::min(std::min(kw, 8), std::max(1, npairs / 9));
     const int kw_opt = option(c, "gemm.kwaves", -1);
     if (kw_opt > 0) kw = std::min(kw_opt, 8);
