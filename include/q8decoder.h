@@ -59,6 +59,22 @@ int q8_argmax_device(q8_ctx *ctx, q8_dptr values, size_t offset, size_t len, q8_
 /* *position += by, on the device (the end of a captured step). */
 int q8_advance_position(q8_ctx *ctx, q8_dptr position, int by);
 
+/* q8_rmsnorm (one row) followed by q8_matmul_decode_group on its output, with
+ * the norm folded into the GEMV launch: every workgroup recomputes the row's
+ * sum of squares exactly as the row norm kernel does, so the results are
+ * bit-identical to the two calls and the normalized row is never written.
+ * The reference runs the two steps apart (model.rs decode step: rmsnorm then
+ * matmul_decode_group); shapes whose GEMV needs a K split take the two-step
+ * path on the device.  `norm_weight` is a host f32[k] made resident like
+ * q8_rmsnorm's. */
+int q8_norm_matmul_decode_group(q8_ctx *ctx, const float *norm_weight, float eps, const q8_group_entry *group,
+                                int count, q8_dptr x, size_t x_offset, int k);
+
+/* q8_rmsnorm (one row) followed by q8_gate_up_silu at n = 1, folded the same
+ * way: act = silu(gate . xn) * (up . xn), xn = rmsnorm(x) * norm_weight. */
+int q8_norm_gate_up_silu(q8_ctx *ctx, const float *norm_weight, float eps, const q8_weight *gate,
+                         const q8_weight *up, q8_dptr x, size_t x_offset, q8_dptr act, size_t act_offset);
+
 /* A random-init out x k Q8_0 weight generated on the device from `seed`
  * (quants uniform in [-127, 127], scales f16(|N(0, scale_std)| / 127)),
  * owned by the context until q8_weight_release or q8_close.  No counterpart in

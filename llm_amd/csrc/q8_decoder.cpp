@@ -133,8 +133,7 @@ int q8_decoder::body(int n, int splits) {
         // attention block (dense_attention, model.rs:869-1043)
         q8_group_entry qkv[3] = {{L.w[Q8_DEC_Q], q, 0}, {L.w[Q8_DEC_K], k, 0}, {L.w[Q8_DEC_V], v, 0}};
         if (n == 1) {
-            DEC_TRY(q8_rmsnorm(c, x, 0, L.attn_norm.data(), E, g.eps, 1, normed, 0));
-            DEC_TRY(q8_matmul_decode_group(c, qkv, 3, normed, 0, E, 0, 0));
+            DEC_TRY(q8_norm_matmul_decode_group(c, L.attn_norm.data(), g.eps, qkv, 3, x, 0, E));
         } else {
             q8_prepared p{};
             DEC_TRY(q8_norm_prepare(c, x, 0, L.attn_norm.data(), E, g.eps, n, &p));
@@ -147,8 +146,7 @@ int q8_decoder::body(int n, int splits) {
         DEC_TRY(q8_matmul(c, L.w[Q8_DEC_O], attn, 0, n, x, 0, nullptr, x, 0));
         // feed-forward block (feed_forward, model.rs:1162-1235)
         if (n == 1) {
-            DEC_TRY(q8_rmsnorm(c, x, 0, L.ffn_norm.data(), E, g.eps, 1, normed, 0));
-            DEC_TRY(q8_gate_up_silu(c, L.w[Q8_DEC_GATE], L.w[Q8_DEC_UP], normed, 0, 1, act, 0, nullptr));
+            DEC_TRY(q8_norm_gate_up_silu(c, L.ffn_norm.data(), g.eps, L.w[Q8_DEC_GATE], L.w[Q8_DEC_UP], x, 0, act, 0));
             DEC_TRY(q8_matmul(c, L.w[Q8_DEC_DOWN], act, 0, 1, x, 0, nullptr, x, 0));
         } else {
             q8_prepared p{};

@@ -274,10 +274,10 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
         rows_[i] = a.m[i].rows;
         tb_[i] = a.m[i].tile_begin;
     }
+    // Single matrix: everything the kernel reads, waited for together before
+    // any arithmetic (an asm is a scheduling boundary): left to itself the
+    // scheduler loads the matrix pointers in a second round.
     if (ONE) {
-        // Everything the kernel reads, waited for together before any
-        // arithmetic (an asm is a scheduling boundary): left to itself the
-        // scheduler loads the matrix pointers in a second round.
         asm volatile("" ::"s"(q_[0]), "s"(sc_[0]), "s"(y_[0]), "s"(bias_[0]), "s"(rows_[0]), "s"(xg), "s"(nb),
                      "s"(W), "s"(S), "s"(ppw), "s"(pps), "s"(slice_magic));
     }
@@ -367,8 +367,59 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
         qb[i] = *(const i32x4 *)(qbase + (size_t)b1 * Q8_UNIT_BYTES);                 \
         dd[i] = (unsigned)sbase[(size_t)bs * Q8_TILE_ROWS];                           \
     }
+    // Folded RMSNorm (multi-matrix launches with norm_w set; the host
+    // guarantees one K slice, >= 256 threads and k <= 1024 * Q8_NORM_ROW_VEC):
+    // the norm weight over this wave's x range, and q8_rmsnorm_row's sum of
+    // squares term for term -- threads 0..255 take float4s tid + 256 j, j
+    // ascending, and reduce with the same shuffle tree and four-wave sum --
+    // so the staged values are bit-identical to that kernel's output.  These
+    // loads go out before the weight stream, so waiting for them does not
+    // wait for it.
+    const bool norm = !ONE && a.norm_w != nullptr;  // kernel-uniform
+    f32x4 wv[Q8_GEMV_STAGE];
+    double ss = 0.0;
+    if (norm) {
+        const f32x4 *nw = reinterpret_cast<const f32x4 *>(a.norm_w);
+#pragma unroll
+        for (int u = 0; u < Q8_GEMV_STAGE; u++) wv[u] = nw[min(st_begin + lane + 64 * u, st_clamp)];
+        if (threadIdx.x < 256) {
+            const f32x4 *xr = reinterpret_cast<const f32x4 *>(xg);
+            const int nv = nb * 8;
+            f32x4 nx[Q8_NORM_ROW_VEC];
+#pragma unroll
+            for (int j = 0; j < Q8_NORM_ROW_VEC; j++) nx[j] = xr[min((int)threadIdx.x + 256 * j, nv - 1)];
+#pragma unroll
+            for (int j = 0; j < Q8_NORM_ROW_VEC; j++) {
+                if ((int)threadIdx.x + 256 * j < nv) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) ss += (double)(nx[j][e] * nx[j][e]);
+                }
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
     Q8_GEMV_LOAD_BATCH(p_begin)
     __builtin_amdgcn_sched_barrier(0);
+
+    float nscale = 1.0f;
+    if (norm) {
+        __shared__ double npart[4];
+        if (threadIdx.x < 256) {
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+            if (lane == 0) npart[wave] = ss;
+        }
+        __syncthreads();
+        const double total_ss = (npart[0] + npart[1]) + (npart[2] + npart[3]);
+        const float mean_square = (float)(total_ss / (double)(nb * 32));
+        nscale = 1.0f / sqrtf(mean_square + a.norm_eps);
+#pragma unroll
+        for (int u = 0; u < Q8_GEMV_STAGE; u++) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) xv[u][e] = (xv[u][e] * nscale) * wv[u][e];
+        }
+    }
 
     // Stores that have nothing to write go to this pad (after the exact-mode
     // block values or the wave sums), so no store sits in an exec branch.
@@ -1735,7 +1786,6 @@ extern "C" __global__ __launch_bounds__(256) void q8_rmsnorm(Q8NormArgs a) {
 // LDS in a fixed order, and the row is scaled from registers: one memory round
 // trip where the wave-per-row kernel above makes one per 256 elements.  The f64
 // sum is the same set of f32 terms as there, in another order.
-#define Q8_NORM_ROW_VEC 8
 extern "C" __global__ __launch_bounds__(256) void q8_rmsnorm_row(Q8NormArgs a) {
     __shared__ double part[4];
     const int tid = threadIdx.x;

@@ -119,7 +119,12 @@ typedef struct {
     float *scratch;      /* S > 1: partial results shared between a tile's workgroups */
     unsigned *counters;  /* S > 1: arrivals per tile, zero between launches */
     unsigned long long slice_magic; /* ceil(2^32 / S): workgroup / S = (workgroup * magic) >> 32 */
+    const float *norm_w; /* non-null (multi-matrix kernels): x is rmsnorm(x) * norm_w, folded in */
+    float norm_eps;
 } Q8GemvArgs;
+
+/* float4s per thread of the 256-thread row RMSNorm (k <= 1024 * this). */
+#define Q8_NORM_ROW_VEC 8
 
 typedef struct {
     const float *x;    /* [n][k] f32 (mode 0) */

@@ -149,6 +149,8 @@ struct q8_ctx {
     size_t tmp_ws_bytes = 0;
     void *act2_ws = nullptr;             // prepared silu(gate) * up written by the fused gate/up GEMM
     size_t act2_ws_bytes = 0;
+    void *norm_ws = nullptr;             // rmsnorm(x) when a norm cannot fold into the decode GEMV
+    size_t norm_ws_bytes = 0;
     void *argmax_ws = nullptr;           // per-workgroup partials + result
     float *split_ws = nullptr;           // partial results of split-K workgroups
     unsigned *counters = nullptr;        // split-K arrival counters (kernels reset them to 0)
@@ -343,7 +345,10 @@ struct Member {
 };
 
 // n = 1 over up to four weights sharing x; silu = 1 fuses silu(m0)*m1 into y of m0.
-int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const float *bias, int silu) {
+// norm_w (device f32[k]) folds rmsnorm(x) * norm_w into a multi-matrix
+// launch; the caller checks gemv_folds_norm first.
+int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const float *bias, int silu,
+             const float *norm_w = nullptr, float norm_eps = 0.0f) {
     const int nb = k / 32;
     int rows_total = 0;
     Q8GemvArgs a{};
@@ -376,8 +381,12 @@ int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const floa
     a.pairs_per_slice = (int)ceil_div((nb + 1) / 2, t.kslices);
     a.scratch = c->split_ws;
     a.counters = c->counters;
+    a.norm_w = norm_w;
+    a.norm_eps = norm_eps;
     const int waves = t.waves_per_tile * slots;
     const int max_threads = pb == 9 ? 512 : 1024;
+    if (norm_w && (t.kslices != 1 || waves * 64 < 256 || k > 1024 * Q8_NORM_ROW_VEC))
+        return fail(Q8_ERR_UNSUPPORTED, "gemv: the folded norm needs one K slice and >= 256 threads");
     if (waves * 64 > max_threads)
         return fail(Q8_ERR_UNSUPPORTED, "gemv: %d waves per workgroup exceed the %d-thread launch bound", waves,
                     max_threads);
@@ -395,8 +404,35 @@ int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const floa
     const unsigned lds =
         (unsigned)(nb * 32 * 4 + ((t.exact && t.kslices == 1) ? slots * 32 * Q8_GEMV_VROW(nb) * 4 : waves * 32 * 4) +
                    Q8_GEMV_PAD_FLOATS * 4);
-    return launch(c, gemv_fn(pb, t.exact, count == 1 && !silu), (unsigned)grid, (unsigned)(waves * 64), lds, &a,
-                  sizeof a);
+    return launch(c, gemv_fn(pb, t.exact, count == 1 && !silu && !norm_w), (unsigned)grid, (unsigned)(waves * 64),
+                  lds, &a, sizeof a);
+}
+
+// Whether run_gemv can fold an RMSNorm into this launch: one K slice (each
+// workgroup sees all of x), >= 256 threads (the row norm's reduction shape)
+// and k within the row norm's reach.
+bool gemv_folds_norm(q8_ctx *c, const Member *m, int count, int k, int silu) {
+    int rows_total = 0;
+    for (int i = 0; i < count; i++) rows_total += m[i].w->out;
+    const int slots = silu ? 2 : 1;
+    const q8_tactic t = plan(c, 1, silu ? m[0].w->out : rows_total, k, slots);
+    const int pb = valid_pb(t.pairs_per_batch) ? t.pairs_per_batch : 5;
+    const int waves = t.waves_per_tile * slots;
+    return t.kslices == 1 && t.pairs_per_wave <= 12 && waves * 64 >= 256 && waves * 64 <= (pb == 9 ? 512 : 1024) &&
+           k <= 1024 * Q8_NORM_ROW_VEC;
+}
+
+int run_rmsnorm(q8_ctx *c, const float *x, int rows, int k, const float *w, float eps, float *out, q8_prepared *p);
+
+// rmsnorm(x) * norm_w then a decode GEMV: folded into one launch when it
+// fits, else the row norm into the norm workspace first.
+int run_norm_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, int silu, const float *norm_w,
+                  float eps) {
+    if (gemv_folds_norm(c, m, count, k, silu)) return run_gemv(c, m, count, x, k, nullptr, silu, norm_w, eps);
+    Q8_TRY(grow(c, &c->norm_ws, &c->norm_ws_bytes, (size_t)k * sizeof(float), "hipMalloc(norm workspace)"));
+    float *xn = static_cast<float *>(c->norm_ws);
+    Q8_TRY(run_rmsnorm(c, reinterpret_cast<const float *>(x), 1, k, norm_w, eps, xn, nullptr));
+    return run_gemv(c, m, count, (q8_dptr)(uintptr_t)xn, k, nullptr, silu);
 }
 
 int run_gemm_h(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n, const float *bias);
@@ -805,6 +841,7 @@ void q8_close(q8_ctx *c) {
     if (c->act_ws) hipFree(c->act_ws);
     if (c->tmp_ws) hipFree(c->tmp_ws);
     if (c->act2_ws) hipFree(c->act2_ws);
+    if (c->norm_ws) hipFree(c->norm_ws);
     if (c->argmax_ws) hipFree(c->argmax_ws);
     if (c->split_ws) hipFree(c->split_ws);
     if (c->counters) hipFree(c->counters);
@@ -1171,6 +1208,53 @@ int q8_gate_up_silu(q8_ctx *c, const q8_weight *gate, const q8_weight *up, q8_dp
     a.up = u;
     a.len = (long long)n * ffn;
     return launch(c, F_SILU_MUL, (unsigned)ceil_div(a.len, 256), 256, 0, &a, sizeof a);
+}
+
+int q8_norm_matmul_decode_group(q8_ctx *c, const float *norm_weight, float eps, const q8_group_entry *group,
+                                int count, q8_dptr x, size_t x_offset, int k) {
+    if (!c || !group || !norm_weight) return fail(Q8_ERR_INVALID, "q8_norm_matmul_decode_group: bad arguments");
+    if (count < 1 || count > Q8_GROUP_MAX)
+        return fail(Q8_ERR_INVALID, "decode matmul group holds one to four matrices (got %d)", count);
+    Q8_TRY(check_k(k));
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    Member m[Q8_GROUP_MAX];
+    for (int i = 0; i < count; i++) {
+        Q8_TRY(check_weight(c, group[i].weight));
+        if (group[i].weight->k != k) return fail(Q8_ERR_INVALID, "group member %d has k = %d, not %d", i, group[i].weight->k, k);
+        m[i].w = group[i].weight;
+        m[i].y = fptr(group[i].y, group[i].y_offset);
+        Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)m[i].y, (size_t)m[i].w->out * 4, "decode y"));
+    }
+    const q8_dptr xp = (q8_dptr)(uintptr_t)fptr(x, x_offset);
+    Q8_TRY(check_span(c, xp, (size_t)k * 4, "decode x"));
+    float *w = nullptr;
+    Q8_TRY(vector_resident(c, norm_weight, (size_t)k, &w));
+    return run_norm_gemv(c, m, count, xp, k, 0, w, eps);
+}
+
+int q8_norm_gate_up_silu(q8_ctx *c, const float *norm_weight, float eps, const q8_weight *gate, const q8_weight *up,
+                         q8_dptr x, size_t x_offset, q8_dptr act, size_t act_offset) {
+    if (!c || !norm_weight) return fail(Q8_ERR_INVALID, "q8_norm_gate_up_silu: bad arguments");
+    Q8_TRY(check_weight(c, gate));
+    Q8_TRY(check_weight(c, up));
+    if (gate->k != up->k || gate->out != up->out)
+        return fail(Q8_ERR_INVALID, "gate is %d x %d but up is %d x %d", gate->out, gate->k, up->out, up->k);
+    const int k = gate->k, ffn = gate->out;
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    float *actp = fptr(act, act_offset);
+    Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)actp, (size_t)ffn * 4, "gate_up act"));
+    const q8_dptr xp = (q8_dptr)(uintptr_t)fptr(x, x_offset);
+    Q8_TRY(check_span(c, xp, (size_t)k * 4, "gate_up x"));
+    float *w = nullptr;
+    Q8_TRY(vector_resident(c, norm_weight, (size_t)k, &w));
+    const q8_tactic t = plan(c, 1, ffn, k, 2);
+    Member m[2] = {{gate, actp}, {up, nullptr}};
+    if (t.pairs_per_wave <= 12 && t.waves_per_tile <= 8) return run_norm_gemv(c, m, 2, xp, k, 1, w, eps);
+    // the pair does not fit one launch: the norm, then the unfused gate/up path
+    Q8_TRY(grow(c, &c->norm_ws, &c->norm_ws_bytes, (size_t)k * sizeof(float), "hipMalloc(norm workspace)"));
+    float *xn = static_cast<float *>(c->norm_ws);
+    Q8_TRY(run_rmsnorm(c, reinterpret_cast<const float *>(xp), 1, k, w, eps, xn, nullptr));
+    return q8_gate_up_silu(c, gate, up, (q8_dptr)(uintptr_t)xn, 0, 1, act, act_offset, nullptr);
 }
 
 int q8_gate_up_silu_prepared(q8_ctx *c, const q8_weight *gate, const q8_weight *up, const q8_prepared *x,

@@ -56,6 +56,7 @@ EXPORTS = (
     "q8_gguf_meta_f32", "q8_gguf_meta_bool", "q8_gguf_meta_str", "q8_gguf_has_key_prefix",
     "q8_gguf_meta_i32_array", "q8_gguf_meta_f32_array", "q8_gguf_meta_str_array", "q8_gguf_weight",
     "q8_rope_append", "q8_attention", "q8_embeddings_device", "q8_argmax_device", "q8_advance_position",
+    "q8_norm_matmul_decode_group", "q8_norm_gate_up_silu",
     "q8_weight_synthetic", "q8_decoder_create_synthetic", "q8_decoder_destroy", "q8_decoder_reset",
     "q8_decoder_position", "q8_decoder_forward", "q8_decoder_generate", "q8_decoder_logits", "q8_decoder_weight",
     "q8_decoder_norm",
@@ -165,6 +166,9 @@ def lib():
         "q8_matmul_prompt_group": (c_int, [vp, ctypes.POINTER(_GroupEntry), c_int, ctypes.POINTER(Prepared),
                                            c_int, c_int, u64, c_size]),
         "q8_gate_up_silu": (c_int, [vp, vp, vp, u64, c_size, c_int, u64, c_size, ctypes.POINTER(Prepared)]),
+        "q8_norm_matmul_decode_group": (c_int, [vp, vp, ctypes.c_float, ctypes.POINTER(_GroupEntry), c_int, u64,
+                                                c_size, c_int]),
+        "q8_norm_gate_up_silu": (c_int, [vp, vp, ctypes.c_float, vp, vp, u64, c_size, u64, c_size]),
         "q8_gate_up_silu_prepared": (c_int, [vp, vp, vp, ctypes.POINTER(Prepared), ctypes.POINTER(Prepared)]),
         "q8_lm_head_argmax": (c_int, [vp, vp, u64, c_size, u64, c_size, ctypes.POINTER(ctypes.c_uint32)]),
         "q8_argmax": (c_int, [vp, u64, c_size, c_size, ctypes.POINTER(ctypes.c_uint32)]),
@@ -440,6 +444,21 @@ class Gpu:
         arr = self._group(members)
         _check(lib().q8_matmul_decode_group(self.handle, arr, len(members), x.ptr, x_offset, k,
                                             bias.ptr if bias is not None else 0, bias_offset))
+
+    def norm_matmul_decode_group(self, weight: np.ndarray, eps: float, members, x: DeviceBuffer, x_offset: int,
+                                 k: int):
+        """rmsnorm(x) then matmul_decode_group, the norm folded into the GEMV."""
+        w = self._norm_weight(weight)
+        arr = self._group(members)
+        _check(lib().q8_norm_matmul_decode_group(self.handle, w.ctypes.data, float(eps), arr, len(members), x.ptr,
+                                                 x_offset, k))
+
+    def norm_gate_up_silu(self, weight: np.ndarray, eps: float, gate: Weight, up: Weight, x: DeviceBuffer,
+                          x_offset: int, act: DeviceBuffer, act_offset: int):
+        """rmsnorm(x) then gate_up_silu at n = 1, the norm folded into the GEMV."""
+        w = self._norm_weight(weight)
+        _check(lib().q8_norm_gate_up_silu(self.handle, w.ctypes.data, float(eps), self.resident(gate),
+                                          self.resident(up), x.ptr, x_offset, act.ptr, act_offset))
 
     def matmul_prompt_group(self, members, prepared: Prepared, n: int, k: int,
                             bias: DeviceBuffer | None = None, bias_offset: int = 0):

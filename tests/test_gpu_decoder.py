@@ -54,6 +54,72 @@ def int_buffer(gpu, value):
     return b
 
 
+def q8w(r, out, k):
+    return q8.Weight(oracle.make_q8_weight(r, out, k), k, out)
+
+
+@pytest.mark.parametrize("outs,k", [((2304, 2304, 2304), 2304), ((2304,), 5760), ((320,), 768), ((96, 64), 32),
+                                    ((1024, 256, 256), 1024), ((64,), 2304)])
+@pytest.mark.parametrize("exact", [1, 0])
+def test_norm_folded_decode_group_equals_norm_then_group(gpu, outs, k, exact):
+    """q8_norm_matmul_decode_group: the fold (or, where the GEMV needs a K
+    split or has fewer than 256 threads, the two-step path it takes instead)
+    is bit-identical to q8_rmsnorm followed by q8_matmul_decode_group, and
+    within the f32 bar of the oracle's rmsnorm + matmul."""
+    gpu.set_option("gemv.exact", exact)
+    r = np.random.default_rng(SEED + k + len(outs))
+    ws = [q8w(r, o, k) for o in outs]
+    x = (r.standard_normal(k) * 3.0).astype(np.float32)
+    x[7] = -40.0
+    nw = (1.0 + 0.1 * r.standard_normal(k)).astype(np.float32)
+    eps = 1e-6
+    xb, xn = gpu.alloc(4 * k), gpu.alloc(4 * k)
+    xb.upload(x)
+    ys = [gpu.alloc(4 * o) for o in outs]
+    refs = [gpu.alloc(4 * o) for o in outs]
+    try:
+        gpu.rmsnorm(xb, 0, nw, eps, 1, xn)
+        gpu.matmul_decode_group([(w, y, 0) for w, y in zip(ws, refs)], xn, 0, k)
+        gpu.norm_matmul_decode_group(nw, eps, [(w, y, 0) for w, y in zip(ws, ys)], xb, 0, k)
+        xo = oracle.rmsnorm(x, nw, eps)
+        for i, (w, o) in enumerate(zip(ws, outs)):
+            got = ys[i].download(np.float32, o)
+            assert_bits(got, refs[i].download(np.float32, o), f"member {i} of {outs} k={k}")
+            assert_close(got, oracle.matmul(w.data, k, o, xo, 1).reshape(-1), f"member {i} vs oracle")
+    finally:
+        gpu.set_option("gemv.exact", -1)
+        for b in [xb, xn] + ys + refs:
+            b.free()
+        for w in ws:
+            gpu.release(w)
+
+
+@pytest.mark.parametrize("ffn,k", [(5760, 2304), (640, 2304), (64, 2304), (2304, 5760)])
+def test_norm_folded_gate_up_silu_equals_norm_then_gate_up(gpu, ffn, k):
+    r = np.random.default_rng(SEED + ffn + k)
+    gw, uw = q8w(r, ffn, k), q8w(r, ffn, k)
+    x = (r.standard_normal(k) * 2.0).astype(np.float32)
+    nw = (1.0 + 0.1 * r.standard_normal(k)).astype(np.float32)
+    eps = 1e-6
+    xb, xn, act, ref = gpu.alloc(4 * k), gpu.alloc(4 * k), gpu.alloc(4 * ffn), gpu.alloc(4 * ffn)
+    xb.upload(x)
+    try:
+        gpu.rmsnorm(xb, 0, nw, eps, 1, xn)
+        gpu.gate_up_silu(gw, uw, xn, 0, 1, ref, 0)
+        gpu.norm_gate_up_silu(nw, eps, gw, uw, xb, 0, act, 0)
+        got = act.download(np.float32, ffn)
+        assert_bits(got, ref.download(np.float32, ffn), f"norm gate_up_silu ffn={ffn} k={k}")
+        xo = oracle.rmsnorm(x, nw, eps)
+        g = oracle.matmul(gw.data, k, ffn, xo, 1)
+        u = oracle.matmul(uw.data, k, ffn, xo, 1)
+        assert_close(got, oracle.silu_mul(g, u).reshape(-1), "norm gate_up_silu vs oracle")
+    finally:
+        for b in (xb, xn, act, ref):
+            b.free()
+        gpu.release(gw)
+        gpu.release(uw)
+
+
 @pytest.mark.parametrize("n,n_head,n_kv,n_rot,position,capacity", [(5, 4, 2, 64, 7, 32), (1, 36, 36, 64, 511, 1024),
                                                                    (40, 4, 4, 32, 3, 64), (6, 2, 1, 64, 30, 32)])
 def test_rope_append_matches_the_oracle(gpu, n, n_head, n_kv, n_rot, position, capacity):
