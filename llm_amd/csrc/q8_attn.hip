@@ -79,21 +79,26 @@ extern "C" __global__ __launch_bounds__(256) void q8_rope_append(Q8RopeArgs a) {
 
 // ---------------------------------------------------------------------------
 // Decode attention for one token: workgroup (head, split) of 16 waves takes
-// positions [begin, end) of the position + 1 visible ones.  Rows are read
-// whole and coalesced, and every load of a pass is issued before it waits:
-//   scores: 8 lanes per key row (16 bytes = 8 dims each), 128 rows per pass;
-//           the 8 partial dots (dims in order, q from LDS) meet by xor
-//           shuffles, then * scale (the reference's dot * scale);
-//   softmax: workgroup max, exp(s - max) in LDS, workgroup sum;
-//   values: 16 lanes per value row (8 bytes = 4 dims each), 64 rows per pass;
-//           the 64 row slots are summed by xor shuffles inside a wave and in
-//           LDS across the waves, in a fixed order.
-// splits == 1 (contexts up to 2K positions) writes acc / sum.  Otherwise each
-// workgroup stores its unnormalised (acc, max, sum) with agent-scope atomic
-// stores and the last workgroup of the head to arrive (an arrival counter,
-// reset by it) rescales them by exp(max_s - max) and writes the row: the same
-// arithmetic as one softmax summed in another order (gpu.cu attention_combine
-// 735-762), in one launch.  Dynamic LDS: ceil(capacity / splits) floats.
+// positions [begin, end) of the position + 1 visible ones, in chunks of
+// 1024 rows.  Eight lanes share a row (16 bytes = 8 dims of it each), and a
+// chunk's key AND value rows are all loaded before any arithmetic, so the
+// whole chunk costs one memory latency:
+//   scores: each lane's 8-dim partial dot (q in registers), summed over the
+//           row's 8 lanes by xor shuffles (every lane of the row ends with the
+//           same bits), then * scale (the reference's dot * scale);
+//   softmax: the chunk's workgroup max m', the running state rescaled by
+//           exp(m - m'), p = exp(s - m') -- with one chunk (up to 1024
+//           positions per split) m is -inf first, so p = exp(s - max) exactly
+//           as the reference forms it;
+//   values: each lane accumulates p * v over its rows for its 8 dims; the row
+//           slots are summed by xor shuffles in a wave and in LDS across waves,
+//           in a fixed order, and so are the weights.
+// splits == 1 writes acc / sum.  Otherwise each workgroup stores its
+// unnormalised (acc, max, sum) with agent-scope atomic stores and the last
+// workgroup of the head to arrive (an arrival counter, reset by it) rescales
+// them by exp(max_s - max) and writes the row: the same arithmetic as one
+// softmax summed in another order (gpu.cu attention_combine 735-762), in one
+// launch.
 // ---------------------------------------------------------------------------
 static __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -105,132 +110,128 @@ static __device__ __forceinline__ float wave_sum(float v) {
     for (int m = 32; m > 0; m >>= 1) v += __shfl_xor(v, m);
     return v;
 }
-
 #define Q8_ATTN_DEC_WAVES 16
-#define Q8_ATTN_KPASS 4  /* key rows per thread-group loaded before the dots: 4 x 128 rows */
-#define Q8_ATTN_VPASS 4  /* value rows per lane group loaded before the sums: 4 x 64 rows */
+#define Q8_ATTN_CHUNK_PASSES 8 /* row passes per chunk: 8 x 128 rows, keys and values loaded together */
+
 extern "C" __global__ __launch_bounds__(64 * Q8_ATTN_DEC_WAVES) void q8_attn_decode(Q8AttnDecodeArgs a) {
     constexpr int W = Q8_ATTN_DEC_WAVES;
     constexpr int T = 64 * W;
     constexpr int HD = Q8_ATTN_HEAD_DIM;
-    extern __shared__ __attribute__((aligned(16))) float wsm[];
-    __shared__ __attribute__((aligned(16))) float qs[HD];
-    __shared__ float red[2 * W];
+    constexpr int RP = T / 8;  // rows per pass
+    constexpr int NP = Q8_ATTN_CHUNK_PASSES;
+    __shared__ float red[W];
+    __shared__ float lsum[W];
     __shared__ __attribute__((aligned(16))) float part[W][HD];
     __shared__ int last_flag;
+    const int position = *a.position;
     const int head = blockIdx.x / a.splits;
     const int split = blockIdx.x - head * a.splits;
     const int kvh = head / (a.n_head / a.n_kv);
     const int kv_dim = a.n_kv * HD;
-    const int visible = min(*a.position + 1, a.capacity);
-    const int per = (visible + a.splits - 1) / a.splits;
-    const int begin = split * per;
-    const int end = min(begin + per, visible);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    if (tid < HD) qs[tid] = a.q[(size_t)head * HD + tid];
-    __syncthreads();
-
-    // scores: thread -> row slot tid / 8 (128 per pass), dims 8 (tid % 8) .. +7
-    const int kc = tid & 7;
-    const f32x4 q0 = *(const f32x4 *)(qs + 8 * kc);
-    const f32x4 q1 = *(const f32x4 *)(qs + 8 * kc + 4);
+    const int kc = tid & 7;     // dims 8 kc .. 8 kc + 7
+    const int slot = tid >> 3;  // row slot of the pass
+    const f32x4 q0 = *(const f32x4 *)(a.q + (size_t)head * HD + 8 * kc);
+    const f32x4 q1 = *(const f32x4 *)(a.q + (size_t)head * HD + 8 * kc + 4);
     const uint16_t *kbase = a.kcache + kvh * HD + 8 * kc;
-    float mx = -INFINITY;
-    for (int p0 = begin + (tid >> 3); p0 < end; p0 += (T / 8) * Q8_ATTN_KPASS) {
-        i32x4 u[Q8_ATTN_KPASS];
+    const uint16_t *vbase = a.vcache + kvh * HD + 8 * kc;
+    float m = -INFINITY;  // running max, workgroup-uniform
+    float l = 0.0f;       // this lane's weights summed over its rows
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    // One chunk: rows c0 + slot + RP j (j < NP), live below `end`.
+    auto chunk = [&](int c0, int end, const i32x4 *ku, const i32x4 *vu) {
+        float sc[NP];
+        float cmax = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < Q8_ATTN_KPASS; j++) {
-            const int p = min(p0 + (T / 8) * j, end - 1);  // clamped in-bounds; the score is not kept past end
-            u[j] = *(const i32x4 *)(kbase + (size_t)p * kv_dim);
-        }
-#pragma unroll
-        for (int j = 0; j < Q8_ATTN_KPASS; j++) {
+        for (int j = 0; j < NP; j++) {
             float dot = 0.0f;
-            dot = __builtin_fmaf(q0[0], f16_to_f32((unsigned)u[j][0] & 0xffffu), dot);
-            dot = __builtin_fmaf(q0[1], f16_to_f32((unsigned)u[j][0] >> 16), dot);
-            dot = __builtin_fmaf(q0[2], f16_to_f32((unsigned)u[j][1] & 0xffffu), dot);
-            dot = __builtin_fmaf(q0[3], f16_to_f32((unsigned)u[j][1] >> 16), dot);
-            dot = __builtin_fmaf(q1[0], f16_to_f32((unsigned)u[j][2] & 0xffffu), dot);
-            dot = __builtin_fmaf(q1[1], f16_to_f32((unsigned)u[j][2] >> 16), dot);
-            dot = __builtin_fmaf(q1[2], f16_to_f32((unsigned)u[j][3] & 0xffffu), dot);
-            dot = __builtin_fmaf(q1[3], f16_to_f32((unsigned)u[j][3] >> 16), dot);
+            dot = __builtin_fmaf(q0[0], f16_to_f32((unsigned)ku[j][0] & 0xffffu), dot);
+            dot = __builtin_fmaf(q0[1], f16_to_f32((unsigned)ku[j][0] >> 16), dot);
+            dot = __builtin_fmaf(q0[2], f16_to_f32((unsigned)ku[j][1] & 0xffffu), dot);
+            dot = __builtin_fmaf(q0[3], f16_to_f32((unsigned)ku[j][1] >> 16), dot);
+            dot = __builtin_fmaf(q1[0], f16_to_f32((unsigned)ku[j][2] & 0xffffu), dot);
+            dot = __builtin_fmaf(q1[1], f16_to_f32((unsigned)ku[j][2] >> 16), dot);
+            dot = __builtin_fmaf(q1[2], f16_to_f32((unsigned)ku[j][3] & 0xffffu), dot);
+            dot = __builtin_fmaf(q1[3], f16_to_f32((unsigned)ku[j][3] >> 16), dot);
             dot += __shfl_xor(dot, 1);
             dot += __shfl_xor(dot, 2);
             dot += __shfl_xor(dot, 4);
-            const int p = p0 + (T / 8) * j;
-            if (p < end) {
-                const float s = dot * a.scale;
-                if (kc == 0) wsm[p - begin] = s;
-                mx = fmaxf(mx, s);
+            sc[j] = dot * a.scale;
+            if (c0 + slot + RP * j < end) cmax = fmaxf(cmax, sc[j]);
+        }
+        cmax = wave_max(cmax);
+        if (lane == 0) red[wave] = cmax;
+        __syncthreads();
+        float mx = m;
+#pragma unroll
+        for (int w = 0; w < W; w++) mx = fmaxf(mx, red[w]);
+        __syncthreads();  // red is rewritten by the next chunk
+        const float f = expf(m - mx);  // 0 on the first chunk (m = -inf), when l and acc are 0
+        l *= f;
+#pragma unroll
+        for (int d = 0; d < 8; d++) acc[d] *= f;
+#pragma unroll
+        for (int j = 0; j < NP; j++) {
+            if (c0 + slot + RP * j < end) {
+                const float pj = expf(sc[j] - mx);
+                l += pj;
+#pragma unroll
+                for (int d = 0; d < 8; d++) {
+                    const unsigned bits = ((unsigned)vu[j][d >> 1] >> (16 * (d & 1))) & 0xffffu;
+                    acc[d] = __builtin_fmaf(pj, f16_to_f32(bits), acc[d]);
+                }
             }
         }
-    }
-    mx = wave_max(mx);
-    if (lane == 0) red[wave] = mx;
-    __syncthreads();
-    mx = red[0];
+        m = mx;
+    };
+    const int visible = min(position + 1, a.capacity);
+    const int per = (visible + a.splits - 1) / a.splits;
+    const int begin = split * per;
+    const int end = min(begin + per, visible);
+    for (int c0 = begin; c0 < end; c0 += RP * NP) {
+        i32x4 ku[NP], vu[NP];
 #pragma unroll
-    for (int w = 1; w < W; w++) mx = fmaxf(mx, red[w]);
-    float sum = 0.0f;
-    for (int p = begin + tid; p < end; p += T) {
-        const float e = expf(wsm[p - begin] - mx);
-        wsm[p - begin] = e;
-        sum += e;
-    }
-    sum = wave_sum(sum);
-    if (lane == 0) red[W + wave] = sum;
-    __syncthreads();  // weights and partial sums complete
-    sum = 0.0f;
-#pragma unroll
-    for (int w = 0; w < W; w++) sum += red[W + w];
-
-    // values: thread -> row slot tid / 16 (64 per pass), dims 4 (tid % 16) .. +3
-    const int vg = tid & 15;
-    const uint16_t *vbase = a.vcache + kvh * HD + 4 * vg;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int p0 = begin + (tid >> 4); p0 < end; p0 += (T / 16) * Q8_ATTN_VPASS) {
-        unsigned long long u[Q8_ATTN_VPASS];
-#pragma unroll
-        for (int j = 0; j < Q8_ATTN_VPASS; j++) {
-            const int p = min(p0 + (T / 16) * j, end - 1);
-            u[j] = *(const unsigned long long *)(vbase + (size_t)p * kv_dim);
+        for (int j = 0; j < NP; j++) {
+            // clamped to the last live row: rows past `end` repeat its address
+            // (no extra traffic) and are masked
+            const int p = min(c0 + slot + RP * j, end - 1);
+            ku[j] = *(const i32x4 *)(kbase + (size_t)p * kv_dim);
+            vu[j] = *(const i32x4 *)(vbase + (size_t)p * kv_dim);
         }
-#pragma unroll
-        for (int j = 0; j < Q8_ATTN_VPASS; j++) {
-            const int p = p0 + (T / 16) * j;
-            if (p < end) {
-                const float w = wsm[p - begin];
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    acc[e] = __builtin_fmaf(w, f16_to_f32((unsigned)(u[j] >> (16 * e)) & 0xffffu), acc[e]);
-            }
-        }
+        chunk(c0, end, ku, vu);
     }
-    // the four row slots of a wave (lanes vg, vg+16, vg+32, vg+48), then the waves
+    // row slots of a wave (lanes with the same kc), then the waves; the
+    // weights once per row (the kc == 0 lanes)
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-        acc[e] += __shfl_xor(acc[e], 16);
-        acc[e] += __shfl_xor(acc[e], 32);
+    for (int d = 0; d < 8; d++) {
+        acc[d] += __shfl_xor(acc[d], 8);
+        acc[d] += __shfl_xor(acc[d], 16);
+        acc[d] += __shfl_xor(acc[d], 32);
     }
-    if (lane < 16) {
-        const f32x4 v4 = {acc[0], acc[1], acc[2], acc[3]};
-        *(f32x4 *)(&part[wave][4 * vg]) = v4;
+    const float lw = wave_sum(kc == 0 ? l : 0.0f);
+    if (lane < 8) {
+        *(f32x4 *)(&part[wave][8 * lane]) = (f32x4){acc[0], acc[1], acc[2], acc[3]};
+        *(f32x4 *)(&part[wave][8 * lane + 4]) = (f32x4){acc[4], acc[5], acc[6], acc[7]};
     }
+    if (lane == 0) lsum[wave] = lw;
     __syncthreads();
     if (wave != 0) {
         if (a.splits == 1) return;
     }
-    float tot = 0.0f;
+    float tot = 0.0f, sum = 0.0f;
     if (wave == 0) {
 #pragma unroll
         for (int w = 0; w < W; w++) tot += part[w][lane];
+#pragma unroll
+        for (int w = 0; w < W; w++) sum += lsum[w];
     }
     if (a.splits == 1) {
         a.out[(size_t)head * HD + lane] = tot / sum;
         return;
     }
+    const float mx = m;
     const size_t base = (size_t)head * a.splits;
     if (wave == 0) {
         store_agent(a.part_acc + (base + split) * HD + lane, tot);

@@ -1476,8 +1476,6 @@ int q8_attention(q8_ctx *c, q8_dptr q, size_t q_offset, q8_dptr kcache, q8_dptr 
         if (n_head > kCounters - kAttnCounterBase)
             return fail(Q8_ERR_UNSUPPORTED, "attention: %d heads exceed the %d arrival counters", n_head,
                         kCounters - kAttnCounterBase);
-        const size_t per = (size_t)ceil_div(capacity, splits);
-        const size_t lds = per * 4;
         const size_t parts = (size_t)n_head * splits;
         if (splits > 1)
             Q8_TRY(grow(c, &c->attn_ws, &c->attn_ws_bytes, parts * (head_dim + 2) * 4, "hipMalloc(attention)"));
@@ -1496,7 +1494,7 @@ int q8_attention(q8_ctx *c, q8_dptr q, size_t q_offset, q8_dptr kcache, q8_dptr 
         a.splits = splits;
         a.capacity = capacity;
         a.scale = scale;
-        return launch(c, F_ATTN_DECODE, (unsigned)parts, 1024, (unsigned)lds, &a, sizeof a);
+        return launch(c, F_ATTN_DECODE, (unsigned)parts, 1024, 0, &a, sizeof a);
     }
     Q8AttnPrefillArgs a{};
     a.q = reinterpret_cast<const float *>(qp);
