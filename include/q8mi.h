@@ -192,6 +192,14 @@ int q8_silu_mul_prepare(q8_ctx *ctx, q8_dptr gate, q8_dptr up, int n, int k, q8_
  * Gpu::plain does; k % 32 == 0. */
 int q8_rmsnorm(q8_ctx *ctx, q8_dptr x, size_t x_offset, const float *weight, int k, float eps, int rows, q8_dptr out,
                size_t out_offset);
+/* Drops the device copy of a host vector that q8_rmsnorm / q8_norm_prepare
+ * (or the norm-folded decode calls) made resident, so the host memory may be
+ * freed and reused: the cache is keyed by (pointer, length), and a new vector
+ * at a reused address would otherwise find the old copy.  The reference keeps
+ * its copies for the life of the Gpu over mmap'd host weights that never
+ * move; this is the counterpart of q8_weight_release for callers whose host
+ * vectors do.  A vector that is not resident is a no-op. */
+int q8_vector_release(q8_ctx *ctx, const float *weight, size_t k);
 /* prepare(rmsnorm(x)) in one pass, the f32 norm never written
  * (Gpu::rmsnorm_prepare, cuda/mod.rs:1414-1445; Compute::norm_prepare,
  * compute.rs:959-984, whose below-threshold f32 branch is q8_rmsnorm).

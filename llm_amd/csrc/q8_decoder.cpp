@@ -246,6 +246,13 @@ void q8_decoder_destroy(q8_decoder *d) {
         for (const q8_weight *w : L.w)
             if (w) q8_weight_release(d->c, w);
     if (d->embd) q8_weight_release(d->c, d->embd);
+    // the norm vectors' device copies are cached by host address: drop them
+    // before the host vectors are freed and their addresses reused
+    for (Layer &L : d->layers) {
+        q8_vector_release(d->c, L.attn_norm.data(), L.attn_norm.size());
+        q8_vector_release(d->c, L.ffn_norm.data(), L.ffn_norm.size());
+    }
+    q8_vector_release(d->c, d->output_norm.data(), d->output_norm.size());
     for (q8_dptr p : d->buffers) q8_free(d->c, p);
     if (d->pinned) (void)hipHostFree(d->pinned);
     delete d;

@@ -1022,6 +1022,17 @@ int q8_weight_release(q8_ctx *c, const q8_weight *w) {
     return Q8_OK;
 }
 
+int q8_vector_release(q8_ctx *c, const float *host, size_t len) {
+    if (!c || !host) return fail(Q8_ERR_INVALID, "q8_vector_release: bad arguments");
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    auto it = c->vectors.find(std::make_pair((uintptr_t)host, len));
+    if (it == c->vectors.end()) return Q8_OK;  // never made resident (or already released)
+    HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");  // no kernel in flight reads it
+    hipFree(it->second);
+    c->vectors.erase(it);
+    return Q8_OK;
+}
+
 int q8_weight_shape(const q8_weight *w, int *k, int *out, size_t *device_bytes) {
     if (!w) return fail(Q8_ERR_INVALID, "q8_weight_shape: null weight");
     if (k) *k = w->k;

@@ -56,7 +56,8 @@ EXPORTS = (
     "q8_gguf_meta_f32", "q8_gguf_meta_bool", "q8_gguf_meta_str", "q8_gguf_has_key_prefix",
     "q8_gguf_meta_i32_array", "q8_gguf_meta_f32_array", "q8_gguf_meta_str_array", "q8_gguf_weight",
     "q8_rope_append", "q8_attention", "q8_embeddings_device", "q8_argmax_device", "q8_advance_position",
-    "q8_norm_matmul_decode_group", "q8_norm_gate_up_silu",
+    "q8_norm_matmul_decode_group", "q8_norm_gate_up_silu", 
+    "q8_vector_release",
     "q8_weight_synthetic", "q8_decoder_create_synthetic", "q8_decoder_destroy", "q8_decoder_reset",
     "q8_decoder_position", "q8_decoder_forward", "q8_decoder_generate", "q8_decoder_logits", "q8_decoder_weight",
     "q8_decoder_norm",
@@ -169,6 +170,7 @@ def lib():
         "q8_norm_matmul_decode_group": (c_int, [vp, vp, ctypes.c_float, ctypes.POINTER(_GroupEntry), c_int, u64,
                                                 c_size, c_int]),
         "q8_norm_gate_up_silu": (c_int, [vp, vp, ctypes.c_float, vp, vp, u64, c_size, u64, c_size]),
+        "q8_vector_release": (c_int, [vp, vp, c_size]),
         "q8_gate_up_silu_prepared": (c_int, [vp, vp, vp, ctypes.POINTER(Prepared), ctypes.POINTER(Prepared)]),
         "q8_lm_head_argmax": (c_int, [vp, vp, u64, c_size, u64, c_size, ctypes.POINTER(ctypes.c_uint32)]),
         "q8_argmax": (c_int, [vp, u64, c_size, c_size, ctypes.POINTER(ctypes.c_uint32)]),

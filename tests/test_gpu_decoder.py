@@ -355,6 +355,30 @@ def test_decoder_graph_replays_are_bit_identical(gpu):
         dec.close()
 
 
+def test_decoders_in_turn_on_one_context_agree(gpu):
+    """Two decoders with the same seed, one after the other on one context,
+    give bit-identical tokens and logits (eager and replayed): the first one's
+    norm vectors, cached by host address, are released with it and cannot be
+    found again at a reused address."""
+    cfg = dm.config(n_layer=3, n_embd=256, n_ff=512, n_head=4, n_head_kv=2, head_dim=64, n_vocab=1000,
+                    capacity=128, max_batch=64)
+    results = []
+    for _ in range(2):
+        dec = dm.Decoder(gpu, cfg, seed=21)
+        try:
+            prompt = np.arange(3, 27, dtype=np.uint32)
+            for _ in range(3):  # eager, capture + replay, replay
+                dec.reset()
+                first = dec.forward(prompt)
+                toks = dec.generate(5)
+                results.append((first, toks.copy(), dec.logits()))
+        finally:
+            dec.close()
+    for first, toks, logits in results[1:]:
+        assert first == results[0][0] and np.array_equal(toks, results[0][1])
+        assert_bits(logits, results[0][2], "logits of the second decoder")
+
+
 def test_decoder_errors(gpu):
     dec = dm.Decoder(gpu, small_config(), seed=13)
     try:

@@ -707,6 +707,32 @@ def norm_rows(r, rows, k):
     return x, w
 
 
+def test_norm_weight_cache_is_keyed_by_host_identity_until_released(gpu):
+    """Norm weights are made resident by (pointer, length) like weights: new
+    contents at the same address are not seen until q8_vector_release drops
+    the device copy (the decoder releases its vectors when destroyed)."""
+    import ctypes
+    r = rng(77)
+    k = 256
+    x = r.standard_normal((1, k)).astype(np.float32)
+    w = (1.0 + 0.1 * r.standard_normal(k)).astype(np.float32)
+    xb, ob = gpu.alloc(4 * k), gpu.alloc(4 * k)
+    xb.upload(x)
+    q8._check(q8.lib().q8_rmsnorm(gpu.handle, xb.ptr, 0, w.ctypes.data, k, ctypes.c_float(EPS), 1, ob.ptr, 0))
+    first = ob.download(np.float32, k)
+    assert_bits(first, oracle.rmsnorm(x[0], w, EPS), "first norm")
+    w *= 2.0  # same address, new contents
+    q8._check(q8.lib().q8_rmsnorm(gpu.handle, xb.ptr, 0, w.ctypes.data, k, ctypes.c_float(EPS), 1, ob.ptr, 0))
+    assert_bits(ob.download(np.float32, k), first, "cached copy (identity key)")
+    q8._check(q8.lib().q8_vector_release(gpu.handle, w.ctypes.data, k))
+    q8._check(q8.lib().q8_vector_release(gpu.handle, w.ctypes.data, k))  # not resident: a no-op
+    q8._check(q8.lib().q8_rmsnorm(gpu.handle, xb.ptr, 0, w.ctypes.data, k, ctypes.c_float(EPS), 1, ob.ptr, 0))
+    assert_bits(ob.download(np.float32, k), oracle.rmsnorm(x[0], w, EPS), "after release")
+    q8._check(q8.lib().q8_vector_release(gpu.handle, w.ctypes.data, k))
+    xb.free()
+    ob.free()
+
+
 @pytest.mark.parametrize("rows,k", [(1, 2304), (3, 32), (5, 5760), (40, 2304), (67, 64)])
 def test_rmsnorm_rows_match_the_reference_bit_for_bit(gpu, rows, k):
     """f32 squares summed in f64, then 1 / sqrt(ms + eps) and (x * s) * w in
