@@ -70,6 +70,20 @@ int q8_advance_position(q8_ctx *ctx, q8_dptr position, int by);
 int q8_norm_matmul_decode_group(q8_ctx *ctx, const float *norm_weight, float eps, const q8_group_entry *group,
                                 int count, q8_dptr x, size_t x_offset, int k);
 
+/* The attention input of one decode token in one launch: q8_rmsnorm, the
+ * q, k, v decode GEMV group over its output, and q8_rope_append on the
+ * results, with the norm folded into the GEMV (as q8_norm_matmul_decode_group)
+ * and the rotation and KV append in its epilogue -- bit-identical to those
+ * three calls.  q [n_head*head_dim] f32 receives the rotated query; k and v
+ * go only into the f16 caches, at row *position (nothing is appended, and q
+ * is not rotated, at a position outside the cache).  The reference runs the
+ * steps as separate kernels (model.rs dense_attention: rmsnorm,
+ * matmul_decode_group, rope_append). */
+int q8_norm_qkv_rope(q8_ctx *ctx, const float *norm_weight, float eps, const q8_weight *wq, const q8_weight *wk,
+                     const q8_weight *wv, q8_dptr x, size_t x_offset, q8_dptr q, size_t q_offset, q8_dptr kcache,
+                     q8_dptr vcache, int n_head, int n_kv, int head_dim, int n_rot, float base, int capacity,
+                     q8_dptr position);
+
 /* q8_rmsnorm (one row) followed by q8_gate_up_silu at n = 1, folded the same
  * way: act = silu(gate . xn) * (up . xn), xn = rmsnorm(x) * norm_weight. */
 int q8_norm_gate_up_silu(q8_ctx *ctx, const float *norm_weight, float eps, const q8_weight *gate,

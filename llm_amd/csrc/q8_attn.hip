@@ -27,9 +27,6 @@
 // rotated k and plain v are rounded to f16 (nearest even) into the cache at
 // rows position + t.  Rows at or past `capacity` are never written.
 // ---------------------------------------------------------------------------
-static __device__ __forceinline__ unsigned f16_bits(float x) {
-    return (unsigned)__builtin_bit_cast(unsigned short, (_Float16)x);
-}
 
 extern "C" __global__ __launch_bounds__(256) void q8_rope_append(Q8RopeArgs a) {
     const int start = *a.position;

@@ -132,15 +132,17 @@ int q8_decoder::body(int n, int splits) {
     for (Layer &L : layers) {
         // attention block (dense_attention, model.rs:869-1043)
         q8_group_entry qkv[3] = {{L.w[Q8_DEC_Q], q, 0}, {L.w[Q8_DEC_K], k, 0}, {L.w[Q8_DEC_V], v, 0}};
-        if (n == 1) {
-            DEC_TRY(q8_norm_matmul_decode_group(c, L.attn_norm.data(), g.eps, qkv, 3, x, 0, E));
+        if (n == 1) {  // norm, q/k/v and rope + KV append in one launch
+            DEC_TRY(q8_norm_qkv_rope(c, L.attn_norm.data(), g.eps, L.w[Q8_DEC_Q], L.w[Q8_DEC_K], L.w[Q8_DEC_V], x, 0,
+                                     q, 0, L.kcache, L.vcache, g.n_head, g.n_head_kv, g.head_dim, g.n_rot,
+                                     g.rope_base, g.capacity, pos));
         } else {
             q8_prepared p{};
             DEC_TRY(q8_norm_prepare(c, x, 0, L.attn_norm.data(), E, g.eps, n, &p));
             DEC_TRY(q8_matmul_prompt_group(c, qkv, 3, &p, n, E, 0, 0));
+            DEC_TRY(q8_rope_append(c, q, 0, k, 0, v, 0, L.kcache, L.vcache, n, g.n_head, g.n_head_kv, g.head_dim,
+                                   g.n_rot, g.rope_base, g.capacity, pos));
         }
-        DEC_TRY(q8_rope_append(c, q, 0, k, 0, v, 0, L.kcache, L.vcache, n, g.n_head, g.n_head_kv, g.head_dim, g.n_rot,
-                               g.rope_base, g.capacity, pos));
         DEC_TRY(q8_attention(c, q, 0, L.kcache, L.vcache, attn, 0, n, g.n_head, g.n_head_kv, g.head_dim, g.capacity,
                              scale, pos, splits));
         DEC_TRY(q8_matmul(c, L.w[Q8_DEC_O], attn, 0, n, x, 0, nullptr, x, 0));

@@ -36,6 +36,11 @@ static __device__ __forceinline__ int perm_lane(int h, int t) { return ((t & 1) 
 // f16 subnormals).  v_cvt_f32_f16 is exact when the wave keeps f16 denormals,
 // which every kernel here does (amdhsa_float_denorm_mode_16_64 = 3, HIP's
 // default without -ffast-math / denormal flushing).
+// f32 -> f16 bits, rounded to nearest even (the KV cache's narrowing).
+static __device__ __forceinline__ unsigned f16_bits(float x) {
+    return (unsigned)__builtin_bit_cast(unsigned short, (_Float16)x);
+}
+
 static __device__ __forceinline__ float f16_to_f32(unsigned h) {
     return (float)__builtin_bit_cast(_Float16, (unsigned short)h);
 }
@@ -376,6 +381,8 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
     // loads go out before the weight stream, so waiting for them does not
     // wait for it.
     const bool norm = !ONE && a.norm_w != nullptr;  // kernel-uniform
+    // the RoPE epilogue's position, read while the weights stream in
+    const int rope_position = (!ONE && a.rope_pos) ? *a.rope_pos : 0;
     f32x4 wv[Q8_GEMV_STAGE];
     double ss = 0.0;
     if (norm) {
@@ -553,6 +560,39 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
         if (row < mrows) {
             const float act = silu_f32(sums[0]) * sums[1];
             my[row] = act;
+        }
+    } else if (!ONE && a.rope_pos) {
+        // RoPE + KV append on the q, k, v members (q8_rope_append's
+        // arithmetic, one token): rows 2i and 2i+1 of a head are lanes r and
+        // r ^ 1 of this tile (head_dim is even and tiles start at multiples of
+        // 32), so each lane takes its partner's value and keeps its half of
+        // the rotated pair.  q is written rotated in f32; k rotated and v as
+        // they are go to the f16 caches at the position's row.  At a position
+        // outside the cache nothing is rotated or appended (q stays as is).
+        const float other = __shfl_xor(sums[0], 1);
+        const int pos = rope_position;
+        const bool in_cache = pos >= 0 && pos < a.capacity;
+        if (row < mrows) {
+            const int d = row % a.head_dim;
+            const int pair = d >> 1;
+            const bool even = (d & 1) == 0;
+            const float x0 = even ? sums[0] : other;
+            const float x1 = even ? other : sums[0];
+            float y0 = x0, y1 = x1;
+            if (in_cache && mi < 2 && 2 * pair < a.n_rot) {
+                const float angle = (float)pos * a.rope_freq[pair];
+                float sn, cs;
+                sincosf(angle, &sn, &cs);
+                y0 = x0 * cs - x1 * sn;
+                y1 = x0 * sn + x1 * cs;
+            }
+            const float out = even ? y0 : y1;
+            if (mi == 0) {
+                my[row] = out;
+            } else if (in_cache) {
+                uint16_t *cache = mi == 1 ? a.kcache : a.vcache;
+                cache[(size_t)pos * mrows + row] = (uint16_t)f16_bits(out);
+            }
         }
     } else if (row < mrows) {
         const float out = mbias ? sums[0] + mbias[row] : sums[0];

@@ -121,6 +121,14 @@ typedef struct {
     unsigned long long slice_magic; /* ceil(2^32 / S): workgroup / S = (workgroup * magic) >> 32 */
     const float *norm_w; /* non-null (multi-matrix kernels): x is rmsnorm(x) * norm_w, folded in */
     float norm_eps;
+    /* RoPE + KV append epilogue (multi-matrix kernels; members q, k, v):
+     * non-null rope_pos turns it on.  q rows rotated into m[0].y; k rotated
+     * and v copied as f16 into kcache / vcache [capacity][rows] at *rope_pos. */
+    const int *rope_pos;
+    const float *rope_freq; /* n_rot / 2 frequencies base^(-2i/n_rot), from the host */
+    uint16_t *kcache;
+    uint16_t *vcache;
+    int head_dim, n_rot, capacity;
 } Q8GemvArgs;
 
 /* float4s per thread of the 256-thread row RMSNorm (k <= 1024 * this). */

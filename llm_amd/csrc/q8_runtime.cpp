@@ -345,10 +345,19 @@ struct Member {
 };
 
 // n = 1 over up to four weights sharing x; silu = 1 fuses silu(m0)*m1 into y of m0.
+// The RoPE + KV append epilogue of a q, k, v decode group.
+struct GemvRope {
+    const int *position;
+    const float *freq;
+    uint16_t *kcache, *vcache;
+    int head_dim, n_rot, capacity;
+};
+
 // norm_w (device f32[k]) folds rmsnorm(x) * norm_w into a multi-matrix
-// launch; the caller checks gemv_folds_norm first.
+// launch (the caller checks gemv_folds_norm first); rope turns on the RoPE
+// epilogue of a three-member q, k, v group.
 int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const float *bias, int silu,
-             const float *norm_w = nullptr, float norm_eps = 0.0f) {
+             const float *norm_w = nullptr, float norm_eps = 0.0f, const GemvRope *rope = nullptr) {
     const int nb = k / 32;
     int rows_total = 0;
     Q8GemvArgs a{};
@@ -383,6 +392,15 @@ int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const floa
     a.counters = c->counters;
     a.norm_w = norm_w;
     a.norm_eps = norm_eps;
+    if (rope) {
+        a.rope_pos = rope->position;
+        a.rope_freq = rope->freq;
+        a.kcache = rope->kcache;
+        a.vcache = rope->vcache;
+        a.head_dim = rope->head_dim;
+        a.n_rot = rope->n_rot;
+        a.capacity = rope->capacity;
+    }
     const int waves = t.waves_per_tile * slots;
     const int max_threads = pb == 9 ? 512 : 1024;
     if (norm_w && (t.kslices != 1 || waves * 64 < 256 || k > 1024 * Q8_NORM_ROW_VEC))
@@ -404,8 +422,8 @@ int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const floa
     const unsigned lds =
         (unsigned)(nb * 32 * 4 + ((t.exact && t.kslices == 1) ? slots * 32 * Q8_GEMV_VROW(nb) * 4 : waves * 32 * 4) +
                    Q8_GEMV_PAD_FLOATS * 4);
-    return launch(c, gemv_fn(pb, t.exact, count == 1 && !silu && !norm_w), (unsigned)grid, (unsigned)(waves * 64),
-                  lds, &a, sizeof a);
+    return launch(c, gemv_fn(pb, t.exact, count == 1 && !silu && !norm_w && !rope), (unsigned)grid,
+                  (unsigned)(waves * 64), lds, &a, sizeof a);
 }
 
 // Whether run_gemv can fold an RMSNorm into this launch: one K slice (each
@@ -427,12 +445,13 @@ int run_rmsnorm(q8_ctx *c, const float *x, int rows, int k, const float *w, floa
 // rmsnorm(x) * norm_w then a decode GEMV: folded into one launch when it
 // fits, else the row norm into the norm workspace first.
 int run_norm_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, int silu, const float *norm_w,
-                  float eps) {
-    if (gemv_folds_norm(c, m, count, k, silu)) return run_gemv(c, m, count, x, k, nullptr, silu, norm_w, eps);
+                  float eps, const GemvRope *rope = nullptr) {
+    if (gemv_folds_norm(c, m, count, k, silu))
+        return run_gemv(c, m, count, x, k, nullptr, silu, norm_w, eps, rope);
     Q8_TRY(grow(c, &c->norm_ws, &c->norm_ws_bytes, (size_t)k * sizeof(float), "hipMalloc(norm workspace)"));
     float *xn = static_cast<float *>(c->norm_ws);
     Q8_TRY(run_rmsnorm(c, reinterpret_cast<const float *>(x), 1, k, norm_w, eps, xn, nullptr));
-    return run_gemv(c, m, count, (q8_dptr)(uintptr_t)xn, k, nullptr, silu);
+    return run_gemv(c, m, count, (q8_dptr)(uintptr_t)xn, k, nullptr, silu, nullptr, 0.0f, rope);
 }
 
 int run_gemm_h(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n, const float *bias);
@@ -1406,26 +1425,11 @@ int q8_argmax_device(q8_ctx *c, q8_dptr values, size_t offset, size_t len, q8_dp
     return launch(c, F_ARGMAX, 1, 256, 0, &a, sizeof a);
 }
 
-int q8_rope_append(q8_ctx *c, q8_dptr q, size_t q_offset, q8_dptr k, size_t k_offset, q8_dptr v, size_t v_offset,
-                   q8_dptr kcache, q8_dptr vcache, int n, int n_head, int n_kv, int head_dim, int n_rot, float base,
-                   int capacity, q8_dptr position) {
-    if (!c) return fail(Q8_ERR_INVALID, "q8_rope_append: null context");
-    if (n < 1 || n_head < 1 || n_kv < 1 || n_head % n_kv || head_dim < 2 || head_dim % 2 || n_rot < 0 ||
-        n_rot > head_dim || n_rot % 2 || capacity < 1)
-        return fail(Q8_ERR_INVALID, "rope_append: bad geometry (n %d, heads %d/%d, head_dim %d, n_rot %d)", n, n_head,
-                    n_kv, head_dim, n_rot);
-    std::lock_guard<std::recursive_mutex> lock(c->mu);
-    const size_t kv_dim = (size_t)n_kv * head_dim;
-    Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)fptr(q, q_offset), (size_t)n * n_head * head_dim * 4, "rope q"));
-    Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)fptr(k, k_offset), (size_t)n * kv_dim * 4, "rope k"));
-    Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)fptr(v, v_offset), (size_t)n * kv_dim * 4, "rope v"));
-    Q8_TRY(check_span(c, kcache, (size_t)capacity * kv_dim * 2, "key cache"));
-    Q8_TRY(check_span(c, vcache, (size_t)capacity * kv_dim * 2, "value cache"));
-    Q8_TRY(check_span(c, position, 4, "position"));
-    // RopeTable::new (ops.rs:121-131): frequency = base.powf(-2.0 * pair / n_rot)
-    // in f32, from the C library's powf as the reference's table is; uploaded
-    // once per (n_rot, base) and kept (never inside a capture: the eager pass
-    // of a shape runs first).
+// RopeTable::new (ops.rs:121-131): frequency = base.powf(-2.0 * pair / n_rot)
+// in f32, from the C library's powf as the reference's table is; uploaded
+// once per (n_rot, base) and kept (never inside a capture: the eager pass of a
+// shape runs first).
+int rope_table(q8_ctx *c, int n_rot, float base, const float **out) {
     uint32_t base_bits;
     std::memcpy(&base_bits, &base, 4);
     const auto fkey = std::make_pair(n_rot, base_bits);
@@ -1443,8 +1447,69 @@ int q8_rope_append(q8_ctx *c, q8_dptr q, size_t q_offset, q8_dptr k, size_t k_of
         }
         fit = c->rope_freq.emplace(fkey, dev).first;
     }
+    *out = fit->second;
+    return Q8_OK;
+}
+
+int q8_norm_qkv_rope(q8_ctx *c, const float *norm_weight, float eps, const q8_weight *wq, const q8_weight *wk,
+                     const q8_weight *wv, q8_dptr x, size_t x_offset, q8_dptr q, size_t q_offset, q8_dptr kcache,
+                     q8_dptr vcache, int n_head, int n_kv, int head_dim, int n_rot, float base, int capacity,
+                     q8_dptr position) {
+    if (!c || !norm_weight) return fail(Q8_ERR_INVALID, "q8_norm_qkv_rope: bad arguments");
+    if (n_head < 1 || n_kv < 1 || n_head % n_kv || head_dim < 2 || head_dim % 2 || n_rot < 0 || n_rot > head_dim ||
+        n_rot % 2 || capacity < 1)
+        return fail(Q8_ERR_INVALID, "norm_qkv_rope: bad geometry (heads %d/%d, head_dim %d, n_rot %d)", n_head, n_kv,
+                    head_dim, n_rot);
+    Q8_TRY(check_weight(c, wq));
+    Q8_TRY(check_weight(c, wk));
+    Q8_TRY(check_weight(c, wv));
+    const int k = wq->k;
+    const int kv_dim = n_kv * head_dim;
+    if (wk->k != k || wv->k != k || wq->out != n_head * head_dim || wk->out != kv_dim || wv->out != kv_dim)
+        return fail(Q8_ERR_INVALID, "norm_qkv_rope: q/k/v weights are %dx%d, %dx%d, %dx%d for %d/%d heads of %d",
+                    wq->out, wq->k, wk->out, wk->k, wv->out, wv->k, n_head, n_kv, head_dim);
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    const q8_dptr xp = (q8_dptr)(uintptr_t)fptr(x, x_offset);
+    float *qp = fptr(q, q_offset);
+    Q8_TRY(check_span(c, xp, (size_t)k * 4, "qkv x"));
+    Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)qp, (size_t)wq->out * 4, "rope q"));
+    Q8_TRY(check_span(c, kcache, (size_t)capacity * kv_dim * 2, "key cache"));
+    Q8_TRY(check_span(c, vcache, (size_t)capacity * kv_dim * 2, "value cache"));
+    Q8_TRY(check_span(c, position, 4, "position"));
+    float *w = nullptr;
+    Q8_TRY(vector_resident(c, norm_weight, (size_t)k, &w));
+    GemvRope rope{};
+    Q8_TRY(rope_table(c, n_rot, base, &rope.freq));
+    rope.position = reinterpret_cast<const int *>(position);
+    rope.kcache = reinterpret_cast<uint16_t *>(kcache);
+    rope.vcache = reinterpret_cast<uint16_t *>(vcache);
+    rope.head_dim = head_dim;
+    rope.n_rot = n_rot;
+    rope.capacity = capacity;
+    Member m[3] = {{wq, qp}, {wk, nullptr}, {wv, nullptr}};
+    return run_norm_gemv(c, m, 3, xp, k, 0, w, eps, &rope);
+}
+
+int q8_rope_append(q8_ctx *c, q8_dptr q, size_t q_offset, q8_dptr k, size_t k_offset, q8_dptr v, size_t v_offset,
+                   q8_dptr kcache, q8_dptr vcache, int n, int n_head, int n_kv, int head_dim, int n_rot, float base,
+                   int capacity, q8_dptr position) {
+    if (!c) return fail(Q8_ERR_INVALID, "q8_rope_append: null context");
+    if (n < 1 || n_head < 1 || n_kv < 1 || n_head % n_kv || head_dim < 2 || head_dim % 2 || n_rot < 0 ||
+        n_rot > head_dim || n_rot % 2 || capacity < 1)
+        return fail(Q8_ERR_INVALID, "rope_append: bad geometry (n %d, heads %d/%d, head_dim %d, n_rot %d)", n, n_head,
+                    n_kv, head_dim, n_rot);
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    const size_t kv_dim = (size_t)n_kv * head_dim;
+    Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)fptr(q, q_offset), (size_t)n * n_head * head_dim * 4, "rope q"));
+    Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)fptr(k, k_offset), (size_t)n * kv_dim * 4, "rope k"));
+    Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)fptr(v, v_offset), (size_t)n * kv_dim * 4, "rope v"));
+    Q8_TRY(check_span(c, kcache, (size_t)capacity * kv_dim * 2, "key cache"));
+    Q8_TRY(check_span(c, vcache, (size_t)capacity * kv_dim * 2, "value cache"));
+    Q8_TRY(check_span(c, position, 4, "position"));
+    const float *freq = nullptr;
+    Q8_TRY(rope_table(c, n_rot, base, &freq));
     Q8RopeArgs a{};
-    a.freq = fit->second;
+    a.freq = freq;
     a.q = fptr(q, q_offset);
     a.k = fptr(k, k_offset);
     a.v = fptr(v, v_offset);

@@ -57,7 +57,7 @@ EXPORTS = (
     "q8_gguf_meta_i32_array", "q8_gguf_meta_f32_array", "q8_gguf_meta_str_array", "q8_gguf_weight",
     "q8_rope_append", "q8_attention", "q8_embeddings_device", "q8_argmax_device", "q8_advance_position",
     "q8_norm_matmul_decode_group", "q8_norm_gate_up_silu", 
-    "q8_vector_release",
+    "q8_vector_release", "q8_norm_qkv_rope",
     "q8_weight_synthetic", "q8_decoder_create_synthetic", "q8_decoder_destroy", "q8_decoder_reset",
     "q8_decoder_position", "q8_decoder_forward", "q8_decoder_generate", "q8_decoder_logits", "q8_decoder_weight",
     "q8_decoder_norm",
@@ -171,6 +171,8 @@ def lib():
                                                 c_size, c_int]),
         "q8_norm_gate_up_silu": (c_int, [vp, vp, ctypes.c_float, vp, vp, u64, c_size, u64, c_size]),
         "q8_vector_release": (c_int, [vp, vp, c_size]),
+        "q8_norm_qkv_rope": (c_int, [vp, vp, ctypes.c_float, vp, vp, vp, u64, c_size, u64, c_size, u64, u64, c_int,
+                                     c_int, c_int, c_int, ctypes.c_float, c_int, u64]),
         "q8_gate_up_silu_prepared": (c_int, [vp, vp, vp, ctypes.POINTER(Prepared), ctypes.POINTER(Prepared)]),
         "q8_lm_head_argmax": (c_int, [vp, vp, u64, c_size, u64, c_size, ctypes.POINTER(ctypes.c_uint32)]),
         "q8_argmax": (c_int, [vp, u64, c_size, c_size, ctypes.POINTER(ctypes.c_uint32)]),
@@ -454,6 +456,16 @@ class Gpu:
         arr = self._group(members)
         _check(lib().q8_norm_matmul_decode_group(self.handle, w.ctypes.data, float(eps), arr, len(members), x.ptr,
                                                  x_offset, k))
+
+    def norm_qkv_rope(self, weight: np.ndarray, eps: float, wq: Weight, wk: Weight, wv: Weight, x: DeviceBuffer,
+                      x_offset: int, q: DeviceBuffer, q_offset: int, kcache: DeviceBuffer, vcache: DeviceBuffer,
+                      n_head: int, n_kv: int, head_dim: int, n_rot: int, base: float, capacity: int,
+                      position: DeviceBuffer):
+        """rmsnorm + q/k/v decode GEMV + rope_append of one token, one launch."""
+        w = self._norm_weight(weight)
+        _check(lib().q8_norm_qkv_rope(self.handle, w.ctypes.data, float(eps), self.resident(wq), self.resident(wk),
+                                      self.resident(wv), x.ptr, x_offset, q.ptr, q_offset, kcache.ptr, vcache.ptr,
+                                      n_head, n_kv, head_dim, n_rot, float(base), capacity, position.ptr))
 
     def norm_gate_up_silu(self, weight: np.ndarray, eps: float, gate: Weight, up: Weight, x: DeviceBuffer,
                           x_offset: int, act: DeviceBuffer, act_offset: int):

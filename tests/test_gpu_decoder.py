@@ -94,6 +94,54 @@ def test_norm_folded_decode_group_equals_norm_then_group(gpu, outs, k, exact):
             gpu.release(w)
 
 
+@pytest.mark.parametrize("E,n_head,n_kv,n_rot,position,capacity", [(2304, 36, 36, 64, 511, 1024),
+                                                                 (256, 4, 2, 64, 7, 32), (256, 4, 2, 32, 0, 16),
+                                                                 (512, 8, 2, 64, 3, 8), (256, 4, 4, 64, 16, 16),
+                                                                 (1024, 16, 4, 16, 4095, 4096)])
+@pytest.mark.parametrize("exact", [1, 0])
+def test_norm_qkv_rope_equals_norm_group_then_rope_append(gpu, E, n_head, n_kv, n_rot, position, capacity, exact):
+    """q8_norm_qkv_rope (norm folded into the q/k/v GEMV, rotation and KV
+    append in its epilogue) against q8_rmsnorm + q8_matmul_decode_group +
+    q8_rope_append: the rotated q and both caches bit-identical, including
+    partial rotation, grouped kv heads, a position at capacity (nothing
+    appended, q unrotated) and the last cache row; cache rows elsewhere keep
+    their fill."""
+    gpu.set_option("gemv.exact", exact)
+    r = np.random.default_rng(SEED + E + n_head + position)
+    hd, base, eps = 64, 10000.0, 1e-6
+    kv_dim = n_kv * hd
+    wq, wk, wv = q8w(r, n_head * hd, E), q8w(r, kv_dim, E), q8w(r, kv_dim, E)
+    x = (r.standard_normal(E) * 2.0).astype(np.float32)
+    nw = (1.0 + 0.1 * r.standard_normal(E)).astype(np.float32)
+    xb, xn = gpu.alloc(4 * E), gpu.alloc(4 * E)
+    xb.upload(x)
+    q1, k1, v1, q2 = gpu.alloc(4 * n_head * hd), gpu.alloc(4 * kv_dim), gpu.alloc(4 * kv_dim), gpu.alloc(4 * n_head * hd)
+    kc1, vc1 = f16_buffer(gpu, capacity, kv_dim), f16_buffer(gpu, capacity, kv_dim)
+    kc2, vc2 = f16_buffer(gpu, capacity, kv_dim), f16_buffer(gpu, capacity, kv_dim)
+    pos = int_buffer(gpu, position)
+    try:
+        print(f"\nnorm_qkv_rope E={E} heads={n_head}/{n_kv} rot={n_rot} pos={position} cap={capacity}", flush=True)
+        gpu.rmsnorm(xb, 0, nw, eps, 1, xn)
+        gpu.matmul_decode_group([(wq, q1, 0), (wk, k1, 0), (wv, v1, 0)], xn, 0, E)
+        gpu.rope_append(q1, k1, v1, kc1, vc1, 1, n_head, n_kv, hd, n_rot, base, capacity, pos)
+        gpu.norm_qkv_rope(nw, eps, wq, wk, wv, xb, 0, q2, 0, kc2, vc2, n_head, n_kv, hd, n_rot, base, capacity, pos)
+        gpu.sync()
+        assert_bits(q2.download(np.float32, n_head * hd), q1.download(np.float32, n_head * hd), "rotated q")
+        for name, a, b in (("key", kc2, kc1), ("value", vc2, vc1)):
+            got = read_f16(a, capacity, kv_dim).view(np.uint16)
+            want = read_f16(b, capacity, kv_dim).view(np.uint16)
+            assert np.array_equal(got, want), f"{name} cache: {int((got != want).sum())} halves differ"
+        kg = read_f16(kc2, capacity, kv_dim)
+        others = [t for t in range(capacity) if t != position]
+        assert (kg[others] == np.float16(-7.0)).all(), "rows other than the position keep their fill"
+    finally:
+        gpu.set_option("gemv.exact", -1)
+        for b in (xb, xn, q1, k1, v1, q2, kc1, vc1, kc2, vc2, pos):
+            b.free()
+        for w in (wq, wk, wv):
+            gpu.release(w)
+
+
 @pytest.mark.parametrize("ffn,k", [(5760, 2304), (640, 2304), (64, 2304), (2304, 5760)])
 def test_norm_folded_gate_up_silu_equals_norm_then_gate_up(gpu, ffn, k):
     r = np.random.default_rng(SEED + ffn + k)
