@@ -188,6 +188,57 @@ def test_every_truncation_of_a_fixture_is_a_format_error():
             assert ("unexpected end of file" in msg or "past end of file" in msg or "bad magic" in msg), (n, msg)
 
 
+def _read_everything(g):
+    """Every accessor over every key and tensor; errors are allowed, crashes are not."""
+    for key in g.keys():
+        kind = g.meta_type(key)
+        for fn in (g.meta_u64, g.meta_f32, g.meta_bool, g.meta_str, g.meta_i32_array, g.meta_f32_array,
+                   g.meta_str_array):
+            try:
+                fn(key)
+            except (q8.Q8Error, ValueError, UnicodeDecodeError):
+                pass
+        assert kind is not None
+    for t in g.tensors():
+        try:
+            d = g.data(t.name)
+            assert d.size * d.itemsize == t.byte_len
+        except q8.Q8Error:
+            pass
+
+
+@pytest.mark.parametrize("fixture", [SPM, DENSE])
+def test_random_header_mutations_parse_or_fail_cleanly(tmp_path, fixture):
+    """Seeded byte mutations of the header (metadata and tensor table): each
+    file either parses -- and then every key, array and tensor view reads
+    back inside the mapping -- or fails with a status, never a crash."""
+    blob = open(fixture, "rb").read()
+    header = GgufFile.open(fixture).layout()["data_start"]
+    rng = np.random.default_rng(0x6775)
+    path = os.path.join(tmp_path, "m.gguf")
+    outcomes = {}
+    for i in range(600):
+        m = bytearray(blob)
+        for _ in range(int(rng.integers(1, 5))):
+            pos = int(rng.integers(4, header))  # past the magic: the interesting part
+            m[pos] = int(rng.integers(0, 256)) if rng.random() < 0.5 else m[pos] ^ (1 << int(rng.integers(0, 8)))
+        with open(path, "wb") as f:
+            f.write(m)
+        try:
+            g = GgufFile.open(path)
+        except q8.Q8Error as e:
+            # EngineError::Format / Io / MissingTensor, or Unsupported for an unknown tensor type id
+            assert e.status in (q8.Q8_ERR_FORMAT, q8.Q8_ERR_IO, q8.Q8_ERR_MISSING, q8.Q8_ERR_UNSUPPORTED), \
+                (i, e.status, e.message)
+            outcomes["error"] = outcomes.get("error", 0) + 1
+            continue
+        _read_everything(g)
+        del g
+        outcomes["parsed"] = outcomes.get("parsed", 0) + 1
+    print(outcomes)
+    assert outcomes.get("error", 0) > 0 and outcomes.get("parsed", 0) > 0
+
+
 # ---- written files: value types, layout rules ----
 
 ALL_TYPES = [("u8", gw.U8, 200), ("i8", gw.I8, -5), ("u16", gw.U16, 60000), ("i16", gw.I16, -300),
