@@ -377,17 +377,28 @@ extern "C" __global__ __launch_bounds__(128) void q8_attn_prefill(Q8AttnPrefillA
             }
             st[kt] = acc;
         }
-        // scale, causal mask, online softmax for query qrow
+        // scale, causal mask, online softmax for query qrow; a tile whose last
+        // key precedes the workgroup's first query needs no mask
         float tm = -INFINITY;
+        if (p0 + 63 <= start + qt * 32) {
 #pragma unroll
-        for (int kt = 0; kt < 2; kt++)
+            for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int p = p0 + 32 * kt + 8 * (v >> 2) + 4 * h + (v & 3);
-                const float sc = (p <= qa) ? st[kt][v] * a.scale : -INFINITY;
-                st[kt][v] = sc;
-                tm = fmaxf(tm, sc);
-            }
+                for (int v = 0; v < 16; v++) {
+                    st[kt][v] = st[kt][v] * a.scale;
+                    tm = fmaxf(tm, st[kt][v]);
+                }
+        } else {
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    const int p = p0 + 32 * kt + 8 * (v >> 2) + 4 * h + (v & 3);
+                    const float sc = (p <= qa) ? st[kt][v] * a.scale : -INFINITY;
+                    st[kt][v] = sc;
+                    tm = fmaxf(tm, sc);
+                }
+        }
         tm = fmaxf(tm, __shfl_xor(tm, 32));
         const float mn = fmaxf(m, tm);
         // a wave's first tile may be all masked for its queries only if it is
