@@ -40,11 +40,26 @@ int q8_rope_append(q8_ctx *ctx, q8_dptr q, size_t q_offset, q8_dptr k, size_t k_
  * attend_host 1075-1126 semantics: scores = dot(q, k) * scale, softmax, sum of
  * weighted values), with f16 keys and values as the reference's device cache.
  * n == 1 runs the split decode kernel (attention_split + attention_combine,
- * gpu.cu:649-762) over `splits` workgroups per head; n > 1 the tiled prefill
+ * gpu.cu:649-762) over `splits` workgroups per head: one split reads its
+ * positions in 1024-row chunks, more splits in 256-row chunks (so about
+ * visible / 256 splits keep each to one chunk); n > 1 the tiled prefill
  * kernel (`splits` ignored).  head_dim must be 64; n_head a multiple of n_kv. */
 int q8_attention(q8_ctx *ctx, q8_dptr q, size_t q_offset, q8_dptr kcache, q8_dptr vcache, q8_dptr out,
                  size_t out_offset, int n, int n_head, int n_kv, int head_dim, int capacity, float scale,
                  q8_dptr position, int splits);
+
+/* q8_attention for one token (n = 1) followed by q8_matmul of its output
+ * through `wo` with y as the residual (y[0 .. wo->out) += wo . attn):
+ * the reference's attend then matmul_add of the output projection (model.rs
+ * dense_attention).  The splits' partials go straight to the GEMV, whose
+ * prologue combines them (the arithmetic of the in-launch combine), so the
+ * attention output is never written and no workgroup waits for another; the
+ * result is bit-identical to the two calls with the same `splits`.  Shapes
+ * the GEMV cannot fold (more than 8 splits, a K split) run the two calls.
+ * wo->k must be n_head * head_dim. */
+int q8_attention_matmul_add(q8_ctx *ctx, q8_dptr q, size_t q_offset, q8_dptr kcache, q8_dptr vcache, int n_head,
+                            int n_kv, int head_dim, int capacity, float scale, q8_dptr position, int splits,
+                            const q8_weight *wo, q8_dptr y, size_t y_offset);
 
 /* q8_embeddings with the token ids already in device memory (u32), so the
  * lookup can sit inside a captured step.  An id >= the vocabulary yields a

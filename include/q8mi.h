@@ -137,9 +137,9 @@ void *q8_stream(q8_ctx *ctx);
 /* Tuning/testing switches; value -1 restores the tactic table's choice.
  * Names: "gemv.exact", "gemv.waves", "gemv.pairs", "gemv.slices",
  * "gemm.smode", "gemm.tpw", "gemm.twaves", "gemm.xcd_remap", "gemm.kwaves",
- * "gemm.slices", "gemm.rwaves", "gemm.pipe", "gemm.f16" (0: int8 prepared activations and
- * the int8-MFMA GEMM for every n; 1: f16 and the f16-MFMA GEMM for every
- * n >= 2). */
+ * "gemm.slices", "gemm.rwaves", "gemm.pipe", "gemm.lds", "gemm.silu",
+ * "gemm.f16" (0: int8 prepared activations and the int8-MFMA GEMM for every
+ * n; 1: f16 and the f16-MFMA GEMM for every n >= 2). */
 int q8_set_option(q8_ctx *ctx, const char *name, int value);
 
 /* ---- device memory: Gpu::alloc / upload / download (cuda/mod.rs:530-567) ---- */

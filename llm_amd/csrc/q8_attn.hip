@@ -4,7 +4,8 @@
 //   q8_rope_append   rotary embedding of q and k, k and v narrowed to the f16
 //                    KV cache                     (gpu.cu rope_append 525-581, ops.rs:152-166)
 //   q8_attn_decode   one token against the cache, positions split over
-//                    workgroups, combined by the last (gpu.cu attention_split 649-733, combine 735-762)
+//                    workgroups, combined by the last or by the next kernel
+//                    (gpu.cu attention_split 649-733, combine 735-762)
 //   q8_attn_prefill  causal attention of n tokens on f16 MFMA (split operands),
 //                    online softmax               (compute.rs attend_host 1075-1126)
 //   q8_synth         seeded synthetic Q8_0 blocks for the benchmark decoder
@@ -75,27 +76,34 @@ extern "C" __global__ __launch_bounds__(256) void q8_rope_append(Q8RopeArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Decode attention for one token: workgroup (head, split) of 16 waves takes
+// Decode attention for one token: workgroup (head, split) of W waves takes
 // positions [begin, end) of the position + 1 visible ones, in chunks of
-// 1024 rows.  Eight lanes share a row (16 bytes = 8 dims of it each), and a
-// chunk's key AND value rows are all loaded before any arithmetic, so the
-// whole chunk costs one memory latency:
+// 8 W NP rows (NP passes of 8 W rows).  Eight lanes share a row (16 bytes =
+// 8 dims of it each), and a chunk's key AND value rows are all loaded before
+// any arithmetic, so the whole chunk costs one memory latency:
 //   scores: each lane's 8-dim partial dot (q in registers), summed over the
 //           row's 8 lanes by xor shuffles (every lane of the row ends with the
 //           same bits), then * scale (the reference's dot * scale);
 //   softmax: the chunk's workgroup max m', the running state rescaled by
-//           exp(m - m'), p = exp(s - m') -- with one chunk (up to 1024
-//           positions per split) m is -inf first, so p = exp(s - max) exactly
-//           as the reference forms it;
+//           exp(m - m'), p = exp(s - m') -- with one chunk per split m is
+//           -inf first, so p = exp(s - max) exactly as the reference forms it;
 //   values: each lane accumulates p * v over its rows for its 8 dims; the row
 //           slots are summed by xor shuffles in a wave and in LDS across waves,
 //           in a fixed order, and so are the weights.
-// splits == 1 writes acc / sum.  Otherwise each workgroup stores its
-// unnormalised (acc, max, sum) with agent-scope atomic stores and the last
-// workgroup of the head to arrive (an arrival counter, reset by it) rescales
-// them by exp(max_s - max) and writes the row: the same arithmetic as one
-// softmax summed in another order (gpu.cu attention_combine 735-762), in one
-// launch.
+// Two shapes: 16 waves x 8 passes (1024-row chunks) for one split per head,
+// 4 waves x 8 passes (256-row chunks) when the positions are split over
+// workgroups, so a split of about 256 positions is one chunk (measured
+// against 16 x 2 and 8 x 2 passes: equal at 600 positions, faster at 4096).
+// splits == 1 writes acc / sum.  defer writes every split's unnormalised
+// (acc, max, sum) for the next kernel to combine (the O projection's GEMV
+// prologue).  Otherwise each workgroup stores them with agent-scope atomic
+// stores and the last workgroup of the head to arrive (an arrival counter,
+// reset by it) combines them:
+//     max = max_s max_s;  e_s = exp(max_s - max);
+//     out = (sum_s acc_s * e_s) / (sum_s sum_s * e_s)   (s ascending, fused
+//     multiply-adds)
+// -- the same arithmetic as one softmax summed in another order (gpu.cu
+// attention_combine 735-762), and the same as the GEMV prologue's.
 // ---------------------------------------------------------------------------
 static __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -107,15 +115,12 @@ static __device__ __forceinline__ float wave_sum(float v) {
     for (int m = 32; m > 0; m >>= 1) v += __shfl_xor(v, m);
     return v;
 }
-#define Q8_ATTN_DEC_WAVES 16
-#define Q8_ATTN_CHUNK_PASSES 8 /* row passes per chunk: 8 x 128 rows, keys and values loaded together */
 
-extern "C" __global__ __launch_bounds__(64 * Q8_ATTN_DEC_WAVES) void q8_attn_decode(Q8AttnDecodeArgs a) {
-    constexpr int W = Q8_ATTN_DEC_WAVES;
+template <int W, int NP>
+static __device__ __forceinline__ void attn_decode_body(const Q8AttnDecodeArgs &a) {
     constexpr int T = 64 * W;
     constexpr int HD = Q8_ATTN_HEAD_DIM;
     constexpr int RP = T / 8;  // rows per pass
-    constexpr int NP = Q8_ATTN_CHUNK_PASSES;
     __shared__ float red[W];
     __shared__ float lsum[W];
     __shared__ __attribute__((aligned(16))) float part[W][HD];
@@ -215,7 +220,7 @@ extern "C" __global__ __launch_bounds__(64 * Q8_ATTN_DEC_WAVES) void q8_attn_dec
     if (lane == 0) lsum[wave] = lw;
     __syncthreads();
     if (wave != 0) {
-        if (a.splits == 1) return;
+        if (a.splits == 1 || a.defer) return;
     }
     float tot = 0.0f, sum = 0.0f;
     if (wave == 0) {
@@ -224,17 +229,24 @@ extern "C" __global__ __launch_bounds__(64 * Q8_ATTN_DEC_WAVES) void q8_attn_dec
 #pragma unroll
         for (int w = 0; w < W; w++) sum += lsum[w];
     }
+    const float mx = m;
+    const size_t base = (size_t)head * a.splits;
+    if (a.defer) {  // wave 0: the next kernel reads these after this one ends
+        a.part_acc[(base + split) * HD + lane] = tot;
+        if (lane == 0) {
+            *(f32x2 *)(a.part_ms + 2 * (base + split)) = (f32x2){mx, sum};
+        }
+        return;
+    }
     if (a.splits == 1) {
         a.out[(size_t)head * HD + lane] = tot / sum;
         return;
     }
-    const float mx = m;
-    const size_t base = (size_t)head * a.splits;
     if (wave == 0) {
         store_agent(a.part_acc + (base + split) * HD + lane, tot);
         if (lane == 0) {
-            store_agent(a.part_max + base + split, mx);
-            store_agent(a.part_sum + base + split, sum);
+            store_agent(a.part_ms + 2 * (base + split), mx);
+            store_agent(a.part_ms + 2 * (base + split) + 1, sum);
         }
     }
     __builtin_amdgcn_s_waitcnt(0);
@@ -248,15 +260,18 @@ extern "C" __global__ __launch_bounds__(64 * Q8_ATTN_DEC_WAVES) void q8_attn_dec
     if (tid == 0) __hip_atomic_store(&a.counters[head], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (wave != 0) return;
     float gmax = -INFINITY;
-    for (int s = 0; s < a.splits; s++) gmax = fmaxf(gmax, load_agent(a.part_max + base + s));
+    for (int s = 0; s < a.splits; s++) gmax = fmaxf(gmax, load_agent(a.part_ms + 2 * (base + s)));
     float num = 0.0f, den = 0.0f;
     for (int s = 0; s < a.splits; s++) {
-        const float f = expf(load_agent(a.part_max + base + s) - gmax);  // an empty split has max -inf: f = 0
-        den += load_agent(a.part_sum + base + s) * f;
-        num += load_agent(a.part_acc + (base + s) * HD + lane) * f;
+        const float f = expf(load_agent(a.part_ms + 2 * (base + s)) - gmax);  // an empty split has max -inf: f = 0
+        den = __builtin_fmaf(load_agent(a.part_ms + 2 * (base + s) + 1), f, den);
+        num = __builtin_fmaf(load_agent(a.part_acc + (base + s) * HD + lane), f, num);
     }
     a.out[(size_t)head * HD + lane] = num / den;
 }
+
+extern "C" __global__ __launch_bounds__(1024) void q8_attn_decode(Q8AttnDecodeArgs a) { attn_decode_body<16, 8>(a); }
+extern "C" __global__ __launch_bounds__(256) void q8_attn_decode_w4(Q8AttnDecodeArgs a) { attn_decode_body<4, 8>(a); }
 
 // ---------------------------------------------------------------------------
 // Prefill attention: n query tokens at cache positions start .. start+n-1, each

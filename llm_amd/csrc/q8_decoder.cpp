@@ -20,6 +20,7 @@
 // workspace (its pointers would be stale).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <map>
@@ -91,9 +92,11 @@ struct q8_decoder {
         graphs.clear();
     }
     int splits_for(int visible) const {
-        // one 16-wave workgroup per head up to 2048 visible positions (no
-        // cross-workgroup combine); beyond, about 1024 positions per workgroup
-        return visible <= 2048 ? 1 : (visible + 1023) / 1024;
+        // one workgroup per head while the positions fit one chunk of the
+        // split kernel; beyond, a split per chunk, up to the eight the output
+        // projection's prologue combines
+        const int rows = q8i::attention_split_rows();
+        return visible <= rows ? 1 : std::min(Q8_ATTN_COMBINE_MAX, (visible + rows - 1) / rows);
     }
     int body(int n, int splits);
     int run(int n, int splits);
@@ -143,9 +146,14 @@ int q8_decoder::body(int n, int splits) {
             DEC_TRY(q8_rope_append(c, q, 0, k, 0, v, 0, L.kcache, L.vcache, n, g.n_head, g.n_head_kv, g.head_dim,
                                    g.n_rot, g.rope_base, g.capacity, pos));
         }
-        DEC_TRY(q8_attention(c, q, 0, L.kcache, L.vcache, attn, 0, n, g.n_head, g.n_head_kv, g.head_dim, g.capacity,
-                             scale, pos, splits));
-        DEC_TRY(q8_matmul(c, L.w[Q8_DEC_O], attn, 0, n, x, 0, nullptr, x, 0));
+        if (n == 1) {  // attention, its split combine folded into the output projection
+            DEC_TRY(q8_attention_matmul_add(c, q, 0, L.kcache, L.vcache, g.n_head, g.n_head_kv, g.head_dim,
+                                            g.capacity, scale, pos, splits, L.w[Q8_DEC_O], x, 0));
+        } else {
+            DEC_TRY(q8_attention(c, q, 0, L.kcache, L.vcache, attn, 0, n, g.n_head, g.n_head_kv, g.head_dim,
+                                 g.capacity, scale, pos, splits));
+            DEC_TRY(q8_matmul(c, L.w[Q8_DEC_O], attn, 0, n, x, 0, nullptr, x, 0));
+        }
         // feed-forward block (feed_forward, model.rs:1162-1235)
         if (n == 1) {
             DEC_TRY(q8_norm_gate_up_silu(c, L.ffn_norm.data(), g.eps, L.w[Q8_DEC_GATE], L.w[Q8_DEC_UP], x, 0, act, 0));

@@ -11,6 +11,9 @@ __attribute__((visibility("hidden"), format(printf, 2, 3))) int set_error(int co
 // Changes whenever the context reallocates a workspace; a graph captured
 // before the change holds freed pointers.
 __attribute__((visibility("hidden"))) unsigned long long workspace_generation(const q8_ctx *c);
+// Positions one chunk of the split decode attention kernel covers: a split of
+// about this many positions is one pass over its keys.
+__attribute__((visibility("hidden"))) int attention_split_rows();
 }  // namespace q8i
 
 #endif

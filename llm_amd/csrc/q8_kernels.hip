@@ -49,6 +49,7 @@ static __device__ __forceinline__ float f16_to_f32(unsigned h) {
 // bytes biased to q + 128, placed under the f16 exponent of 1024 (0x64xx is
 // 1024 + byte), then one packed f16 subtraction of 1152 per two values.
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 static __device__ __forceinline__ unsigned f16_pair(unsigned biased, unsigned sel) {
     const unsigned bits = __builtin_amdgcn_perm(0x64646464u, biased, sel);
@@ -242,8 +243,10 @@ static __device__ __forceinline__ float chain_row(const float *row, int count) {
 }
 
 // ONE: a launch over one matrix (members == 1, no SiLU pair), whose fields
-// are read at static offsets with no selection.
-template <int PB, int EXACT, int ONE>
+// are read at static offsets with no selection.  CMB: x built by the folded
+// attention combine (a separate build, so its registers burden no other
+// launch).
+template <int PB, int EXACT, int ONE, int CMB = 0>
 static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
     extern __shared__ __attribute__((aligned(16))) float smem[];
     __shared__ int last_flag;
@@ -348,12 +351,36 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
     const int st_end = min(16 * p_end, nb * 8);
     const int st_count = st_end - st_begin;  // <= 0 for a wave without pairs
     const int st_clamp = max(st_end - 1, 0);
+    // Folded attention combine (the CMB build; the host guarantees one K
+    // slice, nb * 8 <= threads, head dim 64 and at most Q8_ATTN_COMBINE_MAX
+    // splits): thread v builds float4 v of x from the splits' partials of its
+    // head (16 float4s per head); no x is loaded.  Only the live splits are
+    // read, and only by the waves that hold a float4 of x.
+    constexpr bool comb = CMB != 0;
     f32x4 xv[Q8_GEMV_STAGE];
+    f32x4 cacc[Q8_ATTN_COMBINE_MAX];
+    f32x2 cms[Q8_ATTN_COMBINE_MAX];  // (max, sum)
+    const int ns = comb ? a.attn_splits : 0;
+    const bool comb_wave = comb && (int)(threadIdx.x & ~63u) < nb * 8;  // wave-uniform
+    if constexpr (comb) {
+        const int v = min((int)threadIdx.x, nb * 8 - 1);
+        const int hs = (v >> 4) * ns;  // head * splits
+        if (comb_wave) {
 #pragma unroll
-    for (int u = 0; u < Q8_GEMV_STAGE; u++) {
-        const int i = min(st_begin + lane + 64 * u, st_clamp);
-        const float *xp = xg + 4 * i;
-        xv[u] = (f32x4){xp[0], xp[1], xp[2], xp[3]};
+            for (int s = 0; s < Q8_ATTN_COMBINE_MAX; s++) {
+                if (s < ns) {
+                    cms[s] = *(const f32x2 *)(a.attn_ms + 2 * (hs + s));
+                    cacc[s] = *(const f32x4 *)(a.attn_acc + (size_t)(hs + s) * 64 + 4 * (v & 15));
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < Q8_GEMV_STAGE; u++) {
+            const int i = min(st_begin + lane + 64 * u, st_clamp);
+            const float *xp = xg + 4 * i;
+            xv[u] = (f32x4){xp[0], xp[1], xp[2], xp[3]};
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -432,6 +459,36 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
     // block values or the wave sums), so no store sits in an exec branch.
     float *pad = vbuf + ((EXACT && S == 1) ? nslots * 32 * vrow : nslots * W * 32);
 
+    if constexpr (comb) {
+        // q8_attn_decode's combine, term for term: the head's max over the
+        // splits, e_s = exp(max_s - max) (0 for an empty split), then the
+        // weighted values and weights by fused multiply-adds, s ascending,
+        // and one division per element.
+        if (comb_wave) {
+            float gmax = -INFINITY;
+#pragma unroll
+            for (int s = 0; s < Q8_ATTN_COMBINE_MAX; s++) gmax = s < ns ? fmaxf(gmax, cms[s].x) : gmax;
+            float den = 0.0f;
+            f32x4 num = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s = 0; s < Q8_ATTN_COMBINE_MAX; s++) {
+                if (s < ns) {
+                    const float f = expf(cms[s].x - gmax);
+                    den = __builtin_fmaf(cms[s].y, f, den);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) num[e] = __builtin_fmaf(cacc[s][e], f, num[e]);
+                }
+            }
+            const int v = threadIdx.x;
+            float *d = v < nb * 8 ? xs + (v >> 3) * 32 + ((v & 7) >> 1) + 4 * (v & 1) : pad;
+            d[0] = num.x / den;
+            d[8] = num.y / den;
+            d[16] = num.z / den;
+            d[24] = num.w / den;
+        }
+        __syncthreads();
+    }
+
     // Exact mode: zero each row's tail up to a multiple of four blocks (read
     // by the final sum as whole float4s, after the workgroup barrier).
     if (EXACT && S == 1 && w == 0 && lane < 32) {
@@ -446,7 +503,7 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
     // to the same range), so only a wave-level fence is needed.
 #pragma unroll
     for (int u = 0; u < Q8_GEMV_STAGE; u++) {
-        if (64 * u < st_count) {
+        if (!comb && 64 * u < st_count) {
             const int i = st_begin + lane + 64 * u;
             float *d = i < st_end ? xs + (i >> 3) * 32 + ((i & 7) >> 1) + 4 * (i & 1) : pad;
             d[0] = xv[u].x;
@@ -608,6 +665,9 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
     }                                                                                                    \
     extern "C" __global__ __launch_bounds__(THREADS) void q8_gemv1_pb##PB##_e##EXACT(Q8GemvArgs a) { \
         gemv_body<PB, EXACT, 1>(a);                                                                      \
+    }                                                                                                    \
+    extern "C" __global__ __launch_bounds__(THREADS) void q8_gemvc_pb##PB##_e##EXACT(Q8GemvArgs a) { \
+        gemv_body<PB, EXACT, 1, 1>(a);                                                                   \
     }
 Q8_GEMV_KERNEL(2, 0, 1024)
 Q8_GEMV_KERNEL(2, 1, 1024)

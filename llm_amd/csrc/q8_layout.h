@@ -129,6 +129,14 @@ typedef struct {
     uint16_t *kcache;
     uint16_t *vcache;
     int head_dim, n_rot, capacity;
+    /* Attention split combine as the prologue (the q8_gemvc_* kernels, one
+     * matrix; head dim Q8_ATTN_HEAD_DIM, at most Q8_ATTN_COMBINE_MAX splits,
+     * one float4 of x per thread): x is
+     * sum_s acc_s * e_s / sum_s sum_s * e_s with e_s = exp(max_s - max), per
+     * head, from the partials q8_attn_decode leaves in defer mode. */
+    const float *attn_acc; /* [heads][splits][head_dim] */
+    const float *attn_ms;  /* [heads][splits][2]: max, sum */
+    int attn_splits;
 } Q8GemvArgs;
 
 /* float4s per thread of the 256-thread row RMSNorm (k <= 1024 * this). */
@@ -222,6 +230,7 @@ typedef struct {
  * KV cache layout (one layer): f16 [capacity][n_kv * head_dim], position-major,
  * as the reference's device cache (gpu.cu kv_append 506-519). */
 #define Q8_ATTN_HEAD_DIM 64 /* the head width the attention kernels are built for */
+#define Q8_ATTN_COMBINE_MAX 8 /* most attention splits a GEMV prologue combines */
 #define Q8_ATTN_TILE 64     /* prefill: queries and keys per tile */
 
 typedef struct {
@@ -240,13 +249,13 @@ typedef struct {
     const uint16_t *kcache;
     const uint16_t *vcache;
     float *part_acc;        /* [n_head][splits][head_dim] unnormalised sums */
-    float *part_max;        /* [n_head][splits] */
-    float *part_sum;        /* [n_head][splits] */
+    float *part_ms;         /* [n_head][splits][2]: max, sum */
     float *out;             /* [n_head][head_dim] */
     unsigned *counters;     /* splits > 1: arrivals per head, zero between launches */
     const int *position;    /* device: the token's cache position; it sees position + 1 keys */
     int n_head, n_kv, splits, capacity;
     float scale;
+    int defer;              /* 1: write every split's partials (also at splits = 1), no combine */
 } Q8AttnDecodeArgs;
 
 typedef struct {

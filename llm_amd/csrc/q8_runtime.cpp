@@ -70,6 +70,7 @@ enum Fn {
     F_REPACK,
     F_GEMV_2_0, F_GEMV_2_1, F_GEMV_3_0, F_GEMV_3_1, F_GEMV_5_0, F_GEMV_5_1, F_GEMV_9_0, F_GEMV_9_1,
     F_GEMV1_2_0, F_GEMV1_2_1, F_GEMV1_3_0, F_GEMV1_3_1, F_GEMV1_5_0, F_GEMV1_5_1, F_GEMV1_9_0, F_GEMV1_9_1,
+    F_GEMVC_2_0, F_GEMVC_2_1, F_GEMVC_3_0, F_GEMVC_3_1, F_GEMVC_5_0, F_GEMVC_5_1, F_GEMVC_9_0, F_GEMVC_9_1,
     F_QUANTIZE,
     F_GEMM_S0_T1, F_GEMM_S1_T1, F_GEMM_S1_T2, F_GEMM_S1_T4,
     F_GEMM_H_T1_R4, F_GEMM_H_T2_R2, F_GEMM_H_T2_R4,
@@ -81,7 +82,7 @@ enum Fn {
     F_SILU_MUL,
     F_COPY,
     F_EMBED,
-    F_ROPE, F_ATTN_DECODE, F_ATTN_PREFILL, F_SYNTH, F_ADVANCE,
+    F_ROPE, F_ATTN_DECODE, F_ATTN_DECODE_W4, F_ATTN_PREFILL, F_SYNTH, F_ADVANCE,
     F_COUNT
 };
 
@@ -91,6 +92,8 @@ const char *const kFnNames[F_COUNT] = {
     "q8_gemv_pb5_e0", "q8_gemv_pb5_e1", "q8_gemv_pb9_e0", "q8_gemv_pb9_e1",
     "q8_gemv1_pb2_e0", "q8_gemv1_pb2_e1", "q8_gemv1_pb3_e0", "q8_gemv1_pb3_e1",
     "q8_gemv1_pb5_e0", "q8_gemv1_pb5_e1", "q8_gemv1_pb9_e0", "q8_gemv1_pb9_e1",
+    "q8_gemvc_pb2_e0", "q8_gemvc_pb2_e1", "q8_gemvc_pb3_e0", "q8_gemvc_pb3_e1",
+    "q8_gemvc_pb5_e0", "q8_gemvc_pb5_e1", "q8_gemvc_pb9_e0", "q8_gemvc_pb9_e1",
     "q8_quantize",
     "q8_gemm_s0_t1", "q8_gemm_s1_t1", "q8_gemm_s1_t2", "q8_gemm_s1_t4",
     "q8_gemm_h_t1_r4", "q8_gemm_h_t2_r2", "q8_gemm_h_t2_r4",
@@ -102,7 +105,7 @@ const char *const kFnNames[F_COUNT] = {
     "q8_silu_mul",
     "q8_copy",
     "q8_embed",
-    "q8_rope_append", "q8_attn_decode", "q8_attn_prefill", "q8_synth", "q8_advance",
+    "q8_rope_append", "q8_attn_decode", "q8_attn_decode_w4", "q8_attn_prefill", "q8_synth", "q8_advance",
 };
 
 constexpr int kArgmaxParts = 1024;
@@ -158,6 +161,8 @@ struct q8_ctx {
     size_t token_ws_bytes = 0;
     void *attn_ws = nullptr;             // decode attention partials (acc, max, sum per head and split)
     size_t attn_ws_bytes = 0;
+    void *attn_out_ws = nullptr;         // attention output when q8_attention_matmul_add runs two steps
+    size_t attn_out_ws_bytes = 0;
     std::vector<q8_weight *> owned;      // weights generated on the device (no host identity)
     unsigned long long ws_generation = 0; // bumped whenever a workspace is reallocated
     int cu_count = 0;
@@ -330,9 +335,10 @@ q8_tactic plan(q8_ctx *c, int n, int out, int k, int slots = 1, int fmt = -1) {
     return t;
 }
 
-// one: a launch over a single matrix (q8_gemv1_*, no member selection).
-Fn gemv_fn(int pb, int exact, bool one) {
-    const int base = one ? F_GEMV1_2_0 : F_GEMV_2_0;
+// one: a launch over a single matrix (q8_gemv1_*, no member selection);
+// comb: a single matrix whose x is the folded attention combine (q8_gemvc_*).
+Fn gemv_fn(int pb, int exact, bool one, bool comb = false) {
+    const int base = comb ? F_GEMVC_2_0 : one ? F_GEMV1_2_0 : F_GEMV_2_0;
     const int i = pb == 2 ? 0 : pb == 3 ? 1 : pb == 5 ? 2 : 3;
     return (Fn)(base + 2 * i + (exact ? 1 : 0));
 }
@@ -353,11 +359,20 @@ struct GemvRope {
     int head_dim, n_rot, capacity;
 };
 
+// Decode attention partials a GEMV prologue combines into its x.
+struct GemvCombine {
+    const float *acc, *ms;
+    int splits;
+};
+
 // norm_w (device f32[k]) folds rmsnorm(x) * norm_w into a multi-matrix
 // launch (the caller checks gemv_folds_norm first); rope turns on the RoPE
 // epilogue of a three-member q, k, v group.
+// comb builds x from attention partials instead (the caller checks
+// gemv_folds_combine first; x is then unused).
 int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const float *bias, int silu,
-             const float *norm_w = nullptr, float norm_eps = 0.0f, const GemvRope *rope = nullptr) {
+             const float *norm_w = nullptr, float norm_eps = 0.0f, const GemvRope *rope = nullptr,
+             const GemvCombine *comb = nullptr) {
     const int nb = k / 32;
     int rows_total = 0;
     Q8GemvArgs a{};
@@ -401,10 +416,18 @@ int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const floa
         a.n_rot = rope->n_rot;
         a.capacity = rope->capacity;
     }
+    if (comb) {
+        a.attn_acc = comb->acc;
+        a.attn_ms = comb->ms;
+        a.attn_splits = comb->splits;
+    }
     const int waves = t.waves_per_tile * slots;
     const int max_threads = pb == 9 ? 512 : 1024;
     if (norm_w && (t.kslices != 1 || waves * 64 < 256 || k > 1024 * Q8_NORM_ROW_VEC))
         return fail(Q8_ERR_UNSUPPORTED, "gemv: the folded norm needs one K slice and >= 256 threads");
+    if (comb && (t.kslices != 1 || nb * 8 > waves * 64 || comb->splits < 1 || comb->splits > Q8_ATTN_COMBINE_MAX))
+        return fail(Q8_ERR_UNSUPPORTED, "gemv: the folded attention combine needs one K slice, a thread per float4 "
+                                        "of x and at most %d splits", Q8_ATTN_COMBINE_MAX);
     if (waves * 64 > max_threads)
         return fail(Q8_ERR_UNSUPPORTED, "gemv: %d waves per workgroup exceed the %d-thread launch bound", waves,
                     max_threads);
@@ -422,8 +445,20 @@ int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const floa
     const unsigned lds =
         (unsigned)(nb * 32 * 4 + ((t.exact && t.kslices == 1) ? slots * 32 * Q8_GEMV_VROW(nb) * 4 : waves * 32 * 4) +
                    Q8_GEMV_PAD_FLOATS * 4);
-    return launch(c, gemv_fn(pb, t.exact, count == 1 && !silu && !norm_w && !rope), (unsigned)grid,
+    if (comb && (count != 1 || silu || norm_w || rope))
+        return fail(Q8_ERR_UNSUPPORTED, "gemv: the folded attention combine serves one matrix");
+    return launch(c, gemv_fn(pb, t.exact, count == 1 && !silu && !norm_w && !rope, comb != nullptr), (unsigned)grid,
                   (unsigned)(waves * 64), lds, &a, sizeof a);
+}
+
+// Whether run_gemv can build x from `splits` attention partials over one
+// matrix of k = heads * 64: one K slice and a thread per float4 of x.
+bool gemv_folds_combine(q8_ctx *c, const q8_weight *w, int splits) {
+    const q8_tactic t = plan(c, 1, w->out, w->k, 1);
+    const int pb = valid_pb(t.pairs_per_batch) ? t.pairs_per_batch : 5;
+    const int threads = t.waves_per_tile * 64;
+    return t.kslices == 1 && t.pairs_per_wave <= 12 && threads <= (pb == 9 ? 512 : 1024) &&
+           (w->k / 32) * 8 <= threads && splits >= 1 && splits <= Q8_ATTN_COMBINE_MAX;
 }
 
 // Whether run_gemv can fold an RMSNorm into this launch: one K slice (each
@@ -866,6 +901,7 @@ void q8_close(q8_ctx *c) {
     if (c->counters) hipFree(c->counters);
     if (c->token_ws) hipFree(c->token_ws);
     if (c->attn_ws) hipFree(c->attn_ws);
+    if (c->attn_out_ws) hipFree(c->attn_out_ws);
     for (q8_weight *w : c->owned) {
         hipFree(w->base);
         delete w;
@@ -1527,51 +1563,80 @@ int q8_rope_append(q8_ctx *c, q8_dptr q, size_t q_offset, q8_dptr k, size_t k_of
     return launch(c, F_ROPE, grid, 256, 0, &a, sizeof a);
 }
 
-int q8_attention(q8_ctx *c, q8_dptr q, size_t q_offset, q8_dptr kcache, q8_dptr vcache, q8_dptr out,
-                 size_t out_offset, int n, int n_head, int n_kv, int head_dim, int capacity, float scale,
-                 q8_dptr position, int splits) {
-    if (!c) return fail(Q8_ERR_INVALID, "q8_attention: null context");
+namespace {
+
+// The decode attention kernel for `splits` workgroups per head: one split
+// takes 16 waves over 1024-row chunks, more take 4 waves over 256-row chunks.
+struct AttnShape {
+    Fn fn;
+    unsigned threads;
+    int rows;  // positions per chunk
+};
+AttnShape attn_shape(int splits) {
+    if (splits == 1) return {F_ATTN_DECODE, 1024, 1024};
+    return {F_ATTN_DECODE_W4, 256, 256};
+}
+
+// Decode attention of one token (geometry and spans checked by the caller).
+// defer leaves every split's partials in attn_ws for a GEMV prologue.
+int run_attn_decode(q8_ctx *c, const float *q, q8_dptr kcache, q8_dptr vcache, float *out, int n_head, int n_kv,
+                    int capacity, float scale, q8_dptr position, int splits, int defer) {
+    if (splits < 1 || splits > 1024 || splits > capacity)
+        return fail(Q8_ERR_INVALID, "attention: %d splits for capacity %d", splits, capacity);
+    if (n_head > kCounters - kAttnCounterBase)
+        return fail(Q8_ERR_UNSUPPORTED, "attention: %d heads exceed the %d arrival counters", n_head,
+                    kCounters - kAttnCounterBase);
+    const size_t parts = (size_t)n_head * splits;
+    if (splits > 1 || defer)
+        Q8_TRY(grow(c, &c->attn_ws, &c->attn_ws_bytes, parts * (Q8_ATTN_HEAD_DIM + 2) * 4, "hipMalloc(attention)"));
+    Q8AttnDecodeArgs a{};
+    a.q = q;
+    a.kcache = reinterpret_cast<const uint16_t *>(kcache);
+    a.vcache = reinterpret_cast<const uint16_t *>(vcache);
+    a.part_acc = static_cast<float *>(c->attn_ws);
+    a.part_ms = a.part_acc ? a.part_acc + parts * Q8_ATTN_HEAD_DIM : nullptr;
+    a.out = out;
+    a.counters = c->counters + kAttnCounterBase;
+    a.position = reinterpret_cast<const int *>(position);
+    a.n_head = n_head;
+    a.n_kv = n_kv;
+    a.splits = splits;
+    a.capacity = capacity;
+    a.scale = scale;
+    a.defer = defer;
+    const AttnShape sh = attn_shape(splits);
+    return launch(c, sh.fn, (unsigned)parts, sh.threads, 0, &a, sizeof a);
+}
+
+int check_attention(q8_ctx *c, q8_dptr qp, q8_dptr kcache, q8_dptr vcache, q8_dptr position, int n, int n_head,
+                    int n_kv, int head_dim, int capacity) {
     if (head_dim != Q8_ATTN_HEAD_DIM)
         return fail(Q8_ERR_UNSUPPORTED, "attention kernels are built for head_dim %d, got %d", Q8_ATTN_HEAD_DIM,
                     head_dim);
     if (n < 1 || n_head < 1 || n_kv < 1 || n_head % n_kv || capacity < 1)
         return fail(Q8_ERR_INVALID, "attention: bad geometry (n %d, heads %d/%d, capacity %d)", n, n_head, n_kv,
                     capacity);
-    std::lock_guard<std::recursive_mutex> lock(c->mu);
     const size_t kv_dim = (size_t)n_kv * head_dim;
-    const q8_dptr qp = (q8_dptr)(uintptr_t)fptr(q, q_offset);
-    const q8_dptr op = (q8_dptr)(uintptr_t)fptr(out, out_offset);
     Q8_TRY(check_span(c, qp, (size_t)n * n_head * head_dim * 4, "attention q"));
-    Q8_TRY(check_span(c, op, (size_t)n * n_head * head_dim * 4, "attention out"));
     Q8_TRY(check_span(c, kcache, (size_t)capacity * kv_dim * 2, "key cache"));
     Q8_TRY(check_span(c, vcache, (size_t)capacity * kv_dim * 2, "value cache"));
-    Q8_TRY(check_span(c, position, 4, "position"));
-    if (n == 1) {
-        if (splits < 1 || splits > 1024 || splits > capacity)
-            return fail(Q8_ERR_INVALID, "attention: %d splits for capacity %d", splits, capacity);
-        if (n_head > kCounters - kAttnCounterBase)
-            return fail(Q8_ERR_UNSUPPORTED, "attention: %d heads exceed the %d arrival counters", n_head,
-                        kCounters - kAttnCounterBase);
-        const size_t parts = (size_t)n_head * splits;
-        if (splits > 1)
-            Q8_TRY(grow(c, &c->attn_ws, &c->attn_ws_bytes, parts * (head_dim + 2) * 4, "hipMalloc(attention)"));
-        Q8AttnDecodeArgs a{};
-        a.q = reinterpret_cast<const float *>(qp);
-        a.kcache = reinterpret_cast<const uint16_t *>(kcache);
-        a.vcache = reinterpret_cast<const uint16_t *>(vcache);
-        a.part_acc = static_cast<float *>(c->attn_ws);
-        a.part_max = a.part_acc ? a.part_acc + parts * head_dim : nullptr;
-        a.part_sum = a.part_max ? a.part_max + parts : nullptr;
-        a.out = reinterpret_cast<float *>(op);
-        a.counters = c->counters + kAttnCounterBase;
-        a.position = reinterpret_cast<const int *>(position);
-        a.n_head = n_head;
-        a.n_kv = n_kv;
-        a.splits = splits;
-        a.capacity = capacity;
-        a.scale = scale;
-        return launch(c, F_ATTN_DECODE, (unsigned)parts, 1024, 0, &a, sizeof a);
-    }
+    return check_span(c, position, 4, "position");
+}
+
+}  // namespace
+
+int q8_attention(q8_ctx *c, q8_dptr q, size_t q_offset, q8_dptr kcache, q8_dptr vcache, q8_dptr out,
+                 size_t out_offset, int n, int n_head, int n_kv, int head_dim, int capacity, float scale,
+                 q8_dptr position, int splits) {
+    if (!c) return fail(Q8_ERR_INVALID, "q8_attention: null context");
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    const q8_dptr qp = (q8_dptr)(uintptr_t)fptr(q, q_offset);
+    const q8_dptr op = (q8_dptr)(uintptr_t)fptr(out, out_offset);
+    Q8_TRY(check_attention(c, qp, kcache, vcache, position, n, n_head, n_kv, head_dim, capacity));
+    Q8_TRY(check_span(c, op, (size_t)n * n_head * head_dim * 4, "attention out"));
+    if (n == 1)
+        return run_attn_decode(c, reinterpret_cast<const float *>(qp), kcache, vcache, reinterpret_cast<float *>(op),
+                               n_head, n_kv, capacity, scale, position, splits, 0);
     Q8AttnPrefillArgs a{};
     a.q = reinterpret_cast<const float *>(qp);
     a.kcache = reinterpret_cast<const uint16_t *>(kcache);
@@ -1585,6 +1650,40 @@ int q8_attention(q8_ctx *c, q8_dptr q, size_t q_offset, q8_dptr kcache, q8_dptr 
     a.qtiles = (int)ceil_div(n, 32);
     a.scale = scale;
     return launch(c, F_ATTN_PREFILL, (unsigned)(n_head * a.qtiles), 128, 0, &a, sizeof a);
+}
+
+int q8_attention_matmul_add(q8_ctx *c, q8_dptr q, size_t q_offset, q8_dptr kcache, q8_dptr vcache, int n_head,
+                            int n_kv, int head_dim, int capacity, float scale, q8_dptr position, int splits,
+                            const q8_weight *wo, q8_dptr y, size_t y_offset) {
+    if (!c) return fail(Q8_ERR_INVALID, "q8_attention_matmul_add: null context");
+    Q8_TRY(check_weight(c, wo));
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    const q8_dptr qp = (q8_dptr)(uintptr_t)fptr(q, q_offset);
+    Q8_TRY(check_attention(c, qp, kcache, vcache, position, 1, n_head, n_kv, head_dim, capacity));
+    if (wo->k != n_head * head_dim)
+        return fail(Q8_ERR_INVALID, "output projection takes k = %d, the heads give %d", wo->k, n_head * head_dim);
+    float *yp = fptr(y, y_offset);
+    Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)yp, (size_t)wo->out * 4, "attention output projection y"));
+    const float *qf = reinterpret_cast<const float *>(qp);
+    Member m{wo, yp};
+    if (gemv_folds_combine(c, wo, splits)) {
+        Q8_TRY(run_attn_decode(c, qf, kcache, vcache, nullptr, n_head, n_kv, capacity, scale, position, splits, 1));
+        const size_t parts = (size_t)n_head * splits;
+        const float *acc = static_cast<const float *>(c->attn_ws);
+        const GemvCombine comb{acc, acc + parts * Q8_ATTN_HEAD_DIM, splits};
+        return run_gemv(c, &m, 1, 0, wo->k, yp, 0, nullptr, 0.0f, nullptr, &comb);
+    }
+    // the two steps, through the attention output workspace
+    Q8_TRY(grow(c, &c->attn_out_ws, &c->attn_out_ws_bytes, (size_t)wo->k * 4, "hipMalloc(attention output)"));
+    float *att = static_cast<float *>(c->attn_out_ws);
+    Q8_TRY(run_attn_decode(c, qf, kcache, vcache, att, n_head, n_kv, capacity, scale, position, splits, 0));
+    return run_gemv(c, &m, 1, (q8_dptr)(uintptr_t)att, wo->k, yp, 0);
+}
+
+extern "C++" {
+namespace q8i {
+int attention_split_rows() { return attn_shape(2).rows; }
+}  // namespace q8i
 }
 
 int q8_advance_position(q8_ctx *c, q8_dptr position, int by) {

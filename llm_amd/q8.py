@@ -55,7 +55,7 @@ EXPORTS = (
     "q8_gguf_tensor", "q8_gguf_meta_count", "q8_gguf_meta_key_at", "q8_gguf_meta_type", "q8_gguf_meta_u64",
     "q8_gguf_meta_f32", "q8_gguf_meta_bool", "q8_gguf_meta_str", "q8_gguf_has_key_prefix",
     "q8_gguf_meta_i32_array", "q8_gguf_meta_f32_array", "q8_gguf_meta_str_array", "q8_gguf_weight",
-    "q8_rope_append", "q8_attention", "q8_embeddings_device", "q8_argmax_device", "q8_advance_position",
+    "q8_rope_append", "q8_attention", "q8_attention_matmul_add", "q8_embeddings_device", "q8_argmax_device", "q8_advance_position",
     "q8_norm_matmul_decode_group", "q8_norm_gate_up_silu", 
     "q8_vector_release", "q8_norm_qkv_rope",
     "q8_weight_synthetic", "q8_decoder_create_synthetic", "q8_decoder_destroy", "q8_decoder_reset",
@@ -214,6 +214,8 @@ def lib():
                                    c_int, ctypes.c_float, c_int, u64]),
         "q8_attention": (c_int, [vp, u64, c_size, u64, u64, u64, c_size, c_int, c_int, c_int, c_int, c_int,
                                  ctypes.c_float, u64, c_int]),
+        "q8_attention_matmul_add": (c_int, [vp, u64, c_size, u64, u64, c_int, c_int, c_int, c_int, ctypes.c_float,
+                                            u64, c_int, vp, u64, c_size]),
         "q8_embeddings_device": (c_int, [vp, vp, u64, c_size, u64, c_size]),
         "q8_argmax_device": (c_int, [vp, u64, c_size, c_size, u64]),
         "q8_advance_position": (c_int, [vp, u64, c_int]),
@@ -542,6 +544,15 @@ class Gpu:
                   splits: int = 1, q_offset=0, out_offset=0):
         _check(lib().q8_attention(self.handle, q.ptr, q_offset, kcache.ptr, vcache.ptr, out.ptr, out_offset, n,
                                   n_head, n_kv, head_dim, capacity, float(scale), position.ptr, splits))
+
+    def attention_matmul_add(self, q: DeviceBuffer, kcache: DeviceBuffer, vcache: DeviceBuffer, n_head: int,
+                             n_kv: int, head_dim: int, capacity: int, scale: float, position: DeviceBuffer,
+                             splits: int, wo: Weight, y: DeviceBuffer, q_offset: int = 0, y_offset: int = 0):
+        """One token's attention then y += wo . attn (the split combine folded
+        into the GEMV's prologue)."""
+        _check(lib().q8_attention_matmul_add(self.handle, q.ptr, q_offset, kcache.ptr, vcache.ptr, n_head, n_kv,
+                                             head_dim, capacity, float(scale), position.ptr, splits,
+                                             self.resident(wo), y.ptr, y_offset))
 
     def embeddings_device(self, weight, tokens: DeviceBuffer, n: int, out: DeviceBuffer, out_offset: int = 0):
         _check(lib().q8_embeddings_device(self.handle, self.resident(weight), tokens.ptr, n, out.ptr, out_offset))

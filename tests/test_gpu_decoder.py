@@ -230,6 +230,44 @@ def test_decode_attention_matches_the_oracle(gpu, visible, splits, n_head, n_kv)
     assert_close(got, oracle.attention(q, kf, vf, visible - 1, 0.125), f"decode attention L={visible} s={splits}")
 
 
+@pytest.mark.parametrize("visible,splits,n_head,n_kv", [(1, 1, 4, 2), (200, 1, 36, 36), (600, 3, 36, 36),
+                                                        (640, 8, 36, 36), (4096, 8, 4, 1), (3000, 5, 8, 2),
+                                                        (2000, 12, 8, 8), (300, 2, 32, 8)])
+@pytest.mark.parametrize("exact", [1, 0])
+def test_attention_matmul_add_equals_attention_then_matmul(gpu, visible, splits, n_head, n_kv, exact):
+    """q8_attention_matmul_add: the partials combined in the output
+    projection's GEMV prologue (or, past eight splits, the two calls it makes
+    instead) give y bit-identical to q8_attention with the same splits then
+    q8_matmul with y as the residual; and the attention alone is within the
+    f32 bar of the oracle."""
+    gpu.set_option("gemv.exact", exact)
+    r = np.random.default_rng(SEED + 7 * visible + splits)
+    capacity = max(visible, 256)
+    kf, vf, kc, vc = cache_pair(gpu, r, visible, capacity, n_kv)
+    E = n_head * 64
+    q = (r.standard_normal((1, n_head, 64)) * 2).astype(np.float32)
+    wo = q8w(r, E, E)
+    y0 = r.standard_normal(E).astype(np.float32)
+    qb, att, yref, yf = gpu.alloc(q.nbytes), gpu.alloc(q.nbytes), gpu.alloc(4 * E), gpu.alloc(4 * E)
+    qb.upload(q)
+    yref.upload(y0)
+    yf.upload(y0)
+    pos = int_buffer(gpu, visible - 1)
+    try:
+        print(f"\nattention + O visible={visible} splits={splits} heads={n_head}/{n_kv} exact={exact}", flush=True)
+        gpu.attention(qb, kc, vc, att, 1, n_head, n_kv, 64, capacity, 0.125, pos, splits)
+        gpu.matmul(wo, att, 0, 1, yref, 0, bias=yref)
+        gpu.attention_matmul_add(qb, kc, vc, n_head, n_kv, 64, capacity, 0.125, pos, splits, wo, yf)
+        assert_bits(yf.download(np.float32, E), yref.download(np.float32, E), "fused attention + O projection")
+        a_ref = oracle.attention(q, kf, vf, visible - 1, 0.125)
+        assert_close(att.download(np.float32, q.size).reshape(q.shape), a_ref, "attention vs oracle")
+    finally:
+        gpu.set_option("gemv.exact", -1)
+        for b in (qb, att, yref, yf, kc, vc, pos):
+            b.free()
+        gpu.release(wo)
+
+
 @pytest.mark.parametrize("n,start,n_head,n_kv", [(2, 0, 4, 2), (64, 0, 4, 4), (100, 0, 2, 1), (130, 37, 4, 2),
                                                  (512, 0, 36, 36)])
 def test_prefill_attention_matches_the_oracle(gpu, n, start, n_head, n_kv):
