@@ -293,6 +293,21 @@ extern "C" __global__ __launch_bounds__(256) void q8_attn_decode_w4(Q8AttnDecode
 // ---------------------------------------------------------------------------
 #define Q8_ATTN_VT_STRIDE 72  /* f16 per V^T row in LDS: 64 keys + 8 of padding, 144 B (16-byte rows) */
 
+// e^x for the softmax's x = s - max <= 0 (x = -inf or below the f32 range
+// gives 0): x = n ln2 + r with n = rint(x log2e) and r from a two-part ln2
+// (Cody-Waite reduction: ln2_hi has 15 significant bits, so n ln2_hi is exact
+// for |n| < 2^9), then e^r = 2^(r log2e) on v_exp_f32 (|r log2e| <= 1/2) and
+// 2^n by ldexp.  With a correctly rounded exp2 the result is within 0.85
+// ulp of e^x on [-87, 0] (checked in f32 emulation); v_exp_f32 adds its own
+// (at most 1 ulp).  Nine instructions where the library expf takes ~25.
+static __device__ __forceinline__ float exp_nonpos(float x) {
+    const float n = __builtin_rintf(x * 1.44269504f);
+    float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+    r = __builtin_fmaf(-n, 1.42860682e-06f, r);
+    const float e = __builtin_ldexpf(__builtin_amdgcn_exp2f(r * 1.44269504f), (int)n);
+    return x >= -87.0f ? e : 0.0f;
+}
+
 static __device__ __forceinline__ void split_f16(const float *x, f16x8 &hi, f16x8 &lo) {
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -342,43 +357,26 @@ extern "C" __global__ __launch_bounds__(128) void q8_attn_prefill(Q8AttnPrefillA
     const int last_q = min(qt * 32 + 31, a.n - 1);
     const int kend = min(start + last_q + 1, a.capacity);  // keys [0, kend)
     const int ntiles = (kend + 63) >> 6;
-    for (int t = wave; t < ntiles; t += 2) {
-        const int p0 = t * 64;
-        // K operand rows (keys p0 + 32kt + r), d-slices 16s + 8h: loads issued first
-        i32x4 kk[2][4];
+    // K operand rows (keys p0 + 32kt + r), d-slices 16s + 8h, of this wave's
+    // tile t: the next tile's are loaded while the current one is computed
+    i32x4 kn[2][4];
+    auto load_k = [&](int t) {
 #pragma unroll
         for (int kt = 0; kt < 2; kt++) {
-            const int key = min(p0 + 32 * kt + r, a.capacity - 1);
+            const int key = min(t * 64 + 32 * kt + r, a.capacity - 1);
             const uint16_t *krow = a.kcache + (size_t)key * kv_dim + kvh * HD + 8 * h;
 #pragma unroll
-            for (int s = 0; s < 4; s++) kk[kt][s] = *(const i32x4 *)(krow + 16 * s);
+            for (int s = 0; s < 4; s++) kn[kt][s] = *(const i32x4 *)(krow + 16 * s);
         }
-        // V^T tile (wave-private): lane -> dims 2(lane%32), +1 and keys 16(lane/32) .. +15 and +32
-        {
-            const int dp = lane & 31;
+    };
+    if (wave < ntiles) load_k(wave);
+    for (int t = wave; t < ntiles; t += 2) {
+        const int p0 = t * 64;
+        i32x4 kk[2][4];
 #pragma unroll
-            for (int half_keys = 0; half_keys < 2; half_keys++) {
-                const int kb = 32 * half_keys + 16 * h;
-                unsigned w[16];
+        for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const int key = p0 + kb + i;
-                    w[i] = key < kend ? *(const unsigned *)(a.vcache + (size_t)key * kv_dim + kvh * HD + 2 * dp) : 0u;
-                }
-                i32x4 r0[2], r1[2];
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    r0[j >> 2][j & 3] = (int)__builtin_amdgcn_perm(w[2 * j + 1], w[2 * j], 0x05040100u);
-                    r1[j >> 2][j & 3] = (int)__builtin_amdgcn_perm(w[2 * j + 1], w[2 * j], 0x07060302u);
-                }
-                i32x4 *d0 = (i32x4 *)(vt + (2 * dp) * Q8_ATTN_VT_STRIDE + kb);
-                i32x4 *d1 = (i32x4 *)(vt + (2 * dp + 1) * Q8_ATTN_VT_STRIDE + kb);
-                d0[0] = r0[0];
-                d0[1] = r0[1];
-                d1[0] = r1[0];
-                d1[1] = r1[1];
-            }
-        }
+            for (int s = 0; s < 4; s++) kk[kt][s] = kn[kt][s];
         // S^T: keys x queries
         f32x16 st[2];
 #pragma unroll
@@ -392,6 +390,23 @@ extern "C" __global__ __launch_bounds__(128) void q8_attn_prefill(Q8AttnPrefillA
             }
             st[kt] = acc;
         }
+        // This tile's value rows (lane -> dims 2(lane%32), +1 at keys
+        // 16(lane/32) .. +15 and +32), then the next tile's keys; both land
+        // while the softmax runs.
+        const int dp = lane & 31;
+        unsigned w[2][16];
+#pragma unroll
+        for (int half_keys = 0; half_keys < 2; half_keys++) {
+            const int kb = 32 * half_keys + 16 * h;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                // keys past the last visible one: a clamped (in-bounds) load, then zero
+                const int key = p0 + kb + i;
+                const unsigned u = *(const unsigned *)(a.vcache + (size_t)min(key, kend - 1) * kv_dim + kvh * HD + 2 * dp);
+                w[half_keys][i] = key < kend ? u : 0u;
+            }
+        }
+        if (t + 2 < ntiles) load_k(t + 2);
         // scale, causal mask, online softmax for query qrow; a tile whose last
         // key precedes the workgroup's first query needs no mask
         float tm = -INFINITY;
@@ -418,13 +433,13 @@ extern "C" __global__ __launch_bounds__(128) void q8_attn_prefill(Q8AttnPrefillA
         const float mn = fmaxf(m, tm);
         // a wave's first tile may be all masked for its queries only if it is
         // not tile 0; then m and mn stay -inf: no weight and no rescale
-        const float corr = (mn == -INFINITY) ? 1.0f : expf(m - mn);
+        const float corr = (mn == -INFINITY) ? 1.0f : exp_nonpos(m - mn);
         float rs = 0.0f;
 #pragma unroll
         for (int kt = 0; kt < 2; kt++)
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                const float e = (mn == -INFINITY) ? 0.0f : expf(st[kt][v] - mn);
+                const float e = (mn == -INFINITY) ? 0.0f : exp_nonpos(st[kt][v] - mn);
                 st[kt][v] = e;
                 rs += e;
             }
@@ -435,6 +450,25 @@ extern "C" __global__ __launch_bounds__(128) void q8_attn_prefill(Q8AttnPrefillA
         for (int dt = 0; dt < 2; dt++)
 #pragma unroll
             for (int v = 0; v < 16; v++) o[dt][v] *= corr;
+        // V^T tile (wave-private) from the value rows
+#pragma unroll
+        for (int half_keys = 0; half_keys < 2; half_keys++) {
+            const int kb = 32 * half_keys + 16 * h;
+            i32x4 r0[2], r1[2];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                r0[j >> 2][j & 3] =
+                    (int)__builtin_amdgcn_perm(w[half_keys][2 * j + 1], w[half_keys][2 * j], 0x05040100u);
+                r1[j >> 2][j & 3] =
+                    (int)__builtin_amdgcn_perm(w[half_keys][2 * j + 1], w[half_keys][2 * j], 0x07060302u);
+            }
+            i32x4 *d0 = (i32x4 *)(vt + (2 * dp) * Q8_ATTN_VT_STRIDE + kb);
+            i32x4 *d1 = (i32x4 *)(vt + (2 * dp + 1) * Q8_ATTN_VT_STRIDE + kb);
+            d0[0] = r0[0];
+            d0[1] = r0[1];
+            d1[0] = r1[0];
+            d1[1] = r1[1];
+        }
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's V^T stores are done
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __builtin_amdgcn_wave_barrier();
