@@ -99,6 +99,17 @@ int q8_norm_qkv_rope(q8_ctx *ctx, const float *norm_weight, float eps, const q8_
                      q8_dptr vcache, int n_head, int n_kv, int head_dim, int n_rot, float base, int capacity,
                      q8_dptr position);
 
+/* The prompt counterpart of q8_norm_qkv_rope: q8_matmul_prompt_group of the
+ * q, k, v weights over prepared activations (n tokens) with q8_rope_append in
+ * the GEMM's epilogue -- bit-identical to those two calls.  q [n][n_head *
+ * head_dim] f32 receives the rotated queries; k and v go only into the f16
+ * caches, at rows *position + t (tokens at or past capacity append nothing and
+ * leave their q unrotated).  The reference runs the steps as separate kernels
+ * (model.rs dense_attention: matmul_prompt_group, rope_append). */
+int q8_prompt_qkv_rope(q8_ctx *ctx, const q8_weight *wq, const q8_weight *wk, const q8_weight *wv,
+                       const q8_prepared *prepared, int n, q8_dptr q, size_t q_offset, q8_dptr kcache, q8_dptr vcache,
+                       int n_head, int n_kv, int head_dim, int n_rot, float base, int capacity, q8_dptr position);
+
 /* q8_rmsnorm (one row) followed by q8_gate_up_silu at n = 1, folded the same
  * way: act = silu(gate . xn) * (up . xn), xn = rmsnorm(x) * norm_weight. */
 int q8_norm_gate_up_silu(q8_ctx *ctx, const float *norm_weight, float eps, const q8_weight *gate,

@@ -72,7 +72,7 @@ struct q8_decoder {
     std::vector<Layer> layers;
     const q8_weight *embd = nullptr;
     std::vector<float> output_norm;
-    q8_dptr x = 0, normed = 0, q = 0, k = 0, v = 0, attn = 0, gate = 0, up = 0, act = 0, logits = 0;
+    q8_dptr x = 0, normed = 0, q = 0, attn = 0, act = 0, logits = 0;
     q8_dptr pos = 0, tokens = 0;
     int position = 0;  // host mirror of *pos
     std::map<std::pair<int, int>, void *> graphs;
@@ -134,7 +134,6 @@ int q8_decoder::body(int n, int splits) {
     DEC_TRY(q8_embeddings_device(c, embd, tokens, (size_t)n, x, 0));
     for (Layer &L : layers) {
         // attention block (dense_attention, model.rs:869-1043)
-        q8_group_entry qkv[3] = {{L.w[Q8_DEC_Q], q, 0}, {L.w[Q8_DEC_K], k, 0}, {L.w[Q8_DEC_V], v, 0}};
         if (n == 1) {  // norm, q/k/v and rope + KV append in one launch
             DEC_TRY(q8_norm_qkv_rope(c, L.attn_norm.data(), g.eps, L.w[Q8_DEC_Q], L.w[Q8_DEC_K], L.w[Q8_DEC_V], x, 0,
                                      q, 0, L.kcache, L.vcache, g.n_head, g.n_head_kv, g.head_dim, g.n_rot,
@@ -142,9 +141,9 @@ int q8_decoder::body(int n, int splits) {
         } else {
             q8_prepared p{};
             DEC_TRY(q8_norm_prepare(c, x, 0, L.attn_norm.data(), E, g.eps, n, &p));
-            DEC_TRY(q8_matmul_prompt_group(c, qkv, 3, &p, n, E, 0, 0));
-            DEC_TRY(q8_rope_append(c, q, 0, k, 0, v, 0, L.kcache, L.vcache, n, g.n_head, g.n_head_kv, g.head_dim,
-                                   g.n_rot, g.rope_base, g.capacity, pos));
+            DEC_TRY(q8_prompt_qkv_rope(c, L.w[Q8_DEC_Q], L.w[Q8_DEC_K], L.w[Q8_DEC_V], &p, n, q, 0, L.kcache,
+                                       L.vcache, g.n_head, g.n_head_kv, g.head_dim, g.n_rot, g.rope_base,
+                                       g.capacity, pos));
         }
         if (n == 1) {  // attention, its split combine folded into the output projection
             DEC_TRY(q8_attention_matmul_add(c, q, 0, L.kcache, L.vcache, g.n_head, g.n_head_kv, g.head_dim,
@@ -237,9 +236,7 @@ int q8_decoder_create_synthetic(q8_ctx *c, const q8_decoder_config *config, uint
     const size_t f = sizeof(float);
     if ((rc = d->alloc((size_t)B * E * f, &d->x)) || (rc = d->alloc((size_t)B * E * f, &d->normed)) ||
         (rc = d->alloc((size_t)B * g.n_head * g.head_dim * f, &d->q)) ||
-        (rc = d->alloc((size_t)B * kv_dim * f, &d->k)) || (rc = d->alloc((size_t)B * kv_dim * f, &d->v)) ||
         (rc = d->alloc((size_t)B * g.n_head * g.head_dim * f, &d->attn)) ||
-        (rc = d->alloc((size_t)B * g.n_ff * f, &d->gate)) || (rc = d->alloc((size_t)B * g.n_ff * f, &d->up)) ||
         (rc = d->alloc((size_t)B * g.n_ff * f, &d->act)) || (rc = d->alloc((size_t)g.n_vocab * f, &d->logits)) ||
         (rc = d->alloc(256, &d->pos)) || (rc = d->alloc((size_t)B * 4, &d->tokens)))
         return fail(rc);

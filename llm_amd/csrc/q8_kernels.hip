@@ -780,9 +780,79 @@ extern "C" __global__ __launch_bounds__(256) void q8_quantize(Q8QuantArgs a) {
 // The residual (bias) values are loaded first, all 16 per tile at clamped
 // addresses, so their loads are in flight together; then the stores.
 // ---------------------------------------------------------------------------
+//
+// With rope_pos set (a q, k, v group, member mi), the tile goes through
+// q8_rope_append's arithmetic instead: rows 2i and 2i+1 of a head are lanes r
+// and r ^ 1 (tiles start at multiples of 32 and head_dim is even), so each
+// lane takes its partner's value for the same token by one shuffle and keeps
+// its half of the rotated pair -- the angle (position * freq), sincosf and
+// the f16 narrowing of that kernel.  q is written rotated in f32; k rotated
+// and v as they are go only to the f16 caches, at row position + token.
 template <int TPW>
-static __device__ __forceinline__ void store_tiles(const Q8GemmArgs &a, const Q8GemmMember &mem,
+static __device__ __forceinline__ void store_rope_tiles(const Q8GemmArgs &a, const Q8GemmMember &mem, int mi,
+                                                        const f32x16 (&acc)[TPW], int tt0, int o, int h) {
+    const int start = *a.rope_pos;
+    const int d = o % a.head_dim;
+    const int pair = d >> 1;
+    const bool even = (d & 1) == 0;
+    const bool rot = mi < 2 && 2 * pair < a.n_rot;
+    const float freq = rot ? a.rope_freq[pair] : 0.0f;
+    uint16_t *cache = mi == 1 ? a.kcache : a.vcache;
+    const int odd = even ? 0 : 1;  // of the pair's lanes r, r ^ 1, the odd one takes elements 8..15
+#pragma unroll
+    for (int t = 0; t < TPW; t++) {
+        if (tt0 + t >= a.ttiles) continue;  // wave-uniform
+        const int tok0 = (tt0 + t) * Q8_TILE_TOKENS + 4 * h;  // token of element i: tok0 + 8(i/4) + i%4
+        // The pair's two lanes need the same 16 angles: each computes eight
+        // (the even lane elements 0-7, the odd lane 8-15) and they swap.
+        float sn[16], cs[16];
+        if (mi < 2) {  // wave-uniform
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int i = j + 8 * odd;
+                const float angle = (float)(start + tok0 + 8 * (i >> 2) + (i & 3)) * freq;
+                float sj, cj;
+                sincosf(angle, &sj, &cj);
+                const float so = __shfl_xor(sj, 1), co = __shfl_xor(cj, 1);
+                sn[j] = odd ? so : sj;
+                cs[j] = odd ? co : cj;
+                sn[j + 8] = odd ? sj : so;
+                cs[j + 8] = odd ? cj : co;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float x = acc[t][i];
+            const float other = __shfl_xor(x, 1);  // the partner row, same token
+            const int tok = tok0 + 8 * (i >> 2) + (i & 3);
+            const int pos = start + tok;
+            const bool in_cache = pos >= 0 && pos < a.capacity;
+            if (tok < a.n && o < mem.rows) {
+                const float x0 = even ? x : other;
+                const float x1 = even ? other : x;
+                float y0 = x0, y1 = x1;
+                if (in_cache && rot) {
+                    y0 = x0 * cs[i] - x1 * sn[i];
+                    y1 = x0 * sn[i] + x1 * cs[i];
+                }
+                const float out = even ? y0 : y1;
+                if (mi == 0) {
+                    mem.y[(size_t)tok * mem.rows + o] = out;
+                } else if (in_cache) {
+                    cache[(size_t)pos * mem.rows + o] = (uint16_t)f16_bits(out);
+                }
+            }
+        }
+    }
+}
+
+template <int TPW>
+static __device__ __forceinline__ void store_tiles(const Q8GemmArgs &a, const Q8GemmMember &mem, int mi,
                                                    const f32x16 (&acc)[TPW], int tt0, int o, int h) {
+    if (a.rope_pos) {
+        store_rope_tiles<TPW>(a, mem, mi, acc, tt0, o, h);
+        return;
+    }
     if (o >= mem.rows) return;
 #pragma unroll
     for (int t = 0; t < TPW; t++) {
@@ -1058,7 +1128,7 @@ static __device__ __forceinline__ void gemm_body(const Q8GemmArgs &a) {
     }
     if (kw != 0) return;
 
-    store_tiles<TPW>(a, mem, acc, tt0, g * Q8_TILE_ROWS + r, h);
+    store_tiles<TPW>(a, mem, mi, acc, tt0, g * Q8_TILE_ROWS + r, h);
 }
 
 // ---------------------------------------------------------------------------
@@ -1478,7 +1548,7 @@ static __device__ __forceinline__ void gemm_h_body(const Q8GemmArgs &a) {
         }
     }
     if (kw != 0 || !row_live) return;
-    store_tiles<TPW>(a, mem, acc, tt0, g * Q8_TILE_ROWS + r, h);
+    store_tiles<TPW>(a, mem, mi, acc, tt0, g * Q8_TILE_ROWS + r, h);
 }
 
 // q8_gemm_h_t<TPW>_r<RW>: up to 512 threads (RW x KW waves).
@@ -1685,7 +1755,7 @@ static __device__ __forceinline__ void gemm_p_body(const Q8GemmArgs &a) {
         }
     }
     if (kw != 0) return;
-    store_tiles<TPW>(a, mem, acc, tt0, g * Q8_TILE_ROWS + r, h);
+    store_tiles<TPW>(a, mem, mi, acc, tt0, g * Q8_TILE_ROWS + r, h);
 }
 
 extern "C" __global__ __launch_bounds__(512) void q8_gemm_p_t1(Q8GemmArgs a) { gemm_p_body<1>(a); }

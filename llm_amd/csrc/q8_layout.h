@@ -186,6 +186,16 @@ typedef struct {
     uint8_t *oq;          /* q8_gemm_silu: prepared Q8_0 output of silu(gate) * up (quants) */
     float *os;            /* q8_gemm_silu: its scales */
     int of16;             /* q8_gemm_silu: 1 = f16 prepared units */
+    /* RoPE + KV append epilogue of a q, k, v prompt group (members 0, 1, 2;
+     * non-null rope_pos turns it on): q rows rotated into m[0].y; k rotated
+     * and v copied as f16 into kcache / vcache [capacity][rows] at rows
+     * *rope_pos + token (nothing for tokens outside the cache, whose q stays
+     * unrotated). */
+    const int *rope_pos;
+    const float *rope_freq; /* n_rot / 2 frequencies base^(-2i/n_rot), from the host */
+    uint16_t *kcache;
+    uint16_t *vcache;
+    int head_dim, n_rot, capacity;
 } Q8GemmArgs;
 
 typedef struct {

@@ -489,7 +489,8 @@ int run_norm_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, int s
     return run_gemv(c, m, count, (q8_dptr)(uintptr_t)xn, k, nullptr, silu, nullptr, 0.0f, rope);
 }
 
-int run_gemm_h(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n, const float *bias);
+int run_gemm_h(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n, const float *bias,
+               const GemvRope *rope = nullptr);
 
 // Gate/up GEMM whose epilogue writes silu(gate) * up as prepared Q8_0
 // (q8_gemm_silu) into the second activation workspace: the input stays
@@ -546,14 +547,27 @@ int run_gemm_silu(q8_ctx *c, const q8_weight *gate, const q8_weight *up, const q
     return Q8_OK;
 }
 
-int run_gemm(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n, const float *bias) {
-    if (p->format == Q8_PREPARED_F16) return run_gemm_h(c, m, count, p, n, bias);
+// Sets the RoPE + KV append epilogue of a q, k, v group (rope non-null).
+void set_gemm_rope(Q8GemmArgs &a, const GemvRope *rope) {
+    if (!rope) return;
+    a.rope_pos = rope->position;
+    a.rope_freq = rope->freq;
+    a.kcache = rope->kcache;
+    a.vcache = rope->vcache;
+    a.head_dim = rope->head_dim;
+    a.n_rot = rope->n_rot;
+    a.capacity = rope->capacity;
+}
+
+int run_gemm(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n, const float *bias,
+             const GemvRope *rope = nullptr) {
+    if (p->format == Q8_PREPARED_F16) return run_gemm_h(c, m, count, p, n, bias, rope);
     if (p->format != Q8_PREPARED_I8) return fail(Q8_ERR_INVALID, "prepared activations: unknown format %d", p->format);
     {
         int rows_total = 0;
         for (int i = 0; i < count; i++) rows_total += m[i].w->out;
         const q8_tactic t = plan(c, n, rows_total, p->k, 1, Q8_PREPARED_I8);
-        if (t.rwaves > 0) return run_gemm_h(c, m, count, p, n, bias);
+        if (t.rwaves > 0) return run_gemm_h(c, m, count, p, n, bias, rope);
     }
     const int k = p->k;
     const int nb = k / 32;
@@ -586,6 +600,7 @@ int run_gemm(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n,
     const int kwaves = std::max(1, t.kwaves);
     a.scratch = c->split_ws;
     a.counters = c->counters;
+    set_gemm_rope(a, rope);
     const long long groups = (long long)rt * a.tgroups;
     if (a.kslices > 1) {
         const size_t need = (size_t)rt * a.ttiles * a.kslices * 64 * 16 * sizeof(float);
@@ -610,7 +625,8 @@ int run_gemm(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n,
 // workgroup over TPW token tiles, activations staged in LDS per K group;
 // f16 units on the f16 MFMA (q8_gemm_h) or int8 units on the int8 MFMA
 // (q8_gemm_l), by the prepared format.
-int run_gemm_h(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n, const float *bias) {
+int run_gemm_h(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n, const float *bias,
+               const GemvRope *rope) {
     const int k = p->k;
     const int nb = k / 32;
     Q8GemmArgs a{};
@@ -644,6 +660,7 @@ int run_gemm_h(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int 
     a.kslices = 1;
     a.pairs_per_slice = (nb + 1) / 2;
     a.pairs_per_wave = std::max(1, t.pairs_per_wave);
+    set_gemm_rope(a, rope);
     if ((long long)a.pairs_per_wave * kw < (nb + 1) / 2)
         return fail(Q8_ERR_UNSUPPORTED, "gemm_h: %d K waves x %d pairs miss blocks", kw, a.pairs_per_wave);
     const long long nwg = ceil_div(rt, rw) * (long long)a.tgroups;
@@ -1524,6 +1541,44 @@ int q8_norm_qkv_rope(q8_ctx *c, const float *norm_weight, float eps, const q8_we
     rope.capacity = capacity;
     Member m[3] = {{wq, qp}, {wk, nullptr}, {wv, nullptr}};
     return run_norm_gemv(c, m, 3, xp, k, 0, w, eps, &rope);
+}
+
+int q8_prompt_qkv_rope(q8_ctx *c, const q8_weight *wq, const q8_weight *wk, const q8_weight *wv,
+                       const q8_prepared *prepared, int n, q8_dptr q, size_t q_offset, q8_dptr kcache, q8_dptr vcache,
+                       int n_head, int n_kv, int head_dim, int n_rot, float base, int capacity, q8_dptr position) {
+    if (!c || !prepared) return fail(Q8_ERR_INVALID, "q8_prompt_qkv_rope: bad arguments");
+    if (n_head < 1 || n_kv < 1 || n_head % n_kv || head_dim < 2 || head_dim % 2 || n_rot < 0 || n_rot > head_dim ||
+        n_rot % 2 || capacity < 1)
+        return fail(Q8_ERR_INVALID, "prompt_qkv_rope: bad geometry (heads %d/%d, head_dim %d, n_rot %d)", n_head, n_kv,
+                    head_dim, n_rot);
+    Q8_TRY(check_n(n));
+    Q8_TRY(check_weight(c, wq));
+    Q8_TRY(check_weight(c, wk));
+    Q8_TRY(check_weight(c, wv));
+    const int k = wq->k;
+    const int kv_dim = n_kv * head_dim;
+    if (wk->k != k || wv->k != k || wq->out != n_head * head_dim || wk->out != kv_dim || wv->out != kv_dim)
+        return fail(Q8_ERR_INVALID, "prompt_qkv_rope: q/k/v weights are %dx%d, %dx%d, %dx%d for %d/%d heads of %d",
+                    wq->out, wq->k, wk->out, wk->k, wv->out, wv->k, n_head, n_kv, head_dim);
+    if (prepared->n != n || prepared->k != k)
+        return fail(Q8_ERR_INVALID, "prepared activations are %d x %d, the matmul wants %d x %d", prepared->n,
+                    prepared->k, n, k);
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    float *qp = fptr(q, q_offset);
+    Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)qp, (size_t)n * wq->out * 4, "rope q"));
+    Q8_TRY(check_span(c, kcache, (size_t)capacity * kv_dim * 2, "key cache"));
+    Q8_TRY(check_span(c, vcache, (size_t)capacity * kv_dim * 2, "value cache"));
+    Q8_TRY(check_span(c, position, 4, "position"));
+    GemvRope rope{};
+    Q8_TRY(rope_table(c, n_rot, base, &rope.freq));
+    rope.position = reinterpret_cast<const int *>(position);
+    rope.kcache = reinterpret_cast<uint16_t *>(kcache);
+    rope.vcache = reinterpret_cast<uint16_t *>(vcache);
+    rope.head_dim = head_dim;
+    rope.n_rot = n_rot;
+    rope.capacity = capacity;
+    Member m[3] = {{wq, qp}, {wk, nullptr}, {wv, nullptr}};
+    return run_gemm(c, m, 3, prepared, n, nullptr, &rope);
 }
 
 int q8_rope_append(q8_ctx *c, q8_dptr q, size_t q_offset, q8_dptr k, size_t k_offset, q8_dptr v, size_t v_offset,

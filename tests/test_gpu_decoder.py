@@ -142,6 +142,53 @@ def test_norm_qkv_rope_equals_norm_group_then_rope_append(gpu, E, n_head, n_kv, 
             gpu.release(w)
 
 
+@pytest.mark.parametrize("E,n_head,n_kv,n_rot,n,position,capacity,option", [
+    (2304, 36, 36, 64, 512, 0, 4096, None), (256, 4, 2, 32, 70, 37, 128, None), (512, 8, 2, 64, 40, 100, 128, None),
+    (256, 4, 4, 64, 33, 0, 64, ("gemm.f16", 1)), (1024, 16, 4, 16, 64, 5, 256, ("gemm.pipe", 1)),
+    (2304, 36, 36, 64, 48, 7, 256, ("gemm.slices", 3)), (256, 4, 2, 64, 2, 126, 128, None)])
+def test_prompt_qkv_rope_equals_group_then_rope_append(gpu, E, n_head, n_kv, n_rot, n, position, capacity, option):
+    """q8_prompt_qkv_rope (RoPE + KV append in the q/k/v GEMM's epilogue)
+    against q8_matmul_prompt_group + q8_rope_append on the same prepared
+    activations: the rotated q and both whole caches bit-identical, on the
+    int8, f16-MFMA, pipelined and K-split GEMM paths, with partial rotation,
+    grouped kv heads, and tokens past the cache's end (q unrotated, nothing
+    appended)."""
+    if option:
+        gpu.set_option(*option)
+    r = np.random.default_rng(SEED + E + n + position)
+    hd, base = 64, 10000.0
+    kv_dim = n_kv * hd
+    wq, wk, wv = q8w(r, n_head * hd, E), q8w(r, kv_dim, E), q8w(r, kv_dim, E)
+    x = oracle.make_activations(r, n, E)
+    xb = gpu.alloc(4 * n * E)
+    xb.upload(x)
+    q1, q2 = gpu.alloc(4 * n * n_head * hd), gpu.alloc(4 * n * n_head * hd)
+    k1, v1 = gpu.alloc(4 * n * kv_dim), gpu.alloc(4 * n * kv_dim)
+    kc1, vc1 = f16_buffer(gpu, capacity, kv_dim), f16_buffer(gpu, capacity, kv_dim)
+    kc2, vc2 = f16_buffer(gpu, capacity, kv_dim), f16_buffer(gpu, capacity, kv_dim)
+    pos = int_buffer(gpu, position)
+    try:
+        print(f"\nprompt_qkv_rope E={E} heads={n_head}/{n_kv} rot={n_rot} n={n} pos={position} cap={capacity} "
+              f"{option}", flush=True)
+        p = gpu.prepare(xb, 0, n, E)
+        gpu.matmul_prompt_group([(wq, q1, 0), (wk, k1, 0), (wv, v1, 0)], p, n, E)
+        gpu.rope_append(q1, k1, v1, kc1, vc1, n, n_head, n_kv, hd, n_rot, base, capacity, pos)
+        gpu.prompt_qkv_rope(wq, wk, wv, p, n, q2, kc2, vc2, n_head, n_kv, hd, n_rot, base, capacity, pos)
+        gpu.sync()
+        assert_bits(q2.download(np.float32, n * n_head * hd), q1.download(np.float32, n * n_head * hd), "rotated q")
+        for name, a, b in (("key", kc2, kc1), ("value", vc2, vc1)):
+            got = read_f16(a, capacity, kv_dim).view(np.uint16)
+            want = read_f16(b, capacity, kv_dim).view(np.uint16)
+            assert np.array_equal(got, want), f"{name} cache: {int((got != want).sum())} halves differ"
+    finally:
+        if option:
+            gpu.set_option(option[0], -1)
+        for b in (xb, q1, q2, k1, v1, kc1, vc1, kc2, vc2, pos):
+            b.free()
+        for w in (wq, wk, wv):
+            gpu.release(w)
+
+
 @pytest.mark.parametrize("ffn,k", [(5760, 2304), (640, 2304), (64, 2304), (2304, 5760)])
 def test_norm_folded_gate_up_silu_equals_norm_then_gate_up(gpu, ffn, k):
     r = np.random.default_rng(SEED + ffn + k)
