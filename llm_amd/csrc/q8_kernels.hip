@@ -1882,7 +1882,8 @@ extern "C" __global__ __launch_bounds__(256) void q8_embed(Q8EmbedArgs a) {
 // ---------------------------------------------------------------------------
 // RMSNorm (ops.rs:5-30), as f32 rows and/or straight into prepared Q8_0
 // activations (compute.rs:959-984 norm_prepare; gpu.cu rmsnorm_quantize_rows
-// 351-407).  One wave per token row, four rows per workgroup.
+// 351-407) for rows longer than the 256-thread row kernel below takes.  One
+// wave per token row, four rows per workgroup.
 //
 // The row's squares are taken in f32 and summed in f64 (ggml's choice, kept
 // by the reference), here as per-lane partial sums reduced across the wave;
@@ -1950,18 +1951,23 @@ extern "C" __global__ __launch_bounds__(256) void q8_rmsnorm(Q8NormArgs a) {
     }
 }
 
-// RMSNorm of single rows to f32 (the decode step's norms): a 256-thread
-// workgroup per row.  Each thread loads its float4s of x and w once, up front
-// (k <= 256 * 4 * Q8_NORM_ROW_VEC), adds its squares in f64, the waves meet in
-// LDS in a fixed order, and the row is scaled from registers: one memory round
-// trip where the wave-per-row kernel above makes one per 256 elements.  The f64
-// sum is the same set of f32 terms as there, in another order.
+// RMSNorm with a 256-thread workgroup per row (k <= 256 * 4 * Q8_NORM_ROW_VEC;
+// the decode step's norms, and norm_prepare's rows).  Each thread loads its
+// float4s of x (and w) once, up front, adds its squares in f64, the waves meet
+// in LDS in a fixed order, and the row is scaled from registers: one memory
+// round trip where the wave-per-row kernel above makes one per 256 elements.
+// The f64 sum is the same set of f32 terms as there, in another order.  The
+// prepared Q8_0 output uses that kernel's per-half-block element layout and
+// quantizer; rows from n up to the token-tile boundary are written as zeros.
 extern "C" __global__ __launch_bounds__(256) void q8_rmsnorm_row(Q8NormArgs a) {
     __shared__ double part[4];
     const int tid = threadIdx.x;
+    const int t = blockIdx.x;
     const int k = a.k;
     const int nv = k >> 2;
-    const f32x4 *xr = (const f32x4 *)(a.x + (size_t)blockIdx.x * k);
+    const bool live = t < a.n;  // rows from n to the token-tile boundary quantize as zeros
+    const float *xrow = a.x + (size_t)min(t, a.n - 1) * k;
+    const f32x4 *xr = (const f32x4 *)xrow;
     const f32x4 *wr = (const f32x4 *)a.w;
     f32x4 xv[Q8_NORM_ROW_VEC], wv[Q8_NORM_ROW_VEC];
 #pragma unroll
@@ -1969,7 +1975,32 @@ extern "C" __global__ __launch_bounds__(256) void q8_rmsnorm_row(Q8NormArgs a) {
         const int i = tid + 256 * j;
         const int ic = min(i, nv - 1);  // clamped in-bounds address; the value is unused past nv
         xv[j] = xr[ic];
-        wv[j] = wr[ic];
+        if (a.out) wv[j] = wr[ic];
+    }
+    // Prepared output: thread tid takes half tid % 2 of blocks tid / 2 + 128 g
+    // (the wave-per-row kernel's element layout per half-block), its x and w
+    // loaded with the rest, before the reduction.
+    const int nb = k / 32;
+    const int h = tid & 1;
+    float qx[2][4][4], qw[2][4][4];
+    if (a.xq) {
+#pragma unroll
+        for (int g = 0; g < 2; g++) {
+            const int b = min(128 * g + (tid >> 1), nb - 1);
+            const size_t base = (size_t)b * 32 + 2 * h;
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const size_t i0 = base + 8 * c, i1 = base + 8 * c + 4;
+                qx[g][c][0] = xrow[i0];
+                qx[g][c][1] = xrow[i0 + 1];
+                qx[g][c][2] = xrow[i1];
+                qx[g][c][3] = xrow[i1 + 1];
+                qw[g][c][0] = a.w[i0];
+                qw[g][c][1] = a.w[i0 + 1];
+                qw[g][c][2] = a.w[i1];
+                qw[g][c][3] = a.w[i1 + 1];
+            }
+        }
     }
     double ss = 0.0;
 #pragma unroll
@@ -1986,15 +2017,37 @@ extern "C" __global__ __launch_bounds__(256) void q8_rmsnorm_row(Q8NormArgs a) {
     const double total = (part[0] + part[1]) + (part[2] + part[3]);
     const float mean_square = (float)(total / (double)k);
     const float scale = 1.0f / sqrtf(mean_square + a.eps);
-    f32x4 *orow = (f32x4 *)(a.out + (size_t)blockIdx.x * k);
+    if (a.out && live) {
+        f32x4 *orow = (f32x4 *)(a.out + (size_t)t * k);
 #pragma unroll
-    for (int j = 0; j < Q8_NORM_ROW_VEC; j++) {
-        const int i = tid + 256 * j;
-        if (i < nv) {
-            f32x4 o;
+        for (int j = 0; j < Q8_NORM_ROW_VEC; j++) {
+            const int i = tid + 256 * j;
+            if (i < nv) {
+                f32x4 o;
 #pragma unroll
-            for (int e = 0; e < 4; e++) o[e] = (xv[j][e] * scale) * wv[j][e];
-            orow[i] = o;
+                for (int e = 0; e < 4; e++) o[e] = (xv[j][e] * scale) * wv[j][e];
+                orow[i] = o;
+            }
+        }
+    }
+    if (a.xq) {
+        const int tt = t >> 5;
+#pragma unroll
+        for (int g = 0; g < 2; g++) {
+            if (128 * g >= nb) break;  // workgroup-uniform
+            const int b = min(128 * g + (tid >> 1), nb - 1);  // clamped: every lane joins the shuffle
+            float e[4][4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                e[0][c] = live ? (qx[g][c][0] * scale) * qw[g][c][0] : 0.0f;  // J[h][0] = 2h
+                e[2][c] = live ? (qx[g][c][1] * scale) * qw[g][c][1] : 0.0f;  // J[h][2] = 2h + 1
+                e[1][c] = live ? (qx[g][c][2] * scale) * qw[g][c][2] : 0.0f;  // J[h][1] = 4 + 2h
+                e[3][c] = live ? (qx[g][c][3] * scale) * qw[g][c][3] : 0.0f;  // J[h][3] = 5 + 2h
+            }
+            float peak = half_peak(e);
+            peak = fmaxf(peak, __shfl_xor(peak, 1));
+            if (128 * g + (tid >> 1) < nb)
+                quant_store(e, peak, a.xq, a.xs, (size_t)tt * nb + b, 32 * h + (t & 31), h == 0, a.f16);
         }
     }
 }
