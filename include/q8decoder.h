@@ -48,6 +48,16 @@ int q8_attention(q8_ctx *ctx, q8_dptr q, size_t q_offset, q8_dptr kcache, q8_dpt
                  size_t out_offset, int n, int n_head, int n_kv, int head_dim, int capacity, float scale,
                  q8_dptr position, int splits);
 
+/* q8_attention for a prompt (n >= 2) with its output written straight as
+ * prepared Q8_0 activations (as q8_prepare of the f32 rows would leave them,
+ * bit for bit, in the context's activation workspace: valid until the next
+ * preparation), for the output projection's GEMM.  Each attention workgroup
+ * owns whole Q8_0 blocks (a head's 64 dims are two), so it quantizes its own
+ * rows; the f32 rows are not written.  The reference runs attend, then
+ * prepare (model.rs dense_attention). */
+int q8_attention_prepare(q8_ctx *ctx, q8_dptr q, size_t q_offset, q8_dptr kcache, q8_dptr vcache, int n, int n_head,
+                         int n_kv, int head_dim, int capacity, float scale, q8_dptr position, q8_prepared *out);
+
 /* q8_attention for one token (n = 1) followed by q8_matmul of its output
  * through `wo` with y as the residual (y[0 .. wo->out) += wo . attn):
  * the reference's attend then matmul_add of the output projection (model.rs

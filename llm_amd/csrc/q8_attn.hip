@@ -506,26 +506,58 @@ extern "C" __global__ __launch_bounds__(128) void q8_attn_prefill(Q8AttnPrefillA
             for (int v = 0; v < 16; v++) xo[32 * dt + 8 * (v >> 2) + 4 * h + (v & 3)][r] = o[dt][v];
     }
     __syncthreads();
-    if (wave == 1 || !qlive) return;
+    if (wave == 1) return;
     const float m1 = xm[r], l1 = xl[r];
     const float mt = fmaxf(m, m1);  // finite: key 0 is in tile 0 (wave 0) and visible to every query
     const float c0 = expf(m - mt);
     const float c1 = (m1 == -INFINITY) ? 0.0f : expf(m1 - mt);
     const float lt = l * c0 + l1 * c1;
-    float *orow = a.out + ((size_t)qrow * a.n_head + head) * HD;
+    // res[dt][4g + e]: dim 32 dt + 8 g + 4 h + e of this lane's query (0 for
+    // the padding queries of the last tile)
+    float res[2][16];
 #pragma unroll
     for (int dt = 0; dt < 2; dt++)
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-            f32x4 res;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int v = 4 * g + e;
-                const int d = 32 * dt + 8 * g + 4 * h + e;
-                res[e] = (o[dt][v] * c0 + xo[d][r] * c1) / lt;
-            }
-            *(f32x4 *)(orow + 32 * dt + 8 * g + 4 * h) = res;
+        for (int v = 0; v < 16; v++) {
+            const int d = 32 * dt + 8 * (v >> 2) + 4 * h + (v & 3);
+            res[dt][v] = qlive ? (o[dt][v] * c0 + xo[d][r] * c1) / lt : 0.0f;
         }
+    if (a.out && qlive) {
+        float *orow = a.out + ((size_t)qrow * a.n_head + head) * HD;
+#pragma unroll
+        for (int dt = 0; dt < 2; dt++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+                *(f32x4 *)(orow + 32 * dt + 8 * g + 4 * h) =
+                    (f32x4){res[dt][4 * g], res[dt][4 * g + 1], res[dt][4 * g + 2], res[dt][4 * g + 3]};
+    }
+    if (a.xq) {
+        // The head's 64 dims are Q8_0 blocks 2 head and 2 head + 1 of the
+        // query's row, so this workgroup owns whole prepared units (32
+        // queries x one block).  Unit half hh holds elements 8c + J[hh][q]
+        // (J = {0,4,1,5}, {2,6,3,7}); this lane holds 8c + 4h + {0..3}, so
+        // the pair (r, r + 32) trades two values per chunk, then quantizes
+        // as q8_quantize does (quant_store, the block peak across the pair).
+        const int nb = 2 * a.n_head;
+#pragma unroll
+        for (int dt = 0; dt < 2; dt++) {
+            float e[4][4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const float v0 = res[dt][4 * c], v1 = res[dt][4 * c + 1];
+                const float v2 = res[dt][4 * c + 2], v3 = res[dt][4 * c + 3];
+                const float p0 = __shfl_xor(v0, 32), p1 = __shfl_xor(v1, 32);
+                const float p2 = __shfl_xor(v2, 32), p3 = __shfl_xor(v3, 32);
+                e[0][c] = h == 0 ? v0 : p2;  // 8c + 0 | 8c + 2
+                e[1][c] = h == 0 ? p0 : v2;  // 8c + 4 | 8c + 6
+                e[2][c] = h == 0 ? v1 : p3;  // 8c + 1 | 8c + 3
+                e[3][c] = h == 0 ? p1 : v3;  // 8c + 5 | 8c + 7
+            }
+            float peak = half_peak(e);
+            peak = fmaxf(peak, __shfl_xor(peak, 32));
+            quant_store(e, peak, a.xq, a.xs, (size_t)qt * nb + 2 * head + dt, 32 * h + r, h == 0, a.f16);
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------

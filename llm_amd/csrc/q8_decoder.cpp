@@ -72,7 +72,7 @@ struct q8_decoder {
     std::vector<Layer> layers;
     const q8_weight *embd = nullptr;
     std::vector<float> output_norm;
-    q8_dptr x = 0, normed = 0, q = 0, attn = 0, act = 0, logits = 0;
+    q8_dptr x = 0, normed = 0, q = 0, act = 0, logits = 0;
     q8_dptr pos = 0, tokens = 0;
     int position = 0;  // host mirror of *pos
     std::map<std::pair<int, int>, void *> graphs;
@@ -148,10 +148,11 @@ int q8_decoder::body(int n, int splits) {
         if (n == 1) {  // attention, its split combine folded into the output projection
             DEC_TRY(q8_attention_matmul_add(c, q, 0, L.kcache, L.vcache, g.n_head, g.n_head_kv, g.head_dim,
                                             g.capacity, scale, pos, splits, L.w[Q8_DEC_O], x, 0));
-        } else {
-            DEC_TRY(q8_attention(c, q, 0, L.kcache, L.vcache, attn, 0, n, g.n_head, g.n_head_kv, g.head_dim,
-                                 g.capacity, scale, pos, splits));
-            DEC_TRY(q8_matmul(c, L.w[Q8_DEC_O], attn, 0, n, x, 0, nullptr, x, 0));
+        } else {  // attention written as the output projection's prepared activations
+            q8_prepared pa{};
+            DEC_TRY(q8_attention_prepare(c, q, 0, L.kcache, L.vcache, n, g.n_head, g.n_head_kv, g.head_dim,
+                                         g.capacity, scale, pos, &pa));
+            DEC_TRY(q8_matmul(c, L.w[Q8_DEC_O], 0, 0, n, x, 0, &pa, x, 0));
         }
         // feed-forward block (feed_forward, model.rs:1162-1235)
         if (n == 1) {
@@ -236,7 +237,6 @@ int q8_decoder_create_synthetic(q8_ctx *c, const q8_decoder_config *config, uint
     const size_t f = sizeof(float);
     if ((rc = d->alloc((size_t)B * E * f, &d->x)) || (rc = d->alloc((size_t)B * E * f, &d->normed)) ||
         (rc = d->alloc((size_t)B * g.n_head * g.head_dim * f, &d->q)) ||
-        (rc = d->alloc((size_t)B * g.n_head * g.head_dim * f, &d->attn)) ||
         (rc = d->alloc((size_t)B * g.n_ff * f, &d->act)) || (rc = d->alloc((size_t)g.n_vocab * f, &d->logits)) ||
         (rc = d->alloc(256, &d->pos)) || (rc = d->alloc((size_t)B * 4, &d->tokens)))
         return fail(rc);

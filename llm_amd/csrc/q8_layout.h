@@ -272,10 +272,13 @@ typedef struct {
     const float *q;         /* [n][n_head][head_dim] rotated queries */
     const uint16_t *kcache;
     const uint16_t *vcache;
-    float *out;             /* [n][n_head][head_dim] */
+    float *out;             /* [n][n_head][head_dim], or null */
     const int *position;    /* device: cache position of query 0 */
     int n, n_head, n_kv, capacity, qtiles;
     float scale;
+    uint8_t *xq;            /* non-null: the output also as prepared Q8_0 (units, as q8_quantize writes them) */
+    float *xs;              /* its block scales */
+    int f16;                /* 1: f16 prepared units */
 } Q8AttnPrefillArgs;
 
 typedef struct {

@@ -1664,6 +1664,41 @@ int run_attn_decode(q8_ctx *c, const float *q, q8_dptr kcache, q8_dptr vcache, f
     return launch(c, sh.fn, (unsigned)parts, sh.threads, 0, &a, sizeof a);
 }
 
+// Prompt attention (n >= 2): f32 rows into `out` and/or prepared Q8_0 into
+// `p` (the context's activation workspace, as q8_prepare leaves it).
+int run_attn_prefill(q8_ctx *c, const float *q, q8_dptr kcache, q8_dptr vcache, float *out, q8_prepared *p, int n,
+                     int n_head, int n_kv, int capacity, float scale, q8_dptr position) {
+    Q8AttnPrefillArgs a{};
+    a.q = q;
+    a.kcache = reinterpret_cast<const uint16_t *>(kcache);
+    a.vcache = reinterpret_cast<const uint16_t *>(vcache);
+    a.out = out;
+    a.position = reinterpret_cast<const int *>(position);
+    a.n = n;
+    a.n_head = n_head;
+    a.n_kv = n_kv;
+    a.capacity = capacity;
+    a.qtiles = (int)ceil_div(n, 32);
+    a.scale = scale;
+    if (p) {
+        const int k = n_head * Q8_ATTN_HEAD_DIM;
+        const int nb = k / 32;
+        const int fmt = prepared_format(c, n);
+        const size_t qbytes = (size_t)a.qtiles * nb * (fmt == Q8_PREPARED_F16 ? Q8_UNIT_F16_BYTES : Q8_UNIT_BYTES);
+        const size_t sbytes = (size_t)a.qtiles * nb * Q8_TILE_TOKENS * sizeof(float);
+        Q8_TRY(grow(c, &c->act_ws, &c->act_ws_bytes, align_up(qbytes, kAlign) + sbytes, "hipMalloc(activation)"));
+        a.xq = static_cast<uint8_t *>(c->act_ws);
+        a.xs = reinterpret_cast<float *>(static_cast<uint8_t *>(c->act_ws) + align_up(qbytes, kAlign));
+        a.f16 = fmt == Q8_PREPARED_F16 ? 1 : 0;
+        p->quants = (q8_dptr)(uintptr_t)a.xq;
+        p->scales = (q8_dptr)(uintptr_t)a.xs;
+        p->n = n;
+        p->k = k;
+        p->format = fmt;
+    }
+    return launch(c, F_ATTN_PREFILL, (unsigned)(n_head * a.qtiles), 128, 0, &a, sizeof a);
+}
+
 int check_attention(q8_ctx *c, q8_dptr qp, q8_dptr kcache, q8_dptr vcache, q8_dptr position, int n, int n_head,
                     int n_kv, int head_dim, int capacity) {
     if (head_dim != Q8_ATTN_HEAD_DIM)
@@ -1693,19 +1728,20 @@ int q8_attention(q8_ctx *c, q8_dptr q, size_t q_offset, q8_dptr kcache, q8_dptr 
     if (n == 1)
         return run_attn_decode(c, reinterpret_cast<const float *>(qp), kcache, vcache, reinterpret_cast<float *>(op),
                                n_head, n_kv, capacity, scale, position, splits, 0);
-    Q8AttnPrefillArgs a{};
-    a.q = reinterpret_cast<const float *>(qp);
-    a.kcache = reinterpret_cast<const uint16_t *>(kcache);
-    a.vcache = reinterpret_cast<const uint16_t *>(vcache);
-    a.out = reinterpret_cast<float *>(op);
-    a.position = reinterpret_cast<const int *>(position);
-    a.n = n;
-    a.n_head = n_head;
-    a.n_kv = n_kv;
-    a.capacity = capacity;
-    a.qtiles = (int)ceil_div(n, 32);
-    a.scale = scale;
-    return launch(c, F_ATTN_PREFILL, (unsigned)(n_head * a.qtiles), 128, 0, &a, sizeof a);
+    return run_attn_prefill(c, reinterpret_cast<const float *>(qp), kcache, vcache, reinterpret_cast<float *>(op),
+                            nullptr, n, n_head, n_kv, capacity, scale, position);
+}
+
+int q8_attention_prepare(q8_ctx *c, q8_dptr q, size_t q_offset, q8_dptr kcache, q8_dptr vcache, int n, int n_head,
+                         int n_kv, int head_dim, int capacity, float scale, q8_dptr position, q8_prepared *out) {
+    if (!c || !out) return fail(Q8_ERR_INVALID, "q8_attention_prepare: bad arguments");
+    if (n < 2) return fail(Q8_ERR_INVALID, "q8_attention_prepare: %d tokens (the prompt kernel takes n >= 2)", n);
+    Q8_TRY(check_n(n));
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    const q8_dptr qp = (q8_dptr)(uintptr_t)fptr(q, q_offset);
+    Q8_TRY(check_attention(c, qp, kcache, vcache, position, n, n_head, n_kv, head_dim, capacity));
+    return run_attn_prefill(c, reinterpret_cast<const float *>(qp), kcache, vcache, nullptr, out, n, n_head, n_kv,
+                            capacity, scale, position);
 }
 
 int q8_attention_matmul_add(q8_ctx *c, q8_dptr q, size_t q_offset, q8_dptr kcache, q8_dptr vcache, int n_head,

@@ -55,7 +55,7 @@ EXPORTS = (
     "q8_gguf_tensor", "q8_gguf_meta_count", "q8_gguf_meta_key_at", "q8_gguf_meta_type", "q8_gguf_meta_u64",
     "q8_gguf_meta_f32", "q8_gguf_meta_bool", "q8_gguf_meta_str", "q8_gguf_has_key_prefix",
     "q8_gguf_meta_i32_array", "q8_gguf_meta_f32_array", "q8_gguf_meta_str_array", "q8_gguf_weight",
-    "q8_rope_append", "q8_attention", "q8_attention_matmul_add", "q8_prompt_qkv_rope", "q8_embeddings_device", "q8_argmax_device", "q8_advance_position",
+    "q8_rope_append", "q8_attention", "q8_attention_prepare", "q8_attention_matmul_add", "q8_prompt_qkv_rope", "q8_embeddings_device", "q8_argmax_device", "q8_advance_position",
     "q8_norm_matmul_decode_group", "q8_norm_gate_up_silu", 
     "q8_vector_release", "q8_norm_qkv_rope",
     "q8_weight_synthetic", "q8_decoder_create_synthetic", "q8_decoder_destroy", "q8_decoder_reset",
@@ -216,6 +216,8 @@ def lib():
                                  ctypes.c_float, u64, c_int]),
         "q8_attention_matmul_add": (c_int, [vp, u64, c_size, u64, u64, c_int, c_int, c_int, c_int, ctypes.c_float,
                                             u64, c_int, vp, u64, c_size]),
+        "q8_attention_prepare": (c_int, [vp, u64, c_size, u64, u64, c_int, c_int, c_int, c_int, c_int, ctypes.c_float,
+                                         u64, ctypes.POINTER(Prepared)]),
         "q8_prompt_qkv_rope": (c_int, [vp, vp, vp, vp, vp, c_int, u64, c_size, u64, u64, c_int, c_int, c_int, c_int,
                                        ctypes.c_float, c_int, u64]),
         "q8_embeddings_device": (c_int, [vp, vp, u64, c_size, u64, c_size]),
@@ -555,6 +557,15 @@ class Gpu:
         _check(lib().q8_attention_matmul_add(self.handle, q.ptr, q_offset, kcache.ptr, vcache.ptr, n_head, n_kv,
                                              head_dim, capacity, float(scale), position.ptr, splits,
                                              self.resident(wo), y.ptr, y_offset))
+
+    def attention_prepare(self, q: DeviceBuffer, kcache: DeviceBuffer, vcache: DeviceBuffer, n: int, n_head: int,
+                          n_kv: int, head_dim: int, capacity: int, scale: float, position: DeviceBuffer,
+                          q_offset: int = 0) -> Prepared:
+        """Prompt attention with its output as prepared Q8_0 activations."""
+        p = Prepared()
+        _check(lib().q8_attention_prepare(self.handle, q.ptr, q_offset, kcache.ptr, vcache.ptr, n, n_head, n_kv,
+                                          head_dim, capacity, float(scale), position.ptr, ctypes.byref(p)))
+        return p
 
     def prompt_qkv_rope(self, wq: Weight, wk: Weight, wv: Weight, prepared: Prepared, n: int, q: DeviceBuffer,
                         kcache: DeviceBuffer, vcache: DeviceBuffer, n_head: int, n_kv: int, head_dim: int, n_rot: int,

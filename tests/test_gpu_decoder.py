@@ -315,6 +315,47 @@ def test_attention_matmul_add_equals_attention_then_matmul(gpu, visible, splits,
         gpu.release(wo)
 
 
+@pytest.mark.parametrize("n,start,n_head,n_kv,f16", [(512, 0, 36, 36, -1), (70, 37, 4, 2, -1), (33, 0, 8, 8, 1),
+                                                     (2, 100, 4, 1, -1), (200, 5, 16, 4, 1)])
+def test_attention_prepare_equals_attention_then_prepare(gpu, n, start, n_head, n_kv, f16):
+    """q8_attention_prepare (each prompt-attention workgroup quantizing its
+    own heads' blocks) against q8_attention + q8_prepare of its f32 rows: the
+    prepared quants and scales bit-identical, padding tokens of the last tile
+    included, in the int8 and f16 unit formats."""
+    gpu.set_option("gemm.f16", f16)
+    r = np.random.default_rng(SEED + 3 * n + start)
+    capacity = start + n + 16
+    kf, vf, kc, vc = cache_pair(gpu, r, start + n, capacity, n_kv)
+    q = (r.standard_normal((n, n_head, 64)) * 2).astype(np.float32)
+    qb, out = gpu.alloc(q.nbytes), gpu.alloc(q.nbytes)
+    qb.upload(q)
+    pos = int_buffer(gpu, start)
+    try:
+        print(f"\nattention_prepare n={n} start={start} heads={n_head}/{n_kv} f16={f16}", flush=True)
+        gpu.attention(qb, kc, vc, out, n, n_head, n_kv, 64, capacity, 0.125, pos)
+        ref = gpu.prepare(out, 0, n, n_head * 64)
+        unit = 2048 if ref.format == q8.PREPARED_F16 else 1024
+        nb, tt = n_head * 2, (n + 31) // 32
+
+        def raw(ptr, nbytes):
+            host = np.empty(nbytes, np.uint8)
+            q8._check(q8.lib().q8_download(gpu.handle, host.ctypes.data, ptr, nbytes))
+            return host
+        want_q, want_s = raw(ref.quants, tt * nb * unit), raw(ref.scales, 4 * tt * nb * 32)
+        # the same workspace receives both: fill it with other activations first
+        out.upload((r.standard_normal(q.size) * 5).astype(np.float32))
+        other = gpu.prepare(out, 0, n, n_head * 64)
+        assert not np.array_equal(raw(other.scales, 4 * tt * nb * 32), want_s)
+        got = gpu.attention_prepare(qb, kc, vc, n, n_head, n_kv, 64, capacity, 0.125, pos)
+        assert got.format == ref.format and got.n == n and got.k == n_head * 64
+        assert np.array_equal(raw(got.quants, tt * nb * unit), want_q), "prepared quants differ"
+        assert np.array_equal(raw(got.scales, 4 * tt * nb * 32), want_s), "prepared scales differ"
+    finally:
+        gpu.set_option("gemm.f16", -1)
+        for b in (qb, out, kc, vc, pos):
+            b.free()
+
+
 @pytest.mark.parametrize("n,start,n_head,n_kv", [(2, 0, 4, 2), (64, 0, 4, 4), (100, 0, 2, 1), (130, 37, 4, 2),
                                                  (512, 0, 36, 36)])
 def test_prefill_attention_matches_the_oracle(gpu, n, start, n_head, n_kv):
