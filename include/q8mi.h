@@ -109,6 +109,8 @@ typedef struct {
     int kwaves;          /* GEMM: waves splitting the blocks inside a workgroup */
     int rwaves;          /* f16 GEMM: row-tile waves per workgroup sharing staged activations */
     int pipe;            /* int8 GEMM: 1 = software-pipelined kernel (MFMAs one item ahead) */
+    int row_slice;       /* GEMV over one matrix: rows per workgroup (8, 16; 32 = one 32-row tile) */
+    int slice_loads;     /* GEMV row slices: 16-byte weight loads per lane (3 or 6) */
     const char *name;    /* tactic name, e.g. "matmul.gemv_f32" */
     const char *evidence;
 } q8_tactic;
@@ -136,6 +138,7 @@ int q8_device_info(q8_ctx *ctx, int *cu_count, size_t *total_bytes, size_t *free
 void *q8_stream(q8_ctx *ctx);
 /* Tuning/testing switches; value -1 restores the tactic table's choice.
  * Names: "gemv.exact", "gemv.waves", "gemv.pairs", "gemv.slices",
+ * "gemv.rows" (8, 16 or 32), "gemv.loads" (3 or 6),
  * "gemm.smode", "gemm.tpw", "gemm.twaves", "gemm.xcd_remap", "gemm.kwaves",
  * "gemm.slices", "gemm.rwaves", "gemm.pipe", "gemm.lds", "gemm.silu",
  * "gemm.f16" (0: int8 prepared activations and the int8-MFMA GEMM for every

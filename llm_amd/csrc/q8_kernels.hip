@@ -679,6 +679,137 @@ Q8_GEMV_KERNEL(9, 0, 512)
 Q8_GEMV_KERNEL(9, 1, 512)
 
 // ---------------------------------------------------------------------------
+// Row-slice GEMV (one matrix, n = 1, exact block order): a workgroup owns RS
+// rows of a 32-row tile and the whole K range, so an M-row matrix makes
+// 4 * M / RS workgroups instead of M / 32 (configs[0]: 720 instead of 180),
+// which spreads the weight stream over every CU in near-equal shares.
+//
+// Lane L of a wave takes block j = L / (2 RS) of a load, half h = (L / RS) & 1
+// and row r = L % RS of the slice: its 16 bytes sit at
+// unit + 16 * (32 h + RS s + r) (s = slice in the tile), so each half of each
+// block is one contiguous 16 RS-byte run.  A wave issues all NL of its loads
+// (NL * 64 / (2 RS) consecutive blocks) at once, then stages its range of x.
+// Each lane forms its half's partial exactly as the tile kernel does (the
+// reference's per-lane FMA chain, then the two pair sums), adds its partner
+// half's partial (lane L ^ RS; one add, so the order does not matter), scales
+// by d and parks the block value in LDS; after the barrier one lane per row
+// adds the row's block values left to right (chain_row).  The output is
+// therefore bit-identical to q8_gemv1_*_e1 and to dot_q8_0's AVX2 path
+// (quant.rs:54-78), with the optional residual added last.
+template <int RS, int NL>
+static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    constexpr int LPB = 2 * RS;               // lanes per block
+    constexpr int BPL = 64 / LPB;             // blocks per wave load
+    constexpr int SPT = Q8_TILE_ROWS / RS;    // slices per tile (power of two)
+    constexpr int BPW = NL * BPL;             // blocks per wave
+    static_assert(BPW * 8 <= 64 * Q8_GEMV_STAGE, "x range of a wave exceeds its staging registers");
+    const uint8_t *mq = a.m[0].quants;
+    const uint16_t *msc = a.m[0].scales;
+    float *my = a.m[0].y;
+    const float *mbias = a.m[0].bias;
+    const int mrows = a.m[0].rows;
+    const float *xg = a.x;
+    const int nb = a.nb;
+    asm volatile("" ::"s"(mq), "s"(msc), "s"(my), "s"(mbias), "s"(mrows), "s"(xg), "s"(nb));
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int j = lane / LPB;
+    const int h = (lane / RS) & 1;
+    const int r = lane % RS;
+    const int tile = blockIdx.x / SPT;
+    const int srow = (blockIdx.x % SPT) * RS + r;  // row within the tile
+    const int b_begin = wave * BPW;
+    const int b_end = min(nb, b_begin + BPW);
+    const int b_last = max(b_end - 1, 0);
+    const uint8_t *qbase = mq + (size_t)tile * nb * Q8_UNIT_BYTES + 16 * (32 * h + srow);
+    const uint16_t *sbase = msc + (size_t)tile * nb * Q8_TILE_ROWS + srow;
+    const int vrow = Q8_GEMV_VROW(nb);
+    float *xs = smem;             // nb * 32 floats, permuted
+    float *vbuf = smem + nb * 32; // [RS][vrow] block values
+    float *pad = vbuf + RS * vrow;
+
+    // this wave's x range as natural-order float4s (lanes past its end
+    // re-read the last one)
+    const int st_begin = 8 * b_begin;
+    const int st_end = 8 * b_end;
+    const int st_clamp = max(st_end - 1, 0);
+    f32x4 xv[Q8_GEMV_STAGE];
+#pragma unroll
+    for (int u = 0; u < Q8_GEMV_STAGE; u++) {
+        const float *xp = xg + 4 * min(st_begin + lane + 64 * u, st_clamp);
+        xv[u] = (f32x4){xp[0], xp[1], xp[2], xp[3]};
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // every weight and scale load of the wave, unconditional at clamped
+    // in-bounds blocks
+    i32x4 qv[NL];
+    unsigned dd[NL];
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+        const int b = min(b_begin + i * BPL + j, b_last);
+        qv[i] = *(const i32x4 *)(qbase + (size_t)b * Q8_UNIT_BYTES);
+        dd[i] = (unsigned)sbase[(size_t)b * Q8_TILE_ROWS];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // zero each row's tail up to a multiple of four blocks (chain_row reads
+    // whole float4s)
+    if (wave == 0 && lane < RS) {
+        for (int b = nb; b < ((nb + 3) & ~3); b++) vbuf[r * vrow + b] = 0.0f;
+    }
+    // stage x permuted (the tile kernel's order): float4 slot 8b + 4hh + t
+    // holds x[32b + 8c + J[hh][t]] in component c
+#pragma unroll
+    for (int u = 0; u < Q8_GEMV_STAGE; u++) {
+        if (64 * u < st_end - st_begin) {
+            const int i = st_begin + lane + 64 * u;
+            float *d = i < st_end ? xs + (i >> 3) * 32 + ((i & 7) >> 1) + 4 * (i & 1) : pad;
+            d[0] = xv[u].x;
+            d[8] = xv[u].y;
+            d[16] = xv[u].z;
+            d[24] = xv[u].w;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+        const int bu = b_begin + i * BPL + j;
+        const int b = min(bu, b_last);
+        const float p = half_partial(qv[i], (const f32x4 *)(xs + b * 32 + h * 16));
+        // partner half: lane L ^ RS, by a DPP rotate within the 16-lane row
+        // (RS = 8) or a row swap (RS = 16); the sum of one add is the same
+        // in either order
+        float s01;
+        if constexpr (RS == 8) {
+            s01 = p + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(p), 0x128, 0xf, 0xf, false));
+        } else {
+            const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(p), __float_as_uint(p), false, false);
+            s01 = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        }
+        const float v = f16_to_f32(dd[i]) * s01;
+        *((h == 0 && bu < b_end) ? vbuf + r * vrow + bu : pad) = v;
+    }
+    __syncthreads();
+    if (wave != 0 || lane >= RS) return;
+    const float acc = chain_row(vbuf + r * vrow, nb);
+    const int row = tile * Q8_TILE_ROWS + srow;
+    if (row < mrows) my[row] = mbias ? acc + mbias[row] : acc;
+}
+
+#define Q8_GEMV_RS_KERNEL(RS, NL)                                                                     \
+    extern "C" __global__ __launch_bounds__(1024) void q8_gemv_r##RS##_l##NL(Q8GemvArgs a) { \
+        gemv_rs_body<RS, NL>(a);                                                                      \
+    }
+Q8_GEMV_RS_KERNEL(8, 3)
+Q8_GEMV_RS_KERNEL(8, 6)
+Q8_GEMV_RS_KERNEL(16, 3)
+Q8_GEMV_RS_KERNEL(16, 6)
+
+// ---------------------------------------------------------------------------
 // Activation quantization (quant.rs:98-121), into the prepared tile layout.
 //
 // e[q][c] is half h of one token's block: element 8c + J[h][q].  half_peak is

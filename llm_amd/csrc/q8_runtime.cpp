@@ -71,6 +71,7 @@ enum Fn {
     F_GEMV_2_0, F_GEMV_2_1, F_GEMV_3_0, F_GEMV_3_1, F_GEMV_5_0, F_GEMV_5_1, F_GEMV_9_0, F_GEMV_9_1,
     F_GEMV1_2_0, F_GEMV1_2_1, F_GEMV1_3_0, F_GEMV1_3_1, F_GEMV1_5_0, F_GEMV1_5_1, F_GEMV1_9_0, F_GEMV1_9_1,
     F_GEMVC_2_0, F_GEMVC_2_1, F_GEMVC_3_0, F_GEMVC_3_1, F_GEMVC_5_0, F_GEMVC_5_1, F_GEMVC_9_0, F_GEMVC_9_1,
+    F_GEMV_R8_3, F_GEMV_R8_6, F_GEMV_R16_3, F_GEMV_R16_6,
     F_QUANTIZE,
     F_GEMM_S0_T1, F_GEMM_S1_T1, F_GEMM_S1_T2, F_GEMM_S1_T4,
     F_GEMM_H_T1_R4, F_GEMM_H_T2_R2, F_GEMM_H_T2_R4,
@@ -94,6 +95,7 @@ const char *const kFnNames[F_COUNT] = {
     "q8_gemv1_pb5_e0", "q8_gemv1_pb5_e1", "q8_gemv1_pb9_e0", "q8_gemv1_pb9_e1",
     "q8_gemvc_pb2_e0", "q8_gemvc_pb2_e1", "q8_gemvc_pb3_e0", "q8_gemvc_pb3_e1",
     "q8_gemvc_pb5_e0", "q8_gemvc_pb5_e1", "q8_gemvc_pb9_e0", "q8_gemvc_pb9_e1",
+    "q8_gemv_r8_l3", "q8_gemv_r8_l6", "q8_gemv_r16_l3", "q8_gemv_r16_l6",
     "q8_quantize",
     "q8_gemm_s0_t1", "q8_gemm_s1_t1", "q8_gemm_s1_t2", "q8_gemm_s1_t4",
     "q8_gemm_h_t1_r4", "q8_gemm_h_t2_r2", "q8_gemm_h_t2_r4",
@@ -276,6 +278,18 @@ q8_tactic plan(q8_ctx *c, int n, int out, int k, int slots = 1, int fmt = -1) {
         }
         const int pb = option(c, "gemv.pairs", -1);
         if (pb > 0) t.pairs_per_batch = pb;
+        // the tile kernel's own switches select the tile kernel
+        if (w > 0 || sl > 0 || pb > 0 || !t.exact || t.kslices != 1) {
+            t.row_slice = Q8_TILE_ROWS;
+            t.slice_loads = 0;
+        }
+        const int rows = option(c, "gemv.rows", -1);
+        if (rows > 0) t.row_slice = rows;
+        if (t.row_slice != Q8_TILE_ROWS) {
+            const int loads = option(c, "gemv.loads", -1);
+            if (loads > 0) t.slice_loads = loads;
+            if (t.slice_loads != 3 && t.slice_loads != 6) t.slice_loads = 6;
+        }
     } else {
         t.smode = option(c, "gemm.smode", t.smode) ? 1 : 0;
         t.xcd_remap = option(c, "gemm.xcd_remap", t.xcd_remap) ? 1 : 0;
@@ -350,6 +364,34 @@ struct Member {
     float *y;
 };
 
+// Row-slice GEMV over one matrix (q8_gemv_r{8,16}_l{3,6}): a workgroup per
+// rs rows of a 32-row tile and the whole K range, nl loads per lane, exact
+// block order.  Returns Q8_ERR_UNSUPPORTED (without recording an error) when
+// K needs more than 16 waves, so the caller keeps the tile kernel.
+int run_gemv_rs(q8_ctx *c, const q8_weight *w, float *y, q8_dptr x, const float *bias, int rs, int nl) {
+    const int nb = w->nb;
+    const int bpw = nl * (64 / (2 * rs));
+    const int waves = (int)ceil_div(nb, bpw);
+    if (waves > 16) return Q8_ERR_UNSUPPORTED;
+    Q8GemvArgs a{};
+    a.members = 1;
+    a.m[0].quants = w->quants;
+    a.m[0].scales = w->scales;
+    a.m[0].y = y;
+    a.m[0].bias = bias;
+    a.m[0].rows = w->out;
+    a.total_tiles = w->tiles;
+    a.x = reinterpret_cast<const float *>(x);
+    a.nb = nb;
+    a.waves_per_tile = waves;
+    a.kslices = 1;
+    const long long grid = (long long)w->tiles * (Q8_TILE_ROWS / rs);
+    if (grid > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "gemv: grid of %lld workgroups", grid);
+    const unsigned lds = (unsigned)((nb * 32 + rs * Q8_GEMV_VROW(nb) + Q8_GEMV_PAD_FLOATS) * 4);
+    const Fn f = rs == 8 ? (nl == 3 ? F_GEMV_R8_3 : F_GEMV_R8_6) : (nl == 3 ? F_GEMV_R16_3 : F_GEMV_R16_6);
+    return launch(c, f, (unsigned)grid, (unsigned)(waves * 64), lds, &a, sizeof a);
+}
+
 // n = 1 over up to four weights sharing x; silu = 1 fuses silu(m0)*m1 into y of m0.
 // The RoPE + KV append epilogue of a q, k, v decode group.
 struct GemvRope {
@@ -390,6 +432,11 @@ int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const floa
     }
     const int slots = silu ? 2 : 1;
     const q8_tactic t = plan(c, 1, silu ? m[0].w->out : rows_total, k, slots);
+    if (count == 1 && !silu && !norm_w && !rope && !comb && t.exact && t.kslices == 1 &&
+        (t.row_slice == 8 || t.row_slice == 16)) {
+        const int rc = run_gemv_rs(c, m[0].w, m[0].y, x, bias, t.row_slice, t.slice_loads);
+        if (rc != Q8_ERR_UNSUPPORTED) return rc;
+    }
     if (t.pairs_per_wave > 12)
         return fail(Q8_ERR_UNSUPPORTED, "gemv: %d block pairs per wave exceeds the staging bound of 12",
                     t.pairs_per_wave);
@@ -952,6 +999,7 @@ void *q8_stream(q8_ctx *c) { return c ? (void *)c->stream : nullptr; }
 int q8_set_option(q8_ctx *c, const char *name, int value) {
     if (!c || !name) return fail(Q8_ERR_INVALID, "q8_set_option: bad arguments");
     static const char *const known[] = {"gemv.exact", "gemv.waves",  "gemv.pairs",     "gemv.slices",
+                                        "gemv.rows",  "gemv.loads",
                                         "gemm.smode", "gemm.tpw",    "gemm.twaves",    "gemm.xcd_remap",
                                         "gemm.kwaves", "gemm.slices", "gemm.rwaves",    "gemm.f16",
                                         "gemm.pipe",  "gemm.lds",      "gemm.silu"};
@@ -960,6 +1008,10 @@ int q8_set_option(q8_ctx *c, const char *name, int value) {
     if (!ok) return fail(Q8_ERR_INVALID, "unknown option %s", name);
     if (std::strcmp(name, "gemv.pairs") == 0 && value > 0 && !valid_pb(value))
         return fail(Q8_ERR_INVALID, "gemv.pairs must be one of 2, 3, 5, 9");
+    if (std::strcmp(name, "gemv.rows") == 0 && value >= 0 && value != 0 && value != 8 && value != 16 && value != 32)
+        return fail(Q8_ERR_INVALID, "gemv.rows must be 8, 16 or 32 (32: the tile kernel)");
+    if (std::strcmp(name, "gemv.loads") == 0 && value > 0 && value != 3 && value != 6)
+        return fail(Q8_ERR_INVALID, "gemv.loads must be 3 or 6");
     std::lock_guard<std::recursive_mutex> lock(c->mu);
     c->options[name] = value;
     return Q8_OK;

@@ -76,6 +76,23 @@ void q8_gemv_shape(int out, int k, int cu_count, int slots, q8_tactic *t) {
     t->pairs_per_batch = pairs_per_batch(ppw);
     if (w * slots > 8 && t->pairs_per_batch == 9) t->pairs_per_batch = 5;
     t->exact = 1;
+    // A single matrix with fewer tiles than CUs runs as 16-row slices (two
+    // workgroups per tile, whole K each) with as many waves as fit 16 at three
+    // loads per lane, else six.  Measured MALL-cold on gfx950: O 2304 x 2304
+    // 4.98 -> 3.89 us, down 2304 x 5760 8.25 -> 6.18 us, configs[0]
+    // 5760 x 2304 5.50 -> 5.47 us; the lm_head (3840 tiles) keeps the tile
+    // kernel (51.5 us either way).
+    t->row_slice = Q8_TILE_ROWS;
+    t->slice_loads = 0;
+    if (slots == 1 && tiles < cus) {
+        if (ceil_div(nb, 3 * 2) <= 16) {
+            t->row_slice = 16;
+            t->slice_loads = 3;
+        } else if (ceil_div(nb, 6 * 2) <= 16) {
+            t->row_slice = 16;
+            t->slice_loads = 6;
+        }
+    }
 }
 
 // GEMM launch shape.  A wave owns TPW token tiles of one 32-row tile.  Two

@@ -112,6 +112,7 @@ class Tactic(ctypes.Structure):
                 ("smode", ctypes.c_int),
                 ("xcd_remap", ctypes.c_int), ("kslices", ctypes.c_int), ("kwaves", ctypes.c_int),
                 ("rwaves", ctypes.c_int), ("pipe", ctypes.c_int),
+                ("row_slice", ctypes.c_int), ("slice_loads", ctypes.c_int),
                 ("name", ctypes.c_char_p), ("evidence", ctypes.c_char_p)]
 
     def as_dict(self) -> dict:

@@ -83,6 +83,16 @@ def test_tactic_table_invariants():
     assert len(names) == len(set(names))
 
 
+@pytest.mark.parametrize("out,k,rows,loads", [(2304, 2304, 16, 3), (2304, 5760, 16, 6), (5760, 2304, 16, 3),
+                                              (122880, 2304, 32, 0), (64, 12288, 32, 0)])
+def test_plan_row_slices_follow_the_measured_rule(out, k, rows, loads):
+    """Single-matrix GEMVs with fewer 32-row tiles than CUs run as 16-row
+    slices (three loads per lane when K fits 16 waves, else six); the
+    lm_head and K beyond 16 waves keep the tile kernel."""
+    t = llm_amd.plan(1, out, k)
+    assert (t["row_slice"], t["slice_loads"]) == (rows, loads)
+
+
 @pytest.mark.parametrize("n,out,k", [(1, 5760, 2304), (1, 122880, 2304), (1, 2304, 5760), (1, 4, 32),
                                      (1, 33, 96), (1, 100, 11520), (1, 8000, 16384), (2, 64, 64),
                                      (8, 5760, 2304), (64, 5760, 2304), (512, 11520, 2304), (512, 2304, 5760),
@@ -102,6 +112,13 @@ def test_plan_never_selects_a_rejected_tactic(n, out, k):
         pps = -(-npairs // s)
         assert 1 <= s <= npairs and (s - 1) * pps < npairs  # no empty slice
         assert t["waves_per_tile"] * t["pairs_per_wave"] >= pps
+        # row slices: a workgroup per 8 or 16 rows, at most 16 waves over K
+        assert t["row_slice"] in (8, 16, 32)
+        if t["row_slice"] != 32:
+            assert t["slice_loads"] in (3, 6)
+            blocks_per_wave = t["slice_loads"] * 64 // (2 * t["row_slice"])
+            assert -(-nb // blocks_per_wave) <= 16
+            assert -(-out // 32) < 256  # only where the tile kernel leaves CUs idle
     elif t["kernel"] == q8.KERNEL_GEMM_F16:
         # f16-MFMA family: built variants t1_r4, t2_r2, t2_r4; <= 512 threads
         assert n >= 2

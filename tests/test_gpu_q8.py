@@ -22,7 +22,7 @@ TOL_ABS = 2e-6
 TOL_REL = 1e-5
 SEED = 0x5EED
 J = [[0, 4, 1, 5], [2, 6, 3, 7]]
-OPTIONS = ("gemv.exact", "gemv.waves", "gemv.pairs", "gemv.slices", "gemm.smode", "gemm.tpw", "gemm.twaves",
+OPTIONS = ("gemv.exact", "gemv.waves", "gemv.pairs", "gemv.slices", "gemv.rows", "gemv.loads", "gemm.smode", "gemm.tpw", "gemm.twaves",
            "gemm.xcd_remap", "gemm.kwaves", "gemm.slices", "gemm.rwaves", "gemm.f16", "gemm.pipe", "gemm.lds",
            "gemm.silu")
 
@@ -241,6 +241,59 @@ def test_gemv_launch_shapes_agree(gpu, slices, waves, pairs, exact):
     assert_close(got, ref, what)
     if exact and oracle.simd_path() == "avx2+fma":
         assert_bits(got, ref, what)
+    gpu.release(w)
+
+
+ROW_SLICES = [(8, 3), (8, 6), (16, 3), (16, 6)]
+
+
+@pytest.mark.parametrize("rows,loads", ROW_SLICES)
+@pytest.mark.parametrize("out,k", [(1, 32), (33, 96), (100, 1056), (257, 2304), (5760, 2304), (2304, 5760),
+                                   (96, 224), (40, 12288)])
+def test_gemv_row_slices_match_the_reference(gpu, rows, loads, out, k):
+    """The row-slice GEMV (a workgroup per 8 or 16 rows of a tile, whole K)
+    keeps the exact block order: bit-identical to dot_q8_0's AVX2 path.
+    K = 12288 needs more than 16 waves at 8 rows x 3 loads, where the
+    tile kernel takes over."""
+    gpu.set_option("gemv.rows", rows)
+    gpu.set_option("gemv.loads", loads)
+    r = rng(40 + out + k)
+    w = weight(r, out, k)
+    x = r.standard_normal(k, dtype=np.float32)
+    ref = oracle.matmul(w.data, k, out, x, 1).reshape(-1)
+    got = run_matmul(gpu, w, x, 1).reshape(-1)
+    what = f"gemv rows={rows} loads={loads} {out}x{k}"
+    assert_close(got, ref, what)
+    if oracle.simd_path() == "avx2+fma":
+        assert_bits(got, ref, what)
+    gpu.release(w)
+
+
+@pytest.mark.parametrize("rows,loads", ROW_SLICES)
+def test_gemv_row_slices_residual_subnormals_and_offsets(gpu, rows, loads):
+    """Residual epilogue (compute.rs:537-581), all-subnormal and zero scales,
+    and x at a 4-byte offset, through the row-slice kernels."""
+    gpu.set_option("gemv.rows", rows)
+    gpu.set_option("gemv.loads", loads)
+    r = rng(60 + rows + loads)
+    out, k = 200, 2304
+    scales = np.abs(r.standard_normal(out * k // 32)).astype(np.float32) * 1e-6
+    scales[::7] = 0.0
+    w = weight(r, out, k, scales=scales)
+    x = r.standard_normal(k, dtype=np.float32)
+    y0 = r.standard_normal(out, dtype=np.float32)
+    xb, yb = gpu.alloc(4 * (k + 1)), gpu.alloc(4 * out)
+    xb.upload(np.concatenate([np.full(1, np.nan, np.float32), x]))
+    yb.upload(y0)
+    gpu.matmul(w, xb, 1, 1, yb, 0, bias=yb)
+    got = yb.download(np.float32, out)
+    ref = y0 + oracle.matmul(w.data, k, out, x, 1).reshape(-1)
+    what = f"gemv rows={rows} loads={loads} residual"
+    assert_close(got, ref, what)
+    if oracle.simd_path() == "avx2+fma":
+        assert_bits(got, ref, what)
+    xb.free()
+    yb.free()
     gpu.release(w)
 
 
