@@ -242,6 +242,54 @@ static __device__ __forceinline__ float chain_row(const float *row, int count) {
     return acc;
 }
 
+// Folded attention combine (the q8_gemvc_* and q8_gemv_rc_* prologues):
+// thread v builds float4 v of x from the split partials of its head (16
+// float4s per head), q8_attn_decode's combine term for term: the head's max
+// over the splits, e_s = exp(max_s - max) (0 for an empty split), the
+// weighted values and weights by fused multiply-adds, s ascending, and one
+// division per element.  The caller guarantees head dim 64, at most
+// Q8_ATTN_COMBINE_MAX splits and a thread per float4 of x (threads with
+// v >= nb * 8 load clamped and store to the pad).
+struct CombineRegs {
+    f32x4 acc[Q8_ATTN_COMBINE_MAX];
+    f32x2 ms[Q8_ATTN_COMBINE_MAX];  // (max, sum)
+};
+
+static __device__ __forceinline__ void combine_load(const Q8GemvArgs &a, int nb, int ns, CombineRegs &c) {
+    const int v = min((int)threadIdx.x, nb * 8 - 1);
+    const int hs = (v >> 4) * ns;  // head * splits
+#pragma unroll
+    for (int s = 0; s < Q8_ATTN_COMBINE_MAX; s++) {
+        if (s < ns) {
+            c.ms[s] = *(const f32x2 *)(a.attn_ms + 2 * (hs + s));
+            c.acc[s] = *(const f32x4 *)(a.attn_acc + (size_t)(hs + s) * 64 + 4 * (v & 15));
+        }
+    }
+}
+
+static __device__ __forceinline__ void combine_store(int nb, int ns, const CombineRegs &c, float *xs, float *pad) {
+    float gmax = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < Q8_ATTN_COMBINE_MAX; s++) gmax = s < ns ? fmaxf(gmax, c.ms[s].x) : gmax;
+    float den = 0.0f;
+    f32x4 num = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < Q8_ATTN_COMBINE_MAX; s++) {
+        if (s < ns) {
+            const float f = expf(c.ms[s].x - gmax);
+            den = __builtin_fmaf(c.ms[s].y, f, den);
+#pragma unroll
+            for (int e = 0; e < 4; e++) num[e] = __builtin_fmaf(c.acc[s][e], f, num[e]);
+        }
+    }
+    const int v = threadIdx.x;
+    float *d = v < nb * 8 ? xs + (v >> 3) * 32 + ((v & 7) >> 1) + 4 * (v & 1) : pad;
+    d[0] = num.x / den;
+    d[8] = num.y / den;
+    d[16] = num.z / den;
+    d[24] = num.w / den;
+}
+
 // ONE: a launch over one matrix (members == 1, no SiLU pair), whose fields
 // are read at static offsets with no selection.  CMB: x built by the folded
 // attention combine (a separate build, so its registers burden no other
@@ -358,22 +406,11 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
     // read, and only by the waves that hold a float4 of x.
     constexpr bool comb = CMB != 0;
     f32x4 xv[Q8_GEMV_STAGE];
-    f32x4 cacc[Q8_ATTN_COMBINE_MAX];
-    f32x2 cms[Q8_ATTN_COMBINE_MAX];  // (max, sum)
+    CombineRegs creg;
     const int ns = comb ? a.attn_splits : 0;
     const bool comb_wave = comb && (int)(threadIdx.x & ~63u) < nb * 8;  // wave-uniform
     if constexpr (comb) {
-        const int v = min((int)threadIdx.x, nb * 8 - 1);
-        const int hs = (v >> 4) * ns;  // head * splits
-        if (comb_wave) {
-#pragma unroll
-            for (int s = 0; s < Q8_ATTN_COMBINE_MAX; s++) {
-                if (s < ns) {
-                    cms[s] = *(const f32x2 *)(a.attn_ms + 2 * (hs + s));
-                    cacc[s] = *(const f32x4 *)(a.attn_acc + (size_t)(hs + s) * 64 + 4 * (v & 15));
-                }
-            }
-        }
+        if (comb_wave) combine_load(a, nb, ns, creg);
     } else {
 #pragma unroll
         for (int u = 0; u < Q8_GEMV_STAGE; u++) {
@@ -460,32 +497,7 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
     float *pad = vbuf + ((EXACT && S == 1) ? nslots * 32 * vrow : nslots * W * 32);
 
     if constexpr (comb) {
-        // q8_attn_decode's combine, term for term: the head's max over the
-        // splits, e_s = exp(max_s - max) (0 for an empty split), then the
-        // weighted values and weights by fused multiply-adds, s ascending,
-        // and one division per element.
-        if (comb_wave) {
-            float gmax = -INFINITY;
-#pragma unroll
-            for (int s = 0; s < Q8_ATTN_COMBINE_MAX; s++) gmax = s < ns ? fmaxf(gmax, cms[s].x) : gmax;
-            float den = 0.0f;
-            f32x4 num = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int s = 0; s < Q8_ATTN_COMBINE_MAX; s++) {
-                if (s < ns) {
-                    const float f = expf(cms[s].x - gmax);
-                    den = __builtin_fmaf(cms[s].y, f, den);
-#pragma unroll
-                    for (int e = 0; e < 4; e++) num[e] = __builtin_fmaf(cacc[s][e], f, num[e]);
-                }
-            }
-            const int v = threadIdx.x;
-            float *d = v < nb * 8 ? xs + (v >> 3) * 32 + ((v & 7) >> 1) + 4 * (v & 1) : pad;
-            d[0] = num.x / den;
-            d[8] = num.y / den;
-            d[16] = num.z / den;
-            d[24] = num.w / den;
-        }
+        if (comb_wave) combine_store(nb, ns, creg, xs, pad);
         __syncthreads();
     }
 
@@ -696,7 +708,7 @@ Q8_GEMV_KERNEL(9, 1, 512)
 // adds the row's block values left to right (chain_row).  The output is
 // therefore bit-identical to q8_gemv1_*_e1 and to dot_q8_0's AVX2 path
 // (quant.rs:54-78), with the optional residual added last.
-template <int RS, int NL>
+template <int RS, int NL, int CMB = 0>
 static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
     extern __shared__ __attribute__((aligned(16))) float smem[];
     constexpr int LPB = 2 * RS;               // lanes per block
@@ -711,14 +723,23 @@ static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
     const int mrows = a.m[0].rows;
     const float *xg = a.x;
     const int nb = a.nb;
-    asm volatile("" ::"s"(mq), "s"(msc), "s"(my), "s"(mbias), "s"(mrows), "s"(xg), "s"(nb));
+    asm volatile("" ::"s"(mq), "s"(msc), "s"(my), "s"(mbias), "s"(mrows), "s"(xg), "s"(nb), "s"(a.xcd_order),
+                 "s"(a.total_tiles));
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int j = lane / LPB;
     const int h = (lane / RS) & 1;
     const int r = lane % RS;
-    const int tile = blockIdx.x / SPT;
-    const int srow = (blockIdx.x % SPT) * RS + r;  // row within the tile
+    // xcd_order: workgroup b runs on XCD b % 8 (round-robin dispatch), so
+    // slice s of tile t is workgroup 8 SPT (t / 8) + 8 s + t % 8 and a tile's
+    // slices share one L2 (the 64-byte scale runs of a tile's blocks are
+    // fetched once, not once per XCD).
+    const int bx = blockIdx.x;
+    const int xo = a.xcd_order;
+    const int tile = xo ? (bx / (8 * SPT)) * 8 + (bx & 7) : bx / SPT;
+    const int slice = xo ? (bx >> 3) % SPT : bx % SPT;
+    if (tile >= a.total_tiles) return;  // padding of the XCD order, whole workgroup
+    const int srow = slice * RS + r;  // row within the tile
     const int b_begin = wave * BPW;
     const int b_end = min(nb, b_begin + BPW);
     const int b_last = max(b_end - 1, 0);
@@ -734,11 +755,19 @@ static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
     const int st_begin = 8 * b_begin;
     const int st_end = 8 * b_end;
     const int st_clamp = max(st_end - 1, 0);
+    // CMB: x is built by the folded attention combine instead (the host
+    // guarantees a thread per float4 of x); every wave then reads it.
     f32x4 xv[Q8_GEMV_STAGE];
+    CombineRegs creg;
+    const int ns = CMB ? a.attn_splits : 0;
+    if constexpr (CMB) {
+        combine_load(a, nb, ns, creg);
+    } else {
 #pragma unroll
-    for (int u = 0; u < Q8_GEMV_STAGE; u++) {
-        const float *xp = xg + 4 * min(st_begin + lane + 64 * u, st_clamp);
-        xv[u] = (f32x4){xp[0], xp[1], xp[2], xp[3]};
+        for (int u = 0; u < Q8_GEMV_STAGE; u++) {
+            const float *xp = xg + 4 * min(st_begin + lane + 64 * u, st_clamp);
+            xv[u] = (f32x4){xp[0], xp[1], xp[2], xp[3]};
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
     // every weight and scale load of the wave, unconditional at clamped
@@ -758,11 +787,15 @@ static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
     if (wave == 0 && lane < RS) {
         for (int b = nb; b < ((nb + 3) & ~3); b++) vbuf[r * vrow + b] = 0.0f;
     }
+    if constexpr (CMB) {
+        combine_store(nb, ns, creg, xs, pad);
+        __syncthreads();
+    }
     // stage x permuted (the tile kernel's order): float4 slot 8b + 4hh + t
     // holds x[32b + 8c + J[hh][t]] in component c
 #pragma unroll
     for (int u = 0; u < Q8_GEMV_STAGE; u++) {
-        if (64 * u < st_end - st_begin) {
+        if (!CMB && 64 * u < st_end - st_begin) {
             const int i = st_begin + lane + 64 * u;
             float *d = i < st_end ? xs + (i >> 3) * 32 + ((i & 7) >> 1) + 4 * (i & 1) : pad;
             d[0] = xv[u].x;
@@ -800,9 +833,12 @@ static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
     if (row < mrows) my[row] = mbias ? acc + mbias[row] : acc;
 }
 
-#define Q8_GEMV_RS_KERNEL(RS, NL)                                                                     \
-    extern "C" __global__ __launch_bounds__(1024) void q8_gemv_r##RS##_l##NL(Q8GemvArgs a) { \
-        gemv_rs_body<RS, NL>(a);                                                                      \
+#define Q8_GEMV_RS_KERNEL(RS, NL)                                                                      \
+    extern "C" __global__ __launch_bounds__(1024) void q8_gemv_r##RS##_l##NL(Q8GemvArgs a) {  \
+        gemv_rs_body<RS, NL>(a);                                                                       \
+    }                                                                                                  \
+    extern "C" __global__ __launch_bounds__(1024) void q8_gemv_rc##RS##_l##NL(Q8GemvArgs a) { \
+        gemv_rs_body<RS, NL, 1>(a);                                                                    \
     }
 Q8_GEMV_RS_KERNEL(8, 3)
 Q8_GEMV_RS_KERNEL(8, 6)

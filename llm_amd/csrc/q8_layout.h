@@ -137,6 +137,10 @@ typedef struct {
     const float *attn_acc; /* [heads][splits][head_dim] */
     const float *attn_ms;  /* [heads][splits][2]: max, sum */
     int attn_splits;
+    /* Row-slice kernels: 1 = the slices of a tile are workgroups 8 apart
+     * (one XCD under round-robin dispatch; the grid is padded to whole
+     * groups of eight tiles), 0 = consecutive workgroups. */
+    int xcd_order;
 } Q8GemvArgs;
 
 /* float4s per thread of the 256-thread row RMSNorm (k <= 1024 * this). */

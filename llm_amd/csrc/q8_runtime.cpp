@@ -72,6 +72,7 @@ enum Fn {
     F_GEMV1_2_0, F_GEMV1_2_1, F_GEMV1_3_0, F_GEMV1_3_1, F_GEMV1_5_0, F_GEMV1_5_1, F_GEMV1_9_0, F_GEMV1_9_1,
     F_GEMVC_2_0, F_GEMVC_2_1, F_GEMVC_3_0, F_GEMVC_3_1, F_GEMVC_5_0, F_GEMVC_5_1, F_GEMVC_9_0, F_GEMVC_9_1,
     F_GEMV_R8_3, F_GEMV_R8_6, F_GEMV_R16_3, F_GEMV_R16_6,
+    F_GEMV_RC8_3, F_GEMV_RC8_6, F_GEMV_RC16_3, F_GEMV_RC16_6,
     F_QUANTIZE,
     F_GEMM_S0_T1, F_GEMM_S1_T1, F_GEMM_S1_T2, F_GEMM_S1_T4,
     F_GEMM_H_T1_R4, F_GEMM_H_T2_R2, F_GEMM_H_T2_R4,
@@ -96,6 +97,7 @@ const char *const kFnNames[F_COUNT] = {
     "q8_gemvc_pb2_e0", "q8_gemvc_pb2_e1", "q8_gemvc_pb3_e0", "q8_gemvc_pb3_e1",
     "q8_gemvc_pb5_e0", "q8_gemvc_pb5_e1", "q8_gemvc_pb9_e0", "q8_gemvc_pb9_e1",
     "q8_gemv_r8_l3", "q8_gemv_r8_l6", "q8_gemv_r16_l3", "q8_gemv_r16_l6",
+    "q8_gemv_rc8_l3", "q8_gemv_rc8_l6", "q8_gemv_rc16_l3", "q8_gemv_rc16_l6",
     "q8_quantize",
     "q8_gemm_s0_t1", "q8_gemm_s1_t1", "q8_gemm_s1_t2", "q8_gemm_s1_t4",
     "q8_gemm_h_t1_r4", "q8_gemm_h_t2_r2", "q8_gemm_h_t2_r4",
@@ -364,34 +366,6 @@ struct Member {
     float *y;
 };
 
-// Row-slice GEMV over one matrix (q8_gemv_r{8,16}_l{3,6}): a workgroup per
-// rs rows of a 32-row tile and the whole K range, nl loads per lane, exact
-// block order.  Returns Q8_ERR_UNSUPPORTED (without recording an error) when
-// K needs more than 16 waves, so the caller keeps the tile kernel.
-int run_gemv_rs(q8_ctx *c, const q8_weight *w, float *y, q8_dptr x, const float *bias, int rs, int nl) {
-    const int nb = w->nb;
-    const int bpw = nl * (64 / (2 * rs));
-    const int waves = (int)ceil_div(nb, bpw);
-    if (waves > 16) return Q8_ERR_UNSUPPORTED;
-    Q8GemvArgs a{};
-    a.members = 1;
-    a.m[0].quants = w->quants;
-    a.m[0].scales = w->scales;
-    a.m[0].y = y;
-    a.m[0].bias = bias;
-    a.m[0].rows = w->out;
-    a.total_tiles = w->tiles;
-    a.x = reinterpret_cast<const float *>(x);
-    a.nb = nb;
-    a.waves_per_tile = waves;
-    a.kslices = 1;
-    const long long grid = (long long)w->tiles * (Q8_TILE_ROWS / rs);
-    if (grid > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "gemv: grid of %lld workgroups", grid);
-    const unsigned lds = (unsigned)((nb * 32 + rs * Q8_GEMV_VROW(nb) + Q8_GEMV_PAD_FLOATS) * 4);
-    const Fn f = rs == 8 ? (nl == 3 ? F_GEMV_R8_3 : F_GEMV_R8_6) : (nl == 3 ? F_GEMV_R16_3 : F_GEMV_R16_6);
-    return launch(c, f, (unsigned)grid, (unsigned)(waves * 64), lds, &a, sizeof a);
-}
-
 // n = 1 over up to four weights sharing x; silu = 1 fuses silu(m0)*m1 into y of m0.
 // The RoPE + KV append epilogue of a q, k, v decode group.
 struct GemvRope {
@@ -406,6 +380,46 @@ struct GemvCombine {
     const float *acc, *ms;
     int splits;
 };
+
+// Row-slice GEMV over one matrix (q8_gemv_r{8,16}_l{3,6}; q8_gemv_rc* with
+// x built by the folded attention combine): a workgroup per rs rows of a
+// 32-row tile and the whole K range, nl loads per lane, exact block order.
+// Returns Q8_ERR_UNSUPPORTED (without recording an error) when K needs more
+// than 16 waves, or the combine more threads than that, so the caller keeps
+// the tile kernel.
+int run_gemv_rs(q8_ctx *c, const q8_weight *w, float *y, q8_dptr x, const float *bias, int rs, int nl,
+                const GemvCombine *comb) {
+    const int nb = w->nb;
+    const int bpw = nl * (64 / (2 * rs));
+    const int waves = (int)ceil_div(nb, bpw);
+    if (waves > 16) return Q8_ERR_UNSUPPORTED;
+    if (comb && (nb * 8 > waves * 64 || comb->splits < 1 || comb->splits > Q8_ATTN_COMBINE_MAX))
+        return Q8_ERR_UNSUPPORTED;
+    Q8GemvArgs a{};
+    a.members = 1;
+    a.m[0].quants = w->quants;
+    a.m[0].scales = w->scales;
+    a.m[0].y = y;
+    a.m[0].bias = bias;
+    a.m[0].rows = w->out;
+    a.total_tiles = w->tiles;
+    a.x = reinterpret_cast<const float *>(x);
+    a.nb = nb;
+    a.waves_per_tile = waves;
+    a.kslices = 1;
+    if (comb) {
+        a.attn_acc = comb->acc;
+        a.attn_ms = comb->ms;
+        a.attn_splits = comb->splits;
+    }
+    a.xcd_order = option(c, "gemv.xcd_order", 1) ? 1 : 0;
+    const long long grid = (a.xcd_order ? ceil_div(w->tiles, 8) * 8 : (long long)w->tiles) * (Q8_TILE_ROWS / rs);
+    if (grid > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "gemv: grid of %lld workgroups", grid);
+    const unsigned lds = (unsigned)((nb * 32 + rs * Q8_GEMV_VROW(nb) + Q8_GEMV_PAD_FLOATS) * 4);
+    const int fi = (rs == 8 ? 0 : 2) + (nl == 3 ? 0 : 1);
+    const Fn f = (Fn)((comb ? F_GEMV_RC8_3 : F_GEMV_R8_3) + fi);
+    return launch(c, f, (unsigned)grid, (unsigned)(waves * 64), lds, &a, sizeof a);
+}
 
 // norm_w (device f32[k]) folds rmsnorm(x) * norm_w into a multi-matrix
 // launch (the caller checks gemv_folds_norm first); rope turns on the RoPE
@@ -432,9 +446,9 @@ int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const floa
     }
     const int slots = silu ? 2 : 1;
     const q8_tactic t = plan(c, 1, silu ? m[0].w->out : rows_total, k, slots);
-    if (count == 1 && !silu && !norm_w && !rope && !comb && t.exact && t.kslices == 1 &&
+    if (count == 1 && !silu && !norm_w && !rope && t.exact && t.kslices == 1 &&
         (t.row_slice == 8 || t.row_slice == 16)) {
-        const int rc = run_gemv_rs(c, m[0].w, m[0].y, x, bias, t.row_slice, t.slice_loads);
+        const int rc = run_gemv_rs(c, m[0].w, m[0].y, x, bias, t.row_slice, t.slice_loads, comb);
         if (rc != Q8_ERR_UNSUPPORTED) return rc;
     }
     if (t.pairs_per_wave > 12)
@@ -999,7 +1013,7 @@ void *q8_stream(q8_ctx *c) { return c ? (void *)c->stream : nullptr; }
 int q8_set_option(q8_ctx *c, const char *name, int value) {
     if (!c || !name) return fail(Q8_ERR_INVALID, "q8_set_option: bad arguments");
     static const char *const known[] = {"gemv.exact", "gemv.waves",  "gemv.pairs",     "gemv.slices",
-                                        "gemv.rows",  "gemv.loads",
+                                        "gemv.rows",  "gemv.loads", "gemv.xcd_order",
                                         "gemm.smode", "gemm.tpw",    "gemm.twaves",    "gemm.xcd_remap",
                                         "gemm.kwaves", "gemm.slices", "gemm.rwaves",    "gemm.f16",
                                         "gemm.pipe",  "gemm.lds",      "gemm.silu"};

@@ -280,14 +280,16 @@ def test_decode_attention_matches_the_oracle(gpu, visible, splits, n_head, n_kv)
 @pytest.mark.parametrize("visible,splits,n_head,n_kv", [(1, 1, 4, 2), (200, 1, 36, 36), (600, 3, 36, 36),
                                                         (640, 8, 36, 36), (4096, 8, 4, 1), (3000, 5, 8, 2),
                                                         (2000, 12, 8, 8), (300, 2, 32, 8)])
-@pytest.mark.parametrize("exact", [1, 0])
-def test_attention_matmul_add_equals_attention_then_matmul(gpu, visible, splits, n_head, n_kv, exact):
+@pytest.mark.parametrize("exact,rows", [(1, -1), (1, 8), (1, 32), (0, -1)])
+def test_attention_matmul_add_equals_attention_then_matmul(gpu, visible, splits, n_head, n_kv, exact, rows):
     """q8_attention_matmul_add: the partials combined in the output
     projection's GEMV prologue (or, past eight splits, the two calls it makes
     instead) give y bit-identical to q8_attention with the same splits then
     q8_matmul with y as the residual; and the attention alone is within the
-    f32 bar of the oracle."""
+    f32 bar of the oracle.  rows: the row-slice kernels (-1: the tactic's
+    16-row slices, 8: 8-row slices) or the tile kernel (32)."""
     gpu.set_option("gemv.exact", exact)
+    gpu.set_option("gemv.rows", rows)
     r = np.random.default_rng(SEED + 7 * visible + splits)
     capacity = max(visible, 256)
     kf, vf, kc, vc = cache_pair(gpu, r, visible, capacity, n_kv)
@@ -301,7 +303,8 @@ def test_attention_matmul_add_equals_attention_then_matmul(gpu, visible, splits,
     yf.upload(y0)
     pos = int_buffer(gpu, visible - 1)
     try:
-        print(f"\nattention + O visible={visible} splits={splits} heads={n_head}/{n_kv} exact={exact}", flush=True)
+        print(f"\nattention + O visible={visible} splits={splits} heads={n_head}/{n_kv} exact={exact} rows={rows}",
+              flush=True)
         gpu.attention(qb, kc, vc, att, 1, n_head, n_kv, 64, capacity, 0.125, pos, splits)
         gpu.matmul(wo, att, 0, 1, yref, 0, bias=yref)
         gpu.attention_matmul_add(qb, kc, vc, n_head, n_kv, 64, capacity, 0.125, pos, splits, wo, yf)
@@ -310,6 +313,7 @@ def test_attention_matmul_add_equals_attention_then_matmul(gpu, visible, splits,
         assert_close(att.download(np.float32, q.size).reshape(q.shape), a_ref, "attention vs oracle")
     finally:
         gpu.set_option("gemv.exact", -1)
+        gpu.set_option("gemv.rows", -1)
         for b in (qb, att, yref, yf, kc, vc, pos):
             b.free()
         gpu.release(wo)

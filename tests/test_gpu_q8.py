@@ -22,7 +22,7 @@ TOL_ABS = 2e-6
 TOL_REL = 1e-5
 SEED = 0x5EED
 J = [[0, 4, 1, 5], [2, 6, 3, 7]]
-OPTIONS = ("gemv.exact", "gemv.waves", "gemv.pairs", "gemv.slices", "gemv.rows", "gemv.loads", "gemm.smode", "gemm.tpw", "gemm.twaves",
+OPTIONS = ("gemv.exact", "gemv.waves", "gemv.pairs", "gemv.slices", "gemv.rows", "gemv.loads", "gemv.xcd_order", "gemm.smode", "gemm.tpw", "gemm.twaves",
            "gemm.xcd_remap", "gemm.kwaves", "gemm.slices", "gemm.rwaves", "gemm.f16", "gemm.pipe", "gemm.lds",
            "gemm.silu")
 
@@ -269,14 +269,17 @@ def test_gemv_row_slices_match_the_reference(gpu, rows, loads, out, k):
     gpu.release(w)
 
 
+@pytest.mark.parametrize("order", [0, 1])
 @pytest.mark.parametrize("rows,loads", ROW_SLICES)
-def test_gemv_row_slices_residual_subnormals_and_offsets(gpu, rows, loads):
+@pytest.mark.parametrize("out", [1, 200, 520])
+def test_gemv_row_slices_residual_subnormals_and_offsets(gpu, rows, loads, out, order):
     """Residual epilogue (compute.rs:537-581), all-subnormal and zero scales,
     and x at a 4-byte offset, through the row-slice kernels."""
     gpu.set_option("gemv.rows", rows)
     gpu.set_option("gemv.loads", loads)
-    r = rng(60 + rows + loads)
-    out, k = 200, 2304
+    gpu.set_option("gemv.xcd_order", order)
+    r = rng(60 + rows + loads + out)
+    k = 2304
     scales = np.abs(r.standard_normal(out * k // 32)).astype(np.float32) * 1e-6
     scales[::7] = 0.0
     w = weight(r, out, k, scales=scales)
@@ -288,7 +291,7 @@ def test_gemv_row_slices_residual_subnormals_and_offsets(gpu, rows, loads):
     gpu.matmul(w, xb, 1, 1, yb, 0, bias=yb)
     got = yb.download(np.float32, out)
     ref = y0 + oracle.matmul(w.data, k, out, x, 1).reshape(-1)
-    what = f"gemv rows={rows} loads={loads} residual"
+    what = f"gemv rows={rows} loads={loads} out={out} xcd_order={order} residual"
     assert_close(got, ref, what)
     if oracle.simd_path() == "avx2+fma":
         assert_bits(got, ref, what)
