@@ -455,6 +455,10 @@ def main():
         extras["configs2_lm_head"] = head
     decoder = bench_decoder(gpu, rng) if "decoder" in sections else None
     cpu = cpu_baseline(args.cpu_seconds) if "cpu" in sections and args.cpu_seconds > 0 else None
+    # the kernel the tactic table runs for configs[0] (the one `value` times)
+    t = gpu.plan(1, m, k)
+    gemv_kernel = (f"q8_gemv_r{t['row_slice']}_l{t['slice_loads']}" if t["row_slice"] in (8, 16)
+                   else f"q8_gemv1_pb{t['pairs_per_batch']}_e{t['exact']}")
     gpu.close()
 
     value = gemv["gbs"]
@@ -478,7 +482,7 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(value / HBM_PEAK_GBS, 4) if value is not None else None,
                      "traffic": traffic_from_profile(),
-                     "kernel": "q8_gemv (configs[0])", "bytes_per_launch": gemv["bytes_per_step"],
+                     "kernel": gemv_kernel, "bytes_per_launch": gemv["bytes_per_step"],
                      "mall_hot_gbs": gemv.get("mall_hot")},
         "gemm_n512": {"value": round(gemm["tops"], 2) if gemm["tops"] is not None else None, "unit": "TOPS",
                       "peak": INT8_PEAK_TOPS,
