@@ -76,15 +76,20 @@ void q8_gemv_shape(int out, int k, int cu_count, int slots, q8_tactic *t) {
     t->pairs_per_batch = pairs_per_batch(ppw);
     if (w * slots > 8 && t->pairs_per_batch == 9) t->pairs_per_batch = 5;
     t->exact = 1;
-    // A single matrix with fewer tiles than CUs runs as 16-row slices (two
-    // workgroups per tile, whole K each) with as many waves as fit 16 at three
-    // loads per lane, else six.  Measured MALL-cold on gfx950: O 2304 x 2304
-    // 4.98 -> 3.89 us, down 2304 x 5760 8.25 -> 6.18 us, configs[0]
-    // 5760 x 2304 5.50 -> 5.47 us; the lm_head (3840 tiles) keeps the tile
-    // kernel (51.5 us either way).
+    // A single matrix with fewer tiles than CUs runs in row slices (whole K
+    // per workgroup): 8-row slices (four per tile, three loads per lane) when
+    // 16-row slices would already fill every CU, else 16-row slices with as
+    // many waves as fit 16 at three loads per lane, else six.  Measured
+    // MALL-cold on gfx950 (tile kernel -> slices): configs[0] 5760 x 2304
+    // 5.50 -> 5.36 us (16-row slices 5.50), O 2304 x 2304 4.98 -> 3.95 us
+    // (8-row 4.29), down 2304 x 5760 8.25 -> 6.2 us (8-row 6.84); the lm_head
+    // (3840 tiles) keeps the tile kernel (51.5 us either way).
     t->row_slice = Q8_TILE_ROWS;
     t->slice_loads = 0;
-    if (slots == 1 && tiles < cus) {
+    if (slots == 1 && tiles < cus && 2 * tiles >= cus && ceil_div(nb, 3 * 4) <= 16) {
+        t->row_slice = 8;
+        t->slice_loads = 3;
+    } else if (slots == 1 && tiles < cus) {
         if (ceil_div(nb, 3 * 2) <= 16) {
             t->row_slice = 16;
             t->slice_loads = 3;
