@@ -1,25 +1,47 @@
 """Benchmark of the Q8_0 matmul hot path on one MI355X (BASELINE.json metric:
 "Q8_0 n=1 GEMV HBM GB/s (%peak); n=512 GEMM int8 TOPS (%MFMA peak)").
 
-A step is one n = 1 Q8_0 GEMV of configs[0] (W 5760 x 2304, x f32[2304]),
-each step on the next of R weight copies whose total (> 600 MB) exceeds the
-256 MB Infinity Cache, so every step streams its weights from HBM.  Steps are
-captured into one HIP graph of exactly --steps launches and timed with HIP
-events on the library's own stream.  `value` is that GEMV's HBM throughput:
-algorithmic bytes (M*K/32*34 + 4K + 4M per step) / time per step.
+A step is one n = 1 Q8_0 GEMV of configs[0] (W 5760 x 2304, x f32[2304]).
+Every step reads the next of R weight copies (R x 14.1 MB > 600 MB, more
+than twice the 256 MB Infinity Cache), in one rotation that runs on across
+the warmup and every trial, so whatever --steps is, a copy is read again only
+after all the others: every step streams its weights from HBM.
 
-Also reported (own fixed repetition counts, graphs, events):
-  gemm_n512   configs[3]: the layer's projections at n = 512 (QKV 6912, O 2304,
-              gate|up 2x5760, down 2304x5760) with their activation
-              quantization, in int8 TOPS (2*M*N*K) vs the 5.0 POPS dense peak;
-  extras      configs[1] n = 8 / 64 (GB/s), configs[2] decode layer set and
-              the 122880 x 2304 lm_head GEMV + argmax (GB/s, us);
-  decoder     configs[4]: the 42-layer synthetic decoder (hidden 2304, FFN
-              5760, 36 heads x 64, vocab 122880, f16 KV cache of 4096) with
-              random-init Q8_0 weights generated on the device: a 512-token
-              prefill of random ids, then 128 greedy decode steps (tok/s);
-  cpu_baseline the oracle's C restatement of the reference rayon CPU path
-              (oracle/q8_oracle.c) on this host's cores, on a bounded sample.
+Protocol (the same for every rotating figure below):
+  * an eager pass over all copies, then one graph of --warmup steps;
+  * T >= 5 trials; each captures the next --steps launches of the rotation
+    into a graph and times exactly those steps with HIP events on the
+    library's stream, after an untimed "filler" graph (the next max(steps,
+    R) launches) that keeps the GPU busy while the timed graph is submitted,
+    so host submission never shows in the timed region;
+  * the figure is the median over the trials (all trials are reported).
+`value` is the GEMV's HBM throughput: algorithmic bytes (M*K/32*34 + 4K + 4M
+per step) / median time per step.
+
+Also reported, each on its own rotation:
+  ceilings      what one kernel of this size can do on this box: the best
+                plain streaming read of the configs[0] byte count (the
+                GEMV's achievable ceiling), an empty kernel's cost per graph
+                launch, the sustained int8 MFMA rate (v_mfma_i32_32x32x32_i8
+                only), VALU rate, and the GEMM's per-tile-block instruction
+                mix with operands in registers (its own ceiling);
+  gemm_n512     configs[3]: the layer's projections at n = 512 (QKV 6912,
+                O 2304 + residual, gate|up 2x5760 -> SiLU -> Q8_0, down
+                2304x5760 + residual) with the activation quantization, on
+                rotating copies of the layer (MALL-cold), int8 TOPS
+                (2*M*N*K) vs the 5.0 POPS dense peak; each piece alone too;
+  extras        configs[1] n = 8 / 64, configs[2] decode layer set (rotating
+                layer copies) and the 122880 x 2304 lm_head GEMV + argmax;
+  decoder       configs[4]: the 42-layer synthetic decoder (hidden 2304, FFN
+                5760, 36 heads x 64, vocab 122880, f16 KV cache of 4096),
+                random-init Q8_0 weights generated on the device, reported as
+                llama-bench does (apps/cli/src/bench.rs:83-229): pp512 and
+                tg128 tok/s, mean +- sample std over r = 5 repeats, with the
+                build's code object hash and the tactics its shapes run;
+  cpu_baseline  the oracle's C restatement of the reference rayon CPU path
+                (oracle/q8_oracle.c, AVX2 order) on this host's cores: the
+                configs[0] GEMV in GB/s and the configs[3] layer set in TOPS,
+                each on a bounded sample.
 
 Prints ONE JSON line.  N > 1 GPUs is not part of this build.
 """
@@ -29,6 +51,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 
@@ -40,7 +63,10 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
 MALL_BYTES = 256 << 20
+ROTATE_BYTES = 600e6
+TRIALS = 5
 METRIC = "Q8_0 n=1 GEMV HBM GB/s (%peak); n=512 GEMM int8 TOPS (%MFMA peak)"
+HID, FFN, VOCAB = 2304, 5760, 122880
 
 
 def log(msg: str):
@@ -57,143 +83,138 @@ def make_weight(rng, out, k):
     return q8.Weight(oracle.make_q8_weight(rng, out, k), k, out)
 
 
-def timed_graph(gpu, record, reps: int, warmup: int) -> float:
-    """Capture `record()` once into a graph, replay `warmup` times untimed,
-    then `reps` times between HIP events; returns ms per replay."""
-    record()  # eager run: grows workspaces outside the capture
+def copies_for(nbytes: float) -> int:
+    return max(2, math.ceil(ROTATE_BYTES / nbytes))
+
+
+def rotating_trials(gpu, launch, copies: int, steps: int, warmup: int, trials: int = TRIALS) -> list[float]:
+    """The protocol of the module docstring: `launch(i)` enqueues step i on
+    copy i (mod copies).  Returns ms per step of each trial."""
+    pos = 0
+
+    def graph_of(count):
+        nonlocal pos
+        gpu.graph_begin()
+        for _ in range(count):
+            launch(pos % copies)
+            pos += 1
+        return gpu.graph_end()
+
+    for i in range(copies):  # eager: workspaces grown, every copy touched once
+        launch(i)
     gpu.sync()
-    gpu.graph_begin()
-    record()
-    graph = gpu.graph_end()
-    try:
-        for _ in range(warmup):
-            gpu.graph_launch(graph)
+    if warmup:
+        g = graph_of(warmup)
+        gpu.graph_launch(g)
         gpu.sync()
-        e0, e1 = gpu.event(), gpu.event()
+        gpu.graph_destroy(g)
+    filler = max(steps, copies)
+    out = []
+    e0, e1 = gpu.event(), gpu.event()
+    for _ in range(trials):
+        gf = graph_of(filler)
+        gt = graph_of(steps)
+        gpu.graph_launch(gf)
         gpu.record(e0)
-        for _ in range(reps):
-            gpu.graph_launch(graph)
+        gpu.graph_launch(gt)
         gpu.record(e1)
         ms = gpu.elapsed_ms(e0, e1)
         gpu.sync()
-        gpu.destroy_event(e0)
-        gpu.destroy_event(e1)
-    finally:
-        gpu.graph_destroy(graph)
-    return ms / reps
+        gpu.graph_destroy(gf)
+        gpu.graph_destroy(gt)
+        out.append(ms / steps)
+    gpu.destroy_event(e0)
+    gpu.destroy_event(e1)
+    return out
 
 
-def bench_gemv_rotating(gpu, m, k, steps, warmup, rng, label):
-    """n = 1 GEMV over rotating weight copies (MALL-cold)."""
+def summary(ms_list, work, unit_scale):
+    """Median over trials and the per-trial figures (work / ms * unit_scale)."""
+    med = statistics.median(ms_list)
+    return {"median_us": round(med * 1e3, 3), "value": work / (med * 1e-3) * unit_scale,
+            "trials": [round(work / (m * 1e-3) * unit_scale, 1) for m in ms_list]}
+
+
+# ---------------------------------------------------------------------------
+# configs[0] GEMV (the headline) and its ceiling
+# ---------------------------------------------------------------------------
+
+def bench_gemv(gpu, m, k, steps, warmup, rng):
+    from llm_amd import q8
     base = make_weight(rng, m, k)
     per = gemv_bytes(m, k)
-    copies = max(2, math.ceil(600e6 / per))
-    from llm_amd import q8
+    copies = copies_for(per)
     weights = [base] + [q8.Weight(base.data.copy(), k, m) for _ in range(copies - 1)]
     for w in weights:
         gpu.resident(w)
-    x = rng.standard_normal(k, dtype=np.float32)
-    xb, yb = gpu.alloc(4 * k), gpu.alloc(4 * m)
-    xb.upload(x)
-
-    def record_n(count):
-        def rec():
-            for i in range(count):
-                gpu.matmul(weights[i % copies], xb, 0, 1, yb, 0)
-        return rec
-
-    # warmup graph, then one graph of exactly `steps` launches
-    if warmup:
-        timed_graph(gpu, record_n(min(warmup, 4 * copies)), 1, 0)
-    ms_total = timed_graph(gpu, record_n(steps), 1, 1)
-    ms = ms_total / steps
-    gbs = per / (ms * 1e-3) / 1e9
-    log(f"{label}: {ms * 1e3:.2f} us/step, {gbs:.0f} GB/s over {copies} copies ({copies * per / 1e6:.0f} MB)")
-    for w in weights:
-        gpu.release(w)
-    xb.free()
-    yb.free()
-    return {"us_per_step": ms * 1e3, "gbs": gbs, "bytes_per_step": per, "copies": copies,
-            "total_ms": ms_total}
-
-
-def bench_gemv_hot(gpu, m, k, rng, steps=2000):
-    """The same GEMV on one weight copy (14 MB, resident in the 256 MB
-    Infinity Cache after the first launch): the MALL-hot figure."""
-    w = make_weight(rng, m, k)
-    gpu.resident(w)
     xb, yb = gpu.alloc(4 * k), gpu.alloc(4 * m)
     xb.upload(rng.standard_normal(k, dtype=np.float32))
-
-    def rec():
-        for _ in range(steps):
-            gpu.matmul(w, xb, 0, 1, yb, 0)
-    ms = timed_graph(gpu, rec, 1, 1) / steps
-    gbs = gemv_bytes(m, k) / (ms * 1e-3) / 1e9
-    log(f"configs[0] GEMV MALL-hot: {ms * 1e3:.2f} us/step, {gbs:.0f} GB/s")
-    gpu.release(w)
-    xb.free()
-    yb.free()
-    return round(gbs, 1)
-
-
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "q8_gemv_configs0_traffic.md")
-
-
-def traffic_from_profile():
-    """HBM bytes per configs[0] GEMV launch from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE summary, if it was measured on the code object
-    loaded now (its sha256 is recorded in the summary); otherwise None."""
-    from llm_amd import q8
-    try:
-        text = open(TRAFFIC_PROFILE).read()
-    except OSError:
-        return None
-    fields = {}
-    for line in text.splitlines():
-        if line.startswith("- ") and ": " in line:
-            key, val = line[2:].split(": ", 1)
-            fields[key.strip("` ")] = val.strip("` ")
-    if fields.get("code_object_sha256") != json.loads(q8.build_info())["code_object_sha256"]:
-        return None
-    try:
-        return int(fields["traffic_bytes_per_launch"])
-    except (KeyError, ValueError):
-        return None
-
-
-def bench_gemm_rotating(gpu, m, k, n, reps, rng, label):
-    """n tokens over rotating weight copies, quantization included."""
-    import oracle
-    from llm_amd import q8
-    base = make_weight(rng, m, k)
-    per = m * k // 32 * 34 + n * k * 4 + 4 * n * m
-    copies = max(2, math.ceil(600e6 / (m * k // 32 * 34)))
-    weights = [base] + [q8.Weight(base.data.copy(), k, m) for _ in range(copies - 1)]
-    for w in weights:
-        gpu.resident(w)
-    x = oracle.make_activations(rng, n, k, outlier_rate=0.01)
-    xb, yb = gpu.alloc(4 * n * k), gpu.alloc(4 * n * m)
-    xb.upload(x)
-
-    def rec():
-        for w in weights:
-            gpu.matmul(w, xb, 0, n, yb, 0)
-
-    ms = timed_graph(gpu, rec, reps, 2) / copies
-    gbs = per / (ms * 1e-3) / 1e9
-    tops = 2 * m * n * k / (ms * 1e-3) / 1e12
-    log(f"{label}: {ms * 1e3:.2f} us/matmul, {gbs:.0f} GB/s, {tops:.1f} TOPS")
+    ms = rotating_trials(gpu, lambda i: gpu.matmul(weights[i], xb, 0, 1, yb, 0), copies, steps, warmup)
+    s = summary(ms, per, 1e-9)
+    log(f"configs[0] GEMV: {s['median_us']:.2f} us/step, {s['value']:.0f} GB/s (median of {len(ms)} trials of "
+        f"{steps} steps; trials {s['trials']}) over {copies} copies ({copies * per / 1e6:.0f} MB)")
+    # MALL-hot: one copy, re-read every step
+    hot = rotating_trials(gpu, lambda i: gpu.matmul(base, xb, 0, 1, yb, 0), 1, max(steps, 50), warmup)
+    hs = summary(hot, per, 1e-9)
+    log(f"configs[0] GEMV MALL-hot: {hs['median_us']:.2f} us/step, {hs['value']:.0f} GB/s")
     for w in weights:
         gpu.release(w)
     xb.free()
     yb.free()
-    return {"us": ms * 1e3, "gbs": gbs, "tops": tops, "bytes": per}
+    return {"us_per_step": s["median_us"], "gbs": s["value"], "trials_gbs": s["trials"], "bytes_per_step": per,
+            "copies": copies, "mall_hot_gbs": round(hs["value"], 1), "mall_hot_us": hs["median_us"]}
 
+
+def bench_ceilings(gpu, steps, warmup, read_bytes):
+    """The plain-read ceiling at the GEMV's byte count, an empty kernel, and
+    the MFMA / VALU / tile-block-mix rates."""
+    from llm_amd import q8
+    nbytes = (read_bytes + 15) // 16 * 16
+    copies = copies_for(nbytes)
+    stride = (nbytes + 4095) // 4096 * 4096
+    buf = gpu.alloc(stride * copies)
+    reads = {}
+    for which, name in ((q8.PROBE_READ_L4, "l4"), (q8.PROBE_READ_L8, "l8"), (q8.PROBE_READ_L16, "l16")):
+        ms = rotating_trials(gpu, lambda i, w=which: gpu.probe(w, buf, nbytes, src_offset=i * stride), copies, steps,
+                             warmup)
+        reads[name] = summary(ms, read_bytes, 1e-9)
+    best = max(reads, key=lambda n: reads[n]["value"])
+    log("plain read of " + f"{read_bytes} B, MALL-cold: " +
+        ", ".join(f"{n} {r['median_us']:.2f} us ({r['value']:.0f} GB/s)" for n, r in reads.items()))
+    buf.free()
+    empty = rotating_trials(gpu, lambda i: gpu.probe(q8.PROBE_EMPTY), 1, 200, 20)
+    empty_us = statistics.median(empty) * 1e3
+    cus = gpu.info()["cu_count"]
+    wgs = 4 * cus  # four 4-wave workgroups a CU: four waves a SIMD
+    rates = {}
+    for which, name, per_iter in ((q8.PROBE_MFMA, "mfma", 4), (q8.PROBE_VALU, "valu", 1), (q8.PROBE_MIX, "mix", 2)):
+        iters = 2048 if which != q8.PROBE_VALU else 8192
+        ms = rotating_trials(gpu, lambda i, w=which, it=iters: gpu.probe(w, iters=it, workgroups=wgs), 1, 3, 1)
+        t = statistics.median(ms) * 1e-3
+        units = wgs * 4 * iters * per_iter  # per wave: MFMAs (mfma), 32-VALU groups (valu), tile-blocks (mix)
+        rates[name] = {"units_per_s": units / t, "seconds": t}
+    mfma_tops = rates["mfma"]["units_per_s"] * 65536 / 1e12
+    simds = 4 * cus
+    valu_ns = simds / (rates["valu"]["units_per_s"] * 32) * 1e9  # ns per wave64 VALU op per SIMD
+    mix_ns = simds / rates["mix"]["units_per_s"] * 1e9            # ns per tile-block per SIMD
+    mix_tops = rates["mix"]["units_per_s"] * 65536 / 1e12
+    log(f"empty kernel {empty_us:.2f} us/launch; int8 MFMA only {mfma_tops:.0f} TOPS; VALU {valu_ns:.2f} ns/op/SIMD; "
+        f"GEMM tile-block mix {mix_ns:.1f} ns/SIMD = {mix_tops:.0f} TOPS")
+    return {"read_bytes": read_bytes, "read_copies": copies,
+            "read_gbs": {n: round(r["value"], 1) for n, r in reads.items()},
+            "read_us": {n: r["median_us"] for n, r in reads.items()},
+            "ceiling_gbs": round(reads[best]["value"], 1), "ceiling_kernel": f"q8_probe_read_{best}",
+            "empty_kernel_us_per_launch": round(empty_us, 3),
+            "mfma_i8_tops": round(mfma_tops, 1), "valu_ns_per_op_per_simd": round(valu_ns, 3),
+            "tile_block_mix_ns_per_simd": round(mix_ns, 2), "tile_block_mix_tops": round(mix_tops, 1)}
+
+
+# ---------------------------------------------------------------------------
+# configs[3]: n = 512 layer projections
+# ---------------------------------------------------------------------------
 
 def own_prepared(gpu, prep, n, k):
-    """Copy a prepared operand (quants in either format, then f32 scales) into
-    a buffer we own; returns (Prepared, buffer)."""
+    """Copy a prepared operand (quants, then f32 scales) into a buffer we own."""
     from llm_amd import q8
     qbytes, sbytes = prep.quant_bytes(), prep.scale_bytes()
     buf = gpu.alloc(qbytes + sbytes)
@@ -202,133 +223,176 @@ def own_prepared(gpu, prep, n, k):
     return q8.Prepared(buf.ptr, buf.ptr + qbytes, n, k, prep.format), buf
 
 
-def bench_layer_n512(gpu, reps, rng, n=512):
-    """the four projections at n tokens on the int8 MFMA path."""
+def bench_layer_n512(gpu, steps, warmup, rng, n=512):
+    """configs[3] on rotating copies of the layer's seven weights."""
     import oracle
     from llm_amd import q8
-    hid, ffn = 2304, 5760
-    wq, wk, wv = (make_weight(rng, hid, hid) for _ in range(3))
-    wo = make_weight(rng, hid, hid)
-    wg, wu = make_weight(rng, ffn, hid), make_weight(rng, ffn, hid)
-    wd = make_weight(rng, hid, ffn)
-    for w in (wq, wk, wv, wo, wg, wu, wd):
-        gpu.resident(w)
-    x = oracle.make_activations(rng, n, hid)
-    xb = gpu.alloc(4 * n * hid)
+    names = ("q", "k", "v", "o", "gate", "up", "down")
+    shapes = {"q": (HID, HID), "k": (HID, HID), "v": (HID, HID), "o": (HID, HID), "gate": (FFN, HID),
+              "up": (FFN, HID), "down": (HID, FFN)}
+    base = {nm: make_weight(rng, *shapes[nm]) for nm in names}
+    layer_bytes = sum(w.data.size for w in base.values())
+    copies = copies_for(layer_bytes)
+    layers = [base] + [{nm: q8.Weight(base[nm].data.copy(), base[nm].k, base[nm].out) for nm in names}
+                       for _ in range(copies - 1)]
+    for L in layers:
+        for w in L.values():
+            gpu.resident(w)
+    x = oracle.make_activations(rng, n, HID)
+    xb, hb = gpu.alloc(4 * n * HID), gpu.alloc(4 * n * HID)
     xb.upload(x)
-    qkv = gpu.alloc(4 * n * 3 * hid)
-    hb = gpu.alloc(4 * n * hid)
     hb.upload(x)
-    act = gpu.alloc(4 * n * ffn)
-    ops = {
-        "qkv": 2 * n * 3 * hid * hid,
-        "o": 2 * n * hid * hid,
-        "gate_up": 2 * n * 2 * ffn * hid,
-        "down": 2 * n * hid * ffn,
-    }
-
-    def rec():
-        p = gpu.prepare(xb, 0, n, hid)
-        gpu.matmul_prompt_group([(wq, qkv, 0), (wk, qkv, n * hid), (wv, qkv, 2 * n * hid)], p, n, hid)
-        gpu.matmul(wo, qkv, 0, n, hb, 0, bias=hb)           # O with its residual
-        pd = gpu.gate_up_silu(wg, wu, hb, 0, n, act, 0, want_prepared=True)
-        gpu.matmul(wd, act, 0, n, hb, 0, prepared=pd, bias=hb)  # down with its residual
-
-    ms = timed_graph(gpu, rec, reps, 3)
+    qkv, act, gu = gpu.alloc(4 * n * 3 * HID), gpu.alloc(4 * n * FFN), gpu.alloc(4 * n * 2 * FFN)
+    ops = {"qkv": 2 * n * 3 * HID * HID, "o": 2 * n * HID * HID, "gate_up": 2 * n * 2 * FFN * HID,
+           "down": 2 * n * HID * FFN}
     total_ops = sum(ops.values())
-    tops = total_ops / (ms * 1e-3) / 1e12
-    log(f"n={n} layer set: {ms * 1e3:.1f} us, {tops:.1f} TOPS ({tops / INT8_PEAK_TOPS * 100:.1f}% of int8 peak)")
 
-    # the same work piece by piece (each its own graph): quantization alone and
-    # each projection on already-prepared activations
-    gu = gpu.alloc(4 * n * 2 * ffn)
-    norm_w = (1.0 + 0.1 * rng.standard_normal(hid)).astype(np.float32)  # the fused rmsnorm -> Q8_0 prologue
-    # A Prepared points into the library's one activation workspace (valid
-    # until the next prepare, as the reference's); keep copies in buffers of
-    # our own so both operands stay valid side by side.
-    p, pbuf = own_prepared(gpu, gpu.prepare(xb, 0, n, hid), n, hid)
-    pf, pfbuf = own_prepared(gpu, gpu.prepare(act, 0, n, ffn), n, ffn)
+    def layer_set(i):
+        L = layers[i]
+        p = gpu.prepare(xb, 0, n, HID)
+        gpu.matmul_prompt_group([(L["q"], qkv, 0), (L["k"], qkv, n * HID), (L["v"], qkv, 2 * n * HID)], p, n, HID)
+        gpu.matmul(L["o"], qkv, 0, n, hb, 0, bias=hb)                  # O with its residual
+        pd = gpu.gate_up_silu(L["gate"], L["up"], hb, 0, n, act, 0, want_prepared=True)
+        gpu.matmul(L["down"], act, 0, n, hb, 0, prepared=pd, bias=hb)  # down with its residual
+
+    ms = rotating_trials(gpu, layer_set, copies, max(steps // 4, copies), warmup)
+    s = summary(ms, total_ops, 1e-12)
+    log(f"n={n} layer set (MALL-cold, {copies} layer copies): {s['median_us']:.1f} us, {s['value']:.1f} TOPS "
+        f"({s['value'] / INT8_PEAK_TOPS * 100:.1f}% of int8 peak); trials {s['trials']}")
+
+    # each piece alone on the same rotation; prepared operands copied into
+    # buffers of our own (a Prepared views the one activation workspace)
+    norm_w = (1.0 + 0.1 * rng.standard_normal(HID)).astype(np.float32)
+    p, pbuf = own_prepared(gpu, gpu.prepare(xb, 0, n, HID), n, HID)
+    pf, pfbuf = own_prepared(gpu, gpu.prepare(act, 0, n, FFN), n, FFN)
     pieces = {
-        "quantize_x": lambda: gpu.prepare(xb, 0, n, hid),
-        "quantize_act": lambda: gpu.prepare(act, 0, n, ffn),
-        "norm_prepare_x": lambda: gpu.norm_prepare(xb, 0, norm_w, 1e-6, n),
-        "qkv": lambda: gpu.matmul_prompt_group([(wq, qkv, 0), (wk, qkv, n * hid), (wv, qkv, 2 * n * hid)],
-                                               p, n, hid),
-        "o": lambda: gpu.matmul(wo, qkv, 0, n, hb, 0, prepared=p),
-        "gate_up": lambda: gpu.matmul_prompt_group([(wg, gu, 0), (wu, gu, n * ffn)], p, n, hid),
-        "gate_up_silu": lambda: gpu.gate_up_silu(wg, wu, hb, 0, n, act, 0, want_prepared=True),
-        "down": lambda: gpu.matmul(wd, act, 0, n, hb, 0, prepared=pf),
+        "quantize_x": lambda i: gpu.prepare(xb, 0, n, HID),
+        "quantize_act": lambda i: gpu.prepare(act, 0, n, FFN),
+        "norm_prepare_x": lambda i: gpu.norm_prepare(xb, 0, norm_w, 1e-6, n),
+        "qkv": lambda i: gpu.matmul_prompt_group([(layers[i]["q"], qkv, 0), (layers[i]["k"], qkv, n * HID),
+                                                  (layers[i]["v"], qkv, 2 * n * HID)], p, n, HID),
+        "o": lambda i: gpu.matmul(layers[i]["o"], qkv, 0, n, hb, 0, prepared=p),
+        "gate_up": lambda i: gpu.matmul_prompt_group([(layers[i]["gate"], gu, 0), (layers[i]["up"], gu, n * FFN)],
+                                                     p, n, HID),
+        "gate_up_silu": lambda i: gpu.gate_up_silu(layers[i]["gate"], layers[i]["up"], hb, 0, n, act, 0,
+                                                   want_prepared=True),
+        "down": lambda i: gpu.matmul(layers[i]["down"], act, 0, n, hb, 0, prepared=pf),
     }
     piece_us = {}
-    per_graph = 10  # one graph launch costs more than a kernel: record each piece 10 times per graph
-
-    def repeat(fn):
-        return lambda: [fn() for _ in range(per_graph)]
     for name, fn in pieces.items():
-        piece_us[name] = round(timed_graph(gpu, repeat(fn), reps, 3) / per_graph * 1e3, 2)
+        piece_us[name] = round(statistics.median(rotating_trials(gpu, fn, copies, max(steps // 2, copies), 2)) * 1e3,
+                               2)
+    piece_tops = {nm: round(ops[nm] / (piece_us[nm] * 1e-6) / 1e12, 1) for nm in ("qkv", "o", "gate_up", "down")}
     log("n=512 pieces (us): " + ", ".join(f"{k} {v}" for k, v in piece_us.items()))
-    for w in (wq, wk, wv, wo, wg, wu, wd):
-        gpu.release(w)
-    for b in (xb, qkv, hb, act, gu, pbuf, pfbuf):
+    for L in layers:
+        for w in L.values():
+            gpu.release(w)
+    for b in (xb, hb, qkv, act, gu, pbuf, pfbuf):
         b.free()
-    return {"us": ms * 1e3, "tops": tops, "ops": total_ops, "frac": tops / INT8_PEAK_TOPS,
-            "ops_by_projection": ops, "quantize_us": piece_us["quantize_x"], "projections_us": piece_us}
+    return {"us": s["median_us"], "tops": s["value"], "trials_tops": s["trials"], "ops": total_ops,
+            "frac": s["value"] / INT8_PEAK_TOPS, "ops_by_projection": ops, "copies": copies,
+            "quantize_us": piece_us["quantize_x"], "projections_us": piece_us, "projections_tops": piece_tops}
 
 
-def bench_decode_layer(gpu, reps, rng):
-    """decode n = 1 layer set and the lm_head GEMV + argmax."""
-    hid, ffn, vocab = 2304, 5760, 122880
-    wq, wk, wv, wo = (make_weight(rng, hid, hid) for _ in range(4))
-    wg, wu = make_weight(rng, ffn, hid), make_weight(rng, ffn, hid)
-    wd = make_weight(rng, hid, ffn)
-    for w in (wq, wk, wv, wo, wg, wu, wd):
+# ---------------------------------------------------------------------------
+# configs[1], configs[2]
+# ---------------------------------------------------------------------------
+
+def bench_gemm_configs1(gpu, m, k, n, steps, warmup, rng, label):
+    import oracle
+    from llm_amd import q8
+    base = make_weight(rng, m, k)
+    per = m * k // 32 * 34 + n * k * 4 + 4 * n * m
+    copies = copies_for(m * k // 32 * 34)
+    weights = [base] + [q8.Weight(base.data.copy(), k, m) for _ in range(copies - 1)]
+    for w in weights:
         gpu.resident(w)
-    x = rng.standard_normal(hid, dtype=np.float32)
-    xb, qkv, hb, act = gpu.alloc(4 * hid), gpu.alloc(4 * 3 * hid), gpu.alloc(4 * hid), gpu.alloc(4 * ffn)
+    xb, yb = gpu.alloc(4 * n * k), gpu.alloc(4 * n * m)
+    xb.upload(oracle.make_activations(rng, n, k, outlier_rate=0.01))
+    ms = rotating_trials(gpu, lambda i: gpu.matmul(weights[i], xb, 0, n, yb, 0), copies, max(steps // 2, copies),
+                         warmup)
+    s = summary(ms, per, 1e-9)
+    tops = 2 * m * n * k / (s["median_us"] * 1e-6) / 1e12
+    log(f"{label}: {s['median_us']:.2f} us/matmul, {s['value']:.0f} GB/s, {tops:.1f} TOPS")
+    for w in weights:
+        gpu.release(w)
+    xb.free()
+    yb.free()
+    return {"us": s["median_us"], "gbs": round(s["value"], 1), "tops": round(tops, 2), "bytes": per}
+
+
+def bench_decode_layer(gpu, steps, warmup, rng):
+    """the n = 1 layer set on rotating layer copies, and the
+    lm_head GEMV + argmax (301 MB: larger than the Infinity Cache)."""
+    from llm_amd import q8
+    shapes = [(HID, HID)] * 4 + [(FFN, HID), (FFN, HID), (HID, FFN)]
+    base = [make_weight(rng, *sh) for sh in shapes]
+    wbytes = sum(w.data.size for w in base)
+    copies = copies_for(wbytes)
+    layers = [base] + [[q8.Weight(w.data.copy(), w.k, w.out) for w in base] for _ in range(copies - 1)]
+    for L in layers:
+        for w in L:
+            gpu.resident(w)
+    x = rng.standard_normal(HID, dtype=np.float32)
+    xb, qkv, hb, act = gpu.alloc(4 * HID), gpu.alloc(4 * 3 * HID), gpu.alloc(4 * HID), gpu.alloc(4 * FFN)
     xb.upload(x)
     hb.upload(x)
 
-    def rec():
-        gpu.matmul_decode_group([(wq, qkv, 0), (wk, qkv, hid), (wv, qkv, 2 * hid)], xb, 0, hid)
+    def layer(i):
+        wq, wk, wv, wo, wg, wu, wd = layers[i]
+        gpu.matmul_decode_group([(wq, qkv, 0), (wk, qkv, HID), (wv, qkv, 2 * HID)], xb, 0, HID)
         gpu.matmul(wo, qkv, 0, 1, hb, 0, bias=hb)
         gpu.gate_up_silu(wg, wu, hb, 0, 1, act, 0)
         gpu.matmul(wd, act, 0, 1, hb, 0, bias=hb)
 
-    ms = timed_graph(gpu, rec, reps, 3)
-    wbytes = (4 * hid * hid + 2 * ffn * hid + hid * ffn) // 32 * 34
-    layer = {"us": ms * 1e3, "weight_bytes": wbytes, "gbs": wbytes / (ms * 1e-3) / 1e9}
-    log(f"decode layer set: {ms * 1e3:.1f} us, {layer['gbs']:.0f} GB/s (weights, L2/MALL-warm)")
-    for w in (wq, wk, wv, wo, wg, wu, wd):
-        gpu.release(w)
+    s = summary(rotating_trials(gpu, layer, copies, max(steps // 2, copies), warmup), wbytes, 1e-9)
+    log(f"decode layer set (MALL-cold, {copies} copies): {s['median_us']:.1f} us, {s['value']:.0f} GB/s of weights")
+    for L in layers:
+        for w in L:
+            gpu.release(w)
 
-    wl = make_weight(rng, vocab, hid)
+    wl = make_weight(rng, VOCAB, HID)
     gpu.resident(wl)
-    logits = gpu.alloc(4 * vocab)
-
-    def rec_head():
-        gpu.matmul(wl, xb, 0, 1, logits, 0)
-
-    ms_h = timed_graph(gpu, rec_head, reps, 3)
-    per = gemv_bytes(vocab, hid)
+    logits = gpu.alloc(4 * VOCAB)
+    per = gemv_bytes(VOCAB, HID)
+    h = summary(rotating_trials(gpu, lambda i: gpu.matmul(wl, xb, 0, 1, logits, 0), 1, 20, 2), per, 1e-9)
     t0 = time.perf_counter()
     best = gpu.lm_head_argmax(wl, xb, 0, logits, 0)
-    head = {"us": ms_h * 1e3, "gbs": per / (ms_h * 1e-3) / 1e9, "bytes": per, "argmax": best,
-            "argmax_call_us_host": (time.perf_counter() - t0) * 1e6}
-    log(f"lm_head 122880x2304: {ms_h * 1e3:.1f} us, {head['gbs']:.0f} GB/s")
+    log(f"lm_head 122880x2304: {h['median_us']:.1f} us, {h['value']:.0f} GB/s")
     gpu.release(wl)
     for b in (xb, qkv, hb, act, logits):
         b.free()
-    return layer, head
+    return ({"us": s["median_us"], "weight_bytes": wbytes, "gbs": round(s["value"], 1), "copies": copies},
+            {"us": h["median_us"], "gbs": round(h["value"], 1), "bytes": per, "argmax": best,
+             "argmax_call_us_host": round((time.perf_counter() - t0) * 1e6, 1)})
 
 
-def bench_decoder(gpu, rng, prompt=512, steps=128, reps=3):
-    """prefill `prompt` random ids, then `steps` greedy decode
-    steps, on the 42-layer synthetic decoder.  Each phase runs once untimed
-    (the eager pass, then the capture of its graph) before the timed runs;
-    times are host wall-clock around the calls (which end in a wait), the
-    median of `reps`."""
+# ---------------------------------------------------------------------------
+# configs[4]: the decoder, llama-bench style
+# ---------------------------------------------------------------------------
+
+def tactic_names(gpu):
+    """The kernel each configs shape runs (the tactic table's choice)."""
+    from llm_amd import q8
+    shapes = {"configs0_gemv": (1, 5760, HID), "configs1_n8": (8, 5760, HID), "configs1_n64": (64, 5760, HID),
+              "n512_qkv": (512, 3 * HID, HID), "n512_o": (512, HID, HID), "n512_gate_up": (512, 2 * FFN, HID),
+              "n512_down": (512, HID, FFN), "decode_o": (1, HID, HID), "decode_down": (1, HID, FFN),
+              "lm_head": (1, VOCAB, HID)}
+    out = {}
+    for name, (n, m, k) in shapes.items():
+        t = gpu.plan(n, m, k)
+        out[name] = t.get("name")
+    return out
+
+
+def bench_decoder(gpu, rng, prompt=512, steps=128, reps=5):
+    """pp512 / tg128 as llama-bench reports them: each repeat
+    resets the context, prefills `prompt` random ids (pp) and decodes `steps`
+    greedy tokens (tg); tok/s mean and sample std over `reps` repeats, after
+    one eager pass and one capture pass.  Host wall clock around calls that
+    end in a wait."""
     from llm_amd import decoder as dm
-    cfg = dm.config(n_layer=42, n_embd=2304, n_ff=5760, n_head=36, n_head_kv=36, head_dim=64, n_vocab=122880,
+    cfg = dm.config(n_layer=42, n_embd=HID, n_ff=FFN, n_head=36, n_head_kv=36, head_dim=64, n_vocab=VOCAB,
                     capacity=4096, max_batch=prompt)
     t0 = time.perf_counter()
     dec = dm.Decoder(gpu, cfg, seed=0x5EED)
@@ -354,23 +418,29 @@ def bench_decoder(gpu, rng, prompt=512, steps=128, reps=3):
             tokens = cur
     finally:
         dec.close()
-    t_pre, t_gen = float(np.median(pre)), float(np.median(gen))
-    layer_w = (2304 * 3 * 2304 + 2304 * 2304 + 2 * 5760 * 2304 + 2304 * 5760) // 32 * 34
-    head_w = 122880 * 2304 // 32 * 34
-    per_token = 42 * layer_w + head_w
-    out = {"prefill_tokens": prompt, "prefill_ms": round(t_pre * 1e3, 2),
-           "prefill_tok_s": round(prompt / t_pre, 1),
-           "decode_steps": steps, "decode_ms_per_token": round(t_gen / steps * 1e3, 3),
-           "decode_tok_s": round(steps / t_gen, 1),
+    pp = [prompt / t for t in pre]
+    tg = [steps / t for t in gen]
+    layer_w = (HID * 3 * HID + HID * HID + 2 * FFN * HID + HID * FFN) // 32 * 34
+    per_token = 42 * layer_w + VOCAB * HID // 32 * 34
+    t_gen = statistics.mean(gen)
+    out = {"r": reps,
+           f"pp{prompt}_tok_s": round(statistics.mean(pp), 1), f"pp{prompt}_tok_s_std": round(statistics.stdev(pp), 1),
+           f"tg{steps}_tok_s": round(statistics.mean(tg), 1), f"tg{steps}_tok_s_std": round(statistics.stdev(tg), 2),
+           "prefill_ms": round(statistics.mean(pre) * 1e3, 3),
+           "decode_ms_per_token": round(t_gen / steps * 1e3, 4),
            "decode_weight_bytes_per_token": per_token,
            "decode_weight_gbs": round(per_token * steps / t_gen / 1e9, 1),
            "decode_floor_ms_per_token_at_8tbs": round(per_token / 8e12 * 1e3, 3),
-           "first_tokens": tokens[:8]}
-    log(f"decoder: prefill {prompt} in {t_pre * 1e3:.1f} ms ({out['prefill_tok_s']} tok/s); decode "
-        f"{out['decode_ms_per_token']} ms/token ({out['decode_tok_s']} tok/s, {out['decode_weight_gbs']} GB/s of "
-        f"weights)")
+           "tokens_first_16": tokens[:16], "distinct_tokens": len(set(tokens))}
+    log(f"decoder: pp{prompt} {out[f'pp{prompt}_tok_s']} +- {out[f'pp{prompt}_tok_s_std']} tok/s; tg{steps} "
+        f"{out[f'tg{steps}_tok_s']} +- {out[f'tg{steps}_tok_s_std']} tok/s ({out['decode_ms_per_token']} ms/token, "
+        f"{out['decode_weight_gbs']} GB/s of weights)")
     return out
 
+
+# ---------------------------------------------------------------------------
+# CPU baseline and counter calibration
+# ---------------------------------------------------------------------------
 
 CALIBRATION_BYTES = 64 << 20
 
@@ -386,44 +456,87 @@ def calibration_copy(gpu, reps=3):
     dst.free()
 
 
-def cpu_baseline(seconds: float = 10.0):
-    """The oracle (C restatement of tensor::matmul, rayon-style row split) on
-    this host's cores: configs[0] GEMV for ~`seconds` of wall time."""
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(seconds: float = 8.0):
+    """The oracle (C restatement of tensor::matmul, rayon-style row split,
+    AVX2 order) on this host: the configs[0] GEMV over rotating weight copies
+    (GB/s) and the configs[3] n = 512 layer set (TOPS), each for about
+    `seconds` of wall time.  Threads: every core this process may run on,
+    capped at the box's CPU share for one GPU (OMP_NUM_THREADS, 16 on the
+    GPU boxes), which rayon's default (available_parallelism) would not see."""
     import oracle
     try:
-        cores = len(os.sched_getaffinity(0))
+        affinity = len(os.sched_getaffinity(0))
     except AttributeError:
-        cores = os.cpu_count() or 1
-    threads = max(1, min(cores, 16))
+        affinity = os.cpu_count() or 1
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    threads = max(1, min(affinity, share) if share > 0 else affinity)
     rng = np.random.default_rng(0x5EED)
-    m, k = 5760, 2304
-    data = oracle.make_q8_weight(rng, m, k)
+    m, k = 5760, HID
+    base = oracle.make_q8_weight(rng, m, k)
+    copies = copies_for(base.size)
+    ws = [base] + [base.copy() for _ in range(copies - 1)]
     x = rng.standard_normal(k, dtype=np.float32)
-    oracle.matmul(data, k, m, x, 1, threads=threads)
+    oracle.matmul(ws[0], k, m, x, 1, threads=threads)
     reps = 0
     t0 = time.perf_counter()
     while time.perf_counter() - t0 < seconds:
-        oracle.matmul(data, k, m, x, 1, threads=threads)
+        oracle.matmul(ws[reps % copies], k, m, x, 1, threads=threads)
         reps += 1
     dt = time.perf_counter() - t0
     gbs = gemv_bytes(m, k) * reps / dt / 1e9
-    log(f"cpu baseline: {gbs:.1f} GB/s with {threads} threads ({oracle.simd_path()}), {reps} GEMVs")
+    del ws
+    # configs[3]: the four projections at n = 512
+    n = 512
+    lw = {nm: oracle.make_q8_weight(rng, o, kk) for nm, (o, kk) in
+          {"qkv": (3 * HID, HID), "o": (HID, HID), "gate_up": (2 * FFN, HID), "down": (HID, FFN)}.items()}
+    xa = oracle.make_activations(rng, n, HID)
+    xf = oracle.make_activations(rng, n, FFN)
+    ops = 2 * n * (3 * HID * HID + HID * HID + 2 * FFN * HID + HID * FFN)
+    layers = 0
+    t0 = time.perf_counter()
+    while True:
+        oracle.matmul(lw["qkv"], HID, 3 * HID, xa, n, threads=threads)
+        oracle.matmul(lw["o"], HID, HID, xa, n, threads=threads)
+        oracle.matmul(lw["gate_up"], HID, 2 * FFN, xa, n, threads=threads)
+        oracle.matmul(lw["down"], FFN, HID, xf, n, threads=threads)
+        layers += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt2 = time.perf_counter() - t0
+    tops = ops * layers / dt2 / 1e12
+    model = cpu_model()
+    log(f"cpu baseline ({model}, nproc {os.cpu_count()}, affinity {affinity}, {threads} threads, "
+        f"{oracle.simd_path()}): GEMV {gbs:.1f} GB/s ({reps} GEMVs over {copies} copies); n=512 layer set "
+        f"{tops:.3f} TOPS ({layers} layer sets in {dt2:.1f} s)")
     return {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{reps} configs[0] GEMVs (5760x2304, n=1, f32 x) in {dt:.1f} s, "
-                      f"{oracle.simd_path()} order, threads={threads}, cache-warm 14 MB matrix"}
+            "sample": f"{reps} configs[0] GEMVs (5760x2304, n=1, f32 x) over {copies} rotating weight copies in "
+                      f"{dt:.1f} s; {layers} configs[3] n=512 layer sets in {dt2:.1f} s",
+            "n512_layer_tops": round(tops, 4), "cpu_model": model, "nproc": os.cpu_count(),
+            "affinity_cores": affinity, "threads": threads, "simd_path": oracle.simd_path(),
+            "label": "C restatement of the reference rayon CPU path (oracle/q8_oracle.c)"}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--sections", default="all",
-                    help="comma list of gemv,gemm,extras,decoder,cpu (default all); a profiler run names "
+                    help="comma list of gemv,ceilings,gemm,extras,decoder,cpu (default all); a profiler run names "
                          "one so each kernel's average covers one workload")
     args = ap.parse_args()
-    known = {"gemv", "gemm", "extras", "decoder", "cpu"}
+    known = {"gemv", "ceilings", "gemm", "extras", "decoder", "cpu"}
     sections = set(known) if args.sections == "all" else set(args.sections.split(","))
     unknown = sections - known
     if unknown:
@@ -432,70 +545,105 @@ def main():
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus "
               f"{args.gpus}); the sharding design is described in DESIGN.md", file=sys.stderr)
         sys.exit(2)
+    steps = max(1, args.steps)
+    warmup = max(0, args.warmup)
 
     from llm_amd import q8
     rng = np.random.default_rng(0x5EED)
     gpu = q8.Gpu(0)
     log(f"device {gpu.name}")
     calibration_copy(gpu)
-    m, k = 5760, 2304
+    m, k = 5760, HID
     gemv = {"gbs": None, "us_per_step": None, "bytes_per_step": gemv_bytes(m, k), "copies": None}
     if "gemv" in sections:
-        gemv = bench_gemv_rotating(gpu, m, k, args.steps, args.warmup, rng, "configs[0] GEMV")
+        gemv = bench_gemv(gpu, m, k, steps, warmup, rng)
+    ceil = bench_ceilings(gpu, steps, warmup, gemv_bytes(m, k)) if "ceilings" in sections else {}
     gemm = {"tops": None, "frac": None, "us": None, "ops": None}
     if "gemm" in sections:
-        gemm = bench_layer_n512(gpu, 20, rng)
+        gemm = bench_layer_n512(gpu, steps, warmup, rng)
     extras = {}
     if "extras" in sections:
-        gemv["mall_hot"] = bench_gemv_hot(gpu, m, k, rng)
-        extras["configs1_n8"] = bench_gemm_rotating(gpu, m, k, 8, 5, rng, "configs[1] n=8")
-        extras["configs1_n64"] = bench_gemm_rotating(gpu, m, k, 64, 5, rng, "configs[1] n=64")
-        layer, head = bench_decode_layer(gpu, 50, rng)
+        extras["configs1_n8"] = bench_gemm_configs1(gpu, m, k, 8, steps, warmup, rng, "configs[1] n=8")
+        extras["configs1_n64"] = bench_gemm_configs1(gpu, m, k, 64, steps, warmup, rng, "configs[1] n=64")
+        layer, head = bench_decode_layer(gpu, steps, warmup, rng)
         extras["configs2_decode_layer"] = layer
         extras["configs2_lm_head"] = head
     decoder = bench_decoder(gpu, rng) if "decoder" in sections else None
-    cpu = cpu_baseline(args.cpu_seconds) if "cpu" in sections and args.cpu_seconds > 0 else None
-    # the kernel the tactic table runs for configs[0] (the one `value` times)
-    t = gpu.plan(1, m, k)
-    gemv_kernel = (f"q8_gemv_r{t['row_slice']}_l{t['slice_loads']}" if t["row_slice"] in (8, 16)
-                   else f"q8_gemv1_pb{t['pairs_per_batch']}_e{t['exact']}")
+    tactics = tactic_names(gpu)
+    build = json.loads(q8.build_info())
     gpu.close()
+    cpu = cpu_baseline(args.cpu_seconds) if "cpu" in sections and args.cpu_seconds > 0 else None
 
     value = gemv["gbs"]
+    ceiling = ceil.get("ceiling_gbs")
+
+    def r(v, nd=1):
+        return round(v, nd) if v is not None else None
+
     line = {
         "metric": METRIC,
-        "value": round(value, 1) if value is not None else None,
+        "value": r(value),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": gemv["us_per_step"] / 1e3 if gemv["us_per_step"] is not None else None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q8_0 weights x f32 activations (n=1); int8 x int8 -> int32, f32 scales (n>=2)",
+        "dtype": "f32",
         "data": "synthetic: seeded random Q8_0 weights (q ~ U[-127,127], d = f16(|N(0,0.02)|/127)), x ~ N(0,1)",
-        "config": {"workload": "configs[0] Q8_0 GEMV n=1, W 5760x2304, MALL-cold (rotating copies); "
-                               "plus configs[3] n=512 layer projections",
-                   "M": m, "K": k, "n": 1, "rotating_copies": gemv["copies"]},
-        "roofline": {"bound": "hbm", "achieved": round(value, 1) if value is not None else None,
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "config": {"workload": "configs[0] Q8_0 GEMV n=1, W 5760x2304 (q8_0 weights x f32 x, f32 FMA), MALL-cold "
+                               "(rotating copies); median of 5 trials of --steps steps",
+                   "M": m, "K": k, "n": 1, "rotating_copies": gemv["copies"], "trials": TRIALS},
+        "roofline": {"bound": "hbm", "achieved": r(value), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(value / HBM_PEAK_GBS, 4) if value is not None else None,
-                     "traffic": traffic_from_profile(),
-                     "kernel": gemv_kernel, "bytes_per_launch": gemv["bytes_per_step"],
-                     "mall_hot_gbs": gemv.get("mall_hot")},
-        "gemm_n512": {"value": round(gemm["tops"], 2) if gemm["tops"] is not None else None, "unit": "TOPS",
-                      "peak": INT8_PEAK_TOPS,
+                     "traffic": traffic_from_profile(build),
+                     "kernel": tactics.get("configs0_gemv"), "bytes_per_launch": gemv["bytes_per_step"],
+                     "ceiling_gbs": ceiling, "ceiling_kernel": ceil.get("ceiling_kernel"),
+                     "frac_of_ceiling": round(value / ceiling, 4) if value and ceiling else None,
+                     "trials_gbs": gemv.get("trials_gbs"), "mall_hot_gbs": gemv.get("mall_hot_gbs")},
+        "gemm_n512": {"value": r(gemm["tops"], 2), "unit": "TOPS", "peak": INT8_PEAK_TOPS,
                       "frac": round(gemm["frac"], 4) if gemm["frac"] is not None else None,
-                      "us_per_layer": round(gemm["us"], 2) if gemm["us"] is not None else None,
-                      "ops_per_layer": gemm["ops"],
-                      "quantize_us": gemm.get("quantize_us"),
-                      "projections_us": gemm.get("projections_us")},
+                      "us_per_layer": r(gemm["us"], 2), "ops_per_layer": gemm["ops"],
+                      "mall": f"cold ({gemm.get('copies')} rotating layer copies)",
+                      "trials_tops": gemm.get("trials_tops"),
+                      "mfma_ceiling_tops": ceil.get("mfma_i8_tops"),
+                      "tile_block_ceiling_tops": ceil.get("tile_block_mix_tops"),
+                      "quantize_us": gemm.get("quantize_us"), "projections_us": gemm.get("projections_us"),
+                      "projections_tops": gemm.get("projections_tops")},
+        "ceilings": ceil,
         "extras": extras,
         "decoder_configs4": decoder,
+        "build": {"code_object_sha256": build["code_object_sha256"], "hipcc": build.get("hipcc"),
+                  "tactics": tactics},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "q8_gemv_configs0_traffic.md")
+
+
+def traffic_from_profile(build):
+    """HBM bytes per configs[0] GEMV launch from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary, if it was measured on the code object
+    loaded now (its sha256 is recorded in the summary); otherwise None."""
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None
+    fields = {}
+    for line in text.splitlines():
+        if line.startswith("- ") and ": " in line:
+            key, val = line[2:].split(": ", 1)
+            fields[key.strip("` ")] = val.strip("` ")
+    if fields.get("code_object_sha256") != build["code_object_sha256"]:
+        return None
+    try:
+        return int(fields["traffic_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
 
 
 if __name__ == "__main__":

@@ -273,6 +273,30 @@ int q8_argmax(q8_ctx *ctx, q8_dptr values, size_t offset, size_t len, uint32_t *
 int q8_embeddings(q8_ctx *ctx, const q8_weight *weight, const uint32_t *tokens, size_t n, q8_dptr out,
                   size_t out_offset);
 
+/* ---- measurement kernels (no counterpart in the reference) ----
+ * The ceilings the benchmark quotes the hot-path kernels against, run on the
+ * context's stream like any launch (time them with events or graphs):
+ *   Q8_PROBE_READ_L{4,8,16}  a plain streaming read of `bytes` at `src`
+ *                            (16-byte aligned, a multiple of 16), L 16-byte
+ *                            loads per lane, one pass;
+ *   Q8_PROBE_EMPTY           a one-wave kernel that does nothing;
+ *   Q8_PROBE_MFMA            `iters` x 4 v_mfma_i32_32x32x32_i8 per wave;
+ *   Q8_PROBE_VALU            `iters` x 32 VALU (16 cvt + 16 fma) per wave;
+ *   Q8_PROBE_MIX             `iters` GEMM tile-blocks per wave with operands
+ *                            in registers: an int8 MFMA, half an f32
+ *                            outer-product MFMA and 32 VALU each;
+ * the last three over `workgroups` workgroups of four waves (iters even). */
+enum {
+    Q8_PROBE_READ_L4 = 0,
+    Q8_PROBE_READ_L8 = 1,
+    Q8_PROBE_READ_L16 = 2,
+    Q8_PROBE_EMPTY = 3,
+    Q8_PROBE_MFMA = 4,
+    Q8_PROBE_VALU = 5,
+    Q8_PROBE_MIX = 6
+};
+int q8_probe(q8_ctx *ctx, int which, q8_dptr src, size_t bytes, int iters, int workgroups);
+
 /* ---- tactics: the shape-keyed plan (tactics.rs:229-347, for gfx950) ---- */
 
 /* The tactic a matmul of n tokens over an out x k weight would run. */

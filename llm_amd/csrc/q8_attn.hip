@@ -249,14 +249,19 @@ static __device__ __forceinline__ void attn_decode_body(const Q8AttnDecodeArgs &
             store_agent(a.part_ms + 2 * (base + split) + 1, sum);
         }
     }
-    __builtin_amdgcn_s_waitcnt(0);
+    // Release the partials at agent scope, count the arrival with an acq_rel
+    // read-modify-write, and acquire in the last workgroup before its loads:
+    // the XCDs' L2s are not coherent with each other, so the ordering has to
+    // be stated, not left to the stores having completed.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     __syncthreads();
     if (tid == 0) {
-        const unsigned old = atomicAdd(&a.counters[head], 1u);
+        const unsigned old = __hip_atomic_fetch_add(&a.counters[head], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
         last_flag = (old == (unsigned)(a.splits - 1));
     }
     __syncthreads();
     if (!last_flag) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     if (tid == 0) __hip_atomic_store(&a.counters[head], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (wave != 0) return;
     float gmax = -INFINITY;

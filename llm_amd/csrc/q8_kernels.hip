@@ -247,16 +247,16 @@ static __device__ __forceinline__ float chain_row(const float *row, int count) {
 // float4s per head), q8_attn_decode's combine term for term: the head's max
 // over the splits, e_s = exp(max_s - max) (0 for an empty split), the
 // weighted values and weights by fused multiply-adds, s ascending, and one
-// division per element.  The caller guarantees head dim 64, at most
-// Q8_ATTN_COMBINE_MAX splits and a thread per float4 of x (threads with
-// v >= nb * 8 load clamped and store to the pad).
+// division per element.  The caller guarantees head dim 64 and at most
+// Q8_ATTN_COMBINE_MAX splits; the tile kernel also a thread per float4 of x
+// (threads with v >= nb * 8 load clamped and store to the pad), the
+// row-slice kernels loop over the rest (combine_rest).
 struct CombineRegs {
     f32x4 acc[Q8_ATTN_COMBINE_MAX];
     f32x2 ms[Q8_ATTN_COMBINE_MAX];  // (max, sum)
 };
 
-static __device__ __forceinline__ void combine_load(const Q8GemvArgs &a, int nb, int ns, CombineRegs &c) {
-    const int v = min((int)threadIdx.x, nb * 8 - 1);
+static __device__ __forceinline__ void combine_load_v(const Q8GemvArgs &a, int v, int ns, CombineRegs &c) {
     const int hs = (v >> 4) * ns;  // head * splits
 #pragma unroll
     for (int s = 0; s < Q8_ATTN_COMBINE_MAX; s++) {
@@ -267,7 +267,12 @@ static __device__ __forceinline__ void combine_load(const Q8GemvArgs &a, int nb,
     }
 }
 
-static __device__ __forceinline__ void combine_store(int nb, int ns, const CombineRegs &c, float *xs, float *pad) {
+static __device__ __forceinline__ void combine_load(const Q8GemvArgs &a, int nb, int ns, CombineRegs &c) {
+    combine_load_v(a, min((int)threadIdx.x, nb * 8 - 1), ns, c);
+}
+
+static __device__ __forceinline__ void combine_store_v(int v, int nb, int ns, const CombineRegs &c, float *xs,
+                                                       float *pad) {
     float gmax = -INFINITY;
 #pragma unroll
     for (int s = 0; s < Q8_ATTN_COMBINE_MAX; s++) gmax = s < ns ? fmaxf(gmax, c.ms[s].x) : gmax;
@@ -282,12 +287,26 @@ static __device__ __forceinline__ void combine_store(int nb, int ns, const Combi
             for (int e = 0; e < 4; e++) num[e] = __builtin_fmaf(c.acc[s][e], f, num[e]);
         }
     }
-    const int v = threadIdx.x;
     float *d = v < nb * 8 ? xs + (v >> 3) * 32 + ((v & 7) >> 1) + 4 * (v & 1) : pad;
     d[0] = num.x / den;
     d[8] = num.y / den;
     d[16] = num.z / den;
     d[24] = num.w / den;
+}
+
+static __device__ __forceinline__ void combine_store(int nb, int ns, const CombineRegs &c, float *xs, float *pad) {
+    combine_store_v(threadIdx.x, nb, ns, c, xs, pad);
+}
+
+// The float4s of x past the workgroup's threads (a row-slice launch whose K
+// range needs fewer waves than x has float4s / 64): each thread builds them
+// in turn, v = tid + threads, tid + 2 threads, ..., with the same arithmetic.
+static __device__ __forceinline__ void combine_rest(const Q8GemvArgs &a, int nb, int ns, float *xs, float *pad) {
+    for (int v = (int)(threadIdx.x + blockDim.x); v < nb * 8; v += (int)blockDim.x) {
+        CombineRegs c;
+        combine_load_v(a, v, ns, c);
+        combine_store_v(v, nb, ns, c, xs, pad);
+    }
 }
 
 // ONE: a launch over one matrix (members == 1, no SiLU pair), whose fields
@@ -587,18 +606,20 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
             store_agent(gbuf + ((size_t)(slot * a.total_tiles + gtile) * S + slice) * 32 + r, acc);
         }
         // The last workgroup of the tile to arrive finishes it.  The partials
-        // travel as agent-scope atomic stores and loads (coherent across the
-        // XCDs' L2s without writing back or invalidating whole caches, which
-        // __threadfence does); each wave waits for its stores to complete
-        // before the workgroup's arrival is counted.
-        __builtin_amdgcn_s_waitcnt(0);
+        // travel as agent-scope atomic stores and loads; they are released at
+        // agent scope before the arrival is counted (an acq_rel
+        // read-modify-write) and acquired by the last workgroup before it
+        // loads them.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         __syncthreads();
         if (threadIdx.x == 0) {
-            const unsigned old = atomicAdd(&a.counters[gtile], 1u);
+            const unsigned old = __hip_atomic_fetch_add(&a.counters[gtile], 1u, __ATOMIC_ACQ_REL,
+                                                        __HIP_MEMORY_SCOPE_AGENT);
             last_flag = (old == (unsigned)(S - 1));
         }
         __syncthreads();
         if (!last_flag) return;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         if (threadIdx.x == 0) __hip_atomic_store(&a.counters[gtile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (wave != 0 || lane >= 32) return;
@@ -755,8 +776,9 @@ static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
     const int st_begin = 8 * b_begin;
     const int st_end = 8 * b_end;
     const int st_clamp = max(st_end - 1, 0);
-    // CMB: x is built by the folded attention combine instead (the host
-    // guarantees a thread per float4 of x); every wave then reads it.
+    // CMB: x is built by the folded attention combine instead (a thread per
+    // float4 of x, in turn where x has more float4s than the workgroup has
+    // threads); every wave then reads it.
     f32x4 xv[Q8_GEMV_STAGE];
     CombineRegs creg;
     const int ns = CMB ? a.attn_splits : 0;
@@ -789,6 +811,7 @@ static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
     }
     if constexpr (CMB) {
         combine_store(nb, ns, creg, xs, pad);
+        combine_rest(a, nb, ns, xs, pad);
         __syncthreads();
     }
     // stage x permuted (the tile kernel's order): float4 slot 8b + 4hh + t
@@ -2225,3 +2248,4 @@ extern "C" __global__ __launch_bounds__(256) void q8_silu_mul(Q8EltArgs a) {
 }
 
 #include "q8_attn.hip"
+#include "q8_probe.hip"

@@ -85,6 +85,7 @@ enum Fn {
     F_COPY,
     F_EMBED,
     F_ROPE, F_ATTN_DECODE, F_ATTN_DECODE_W4, F_ATTN_PREFILL, F_SYNTH, F_ADVANCE,
+    F_PROBE_READ_L4, F_PROBE_READ_L8, F_PROBE_READ_L16, F_PROBE_EMPTY, F_PROBE_MFMA, F_PROBE_VALU, F_PROBE_MIX,
     F_COUNT
 };
 
@@ -110,6 +111,8 @@ const char *const kFnNames[F_COUNT] = {
     "q8_copy",
     "q8_embed",
     "q8_rope_append", "q8_attn_decode", "q8_attn_decode_w4", "q8_attn_prefill", "q8_synth", "q8_advance",
+    "q8_probe_read_l4", "q8_probe_read_l8", "q8_probe_read_l16", "q8_probe_empty", "q8_probe_mfma",
+    "q8_probe_valu", "q8_probe_mix",
 };
 
 constexpr int kArgmaxParts = 1024;
@@ -159,6 +162,7 @@ struct q8_ctx {
     void *norm_ws = nullptr;             // rmsnorm(x) when a norm cannot fold into the decode GEMV
     size_t norm_ws_bytes = 0;
     void *argmax_ws = nullptr;           // per-workgroup partials + result
+    unsigned *probe_sink = nullptr;      // the measurement kernels' never-written result slot
     float *split_ws = nullptr;           // partial results of split-K workgroups
     unsigned *counters = nullptr;        // split-K arrival counters (kernels reset them to 0)
     void *token_ws = nullptr;            // token ids of the embedding lookup
@@ -385,16 +389,15 @@ struct GemvCombine {
 // x built by the folded attention combine): a workgroup per rs rows of a
 // 32-row tile and the whole K range, nl loads per lane, exact block order.
 // Returns Q8_ERR_UNSUPPORTED (without recording an error) when K needs more
-// than 16 waves, or the combine more threads than that, so the caller keeps
-// the tile kernel.
+// than 16 waves, or the combine more splits than it holds, so the caller
+// keeps the tile kernel.
 int run_gemv_rs(q8_ctx *c, const q8_weight *w, float *y, q8_dptr x, const float *bias, int rs, int nl,
                 const GemvCombine *comb) {
     const int nb = w->nb;
     const int bpw = nl * (64 / (2 * rs));
     const int waves = (int)ceil_div(nb, bpw);
     if (waves > 16) return Q8_ERR_UNSUPPORTED;
-    if (comb && (nb * 8 > waves * 64 || comb->splits < 1 || comb->splits > Q8_ATTN_COMBINE_MAX))
-        return Q8_ERR_UNSUPPORTED;
+    if (comb && (comb->splits < 1 || comb->splits > Q8_ATTN_COMBINE_MAX)) return Q8_ERR_UNSUPPORTED;
     Q8GemvArgs a{};
     a.members = 1;
     a.m[0].quants = w->quants;
@@ -944,6 +947,8 @@ int q8_open(int device, q8_ctx **out) {
         if (rc != Q8_OK) break;
         he = hipMalloc(&c->argmax_ws, kArgmaxParts * 8 + 256);
         if (he != hipSuccess) { rc = hip_fail(he, "hipMalloc(argmax)"); break; }
+        he = hipMalloc((void **)&c->probe_sink, 256);
+        if (he != hipSuccess) { rc = hip_fail(he, "hipMalloc(probe sink)"); break; }
         he = hipMalloc((void **)&c->split_ws, kSplitBytes);
         if (he != hipSuccess) { rc = hip_fail(he, "hipMalloc(split scratch)"); break; }
         he = hipMalloc((void **)&c->counters, kCounters * sizeof(unsigned));
@@ -976,6 +981,7 @@ void q8_close(q8_ctx *c) {
     if (c->act2_ws) hipFree(c->act2_ws);
     if (c->norm_ws) hipFree(c->norm_ws);
     if (c->argmax_ws) hipFree(c->argmax_ws);
+    if (c->probe_sink) hipFree(c->probe_sink);
     if (c->split_ws) hipFree(c->split_ws);
     if (c->counters) hipFree(c->counters);
     if (c->token_ws) hipFree(c->token_ws);
@@ -1472,6 +1478,43 @@ int q8_copy_device(q8_ctx *c, q8_dptr dst, q8_dptr src, size_t bytes) {
     a.bytes = (long long)bytes;
     a.blocks = (int)std::min<long long>(ceil_div((long long)(bytes / 16), 256), 8LL * c->cu_count);
     return launch(c, F_COPY, (unsigned)a.blocks, 256, 0, &a, sizeof a);
+}
+
+int q8_probe(q8_ctx *c, int which, q8_dptr src, size_t bytes, int iters, int workgroups) {
+    if (!c) return fail(Q8_ERR_INVALID, "q8_probe: null context");
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    Q8ProbeArgs a{};
+    a.never = 0x7fc0dead;  // a NaN payload: no XOR of the data or float sum is compared equal by chance
+    a.sink = c->probe_sink;
+    switch (which) {
+    case Q8_PROBE_READ_L4:
+    case Q8_PROBE_READ_L8:
+    case Q8_PROBE_READ_L16: {
+        if (bytes == 0 || bytes % 16 != 0 || src % 16 != 0)
+            return fail(Q8_ERR_INVALID, "q8_probe: read needs a 16-byte aligned source and a multiple of 16 bytes");
+        Q8_TRY(check_span(c, src, bytes, "probe src"));
+        const int l = which == Q8_PROBE_READ_L4 ? 4 : which == Q8_PROBE_READ_L8 ? 8 : 16;
+        const long long grid = ceil_div((long long)bytes, 256LL * 16 * l);
+        if (grid > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "q8_probe: %zu bytes", bytes);
+        a.src = reinterpret_cast<const uint8_t *>(src);
+        a.bytes = (long long)bytes;
+        const Fn f = l == 4 ? F_PROBE_READ_L4 : l == 8 ? F_PROBE_READ_L8 : F_PROBE_READ_L16;
+        return launch(c, f, (unsigned)grid, 256, 0, &a, sizeof a);
+    }
+    case Q8_PROBE_EMPTY:
+        return launch(c, F_PROBE_EMPTY, 1, 64, 0, &a, sizeof a);
+    case Q8_PROBE_MFMA:
+    case Q8_PROBE_VALU:
+    case Q8_PROBE_MIX: {
+        if (iters < 2 || iters % 2 != 0 || workgroups < 1)
+            return fail(Q8_ERR_INVALID, "q8_probe: iters must be even and >= 2, workgroups >= 1");
+        a.iters = iters;
+        const Fn f = which == Q8_PROBE_MFMA ? F_PROBE_MFMA : which == Q8_PROBE_VALU ? F_PROBE_VALU : F_PROBE_MIX;
+        return launch(c, f, (unsigned)workgroups, 256, 0, &a, sizeof a);
+    }
+    default:
+        return fail(Q8_ERR_INVALID, "q8_probe: unknown probe %d", which);
+    }
 }
 
 int q8_lm_head_argmax(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset, q8_dptr logits,

@@ -47,7 +47,7 @@ EXPORTS = (
     "q8_weight_resident", "q8_weight_release", "q8_weight_shape", "q8_weight_export",
     "q8_matmul", "q8_prepare", "q8_silu_mul_prepare", "q8_rmsnorm", "q8_norm_prepare", "q8_silu_mul",
     "q8_matmul_decode_group", "q8_matmul_prompt_group", "q8_gate_up_silu", "q8_gate_up_silu_prepared",
-    "q8_lm_head_argmax", "q8_argmax", "q8_copy_device", "q8_embeddings",
+    "q8_lm_head_argmax", "q8_argmax", "q8_copy_device", "q8_embeddings", "q8_probe",
     "q8_plan", "q8_tactic_count", "q8_tactic_row",
     "q8_event_create", "q8_event_record", "q8_event_elapsed_ms", "q8_event_destroy",
     "q8_graph_begin", "q8_graph_end", "q8_graph_launch", "q8_graph_destroy",
@@ -62,6 +62,9 @@ EXPORTS = (
     "q8_decoder_position", "q8_decoder_forward", "q8_decoder_generate", "q8_decoder_logits", "q8_decoder_weight",
     "q8_decoder_norm",
 )
+
+
+PROBE_READ_L4, PROBE_READ_L8, PROBE_READ_L16, PROBE_EMPTY, PROBE_MFMA, PROBE_VALU, PROBE_MIX = range(7)
 
 
 class Q8Error(RuntimeError):
@@ -178,6 +181,7 @@ def lib():
         "q8_lm_head_argmax": (c_int, [vp, vp, u64, c_size, u64, c_size, ctypes.POINTER(ctypes.c_uint32)]),
         "q8_argmax": (c_int, [vp, u64, c_size, c_size, ctypes.POINTER(ctypes.c_uint32)]),
         "q8_copy_device": (c_int, [vp, u64, u64, c_size]),
+        "q8_probe": (c_int, [vp, c_int, u64, c_size, c_int, c_int]),
         "q8_embeddings": (c_int, [vp, vp, ctypes.POINTER(ctypes.c_uint32), c_size, u64, c_size]),
         "q8_plan": (c_int, [vp, c_int, c_int, c_int, ctypes.POINTER(Tactic)]),
         "q8_tactic_count": (c_int, []),
@@ -595,6 +599,12 @@ class Gpu:
 
     def plan(self, n: int, out: int, k: int) -> dict:
         return plan(n, out, k, self)
+
+    def probe(self, which: int, src: "DeviceBuffer | None" = None, nbytes: int = 0, iters: int = 0,
+              workgroups: int = 0, src_offset: int = 0):
+        """Launch a measurement kernel (q8_probe, PROBE_* below)."""
+        ptr = src.ptr + src_offset if src is not None else 0
+        _check(lib().q8_probe(self.handle, which, ptr, nbytes, iters, workgroups))
 
     # ---- timing and graphs ----
     def event(self):

@@ -16,14 +16,17 @@ How each function is pinned (and where the pin lives):
   including every subnormal ``m * 2**-24``) and the reference KATs of
   ``apps/engine/tests/quant_q8.rs:13-63``; ``tests/test_oracle.py``.
 * ``dot_q8_0`` (AVX2 and scalar orders) -- the KATs of ``quant_q8.rs:14-44`` and
-  ``matmul.rs:139-152`` (f64 references, 1e-4 / 1e-3) plus an exact-order
-  restatement in numpy float32 (``tests/test_oracle.py``) that fails on a
-  dropped term, a wrong chunk order or a transposed operand.
+  ``matmul.rs:139-152`` (f64 references, 1e-4 / 1e-3), exact-arithmetic cases
+  (``tests/test_oracle.py``), and an independent exact-order restatement in
+  Python with each f32 operation rounded once (FMAs rounded from the exact
+  rational) that must agree bit for bit on random rows, in both orders
+  (``tests/test_oracle_order.py``).
 * ``quantize_q8_0`` -- closed form: scale = peak/127, half-away rounding,
   saturation, NaN and all-zero blocks; ``tests/test_oracle.py``.
 * ``dot_q8_0_q8_0`` -- the int32 block dot by brute force in int64, the KATs of
-  ``matmul.rs:154-168`` and ``matmul.rs:170-198``, and an exact-order numpy
-  restatement of both the scalar and the AVX2 lane order.
+  ``matmul.rs:154-168`` and ``matmul.rs:170-198``, and the same exact-order
+  restatement of both the scalar and the AVX2 lane order
+  (``tests/test_oracle_order.py``).
 * ``matmul`` -- ``matmul.rs:139-198`` and the row/thread independence the
   reference relies on (``tensor.rs:127-148``).
 * ``silu`` / ``rmsnorm`` / ``argmax`` -- ``ops.rs``'s hand values

@@ -74,7 +74,7 @@ def test_gguf_weight_gemv_matches_the_oracle(gpu, model, name):
         c.download(yb, y)
     finally:
         gpu.set_option("gemv.exact", -1)
-    if oracle.simd_path() == "avx2":
+    if oracle.simd_path() == "avx2+fma":
         assert_bits(y, ref, f"{name} n=1 exact")
     else:
         assert_close(y, ref, f"{name} n=1 exact")
@@ -164,7 +164,7 @@ def test_tied_embedding_is_also_the_lm_head(gpu, model):
     c.embeddings(w, [123], xb, 0)
     x = dequant_rows(data, k, [123]).reshape(-1).astype(np.float32)
     ref = oracle.matmul(data, k, vocab, x, 1).reshape(-1)
-    exact = oracle.simd_path() == "avx2"
+    exact = oracle.simd_path() == "avx2+fma"
     gpu.set_option("gemv.exact", 1 if exact else -1)
     try:
         top = gpu.lm_head_argmax(w, xb, 0, logits, 0)

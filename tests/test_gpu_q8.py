@@ -59,31 +59,88 @@ def exact_matmul(wdata, k, out, x, n):
     return y
 
 
+CLAUSE_LOG = []  # (what, outputs that used the accuracy clause, outputs checked); printed in the summary
+
+
+def exact_at(wdata, k, out, x=None, n=None, quants=None, scales=None):
+    """A function of flat output indices t*out + o giving the exact value of
+    the n >= 2 product there (f64 sum of the integer block dots times the f32
+    scale products d_w*s_x) and the sum of the block terms' magnitudes, for
+    assert_parity on shapes where the whole exact product is too slow in
+    numpy.  The activations come as f32 x (the
+    reference quantization is applied, quantize_q8_0) or already quantized
+    (quants [n, k] int8, scales [n, k/32] f32)."""
+    nb = k // 32
+    raw = np.asarray(wdata, np.uint8).reshape(out, nb, 34)
+    if quants is None:
+        x = np.asarray(x, np.float32).reshape(n, k)
+
+    def token(t):
+        if quants is not None:
+            return np.asarray(quants[t], np.int64).reshape(nb, 32), np.asarray(scales[t], np.float32)
+        qx, sx = oracle.quantize_q8_0(x[t])
+        return qx.astype(np.int64).reshape(nb, 32), sx
+
+    def at(flat):
+        flat = np.asarray(flat, np.int64).reshape(-1)
+        res = np.empty(flat.size)
+        mag = np.empty(flat.size)
+        tok, row = flat // out, flat % out
+        for t in np.unique(tok):
+            sel = np.flatnonzero(tok == t)
+            o = row[sel]
+            qx, sx = token(int(t))
+            d = raw[o, :, 0:2].copy().view(np.float16).astype(np.float32).reshape(o.size, nb)
+            qw = raw[o, :, 2:].copy().view(np.int8).astype(np.int64)
+            blk = (qw * qx[None]).sum(axis=2)
+            comb = (d * sx[None, :]).astype(np.float32).astype(np.float64)  # d_w*s_x rounded to f32
+            terms = blk * comb
+            res[sel] = terms.sum(axis=1)
+            mag[sel] = np.abs(terms).sum(axis=1)
+        return res, mag
+    return at
+
+
+U32 = 2.0 ** -24  # f32 unit roundoff
+
+
 def assert_parity(got, ref, exact, what, max_frac=1e-3):
-    """n >= 2 bar: |got - ref| <= 2e-6 + 1e-5|ref|, or -- where the reference's
-    own f32 rounding error is comparable to that bar (K = 5760 with outliers:
-    up to 2.9e-6) -- got is as accurate as the reference: its error against
-    the exact value is at most twice the reference's own.  Two f32 sums of the
-    same terms in different orders each carry such an error, on either side of
-    the exact value, so their distance can exceed the bar while both are
-    equally good.  The second clause may carry at most `max_frac` of the
-    outputs."""
+    """n >= 2 bar: |got - ref| <= 2e-6 + 1e-5|ref|.  Where two f32 sums of the
+    same block terms in different orders differ by more than that (the
+    reference's own error reaches 2.9e-6 at K = 5760 with outliers, and sums
+    that cancel -- terms adding up to 15.8 in magnitude for a result of 0.02
+    -- carry errors of a few roundings at the scale of the terms), an output
+    passes the accuracy clause instead if its error against the exact value is
+    at most twice the reference's own, or at most 4 u T, where T is the sum of
+    the block terms' magnitudes and u = 2^-24: the error of four f32 roundings
+    at the size of the terms (the textbook bound for a sum of nb terms is
+    (nb - 1) u T).  At most `max_frac` of the outputs may need the clause.
+    `exact` is the exact product (array; T is then not used) or a function of
+    flat indices returning (exact, T) (exact_at), evaluated only where the
+    first clause fails."""
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float32).astype(np.float64)
-    exact = np.asarray(exact, np.float64).reshape(ref.shape)
     assert got.shape == ref.shape, f"{what}: shape {got.shape} vs {ref.shape}"
     within = np.abs(got - ref) <= TOL_ABS + TOL_REL * np.abs(ref)
-    no_worse = np.abs(got - exact) <= 2.0 * np.abs(ref - exact)
-    bad = ~(within | no_worse)
-    if bad.any():
-        i = int(np.flatnonzero(bad.reshape(-1))[0])
-        raise AssertionError(f"{what}: {int(bad.sum())} of {bad.size} outside tolerance and less accurate than "
-                             f"the reference; first at {i}: got {got.reshape(-1)[i]!r} ref {ref.reshape(-1)[i]!r} "
-                             f"exact {exact.reshape(-1)[i]!r}")
-    frac = float((~within).mean())
-    if frac:
-        print(f"{what}: {int((~within).sum())} outputs beyond the bar, each closer to exact than the reference",
+    idx = np.flatnonzero(~within.reshape(-1))
+    if idx.size:
+        g, r = got.reshape(-1)[idx], ref.reshape(-1)[idx]
+        if callable(exact):
+            e, mag = exact(idx)
+        else:
+            e, mag = np.asarray(exact, np.float64).reshape(-1)[idx], np.zeros(idx.size)
+        err = np.abs(g - e)
+        no_worse = (err <= 2.0 * np.abs(r - e)) | (err <= 4.0 * U32 * mag)
+        if not no_worse.all():
+            i = int(np.flatnonzero(~no_worse)[0])
+            raise AssertionError(f"{what}: {int((~no_worse).sum())} of {ref.size} outside tolerance and less "
+                                 f"accurate than the reference; first at {int(idx[i])}: got {g[i]!r} ref {r[i]!r} "
+                                 f"exact {e[i]!r} (term magnitudes {mag[i]:.4g})")
+        print(f"{what}: {idx.size} outputs beyond the bar, each within the accuracy clause "
+              f"(max error {float(err.max()):.3e}, max of 2|ref - exact| {float(2 * np.abs(r - e).max()):.3e})",
               flush=True)
+    CLAUSE_LOG.append((what, int(idx.size), int(ref.size)))
+    frac = idx.size / ref.size
     assert frac <= max_frac, f"{what}: {frac:.2e} of outputs needed the accuracy clause"
 
 
