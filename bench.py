@@ -9,11 +9,12 @@ after all the others: every step streams its weights from HBM.
 
 Protocol (the same for every rotating figure below):
   * an eager pass over all copies, then one graph of --warmup steps;
-  * T >= 5 trials; each captures the next --steps launches of the rotation
-    into a graph and times exactly those steps with HIP events on the
-    library's stream, after an untimed "filler" graph (the next max(steps,
-    R) launches) that keeps the GPU busy while the timed graph is submitted,
-    so host submission never shows in the timed region;
+  * T >= 5 trials; each captures into one graph an untimed "filler" (the
+    next max(steps, R) launches of the rotation), then exactly --steps
+    launches between two event nodes, and times those steps with the events
+    (HIP events on the library's stream, recorded inside the graph): the
+    timed kernels run back to back in the middle of one graph, so neither
+    host submission nor a graph boundary shows in the timed region;
   * the figure is the median over the trials (all trials are reported).
 `value` is the GEMV's HBM throughput: algorithmic bytes (M*K/32*34 + 4K + 4M
 per step) / median time per step.
@@ -92,19 +93,19 @@ def rotating_trials(gpu, launch, copies: int, steps: int, warmup: int, trials: i
     copy i (mod copies).  Returns ms per step of each trial."""
     pos = 0
 
-    def graph_of(count):
+    def record(count):
         nonlocal pos
-        gpu.graph_begin()
         for _ in range(count):
             launch(pos % copies)
             pos += 1
-        return gpu.graph_end()
 
     for i in range(copies):  # eager: workspaces grown, every copy touched once
         launch(i)
     gpu.sync()
     if warmup:
-        g = graph_of(warmup)
+        gpu.graph_begin()
+        record(warmup)
+        g = gpu.graph_end()
         gpu.graph_launch(g)
         gpu.sync()
         gpu.graph_destroy(g)
@@ -112,16 +113,18 @@ def rotating_trials(gpu, launch, copies: int, steps: int, warmup: int, trials: i
     out = []
     e0, e1 = gpu.event(), gpu.event()
     for _ in range(trials):
-        gf = graph_of(filler)
-        gt = graph_of(steps)
-        gpu.graph_launch(gf)
+        # one graph: the filler launches, then the timed steps between two
+        # event nodes, so no graph boundary or host submission is timed
+        gpu.graph_begin()
+        record(filler)
         gpu.record(e0)
-        gpu.graph_launch(gt)
+        record(steps)
         gpu.record(e1)
+        g = gpu.graph_end()
+        gpu.graph_launch(g)
         ms = gpu.elapsed_ms(e0, e1)
         gpu.sync()
-        gpu.graph_destroy(gf)
-        gpu.graph_destroy(gt)
+        gpu.graph_destroy(g)
         out.append(ms / steps)
     gpu.destroy_event(e0)
     gpu.destroy_event(e1)

@@ -309,6 +309,8 @@ int q8_tactic_row(int i, q8_tactic *tactic, int *rank, int *maturity);
 /* ---- timing and graphs (cuEvent* / cuGraph*, sys.rs:76-123) ---- */
 
 int q8_event_create(q8_ctx *ctx, void **event);
+/* Records on the context's stream; while the stream is being captured the
+ * record becomes an event node of the graph (hipEventRecordExternal). */
 int q8_event_record(q8_ctx *ctx, void *event);
 /* Waits for `end`, then returns the milliseconds between the two. */
 int q8_event_elapsed_ms(void *start, void *end, float *ms);

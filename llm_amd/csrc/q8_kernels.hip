@@ -729,7 +729,14 @@ Q8_GEMV_KERNEL(9, 1, 512)
 // adds the row's block values left to right (chain_row).  The output is
 // therefore bit-identical to q8_gemv1_*_e1 and to dot_q8_0's AVX2 path
 // (quant.rs:54-78), with the optional residual added last.
-template <int RS, int NL, int CMB = 0>
+//
+// EX = 0 keeps every block value bit-identical but sums them in a fixed tree
+// instead of left to right: each lane adds its NL block values in order, the
+// lanes of a row (one per load slot j) meet by xor shuffles in a fixed order,
+// and wave 0 adds the waves' row sums in wave order.  Deterministic, within
+// f32 rounding of the reference's left-to-right sum, and it drops the
+// serial 72-add chain and its LDS round trips from the end of the kernel.
+template <int RS, int NL, int CMB = 0, int EX = 1>
 static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
     extern __shared__ __attribute__((aligned(16))) float smem[];
     constexpr int LPB = 2 * RS;               // lanes per block
@@ -806,7 +813,7 @@ static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
 
     // zero each row's tail up to a multiple of four blocks (chain_row reads
     // whole float4s)
-    if (wave == 0 && lane < RS) {
+    if (EX && wave == 0 && lane < RS) {
         for (int b = nb; b < ((nb + 3) & ~3); b++) vbuf[r * vrow + b] = 0.0f;
     }
     if constexpr (CMB) {
@@ -831,6 +838,7 @@ static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
+    float lsum = 0.0f;  // EX = 0: this lane's block values, in load order
 #pragma unroll
     for (int i = 0; i < NL; i++) {
         const int bu = b_begin + i * BPL + j;
@@ -847,11 +855,30 @@ static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
             s01 = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
         }
         const float v = f16_to_f32(dd[i]) * s01;
-        *((h == 0 && bu < b_end) ? vbuf + r * vrow + bu : pad) = v;
+        if constexpr (EX) {
+            *((h == 0 && bu < b_end) ? vbuf + r * vrow + bu : pad) = v;
+        } else {
+            lsum = bu < b_end ? lsum + v : lsum;
+        }
+    }
+    if constexpr (!EX) {
+        // the BPL lanes of row r (load slots j) in a fixed order: xor 16
+        // then xor 32 (RS = 8), xor 32 (RS = 16); both halves h hold the
+        // same sums, lane r (j = 0, h = 0) keeps the wave's row sum
+        if constexpr (BPL >= 4) lsum = lsum + __shfl_xor(lsum, 16);
+        if constexpr (BPL >= 2) lsum = lsum + __shfl_xor(lsum, 32);
+        if (lane < RS) vbuf[wave * RS + r] = lsum;
     }
     __syncthreads();
     if (wave != 0 || lane >= RS) return;
-    const float acc = chain_row(vbuf + r * vrow, nb);
+    float acc;
+    if constexpr (EX) {
+        acc = chain_row(vbuf + r * vrow, nb);
+    } else {
+        const int nw = (int)(blockDim.x >> 6);
+        acc = vbuf[r];
+        for (int w2 = 1; w2 < nw; w2++) acc = acc + vbuf[w2 * RS + r];
+    }
     const int row = tile * Q8_TILE_ROWS + srow;
     if (row < mrows) my[row] = mbias ? acc + mbias[row] : acc;
 }
@@ -862,6 +889,12 @@ static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
     }                                                                                                  \
     extern "C" __global__ __launch_bounds__(1024) void q8_gemv_rc##RS##_l##NL(Q8GemvArgs a) { \
         gemv_rs_body<RS, NL, 1>(a);                                                                    \
+    }                                                                                                  \
+    extern "C" __global__ __launch_bounds__(1024) void q8_gemv_r##RS##_l##NL##_e0(Q8GemvArgs a) { \
+        gemv_rs_body<RS, NL, 0, 0>(a);                                                                 \
+    }                                                                                                  \
+    extern "C" __global__ __launch_bounds__(1024) void q8_gemv_rc##RS##_l##NL##_e0(Q8GemvArgs a) { \
+        gemv_rs_body<RS, NL, 1, 0>(a);                                                                 \
     }
 Q8_GEMV_RS_KERNEL(8, 3)
 Q8_GEMV_RS_KERNEL(8, 6)

@@ -73,6 +73,8 @@ enum Fn {
     F_GEMVC_2_0, F_GEMVC_2_1, F_GEMVC_3_0, F_GEMVC_3_1, F_GEMVC_5_0, F_GEMVC_5_1, F_GEMVC_9_0, F_GEMVC_9_1,
     F_GEMV_R8_3, F_GEMV_R8_6, F_GEMV_R16_3, F_GEMV_R16_6,
     F_GEMV_RC8_3, F_GEMV_RC8_6, F_GEMV_RC16_3, F_GEMV_RC16_6,
+    F_GEMV_R8_3_E0, F_GEMV_R8_6_E0, F_GEMV_R16_3_E0, F_GEMV_R16_6_E0,
+    F_GEMV_RC8_3_E0, F_GEMV_RC8_6_E0, F_GEMV_RC16_3_E0, F_GEMV_RC16_6_E0,
     F_QUANTIZE,
     F_GEMM_S0_T1, F_GEMM_S1_T1, F_GEMM_S1_T2, F_GEMM_S1_T4,
     F_GEMM_H_T1_R4, F_GEMM_H_T2_R2, F_GEMM_H_T2_R4,
@@ -99,6 +101,8 @@ const char *const kFnNames[F_COUNT] = {
     "q8_gemvc_pb5_e0", "q8_gemvc_pb5_e1", "q8_gemvc_pb9_e0", "q8_gemvc_pb9_e1",
     "q8_gemv_r8_l3", "q8_gemv_r8_l6", "q8_gemv_r16_l3", "q8_gemv_r16_l6",
     "q8_gemv_rc8_l3", "q8_gemv_rc8_l6", "q8_gemv_rc16_l3", "q8_gemv_rc16_l6",
+    "q8_gemv_r8_l3_e0", "q8_gemv_r8_l6_e0", "q8_gemv_r16_l3_e0", "q8_gemv_r16_l6_e0",
+    "q8_gemv_rc8_l3_e0", "q8_gemv_rc8_l6_e0", "q8_gemv_rc16_l3_e0", "q8_gemv_rc16_l6_e0",
     "q8_quantize",
     "q8_gemm_s0_t1", "q8_gemm_s1_t1", "q8_gemm_s1_t2", "q8_gemm_s1_t4",
     "q8_gemm_h_t1_r4", "q8_gemm_h_t2_r2", "q8_gemm_h_t2_r4",
@@ -285,7 +289,7 @@ q8_tactic plan(q8_ctx *c, int n, int out, int k, int slots = 1, int fmt = -1) {
         const int pb = option(c, "gemv.pairs", -1);
         if (pb > 0) t.pairs_per_batch = pb;
         // the tile kernel's own switches select the tile kernel
-        if (w > 0 || sl > 0 || pb > 0 || !t.exact || t.kslices != 1) {
+        if (w > 0 || sl > 0 || pb > 0 || t.kslices != 1) {
             t.row_slice = Q8_TILE_ROWS;
             t.slice_loads = 0;
         }
@@ -392,7 +396,7 @@ struct GemvCombine {
 // than 16 waves, or the combine more splits than it holds, so the caller
 // keeps the tile kernel.
 int run_gemv_rs(q8_ctx *c, const q8_weight *w, float *y, q8_dptr x, const float *bias, int rs, int nl,
-                const GemvCombine *comb) {
+                const GemvCombine *comb, int exact) {
     const int nb = w->nb;
     const int bpw = nl * (64 / (2 * rs));
     const int waves = (int)ceil_div(nb, bpw);
@@ -420,7 +424,7 @@ int run_gemv_rs(q8_ctx *c, const q8_weight *w, float *y, q8_dptr x, const float 
     if (grid > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "gemv: grid of %lld workgroups", grid);
     const unsigned lds = (unsigned)((nb * 32 + rs * Q8_GEMV_VROW(nb) + Q8_GEMV_PAD_FLOATS) * 4);
     const int fi = (rs == 8 ? 0 : 2) + (nl == 3 ? 0 : 1);
-    const Fn f = (Fn)((comb ? F_GEMV_RC8_3 : F_GEMV_R8_3) + fi);
+    const Fn f = (Fn)((exact ? (comb ? F_GEMV_RC8_3 : F_GEMV_R8_3) : (comb ? F_GEMV_RC8_3_E0 : F_GEMV_R8_3_E0)) + fi);
     return launch(c, f, (unsigned)grid, (unsigned)(waves * 64), lds, &a, sizeof a);
 }
 
@@ -449,9 +453,8 @@ int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const floa
     }
     const int slots = silu ? 2 : 1;
     const q8_tactic t = plan(c, 1, silu ? m[0].w->out : rows_total, k, slots);
-    if (count == 1 && !silu && !norm_w && !rope && t.exact && t.kslices == 1 &&
-        (t.row_slice == 8 || t.row_slice == 16)) {
-        const int rc = run_gemv_rs(c, m[0].w, m[0].y, x, bias, t.row_slice, t.slice_loads, comb);
+    if (count == 1 && !silu && !norm_w && !rope && t.kslices == 1 && (t.row_slice == 8 || t.row_slice == 16)) {
+        const int rc = run_gemv_rs(c, m[0].w, m[0].y, x, bias, t.row_slice, t.slice_loads, comb, t.exact);
         if (rc != Q8_ERR_UNSUPPORTED) return rc;
     }
     if (t.pairs_per_wave > 12)
@@ -1987,7 +1990,14 @@ int q8_event_create(q8_ctx *c, void **ev) {
 
 int q8_event_record(q8_ctx *c, void *ev) {
     if (!c || !ev) return fail(Q8_ERR_INVALID, "q8_event_record: bad arguments");
-    HIP_TRY(hipEventRecord((hipEvent_t)ev, c->stream), "hipEventRecord");
+    // during capture the record becomes an event node of the graph (timing
+    // inside one graph, with no graph boundary in the timed region)
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    HIP_TRY(hipStreamIsCapturing(c->stream, &st), "hipStreamIsCapturing");
+    if (st == hipStreamCaptureStatusActive)
+        HIP_TRY(hipEventRecordWithFlags((hipEvent_t)ev, c->stream, hipEventRecordExternal), "hipEventRecordWithFlags");
+    else
+        HIP_TRY(hipEventRecord((hipEvent_t)ev, c->stream), "hipEventRecord");
     return Q8_OK;
 }
 
