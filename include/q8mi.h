@@ -179,6 +179,27 @@ int q8_weight_export(q8_ctx *ctx, const q8_weight *weight, void *gguf_bytes, siz
 int q8_matmul(q8_ctx *ctx, const q8_weight *weight, q8_dptr x, size_t x_offset, int n, q8_dptr y,
               size_t y_offset, const q8_prepared *prepared, q8_dptr bias, size_t bias_offset);
 
+/* The scratch of q8_matmul_noalloc: a static device array of this size on
+ * each GPU the library runs on, held until the process ends. */
+#define Q8_NOALLOC_SCRATCH_BYTES (8u << 20)
+
+/* q8_matmul (above) without allocating: no counterpart in the reference.  For
+ * callers that cannot allocate device memory -- code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc: this entry point calls
+ * no hipMalloc, hipFree or allocating library routine.  The caller passes a
+ * resident weight and its own x, y and bias; n >= 2 quantizes x into the
+ * static array of Q8_NOALLOC_SCRATCH_BYTES (int8 units, at most
+ * ceil(n/32) * (k/32) * 1152 bytes: n = 1024 at k = 5760 fits, larger shapes are
+ * Q8_ERR_UNSUPPORTED), and the GEMM keeps every block of a row tile in one
+ * workgroup (no split-K partials).  n == 1 runs the GEMV, which needs no
+ * scratch (Q8_ERR_UNSUPPORTED if its K would be split).  Results equal
+ * q8_matmul's within the n >= 2 parity bar (bit-identical where q8_matmul
+ * does not split K).  Every call on one GPU shares that GPU's array, which
+ * keeps the last call's bytes (each call rewrites all it reads); calls that
+ * overlap on one GPU (several streams or processes) race on it. */
+int q8_matmul_noalloc(q8_ctx *ctx, const q8_weight *weight, q8_dptr x, size_t x_offset, int n, q8_dptr y,
+                      size_t y_offset, q8_dptr bias, size_t bias_offset);
+
 /* Quantize n rows of k f32 activations once for several matmuls:
  * Gpu::prepare (cuda/mod.rs:1381-1410) / Compute::prepare (compute.rs:376-395). */
 int q8_prepare(q8_ctx *ctx, q8_dptr x, size_t x_offset, int n, int k, q8_prepared *out);

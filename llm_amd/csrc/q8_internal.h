@@ -14,6 +14,9 @@ __attribute__((visibility("hidden"))) unsigned long long workspace_generation(co
 // Positions one chunk of the split decode attention kernel covers: a split of
 // about this many positions is one pass over its keys.
 __attribute__((visibility("hidden"))) int attention_split_rows();
+// The device address of q8_matmul_noalloc's static scratch on `device`, which
+// must be the current device (q8_noalloc.hip); status code.
+__attribute__((visibility("hidden"))) int noalloc_scratch(int device, void **out);
 }  // namespace q8i
 
 #endif

@@ -167,6 +167,7 @@ struct q8_ctx {
     size_t norm_ws_bytes = 0;
     void *argmax_ws = nullptr;           // per-workgroup partials + result
     unsigned *probe_sink = nullptr;      // the measurement kernels' never-written result slot
+    void *noalloc = nullptr;             // this device's static scratch of q8_matmul_noalloc (not owned)
     float *split_ws = nullptr;           // partial results of split-K workgroups
     unsigned *counters = nullptr;        // split-K arrival counters (kernels reset them to 0)
     void *token_ws = nullptr;            // token ids of the embedding lookup
@@ -626,8 +627,10 @@ void set_gemm_rope(Q8GemmArgs &a, const GemvRope *rope) {
     a.capacity = rope->capacity;
 }
 
+// no_split: keep every block of a row tile in one workgroup (no partial
+// results or arrival counters in the context's split scratch).
 int run_gemm(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n, const float *bias,
-             const GemvRope *rope = nullptr) {
+             const GemvRope *rope = nullptr, bool no_split = false) {
     if (p->format == Q8_PREPARED_F16) return run_gemm_h(c, m, count, p, n, bias, rope);
     if (p->format != Q8_PREPARED_I8) return fail(Q8_ERR_INVALID, "prepared activations: unknown format %d", p->format);
     {
@@ -651,7 +654,11 @@ int run_gemm(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n,
         rt += m[i].w->tiles;
         rows_total += m[i].w->out;
     }
-    const q8_tactic t = plan(c, n, rows_total, k, 1, Q8_PREPARED_I8);
+    q8_tactic t = plan(c, n, rows_total, k, 1, Q8_PREPARED_I8);
+    if (no_split && t.kslices > 1) {
+        t.kslices = 1;
+        t.pairs_per_wave = (int)ceil_div((nb + 1) / 2, std::max(1, t.kwaves));
+    }
     a.total_rtiles = rt;
     a.xq = reinterpret_cast<const uint8_t *>(p->quants);
     a.xs = reinterpret_cast<const float *>(p->scales);
@@ -665,8 +672,8 @@ int run_gemm(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n,
     a.pairs_per_slice = (int)ceil_div((nb + 1) / 2, a.kslices);
     a.pairs_per_wave = std::max(1, t.pairs_per_wave);
     const int kwaves = std::max(1, t.kwaves);
-    a.scratch = c->split_ws;
-    a.counters = c->counters;
+    a.scratch = no_split ? nullptr : c->split_ws;
+    a.counters = no_split ? nullptr : c->counters;
     set_gemm_rope(a, rope);
     const long long groups = (long long)rt * a.tgroups;
     if (a.kslices > 1) {
@@ -743,19 +750,30 @@ int run_gemm_h(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int 
     return launch(c, f, (unsigned)nwg, (unsigned)(64 * rw * kw), lds, &a, sizeof a);
 }
 
-int prepare_into(q8_ctx *c, q8_dptr x, q8_dptr gate, q8_dptr up, int n, int k, q8_prepared *out) {
+// Bytes of prepared activations for n tokens of k in format fmt: the units
+// (padded to kAlign) then the f32 scales.
+size_t prepared_bytes(int n, int k, int fmt, size_t *qbytes_out) {
+    const long long ttiles = ceil_div(n, 32);
+    const size_t qbytes =
+        (size_t)ttiles * (k / 32) * (fmt == Q8_PREPARED_F16 ? Q8_UNIT_F16_BYTES : Q8_UNIT_BYTES);
+    if (qbytes_out) *qbytes_out = qbytes;
+    return align_up(qbytes, kAlign) + (size_t)ttiles * (k / 32) * Q8_TILE_TOKENS * sizeof(float);
+}
+
+// q8_quantize of x (or of silu(gate) * up) into prepared activations at
+// `base` (prepared_bytes(n, k, fmt) bytes).
+int run_quantize(q8_ctx *c, q8_dptr x, q8_dptr gate, q8_dptr up, int n, int k, int fmt, void *base,
+                 q8_prepared *out) {
     const int nb = k / 32;
     const long long ttiles = ceil_div(n, 32);
-    const int fmt = prepared_format(c, n);
-    const size_t qbytes = (size_t)ttiles * nb * (fmt == Q8_PREPARED_F16 ? Q8_UNIT_F16_BYTES : Q8_UNIT_BYTES);
-    const size_t sbytes = (size_t)ttiles * nb * Q8_TILE_TOKENS * sizeof(float);
-    Q8_TRY(grow(c, &c->act_ws, &c->act_ws_bytes, align_up(qbytes, kAlign) + sbytes, "hipMalloc(activation)"));
+    size_t qbytes = 0;
+    prepared_bytes(n, k, fmt, &qbytes);
     Q8QuantArgs a{};
     a.x = reinterpret_cast<const float *>(x);
     a.gate = reinterpret_cast<const float *>(gate);
     a.up = reinterpret_cast<const float *>(up);
-    a.xq = static_cast<uint8_t *>(c->act_ws);
-    a.xs = reinterpret_cast<float *>(static_cast<uint8_t *>(c->act_ws) + align_up(qbytes, kAlign));
+    a.xq = static_cast<uint8_t *>(base);
+    a.xs = reinterpret_cast<float *>(static_cast<uint8_t *>(base) + align_up(qbytes, kAlign));
     a.n = n;
     a.nb = nb;
     a.ttiles = (int)ttiles;
@@ -770,6 +788,12 @@ int prepare_into(q8_ctx *c, q8_dptr x, q8_dptr gate, q8_dptr up, int n, int k, q
     out->k = k;
     out->format = fmt;
     return Q8_OK;
+}
+
+int prepare_into(q8_ctx *c, q8_dptr x, q8_dptr gate, q8_dptr up, int n, int k, q8_prepared *out) {
+    const int fmt = prepared_format(c, n);
+    Q8_TRY(grow(c, &c->act_ws, &c->act_ws_bytes, prepared_bytes(n, k, fmt, nullptr), "hipMalloc(activation)"));
+    return run_quantize(c, x, gate, up, n, k, fmt, c->act_ws, out);
 }
 
 // Gpu::plain (cuda/mod.rs, used by rmsnorm_prepare 1414-1445): an f32 vector
@@ -952,6 +976,8 @@ int q8_open(int device, q8_ctx **out) {
         if (he != hipSuccess) { rc = hip_fail(he, "hipMalloc(argmax)"); break; }
         he = hipMalloc((void **)&c->probe_sink, 256);
         if (he != hipSuccess) { rc = hip_fail(he, "hipMalloc(probe sink)"); break; }
+        rc = q8i::noalloc_scratch(device, &c->noalloc);  // the device is current (hipSetDevice above)
+        if (rc != Q8_OK) break;
         he = hipMalloc((void **)&c->split_ws, kSplitBytes);
         if (he != hipSuccess) { rc = hip_fail(he, "hipMalloc(split scratch)"); break; }
         he = hipMalloc((void **)&c->counters, kCounters * sizeof(unsigned));
@@ -1313,6 +1339,38 @@ int q8_matmul(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset, int n, 
         prepared = &own;
     }
     return q8_matmul_prompt_group(c, &e, 1, prepared, n, w->k, bias, bias_offset);
+}
+
+int q8_matmul_noalloc(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset, int n, q8_dptr y,
+                      size_t y_offset, q8_dptr bias, size_t bias_offset) {
+    if (!c) return fail(Q8_ERR_INVALID, "q8_matmul_noalloc: null context");
+    Q8_TRY(check_weight(c, w));
+    Q8_TRY(check_n(n));
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    const int k = w->k;
+    if (n == 1) {
+        // the GEMV reads x and writes y only, unless K is split over workgroups
+        if (plan(c, 1, w->out, k, 1).kslices != 1)
+            return fail(Q8_ERR_UNSUPPORTED, "q8_matmul_noalloc: the %d x %d GEMV splits K over workgroups, which "
+                                            "needs scratch", w->out, k);
+        q8_group_entry e{w, y, y_offset};
+        return q8_matmul_decode_group(c, &e, 1, x, x_offset, k, bias, bias_offset);
+    }
+    if (!c->noalloc) return fail(Q8_ERR_NO_DEVICE, "q8_matmul_noalloc: no device scratch");
+    const size_t need = prepared_bytes(n, k, Q8_PREPARED_I8, nullptr);
+    if (need > Q8_NOALLOC_SCRATCH_BYTES)
+        return fail(Q8_ERR_UNSUPPORTED, "q8_matmul_noalloc: %d tokens of k = %d need %zu bytes of quantized "
+                                        "activations, more than the %u-byte scratch", n, k, need,
+                    (unsigned)Q8_NOALLOC_SCRATCH_BYTES);
+    const q8_dptr xp = (q8_dptr)(uintptr_t)fptr(x, x_offset);
+    Q8_TRY(check_span(c, xp, (size_t)n * k * 4, "noalloc x"));
+    Member m{w, fptr(y, y_offset)};
+    Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)m.y, (size_t)n * w->out * 4, "noalloc y"));
+    const float *b = fptr(bias, bias_offset);
+    if (b) Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)b, (size_t)n * w->out * 4, "noalloc bias"));
+    q8_prepared p{};
+    Q8_TRY(run_quantize(c, xp, 0, 0, n, k, Q8_PREPARED_I8, c->noalloc, &p));
+    return run_gemm(c, &m, 1, &p, n, b, nullptr, true);
 }
 
 int q8_gate_up_silu(q8_ctx *c, const q8_weight *gate, const q8_weight *up, q8_dptr x, size_t x_offset, int n,
