@@ -149,7 +149,13 @@ typedef struct {
 enum { Q8_DEC_Q = 0, Q8_DEC_K, Q8_DEC_V, Q8_DEC_O, Q8_DEC_GATE, Q8_DEC_UP, Q8_DEC_DOWN };
 
 /* Random-init weights on the device (q8_weight_synthetic, one seed per
- * matrix), norm weights near 1, an f16 KV cache of `capacity` positions. */
+ * matrix), norm weights near 1, an f16 KV cache of `capacity` positions.
+ * Creation also plans the context's workspaces for the decoder's largest
+ * pass (q8_workspace_plan: max_batch tokens, the widest row, every attention
+ * split count up to `capacity`), builds the rotation table, makes the norm
+ * weights resident and reserves the pinned token buffer of q8_decoder_generate,
+ * as the reference's Workspace is sized once per context (workspace.rs:171-342):
+ * forwards and steps within the configuration allocate nothing. */
 int q8_decoder_create_synthetic(q8_ctx *ctx, const q8_decoder_config *config, uint64_t seed, q8_decoder **out);
 void q8_decoder_destroy(q8_decoder *dec);
 /* Empty the cache: the next forward starts at position 0 (KvCache::reset). */
@@ -176,6 +182,14 @@ int q8_decoder_logits(q8_decoder *dec, float *host, size_t len);
  * layer < 0 the output norm (host pointer of n_embd floats). */
 int q8_decoder_weight(const q8_decoder *dec, int layer, int which, const q8_weight **weight);
 int q8_decoder_norm(const q8_decoder *dec, int layer, int which, const float **weight);
+
+/* Graph bookkeeping of a decoder: graphs held now, captured and dropped
+ * since creation, and passes run eagerly (the first of each shape).  A
+ * dropped graph means a workspace moved under it. */
+typedef struct {
+    int graphs, captured, dropped, eager;
+} q8_decoder_stats;
+int q8_decoder_graph_stats(const q8_decoder *dec, q8_decoder_stats *stats);
 
 #ifdef __cplusplus
 }

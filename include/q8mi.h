@@ -153,6 +153,38 @@ int q8_upload(q8_ctx *ctx, q8_dptr dst, const void *src, size_t bytes);
 int q8_download(q8_ctx *ctx, void *dst, q8_dptr src, size_t bytes);
 int q8_sync(q8_ctx *ctx);
 
+/* ---- workspace plan: BufferPlan / scratch_requests (apps/engine/src/workspace.rs:63-106, 171-342) ----
+ * The context's per-call workspaces (prepared activations, the fused
+ * feed-forward's second activation and f32 products, the norm row, token
+ * ids, decode attention partials and output) grow on demand.  A caller that
+ * knows the largest shapes it will serve plans them once: every workspace
+ * gets a region of one device allocation, each as large as the shape needs
+ * (or as it already is, if larger), and no call within the shape allocates
+ * again.  A plan the current workspaces already cover changes nothing.  The
+ * reference overlaps regions whose phases never meet; here they are
+ * disjoint, so any order of calls is safe.  Planning moves workspaces when
+ * it allocates: graphs captured before must be dropped (the generation in
+ * q8_workspace_info changes). */
+typedef struct {
+    int max_tokens;  /* most tokens of any call, 1..Q8_MAX_TOKENS */
+    int max_k;       /* longest activation row: the widest weight k, attention heads x 64, norm width */
+    int max_ff;      /* width of the fused gate/up calls (0: none) */
+    int attn_heads;  /* query heads of the decode attention calls (0: none) */
+    int attn_splits; /* most splits those calls use (0 or 1: unsplit) */
+    int rope_n_rot;  /* rotation table built now (RopeTable::new, ops.rs:121-131); 0: none */
+    float rope_base;
+} q8_workspace_shape;
+typedef struct {
+    uint64_t bytes;       /* device bytes the workspaces hold */
+    uint64_t arena_bytes; /* of which in the planned allocation */
+    uint64_t allocations; /* device allocations this context has made since q8_open */
+    uint64_t generation;  /* changes whenever a workspace moves */
+    int regions;          /* regions of the plan (q8_workspace_region) */
+} q8_workspace_info;
+int q8_workspace_plan(q8_ctx *ctx, const q8_workspace_shape *shape);
+int q8_workspace_query(q8_ctx *ctx, q8_workspace_info *info);
+int q8_workspace_region(q8_ctx *ctx, int index, const char **name, uint64_t *offset, uint64_t *bytes);
+
 /* ---- weight residency: Gpu::quantized / reserve (cuda/mod.rs:1758-1790) ----
  * Uploads GGUF Q8_0 bytes (`out` rows of k/32 blocks of 34 bytes) once and
  * repacks them on the device into the tile layout; cached by the host
@@ -224,6 +256,9 @@ int q8_rmsnorm(q8_ctx *ctx, q8_dptr x, size_t x_offset, const float *weight, int
  * move; this is the counterpart of q8_weight_release for callers whose host
  * vectors do.  A vector that is not resident is a no-op. */
 int q8_vector_release(q8_ctx *ctx, const float *weight, size_t k);
+/* Makes a host vector resident now rather than on first use (Gpu::plain's
+ * upload, cuda/mod.rs:1414-1445), so a planned token path allocates nothing. */
+int q8_vector_resident(q8_ctx *ctx, const float *weight, size_t k);
 /* prepare(rmsnorm(x)) in one pass, the f32 norm never written
  * (Gpu::rmsnorm_prepare, cuda/mod.rs:1414-1445; Compute::norm_prepare,
  * compute.rs:959-984, whose below-threshold f32 branch is q8_rmsnorm).

@@ -14,10 +14,11 @@
 // and the greedy argmax, written to the token slot the next step embeds.
 //
 // Graphs: a pass of shape (n, attention splits) runs eagerly the first time
-// (it grows the context's workspaces and makes the norm weights resident) and
-// is captured into a graph the next time; replays read the position from
-// device memory.  A captured graph is dropped when the context reallocates a
-// workspace (its pointers would be stale).
+// and is captured into a graph the next time; replays read the position from
+// device memory.  Creation plans every workspace a pass uses, so passes
+// allocate nothing; a captured graph is still dropped if the context's
+// workspaces move (another caller of the context grew one), since its
+// pointers would be stale.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -81,6 +82,7 @@ struct q8_decoder {
     uint32_t *pinned = nullptr;  // generate(): tokens read back without a wait per step
     int pinned_len = 0;
     std::vector<q8_dptr> buffers;
+    int captured = 0, dropped = 0, eager = 0;
 
     int alloc(size_t bytes, q8_dptr *p) {
         DEC_TRY(q8_alloc(c, bytes, p));
@@ -89,8 +91,10 @@ struct q8_decoder {
     }
     void drop_graphs() {
         for (auto &g : graphs) q8_graph_destroy(g.second);
+        dropped += (int)graphs.size();
         graphs.clear();
     }
+    int plan();
     int splits_for(int visible) const {
         // one workgroup per head while the positions fit one chunk of the
         // split kernel; beyond, a split per chunk, up to the eight the output
@@ -180,6 +184,7 @@ int q8_decoder::run(int n, int splits) {
     auto it = graphs.find(key);
     if (it != graphs.end()) return q8_graph_launch(c, it->second);
     if (runs[key]++ == 0) {
+        eager++;
         const int rc = body(n, splits);
         sync_generation();  // the eager run may have grown workspaces under older graphs
         return rc;
@@ -198,7 +203,38 @@ int q8_decoder::run(int n, int splits) {
         return set_error(Q8_ERR_HIP, "decoder: a workspace grew during capture");
     }
     graphs[key] = graph;
+    captured++;
     return q8_graph_launch(c, graph);
+}
+
+// Everything a pass may allocate, allocated now (Workspace sizing per
+// context, workspace.rs:171-342): the workspaces for max_batch tokens and
+// the widest row, the attention partials for the most splits any position
+// up to `capacity` uses, the rotation table, the resident norm weights, and
+// the pinned buffer generate() reads tokens into.
+int q8_decoder::plan() {
+    const q8_decoder_config &g = cfg;
+    q8_workspace_shape s{};
+    s.max_tokens = g.max_batch;
+    s.max_k = std::max(std::max(g.n_embd, g.n_ff), g.n_head * g.head_dim);
+    s.max_ff = g.n_ff;
+    s.attn_heads = g.n_head;
+    s.attn_splits = splits_for(g.capacity);  // splits grow with the visible positions
+    s.rope_n_rot = g.n_rot;
+    s.rope_base = g.rope_base;
+    DEC_TRY(q8_workspace_plan(c, &s));
+    for (Layer &L : layers) {
+        DEC_TRY(q8_vector_resident(c, L.attn_norm.data(), L.attn_norm.size()));
+        DEC_TRY(q8_vector_resident(c, L.ffn_norm.data(), L.ffn_norm.size()));
+    }
+    DEC_TRY(q8_vector_resident(c, output_norm.data(), output_norm.size()));
+    if (hipHostMalloc((void **)&pinned, (size_t)g.capacity * 4, 0) != hipSuccess) {
+        pinned = nullptr;
+        return set_error(Q8_ERR_OUT_OF_MEMORY, "hipHostMalloc(%d tokens)", g.capacity);
+    }
+    pinned_len = g.capacity;
+    generation = q8i::workspace_generation(c);
+    return Q8_OK;
 }
 
 extern "C" {
@@ -240,7 +276,7 @@ int q8_decoder_create_synthetic(q8_ctx *c, const q8_decoder_config *config, uint
         (rc = d->alloc((size_t)B * g.n_ff * f, &d->act)) || (rc = d->alloc((size_t)g.n_vocab * f, &d->logits)) ||
         (rc = d->alloc(256, &d->pos)) || (rc = d->alloc((size_t)B * 4, &d->tokens)))
         return fail(rc);
-    if ((rc = q8_decoder_reset(d))) return fail(rc);
+    if ((rc = d->plan()) || (rc = q8_decoder_reset(d))) return fail(rc);
     *out = d;
     return Q8_OK;
 }
@@ -303,14 +339,9 @@ int q8_decoder_generate(q8_decoder *d, int steps, uint32_t *out) {
     if (d->position + steps > d->cfg.capacity)
         return set_error(Q8_ERR_UNSUPPORTED, "context full: %d of %d tokens used", d->position + steps,
                          d->cfg.capacity);
-    if (d->pinned_len < steps) {
-        if (d->pinned) (void)hipHostFree(d->pinned);
-        d->pinned = nullptr;
-        d->pinned_len = 0;
-        if (hipHostMalloc((void **)&d->pinned, (size_t)steps * 4, 0) != hipSuccess)
-            return set_error(Q8_ERR_OUT_OF_MEMORY, "hipHostMalloc(%d tokens)", steps);
-        d->pinned_len = steps;
-    }
+    if (d->pinned_len < steps)  // reserved for the whole context at creation
+        return set_error(Q8_ERR_INVALID, "generate: %d steps exceed the %d-token pinned buffer", steps,
+                         d->pinned_len);
     // one split count for the whole run, sized for its last step
     const int splits = d->splits_for(d->position + steps);
     hipStream_t stream = (hipStream_t)q8_stream(d->c);
@@ -342,6 +373,15 @@ int q8_decoder_weight(const q8_decoder *d, int layer, int which, const q8_weight
     if (layer >= (int)d->layers.size() || which < 0 || which > Q8_DEC_DOWN)
         return set_error(Q8_ERR_INVALID, "decoder weight (%d, %d) out of range", layer, which);
     *weight = d->layers[layer].w[which];
+    return Q8_OK;
+}
+
+int q8_decoder_graph_stats(const q8_decoder *d, q8_decoder_stats *stats) {
+    if (!d || !stats) return set_error(Q8_ERR_INVALID, "q8_decoder_graph_stats: bad arguments");
+    stats->graphs = (int)d->graphs.size();
+    stats->captured = d->captured;
+    stats->dropped = d->dropped;
+    stats->eager = d->eager;
     return Q8_OK;
 }
 

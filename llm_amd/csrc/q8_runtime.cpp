@@ -178,6 +178,14 @@ struct q8_ctx {
     size_t attn_out_ws_bytes = 0;
     std::vector<q8_weight *> owned;      // weights generated on the device (no host identity)
     unsigned long long ws_generation = 0; // bumped whenever a workspace is reallocated
+    unsigned long long allocations = 0;   // device allocations made through dev_malloc
+    void *arena = nullptr;                // one allocation holding every planned workspace
+    size_t arena_bytes = 0;
+    struct Region {
+        const char *name;
+        size_t offset, bytes;
+    };
+    std::vector<Region> regions;          // the arena's layout, as planned
     int cu_count = 0;
     size_t total_mem = 0;
     size_t max_lds = 0;
@@ -220,17 +228,33 @@ int launch(q8_ctx *c, Fn f, unsigned grid, unsigned block, unsigned lds, void *a
     return Q8_OK;
 }
 
+// Every device allocation of the context goes through here and is counted
+// (q8_workspace_query): a caller that planned its workspaces can check that
+// its token path allocates nothing.
+hipError_t dev_malloc(q8_ctx *c, void **p, size_t bytes) {
+    const hipError_t e = hipMalloc(p, bytes);
+    if (e == hipSuccess) c->allocations++;
+    return e;
+}
+
+bool in_arena(const q8_ctx *c, const void *p) {
+    const uintptr_t a = (uintptr_t)c->arena, q = (uintptr_t)p;
+    return c->arena && q >= a && q < a + c->arena_bytes;
+}
+
+// A workspace too small for `need` moves to an allocation of its own (the
+// arena region it may have held stays reserved until the next plan).
 int grow(q8_ctx *c, void **buf, size_t *have, size_t need, const char *what) {
     if (*have >= need) return Q8_OK;
     if (*buf) {
         HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-        HIP_TRY(hipFree(*buf), "hipFree");
+        if (!in_arena(c, *buf)) HIP_TRY(hipFree(*buf), "hipFree");
         *buf = nullptr;
         *have = 0;
     }
     c->ws_generation++;  // graphs captured over the old buffer must not be replayed
     const size_t bytes = align_up(need, 1 << 20);
-    HIP_TRY(hipMalloc(buf, bytes), what);
+    HIP_TRY(dev_malloc(c, buf, bytes), what);
     *have = bytes;
     return Q8_OK;
 }
@@ -806,7 +830,7 @@ int vector_resident(q8_ctx *c, const float *host, size_t len, float **out) {
         return Q8_OK;
     }
     float *dev = nullptr;
-    HIP_TRY(hipMalloc(reinterpret_cast<void **>(&dev), len * sizeof(float)), "hipMalloc(norm weight)");
+    HIP_TRY(dev_malloc(c, reinterpret_cast<void **>(&dev), len * sizeof(float)), "hipMalloc(norm weight)");
     hipError_t e = hipMemcpyAsync(dev, host, len * sizeof(float), hipMemcpyHostToDevice, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) {
@@ -972,15 +996,15 @@ int q8_open(int device, q8_ctx **out) {
                           hipGetErrorString(he));
         }
         if (rc != Q8_OK) break;
-        he = hipMalloc(&c->argmax_ws, kArgmaxParts * 8 + 256);
+        he = dev_malloc(c, &c->argmax_ws, kArgmaxParts * 8 + 256);
         if (he != hipSuccess) { rc = hip_fail(he, "hipMalloc(argmax)"); break; }
-        he = hipMalloc((void **)&c->probe_sink, 256);
+        he = dev_malloc(c, (void **)&c->probe_sink, 256);
         if (he != hipSuccess) { rc = hip_fail(he, "hipMalloc(probe sink)"); break; }
         rc = q8i::noalloc_scratch(device, &c->noalloc);  // the device is current (hipSetDevice above)
         if (rc != Q8_OK) break;
-        he = hipMalloc((void **)&c->split_ws, kSplitBytes);
+        he = dev_malloc(c, (void **)&c->split_ws, kSplitBytes);
         if (he != hipSuccess) { rc = hip_fail(he, "hipMalloc(split scratch)"); break; }
-        he = hipMalloc((void **)&c->counters, kCounters * sizeof(unsigned));
+        he = dev_malloc(c, (void **)&c->counters, kCounters * sizeof(unsigned));
         if (he != hipSuccess) { rc = hip_fail(he, "hipMalloc(counters)"); break; }
         he = hipMemset(c->counters, 0, kCounters * sizeof(unsigned));
         if (he == hipSuccess) he = hipDeviceSynchronize();
@@ -1005,17 +1029,13 @@ void q8_close(q8_ctx *c) {
     for (auto &kv : c->vectors) hipFree(kv.second);
     for (auto &kv : c->rope_freq) hipFree(kv.second);
     for (auto &kv : c->allocs) hipFree(reinterpret_cast<void *>(kv.first));
-    if (c->act_ws) hipFree(c->act_ws);
-    if (c->tmp_ws) hipFree(c->tmp_ws);
-    if (c->act2_ws) hipFree(c->act2_ws);
-    if (c->norm_ws) hipFree(c->norm_ws);
+    for (void *w : {c->act_ws, c->tmp_ws, c->act2_ws, c->norm_ws, c->token_ws, c->attn_ws, c->attn_out_ws})
+        if (w && !in_arena(c, w)) hipFree(w);
+    if (c->arena) hipFree(c->arena);
     if (c->argmax_ws) hipFree(c->argmax_ws);
     if (c->probe_sink) hipFree(c->probe_sink);
     if (c->split_ws) hipFree(c->split_ws);
     if (c->counters) hipFree(c->counters);
-    if (c->token_ws) hipFree(c->token_ws);
-    if (c->attn_ws) hipFree(c->attn_ws);
-    if (c->attn_out_ws) hipFree(c->attn_out_ws);
     for (q8_weight *w : c->owned) {
         hipFree(w->base);
         delete w;
@@ -1071,7 +1091,7 @@ int q8_alloc(q8_ctx *c, size_t bytes, q8_dptr *out) {
     std::lock_guard<std::recursive_mutex> lock(c->mu);
     HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
     void *p = nullptr;
-    HIP_TRY(hipMalloc(&p, bytes), "hipMalloc");
+    HIP_TRY(dev_malloc(c, &p, bytes), "hipMalloc");
     c->allocs[(uintptr_t)p] = bytes;
     *out = (q8_dptr)(uintptr_t)p;
     return Q8_OK;
@@ -1086,6 +1106,125 @@ int q8_free(q8_ctx *c, q8_dptr ptr) {
     HIP_TRY(hipFree(reinterpret_cast<void *>(ptr)), "hipFree");
     c->allocs.erase(it);
     return Q8_OK;
+}
+
+int rope_table(q8_ctx *c, int n_rot, float base, const float **out);
+
+// BufferPlan::plan / scratch_requests (apps/engine/src/workspace.rs:63-106,
+// 171-342): every per-call workspace sized once for the largest shapes the
+// caller will serve.  The reference packs requests whose phases do not
+// overlap into shared offsets to fit consumer memory; here each workspace
+// gets a region of its own in one allocation (a few tens of MB against
+// 288 GB of HBM), so any order of calls is safe and no liveness analysis
+// can be wrong.
+int q8_workspace_plan(q8_ctx *c, const q8_workspace_shape *s) {
+    if (!c || !s) return fail(Q8_ERR_INVALID, "q8_workspace_plan: bad arguments");
+    if (s->max_tokens < 1 || s->max_tokens > Q8_MAX_TOKENS || s->max_k < 32 || s->max_k % 32 || s->max_ff < 0 ||
+        s->max_ff % 32 || s->attn_heads < 0 || s->attn_heads > kCounters - kAttnCounterBase || s->attn_splits < 0 ||
+        s->attn_splits > 1024 || s->rope_n_rot < 0 || s->rope_n_rot % 2 || s->rope_n_rot > Q8_ATTN_HEAD_DIM)
+        return fail(Q8_ERR_INVALID,
+                    "workspace shape: tokens %d (1..%d), k %d and ff %d (multiples of 32), heads %d, splits %d, "
+                    "rot %d",
+                    s->max_tokens, Q8_MAX_TOKENS, s->max_k, s->max_ff, s->attn_heads, s->attn_splits, s->rope_n_rot);
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+    if (s->rope_n_rot > 0) {
+        const float *freq = nullptr;
+        Q8_TRY(rope_table(c, s->rope_n_rot, s->rope_base, &freq));
+    }
+    const int T = s->max_tokens, K = s->max_k, F = s->max_ff, H = s->attn_heads;
+    auto prepared_max = [](int n, int k) {
+        return std::max(prepared_bytes(n, k, Q8_PREPARED_I8, nullptr), prepared_bytes(n, k, Q8_PREPARED_F16, nullptr));
+    };
+    struct Slot {
+        const char *name;
+        void **buf;
+        size_t *have;
+        size_t need;
+    };
+    const Slot slots[] = {
+        // prepared activations: prompts, prompt attention, the n = 1 quantize
+        {"activation", &c->act_ws, &c->act_ws_bytes, prepared_max(T, K)},
+        // silu(gate) * up prepared by the fused gate/up GEMM (n >= 2)
+        {"activation 2", &c->act2_ws, &c->act2_ws_bytes, F && T >= 2 ? prepared_max(T, F) : 0},
+        // gate and up f32 products of the unfused feed-forward pair
+        {"ffn", &c->tmp_ws, &c->tmp_ws_bytes, F ? 2 * align_up((size_t)T * F * 4, kAlign) : 0},
+        // one normalized row when a norm does not fold into its decode GEMV
+        {"norm", &c->norm_ws, &c->norm_ws_bytes, (size_t)K * 4},
+        // token ids of q8_embeddings
+        {"token ids", &c->token_ws, &c->token_ws_bytes, (size_t)T * 4},
+        // decode attention partials: accumulator, max and sum per head and split
+        {"attention", &c->attn_ws, &c->attn_ws_bytes,
+         H ? (size_t)H * std::max(1, s->attn_splits) * (Q8_ATTN_HEAD_DIM + 2) * 4 : 0},
+        // attention output when it cannot fold into the output projection
+        {"attention output", &c->attn_out_ws, &c->attn_out_ws_bytes, (size_t)H * Q8_ATTN_HEAD_DIM * 4},
+    };
+    bool covered = true;
+    for (const Slot &sl : slots) covered = covered && *sl.have >= sl.need;
+    if (covered) return Q8_OK;  // nothing moves: graphs over the current workspaces stay valid
+    // each region is the larger of the plan and what the workspace holds, so
+    // a plan never takes room from shapes earlier calls already used
+    constexpr size_t kRegionAlign = 64 << 10;
+    std::vector<q8_ctx::Region> layout;
+    size_t total = 0;
+    for (const Slot &sl : slots) {
+        const size_t b = align_up(std::max(sl.need, *sl.have), kRegionAlign);
+        layout.push_back({sl.name, total, b});
+        total += b;
+    }
+    HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    void *arena = nullptr;
+    HIP_TRY(dev_malloc(c, &arena, total), "hipMalloc(workspace arena)");
+    for (const Slot &sl : slots)
+        if (*sl.buf && !in_arena(c, *sl.buf)) hipFree(*sl.buf);
+    if (c->arena) hipFree(c->arena);
+    c->arena = arena;
+    c->arena_bytes = total;
+    c->regions = layout;
+    for (size_t i = 0; i < layout.size(); i++) {
+        *slots[i].buf = layout[i].bytes ? static_cast<uint8_t *>(arena) + layout[i].offset : nullptr;
+        *slots[i].have = layout[i].bytes;
+    }
+    c->ws_generation++;  // every workspace moved
+    return Q8_OK;
+}
+
+int q8_workspace_query(q8_ctx *c, q8_workspace_info *info) {
+    if (!c || !info) return fail(Q8_ERR_INVALID, "q8_workspace_query: bad arguments");
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    uint64_t outside = 0;
+    const std::pair<void *, size_t> ws[] = {{c->act_ws, c->act_ws_bytes},     {c->act2_ws, c->act2_ws_bytes},
+                                            {c->tmp_ws, c->tmp_ws_bytes},     {c->norm_ws, c->norm_ws_bytes},
+                                            {c->token_ws, c->token_ws_bytes}, {c->attn_ws, c->attn_ws_bytes},
+                                            {c->attn_out_ws, c->attn_out_ws_bytes}};
+    for (const auto &w : ws)
+        if (w.first && !in_arena(c, w.first)) outside += w.second;
+    info->bytes = c->arena_bytes + outside;
+    info->arena_bytes = c->arena_bytes;
+    info->allocations = c->allocations;
+    info->generation = c->ws_generation;
+    info->regions = (int)c->regions.size();
+    return Q8_OK;
+}
+
+int q8_workspace_region(q8_ctx *c, int index, const char **name, uint64_t *offset, uint64_t *bytes) {
+    if (!c) return fail(Q8_ERR_INVALID, "q8_workspace_region: null context");
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    if (index < 0 || index >= (int)c->regions.size())
+        return fail(Q8_ERR_INVALID, "workspace region %d of %zu", index, c->regions.size());
+    const q8_ctx::Region &r = c->regions[index];
+    if (name) *name = r.name;
+    if (offset) *offset = r.offset;
+    if (bytes) *bytes = r.bytes;
+    return Q8_OK;
+}
+
+int q8_vector_resident(q8_ctx *c, const float *weight, size_t k) {
+    if (!c || !weight || k == 0) return fail(Q8_ERR_INVALID, "q8_vector_resident: bad arguments");
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+    float *w = nullptr;
+    return vector_resident(c, weight, k, &w);
 }
 
 int q8_upload(q8_ctx *c, q8_dptr dst, const void *src, size_t bytes) {
@@ -1138,8 +1277,8 @@ int q8_weight_resident(q8_ctx *c, const void *bytes, size_t nbytes, int k, int o
     const size_t sbytes = (size_t)tiles * nb * Q8_TILE_ROWS * 2;
     const size_t total = align_up(qbytes, kAlign) + sbytes;
     void *base = nullptr, *staging = nullptr;
-    HIP_TRY(hipMalloc(&base, total), "hipMalloc(weight)");
-    hipError_t e = hipMalloc(&staging, nbytes);
+    HIP_TRY(dev_malloc(c, &base, total), "hipMalloc(weight)");
+    hipError_t e = dev_malloc(c, &staging, nbytes);
     if (e != hipSuccess) {
         hipFree(base);
         return hip_fail(e, "hipMalloc(weight staging)");
@@ -1222,7 +1361,7 @@ int q8_weight_export(q8_ctx *c, const q8_weight *w, void *dst, size_t nbytes) {
     if (nbytes != expect) return fail(Q8_ERR_INVALID, "export buffer holds %zu bytes, weight is %zu", nbytes, expect);
     std::lock_guard<std::recursive_mutex> lock(c->mu);
     void *staging = nullptr;
-    HIP_TRY(hipMalloc(&staging, nbytes), "hipMalloc(export)");
+    HIP_TRY(dev_malloc(c, &staging, nbytes), "hipMalloc(export)");
     Q8RepackArgs a{};
     a.dst = static_cast<uint8_t *>(staging);
     a.quants = w->quants;
@@ -1662,7 +1801,7 @@ int rope_table(q8_ctx *c, int n_rot, float base, const float **out) {
         std::vector<float> table(std::max(1, n_rot / 2));
         for (int i = 0; i < n_rot / 2; i++) table[i] = powf(base, (-2.0f * (float)i) / (float)n_rot);
         float *dev = nullptr;
-        HIP_TRY(hipMalloc(reinterpret_cast<void **>(&dev), table.size() * 4), "hipMalloc(rope table)");
+        HIP_TRY(dev_malloc(c, reinterpret_cast<void **>(&dev), table.size() * 4), "hipMalloc(rope table)");
         hipError_t e = hipMemcpyAsync(dev, table.data(), table.size() * 4, hipMemcpyHostToDevice, c->stream);
         if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
         if (e != hipSuccess) {
@@ -1971,8 +2110,8 @@ int q8_weight_synthetic(q8_ctx *c, int k, int out, uint64_t seed, float scale_st
     const long long threads = (long long)tiles * Q8_TILE_ROWS * nb;
     if (threads > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "weight of %lld blocks is too large", threads);
     void *base = nullptr, *staging = nullptr;
-    HIP_TRY(hipMalloc(&base, total), "hipMalloc(weight)");
-    hipError_t e = hipMalloc(&staging, nbytes);
+    HIP_TRY(dev_malloc(c, &base, total), "hipMalloc(weight)");
+    hipError_t e = dev_malloc(c, &staging, nbytes);
     if (e != hipSuccess) {
         hipFree(base);
         return hip_fail(e, "hipMalloc(weight staging)");

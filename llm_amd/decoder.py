@@ -13,7 +13,7 @@ import ctypes
 
 import numpy as np
 
-from .q8 import DecoderConfig, DeviceWeight, Gpu, _check, lib
+from .q8 import DecoderConfig, DecoderStats, DeviceWeight, Gpu, _check, lib
 
 Q, K, V, O, GATE, UP, DOWN = range(7)
 
@@ -80,6 +80,12 @@ class Decoder:
             k, out = {Q: (c.n_embd, hd), K: (c.n_embd, kv), V: (c.n_embd, kv), O: (hd, c.n_embd),
                       GATE: (c.n_embd, c.n_ff), UP: (c.n_embd, c.n_ff), DOWN: (c.n_ff, c.n_embd)}[which]
         return DeviceWeight(h.value, k, out)
+
+    def graph_stats(self) -> dict:
+        """Graphs held, captured and dropped, and eager passes (q8_decoder_graph_stats)."""
+        st = DecoderStats()
+        _check(lib().q8_decoder_graph_stats(self.handle, ctypes.byref(st)))
+        return {f: getattr(st, f) for f, _ in st._fields_}
 
     def norm(self, layer: int, which: int = 0) -> np.ndarray:
         p = ctypes.POINTER(ctypes.c_float)()

@@ -60,7 +60,8 @@ EXPORTS = (
     "q8_vector_release", "q8_norm_qkv_rope",
     "q8_weight_synthetic", "q8_decoder_create_synthetic", "q8_decoder_destroy", "q8_decoder_reset",
     "q8_decoder_position", "q8_decoder_forward", "q8_decoder_generate", "q8_decoder_logits", "q8_decoder_weight",
-    "q8_decoder_norm",
+    "q8_decoder_norm", "q8_decoder_graph_stats",
+    "q8_workspace_plan", "q8_workspace_query", "q8_workspace_region", "q8_vector_resident",
 )
 
 
@@ -102,6 +103,23 @@ class DecoderConfig(ctypes.Structure):
     _fields_ = [(f, ctypes.c_int) for f in ("n_layer", "n_embd", "n_ff", "n_head", "n_head_kv", "head_dim",
                                             "n_rot", "n_vocab", "capacity", "max_batch")] + \
                [("eps", ctypes.c_float), ("rope_base", ctypes.c_float)]
+
+
+class WorkspaceShape(ctypes.Structure):
+    """q8_workspace_shape (include/q8mi.h)."""
+    _fields_ = [(f, ctypes.c_int) for f in ("max_tokens", "max_k", "max_ff", "attn_heads", "attn_splits",
+                                            "rope_n_rot")] + [("rope_base", ctypes.c_float)]
+
+
+class WorkspaceInfo(ctypes.Structure):
+    """q8_workspace_info (include/q8mi.h)."""
+    _fields_ = [(f, ctypes.c_uint64) for f in ("bytes", "arena_bytes", "allocations", "generation")] + \
+               [("regions", ctypes.c_int)]
+
+
+class DecoderStats(ctypes.Structure):
+    """q8_decoder_stats (include/q8decoder.h)."""
+    _fields_ = [(f, ctypes.c_int) for f in ("graphs", "captured", "dropped", "eager")]
 
 
 class _GroupEntry(ctypes.Structure):
@@ -239,6 +257,12 @@ def lib():
         "q8_decoder_logits": (c_int, [vp, ctypes.POINTER(ctypes.c_float), c_size]),
         "q8_decoder_weight": (c_int, [vp, c_int, c_int, ctypes.POINTER(vp)]),
         "q8_decoder_norm": (c_int, [vp, c_int, c_int, ctypes.POINTER(ctypes.POINTER(ctypes.c_float))]),
+        "q8_decoder_graph_stats": (c_int, [vp, ctypes.POINTER(DecoderStats)]),
+        "q8_workspace_plan": (c_int, [vp, ctypes.POINTER(WorkspaceShape)]),
+        "q8_workspace_query": (c_int, [vp, ctypes.POINTER(WorkspaceInfo)]),
+        "q8_workspace_region": (c_int, [vp, c_int, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(u64),
+                                        ctypes.POINTER(u64)]),
+        "q8_vector_resident": (c_int, [vp, vp, c_size]),
     }
     assert set(sig) == set(EXPORTS)
     for name, (res, args) in sig.items():
@@ -378,6 +402,25 @@ class Gpu:
 
     def sync(self):
         _check(lib().q8_sync(self.handle))
+
+    def workspace_plan(self, max_tokens: int, max_k: int, max_ff: int = 0, attn_heads: int = 0,
+                       attn_splits: int = 0, rope_n_rot: int = 0, rope_base: float = 10000.0):
+        """q8_workspace_plan: size every workspace once for these shapes."""
+        s = WorkspaceShape(max_tokens, max_k, max_ff, attn_heads, attn_splits, rope_n_rot, rope_base)
+        _check(lib().q8_workspace_plan(self.handle, ctypes.byref(s)))
+
+    def workspace(self) -> dict:
+        """q8_workspace_query plus the plan's regions (name, offset, bytes)."""
+        info = WorkspaceInfo()
+        _check(lib().q8_workspace_query(self.handle, ctypes.byref(info)))
+        d = {f: getattr(info, f) for f, _ in info._fields_}
+        regions = []
+        for i in range(info.regions):
+            name, off, nb = ctypes.c_char_p(), ctypes.c_uint64(), ctypes.c_uint64()
+            _check(lib().q8_workspace_region(self.handle, i, ctypes.byref(name), ctypes.byref(off), ctypes.byref(nb)))
+            regions.append((name.value.decode(), off.value, nb.value))
+        d["layout"] = regions
+        return d
 
     def resident(self, weight: Weight):
         """Gpu::quantized: upload + repack once, cached by identity."""

@@ -1,0 +1,149 @@
+"""The workspace plan (q8_workspace_plan, include/q8mi.h) and the decoder's
+use of it (include/q8decoder.h), through the C-ABI.
+
+The reference sizes its scratch once per context from the shapes it will
+serve (BufferPlan::plan and scratch_requests, apps/engine/src/workspace.rs:
+63-106 and 171-342) and never allocates on the token path.  Here: a planned
+context serves every call within its shape without a device allocation; a
+decoder at the configs[4] geometry (hidden 2304, FFN 5760, 36 x 64 heads,
+vocab 122 880, 4096-position cache, 512-token prompts) runs prefills and 128
+decode steps with the context's allocation count and workspace generation
+unchanged and no captured graph dropped."""
+import numpy as np
+import pytest
+
+import oracle
+from llm_amd import decoder as dm
+from llm_amd import q8
+
+pytestmark = pytest.mark.gpu
+
+SEED = 0x5EED
+N, HID, FFN, HEADS = 512, 2304, 5760, 36
+REGIONS = ["activation", "activation 2", "ffn", "norm", "token ids", "attention", "attention output"]
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    g = q8.Gpu(0)
+    yield g
+    g.close()
+
+
+def prepared_bytes(n, k, f16):
+    tiles, nb = (n + 31) // 32, k // 32
+    q = tiles * nb * (2048 if f16 else 1024)
+    return (q + 255) // 256 * 256 + tiles * nb * 32 * 4
+
+
+def test_plan_layout_and_calls_within_it_allocate_nothing():
+    g = q8.Gpu(0)  # a context of its own: the plan starts from empty workspaces
+    try:
+        before = g.workspace()
+        assert before["regions"] == 0 and before["arena_bytes"] == 0
+        g.workspace_plan(max_tokens=N, max_k=FFN, max_ff=FFN, attn_heads=HEADS, attn_splits=8, rope_n_rot=64)
+        planned = g.workspace()
+        print("plan:", planned)
+        # one arena and the rotation table; every workspace moved once
+        assert planned["allocations"] == before["allocations"] + 2
+        assert planned["generation"] == before["generation"] + 1
+        layout = planned["layout"]
+        assert [r[0] for r in layout] == REGIONS
+        end = 0
+        for name, off, nbytes in layout:  # disjoint, in order, 64 KiB aligned
+            assert off == end and off % 65536 == 0
+            end = off + nbytes
+        assert end == planned["arena_bytes"] == planned["bytes"]
+        need = {"activation": prepared_bytes(N, FFN, True), "activation 2": prepared_bytes(N, FFN, True),
+                "ffn": 2 * N * FFN * 4, "norm": FFN * 4, "token ids": N * 4,
+                "attention": HEADS * 8 * 66 * 4, "attention output": HEADS * 64 * 4}
+        for name, _, nbytes in layout:
+            assert need[name] <= nbytes < need[name] + 65536, name
+
+        # a plan the workspaces already cover changes nothing
+        g.workspace_plan(max_tokens=64, max_k=HID, max_ff=FFN, attn_heads=HEADS, attn_splits=2)
+        again = g.workspace()
+        assert (again["allocations"], again["generation"], again["layout"]) == \
+            (planned["allocations"], planned["generation"], layout)
+
+        # calls within the shape: the weights and buffers are the caller's
+        # allocations; the calls themselves make none
+        r = np.random.default_rng(SEED)
+        wg, wu, wd = (q8.Weight(oracle.make_q8_weight(r, o, k), k, o) for o, k in ((FFN, HID), (FFN, HID), (HID, FFN)))
+        for w in (wg, wu, wd):
+            g.resident(w)
+        x = g.alloc(4 * N * FFN)
+        x.upload(r.standard_normal(N * HID).astype(np.float32))
+        y = g.alloc(4 * N * FFN)
+        act = g.alloc(4 * N * FFN)
+        norm_w = (1.0 + 0.01 * r.standard_normal(HID)).astype(np.float32)
+        g.rmsnorm(x, 0, norm_w, 1e-6, 1, y, 0)  # the norm weight made resident (a first use)
+        g.sync()
+        start = g.workspace()
+        for n in (N, 64, 8, 1):
+            g.matmul(wg, x, 0, n, y, 0)
+            p = g.norm_prepare(x, 0, norm_w, 1e-6, n)
+            if n >= 2:
+                pd = g.gate_up_silu_prepared(wg, wu, p)
+                g.matmul(wd, act, 0, n, y, 0, prepared=pd)
+                g.gate_up_silu(wg, wu, x, 0, n, act, 0)
+            else:
+                g.norm_gate_up_silu(norm_w, 1e-6, wg, wu, x, 0, act, 0)
+            g.matmul(wd, act, 0, n, y, 0)
+        g.sync()
+        end_info = g.workspace()
+        assert (end_info["allocations"], end_info["generation"]) == (start["allocations"], start["generation"])
+
+        # a larger shape moves the workspaces once, into one new arena
+        g.workspace_plan(max_tokens=1024, max_k=FFN, max_ff=FFN, attn_heads=HEADS, attn_splits=8)
+        grown = g.workspace()
+        assert grown["allocations"] == end_info["allocations"] + 1
+        assert grown["generation"] == end_info["generation"] + 1
+        assert grown["arena_bytes"] > planned["arena_bytes"]
+        for b in (x, y, act):
+            b.free()
+    finally:
+        g.close()
+
+
+def test_plan_rejects_bad_shapes(gpu):
+    for kw in (dict(max_tokens=0, max_k=64), dict(max_tokens=1025, max_k=64), dict(max_tokens=8, max_k=33),
+               dict(max_tokens=8, max_k=64, max_ff=40), dict(max_tokens=8, max_k=64, attn_splits=2000),
+               dict(max_tokens=8, max_k=64, rope_n_rot=3)):
+        with pytest.raises(q8.Q8Error):
+            gpu.workspace_plan(**kw)
+
+
+def test_decoder_prefill_and_128_steps_allocate_nothing(gpu):
+    """A two-layer decoder at the configs[4] geometry: creation plans the
+    workspaces; then a 512-token prefill, 128 decode steps (two generate
+    calls and single-token forwards), a reset and the same prefill again.
+    The context's device allocations and workspace generation stay as they
+    were after creation, no captured graph is dropped, and the replayed
+    prefill chooses the same tokens as the first."""
+    cfg = dm.config(n_layer=2, n_embd=HID, n_ff=FFN, n_head=HEADS, n_head_kv=HEADS, head_dim=64, n_vocab=122880,
+                    capacity=4096, max_batch=N)
+    dec = dm.Decoder(gpu, cfg, seed=SEED)
+    try:
+        created = gpu.workspace()
+        print("after creation:", {k: v for k, v in created.items() if k != "layout"})
+        prompt = np.random.default_rng(SEED).integers(0, cfg.n_vocab, N, dtype=np.uint32)
+        first = [dec.forward(prompt)]
+        first += list(dec.generate(60))
+        for _ in range(4):
+            first.append(dec.forward([first[-1]]))
+        first += list(dec.generate(64))
+        assert dec.position == N + 128
+        dec.reset()
+        second = [dec.forward(prompt)] + list(dec.generate(8))
+        assert second == first[:9]
+        gpu.sync()
+        after = gpu.workspace()
+        stats = dec.graph_stats()
+        print("after 2 prefills + 136 steps:", {k: v for k, v in after.items() if k != "layout"}, stats)
+        assert after["allocations"] == created["allocations"], "a pass allocated device memory"
+        assert after["generation"] == created["generation"], "a workspace moved"
+        assert stats["dropped"] == 0
+        assert stats["captured"] >= 2 and stats["graphs"] == stats["captured"]
+    finally:
+        dec.close()
