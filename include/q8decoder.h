@@ -86,8 +86,12 @@ int q8_advance_position(q8_ctx *ctx, q8_dptr position, int by);
 
 /* q8_rmsnorm (one row) followed by q8_matmul_decode_group on its output, with
  * the norm folded into the GEMV launch: every workgroup recomputes the row's
- * sum of squares exactly as the row norm kernel does, so the results are
- * bit-identical to the two calls and the normalized row is never written.
+ * sum of squares exactly as the row norm kernel does, and the normalized row
+ * is never written.  With option "gemv.exact" = 1 each workgroup waits for
+ * the scale and multiplies x by it before the dot products, so the results
+ * are bit-identical to the two calls; in the default block order it stages
+ * x * weight and multiplies the row sums by the scale instead (no wait
+ * inside the launch; within f32 rounding of the two calls).
  * The reference runs the two steps apart (model.rs decode step: rmsnorm then
  * matmul_decode_group); shapes whose GEMV needs a K split take the two-step
  * path on the device.  `norm_weight` is a host f32[k] made resident like
@@ -99,7 +103,8 @@ int q8_norm_matmul_decode_group(q8_ctx *ctx, const float *norm_weight, float eps
  * q, k, v decode GEMV group over its output, and q8_rope_append on the
  * results, with the norm folded into the GEMV (as q8_norm_matmul_decode_group)
  * and the rotation and KV append in its epilogue -- bit-identical to those
- * three calls.  q [n_head*head_dim] f32 receives the rotated query; k and v
+ * three calls with "gemv.exact" = 1, within f32 rounding of them otherwise
+ * (the folded norm's two modes).  q [n_head*head_dim] f32 receives the rotated query; k and v
  * go only into the f16 caches, at row *position (nothing is appended, and q
  * is not rotated, at a position outside the cache).  The reference runs the
  * steps as separate kernels (model.rs dense_attention: rmsnorm,
@@ -121,7 +126,8 @@ int q8_prompt_qkv_rope(q8_ctx *ctx, const q8_weight *wq, const q8_weight *wk, co
                        int n_head, int n_kv, int head_dim, int n_rot, float base, int capacity, q8_dptr position);
 
 /* q8_rmsnorm (one row) followed by q8_gate_up_silu at n = 1, folded the same
- * way: act = silu(gate . xn) * (up . xn), xn = rmsnorm(x) * norm_weight. */
+ * way (bit-identical to the two calls with "gemv.exact" = 1):
+ * act = silu(gate . xn) * (up . xn), xn = rmsnorm(x) * norm_weight. */
 int q8_norm_gate_up_silu(q8_ctx *ctx, const float *norm_weight, float eps, const q8_weight *gate,
                          const q8_weight *up, q8_dptr x, size_t x_offset, q8_dptr act, size_t act_offset);
 

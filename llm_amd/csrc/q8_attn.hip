@@ -106,14 +106,20 @@ extern "C" __global__ __launch_bounds__(256) void q8_rope_append(Q8RopeArgs a) {
 // attention_combine 735-762), and the same as the GEMV prologue's.
 // ---------------------------------------------------------------------------
 static __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int m = 32; m > 0; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
-    return v;
+    v = xor_max<32>(v);
+    v = xor_max<16>(v);
+    v = xor_max<8>(v);
+    v = xor_max<4>(v);
+    v = xor_max<2>(v);
+    return xor_max<1>(v);
 }
 static __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int m = 32; m > 0; m >>= 1) v += __shfl_xor(v, m);
-    return v;
+    v = xor_add<32>(v);
+    v = xor_add<16>(v);
+    v = xor_add<8>(v);
+    v = xor_add<4>(v);
+    v = xor_add<2>(v);
+    return xor_add<1>(v);
 }
 
 template <int W, int NP>
@@ -135,15 +141,13 @@ static __device__ __forceinline__ void attn_decode_body(const Q8AttnDecodeArgs &
     const int wave = tid >> 6;
     const int kc = tid & 7;     // dims 8 kc .. 8 kc + 7
     const int slot = tid >> 3;  // row slot of the pass
-    const f32x4 q0 = *(const f32x4 *)(a.q + (size_t)head * HD + 8 * kc);
-    const f32x4 q1 = *(const f32x4 *)(a.q + (size_t)head * HD + 8 * kc + 4);
     const uint16_t *kbase = a.kcache + kvh * HD + 8 * kc;
     const uint16_t *vbase = a.vcache + kvh * HD + 8 * kc;
     float m = -INFINITY;  // running max, workgroup-uniform
     float l = 0.0f;       // this lane's weights summed over its rows
     float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
     // One chunk: rows c0 + slot + RP j (j < NP), live below `end`.
-    auto chunk = [&](int c0, int end, const i32x4 *ku, const i32x4 *vu) {
+    auto chunk = [&](int c0, int end, const f32x4 &q0, const f32x4 &q1, const i32x4 *ku, const i32x4 *vu) {
         float sc[NP];
         float cmax = -INFINITY;
 #pragma unroll
@@ -157,9 +161,9 @@ static __device__ __forceinline__ void attn_decode_body(const Q8AttnDecodeArgs &
             dot = __builtin_fmaf(q1[1], f16_to_f32((unsigned)ku[j][2] >> 16), dot);
             dot = __builtin_fmaf(q1[2], f16_to_f32((unsigned)ku[j][3] & 0xffffu), dot);
             dot = __builtin_fmaf(q1[3], f16_to_f32((unsigned)ku[j][3] >> 16), dot);
-            dot += __shfl_xor(dot, 1);
-            dot += __shfl_xor(dot, 2);
-            dot += __shfl_xor(dot, 4);
+            dot = xor_add<1>(dot);
+            dot = xor_add<2>(dot);
+            dot = xor_add<4>(dot);
             sc[j] = dot * a.scale;
             if (c0 + slot + RP * j < end) cmax = fmaxf(cmax, sc[j]);
         }
@@ -192,25 +196,35 @@ static __device__ __forceinline__ void attn_decode_body(const Q8AttnDecodeArgs &
     const int per = (visible + a.splits - 1) / a.splits;
     const int begin = split * per;
     const int end = min(begin + per, visible);
-    for (int c0 = begin; c0 < end; c0 += RP * NP) {
-        i32x4 ku[NP], vu[NP];
+    // A chunk's key and value rows, clamped to the last live row: rows past
+    // `end` repeat its address (no extra traffic) and are masked.  The first
+    // chunk is issued before q is read and every later one while the
+    // previous is computed, so a split of one chunk waits for one memory
+    // latency.
+    i32x4 ku[NP], vu[NP];
+    auto load_chunk = [&](int c0) {
 #pragma unroll
         for (int j = 0; j < NP; j++) {
-            // clamped to the last live row: rows past `end` repeat its address
-            // (no extra traffic) and are masked
             const int p = min(c0 + slot + RP * j, end - 1);
             ku[j] = *(const i32x4 *)(kbase + (size_t)p * kv_dim);
             vu[j] = *(const i32x4 *)(vbase + (size_t)p * kv_dim);
         }
-        chunk(c0, end, ku, vu);
+    };
+    if (begin < end) load_chunk(begin);
+    const f32x4 q0 = *(const f32x4 *)(a.q + (size_t)head * HD + 8 * kc);
+    const f32x4 q1 = *(const f32x4 *)(a.q + (size_t)head * HD + 8 * kc + 4);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int c0 = begin; c0 < end; c0 += RP * NP) {
+        chunk(c0, end, q0, q1, ku, vu);
+        if (c0 + RP * NP < end) load_chunk(c0 + RP * NP);
     }
     // row slots of a wave (lanes with the same kc), then the waves; the
     // weights once per row (the kc == 0 lanes)
 #pragma unroll
     for (int d = 0; d < 8; d++) {
-        acc[d] += __shfl_xor(acc[d], 8);
-        acc[d] += __shfl_xor(acc[d], 16);
-        acc[d] += __shfl_xor(acc[d], 32);
+        acc[d] = xor_add<8>(acc[d]);
+        acc[d] = xor_add<16>(acc[d]);
+        acc[d] = xor_add<32>(acc[d]);
     }
     const float lw = wave_sum(kc == 0 ? l : 0.0f);
     if (lane < 8) {

@@ -169,6 +169,56 @@ static __device__ __forceinline__ float half_partial(i32x4 q, const f32x4 *xh) {
     return (a0 + a1) + (a2 + a3);
 }
 
+// Butterfly steps without an LDS round trip: v op v[lane ^ M].  M < 16 by
+// DPP within a 16-lane row (quad permutes for 1 and 2, a row shift each way
+// for 4, the row rotate by 8 for 8), M = 16 and 32 by the gfx950 row swaps,
+// which leave (own, partner) or (partner, own) in the pair they return --
+// the same sum and max either way, as both are commutative.  Bit-identical
+// to the same butterfly through __shfl_xor.
+template <int CTRL>
+static __device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int M>
+static __device__ __forceinline__ float xor_partner(float v) {
+    static_assert(M == 1 || M == 2 || M == 4 || M == 8, "DPP partners within a row");
+    if constexpr (M == 1) return dpp_mov<0xb1>(v);  // quad_perm [1, 0, 3, 2]
+    if constexpr (M == 2) return dpp_mov<0x4e>(v);  // quad_perm [2, 3, 0, 1]
+    if constexpr (M == 4) {
+        const float up = dpp_mov<0x104>(v);    // row_shl:4, lane i <- i + 4
+        const float down = dpp_mov<0x114>(v);  // row_shr:4, lane i <- i - 4
+        return (threadIdx.x & 4) ? down : up;
+    }
+    return dpp_mov<0x128>(v);  // row_ror:8, lane i <- (i + 8) mod 16
+}
+template <int M>
+static __device__ __forceinline__ float xor_add(float v) {
+    if constexpr (M == 16 || M == 32) {
+        const auto sw = M == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false)
+                                : __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    } else {
+        return v + xor_partner<M>(v);
+    }
+}
+template <int M>
+static __device__ __forceinline__ float xor_max(float v) {
+    if constexpr (M == 16 || M == 32) {
+        const auto sw = M == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false)
+                                : __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    } else {
+        return fmaxf(v, xor_partner<M>(v));
+    }
+}
+// The folded RMSNorm's scale from q8_rmsnorm_row's four wave sums:
+// 1 / sqrt(mean square + eps), the mean square rounded once from f64.
+static __device__ __forceinline__ float norm_scale(const double *npart, int k, float eps) {
+    const double total = (npart[0] + npart[1]) + (npart[2] + npart[3]);
+    const float mean_square = (float)(total / (double)k);
+    return 1.0f / sqrtf(mean_square + eps);
+}
+
 // Float4 slots of x one lane stages: a wave covers at most
 // 64 * Q8_GEMV_STAGE / 16 = 12 block pairs (the host's tactic keeps to it).
 #define Q8_GEMV_STAGE 3
@@ -459,55 +509,64 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
     // guarantees one K slice, >= 256 threads and k <= 1024 * Q8_NORM_ROW_VEC):
     // the norm weight over this wave's x range, and q8_rmsnorm_row's sum of
     // squares term for term -- threads 0..255 take float4s tid + 256 j, j
-    // ascending, and reduce with the same shuffle tree and four-wave sum --
-    // so the staged values are bit-identical to that kernel's output.  These
-    // loads go out before the weight stream, so waiting for them does not
-    // wait for it.
+    // ascending, and reduce with the same shuffle tree and four-wave sum.
+    // Those x loads go out before the weight stream and are summed after it
+    // is issued.  EXACT: the staged values are (x * scale) * w, bit-identical
+    // to that kernel's output, after a workgroup barrier for the scale.
+    // Otherwise no barrier waits for the scale (it would hold every wave until
+    // the slowest had its x, and push the rest of the launch out from under
+    // the weight stream): x * w is staged, the four wave sums meet at the
+    // kernel's final barrier, and the row sums are multiplied by the scale.
     const bool norm = !ONE && a.norm_w != nullptr;  // kernel-uniform
     // the RoPE epilogue's position, read while the weights stream in
     const int rope_position = (!ONE && a.rope_pos) ? *a.rope_pos : 0;
     f32x4 wv[Q8_GEMV_STAGE];
-    double ss = 0.0;
+    f32x4 nx[Q8_NORM_ROW_VEC];
+    const int nv = nb * 8;
     if (norm) {
         const f32x4 *nw = reinterpret_cast<const f32x4 *>(a.norm_w);
 #pragma unroll
         for (int u = 0; u < Q8_GEMV_STAGE; u++) wv[u] = nw[min(st_begin + lane + 64 * u, st_clamp)];
         if (threadIdx.x < 256) {
             const f32x4 *xr = reinterpret_cast<const f32x4 *>(xg);
-            const int nv = nb * 8;
-            f32x4 nx[Q8_NORM_ROW_VEC];
 #pragma unroll
             for (int j = 0; j < Q8_NORM_ROW_VEC; j++) nx[j] = xr[min((int)threadIdx.x + 256 * j, nv - 1)];
-#pragma unroll
-            for (int j = 0; j < Q8_NORM_ROW_VEC; j++) {
-                if ((int)threadIdx.x + 256 * j < nv) {
-#pragma unroll
-                    for (int e = 0; e < 4; e++) ss += (double)(nx[j][e] * nx[j][e]);
-                }
-            }
         }
     }
     __builtin_amdgcn_sched_barrier(0);
 
+    // the weight stream goes out before anything waits for x
     Q8_GEMV_LOAD_BATCH(p_begin)
     __builtin_amdgcn_sched_barrier(0);
 
-    float nscale = 1.0f;
-    if (norm) {
-        __shared__ double npart[4];
-        if (threadIdx.x < 256) {
+    __shared__ double npart[4];
+    if (norm && threadIdx.x < 256) {
+        double ss = 0.0;
 #pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
-            if (lane == 0) npart[wave] = ss;
+        for (int j = 0; j < Q8_NORM_ROW_VEC; j++) {
+            if ((int)threadIdx.x + 256 * j < nv) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) ss += (double)(nx[j][e] * nx[j][e]);
+            }
         }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+        if (lane == 0) npart[wave] = ss;
+    }
+    float nscale = 1.0f;
+    if (norm && EXACT) {
         __syncthreads();
-        const double total_ss = (npart[0] + npart[1]) + (npart[2] + npart[3]);
-        const float mean_square = (float)(total_ss / (double)(nb * 32));
-        nscale = 1.0f / sqrtf(mean_square + a.norm_eps);
+        nscale = norm_scale(npart, nb * 32, a.norm_eps);
 #pragma unroll
         for (int u = 0; u < Q8_GEMV_STAGE; u++) {
 #pragma unroll
             for (int e = 0; e < 4; e++) xv[u][e] = (xv[u][e] * nscale) * wv[u][e];
+        }
+    } else if (norm) {
+#pragma unroll
+        for (int u = 0; u < Q8_GEMV_STAGE; u++) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) xv[u][e] = xv[u][e] * wv[u][e];
         }
     }
 
@@ -643,6 +702,11 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
             }
             sums[sl] = acc;
         }
+    }
+    if (!EXACT && norm) {  // the norm's scale, applied to the row sums
+        const float s = norm_scale(npart, nb * 32, a.norm_eps);
+        sums[0] *= s;
+        sums[1] *= s;
     }
     const int row = tile * Q8_TILE_ROWS + r;
     if (silu) {
@@ -783,13 +847,20 @@ static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
     const int st_begin = 8 * b_begin;
     const int st_end = 8 * b_end;
     const int st_clamp = max(st_end - 1, 0);
-    // CMB: x is built by the folded attention combine instead (a thread per
-    // float4 of x, in turn where x has more float4s than the workgroup has
-    // threads); every wave then reads it.
+    // CMB: x is built by the folded attention combine instead.  Where a
+    // wave's range is at most one float4 per lane (CMBW), each wave builds its
+    // own range and no workgroup barrier waits for the others; otherwise a
+    // thread per float4 of x (in turn where x has more float4s than the
+    // workgroup has threads), then a barrier.  The arithmetic per float4 is
+    // the same either way.
+    constexpr bool CMBW = CMB && BPW * 8 <= 64;
     f32x4 xv[Q8_GEMV_STAGE];
     CombineRegs creg;
     const int ns = CMB ? a.attn_splits : 0;
-    if constexpr (CMB) {
+    const int cmb_v = (lane < st_end - st_begin) ? st_begin + lane : nb * 8;  // CMBW: nb * 8 = the pad
+    if constexpr (CMBW) {
+        combine_load_v(a, min(cmb_v, st_clamp), ns, creg);
+    } else if constexpr (CMB) {
         combine_load(a, nb, ns, creg);
     } else {
 #pragma unroll
@@ -816,7 +887,9 @@ static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
     if (EX && wave == 0 && lane < RS) {
         for (int b = nb; b < ((nb + 3) & ~3); b++) vbuf[r * vrow + b] = 0.0f;
     }
-    if constexpr (CMB) {
+    if constexpr (CMBW) {
+        combine_store_v(cmb_v, nb, ns, creg, xs, pad);
+    } else if constexpr (CMB) {
         combine_store(nb, ns, creg, xs, pad);
         combine_rest(a, nb, ns, xs, pad);
         __syncthreads();
@@ -900,6 +973,265 @@ Q8_GEMV_RS_KERNEL(8, 3)
 Q8_GEMV_RS_KERNEL(8, 6)
 Q8_GEMV_RS_KERNEL(16, 3)
 Q8_GEMV_RS_KERNEL(16, 6)
+
+// ---------------------------------------------------------------------------
+// Row-slice GEMV over a decode group (q8_gemv_g*: up to four matrices sharing
+// x; with rope_pos set, the RoPE + KV append epilogue of a q, k, v group) or
+// over the gate/up pair (q8_gemv_s*, SILU: y_gate = silu(gate . x) * (up . x)),
+// with the RMSNorm of x optionally folded in (norm_w).  A workgroup owns RS
+// rows of one 32-row tile -- of each matrix of the pair -- and the whole K
+// range: gemv_rs_body's lane layout, block arithmetic, x staging and row sums
+// (SILU: waves [0, W) take the gate rows, [W, 2W) the same up rows, and both
+// stage identical x values into the same LDS slots), and gemv_body's member
+// selection, folded norm and epilogues.  In exact mode the outputs are
+// therefore bit-identical to the multi-matrix tile kernels' (q8_gemv_pb*_e1);
+// EX = 0 sums the block values in gemv_rs_body's fixed tree.
+// ---------------------------------------------------------------------------
+template <int RS, int NL, int EX, int SILU>
+static __device__ __forceinline__ void gemv_rsg_body(const Q8GemvArgs &a) {
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    constexpr int LPB = 2 * RS;
+    constexpr int BPL = 64 / LPB;
+    constexpr int SPT = Q8_TILE_ROWS / RS;
+    constexpr int BPW = NL * BPL;
+    constexpr int NSLOT = SILU ? 2 : 1;
+    static_assert(BPW * 8 <= 64 * Q8_GEMV_STAGE, "x range of a wave exceeds its staging registers");
+    const int nb = a.nb;
+    const int members = a.members;
+    const int nw = a.waves_per_tile;  // waves per slot
+    const float *xg = a.x;
+    const uint8_t *q_[Q8_GROUP_MAX];
+    const uint16_t *sc_[Q8_GROUP_MAX];
+    float *y_[Q8_GROUP_MAX];
+    const float *bias_[Q8_GROUP_MAX];
+    int rows_[Q8_GROUP_MAX], tb_[Q8_GROUP_MAX];
+#pragma unroll
+    for (int i = 0; i < Q8_GROUP_MAX; i++) {
+        q_[i] = a.m[i].quants;
+        sc_[i] = a.m[i].scales;
+        y_[i] = a.m[i].y;
+        bias_[i] = a.m[i].bias;
+        rows_[i] = a.m[i].rows;
+        tb_[i] = a.m[i].tile_begin;
+    }
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int slot = (SILU && wave >= nw) ? 1 : 0;
+    const int w = wave - slot * nw;
+    const int j = lane / LPB;
+    const int h = (lane / RS) & 1;
+    const int r = lane % RS;
+    const int bx = blockIdx.x;
+    const int xo = a.xcd_order;
+    const int gtile = xo ? (bx / (8 * SPT)) * 8 + (bx & 7) : bx / SPT;
+    const int slice = xo ? (bx >> 3) % SPT : bx % SPT;
+    if (gtile >= a.total_tiles) return;  // padding of the XCD order, whole workgroup
+    int by_tile = 0;
+#pragma unroll
+    for (int i = 1; i < Q8_GROUP_MAX; i++) by_tile += (int)(i < members) & (int)(gtile >= tb_[i]);
+    const int mi = SILU ? slot : by_tile;
+    const uint8_t *mq = q_[0];
+    const uint16_t *msc = sc_[0];
+    float *my = y_[0];
+    const float *mbias = bias_[0];
+    int mrows = rows_[0];
+    int mtb = tb_[0];
+#pragma unroll
+    for (int i = 1; i < Q8_GROUP_MAX; i++) {
+        const bool take = mi == i;
+        mq = take ? q_[i] : mq;
+        msc = take ? sc_[i] : msc;
+        my = take ? y_[i] : my;
+        mbias = take ? bias_[i] : mbias;
+        mrows = take ? rows_[i] : mrows;
+        mtb = take ? tb_[i] : mtb;
+    }
+    const int tile = SILU ? gtile : gtile - mtb;
+    const int srow = slice * RS + r;
+    const int b_begin = w * BPW;
+    const int b_end = min(nb, b_begin + BPW);
+    const int b_last = max(b_end - 1, 0);
+    const uint8_t *qbase = mq + (size_t)tile * nb * Q8_UNIT_BYTES + 16 * (32 * h + srow);
+    const uint16_t *sbase = msc + (size_t)tile * nb * Q8_TILE_ROWS + srow;
+    const int vrow = Q8_GEMV_VROW(nb);
+    float *xs = smem;              // nb * 32 floats, permuted
+    float *vbuf = smem + nb * 32;  // EX: [NSLOT][RS][vrow] block values; else [NSLOT * nw][RS] wave sums
+    float *pad = vbuf + (EX ? NSLOT * RS * vrow : NSLOT * nw * RS);
+
+    const int st_begin = 8 * b_begin;
+    const int st_end = 8 * b_end;
+    const int st_clamp = max(st_end - 1, 0);
+    f32x4 xv[Q8_GEMV_STAGE];
+#pragma unroll
+    for (int u = 0; u < Q8_GEMV_STAGE; u++) {
+        const float *xp = xg + 4 * min(st_begin + lane + 64 * u, st_clamp);
+        xv[u] = (f32x4){xp[0], xp[1], xp[2], xp[3]};
+    }
+    // folded norm (gemv_body's): q8_rmsnorm_row's sum of squares in threads
+    // 0..255 from x loads issued before the weights and summed after; EX
+    // stages (x * scale) * w after a barrier, bit-identical to the tile
+    // kernel, else x * w with the scale applied to the row sums
+    const bool norm = a.norm_w != nullptr;  // kernel-uniform
+    const int rope_position = a.rope_pos ? *a.rope_pos : 0;
+    f32x4 wv[Q8_GEMV_STAGE];
+    f32x4 nx[Q8_NORM_ROW_VEC];
+    const int nv = nb * 8;
+    if (norm) {
+        const f32x4 *nwp = reinterpret_cast<const f32x4 *>(a.norm_w);
+#pragma unroll
+        for (int u = 0; u < Q8_GEMV_STAGE; u++) wv[u] = nwp[min(st_begin + lane + 64 * u, st_clamp)];
+        if (threadIdx.x < 256) {
+            const f32x4 *xr = reinterpret_cast<const f32x4 *>(xg);
+#pragma unroll
+            for (int jj = 0; jj < Q8_NORM_ROW_VEC; jj++) nx[jj] = xr[min((int)threadIdx.x + 256 * jj, nv - 1)];
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // the weight stream goes out before anything waits for x
+    i32x4 qv[NL];
+    unsigned dd[NL];
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+        const int b = min(b_begin + i * BPL + j, b_last);
+        qv[i] = *(const i32x4 *)(qbase + (size_t)b * Q8_UNIT_BYTES);
+        dd[i] = (unsigned)sbase[(size_t)b * Q8_TILE_ROWS];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __shared__ double npart[4];
+    if (norm && threadIdx.x < 256) {
+        double ss = 0.0;
+#pragma unroll
+        for (int jj = 0; jj < Q8_NORM_ROW_VEC; jj++) {
+            if ((int)threadIdx.x + 256 * jj < nv) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) ss += (double)(nx[jj][e] * nx[jj][e]);
+            }
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+        if (lane == 0) npart[wave] = ss;
+    }
+    if (norm) {
+        float nscale = 1.0f;
+        if constexpr (EX) {
+            __syncthreads();
+            nscale = norm_scale(npart, nb * 32, a.norm_eps);
+        }
+#pragma unroll
+        for (int u = 0; u < Q8_GEMV_STAGE; u++) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) xv[u][e] = EX ? (xv[u][e] * nscale) * wv[u][e] : xv[u][e] * wv[u][e];
+        }
+    }
+    if (EX && w == 0 && lane < RS) {
+        for (int b = nb; b < ((nb + 3) & ~3); b++) vbuf[(slot * RS + r) * vrow + b] = 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < Q8_GEMV_STAGE; u++) {
+        if (64 * u < st_end - st_begin) {
+            const int i = st_begin + lane + 64 * u;
+            float *d = i < st_end ? xs + (i >> 3) * 32 + ((i & 7) >> 1) + 4 * (i & 1) : pad;
+            d[0] = xv[u].x;
+            d[8] = xv[u].y;
+            d[16] = xv[u].z;
+            d[24] = xv[u].w;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    float lsum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+        const int bu = b_begin + i * BPL + j;
+        const int b = min(bu, b_last);
+        const float p = half_partial(qv[i], (const f32x4 *)(xs + b * 32 + h * 16));
+        float s01;
+        if constexpr (RS == 8) {
+            s01 = p + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(p), 0x128, 0xf, 0xf, false));
+        } else {
+            const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(p), __float_as_uint(p), false, false);
+            s01 = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        }
+        const float v = f16_to_f32(dd[i]) * s01;
+        if constexpr (EX) {
+            *((h == 0 && bu < b_end) ? vbuf + (slot * RS + r) * vrow + bu : pad) = v;
+        } else {
+            lsum = bu < b_end ? lsum + v : lsum;
+        }
+    }
+    if constexpr (!EX) {
+        if constexpr (BPL >= 4) lsum = lsum + __shfl_xor(lsum, 16);
+        if constexpr (BPL >= 2) lsum = lsum + __shfl_xor(lsum, 32);
+        if (lane < RS) vbuf[wave * RS + r] = lsum;
+    }
+    __syncthreads();
+    if (wave != 0 || lane >= RS) return;
+    float sums[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int sl = 0; sl < NSLOT; sl++) {
+        if constexpr (EX) {
+            sums[sl] = chain_row(vbuf + (sl * RS + r) * vrow, nb);
+        } else {
+            float acc = vbuf[(sl * nw) * RS + r];
+            for (int w2 = 1; w2 < nw; w2++) acc = acc + vbuf[(sl * nw + w2) * RS + r];
+            sums[sl] = acc;
+        }
+    }
+    if (!EX && norm) {  // the norm's scale, applied to the row sums
+        const float s = norm_scale(npart, nb * 32, a.norm_eps);
+        sums[0] *= s;
+        sums[1] *= s;
+    }
+    const int row = tile * Q8_TILE_ROWS + srow;
+    if constexpr (SILU) {
+        if (row < mrows) my[row] = silu_f32(sums[0]) * sums[1];
+    } else if (a.rope_pos) {
+        // gemv_body's RoPE + KV append: rows 2i and 2i+1 of a head are lanes
+        // r and r ^ 1 of wave 0 (RS is even, slices start at even rows)
+        const float other = __shfl_xor(sums[0], 1);
+        const int pos = rope_position;
+        const bool in_cache = pos >= 0 && pos < a.capacity;
+        if (row < mrows) {
+            const int d = row % a.head_dim;
+            const int pair = d >> 1;
+            const bool even = (d & 1) == 0;
+            const float x0 = even ? sums[0] : other;
+            const float x1 = even ? other : sums[0];
+            float y0 = x0, y1 = x1;
+            if (in_cache && mi < 2 && 2 * pair < a.n_rot) {
+                const float angle = (float)pos * a.rope_freq[pair];
+                float sn, cs;
+                sincosf(angle, &sn, &cs);
+                y0 = x0 * cs - x1 * sn;
+                y1 = x0 * sn + x1 * cs;
+            }
+            const float out = even ? y0 : y1;
+            if (mi == 0) {
+                my[row] = out;
+            } else if (in_cache) {
+                uint16_t *cache = mi == 1 ? a.kcache : a.vcache;
+                cache[(size_t)pos * mrows + row] = (uint16_t)f16_bits(out);
+            }
+        }
+    } else if (row < mrows) {
+        my[row] = mbias ? sums[0] + mbias[row] : sums[0];
+    }
+}
+
+#define Q8_GEMV_RSG_KERNEL(KIND, SILU, RS, NL)                                                                  \
+    extern "C" __global__ __launch_bounds__(1024) void q8_gemv_##KIND##RS##_l##NL(Q8GemvArgs a) {            \
+        gemv_rsg_body<RS, NL, 1, SILU>(a);                                                                     \
+    }                                                                                                          \
+    extern "C" __global__ __launch_bounds__(1024) void q8_gemv_##KIND##RS##_l##NL##_e0(Q8GemvArgs a) {       \
+        gemv_rsg_body<RS, NL, 0, SILU>(a);                                                                     \
+    }
+Q8_GEMV_RSG_KERNEL(g, 0, 8, 3)
+Q8_GEMV_RSG_KERNEL(g, 0, 16, 3)
+Q8_GEMV_RSG_KERNEL(g, 0, 16, 6)
+Q8_GEMV_RSG_KERNEL(s, 1, 8, 3)
+Q8_GEMV_RSG_KERNEL(s, 1, 16, 6)
 
 // ---------------------------------------------------------------------------
 // Activation quantization (quant.rs:98-121), into the prepared tile layout.

@@ -75,6 +75,8 @@ enum Fn {
     F_GEMV_RC8_3, F_GEMV_RC8_6, F_GEMV_RC16_3, F_GEMV_RC16_6,
     F_GEMV_R8_3_E0, F_GEMV_R8_6_E0, F_GEMV_R16_3_E0, F_GEMV_R16_6_E0,
     F_GEMV_RC8_3_E0, F_GEMV_RC8_6_E0, F_GEMV_RC16_3_E0, F_GEMV_RC16_6_E0,
+    F_GEMV_G8_3, F_GEMV_G16_3, F_GEMV_G16_6, F_GEMV_S8_3, F_GEMV_S16_6,
+    F_GEMV_G8_3_E0, F_GEMV_G16_3_E0, F_GEMV_G16_6_E0, F_GEMV_S8_3_E0, F_GEMV_S16_6_E0,
     F_QUANTIZE,
     F_GEMM_S0_T1, F_GEMM_S1_T1, F_GEMM_S1_T2, F_GEMM_S1_T4,
     F_GEMM_H_T1_R4, F_GEMM_H_T2_R2, F_GEMM_H_T2_R4,
@@ -103,6 +105,8 @@ const char *const kFnNames[F_COUNT] = {
     "q8_gemv_rc8_l3", "q8_gemv_rc8_l6", "q8_gemv_rc16_l3", "q8_gemv_rc16_l6",
     "q8_gemv_r8_l3_e0", "q8_gemv_r8_l6_e0", "q8_gemv_r16_l3_e0", "q8_gemv_r16_l6_e0",
     "q8_gemv_rc8_l3_e0", "q8_gemv_rc8_l6_e0", "q8_gemv_rc16_l3_e0", "q8_gemv_rc16_l6_e0",
+    "q8_gemv_g8_l3", "q8_gemv_g16_l3", "q8_gemv_g16_l6", "q8_gemv_s8_l3", "q8_gemv_s16_l6",
+    "q8_gemv_g8_l3_e0", "q8_gemv_g16_l3_e0", "q8_gemv_g16_l6_e0", "q8_gemv_s8_l3_e0", "q8_gemv_s16_l6_e0",
     "q8_quantize",
     "q8_gemm_s0_t1", "q8_gemm_s1_t1", "q8_gemm_s1_t2", "q8_gemm_s1_t4",
     "q8_gemm_h_t1_r4", "q8_gemm_h_t2_r2", "q8_gemm_h_t2_r4",
@@ -453,6 +457,32 @@ int run_gemv_rs(q8_ctx *c, const q8_weight *w, float *y, q8_dptr x, const float 
     return launch(c, f, (unsigned)grid, (unsigned)(waves * 64), lds, &a, sizeof a);
 }
 
+// Row-slice shape of a multi-matrix decode launch (q8_gemv_g* for a group,
+// q8_gemv_s* for the gate/up pair): rows per slice and loads per lane from
+// the options "gemv.group_rows" (8 or 16; unset, 0 or 32: the tile kernel,
+// which measured faster on the decode step's QKV and gate/up shapes) and
+// "gemv.group_loads".  False when no built variant fits: more than 16 waves, or a folded
+// norm without the 256 threads its reduction takes.
+bool rsg_shape(q8_ctx *c, int nb, int silu, bool norm, int *rs, int *nl, int *nw) {
+    const int rows = option(c, "gemv.group_rows", -1);
+    if (rows <= 0 || rows == 32) return false;  // default: the tile kernel (faster at the decode shapes)
+    int r = rows;
+    int l = option(c, "gemv.group_loads", -1);
+    if (l <= 0) l = 3;
+    if (silu && r == 16) l = 6;  // built pair variants: s8_l3, s16_l6
+    if (silu && r == 8) l = 3;
+    if (!silu && r == 8) l = 3;  // built group variants: g8_l3, g16_l3, g16_l6
+    const int bpw = l * (64 / (2 * r));
+    const int waves_slot = (int)ceil_div(nb, bpw);
+    const int waves = waves_slot * (silu ? 2 : 1);
+    if (waves > 16) return false;
+    if (norm && (waves * 64 < 256 || nb * 32 > 1024 * Q8_NORM_ROW_VEC)) return false;
+    *rs = r;
+    *nl = l;
+    *nw = waves_slot;
+    return true;
+}
+
 // norm_w (device f32[k]) folds rmsnorm(x) * norm_w into a multi-matrix
 // launch (the caller checks gemv_folds_norm first); rope turns on the RoPE
 // epilogue of a three-member q, k, v group.
@@ -481,6 +511,35 @@ int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const floa
     if (count == 1 && !silu && !norm_w && !rope && t.kslices == 1 && (t.row_slice == 8 || t.row_slice == 16)) {
         const int rc = run_gemv_rs(c, m[0].w, m[0].y, x, bias, t.row_slice, t.slice_loads, comb, t.exact);
         if (rc != Q8_ERR_UNSUPPORTED) return rc;
+    }
+    int rs = 0, nl = 0, nw = 0;
+    if ((count > 1 || silu) && !comb && rsg_shape(c, nb, silu, norm_w != nullptr, &rs, &nl, &nw)) {
+        a.total_tiles = silu ? m[0].w->tiles : tile;
+        a.x = reinterpret_cast<const float *>(x);
+        a.nb = nb;
+        a.waves_per_tile = nw;
+        a.silu_pair = silu;
+        a.kslices = 1;
+        a.norm_w = norm_w;
+        a.norm_eps = norm_eps;
+        if (rope) {
+            a.rope_pos = rope->position;
+            a.rope_freq = rope->freq;
+            a.kcache = rope->kcache;
+            a.vcache = rope->vcache;
+            a.head_dim = rope->head_dim;
+            a.n_rot = rope->n_rot;
+            a.capacity = rope->capacity;
+        }
+        a.xcd_order = option(c, "gemv.xcd_order", 1) ? 1 : 0;
+        const long long grid =
+            (a.xcd_order ? ceil_div(a.total_tiles, 8) * 8 : (long long)a.total_tiles) * (Q8_TILE_ROWS / rs);
+        if (grid > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "gemv: grid of %lld workgroups", grid);
+        const unsigned lds = (unsigned)((nb * 32 + (t.exact ? slots * rs * Q8_GEMV_VROW(nb) : slots * nw * rs) +
+                                         Q8_GEMV_PAD_FLOATS) * 4);
+        const int vi = silu ? (rs == 8 ? 3 : 4) : (rs == 8 ? 0 : nl == 3 ? 1 : 2);
+        const Fn f = (Fn)((t.exact ? F_GEMV_G8_3 : F_GEMV_G8_3_E0) + vi);
+        return launch(c, f, (unsigned)grid, (unsigned)(nw * slots * 64), lds, &a, sizeof a);
     }
     if (t.pairs_per_wave > 12)
         return fail(Q8_ERR_UNSUPPORTED, "gemv: %d block pairs per wave exceeds the staging bound of 12",
@@ -557,6 +616,8 @@ bool gemv_folds_combine(q8_ctx *c, const q8_weight *w, int splits) {
 // workgroup sees all of x), >= 256 threads (the row norm's reduction shape)
 // and k within the row norm's reach.
 bool gemv_folds_norm(q8_ctx *c, const Member *m, int count, int k, int silu) {
+    int rs = 0, nl = 0, nw = 0;
+    if ((count > 1 || silu) && rsg_shape(c, k / 32, silu, true, &rs, &nl, &nw)) return true;
     int rows_total = 0;
     for (int i = 0; i < count; i++) rows_total += m[i].w->out;
     const int slots = silu ? 2 : 1;
@@ -1068,7 +1129,8 @@ void *q8_stream(q8_ctx *c) { return c ? (void *)c->stream : nullptr; }
 int q8_set_option(q8_ctx *c, const char *name, int value) {
     if (!c || !name) return fail(Q8_ERR_INVALID, "q8_set_option: bad arguments");
     static const char *const known[] = {"gemv.exact", "gemv.waves",  "gemv.pairs",     "gemv.slices",
-                                        "gemv.rows",  "gemv.loads", "gemv.xcd_order",
+                                        "gemv.rows",  "gemv.loads", "gemv.xcd_order", "gemv.group_rows",
+                                        "gemv.group_loads",
                                         "gemm.smode", "gemm.tpw",    "gemm.twaves",    "gemm.xcd_remap",
                                         "gemm.kwaves", "gemm.slices", "gemm.rwaves",    "gemm.f16",
                                         "gemm.pipe",  "gemm.lds",      "gemm.silu"};
@@ -1081,6 +1143,10 @@ int q8_set_option(q8_ctx *c, const char *name, int value) {
         return fail(Q8_ERR_INVALID, "gemv.rows must be 8, 16 or 32 (32: the tile kernel)");
     if (std::strcmp(name, "gemv.loads") == 0 && value > 0 && value != 3 && value != 6)
         return fail(Q8_ERR_INVALID, "gemv.loads must be 3 or 6");
+    if (std::strcmp(name, "gemv.group_rows") == 0 && value > 0 && value != 8 && value != 16 && value != 32)
+        return fail(Q8_ERR_INVALID, "gemv.group_rows must be 0 or 32 (the tile kernel), 8 or 16");
+    if (std::strcmp(name, "gemv.group_loads") == 0 && value > 0 && value != 3 && value != 6)
+        return fail(Q8_ERR_INVALID, "gemv.group_loads must be 3 or 6");
     std::lock_guard<std::recursive_mutex> lock(c->mu);
     c->options[name] = value;
     return Q8_OK;
