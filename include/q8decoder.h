@@ -81,6 +81,19 @@ int q8_embeddings_device(q8_ctx *ctx, const q8_weight *weight, q8_dptr tokens, s
  * returning it: the greedy token fed back to the next step on the device. */
 int q8_argmax_device(q8_ctx *ctx, q8_dptr values, size_t offset, size_t len, q8_dptr result);
 
+/* The output norm, lm_head and greedy choice of a decode step (model.rs
+ * output_norm + lm_head, 806-832; sampler.rs:167-175 argmax): logits =
+ * weight . (rmsnorm(x) * norm_weight) (norm_weight null: no norm) written to
+ * `logits`, and the first index of their maximum (NaN never wins; a NaN at
+ * index 0 gives 0) written as a u32 to device memory at `result`.  The norm
+ * (q8_rmsnorm's kernel), then the GEMV, whose epilogue also leaves each
+ * 32-row tile's best candidate, then one workgroup that picks among them
+ * (q8_argmax's second stage): the argmax never reads the logits back (shapes
+ * whose GEMV splits K take the two-stage argmax).  Bit-identical to
+ * q8_rmsnorm + q8_matmul + q8_argmax_device. */
+int q8_norm_lm_head_argmax(q8_ctx *ctx, const float *norm_weight, float eps, const q8_weight *weight, q8_dptr x,
+                           size_t x_offset, q8_dptr logits, size_t logits_offset, q8_dptr result);
+
 /* *position += by, on the device (the end of a captured step). */
 int q8_advance_position(q8_ctx *ctx, q8_dptr position, int by);
 

@@ -73,7 +73,7 @@ struct q8_decoder {
     std::vector<Layer> layers;
     const q8_weight *embd = nullptr;
     std::vector<float> output_norm;
-    q8_dptr x = 0, normed = 0, q = 0, act = 0, logits = 0;
+    q8_dptr x = 0, q = 0, act = 0, logits = 0;
     q8_dptr pos = 0, tokens = 0;
     int position = 0;  // host mirror of *pos
     std::map<std::pair<int, int>, void *> graphs;
@@ -171,9 +171,7 @@ int q8_decoder::body(int n, int splits) {
         }
     }
     // output norm of the last row, lm_head, greedy choice into the token slot
-    DEC_TRY(q8_rmsnorm(c, x, (size_t)(n - 1) * E, output_norm.data(), E, g.eps, 1, normed, 0));
-    DEC_TRY(q8_matmul(c, embd, normed, 0, 1, logits, 0, nullptr, 0, 0));
-    DEC_TRY(q8_argmax_device(c, logits, 0, (size_t)g.n_vocab, tokens));
+    DEC_TRY(q8_norm_lm_head_argmax(c, output_norm.data(), g.eps, embd, x, (size_t)(n - 1) * E, logits, 0, tokens));
     return q8_advance_position(c, pos, n);
 }
 
@@ -271,7 +269,7 @@ int q8_decoder_create_synthetic(q8_ctx *c, const q8_decoder_config *config, uint
         if ((rc = d->alloc(cache, &L.kcache)) || (rc = d->alloc(cache, &L.vcache))) return fail(rc);
     }
     const size_t f = sizeof(float);
-    if ((rc = d->alloc((size_t)B * E * f, &d->x)) || (rc = d->alloc((size_t)B * E * f, &d->normed)) ||
+    if ((rc = d->alloc((size_t)B * E * f, &d->x)) ||
         (rc = d->alloc((size_t)B * g.n_head * g.head_dim * f, &d->q)) ||
         (rc = d->alloc((size_t)B * g.n_ff * f, &d->act)) || (rc = d->alloc((size_t)g.n_vocab * f, &d->logits)) ||
         (rc = d->alloc(256, &d->pos)) || (rc = d->alloc((size_t)B * 4, &d->tokens)))

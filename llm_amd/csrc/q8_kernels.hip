@@ -219,6 +219,15 @@ static __device__ __forceinline__ float norm_scale(const double *npart, int k, f
     return 1.0f / sqrtf(mean_square + eps);
 }
 
+// The greedy argmax's order (sampler.rs:167-175, q8_argmax below): a larger
+// value wins, equal values go to the lower index, index 0xffffffff (no
+// candidate) loses to anything.
+static __device__ __forceinline__ bool better(float av, unsigned ai, float bv, unsigned bi) {
+    if (ai == 0xffffffffu) return false;
+    if (bi == 0xffffffffu) return true;
+    return av > bv || (av == bv && ai < bi);
+}
+
 // Float4 slots of x one lane stages: a wave covers at most
 // 64 * Q8_GEMV_STAGE / 16 = 12 block pairs (the host's tactic keeps to it).
 #define Q8_GEMV_STAGE 3
@@ -530,7 +539,9 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
         if (threadIdx.x < 256) {
             const f32x4 *xr = reinterpret_cast<const f32x4 *>(xg);
 #pragma unroll
-            for (int j = 0; j < Q8_NORM_ROW_VEC; j++) nx[j] = xr[min((int)threadIdx.x + 256 * j, nv - 1)];
+            for (int j = 0; j < Q8_NORM_ROW_VEC; j++) {  // only the float4s the sum takes
+                if ((int)threadIdx.x + 256 * j < nv) nx[j] = xr[threadIdx.x + 256 * j];
+            }
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -748,9 +759,28 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
                 cache[(size_t)pos * mrows + row] = (uint16_t)f16_bits(out);
             }
         }
-    } else if (row < mrows) {
+    } else {
         const float out = mbias ? sums[0] + mbias[row] : sums[0];
-        my[row] = out;
+        if (row < mrows) my[row] = out;
+        if (a.amax_value) {
+            // this tile's greedy-argmax candidate: the best (value, lowest
+            // row) of its 32 outputs, NaN and padding rows excluded
+            float bv = out;
+            unsigned bi = (row < mrows && out == out) ? (unsigned)row : 0xffffffffu;
+#pragma unroll
+            for (int m = 16; m >= 1; m >>= 1) {
+                const float ov = __shfl_xor(bv, m);
+                const unsigned oi = (unsigned)__shfl_xor((int)bi, m);
+                if (better(ov, oi, bv, bi)) {
+                    bv = ov;
+                    bi = oi;
+                }
+            }
+            if (lane == 0) {
+                a.amax_value[gtile] = bv;
+                a.amax_index[gtile] = bi;
+            }
+        }
     }
 }
 
@@ -1083,7 +1113,9 @@ static __device__ __forceinline__ void gemv_rsg_body(const Q8GemvArgs &a) {
         if (threadIdx.x < 256) {
             const f32x4 *xr = reinterpret_cast<const f32x4 *>(xg);
 #pragma unroll
-            for (int jj = 0; jj < Q8_NORM_ROW_VEC; jj++) nx[jj] = xr[min((int)threadIdx.x + 256 * jj, nv - 1)];
+            for (int jj = 0; jj < Q8_NORM_ROW_VEC; jj++) {  // only the float4s the sum takes
+                if ((int)threadIdx.x + 256 * jj < nv) nx[jj] = xr[threadIdx.x + 256 * jj];
+            }
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -2328,11 +2360,6 @@ extern "C" __global__ __launch_bounds__(512) void q8_gemm_s1_t4(Q8GemmArgs a) { 
 // reduction below keeps exactly that rule: best = (value, lowest index) over
 // the non-NaN values, then index 0 if values[0] is NaN.
 // ---------------------------------------------------------------------------
-static __device__ __forceinline__ bool better(float av, unsigned ai, float bv, unsigned bi) {
-    if (ai == 0xffffffffu) return false;
-    if (bi == 0xffffffffu) return true;
-    return av > bv || (av == bv && ai < bi);
-}
 
 extern "C" __global__ __launch_bounds__(256) void q8_argmax(Q8ArgmaxArgs a) {
     __shared__ float sv[256];
@@ -2351,12 +2378,23 @@ extern "C" __global__ __launch_bounds__(256) void q8_argmax(Q8ArgmaxArgs a) {
             }
         }
     } else {
-        for (int i = threadIdx.x; i < a.parts; i += blockDim.x) {
-            const float v = a.part_value[i];
-            const unsigned ix = a.part_index[i];
-            if (better(v, ix, bv, bi)) {
-                bv = v;
-                bi = ix;
+        // eight candidates a thread per round, all loaded before any is
+        // compared (the order does not matter: `better` is a total order)
+        for (int i0 = threadIdx.x; i0 < a.parts; i0 += 8 * (int)blockDim.x) {
+            float v[8];
+            unsigned ix[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int i = i0 + u * (int)blockDim.x;
+                v[u] = i < a.parts ? a.part_value[i] : 0.0f;
+                ix[u] = i < a.parts ? a.part_index[i] : 0xffffffffu;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                if (better(v[u], ix[u], bv, bi)) {
+                    bv = v[u];
+                    bi = ix[u];
+                }
             }
         }
     }

@@ -141,6 +141,11 @@ typedef struct {
      * (one XCD under round-robin dispatch; the grid is padded to whole
      * groups of eight tiles), 0 = consecutive workgroups. */
     int xcd_order;
+    /* Greedy-argmax partials of a one-matrix tile-kernel launch (the lm_head):
+     * non-null, each 32-row tile writes its best (value, lowest index) over
+     * its non-NaN outputs to [tile], or index 0xffffffff if it has none. */
+    float *amax_value;
+    unsigned *amax_index;
 } Q8GemvArgs;
 
 /* float4s per thread of the 256-thread row RMSNorm (k <= 1024 * this). */

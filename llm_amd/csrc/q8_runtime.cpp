@@ -124,6 +124,9 @@ const char *const kFnNames[F_COUNT] = {
 };
 
 constexpr int kArgmaxParts = 1024;
+// Partials the argmax workspace holds: the lm_head GEMV writes one per 32-row
+// tile (122880 rows: 3840), the two-stage argmax kArgmaxParts.
+constexpr int kArgmaxMaxParts = 65536;
 // Split-K scratch, allocated once at open: 32 MiB of partial results and
 // 65536 arrival counters (zeroed once; each launch's last workgroup re-zeroes
 // the counters it used, so no memset is ever recorded into a graph).
@@ -488,9 +491,16 @@ bool rsg_shape(q8_ctx *c, int nb, int silu, bool norm, int *rs, int *nl, int *nw
 // epilogue of a three-member q, k, v group.
 // comb builds x from attention partials instead (the caller checks
 // gemv_folds_combine first; x is then unused).
+// amax: a one-matrix launch also writes each tile's greedy-argmax candidate
+// (the tile kernel's epilogue; row slices are not taken).
+struct GemvArgmax {
+    float *value;
+    unsigned *index;
+};
+
 int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const float *bias, int silu,
              const float *norm_w = nullptr, float norm_eps = 0.0f, const GemvRope *rope = nullptr,
-             const GemvCombine *comb = nullptr) {
+             const GemvCombine *comb = nullptr, const GemvArgmax *amax = nullptr) {
     const int nb = k / 32;
     int rows_total = 0;
     Q8GemvArgs a{};
@@ -508,7 +518,10 @@ int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const floa
     }
     const int slots = silu ? 2 : 1;
     const q8_tactic t = plan(c, 1, silu ? m[0].w->out : rows_total, k, slots);
-    if (count == 1 && !silu && !norm_w && !rope && t.kslices == 1 && (t.row_slice == 8 || t.row_slice == 16)) {
+    if (amax && (count != 1 || silu || rope || comb))
+        return fail(Q8_ERR_INVALID, "gemv: argmax partials come from one plain matrix");
+    if (count == 1 && !silu && !norm_w && !rope && !amax && t.kslices == 1 &&
+        (t.row_slice == 8 || t.row_slice == 16)) {
         const int rc = run_gemv_rs(c, m[0].w, m[0].y, x, bias, t.row_slice, t.slice_loads, comb, t.exact);
         if (rc != Q8_ERR_UNSUPPORTED) return rc;
     }
@@ -572,6 +585,11 @@ int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const floa
         a.attn_ms = comb->ms;
         a.attn_splits = comb->splits;
     }
+    if (amax) {
+        if (tile > kArgmaxMaxParts) return fail(Q8_ERR_UNSUPPORTED, "argmax over %d tiles", tile);
+        a.amax_value = amax->value;
+        a.amax_index = amax->index;
+    }
     const int waves = t.waves_per_tile * slots;
     const int max_threads = pb == 9 ? 512 : 1024;
     if (norm_w && (t.kslices != 1 || waves * 64 < 256 || k > 1024 * Q8_NORM_ROW_VEC))
@@ -584,7 +602,7 @@ int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const floa
                     max_threads);
     if (t.kslices > 1) {
         const size_t need = (size_t)slots * a.total_tiles * (t.exact ? nb : t.kslices) * 32 * sizeof(float);
-        if (need > kSplitBytes || a.total_tiles > kCounters)
+        if (need > kSplitBytes || a.total_tiles > kAttnCounterBase)
             return fail(Q8_ERR_UNSUPPORTED, "gemv: split-K needs %zu bytes of scratch for %d tiles", need,
                         a.total_tiles);
     }
@@ -763,7 +781,7 @@ int run_gemm(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n,
     const long long groups = (long long)rt * a.tgroups;
     if (a.kslices > 1) {
         const size_t need = (size_t)rt * a.ttiles * a.kslices * 64 * 16 * sizeof(float);
-        if (need > kSplitBytes || groups > kCounters)
+        if (need > kSplitBytes || groups > kAttnCounterBase)
             return fail(Q8_ERR_UNSUPPORTED, "gemm: split-K needs %zu bytes of scratch", need);
     }
     const long long nwg = groups * a.kslices;
@@ -965,8 +983,8 @@ int argmax_into(q8_ctx *c, q8_dptr values, size_t len, uint32_t *out) {
     a.values = reinterpret_cast<const float *>(values);
     a.len = (long long)len;
     a.part_value = reinterpret_cast<float *>(ws);
-    a.part_index = reinterpret_cast<unsigned *>(ws + kArgmaxParts * 4);
-    a.result = reinterpret_cast<unsigned *>(ws + kArgmaxParts * 8);
+    a.part_index = reinterpret_cast<unsigned *>(ws + kArgmaxMaxParts * 4);
+    a.result = reinterpret_cast<unsigned *>(ws + kArgmaxMaxParts * 8);
     const int parts = (int)std::min<long long>(kArgmaxParts, std::max<long long>(1, ceil_div((long long)len, 4096)));
     a.parts = parts;
     a.stage = 0;
@@ -1057,7 +1075,7 @@ int q8_open(int device, q8_ctx **out) {
                           hipGetErrorString(he));
         }
         if (rc != Q8_OK) break;
-        he = dev_malloc(c, &c->argmax_ws, kArgmaxParts * 8 + 256);
+        he = dev_malloc(c, &c->argmax_ws, kArgmaxMaxParts * 8 + 256);
         if (he != hipSuccess) { rc = hip_fail(he, "hipMalloc(argmax)"); break; }
         he = dev_malloc(c, (void **)&c->probe_sink, 256);
         if (he != hipSuccess) { rc = hip_fail(he, "hipMalloc(probe sink)"); break; }
@@ -1788,9 +1806,62 @@ int q8_lm_head_argmax(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset,
     if (!c || !argmax) return fail(Q8_ERR_INVALID, "q8_lm_head_argmax: bad arguments");
     Q8_TRY(check_weight(c, w));
     std::lock_guard<std::recursive_mutex> lock(c->mu);
-    q8_group_entry e{w, logits, logits_offset};
-    Q8_TRY(q8_matmul_decode_group(c, &e, 1, x, x_offset, w->k, 0, 0));
-    return argmax_into(c, (q8_dptr)(uintptr_t)fptr(logits, logits_offset), (size_t)w->out, argmax);
+    uint8_t *ws = static_cast<uint8_t *>(c->argmax_ws);
+    const q8_dptr slot = (q8_dptr)(uintptr_t)(ws + (size_t)kArgmaxMaxParts * 8);
+    Q8_TRY(q8_norm_lm_head_argmax(c, nullptr, 0.0f, w, x, x_offset, logits, logits_offset, slot));
+    uint32_t result = 0;
+    HIP_TRY(hipMemcpyAsync(&result, reinterpret_cast<void *>(slot), 4, hipMemcpyDeviceToHost, c->stream),
+            "hipMemcpyAsync(argmax)");
+    HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    *argmax = result;
+    return Q8_OK;
+}
+
+// Output norm, lm_head and greedy choice: the row norm into the norm
+// workspace (not folded: every one of the lm_head's thousands of workgroups
+// would sum the row's squares again, 63.8 against 49.4 + 3.7 us measured),
+// the GEMV, which writes the logits and each 32-row tile's best candidate,
+// and one workgroup of q8_argmax's second stage picking among the candidates
+// -- the argmax's first pass over the logits is gone.  Shapes whose GEMV
+// cannot carry the partials (a K split) run the two-stage argmax.
+int q8_norm_lm_head_argmax(q8_ctx *c, const float *norm_weight, float eps, const q8_weight *w, q8_dptr x,
+                           size_t x_offset, q8_dptr logits, size_t logits_offset, q8_dptr result) {
+    if (!c || !w) return fail(Q8_ERR_INVALID, "q8_norm_lm_head_argmax: bad arguments");
+    Q8_TRY(check_weight(c, w));
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    const int k = w->k;
+    const q8_dptr xp = (q8_dptr)(uintptr_t)fptr(x, x_offset);
+    Q8_TRY(check_span(c, xp, (size_t)k * 4, "lm_head x"));
+    float *yp = fptr(logits, logits_offset);
+    Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)yp, (size_t)w->out * 4, "lm_head logits"));
+    Q8_TRY(check_span(c, result, 4, "argmax result"));
+    q8_dptr xin = xp;
+    if (norm_weight) {
+        float *nw = nullptr;
+        Q8_TRY(vector_resident(c, norm_weight, (size_t)k, &nw));
+        Q8_TRY(grow(c, &c->norm_ws, &c->norm_ws_bytes, (size_t)k * sizeof(float), "hipMalloc(norm workspace)"));
+        Q8_TRY(run_rmsnorm(c, reinterpret_cast<const float *>(xp), 1, k, nw, eps, static_cast<float *>(c->norm_ws),
+                           nullptr));
+        xin = (q8_dptr)(uintptr_t)c->norm_ws;
+    }
+    Member m{w, yp};
+    const q8_tactic t = plan(c, 1, w->out, k, 1);
+    if (t.kslices == 1 && w->tiles <= kArgmaxMaxParts) {
+        uint8_t *ws = static_cast<uint8_t *>(c->argmax_ws);
+        const GemvArgmax amax{reinterpret_cast<float *>(ws), reinterpret_cast<unsigned *>(ws + kArgmaxMaxParts * 4)};
+        Q8_TRY(run_gemv(c, &m, 1, xin, k, nullptr, 0, nullptr, 0.0f, nullptr, nullptr, &amax));
+        Q8ArgmaxArgs a{};
+        a.values = yp;
+        a.len = w->out;
+        a.part_value = amax.value;
+        a.part_index = amax.index;
+        a.result = reinterpret_cast<unsigned *>(result);
+        a.parts = w->tiles;
+        a.stage = 1;
+        return launch(c, F_ARGMAX, 1, 256, 0, &a, sizeof a);
+    }
+    Q8_TRY(run_gemv(c, &m, 1, xin, k, nullptr, 0));
+    return q8_argmax_device(c, (q8_dptr)(uintptr_t)yp, 0, (size_t)w->out, result);
 }
 
 int q8_embeddings(q8_ctx *c, const q8_weight *w, const uint32_t *tokens, size_t n, q8_dptr out,
@@ -1845,7 +1916,7 @@ int q8_argmax_device(q8_ctx *c, q8_dptr values, size_t offset, size_t len, q8_dp
     a.values = reinterpret_cast<const float *>(v);
     a.len = (long long)len;
     a.part_value = reinterpret_cast<float *>(ws);
-    a.part_index = reinterpret_cast<unsigned *>(ws + kArgmaxParts * 4);
+    a.part_index = reinterpret_cast<unsigned *>(ws + kArgmaxMaxParts * 4);
     a.result = reinterpret_cast<unsigned *>(result);
     a.parts = (int)std::min<long long>(kArgmaxParts, std::max<long long>(1, ceil_div((long long)len, 4096)));
     a.stage = 0;

@@ -55,11 +55,10 @@ void q8_gemv_shape(int out, int k, int cu_count, int slots, q8_tactic *t) {
     const int npairs = ceil_div(nb, 2);
     const int cus = std::max(cu_count, 1);
     const int max_w = 16 / slots;
-    int w;
-    if (tiles >= 2 * cus)
-        w = std::min(std::min(4, max_w), npairs);
-    else
-        w = std::min(max_w, std::max(1, ceil_div(npairs, 3)));
+    // about three block pairs per wave, at any tile count: the lm_head
+    // (122880 x 2304, 3840 tiles) measured 46.3 us at four waves per tile and
+    // 42.7 us at twelve (one 301 MB copy, gfx950)
+    int w = std::min(max_w, std::max(1, ceil_div(npairs, 3)));
     int ppw = ceil_div(npairs, w);
     if (ppw > 12) ppw = 12;  // LDS staging bound of a wave
     w = ceil_div(npairs, ppw);

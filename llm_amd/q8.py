@@ -60,7 +60,7 @@ EXPORTS = (
     "q8_vector_release", "q8_norm_qkv_rope",
     "q8_weight_synthetic", "q8_decoder_create_synthetic", "q8_decoder_destroy", "q8_decoder_reset",
     "q8_decoder_position", "q8_decoder_forward", "q8_decoder_generate", "q8_decoder_logits", "q8_decoder_weight",
-    "q8_decoder_norm", "q8_decoder_graph_stats",
+    "q8_decoder_norm", "q8_decoder_graph_stats", "q8_norm_lm_head_argmax",
     "q8_workspace_plan", "q8_workspace_query", "q8_workspace_region", "q8_vector_resident",
 )
 
@@ -258,6 +258,7 @@ def lib():
         "q8_decoder_weight": (c_int, [vp, c_int, c_int, ctypes.POINTER(vp)]),
         "q8_decoder_norm": (c_int, [vp, c_int, c_int, ctypes.POINTER(ctypes.POINTER(ctypes.c_float))]),
         "q8_decoder_graph_stats": (c_int, [vp, ctypes.POINTER(DecoderStats)]),
+        "q8_norm_lm_head_argmax": (c_int, [vp, vp, ctypes.c_float, vp, u64, c_size, u64, c_size, u64]),
         "q8_workspace_plan": (c_int, [vp, ctypes.POINTER(WorkspaceShape)]),
         "q8_workspace_query": (c_int, [vp, ctypes.POINTER(WorkspaceInfo)]),
         "q8_workspace_region": (c_int, [vp, c_int, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(u64),
@@ -626,6 +627,13 @@ class Gpu:
 
     def embeddings_device(self, weight, tokens: DeviceBuffer, n: int, out: DeviceBuffer, out_offset: int = 0):
         _check(lib().q8_embeddings_device(self.handle, self.resident(weight), tokens.ptr, n, out.ptr, out_offset))
+
+    def norm_lm_head_argmax(self, weight, eps: float, lm_head: Weight, x: DeviceBuffer, x_offset: int,
+                            logits: DeviceBuffer, logits_offset: int, result: DeviceBuffer):
+        """Output norm (weight None: none) + lm_head GEMV + greedy argmax into device memory."""
+        w = self._norm_weight(weight).ctypes.data if weight is not None else None
+        _check(lib().q8_norm_lm_head_argmax(self.handle, w, float(eps), self.resident(lm_head), x.ptr, x_offset,
+                                            logits.ptr, logits_offset, result.ptr))
 
     def argmax_device(self, values: DeviceBuffer, offset: int, length: int, result: DeviceBuffer):
         _check(lib().q8_argmax_device(self.handle, values.ptr, offset, length, result.ptr))

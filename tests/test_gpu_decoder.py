@@ -530,6 +530,69 @@ def test_device_token_ops(gpu):
     assert int(pos.download(np.int32, 1)[0]) == 18
 
 
+@pytest.mark.parametrize("vocab,k,ties,nan,norm", [(122880, 2304, False, False, True), (1000, 256, False, False, True),
+                                                   (4096, 512, True, False, True), (4096, 512, True, False, False),
+                                                   (333, 96, False, True, True), (70000, 2304, True, False, False)])
+@pytest.mark.parametrize("exact", [1, 0])
+def test_norm_lm_head_argmax_equals_norm_matmul_argmax(gpu, vocab, k, ties, nan, norm, exact):
+    """q8_norm_lm_head_argmax (the lm_head GEMV leaving each tile's best
+    candidate, then one workgroup choosing) against q8_rmsnorm + q8_matmul +
+    q8_argmax_device: the same token, including equal maxima in different
+    tiles and inside a tile (the lowest index wins), a NaN input (every logit
+    NaN: token 0), a vocabulary that ends inside a tile, and no norm; the
+    logits bit-identical in exact mode (in the tree order within the f32 bar:
+    the partials need the tile kernel, where a small matmul takes row
+    slices); the token always equals the oracle's argmax over the device's
+    own logits."""
+    gpu.set_option("gemv.exact", exact)
+    r = np.random.default_rng(SEED + vocab + k)
+    data = oracle.make_q8_weight(r, vocab, k)
+    x = (r.standard_normal(k) * 2).astype(np.float32)
+    if nan:
+        x[5] = np.nan
+    nw = (1.0 + 0.1 * r.standard_normal(k)).astype(np.float32)
+    copies = (3, 17, 40, vocab // 2, vocab - 1)
+    if ties:  # the oracle's top row, its scales doubled (a clear maximum), copied: equal maxima across tiles
+        src = oracle.argmax(oracle.matmul(data, k, vocab, oracle.rmsnorm(x, nw, 1e-6) if norm else x, 1))
+        rows = data.reshape(vocab, -1)
+        blocks = rows[src].reshape(k // 32, 34)
+        d = blocks[:, :2].copy().view(np.float16)
+        blocks[:, :2] = (d.astype(np.float32) * 2).astype(np.float16).view(np.uint8).reshape(-1, 2)
+        rows[src] = blocks.reshape(-1)
+        for dst in copies:
+            rows[dst] = rows[src]
+    w = q8.Weight(data, k, vocab)
+    xb, xn, la, lb = gpu.alloc(4 * k), gpu.alloc(4 * k), gpu.alloc(4 * vocab), gpu.alloc(4 * vocab)
+    ta, tb = gpu.alloc(256), gpu.alloc(256)
+    xb.upload(x)
+    try:
+        print(f"\nlm_head argmax vocab={vocab} k={k} ties={ties} nan={nan} norm={norm} exact={exact}", flush=True)
+        if norm:
+            gpu.rmsnorm(xb, 0, nw, 1e-6, 1, xn, 0)
+            gpu.matmul(w, xn, 0, 1, la, 0)
+        else:
+            gpu.matmul(w, xb, 0, 1, la, 0)
+        gpu.argmax_device(la, 0, vocab, ta)
+        gpu.norm_lm_head_argmax(nw if norm else None, 1e-6, w, xb, 0, lb, 0, tb)
+        want, got = int(ta.download(np.uint32, 1)[0]), int(tb.download(np.uint32, 1)[0])
+        ga, gb = la.download(np.float32, vocab), lb.download(np.float32, vocab)
+        if exact:
+            assert_bits(gb, ga, "logits")
+            assert got == want
+        elif not nan:  # the tile kernel's block tree, where the plain matmul may take row slices
+            assert_close(gb, ga, "logits (tree order)")
+        assert got == oracle.argmax(gb), f"token {got}, oracle argmax of the same logits {oracle.argmax(gb)}"
+        if nan:
+            assert got == 0
+        if ties:
+            assert got == min(min(copies), src), f"token {got}: the lowest of the equal maxima is {min(min(copies), src)}"
+    finally:
+        gpu.set_option("gemv.exact", -1)
+        for b in (xb, xn, la, lb, ta, tb):
+            b.free()
+        gpu.release(w)
+
+
 def test_synthetic_weights_are_valid_q8_0_and_seeded(gpu):
     a = gpu.weight_synthetic(2304, 96, seed=7)
     b = gpu.weight_synthetic(2304, 96, seed=7)
