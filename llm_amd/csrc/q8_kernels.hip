@@ -211,6 +211,24 @@ static __device__ __forceinline__ float xor_max(float v) {
         return fmaxf(v, xor_partner<M>(v));
     }
 }
+
+// The same butterfly step on an f64 (the folded norm's sums of squares): both
+// 32-bit halves move with the same DPP or row swap.
+template <int M>
+static __device__ __forceinline__ double xor_add_f64(double v) {
+    const unsigned lo = (unsigned)__double2loint(v), hi = (unsigned)__double2hiint(v);
+    if constexpr (M == 16 || M == 32) {
+        const auto sl = M == 16 ? __builtin_amdgcn_permlane16_swap(lo, lo, false, false)
+                                : __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+        const auto sh = M == 16 ? __builtin_amdgcn_permlane16_swap(hi, hi, false, false)
+                                : __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+        return __hiloint2double((int)sh[0], (int)sl[0]) + __hiloint2double((int)sh[1], (int)sl[1]);
+    } else {
+        const float plo = xor_partner<M>(__uint_as_float(lo));
+        const float phi = xor_partner<M>(__uint_as_float(hi));
+        return v + __hiloint2double((int)__float_as_uint(phi), (int)__float_as_uint(plo));
+    }
+}
 // The folded RMSNorm's scale from q8_rmsnorm_row's four wave sums:
 // 1 / sqrt(mean square + eps), the mean square rounded once from f64.
 static __device__ __forceinline__ float norm_scale(const double *npart, int k, float eps) {
@@ -560,8 +578,12 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
                 for (int e = 0; e < 4; e++) ss += (double)(nx[j][e] * nx[j][e]);
             }
         }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+        ss = xor_add_f64<32>(ss);
+        ss = xor_add_f64<16>(ss);
+        ss = xor_add_f64<8>(ss);
+        ss = xor_add_f64<4>(ss);
+        ss = xor_add_f64<2>(ss);
+        ss = xor_add_f64<1>(ss);
         if (lane == 0) npart[wave] = ss;
     }
     float nscale = 1.0f;
@@ -968,8 +990,8 @@ static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
         // the BPL lanes of row r (load slots j) in a fixed order: xor 16
         // then xor 32 (RS = 8), xor 32 (RS = 16); both halves h hold the
         // same sums, lane r (j = 0, h = 0) keeps the wave's row sum
-        if constexpr (BPL >= 4) lsum = lsum + __shfl_xor(lsum, 16);
-        if constexpr (BPL >= 2) lsum = lsum + __shfl_xor(lsum, 32);
+        if constexpr (BPL >= 4) lsum = xor_add<16>(lsum);
+        if constexpr (BPL >= 2) lsum = xor_add<32>(lsum);
         if (lane < RS) vbuf[wave * RS + r] = lsum;
     }
     __syncthreads();
@@ -1139,8 +1161,12 @@ static __device__ __forceinline__ void gemv_rsg_body(const Q8GemvArgs &a) {
                 for (int e = 0; e < 4; e++) ss += (double)(nx[jj][e] * nx[jj][e]);
             }
         }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+        ss = xor_add_f64<32>(ss);
+        ss = xor_add_f64<16>(ss);
+        ss = xor_add_f64<8>(ss);
+        ss = xor_add_f64<4>(ss);
+        ss = xor_add_f64<2>(ss);
+        ss = xor_add_f64<1>(ss);
         if (lane == 0) npart[wave] = ss;
     }
     if (norm) {
@@ -1194,8 +1220,8 @@ static __device__ __forceinline__ void gemv_rsg_body(const Q8GemvArgs &a) {
         }
     }
     if constexpr (!EX) {
-        if constexpr (BPL >= 4) lsum = lsum + __shfl_xor(lsum, 16);
-        if constexpr (BPL >= 2) lsum = lsum + __shfl_xor(lsum, 32);
+        if constexpr (BPL >= 4) lsum = xor_add<16>(lsum);
+        if constexpr (BPL >= 2) lsum = xor_add<32>(lsum);
         if (lane < RS) vbuf[wave * RS + r] = lsum;
     }
     __syncthreads();
