@@ -22,10 +22,12 @@ per step) / median time per step.
 Also reported, each on its own rotation:
   ceilings      what one kernel of this size can do on this box: the best
                 plain streaming read of the configs[0] byte count (the
-                GEMV's achievable ceiling), an empty kernel's cost per graph
-                launch, the sustained int8 MFMA rate (v_mfma_i32_32x32x32_i8
-                only), VALU rate, and the GEMM's per-tile-block instruction
-                mix with operands in registers (its own ceiling);
+                GEMV's achievable ceiling) and of the decode step's launch
+                sizes, an empty kernel's cost per graph launch, the
+                sustained int8 MFMA rate (v_mfma_i32_32x32x32_i8 only), VALU
+                rate, and the GEMM's per-tile-block instruction mix with
+                operands in registers (its own ceiling), for the int8 and the
+                f16-MFMA families;
   gemm_n512     configs[3]: the layer's projections at n = 512 (QKV 6912,
                 O 2304 + residual, gate|up 2x5760 -> SiLU -> Q8_0, down
                 2304x5760 + residual) with the activation quantization, on
@@ -185,12 +187,33 @@ def bench_ceilings(gpu, steps, warmup, read_bytes):
     log("plain read of " + f"{read_bytes} B, MALL-cold: " +
         ", ".join(f"{n} {r['median_us']:.2f} us ({r['value']:.0f} GB/s)" for n, r in reads.items()))
     buf.free()
+    # the same ceiling at the byte counts of the decode step's launches
+    # (weights only): what one launch of that size can read on this box
+    decode_reads = {}
+    for name, nb in (("o", HID * HID // 32 * 34), ("qkv", 3 * HID * HID // 32 * 34),
+                     ("down", FFN * HID // 32 * 34), ("gate_up", 2 * FFN * HID // 32 * 34),
+                     ("lm_head", VOCAB * HID // 32 * 34)):
+        nbr = (nb + 15) // 16 * 16
+        cp = copies_for(nbr)
+        st = (nbr + 4095) // 4096 * 4096
+        rb = gpu.alloc(st * cp)
+        best_us = None
+        for which in (q8.PROBE_READ_L4, q8.PROBE_READ_L8, q8.PROBE_READ_L16):
+            ms = rotating_trials(gpu, lambda i, w=which: gpu.probe(w, rb, nbr, src_offset=i * st), cp,
+                                 max(cp, min(steps, 100)), min(warmup, 10))
+            us = statistics.median(ms) * 1e3
+            best_us = us if best_us is None else min(best_us, us)
+        rb.free()
+        decode_reads[name] = {"bytes": nb, "us": round(best_us, 3), "gbs": round(nb / (best_us * 1e-6) / 1e9, 1)}
+    log("plain reads at the decode launches' sizes, MALL-cold: " +
+        ", ".join(f"{n} {v['bytes'] / 1e6:.1f} MB {v['us']:.2f} us" for n, v in decode_reads.items()))
     empty = rotating_trials(gpu, lambda i: gpu.probe(q8.PROBE_EMPTY), 1, 200, 20)
     empty_us = statistics.median(empty) * 1e3
     cus = gpu.info()["cu_count"]
     wgs = 4 * cus  # four 4-wave workgroups a CU: four waves a SIMD
     rates = {}
-    for which, name, per_iter in ((q8.PROBE_MFMA, "mfma", 4), (q8.PROBE_VALU, "valu", 1), (q8.PROBE_MIX, "mix", 2)):
+    for which, name, per_iter in ((q8.PROBE_MFMA, "mfma", 4), (q8.PROBE_VALU, "valu", 1), (q8.PROBE_MIX, "mix", 2),
+                                  (q8.PROBE_MIX_F16, "mix_f16", 2)):
         iters = 2048 if which != q8.PROBE_VALU else 8192
         ms = rotating_trials(gpu, lambda i, w=which, it=iters: gpu.probe(w, iters=it, workgroups=wgs), 1, 3, 1)
         t = statistics.median(ms) * 1e-3
@@ -201,15 +224,17 @@ def bench_ceilings(gpu, steps, warmup, read_bytes):
     valu_ns = simds / (rates["valu"]["units_per_s"] * 32) * 1e9  # ns per wave64 VALU op per SIMD
     mix_ns = simds / rates["mix"]["units_per_s"] * 1e9            # ns per tile-block per SIMD
     mix_tops = rates["mix"]["units_per_s"] * 65536 / 1e12
+    mix16_ns = simds / rates["mix_f16"]["units_per_s"] * 1e9
     log(f"empty kernel {empty_us:.2f} us/launch; int8 MFMA only {mfma_tops:.0f} TOPS; VALU {valu_ns:.2f} ns/op/SIMD; "
-        f"GEMM tile-block mix {mix_ns:.1f} ns/SIMD = {mix_tops:.0f} TOPS")
+        f"GEMM tile-block mix {mix_ns:.1f} ns/SIMD = {mix_tops:.0f} TOPS (f16-MFMA family's mix {mix16_ns:.1f} ns)")
     return {"read_bytes": read_bytes, "read_copies": copies,
             "read_gbs": {n: round(r["value"], 1) for n, r in reads.items()},
             "read_us": {n: r["median_us"] for n, r in reads.items()},
             "ceiling_gbs": round(reads[best]["value"], 1), "ceiling_kernel": f"q8_probe_read_{best}",
             "empty_kernel_us_per_launch": round(empty_us, 3),
             "mfma_i8_tops": round(mfma_tops, 1), "valu_ns_per_op_per_simd": round(valu_ns, 3),
-            "tile_block_mix_ns_per_simd": round(mix_ns, 2), "tile_block_mix_tops": round(mix_tops, 1)}
+            "tile_block_mix_ns_per_simd": round(mix_ns, 2), "tile_block_mix_tops": round(mix_tops, 1),
+            "tile_block_mix_f16_ns_per_simd": round(mix16_ns, 2), "decode_launch_reads": decode_reads}
 
 
 # ---------------------------------------------------------------------------

@@ -90,7 +90,10 @@ int q8_argmax_device(q8_ctx *ctx, q8_dptr values, size_t offset, size_t len, q8_
  * 32-row tile's best candidate, then one workgroup that picks among them
  * (q8_argmax's second stage): the argmax never reads the logits back (shapes
  * whose GEMV splits K take the two-stage argmax).  Bit-identical to
- * q8_rmsnorm + q8_matmul + q8_argmax_device. */
+ * q8_rmsnorm + q8_matmul + q8_argmax_device with "gemv.exact" = 1, and in
+ * the default block order wherever q8_matmul also runs the tile kernel (the
+ * lm_head shapes: more row tiles than CUs); where q8_matmul takes row slices
+ * instead, the two orders agree within 2e-6 + 1e-5 |ref|. */
 int q8_norm_lm_head_argmax(q8_ctx *ctx, const float *norm_weight, float eps, const q8_weight *weight, q8_dptr x,
                            size_t x_offset, q8_dptr logits, size_t logits_offset, q8_dptr result);
 

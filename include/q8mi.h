@@ -341,7 +341,10 @@ int q8_embeddings(q8_ctx *ctx, const q8_weight *weight, const uint32_t *tokens, 
  *   Q8_PROBE_MIX             `iters` GEMM tile-blocks per wave with operands
  *                            in registers: an int8 MFMA, half an f32
  *                            outer-product MFMA and 32 VALU each;
- * the last three over `workgroups` workgroups of four waves (iters even). */
+ *   Q8_PROBE_MIX_F16         the same for the f16-MFMA family: two
+ *                            v_mfma_f32_32x32x16_f16, half an outer-product
+ *                            MFMA and 16 fma per tile-block;
+ * the last four over `workgroups` workgroups of four waves (iters even). */
 enum {
     Q8_PROBE_READ_L4 = 0,
     Q8_PROBE_READ_L8 = 1,
@@ -349,7 +352,8 @@ enum {
     Q8_PROBE_EMPTY = 3,
     Q8_PROBE_MFMA = 4,
     Q8_PROBE_VALU = 5,
-    Q8_PROBE_MIX = 6
+    Q8_PROBE_MIX = 6,
+    Q8_PROBE_MIX_F16 = 7
 };
 int q8_probe(q8_ctx *ctx, int which, q8_dptr src, size_t bytes, int iters, int workgroups);
 

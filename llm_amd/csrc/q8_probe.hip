@@ -18,7 +18,11 @@
 //                            scale MFMA (v_mfma_f32_32x32x1_2b_f32 per block
 //                            pair) and the 32 VALU of the block scale, with
 //                            the next pair's MFMAs issued before this pair's
-//                            VALU (what overlap one wave can get).
+//                            VALU (what overlap one wave can get);
+//   q8_probe_mix_f16         the same tile-blocks for the f16-MFMA family:
+//                            two v_mfma_f32_32x32x16_f16 per block (the exact
+//                            integer dot, already f32), half a scale-product
+//                            MFMA and 16 fma (no converts).
 // Results feed `sink` only when equal to `never` (the host passes a value no
 // result takes), so no work is dead and nothing is written.
 
@@ -121,6 +125,56 @@ extern "C" __global__ __launch_bounds__(256) void q8_probe_mix(Q8ProbeArgs a) {
     for (int it = 0; it < a.iters; it += 2) {
         Q8_PROBE_PAIR(i0, i1, sc, j0, j1, tc);
         Q8_PROBE_PAIR(j0, j1, tc, i0, i1, sc);
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) s += acc[i];
+    if (__float_as_uint(s) == a.never) a.sink[0] = 1u;
+}
+
+// The f16-MFMA family's tile-block: the block dot as two K = 16 f16 MFMAs
+// (quants are exact in f16) straight into f32, then acc += dot * (d_w s_x)
+// from the outer-product MFMA; same software pipeline as q8_probe_mix.
+#define Q8_PROBE_F16_DOT(xa, xb, wa, wb)                                                                   \
+    __builtin_amdgcn_mfma_f32_32x32x16_f16(                                                              \
+        __builtin_bit_cast(f16x8, xb), __builtin_bit_cast(f16x8, wb),                                    \
+        __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, xa), __builtin_bit_cast(f16x8, wa), \
+                                               f16zero, 0, 0, 0),                                        \
+        0, 0, 0)
+#define Q8_PROBE_F16_PAIR(ca, cb, sc, na, nb, nsc)                                                       \
+    do {                                                                                                 \
+        asm volatile("" : "+v"(hx0), "+v"(hx1), "+v"(hy0), "+v"(hy1), "+v"(hw0), "+v"(hw1), "+v"(hv0), "+v"(hv1)); \
+        asm volatile("" : "+v"(sx));                                                                     \
+        na = Q8_PROBE_F16_DOT(hx0, hx1, hw0, hw1);                                                       \
+        nb = Q8_PROBE_F16_DOT(hy0, hy1, hv0, hv1);                                                       \
+        nsc = __builtin_amdgcn_mfma_f32_32x32x1f32(sx, dw, fzero, 0, 0, 0);                              \
+        _Pragma("unroll") for (int i = 0; i < 16; i++) acc[i] = __builtin_fmaf(ca[i], sc[i], acc[i]);    \
+        _Pragma("unroll") for (int i = 0; i < 16; i++) acc[i] = __builtin_fmaf(cb[i], sc[16 + i], acc[i]); \
+    } while (0)
+
+extern "C" __global__ __launch_bounds__(256) void q8_probe_mix_f16(Q8ProbeArgs a) {
+    const int lane = threadIdx.x & 63;
+    // small integers as f16 bit patterns (exact), as the f16 prepared units hold
+    i32x4 hx0, hx1, hy0, hy1, hw0, hw1, hv0, hv1;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const unsigned e = 0x3c00u + (unsigned)((lane + i) & 7) * 0x40u;  // 1.0 .. 1.4375
+        hx0[i] = (int)(e | (e << 16)); hx1[i] = (int)((e + 0x10u) | (e << 16));
+        hy0[i] = (int)(e ^ 0x8000u); hy1[i] = (int)(e | 0x80000000u);
+        hw0[i] = (int)(e + 0x20u); hw1[i] = (int)(e << 16); hv0[i] = (int)e; hv1[i] = (int)(e | (e << 16));
+    }
+    float sx = 1e-3f * (float)(lane + 1);
+    const float dw = 2e-3f * (float)(64 - lane);
+    const f32x16 f16zero = {};
+    const f32x32 fzero = {};
+    f32x16 acc = {};
+    f32x16 d0 = Q8_PROBE_F16_DOT(hx0, hx1, hw0, hw1), d1 = Q8_PROBE_F16_DOT(hy0, hy1, hv0, hv1);
+    f32x32 sc = __builtin_amdgcn_mfma_f32_32x32x1f32(sx, dw, fzero, 0, 0, 0);
+    f32x16 e0, e1;
+    f32x32 tc;
+    for (int it = 0; it < a.iters; it += 2) {
+        Q8_PROBE_F16_PAIR(d0, d1, sc, e0, e1, tc);
+        Q8_PROBE_F16_PAIR(e0, e1, tc, d0, d1, sc);
     }
     float s = 0.0f;
 #pragma unroll

@@ -90,6 +90,7 @@ enum Fn {
     F_EMBED,
     F_ROPE, F_ATTN_DECODE, F_ATTN_DECODE_W4, F_ATTN_PREFILL, F_SYNTH, F_ADVANCE,
     F_PROBE_READ_L4, F_PROBE_READ_L8, F_PROBE_READ_L16, F_PROBE_EMPTY, F_PROBE_MFMA, F_PROBE_VALU, F_PROBE_MIX,
+    F_PROBE_MIX_F16,
     F_COUNT
 };
 
@@ -120,7 +121,7 @@ const char *const kFnNames[F_COUNT] = {
     "q8_embed",
     "q8_rope_append", "q8_attn_decode", "q8_attn_decode_w4", "q8_attn_prefill", "q8_synth", "q8_advance",
     "q8_probe_read_l4", "q8_probe_read_l8", "q8_probe_read_l16", "q8_probe_empty", "q8_probe_mfma",
-    "q8_probe_valu", "q8_probe_mix",
+    "q8_probe_valu", "q8_probe_mix", "q8_probe_mix_f16",
 };
 
 constexpr int kArgmaxParts = 1024;
@@ -1789,11 +1790,15 @@ int q8_probe(q8_ctx *c, int which, q8_dptr src, size_t bytes, int iters, int wor
         return launch(c, F_PROBE_EMPTY, 1, 64, 0, &a, sizeof a);
     case Q8_PROBE_MFMA:
     case Q8_PROBE_VALU:
-    case Q8_PROBE_MIX: {
+    case Q8_PROBE_MIX:
+    case Q8_PROBE_MIX_F16: {
         if (iters < 2 || iters % 2 != 0 || workgroups < 1)
             return fail(Q8_ERR_INVALID, "q8_probe: iters must be even and >= 2, workgroups >= 1");
         a.iters = iters;
-        const Fn f = which == Q8_PROBE_MFMA ? F_PROBE_MFMA : which == Q8_PROBE_VALU ? F_PROBE_VALU : F_PROBE_MIX;
+        const Fn f = which == Q8_PROBE_MFMA ? F_PROBE_MFMA
+                     : which == Q8_PROBE_VALU ? F_PROBE_VALU
+                     : which == Q8_PROBE_MIX ? F_PROBE_MIX
+                                             : F_PROBE_MIX_F16;
         return launch(c, f, (unsigned)workgroups, 256, 0, &a, sizeof a);
     }
     default:

@@ -65,7 +65,7 @@ EXPORTS = (
 )
 
 
-PROBE_READ_L4, PROBE_READ_L8, PROBE_READ_L16, PROBE_EMPTY, PROBE_MFMA, PROBE_VALU, PROBE_MIX = range(7)
+PROBE_READ_L4, PROBE_READ_L8, PROBE_READ_L16, PROBE_EMPTY, PROBE_MFMA, PROBE_VALU, PROBE_MIX, PROBE_MIX_F16 = range(8)
 
 
 class Q8Error(RuntimeError):
