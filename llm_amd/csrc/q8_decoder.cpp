@@ -96,11 +96,26 @@ struct q8_decoder {
     }
     int plan();
     int splits_for(int visible) const {
-        // one workgroup per head while the positions fit one chunk of the
-        // split kernel; beyond, a split per chunk, up to the eight the output
-        // projection's prologue combines
+        // Always the split kernel with its combine folded into the output
+        // projection (two splits at least): one 16-wave workgroup per head
+        // leaves most CUs idle (configs[4] geometry, whole decode step, 16 to
+        // 256 positions: 1.38-1.42 ms with one split, 1.30-1.33 with two).
+        // Each split walks its chunks in turn and every split adds to the
+        // combine (at most eight), so: the fewest chunks per split that eight
+        // splits allow, then the fewest splits at that many chunks (2400
+        // positions: 5 splits 1.550 ms vs 8 splits 1.618; 3000: 6 splits
+        // 1.593 vs 1.658; up to 2048 positions a split per chunk, measured
+        // best or within 0.3%).
         const int rows = q8i::attention_split_rows();
-        return visible <= rows ? 1 : std::min(Q8_ATTN_COMBINE_MAX, (visible + rows - 1) / rows);
+        if (visible <= 1) return 1;
+        if (visible <= 2 * rows) return 2;
+        const int chunks = (visible + Q8_ATTN_COMBINE_MAX * rows - 1) / (Q8_ATTN_COMBINE_MAX * rows);
+        return std::min(Q8_ATTN_COMBINE_MAX, (visible + chunks * rows - 1) / (chunks * rows));
+    }
+    int max_splits(int capacity) const {
+        // the most splits any visible count up to `capacity` takes (counts
+        // past eight chunks fall back to fewer splits)
+        return splits_for(std::min(capacity, Q8_ATTN_COMBINE_MAX * q8i::attention_split_rows()));
     }
     int body(int n, int splits);
     int run(int n, int splits);
@@ -217,7 +232,7 @@ int q8_decoder::plan() {
     s.max_k = std::max(std::max(g.n_embd, g.n_ff), g.n_head * g.head_dim);
     s.max_ff = g.n_ff;
     s.attn_heads = g.n_head;
-    s.attn_splits = splits_for(g.capacity);  // splits grow with the visible positions
+    s.attn_splits = max_splits(g.capacity);
     s.rope_n_rot = g.n_rot;
     s.rope_base = g.rope_base;
     DEC_TRY(q8_workspace_plan(c, &s));
