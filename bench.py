@@ -22,12 +22,13 @@ per step) / median time per step.
 Also reported, each on its own rotation:
   ceilings      what one kernel of this size can do on this box: the best
                 plain streaming read of the configs[0] byte count (the
-                GEMV's achievable ceiling) and of the decode step's launch
-                sizes, an empty kernel's cost per graph launch, the
-                sustained int8 MFMA rate (v_mfma_i32_32x32x32_i8 only), VALU
-                rate, and the GEMM's per-tile-block instruction mix with
-                operands in registers (its own ceiling), for the int8 and the
-                f16-MFMA families;
+                GEMV's achievable ceiling), an empty kernel's cost per graph
+                launch, the sustained int8 MFMA rate (v_mfma_i32_32x32x32_i8
+                only), VALU rate, and the GEMM's per-tile-block instruction
+                mix with operands in registers (its own ceiling), for the
+                int8 and the f16-MFMA families;
+  reads         the same plain-read ceiling at the byte counts of the decode
+                step's launches (reported under ceilings);
   gemm_n512     configs[3]: the layer's projections at n = 512 (QKV 6912,
                 O 2304 + residual, gate|up 2x5760 -> SiLU -> Q8_0, down
                 2304x5760 + residual) with the activation quantization, on
@@ -187,26 +188,6 @@ def bench_ceilings(gpu, steps, warmup, read_bytes):
     log("plain read of " + f"{read_bytes} B, MALL-cold: " +
         ", ".join(f"{n} {r['median_us']:.2f} us ({r['value']:.0f} GB/s)" for n, r in reads.items()))
     buf.free()
-    # the same ceiling at the byte counts of the decode step's launches
-    # (weights only): what one launch of that size can read on this box
-    decode_reads = {}
-    for name, nb in (("o", HID * HID // 32 * 34), ("qkv", 3 * HID * HID // 32 * 34),
-                     ("down", FFN * HID // 32 * 34), ("gate_up", 2 * FFN * HID // 32 * 34),
-                     ("lm_head", VOCAB * HID // 32 * 34)):
-        nbr = (nb + 15) // 16 * 16
-        cp = copies_for(nbr)
-        st = (nbr + 4095) // 4096 * 4096
-        rb = gpu.alloc(st * cp)
-        best_us = None
-        for which in (q8.PROBE_READ_L4, q8.PROBE_READ_L8, q8.PROBE_READ_L16):
-            ms = rotating_trials(gpu, lambda i, w=which: gpu.probe(w, rb, nbr, src_offset=i * st), cp,
-                                 max(cp, min(steps, 100)), min(warmup, 10))
-            us = statistics.median(ms) * 1e3
-            best_us = us if best_us is None else min(best_us, us)
-        rb.free()
-        decode_reads[name] = {"bytes": nb, "us": round(best_us, 3), "gbs": round(nb / (best_us * 1e-6) / 1e9, 1)}
-    log("plain reads at the decode launches' sizes, MALL-cold: " +
-        ", ".join(f"{n} {v['bytes'] / 1e6:.1f} MB {v['us']:.2f} us" for n, v in decode_reads.items()))
     empty = rotating_trials(gpu, lambda i: gpu.probe(q8.PROBE_EMPTY), 1, 200, 20)
     empty_us = statistics.median(empty) * 1e3
     cus = gpu.info()["cu_count"]
@@ -234,7 +215,34 @@ def bench_ceilings(gpu, steps, warmup, read_bytes):
             "empty_kernel_us_per_launch": round(empty_us, 3),
             "mfma_i8_tops": round(mfma_tops, 1), "valu_ns_per_op_per_simd": round(valu_ns, 3),
             "tile_block_mix_ns_per_simd": round(mix_ns, 2), "tile_block_mix_tops": round(mix_tops, 1),
-            "tile_block_mix_f16_ns_per_simd": round(mix16_ns, 2), "decode_launch_reads": decode_reads}
+            "tile_block_mix_f16_ns_per_simd": round(mix16_ns, 2)}
+
+
+def bench_launch_reads(gpu, steps, warmup):
+    """The plain-read ceiling at the byte counts of the decode step's
+    launches (weights only): what one launch of that size can read on this
+    box.  Its own section: a rocprofv3 kernel trace of it died on the host
+    inside hipGraphLaunch, so traced runs leave it out."""
+    from llm_amd import q8
+    decode_reads = {}
+    for name, nb in (("o", HID * HID // 32 * 34), ("qkv", 3 * HID * HID // 32 * 34),
+                     ("down", FFN * HID // 32 * 34), ("gate_up", 2 * FFN * HID // 32 * 34),
+                     ("lm_head", VOCAB * HID // 32 * 34)):
+        nbr = (nb + 15) // 16 * 16
+        cp = copies_for(nbr)
+        st = (nbr + 4095) // 4096 * 4096
+        rb = gpu.alloc(st * cp)
+        best_us = None
+        for which in (q8.PROBE_READ_L4, q8.PROBE_READ_L8, q8.PROBE_READ_L16):
+            ms = rotating_trials(gpu, lambda i, w=which: gpu.probe(w, rb, nbr, src_offset=i * st), cp,
+                                 max(cp, min(steps, 100)), min(warmup, 10))
+            us = statistics.median(ms) * 1e3
+            best_us = us if best_us is None else min(best_us, us)
+        rb.free()
+        decode_reads[name] = {"bytes": nb, "us": round(best_us, 3), "gbs": round(nb / (best_us * 1e-6) / 1e9, 1)}
+    log("plain reads at the decode launches' sizes, MALL-cold: " +
+        ", ".join(f"{n} {v['bytes'] / 1e6:.1f} MB {v['us']:.2f} us" for n, v in decode_reads.items()))
+    return decode_reads
 
 
 # ---------------------------------------------------------------------------
@@ -561,10 +569,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--sections", default="all",
-                    help="comma list of gemv,ceilings,gemm,extras,decoder,cpu (default all); a profiler run names "
-                         "one so each kernel's average covers one workload")
+                    help="comma list of gemv,ceilings,reads,gemm,extras,decoder,cpu (default all); a profiler run "
+                         "names one so each kernel's average covers one workload")
     args = ap.parse_args()
-    known = {"gemv", "ceilings", "gemm", "extras", "decoder", "cpu"}
+    known = {"gemv", "ceilings", "reads", "gemm", "extras", "decoder", "cpu"}
     sections = set(known) if args.sections == "all" else set(args.sections.split(","))
     unknown = sections - known
     if unknown:
@@ -586,6 +594,8 @@ def main():
     if "gemv" in sections:
         gemv = bench_gemv(gpu, m, k, steps, warmup, rng)
     ceil = bench_ceilings(gpu, steps, warmup, gemv_bytes(m, k)) if "ceilings" in sections else {}
+    if "reads" in sections:
+        ceil["decode_launch_reads"] = bench_launch_reads(gpu, steps, warmup)
     gemm = {"tops": None, "frac": None, "us": None, "ops": None}
     if "gemm" in sections:
         gemm = bench_layer_n512(gpu, steps, warmup, rng)

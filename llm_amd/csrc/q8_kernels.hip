@@ -906,6 +906,7 @@ static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
     // workgroup has threads), then a barrier.  The arithmetic per float4 is
     // the same either way.
     constexpr bool CMBW = CMB && BPW * 8 <= 64;
+    constexpr int XS = (BPW * 8 + 63) / 64;  // x float4s a lane stages
     f32x4 xv[Q8_GEMV_STAGE];
     CombineRegs creg;
     const int ns = CMB ? a.attn_splits : 0;
@@ -916,7 +917,7 @@ static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
         combine_load(a, nb, ns, creg);
     } else {
 #pragma unroll
-        for (int u = 0; u < Q8_GEMV_STAGE; u++) {
+        for (int u = 0; u < XS; u++) {
             const float *xp = xg + 4 * min(st_begin + lane + 64 * u, st_clamp);
             xv[u] = (f32x4){xp[0], xp[1], xp[2], xp[3]};
         }
@@ -949,7 +950,7 @@ static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
     // stage x permuted (the tile kernel's order): float4 slot 8b + 4hh + t
     // holds x[32b + 8c + J[hh][t]] in component c
 #pragma unroll
-    for (int u = 0; u < Q8_GEMV_STAGE; u++) {
+    for (int u = 0; u < XS; u++) {
         if (!CMB && 64 * u < st_end - st_begin) {
             const int i = st_begin + lane + 64 * u;
             float *d = i < st_end ? xs + (i >> 3) * 32 + ((i & 7) >> 1) + 4 * (i & 1) : pad;
@@ -1046,6 +1047,7 @@ static __device__ __forceinline__ void gemv_rsg_body(const Q8GemvArgs &a) {
     constexpr int BPL = 64 / LPB;
     constexpr int SPT = Q8_TILE_ROWS / RS;
     constexpr int BPW = NL * BPL;
+    constexpr int XS = (BPW * 8 + 63) / 64;  // x float4s a lane stages
     constexpr int NSLOT = SILU ? 2 : 1;
     static_assert(BPW * 8 <= 64 * Q8_GEMV_STAGE, "x range of a wave exceeds its staging registers");
     const int nb = a.nb;
@@ -1115,7 +1117,7 @@ static __device__ __forceinline__ void gemv_rsg_body(const Q8GemvArgs &a) {
     const int st_clamp = max(st_end - 1, 0);
     f32x4 xv[Q8_GEMV_STAGE];
 #pragma unroll
-    for (int u = 0; u < Q8_GEMV_STAGE; u++) {
+    for (int u = 0; u < XS; u++) {
         const float *xp = xg + 4 * min(st_begin + lane + 64 * u, st_clamp);
         xv[u] = (f32x4){xp[0], xp[1], xp[2], xp[3]};
     }
@@ -1131,7 +1133,7 @@ static __device__ __forceinline__ void gemv_rsg_body(const Q8GemvArgs &a) {
     if (norm) {
         const f32x4 *nwp = reinterpret_cast<const f32x4 *>(a.norm_w);
 #pragma unroll
-        for (int u = 0; u < Q8_GEMV_STAGE; u++) wv[u] = nwp[min(st_begin + lane + 64 * u, st_clamp)];
+        for (int u = 0; u < XS; u++) wv[u] = nwp[min(st_begin + lane + 64 * u, st_clamp)];
         if (threadIdx.x < 256) {
             const f32x4 *xr = reinterpret_cast<const f32x4 *>(xg);
 #pragma unroll
@@ -1176,7 +1178,7 @@ static __device__ __forceinline__ void gemv_rsg_body(const Q8GemvArgs &a) {
             nscale = norm_scale(npart, nb * 32, a.norm_eps);
         }
 #pragma unroll
-        for (int u = 0; u < Q8_GEMV_STAGE; u++) {
+        for (int u = 0; u < XS; u++) {
 #pragma unroll
             for (int e = 0; e < 4; e++) xv[u][e] = EX ? (xv[u][e] * nscale) * wv[u][e] : xv[u][e] * wv[u][e];
         }
@@ -1185,7 +1187,7 @@ static __device__ __forceinline__ void gemv_rsg_body(const Q8GemvArgs &a) {
         for (int b = nb; b < ((nb + 3) & ~3); b++) vbuf[(slot * RS + r) * vrow + b] = 0.0f;
     }
 #pragma unroll
-    for (int u = 0; u < Q8_GEMV_STAGE; u++) {
+    for (int u = 0; u < XS; u++) {
         if (64 * u < st_end - st_begin) {
             const int i = st_begin + lane + 64 * u;
             float *d = i < st_end ? xs + (i >> 3) * 32 + ((i & 7) >> 1) + 4 * (i & 1) : pad;
