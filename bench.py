@@ -1,4 +1,4 @@
-"""Benchmark of the Q8_0 matmul hot path on one MI355X (BASELINE.json metric:
+"""Benchmark of the Q8_0 matmul hot path on one MI355X (the benchmark's metric:
 "Q8_0 n=1 GEMV HBM GB/s (%peak); n=512 GEMM int8 TOPS (%MFMA peak)").
 
 A step is one n = 1 Q8_0 GEMV of configs[0] (W 5760 x 2304, x f32[2304]).
@@ -579,7 +579,7 @@ def main():
         ap.error(f"unknown sections {sorted(unknown)}")
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus "
-              f"{args.gpus}); the sharding design is described in DESIGN.md", file=sys.stderr)
+              f"{args.gpus}); it shards by output rows, which one GPU does not exercise", file=sys.stderr)
         sys.exit(2)
     steps = max(1, args.steps)
     warmup = max(0, args.warmup)

@@ -1,7 +1,7 @@
 """Python binding of libq8mi.so (include/q8mi.h) -- the test/bench host side.
 
 ``Gpu`` wraps the C-ABI one to one (it is what a Rust ``hip/sys.rs`` would
-declare, see INTEGRATION.md).  ``Compute`` mirrors the matmul entry points of
+declare).  ``Compute`` mirrors the matmul entry points of
 the reference engine's ``Compute`` (apps/engine/src/compute.rs:376-581,
 931-1019) over device ``Activation``s, so the parity tests read like the
 reference's own (apps/engine/tests/gpu_matmul.rs:57-65):

@@ -213,7 +213,7 @@ def argmax(values: np.ndarray) -> int:
 
 
 # ---------------------------------------------------------------------------
-# Seeded synthetic inputs (the shapes and distributions of BASELINE configs).
+# Seeded synthetic inputs (the shapes and distributions of the benchmark configs).
 # ---------------------------------------------------------------------------
 
 def make_q8_weight(rng: np.random.Generator, out: int, k: int, scale_std: float = 0.02,

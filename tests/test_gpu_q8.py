@@ -1,6 +1,6 @@
 """GPU parity of the HIP Q8_0 path against the CPU oracle, through the C-ABI.
 
-Bars:
+Bars (the path's parity targets):
   * integer/byte work bit-exact: the device weight layout (round trip), the
     quantized activations (q and scales), the int32 block dot;
   * f32 outputs within |d| <= 2e-6 + 1e-5*|ref| (TOL_ABS, TOL_REL below);
