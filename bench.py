@@ -20,6 +20,10 @@ Protocol (the same for every rotating figure below):
 per step) / median time per step.
 
 Also reported, each on its own rotation:
+  configs0_quantized_x  the same GEMV with x quantized to Q8_0 per 32-block
+                first, as configs[0]'s wording reads (q8_matmul_q8: the
+                n >= 2 arithmetic of tensor::matmul at n = 1, quantization
+                and int8 block dots in one launch);
   ceilings      what one kernel of this size can do on this box: the best
                 plain streaming read of the configs[0] byte count (the
                 GEMV's achievable ceiling), an empty kernel's cost per graph
@@ -163,12 +167,19 @@ def bench_gemv(gpu, m, k, steps, warmup, rng):
     hot = rotating_trials(gpu, lambda i: gpu.matmul(base, xb, 0, 1, yb, 0), 1, max(steps, 50), warmup)
     hs = summary(hot, per, 1e-9)
     log(f"configs[0] GEMV MALL-hot: {hs['median_us']:.2f} us/step, {hs['value']:.0f} GB/s")
+    # x quantized to Q8_0 first, as the n >= 2 path does (q8_matmul_q8: one
+    # launch quantizes x and takes the int8 block dots), same rotation
+    q8x = rotating_trials(gpu, lambda i: gpu.matmul_q8(weights[i], xb, 0, 1, yb, 0), copies, steps, warmup)
+    qs = summary(q8x, per, 1e-9)
+    log(f"configs[0] GEMV on Q8_0-quantized x: {qs['median_us']:.2f} us/step, {qs['value']:.0f} GB/s "
+        f"(trials {qs['trials']})")
     for w in weights:
         gpu.release(w)
     xb.free()
     yb.free()
     return {"us_per_step": s["median_us"], "gbs": s["value"], "trials_gbs": s["trials"], "bytes_per_step": per,
-            "copies": copies, "mall_hot_gbs": round(hs["value"], 1), "mall_hot_us": hs["median_us"]}
+            "copies": copies, "mall_hot_gbs": round(hs["value"], 1), "mall_hot_us": hs["median_us"],
+            "q8x_gbs": round(qs["value"], 1), "q8x_us": qs["median_us"], "q8x_trials_gbs": qs["trials"]}
 
 
 def bench_ceilings(gpu, steps, warmup, read_bytes):
@@ -641,6 +652,11 @@ def main():
                      "ceiling_gbs": ceiling, "ceiling_kernel": ceil.get("ceiling_kernel"),
                      "frac_of_ceiling": round(value / ceiling, 4) if value and ceiling else None,
                      "trials_gbs": gemv.get("trials_gbs"), "mall_hot_gbs": gemv.get("mall_hot_gbs")},
+        "configs0_quantized_x": {"value": gemv.get("q8x_gbs"), "unit": "GB/s", "us_per_step": gemv.get("q8x_us"),
+                                 "frac": round(gemv["q8x_gbs"] / HBM_PEAK_GBS, 4) if gemv.get("q8x_gbs") else None,
+                                 "trials_gbs": gemv.get("q8x_trials_gbs"), "entry": "q8_matmul_q8",
+                                 "workload": "configs[0] with x quantized to Q8_0 per 32-block in the same launch "
+                                             "(the n >= 2 arithmetic at n = 1), int8 block dots"},
         "gemm_n512": {"value": r(gemm["tops"], 2), "unit": "TOPS", "peak": INT8_PEAK_TOPS,
                       "frac": round(gemm["frac"], 4) if gemm["frac"] is not None else None,
                       "us_per_layer": r(gemm["us"], 2), "ops_per_layer": gemm["ops"],

@@ -211,6 +211,18 @@ int q8_weight_export(q8_ctx *ctx, const q8_weight *weight, void *gguf_bytes, siz
 int q8_matmul(q8_ctx *ctx, const q8_weight *weight, q8_dptr x, size_t x_offset, int n, q8_dptr y,
               size_t y_offset, const q8_prepared *prepared, q8_dptr bias, size_t bias_offset);
 
+/* q8_matmul with x quantized to Q8_0 at every n, n = 1 included: the n >= 2
+ * arithmetic of tensor::matmul (tensor.rs:104-148 -- quantize_q8_0,
+ * quant.rs:98-121, then Weight::dot_row_quantized / dot_q8_0_q8_0,
+ * tensor.rs:56-73, quant.rs:127-154) for one token too, where the reference's
+ * n = 1 path (q8_matmul) keeps x in f32.  n >= 2 is q8_matmul.  At n = 1 one
+ * launch quantizes x (every workgroup the range it reads, bytes equal to
+ * quantize_q8_0's), takes each block's int32 dot exactly and multiplies it by
+ * d_w * d_x; the block values of a row are summed in a fixed tree, within the
+ * n >= 2 parity bar of the reference.  `bias` as in q8_matmul. */
+int q8_matmul_q8(q8_ctx *ctx, const q8_weight *weight, q8_dptr x, size_t x_offset, int n, q8_dptr y,
+                 size_t y_offset, q8_dptr bias, size_t bias_offset);
+
 /* The scratch of q8_matmul_noalloc: a static device array of this size on
  * each GPU the library runs on, held until the process ends. */
 #define Q8_NOALLOC_SCRATCH_BYTES (8u << 20)

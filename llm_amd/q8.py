@@ -45,7 +45,8 @@ EXPORTS = (
     "q8_open", "q8_close", "q8_device_name", "q8_device_info", "q8_stream", "q8_set_option",
     "q8_alloc", "q8_free", "q8_upload", "q8_download", "q8_sync",
     "q8_weight_resident", "q8_weight_release", "q8_weight_shape", "q8_weight_export",
-    "q8_matmul", "q8_matmul_noalloc", "q8_prepare", "q8_silu_mul_prepare", "q8_rmsnorm", "q8_norm_prepare", "q8_silu_mul",
+    "q8_matmul", "q8_matmul_noalloc", "q8_matmul_q8", "q8_prepare", "q8_silu_mul_prepare", "q8_rmsnorm",
+    "q8_norm_prepare", "q8_silu_mul",
     "q8_matmul_decode_group", "q8_matmul_prompt_group", "q8_gate_up_silu", "q8_gate_up_silu_prepared",
     "q8_lm_head_argmax", "q8_argmax", "q8_copy_device", "q8_embeddings", "q8_probe",
     "q8_plan", "q8_tactic_count", "q8_tactic_row",
@@ -181,6 +182,7 @@ def lib():
         "q8_weight_export": (c_int, [vp, vp, vp, c_size]),
         "q8_matmul": (c_int, [vp, vp, u64, c_size, c_int, u64, c_size, ctypes.POINTER(Prepared), u64, c_size]),
         "q8_matmul_noalloc": (c_int, [vp, vp, u64, c_size, c_int, u64, c_size, u64, c_size]),
+        "q8_matmul_q8": (c_int, [vp, vp, u64, c_size, c_int, u64, c_size, u64, c_size]),
         "q8_prepare": (c_int, [vp, u64, c_size, c_int, c_int, ctypes.POINTER(Prepared)]),
         "q8_silu_mul_prepare": (c_int, [vp, u64, u64, c_int, c_int, ctypes.POINTER(Prepared)]),
         "q8_silu_mul": (c_int, [vp, u64, u64, u64, c_size]),
@@ -451,6 +453,13 @@ class Gpu:
         _check(lib().q8_matmul(self.handle, h, x.ptr, x_offset, n, y.ptr, y_offset,
                                ctypes.byref(prepared) if prepared is not None else None,
                                bias.ptr if bias is not None else 0, bias_offset))
+
+    def matmul_q8(self, weight: Weight, x: DeviceBuffer, x_offset: int, n: int, y: DeviceBuffer, y_offset: int,
+                  bias: DeviceBuffer | None = None, bias_offset: int = 0):
+        """q8_matmul_q8: x quantized to Q8_0 at every n, n = 1 included."""
+        h = self.resident(weight)
+        _check(lib().q8_matmul_q8(self.handle, h, x.ptr, x_offset, n, y.ptr, y_offset,
+                                  bias.ptr if bias is not None else 0, bias_offset))
 
     def prepare(self, x: DeviceBuffer, x_offset: int, n: int, k: int) -> Prepared:
         p = Prepared()

@@ -1,0 +1,166 @@
+"""q8_matmul_q8 (include/q8mi.h) through the C-ABI: x quantized to Q8_0 at
+every n, n = 1 included -- the n >= 2 arithmetic of tensor::matmul
+(tensor.rs:104-148: quantize_q8_0, then dot_q8_0_q8_0 per row) applied to one
+token, as configs[0]'s "activation quantized per 32-block to Q8_0 exactly as
+the reference does" reads.
+
+The oracle for one token is the reference's own n >= 2 path run on two copies
+of the token (oracle.matmul with n = 2 quantizes every token and takes
+dot_q8_0_q8_0 per row); the bar is the n >= 2 one (assert_parity against the
+exact block sums).  The int32 block dot is pinned exactly by power-of-two
+problems, the quantizer's rounding (half away from zero), NaN and zero blocks
+by crafted x, and n >= 2 equals q8_matmul bit for bit.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from llm_amd import q8
+from test_gpu_q8 import assert_bits, assert_parity, exact_at, exact_problem
+
+pytestmark = pytest.mark.gpu
+
+SEED = 0x5EED
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    g = q8.Gpu(0)
+    yield g
+    g.close()
+
+
+def rng(i):
+    return np.random.default_rng(SEED + 9000 + i)
+
+
+def weight(r, out, k, **kw):
+    return q8.Weight(oracle.make_q8_weight(r, out, k, **kw), k, out)
+
+
+def run_q8(gpu, w, x, n, x_offset=0, bias=None):
+    k, out = w.k, w.out
+    xb = gpu.alloc(4 * (n * k + x_offset))
+    yb = gpu.alloc(4 * n * out)
+    xb.upload(np.concatenate([np.zeros(x_offset, np.float32), x.reshape(-1).astype(np.float32)]))
+    bb = None
+    if bias is not None:
+        yb.upload(bias.astype(np.float32))
+        bb = yb
+    gpu.matmul_q8(w, xb, x_offset, n, yb, 0, bias=bb)
+    y = yb.download(np.float32, n * out).reshape(n, out)
+    xb.free()
+    yb.free()
+    return y
+
+
+def oracle_one(w, x):
+    """The reference's n >= 2 arithmetic for one token: two copies through
+    tensor::matmul's quantized path, the first row of the result."""
+    x2 = np.stack([x, x]).astype(np.float32)
+    return oracle.matmul(w.data, w.k, w.out, x2, 2)[0]
+
+
+@pytest.mark.parametrize("out,k", [(5760, 2304), (2304, 2304), (2304, 5760), (6912, 2304), (1, 32), (33, 96),
+                                   (200, 1056), (40, 12288), (122880, 2304)])
+def test_one_token_matches_the_reference(gpu, out, k):
+    r = rng(out + k)
+    w = weight(r, out, k)
+    x = oracle.make_activations(r, 1, k, outlier_rate=0.01).reshape(k)
+    print(f"\nq8_matmul_q8 n=1 {out} x {k}", flush=True)
+    got = run_q8(gpu, w, x, 1)[0]
+    ref = oracle_one(w, x)
+    qx, sx = oracle.quantize_q8_0(x)
+    assert_parity(got, ref, exact_at(w.data, k, out, quants=qx.reshape(1, k), scales=sx.reshape(1, -1)),
+                  f"q8_matmul_q8 n=1 {out}x{k}")
+    if out == 122880:  # the greedy choice, where the top two differ by more than the bar
+        top2 = np.sort(ref)[-2:]
+        if top2[1] - top2[0] > 2 * (2e-6 + 1e-5 * abs(top2[1])):
+            assert int(np.argmax(got)) == oracle.argmax(ref)
+    gpu.release(w)
+
+
+@pytest.mark.parametrize("k", [32, 64, 96, 1024])
+def test_int32_block_dot_is_exact(gpu, k):
+    """Power-of-two scales and block peaks of exactly 127 * s_x: every quant
+    is the integer itself and every f32 step exact, so y is the integer sum."""
+    r = rng(100 + k)
+    w, x, y = exact_problem(r, 40, k, 1)
+    got = run_q8(gpu, w, x[0], 1)
+    assert_bits(got, y, f"q8_matmul_q8 exact k={k}")
+    gpu.release(w)
+
+
+def test_rounding_nan_and_zero_blocks(gpu):
+    """Block 0: quants at exact half steps (v * 127 / peak = j + 0.5 rounds
+    away from zero); block 1: all zero (scale 0); block 2: a NaN (quant 0,
+    ignored by the peak); block 3: ordinary.  Against the oracle's quantizer."""
+    k, out = 128, 64
+    r = rng(7)
+    w = weight(r, out, k)
+    x = r.standard_normal(k).astype(np.float32)
+    x[0] = 127.0  # peak 127: inverse 1, so v * inverse = v, a half step
+    x[1:32] = np.array([j + 0.5 for j in range(-15, 16)], np.float32)
+    x[32:64] = 0.0
+    x[70] = np.nan
+    got = run_q8(gpu, w, x, 1)[0]
+    ref = oracle_one(w, x)
+    qx, sx = oracle.quantize_q8_0(x)
+    assert np.isfinite(got).all()
+    assert_parity(got, ref, exact_at(w.data, k, out, quants=qx.reshape(1, k), scales=sx.reshape(1, -1)),
+                  "q8_matmul_q8 rounding/NaN/zero")
+    gpu.release(w)
+
+
+@pytest.mark.parametrize("x_offset", [1, 2, 3])
+def test_offset_and_residual(gpu, x_offset):
+    r = rng(200 + x_offset)
+    out, k = 2304, 2304
+    w = weight(r, out, k)
+    x = oracle.make_activations(r, 1, k).reshape(k)
+    res = r.standard_normal(out).astype(np.float32)
+    got = run_q8(gpu, w, x, 1, x_offset=x_offset, bias=res)[0]
+    ref = (res + oracle_one(w, x)).astype(np.float32)
+    qx, sx = oracle.quantize_q8_0(x)
+    ex = exact_at(w.data, k, out, quants=qx.reshape(1, k), scales=sx.reshape(1, -1))
+    assert_parity(got, ref, lambda idx: tuple(np.add(e, (res.reshape(-1)[idx].astype(np.float64) if i == 0 else 0))
+                                              for i, e in enumerate(ex(idx))),
+                  f"q8_matmul_q8 residual, x at +{x_offset}")
+    gpu.release(w)
+
+
+@pytest.mark.parametrize("n", [2, 8, 64])
+def test_batches_are_q8_matmul(gpu, n):
+    r = rng(300 + n)
+    out, k = 392, 2304
+    w = weight(r, out, k)
+    x = oracle.make_activations(r, n, k, outlier_rate=0.01)
+    xb, y1, y2 = gpu.alloc(4 * n * k), gpu.alloc(4 * n * out), gpu.alloc(4 * n * out)
+    xb.upload(x)
+    gpu.matmul(w, xb, 0, n, y1, 0)
+    gpu.matmul_q8(w, xb, 0, n, y2, 0)
+    assert_bits(y2.download(np.float32, n * out), y1.download(np.float32, n * out), f"q8_matmul_q8 n={n}")
+    for b in (xb, y1, y2):
+        b.free()
+    gpu.release(w)
+
+
+def test_deterministic_and_errors(gpu):
+    r = rng(400)
+    w = weight(r, 5760, 2304)
+    x = oracle.make_activations(r, 1, 2304).reshape(2304)
+    a = run_q8(gpu, w, x, 1)
+    b = run_q8(gpu, w, x, 1)
+    assert_bits(a, b, "q8_matmul_q8 run to run")
+    gpu.release(w)
+    big = weight(r, 32, 32 * 400)  # 400 blocks: more than 16 waves of the widest slice
+    xb, yb = gpu.alloc(4 * 32 * 400), gpu.alloc(4 * 32)
+    with pytest.raises(q8.Q8Error):
+        gpu.matmul_q8(big, xb, 0, 1, yb, 0)
+    with pytest.raises(q8.Q8Error):
+        gpu.matmul_q8(big, xb, 0, 1025, yb, 0)
+    small = gpu.alloc(4 * 100)
+    with pytest.raises(q8.Q8Error):  # x shorter than k
+        gpu.matmul_q8(weight(r, 64, 2304), small, 0, 1, yb, 0)
+    for buf in (xb, yb, small):
+        buf.free()
