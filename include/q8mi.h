@@ -206,7 +206,10 @@ int q8_weight_export(q8_ctx *ctx, const q8_weight *weight, void *gguf_bytes, siz
  * matmul_add (compute.rs:399-431, 537-581).  `prepared` may be NULL (the
  * activations are then quantized here for n >= 2); `bias` != 0 adds
  * bias[bias_offset + t*out + o] in the epilogue (the fused residual; it may
- * alias y).  n == 1 takes the GEMV, n >= 2 the MFMA GEMM; n > Q8_MAX_TOKENS
+ * alias y).  n == 1 takes the GEMV; n == 2 without `prepared` the
+ * quantized-x GEMV (x quantized to Q8_0 in the launch, the weights read once
+ * for both tokens; option "gemm.small_gemv" = 0 turns it off), else the MFMA
+ * GEMM -- both under the n >= 2 arithmetic; n > Q8_MAX_TOKENS
  * is Q8_ERR_UNSUPPORTED as in the reference. */
 int q8_matmul(q8_ctx *ctx, const q8_weight *weight, q8_dptr x, size_t x_offset, int n, q8_dptr y,
               size_t y_offset, const q8_prepared *prepared, q8_dptr bias, size_t bias_offset);
@@ -231,7 +234,8 @@ int q8_matmul_q8(q8_ctx *ctx, const q8_weight *weight, q8_dptr x, size_t x_offse
  * callers that cannot allocate device memory -- code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc: this entry point calls
  * no hipMalloc, hipFree or allocating library routine.  The caller passes a
- * resident weight and its own x, y and bias; n >= 2 quantizes x into the
+ * resident weight and its own x, y and bias; n == 2 takes q8_matmul's
+ * quantized-x GEMV (x quantized in LDS, no scratch); larger n quantizes x into the
  * static array of Q8_NOALLOC_SCRATCH_BYTES (int8 units, at most
  * ceil(n/32) * (k/32) * 1152 bytes: n = 1024 at k = 5760 fits, larger shapes are
  * Q8_ERR_UNSUPPORTED), and the GEMM keeps every block of a row tile in one

@@ -1028,30 +1028,37 @@ Q8_GEMV_RS_KERNEL(16, 3)
 Q8_GEMV_RS_KERNEL(16, 6)
 
 // ---------------------------------------------------------------------------
-// Row-slice GEMV on Q8_0-quantized x: n = 1 under the n >= 2 arithmetic of
-// tensor::matmul (tensor.rs:104-148): x quantized per 32-block by
-// quantize_q8_0 (quant.rs:98-121), each row then the int8 block dots of
+// Row-slice GEMV on Q8_0-quantized x: one to NT tokens under the n >= 2
+// arithmetic of tensor::matmul (tensor.rs:104-148): x quantized per 32-block
+// by quantize_q8_0 (quant.rs:98-121), each row then the int8 block dots of
 // dot_q8_0_q8_0 (quant.rs:127-154; Weight::dot_row_quantized,
-// tensor.rs:56-73).
+// tensor.rs:56-73).  At n = 1 it is q8_matmul_q8; at n = 2 the small side of
+// q8_matmul's GEMV-to-GEMM switch: the weight stream is read once for both
+// tokens, one launch instead of a quantize launch and an MFMA GEMM.  Every
+// workgroup quantizes the x it reads, so the quantization is repeated once
+// per workgroup: at four and eight tokens that work outgrew the GEMM's
+// (configs[1] W, 5760 x 2304: n = 2 7.25 us against 10.45; n = 4 11.5 against
+// 10.5; n = 8 24.0 against 10.7), so only one and two tokens are built.
 //
 // gemv_rs_body's slices, lanes and weight stream.  Each wave quantizes its
-// own range of x, with q8_quantize's arithmetic (peak = max |v| with NaN
-// ignored, scale = peak / 127, q = sat(round(v * 127 / peak))), into LDS in
-// the weight units' order: byte 16 h + 4 t + c of block b is element
+// own range of every token's x, with q8_quantize's arithmetic (peak = max |v|
+// with NaN ignored, scale = peak / 127, q = sat(round(v * 127 / peak))), into
+// LDS in the weight units' order: byte 16 h + 4 t + c of block b is element
 // 8c + J[h][t], so dword t of a lane's 16 weight bytes meets dword t of x.  A
 // half block's 16 products are four v_dot4_i32_i8 (exact); the partner half
 // (lane L ^ RS) completes the int32 block dot; the block value is
 // (d_w * d_x) * float(isum), dot_q8_0_q8_0's scalar order; the blocks of a
-// row are summed in gemv_rs_body's fixed tree.
+// row are summed in gemv_rs_body's fixed tree, per token.  Tokens past
+// a.tokens (NT > n) re-read the last token and write nothing.
 // ---------------------------------------------------------------------------
-template <int RS, int NL>
+template <int RS, int NL, int NT>
 static __device__ __forceinline__ void gemv_q8x_body(const Q8GemvArgs &a) {
     extern __shared__ __attribute__((aligned(16))) float smem[];
     constexpr int LPB = 2 * RS;               // lanes per block
     constexpr int BPL = 64 / LPB;             // blocks per wave load
     constexpr int SPT = Q8_TILE_ROWS / RS;    // slices per tile
     constexpr int BPW = NL * BPL;             // blocks per wave
-    constexpr int XS = (BPW * 8 + 63) / 64;   // x float4s a lane quantizes
+    constexpr int XS = (BPW * 8 + 63) / 64;   // x float4s a lane quantizes per token
     static_assert(BPW * 8 <= 64 * Q8_GEMV_STAGE, "x range of a wave exceeds its staging registers");
     const uint8_t *mq = a.m[0].quants;
     const uint16_t *msc = a.m[0].scales;
@@ -1060,10 +1067,12 @@ static __device__ __forceinline__ void gemv_q8x_body(const Q8GemvArgs &a) {
     const int mrows = a.m[0].rows;
     const float *xg = a.x;
     const int nb = a.nb;
+    const int ntok = NT == 1 ? 1 : a.tokens;
     asm volatile("" ::"s"(mq), "s"(msc), "s"(my), "s"(mbias), "s"(mrows), "s"(xg), "s"(nb), "s"(a.xcd_order),
-                 "s"(a.total_tiles));
+                 "s"(a.total_tiles), "s"(ntok));
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nw = (int)(blockDim.x >> 6);
     const int j = lane / LPB;
     const int h = (lane / RS) & 1;
     const int r = lane % RS;
@@ -1078,19 +1087,23 @@ static __device__ __forceinline__ void gemv_q8x_body(const Q8GemvArgs &a) {
     const int b_last = max(b_end - 1, 0);
     const uint8_t *qbase = mq + (size_t)tile * nb * Q8_UNIT_BYTES + 16 * (32 * h + srow);
     const uint16_t *sbase = msc + (size_t)tile * nb * Q8_TILE_ROWS + srow;
-    uint8_t *xq = reinterpret_cast<uint8_t *>(smem);  // nb * 32 quant bytes, permuted
-    float *xd = smem + nb * 8;                         // nb block scales
-    float *vbuf = xd + nb;                             // [waves][RS] row sums
-    float *pad = vbuf + (blockDim.x >> 6) * RS;        // stores of dead lanes land here, unread
+    uint8_t *xq = reinterpret_cast<uint8_t *>(smem);  // [NT][nb * 32] quant bytes, permuted
+    float *xd = smem + NT * nb * 8;                    // [NT][nb] block scales
+    float *vbuf = xd + NT * nb;                        // [NT][waves][RS] row sums
+    float *pad = vbuf + NT * nw * RS;                  // stores of dead lanes land here, unread
 
     const int st_begin = 8 * b_begin;
     const int st_end = 8 * b_end;
     const int st_clamp = max(st_end - 1, 0);
-    f32x4 xv[XS];
+    f32x4 xv[NT][XS];
 #pragma unroll
-    for (int u = 0; u < XS; u++) {
-        const float *xp = xg + 4 * min(st_begin + lane + 64 * u, st_clamp);
-        xv[u] = (f32x4){xp[0], xp[1], xp[2], xp[3]};
+    for (int t = 0; t < NT; t++) {
+        const float *xt = xg + (size_t)min(t, ntok - 1) * nb * 32;
+#pragma unroll
+        for (int u = 0; u < XS; u++) {
+            const float *xp = xt + 4 * min(st_begin + lane + 64 * u, st_clamp);
+            xv[t][u] = (f32x4){xp[0], xp[1], xp[2], xp[3]};
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
     i32x4 qv[NL];
@@ -1107,70 +1120,88 @@ static __device__ __forceinline__ void gemv_q8x_body(const Q8GemvArgs &a) {
     // the 8 float4s of a block sit in 8 aligned lanes (st_begin is a multiple
     // of 8), so the block peak is a max over lanes ^ 1, 2, 4
 #pragma unroll
-    for (int u = 0; u < XS; u++) {
-        const int i = st_begin + lane + 64 * u;
-        const f32x4 v = xv[u];
-        float pk = fmaxf(fmaxf(fmaxf(fmaxf(0.0f, fabsf(v.x)), fabsf(v.y)), fabsf(v.z)), fabsf(v.w));
-        pk = xor_max<1>(pk);
-        pk = xor_max<2>(pk);
-        pk = xor_max<4>(pk);
-        const float scale = pk / 127.0f;
-        const float inverse = pk > 0.0f ? 127.0f / pk : 0.0f;
-        const bool live = i < st_end;  // whole blocks: st_end is a multiple of 8
-        const int blk = i >> 3;
-        const int c = (i & 7) >> 1;
-        // component k is element 8c + J[h'][t] with h' = k >> 1, t = 2 (k & 1) + (i & 1)
-        uint8_t *base = live ? xq + blk * 32 + c + 4 * (i & 1) : reinterpret_cast<uint8_t *>(pad);
-        base[0] = (uint8_t)sat_i8(roundf(v.x * inverse));
-        base[8] = (uint8_t)sat_i8(roundf(v.y * inverse));
-        base[16] = (uint8_t)sat_i8(roundf(v.z * inverse));
-        base[24] = (uint8_t)sat_i8(roundf(v.w * inverse));
-        if (live && (i & 7) == 0) xd[blk] = scale;
+    for (int t = 0; t < NT; t++) {
+#pragma unroll
+        for (int u = 0; u < XS; u++) {
+            const int i = st_begin + lane + 64 * u;
+            const f32x4 v = xv[t][u];
+            float pk = fmaxf(fmaxf(fmaxf(fmaxf(0.0f, fabsf(v.x)), fabsf(v.y)), fabsf(v.z)), fabsf(v.w));
+            pk = xor_max<1>(pk);
+            pk = xor_max<2>(pk);
+            pk = xor_max<4>(pk);
+            const float scale = pk / 127.0f;
+            const float inverse = pk > 0.0f ? 127.0f / pk : 0.0f;
+            const bool live = i < st_end;  // whole blocks: st_end is a multiple of 8
+            const int blk = i >> 3;
+            const int c = (i & 7) >> 1;
+            // component k is element 8c + J[h'][t'] with h' = k >> 1, t' = 2 (k & 1) + (i & 1)
+            uint8_t *base = live ? xq + (t * nb + blk) * 32 + c + 4 * (i & 1) : reinterpret_cast<uint8_t *>(pad);
+            base[0] = (uint8_t)sat_i8(roundf(v.x * inverse));
+            base[8] = (uint8_t)sat_i8(roundf(v.y * inverse));
+            base[16] = (uint8_t)sat_i8(roundf(v.z * inverse));
+            base[24] = (uint8_t)sat_i8(roundf(v.w * inverse));
+            if (live && (i & 7) == 0) xd[t * nb + blk] = scale;
+        }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    float lsum = 0.0f;
+    float lsum[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) lsum[t] = 0.0f;
 #pragma unroll
     for (int i = 0; i < NL; i++) {
         const int bu = b_begin + i * BPL + j;
         const int b = min(bu, b_last);
-        const i32x4 xw = *(const i32x4 *)(xq + b * 32 + 16 * h);
-        int s = __builtin_amdgcn_sdot4(qv[i].x, xw.x, 0, false);
-        s = __builtin_amdgcn_sdot4(qv[i].y, xw.y, s, false);
-        s = __builtin_amdgcn_sdot4(qv[i].z, xw.z, s, false);
-        s = __builtin_amdgcn_sdot4(qv[i].w, xw.w, s, false);
-        int isum;
-        if constexpr (RS == 8) {
-            isum = s + __builtin_amdgcn_mov_dpp(s, 0x128, 0xf, 0xf, false);  // lane ^ 8 by row_ror:8
-        } else {
-            const auto sw = __builtin_amdgcn_permlane16_swap((unsigned)s, (unsigned)s, false, false);
-            isum = (int)(sw[0] + sw[1]);
+        const float dw = f16_to_f32(dd[i]);
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const i32x4 xw = *(const i32x4 *)(xq + (t * nb + b) * 32 + 16 * h);
+            int s = __builtin_amdgcn_sdot4(qv[i].x, xw.x, 0, false);
+            s = __builtin_amdgcn_sdot4(qv[i].y, xw.y, s, false);
+            s = __builtin_amdgcn_sdot4(qv[i].z, xw.z, s, false);
+            s = __builtin_amdgcn_sdot4(qv[i].w, xw.w, s, false);
+            int isum;
+            if constexpr (RS == 8) {
+                isum = s + __builtin_amdgcn_mov_dpp(s, 0x128, 0xf, 0xf, false);  // lane ^ 8 by row_ror:8
+            } else {
+                const auto sw = __builtin_amdgcn_permlane16_swap((unsigned)s, (unsigned)s, false, false);
+                isum = (int)(sw[0] + sw[1]);
+            }
+            const float v = (dw * xd[t * nb + b]) * (float)isum;
+            lsum[t] = bu < b_end ? lsum[t] + v : lsum[t];
         }
-        const float v = (f16_to_f32(dd[i]) * xd[b]) * (float)isum;
-        lsum = bu < b_end ? lsum + v : lsum;
     }
-    if constexpr (BPL >= 4) lsum = xor_add<16>(lsum);
-    if constexpr (BPL >= 2) lsum = xor_add<32>(lsum);
-    if (lane < RS) vbuf[wave * RS + r] = lsum;
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        float ls = lsum[t];
+        if constexpr (BPL >= 4) ls = xor_add<16>(ls);
+        if constexpr (BPL >= 2) ls = xor_add<32>(ls);
+        if (lane < RS) vbuf[(t * nw + wave) * RS + r] = ls;
+    }
     __syncthreads();
     if (wave != 0 || lane >= RS) return;
-    const int nw = (int)(blockDim.x >> 6);
-    float acc = vbuf[r];
-    for (int w2 = 1; w2 < nw; w2++) acc = acc + vbuf[w2 * RS + r];
     const int row = tile * Q8_TILE_ROWS + srow;
-    if (row < mrows) my[row] = mbias ? acc + mbias[row] : acc;
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        if (t < ntok) {
+            float acc = vbuf[t * nw * RS + r];
+            for (int w2 = 1; w2 < nw; w2++) acc = acc + vbuf[(t * nw + w2) * RS + r];
+            const size_t o = (size_t)t * mrows + row;
+            if (row < mrows) my[o] = mbias ? acc + mbias[o] : acc;
+        }
+    }
 }
 
-#define Q8_GEMV_Q8X_KERNEL(RS, NL)                                                                    \
-    extern "C" __global__ __launch_bounds__(1024) void q8_gemv_q8x_r##RS##_l##NL(Q8GemvArgs a) { \
-        gemv_q8x_body<RS, NL>(a);                                                                     \
+#define Q8_GEMV_Q8X_KERNEL(RS, NL, NT)                                                                   \
+    extern "C" __global__ __launch_bounds__(1024) void q8_gemv_q8x##NT##_r##RS##_l##NL(Q8GemvArgs a) { \
+        gemv_q8x_body<RS, NL, NT>(a);                                                                    \
     }
-Q8_GEMV_Q8X_KERNEL(8, 3)
-Q8_GEMV_Q8X_KERNEL(8, 6)
-Q8_GEMV_Q8X_KERNEL(16, 3)
-Q8_GEMV_Q8X_KERNEL(16, 6)
+#define Q8_GEMV_Q8X_TOKENS(NT) \
+    Q8_GEMV_Q8X_KERNEL(8, 3, NT) Q8_GEMV_Q8X_KERNEL(8, 6, NT) Q8_GEMV_Q8X_KERNEL(16, 3, NT) Q8_GEMV_Q8X_KERNEL(16, 6, NT)
+Q8_GEMV_Q8X_TOKENS(1)
+Q8_GEMV_Q8X_TOKENS(2)
 
 // ---------------------------------------------------------------------------
 // Row-slice GEMV over a decode group (q8_gemv_g*: up to four matrices sharing

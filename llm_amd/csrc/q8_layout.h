@@ -146,6 +146,9 @@ typedef struct {
      * its non-NaN outputs to [tile], or index 0xffffffff if it has none. */
     float *amax_value;
     unsigned *amax_index;
+    /* The quantized-x kernels (q8_gemv_q8x_*): tokens 1..NT of x, k floats
+     * apart; y and bias [tokens][rows]. */
+    int tokens;
 } Q8GemvArgs;
 
 /* float4s per thread of the 256-thread row RMSNorm (k <= 1024 * this). */

@@ -77,7 +77,8 @@ enum Fn {
     F_GEMV_RC8_3_E0, F_GEMV_RC8_6_E0, F_GEMV_RC16_3_E0, F_GEMV_RC16_6_E0,
     F_GEMV_G8_3, F_GEMV_G16_3, F_GEMV_G16_6, F_GEMV_S8_3, F_GEMV_S16_6,
     F_GEMV_G8_3_E0, F_GEMV_G16_3_E0, F_GEMV_G16_6_E0, F_GEMV_S8_3_E0, F_GEMV_S16_6_E0,
-    F_GEMV_Q8X_8_3, F_GEMV_Q8X_8_6, F_GEMV_Q8X_16_3, F_GEMV_Q8X_16_6,
+    F_GEMV_Q8X1_8_3, F_GEMV_Q8X1_8_6, F_GEMV_Q8X1_16_3, F_GEMV_Q8X1_16_6,
+    F_GEMV_Q8X2_8_3, F_GEMV_Q8X2_8_6, F_GEMV_Q8X2_16_3, F_GEMV_Q8X2_16_6,
     F_QUANTIZE,
     F_GEMM_S0_T1, F_GEMM_S1_T1, F_GEMM_S1_T2, F_GEMM_S1_T4,
     F_GEMM_H_T1_R4, F_GEMM_H_T2_R2, F_GEMM_H_T2_R4,
@@ -109,7 +110,8 @@ const char *const kFnNames[F_COUNT] = {
     "q8_gemv_rc8_l3_e0", "q8_gemv_rc8_l6_e0", "q8_gemv_rc16_l3_e0", "q8_gemv_rc16_l6_e0",
     "q8_gemv_g8_l3", "q8_gemv_g16_l3", "q8_gemv_g16_l6", "q8_gemv_s8_l3", "q8_gemv_s16_l6",
     "q8_gemv_g8_l3_e0", "q8_gemv_g16_l3_e0", "q8_gemv_g16_l6_e0", "q8_gemv_s8_l3_e0", "q8_gemv_s16_l6_e0",
-    "q8_gemv_q8x_r8_l3", "q8_gemv_q8x_r8_l6", "q8_gemv_q8x_r16_l3", "q8_gemv_q8x_r16_l6",
+    "q8_gemv_q8x1_r8_l3", "q8_gemv_q8x1_r8_l6", "q8_gemv_q8x1_r16_l3", "q8_gemv_q8x1_r16_l6",
+    "q8_gemv_q8x2_r8_l3", "q8_gemv_q8x2_r8_l6", "q8_gemv_q8x2_r16_l3", "q8_gemv_q8x2_r16_l6",
     "q8_quantize",
     "q8_gemm_s0_t1", "q8_gemm_s1_t1", "q8_gemm_s1_t2", "q8_gemm_s1_t4",
     "q8_gemm_h_t1_r4", "q8_gemm_h_t2_r2", "q8_gemm_h_t2_r4",
@@ -1154,7 +1156,7 @@ int q8_set_option(q8_ctx *c, const char *name, int value) {
                                         "gemv.group_loads",
                                         "gemm.smode", "gemm.tpw",    "gemm.twaves",    "gemm.xcd_remap",
                                         "gemm.kwaves", "gemm.slices", "gemm.rwaves",    "gemm.f16",
-                                        "gemm.pipe",  "gemm.lds",      "gemm.silu"};
+                                        "gemm.pipe",  "gemm.lds",      "gemm.silu",      "gemm.small_gemv"};
     bool ok = false;
     for (const char *k : known) ok = ok || std::strcmp(k, name) == 0;
     if (!ok) return fail(Q8_ERR_INVALID, "unknown option %s", name);
@@ -1551,6 +1553,8 @@ int q8_matmul_prompt_group(q8_ctx *c, const q8_group_entry *group, int count, co
     return run_gemm(c, m, count, prepared, n, b);
 }
 
+int run_gemv_q8x(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset, int n, float *y, const float *bias);
+
 int q8_matmul(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset, int n, q8_dptr y, size_t y_offset,
               const q8_prepared *prepared, q8_dptr bias, size_t bias_offset) {
     if (!c) return fail(Q8_ERR_INVALID, "q8_matmul: null context");
@@ -1559,6 +1563,11 @@ int q8_matmul(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset, int n, 
     q8_group_entry e{w, y, y_offset};
     if (n == 1) return q8_matmul_decode_group(c, &e, 1, x, x_offset, w->k, bias, bias_offset);
     std::lock_guard<std::recursive_mutex> lock(c->mu);
+    if (!prepared && n == 2 && option(c, "gemm.small_gemv", 1)) {
+        // two tokens of f32 x: the quantized-x GEMV reads the weights once for both
+        const int rc = run_gemv_q8x(c, w, x, x_offset, n, fptr(y, y_offset), bias ? fptr(bias, bias_offset) : nullptr);
+        if (rc != Q8_ERR_UNSUPPORTED) return rc;
+    }
     q8_prepared own{};
     if (!prepared) {
         Q8_TRY(q8_prepare(c, x, x_offset, n, w->k, &own));
@@ -1567,23 +1576,20 @@ int q8_matmul(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset, int n, 
     return q8_matmul_prompt_group(c, &e, 1, prepared, n, w->k, bias, bias_offset);
 }
 
-int q8_matmul_q8(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset, int n, q8_dptr y, size_t y_offset,
-                 q8_dptr bias, size_t bias_offset) {
-    if (!c) return fail(Q8_ERR_INVALID, "q8_matmul_q8: null context");
-    Q8_TRY(check_weight(c, w));
-    Q8_TRY(check_n(n));
-    if (n >= 2) return q8_matmul(c, w, x, x_offset, n, y, y_offset, nullptr, bias, bias_offset);
-    std::lock_guard<std::recursive_mutex> lock(c->mu);
+// The quantized-x row-slice GEMV (q8_gemv_q8x{1,2}_*) over one or two
+// tokens of f32 x: the f32 GEMV's row slices where its tactic takes them,
+// else 16-row slices (8-row with six loads past 192 blocks), at most 16
+// waves; Q8_ERR_UNSUPPORTED past that or past 64 KiB of LDS (the caller may
+// keep the GEMM).
+int run_gemv_q8x(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset, int n, float *y, const float *bias) {
     const int k = w->k;
     const int nb = w->nb;
+    if (n < 1 || n > 2) return fail(Q8_ERR_UNSUPPORTED, "quantized-x GEMV: %d tokens (1 or 2)", n);
+    const int nt = n;
     const q8_dptr xp = (q8_dptr)(uintptr_t)fptr(x, x_offset);
-    float *yp = fptr(y, y_offset);
-    const float *bp = bias ? fptr(bias, bias_offset) : nullptr;
-    Q8_TRY(check_span(c, xp, (size_t)k * 4, "q8_matmul_q8 x"));
-    Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)yp, (size_t)w->out * 4, "q8_matmul_q8 y"));
-    if (bp) Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)bp, (size_t)w->out * 4, "q8_matmul_q8 bias"));
-    // the f32 GEMV's row slices where its tactic takes them, else 16-row
-    // slices (8-row with six loads past 192 blocks) with at most 16 waves
+    Q8_TRY(check_span(c, xp, (size_t)n * k * 4, "gemv x"));
+    Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)y, (size_t)n * w->out * 4, "gemv y"));
+    if (bias) Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)bias, (size_t)n * w->out * 4, "gemv bias"));
     const q8_tactic t = plan(c, 1, w->out, k, 1);
     int rs = 16, nl = nb <= 96 ? 3 : 6;
     if (t.row_slice == 8 || t.row_slice == 16) {
@@ -1597,26 +1603,39 @@ int q8_matmul_q8(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset, int 
     const int bpw = nl * (64 / (2 * rs));
     const int waves = (int)ceil_div(nb, bpw);
     if (waves > 16)
-        return fail(Q8_ERR_UNSUPPORTED, "q8_matmul_q8: k = %d needs %d waves a workgroup (16 at most)", k, waves);
+        return fail(Q8_ERR_UNSUPPORTED, "quantized-x GEMV: k = %d needs %d waves a workgroup (16 at most)", k, waves);
+    // quant bytes and block scales per token, the waves' row sums, the dead lanes' pad
+    const size_t lds = ((size_t)nt * nb * 8 + (size_t)nt * nb + (size_t)nt * waves * rs + Q8_GEMV_PAD_FLOATS) * 4;
+    if (lds > 65536)
+        return fail(Q8_ERR_UNSUPPORTED, "quantized-x GEMV: %zu bytes of LDS for %d tokens of k = %d", lds, nt, k);
     Q8GemvArgs a{};
     a.members = 1;
     a.m[0].quants = w->quants;
     a.m[0].scales = w->scales;
-    a.m[0].y = yp;
-    a.m[0].bias = bp;
+    a.m[0].y = y;
+    a.m[0].bias = bias;
     a.m[0].rows = w->out;
     a.total_tiles = w->tiles;
     a.x = reinterpret_cast<const float *>(xp);
     a.nb = nb;
     a.waves_per_tile = waves;
     a.kslices = 1;
+    a.tokens = n;
     a.xcd_order = option(c, "gemv.xcd_order", 1) ? 1 : 0;
     const long long grid = (a.xcd_order ? ceil_div(w->tiles, 8) * 8 : (long long)w->tiles) * (Q8_TILE_ROWS / rs);
-    if (grid > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "q8_matmul_q8: grid of %lld workgroups", grid);
-    // quant bytes, block scales, the waves' row sums, the dead lanes' pad
-    const unsigned lds = (unsigned)((nb * 8 + nb + waves * rs + Q8_GEMV_PAD_FLOATS) * 4);
-    const Fn f = (Fn)(F_GEMV_Q8X_8_3 + (rs == 8 ? 0 : 2) + (nl == 3 ? 0 : 1));
-    return launch(c, f, (unsigned)grid, (unsigned)(waves * 64), lds, &a, sizeof a);
+    if (grid > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "quantized-x GEMV: grid of %lld workgroups", grid);
+    const Fn f = (Fn)(F_GEMV_Q8X1_8_3 + 4 * (nt - 1) + (rs == 8 ? 0 : 2) + (nl == 3 ? 0 : 1));
+    return launch(c, f, (unsigned)grid, (unsigned)(waves * 64), (unsigned)lds, &a, sizeof a);
+}
+
+int q8_matmul_q8(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset, int n, q8_dptr y, size_t y_offset,
+                 q8_dptr bias, size_t bias_offset) {
+    if (!c) return fail(Q8_ERR_INVALID, "q8_matmul_q8: null context");
+    Q8_TRY(check_weight(c, w));
+    Q8_TRY(check_n(n));
+    if (n >= 2) return q8_matmul(c, w, x, x_offset, n, y, y_offset, nullptr, bias, bias_offset);
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    return run_gemv_q8x(c, w, x, x_offset, 1, fptr(y, y_offset), bias ? fptr(bias, bias_offset) : nullptr);
 }
 
 int q8_matmul_noalloc(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset, int n, q8_dptr y,
@@ -1633,6 +1652,11 @@ int q8_matmul_noalloc(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset,
                                             "needs scratch", w->out, k);
         q8_group_entry e{w, y, y_offset};
         return q8_matmul_decode_group(c, &e, 1, x, x_offset, k, bias, bias_offset);
+    }
+    if (n == 2 && option(c, "gemm.small_gemv", 1)) {
+        // q8_matmul's two-token GEMV: x is quantized in LDS, no scratch
+        const int rc = run_gemv_q8x(c, w, x, x_offset, n, fptr(y, y_offset), bias ? fptr(bias, bias_offset) : nullptr);
+        if (rc != Q8_ERR_UNSUPPORTED) return rc;
     }
     if (!c->noalloc) return fail(Q8_ERR_NO_DEVICE, "q8_matmul_noalloc: no device scratch");
     const size_t need = prepared_bytes(n, k, Q8_PREPARED_I8, nullptr);

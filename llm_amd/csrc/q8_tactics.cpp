@@ -14,6 +14,12 @@ const Q8TacticRow kRows[] = {
     {"matmul.gemm_mfma_i8", Q8_KERNEL_GEMM, 2, Q8_MAX_TOKENS, Q8_MATURITY_MEASURED, 10,
      "n >= 2 quantizes activations (tensor.rs:104-125); v_mfma_i32_32x32x32_i8 is one Q8_0 block "
      "per instruction, exact int32, scale products on v_mfma_f32_32x32x1_2b_f32"},
+    {"matmul.gemv_q8x_two_tokens", Q8_KERNEL_GEMV, 2, 2, Q8_MATURITY_MEASURED, 9,
+     "f32 x at n = 2 (q8_matmul without prepared activations; ranked below the GEMM, which plans for "
+     "prepared activations keep): x quantized to Q8_0 in the GEMV's own launch, four v_dot4_i32_i8 per "
+     "half block, the weight stream read once for both tokens; configs[1]'s W: 7.25 us against 10.45 us "
+     "for quantize + int8 MFMA GEMM.  At n = 4 and 8 the quantization every workgroup repeats outgrew "
+     "the GEMM (11.5 and 24.0 us against 10.5)"},
     {"matmul.gemm_mfma_f16", Q8_KERNEL_GEMM_F16, 2, Q8_MAX_TOKENS, Q8_MATURITY_EXPERIMENTAL, 5,
      "quants are integers |q| <= 127, exact in f16: two v_mfma_f32_32x32x16_f16 give each block's int32 "
      "dot already in f32, removing the 16 v_cvt_f32_i32 per 32x32 tile and block that bound the int8 "

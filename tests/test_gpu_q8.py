@@ -24,7 +24,7 @@ SEED = 0x5EED
 J = [[0, 4, 1, 5], [2, 6, 3, 7]]
 OPTIONS = ("gemv.exact", "gemv.waves", "gemv.pairs", "gemv.slices", "gemv.rows", "gemv.loads", "gemv.xcd_order", "gemm.smode", "gemm.tpw", "gemm.twaves",
            "gemm.xcd_remap", "gemm.kwaves", "gemm.slices", "gemm.rwaves", "gemm.f16", "gemm.pipe", "gemm.lds",
-           "gemm.silu")
+           "gemm.silu", "gemm.small_gemv")
 
 
 def assert_close(got, ref, what):

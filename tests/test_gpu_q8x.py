@@ -9,7 +9,9 @@ of the token (oracle.matmul with n = 2 quantizes every token and takes
 dot_q8_0_q8_0 per row); the bar is the n >= 2 one (assert_parity against the
 exact block sums).  The int32 block dot is pinned exactly by power-of-two
 problems, the quantizer's rounding (half away from zero), NaN and zero blocks
-by crafted x, and n >= 2 equals q8_matmul bit for bit.
+by crafted x, and n >= 2 equals q8_matmul bit for bit; at n = 2, where
+q8_matmul itself takes the quantized-x GEMV, the GEMM (option
+gemm.small_gemv = 0) is held to the same bar.
 """
 import numpy as np
 import pytest
@@ -164,3 +166,32 @@ def test_deterministic_and_errors(gpu):
         gpu.matmul_q8(weight(r, 64, 2304), small, 0, 1, yb, 0)
     for buf in (xb, yb, small):
         buf.free()
+
+
+@pytest.mark.parametrize("out,k", [(5760, 2304), (392, 2304), (2304, 5760), (64, 96)])
+def test_two_tokens_gemv_and_gemm(gpu, out, k):
+    """q8_matmul at n = 2 on f32 x takes the two-token quantized-x GEMV;
+    option gemm.small_gemv = 0 keeps the int8 MFMA GEMM.  Both within the
+    n >= 2 bar of the reference, and the GEMV equals q8_matmul_q8."""
+    r = rng(500 + out + k)
+    w = weight(r, out, k)
+    x = oracle.make_activations(r, 2, k, outlier_rate=0.01)
+    ref = oracle.matmul(w.data, k, out, x, 2)
+    ex = exact_at(w.data, k, out, x, 2)
+    xb, ya, yb, yc = gpu.alloc(4 * 2 * k), gpu.alloc(4 * 2 * out), gpu.alloc(4 * 2 * out), gpu.alloc(4 * 2 * out)
+    xb.upload(x)
+    try:
+        gpu.matmul(w, xb, 0, 2, ya, 0)
+        gpu.matmul_q8(w, xb, 0, 2, yc, 0)
+        gpu.set_option("gemm.small_gemv", 0)
+        gpu.matmul(w, xb, 0, 2, yb, 0)
+    finally:
+        gpu.set_option("gemm.small_gemv", -1)
+    got_gemv = ya.download(np.float32, 2 * out).reshape(2, out)
+    got_gemm = yb.download(np.float32, 2 * out).reshape(2, out)
+    assert_parity(got_gemv, ref, ex, f"two-token GEMV {out}x{k}")
+    assert_parity(got_gemm, ref, ex, f"two-token GEMM {out}x{k}")
+    assert_bits(yc.download(np.float32, 2 * out).reshape(2, out), got_gemv, "q8_matmul_q8 n=2")
+    for b in (xb, ya, yb, yc):
+        b.free()
+    gpu.release(w)
