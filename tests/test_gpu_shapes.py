@@ -1,0 +1,96 @@
+"""Seeded random shapes through every matmul entry point, against the oracle.
+
+The fixed-shape tests pin the benchmark shapes and the edge cases by hand;
+this sweep draws (out, k, n) at random -- out from 1 to 3000 (partial row
+tiles, fewer and more tiles than CUs), k = 32 * [1, 200] (odd block counts,
+one block, K past one wave's staging), n from the decode GEMV through the
+two-token GEMV to the MFMA GEMM's partial token tiles -- so that every launch
+plan the tactic table derives (row slices, the tile kernel, K splits, token
+groups) meets the oracle under the bar of its path:
+  * n = 1 in the exact block order: bit-identical to the reference's AVX2
+    order where the host oracle takes it (tensor.rs:96-101, quant.rs:54-91);
+  * n = 1 in the default tree order and every n >= 2: within
+    2e-6 + 1e-5 |ref| of the reference (assert_parity, tensor.rs:104-148);
+  * q8_matmul_q8 at n = 1: the n >= 2 arithmetic on one token, same bar.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from llm_amd import q8
+from test_gpu_q8 import assert_bits, assert_parity, exact_at
+
+pytestmark = pytest.mark.gpu
+
+SEED = 0x5EED + 0x5A5A
+CASES = 60
+
+
+def draw(i):
+    r = np.random.default_rng(SEED + i)
+    out = int(r.choice([int(r.integers(1, 64)), int(r.integers(64, 800)), int(r.integers(800, 3000))]))
+    k = 32 * int(r.choice([1, int(r.integers(2, 40)), int(r.integers(40, 201))]))
+    n = int(r.choice([1, 1, 2, 3, 7, 8, 31, 33, int(r.integers(34, 300))]))
+    return out, k, n
+
+
+def dequant(wdata, out, k):
+    """W as f64: d * q per block (exact)."""
+    raw = np.asarray(wdata, np.uint8).reshape(out, k // 32, 34)
+    d = raw[:, :, 0:2].copy().view(np.float16).astype(np.float64)
+    q = raw[:, :, 2:].copy().view(np.int8).astype(np.float64)
+    return (d * q).reshape(out, k)
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    g = q8.Gpu(0)
+    yield g
+    g.close()
+
+
+@pytest.mark.parametrize("case", range(CASES))
+def test_random_shape(gpu, case):
+    out, k, n = draw(case)
+    r = np.random.default_rng(SEED + 1000 + case)
+    w = q8.Weight(oracle.make_q8_weight(r, out, k), k, out)
+    x = oracle.make_activations(r, n, k, outlier_rate=0.01)
+    plan = gpu.plan(n, out, k)
+    print(f"\nrandom case {case}: out={out} k={k} n={n} plan {plan.get('name')} row_slice {plan.get('row_slice')} "
+          f"kslices {plan.get('kslices')}", flush=True)
+    xb, yb = gpu.alloc(4 * n * k), gpu.alloc(4 * n * out)
+    xb.upload(x)
+    try:
+        ref = oracle.matmul(w.data, k, out, x, n)
+        what = f"random out={out} k={k} n={n}"
+        if n == 1:
+            gpu.set_option("gemv.exact", 1)
+            gpu.matmul(w, xb, 0, 1, yb, 0)
+            got = yb.download(np.float32, out)
+            if oracle.simd_path() == "avx2+fma":
+                assert_bits(got, ref.reshape(-1), what + " exact order")
+            else:
+                assert_parity(got, ref.reshape(-1), dequant(w.data, out, k) @ x.reshape(-1).astype(np.float64),
+                              what + " exact order")
+            gpu.set_option("gemv.exact", -1)
+            gpu.matmul(w, xb, 0, 1, yb, 0)
+            tree = yb.download(np.float32, out)
+            assert_parity(tree, ref.reshape(-1), dequant(w.data, out, k) @ x.reshape(-1).astype(np.float64),
+                          what + " tree order")
+            # q8_matmul_q8: x quantized, the n >= 2 arithmetic on one token
+            gpu.matmul_q8(w, xb, 0, 1, yb, 0)
+            q8y = yb.download(np.float32, out)
+            x2 = np.stack([x.reshape(-1), x.reshape(-1)])
+            ref2 = oracle.matmul(w.data, k, out, x2, 2)[0]
+            qx, sx = oracle.quantize_q8_0(x.reshape(-1))
+            assert_parity(q8y, ref2, exact_at(w.data, k, out, quants=qx.reshape(1, k), scales=sx.reshape(1, -1)),
+                          what + " quantized x")
+        else:
+            gpu.matmul(w, xb, 0, n, yb, 0)
+            got = yb.download(np.float32, n * out).reshape(n, out)
+            assert_parity(got, ref, exact_at(w.data, k, out, x, n), what)
+    finally:
+        gpu.set_option("gemv.exact", -1)
+        xb.free()
+        yb.free()
+        gpu.release(w)
