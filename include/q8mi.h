@@ -163,8 +163,9 @@ int q8_sync(q8_ctx *ctx);
  * again.  A plan the current workspaces already cover changes nothing.  The
  * reference overlaps regions whose phases never meet; here they are
  * disjoint, so any order of calls is safe.  Planning moves workspaces when
- * it allocates: graphs captured before must be dropped (the generation in
- * q8_workspace_info changes). */
+ * it allocates, without copying them: graphs captured before must be dropped
+ * (the generation in q8_workspace_info changes) and q8_prepared views taken
+ * before no longer point at live activations -- plan first, then prepare. */
 typedef struct {
     int max_tokens;  /* most tokens of any call, 1..Q8_MAX_TOKENS */
     int max_k;       /* longest activation row: the widest weight k, attention heads x 64, norm width */
