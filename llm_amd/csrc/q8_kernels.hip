@@ -212,6 +212,29 @@ static __device__ __forceinline__ float xor_max(float v) {
     }
 }
 
+// Reads one dword of every 64-byte line of the explicit kernel arguments
+// (ARGS) as one batch of scalar loads with one wait.  Kernel arguments are
+// read through the scalar cache a line at a time, and a prologue whose
+// argument reads depend on each other (the XCD remap, then the tile split,
+// then the member, then its pointers) otherwise takes one scalar-cache miss
+// per line in series before its first weight load; after this every later
+// argument read hits.  Every read stays inside the explicit arguments.  Used
+// by the GEMMs (configs[1] n = 8 and 64: 0.5 us less per launch); the GEMVs
+// read their arguments in one batch already and measured slower with it.
+// GROUP_SIZE: the workgroup size too (a hidden argument past the explicit
+// ones), for kernels that read it.
+template <typename ARGS, bool GROUP_SIZE = false>
+static __device__ __forceinline__ void kernarg_lines() {
+    constexpr int LINES = ((int)sizeof(ARGS) + 63) / 64;
+    static_assert(LINES <= 8, "kernel arguments past eight lines");
+    const uint32_t *kp = (const uint32_t *)__builtin_amdgcn_kernarg_segment_ptr();
+    uint32_t v[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = kp[16 * min(i, LINES - 1)];
+    const uint32_t gs = GROUP_SIZE ? (uint32_t)blockDim.x : 0u;
+    asm volatile("" ::"s"(v[0]), "s"(v[1]), "s"(v[2]), "s"(v[3]), "s"(v[4]), "s"(v[5]), "s"(v[6]), "s"(v[7]), "s"(gs));
+}
+
 // The same butterfly step on an f64 (the folded norm's sums of squares): both
 // 32-bit halves move with the same DPP or row swap.
 template <int M>
@@ -869,6 +892,9 @@ static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
     const int nb = a.nb;
     asm volatile("" ::"s"(mq), "s"(msc), "s"(my), "s"(mbias), "s"(mrows), "s"(xg), "s"(nb), "s"(a.xcd_order),
                  "s"(a.total_tiles));
+    // the combine's partials in the same kernel-argument read: a second read
+    // would wait ahead of the first partial and weight loads
+    if constexpr (CMB) asm volatile("" ::"s"(a.attn_acc), "s"(a.attn_ms), "s"(a.attn_splits));
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int j = lane / LPB;
@@ -1072,7 +1098,6 @@ static __device__ __forceinline__ void gemv_q8x_body(const Q8GemvArgs &a) {
                  "s"(a.total_tiles), "s"(ntok));
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nw = (int)(blockDim.x >> 6);
     const int j = lane / LPB;
     const int h = (lane / RS) & 1;
     const int r = lane % RS;
@@ -1087,10 +1112,13 @@ static __device__ __forceinline__ void gemv_q8x_body(const Q8GemvArgs &a) {
     const int b_last = max(b_end - 1, 0);
     const uint8_t *qbase = mq + (size_t)tile * nb * Q8_UNIT_BYTES + 16 * (32 * h + srow);
     const uint16_t *sbase = msc + (size_t)tile * nb * Q8_TILE_ROWS + srow;
+    // the pad sits before the row sums so that no address of the quantize
+    // step waits on the workgroup size (a second kernel-argument read ahead
+    // of the first weight load measured 0.3 us on configs[0])
     uint8_t *xq = reinterpret_cast<uint8_t *>(smem);  // [NT][nb * 32] quant bytes, permuted
     float *xd = smem + NT * nb * 8;                    // [NT][nb] block scales
-    float *vbuf = xd + NT * nb;                        // [NT][waves][RS] row sums
-    float *pad = vbuf + NT * nw * RS;                  // stores of dead lanes land here, unread
+    float *pad = xd + NT * nb;                         // stores of dead lanes land here, unread
+    float *vbuf = pad + Q8_GEMV_PAD_FLOATS;            // [NT][waves][RS] row sums
 
     const int st_begin = 8 * b_begin;
     const int st_end = 8 * b_end;
@@ -1169,10 +1197,15 @@ static __device__ __forceinline__ void gemv_q8x_body(const Q8GemvArgs &a) {
                 const auto sw = __builtin_amdgcn_permlane16_swap((unsigned)s, (unsigned)s, false, false);
                 isum = (int)(sw[0] + sw[1]);
             }
-            const float v = (dw * xd[t * nb + b]) * (float)isum;
+            // the scale read stays unconditional: sunk under the bu < b_end
+            // select it became an exec-masked branch per load (measured slower)
+            float xs = xd[t * nb + b];
+            asm volatile("" : "+v"(xs));
+            const float v = (dw * xs) * (float)isum;
             lsum[t] = bu < b_end ? lsum[t] + v : lsum[t];
         }
     }
+    const int nw = (int)(blockDim.x >> 6);
 #pragma unroll
     for (int t = 0; t < NT; t++) {
         float ls = lsum[t];
@@ -1698,6 +1731,7 @@ template <int SMODE, int TPW>
 static __device__ __forceinline__ void gemm_body(const Q8GemmArgs &a) {
     extern __shared__ __attribute__((aligned(16))) float gsm[];  // [kwaves-1][twaves][TPW][64][16]
     __shared__ int last_flag;
+    kernarg_lines<Q8GemmArgs>();
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform, in an SGPR
     const int TW = a.twaves;
@@ -1949,6 +1983,7 @@ struct SiluOps {
 
 extern "C" __global__ __launch_bounds__(512) void q8_gemm_silu(Q8GemmArgs a) {
     extern __shared__ __attribute__((aligned(16))) float ssm[];
+    kernarg_lines<Q8GemmArgs, true>();
     const int lane = threadIdx.x & 63;
     const int kw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int KW = blockDim.x >> 6;
@@ -2138,6 +2173,7 @@ template <int TPW, int RW, bool I8 = false>
 static __device__ __forceinline__ void gemm_h_body(const Q8GemmArgs &a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t hsm[];
     constexpr int UNIT = I8 ? Q8_UNIT_BYTES : Q8_UNIT_F16_BYTES;  // activation unit in LDS and HBM
+    kernarg_lines<Q8GemmArgs, true>();
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int KW = (blockDim.x >> 6) / RW;
@@ -2391,6 +2427,7 @@ struct PipeRes {
 template <int TPW>
 static __device__ __forceinline__ void gemm_p_body(const Q8GemmArgs &a) {
     extern __shared__ __attribute__((aligned(16))) float psm[];  // [kwaves-1][twaves][TPW][64][16]
+    kernarg_lines<Q8GemmArgs>();
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int TW = a.twaves;
