@@ -138,7 +138,7 @@ int q8_device_info(q8_ctx *ctx, int *cu_count, size_t *total_bytes, size_t *free
 void *q8_stream(q8_ctx *ctx);
 /* Tuning/testing switches; value -1 restores the tactic table's choice.
  * Names: "gemv.exact", "gemv.waves", "gemv.pairs", "gemv.slices",
- * "gemv.rows" (8, 16 or 32), "gemv.loads" (3 or 6), "gemv.xcd_order" (0 or 1),
+ * "gemv.rows" (8, 16 or 32), "gemv.loads" (2 with 8-row slices, 3 or 6), "gemv.xcd_order" (0 or 1),
  * "gemm.smode", "gemm.tpw", "gemm.twaves", "gemm.xcd_remap", "gemm.kwaves",
  * "gemm.slices", "gemm.rwaves", "gemm.pipe", "gemm.lds", "gemm.silu",
  * "gemm.f16" (0: int8 prepared activations and the int8-MFMA GEMM for every

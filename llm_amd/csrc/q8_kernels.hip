@@ -1048,6 +1048,7 @@ static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
     extern "C" __global__ __launch_bounds__(1024) void q8_gemv_rc##RS##_l##NL##_e0(Q8GemvArgs a) { \
         gemv_rs_body<RS, NL, 1, 0>(a);                                                                 \
     }
+Q8_GEMV_RS_KERNEL(8, 2)
 Q8_GEMV_RS_KERNEL(8, 3)
 Q8_GEMV_RS_KERNEL(8, 6)
 Q8_GEMV_RS_KERNEL(16, 3)
@@ -1231,8 +1232,9 @@ static __device__ __forceinline__ void gemv_q8x_body(const Q8GemvArgs &a) {
     extern "C" __global__ __launch_bounds__(1024) void q8_gemv_q8x##NT##_r##RS##_l##NL(Q8GemvArgs a) { \
         gemv_q8x_body<RS, NL, NT>(a);                                                                    \
     }
-#define Q8_GEMV_Q8X_TOKENS(NT) \
-    Q8_GEMV_Q8X_KERNEL(8, 3, NT) Q8_GEMV_Q8X_KERNEL(8, 6, NT) Q8_GEMV_Q8X_KERNEL(16, 3, NT) Q8_GEMV_Q8X_KERNEL(16, 6, NT)
+#define Q8_GEMV_Q8X_TOKENS(NT)                                                                          \
+    Q8_GEMV_Q8X_KERNEL(8, 2, NT) Q8_GEMV_Q8X_KERNEL(8, 3, NT) Q8_GEMV_Q8X_KERNEL(8, 6, NT)                 \
+    Q8_GEMV_Q8X_KERNEL(16, 3, NT) Q8_GEMV_Q8X_KERNEL(16, 6, NT)
 Q8_GEMV_Q8X_TOKENS(1)
 Q8_GEMV_Q8X_TOKENS(2)
 

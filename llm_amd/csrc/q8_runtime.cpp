@@ -79,6 +79,7 @@ enum Fn {
     F_GEMV_G8_3_E0, F_GEMV_G16_3_E0, F_GEMV_G16_6_E0, F_GEMV_S8_3_E0, F_GEMV_S16_6_E0,
     F_GEMV_Q8X1_8_3, F_GEMV_Q8X1_8_6, F_GEMV_Q8X1_16_3, F_GEMV_Q8X1_16_6,
     F_GEMV_Q8X2_8_3, F_GEMV_Q8X2_8_6, F_GEMV_Q8X2_16_3, F_GEMV_Q8X2_16_6,
+    F_GEMV_R8_2, F_GEMV_RC8_2, F_GEMV_R8_2_E0, F_GEMV_RC8_2_E0, F_GEMV_Q8X1_8_2, F_GEMV_Q8X2_8_2,
     F_QUANTIZE,
     F_GEMM_S0_T1, F_GEMM_S1_T1, F_GEMM_S1_T2, F_GEMM_S1_T4,
     F_GEMM_H_T1_R4, F_GEMM_H_T2_R2, F_GEMM_H_T2_R4,
@@ -112,6 +113,8 @@ const char *const kFnNames[F_COUNT] = {
     "q8_gemv_g8_l3_e0", "q8_gemv_g16_l3_e0", "q8_gemv_g16_l6_e0", "q8_gemv_s8_l3_e0", "q8_gemv_s16_l6_e0",
     "q8_gemv_q8x1_r8_l3", "q8_gemv_q8x1_r8_l6", "q8_gemv_q8x1_r16_l3", "q8_gemv_q8x1_r16_l6",
     "q8_gemv_q8x2_r8_l3", "q8_gemv_q8x2_r8_l6", "q8_gemv_q8x2_r16_l3", "q8_gemv_q8x2_r16_l6",
+    "q8_gemv_r8_l2", "q8_gemv_rc8_l2", "q8_gemv_r8_l2_e0", "q8_gemv_rc8_l2_e0", "q8_gemv_q8x1_r8_l2",
+    "q8_gemv_q8x2_r8_l2",
     "q8_quantize",
     "q8_gemm_s0_t1", "q8_gemm_s1_t1", "q8_gemm_s1_t2", "q8_gemm_s1_t4",
     "q8_gemm_h_t1_r4", "q8_gemm_h_t2_r2", "q8_gemm_h_t2_r4",
@@ -335,7 +338,8 @@ q8_tactic plan(q8_ctx *c, int n, int out, int k, int slots = 1, int fmt = -1) {
         if (t.row_slice != Q8_TILE_ROWS) {
             const int loads = option(c, "gemv.loads", -1);
             if (loads > 0) t.slice_loads = loads;
-            if (t.slice_loads != 3 && t.slice_loads != 6) t.slice_loads = 6;
+            if (t.slice_loads != 2 && t.slice_loads != 3 && t.slice_loads != 6) t.slice_loads = 6;
+            if (t.slice_loads == 2 && t.row_slice != 8) t.slice_loads = 3;  // two loads: 8-row slices only
         }
     } else {
         t.smode = option(c, "gemm.smode", t.smode) ? 1 : 0;
@@ -460,8 +464,14 @@ int run_gemv_rs(q8_ctx *c, const q8_weight *w, float *y, q8_dptr x, const float 
     const long long grid = (a.xcd_order ? ceil_div(w->tiles, 8) * 8 : (long long)w->tiles) * (Q8_TILE_ROWS / rs);
     if (grid > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "gemv: grid of %lld workgroups", grid);
     const unsigned lds = (unsigned)((nb * 32 + rs * Q8_GEMV_VROW(nb) + Q8_GEMV_PAD_FLOATS) * 4);
-    const int fi = (rs == 8 ? 0 : 2) + (nl == 3 ? 0 : 1);
-    const Fn f = (Fn)((exact ? (comb ? F_GEMV_RC8_3 : F_GEMV_R8_3) : (comb ? F_GEMV_RC8_3_E0 : F_GEMV_R8_3_E0)) + fi);
+    Fn f;
+    if (nl == 2) {  // built for 8-row slices only
+        if (rs != 8) return Q8_ERR_UNSUPPORTED;
+        f = exact ? (comb ? F_GEMV_RC8_2 : F_GEMV_R8_2) : (comb ? F_GEMV_RC8_2_E0 : F_GEMV_R8_2_E0);
+    } else {
+        const int fi = (rs == 8 ? 0 : 2) + (nl == 3 ? 0 : 1);
+        f = (Fn)((exact ? (comb ? F_GEMV_RC8_3 : F_GEMV_R8_3) : (comb ? F_GEMV_RC8_3_E0 : F_GEMV_R8_3_E0)) + fi);
+    }
     return launch(c, f, (unsigned)grid, (unsigned)(waves * 64), lds, &a, sizeof a);
 }
 
@@ -1164,8 +1174,8 @@ int q8_set_option(q8_ctx *c, const char *name, int value) {
         return fail(Q8_ERR_INVALID, "gemv.pairs must be one of 2, 3, 5, 9");
     if (std::strcmp(name, "gemv.rows") == 0 && value >= 0 && value != 0 && value != 8 && value != 16 && value != 32)
         return fail(Q8_ERR_INVALID, "gemv.rows must be 8, 16 or 32 (32: the tile kernel)");
-    if (std::strcmp(name, "gemv.loads") == 0 && value > 0 && value != 3 && value != 6)
-        return fail(Q8_ERR_INVALID, "gemv.loads must be 3 or 6");
+    if (std::strcmp(name, "gemv.loads") == 0 && value > 0 && value != 2 && value != 3 && value != 6)
+        return fail(Q8_ERR_INVALID, "gemv.loads must be 2 (8-row slices), 3 or 6");
     if (std::strcmp(name, "gemv.group_rows") == 0 && value > 0 && value != 8 && value != 16 && value != 32)
         return fail(Q8_ERR_INVALID, "gemv.group_rows must be 0 or 32 (the tile kernel), 8 or 16");
     if (std::strcmp(name, "gemv.group_loads") == 0 && value > 0 && value != 3 && value != 6)
@@ -1594,7 +1604,7 @@ int run_gemv_q8x(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset, int 
     int rs = 16, nl = nb <= 96 ? 3 : 6;
     if (t.row_slice == 8 || t.row_slice == 16) {
         rs = t.row_slice;
-        nl = t.slice_loads == 3 ? 3 : 6;
+        nl = t.slice_loads == 2 || t.slice_loads == 3 ? t.slice_loads : 6;
     }
     if (nb > 16 * nl * (64 / (2 * rs))) {
         rs = 8;
@@ -1624,7 +1634,8 @@ int run_gemv_q8x(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset, int 
     a.xcd_order = option(c, "gemv.xcd_order", 1) ? 1 : 0;
     const long long grid = (a.xcd_order ? ceil_div(w->tiles, 8) * 8 : (long long)w->tiles) * (Q8_TILE_ROWS / rs);
     if (grid > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "quantized-x GEMV: grid of %lld workgroups", grid);
-    const Fn f = (Fn)(F_GEMV_Q8X1_8_3 + 4 * (nt - 1) + (rs == 8 ? 0 : 2) + (nl == 3 ? 0 : 1));
+    const Fn f = nl == 2 ? (nt == 1 ? F_GEMV_Q8X1_8_2 : F_GEMV_Q8X2_8_2)
+                         : (Fn)(F_GEMV_Q8X1_8_3 + 4 * (nt - 1) + (rs == 8 ? 0 : 2) + (nl == 3 ? 0 : 1));
     return launch(c, f, (unsigned)grid, (unsigned)(waves * 64), (unsigned)lds, &a, sizeof a);
 }
 

@@ -99,6 +99,13 @@ void q8_gemv_shape(int out, int k, int cu_count, int slots, q8_tactic *t) {
     if (slots == 1 && tiles < cus && 2 * tiles >= cus && ceil_div(nb, 3 * 4) <= 16) {
         t->row_slice = 8;
         t->slice_loads = 3;
+        // Two loads per lane (eight blocks a wave, more and shorter waves)
+        // where every workgroup is resident at once, 32 waves a CU (eight per
+        // SIMD): configs[0] 5.13 -> 4.94 us, 4096 x 2304 4.43 -> 4.22 us; where
+        // a second round of workgroups would be needed it loses (6912 x 2304:
+        // 5.60 against 5.76 at three loads, 5.43 in 16-row slices).
+        const int w2 = ceil_div(nb, 2 * 4);
+        if (w2 <= 16 && 4 * tiles <= cus * (32 / w2)) t->slice_loads = 2;
     } else if (slots == 1 && tiles < cus) {
         if (ceil_div(nb, 3 * 2) <= 16) {
             t->row_slice = 16;

@@ -83,15 +83,16 @@ def test_tactic_table_invariants():
     assert len(names) == len(set(names))
 
 
-@pytest.mark.parametrize("out,k,rows,loads", [(2304, 2304, 16, 3), (2304, 5760, 16, 6), (5760, 2304, 8, 3),
-                                              (4096, 4096, 8, 3), (4096, 8192, 32, 0), (122880, 2304, 32, 0),
-                                              (64, 12288, 32, 0)])
+@pytest.mark.parametrize("out,k,rows,loads", [(2304, 2304, 16, 3), (2304, 5760, 16, 6), (5760, 2304, 8, 2),
+                                              (4096, 4096, 8, 2), (6912, 2304, 8, 3), (4096, 8192, 32, 0),
+                                              (122880, 2304, 32, 0), (64, 12288, 32, 0)])
 def test_plan_row_slices_follow_the_measured_rule(out, k, rows, loads):
     """Single-matrix GEMVs with fewer 32-row tiles than CUs run in row
     slices: 8 rows where 16-row slices would already fill the CUs (and K
-    fits 16 waves of three loads), else 16 rows (three loads per lane when K
-    fits 16 waves, else six); the lm_head and K beyond 16 waves keep the tile
-    kernel."""
+    fits 16 waves of three loads) -- two loads per lane where every
+    workgroup of nine or more waves is resident at once, else three -- else
+    16 rows (three loads per lane when K fits 16 waves, else six); the
+    lm_head and K beyond 16 waves keep the tile kernel."""
     t = llm_amd.plan(1, out, k)
     assert (t["row_slice"], t["slice_loads"]) == (rows, loads)
 
@@ -118,10 +119,14 @@ def test_plan_never_selects_a_rejected_tactic(n, out, k):
         # row slices: a workgroup per 8 or 16 rows, at most 16 waves over K
         assert t["row_slice"] in (8, 16, 32)
         if t["row_slice"] != 32:
-            assert t["slice_loads"] in (3, 6)
+            assert t["slice_loads"] in ((2, 3, 6) if t["row_slice"] == 8 else (3, 6))
             blocks_per_wave = t["slice_loads"] * 64 // (2 * t["row_slice"])
-            assert -(-nb // blocks_per_wave) <= 16
-            assert -(-out // 32) < 256  # only where the tile kernel leaves CUs idle
+            waves = -(-nb // blocks_per_wave)
+            assert waves <= 16
+            tiles = -(-out // 32)
+            assert tiles < 256  # only where the tile kernel leaves CUs idle
+            if t["slice_loads"] == 2:  # every workgroup resident at once (32 waves a CU, 256 CUs)
+                assert 4 * tiles <= 256 * (32 // waves)
     elif t["kernel"] == q8.KERNEL_GEMM_F16:
         # f16-MFMA family: built variants t1_r4, t2_r2, t2_r4; <= 512 threads
         assert n >= 2

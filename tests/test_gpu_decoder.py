@@ -399,15 +399,15 @@ def test_decode_attention_matches_the_oracle(gpu, visible, splits, n_head, n_kv)
 @pytest.mark.parametrize("visible,splits,n_head,n_kv", [(1, 1, 4, 2), (200, 1, 36, 36), (600, 3, 36, 36),
                                                         (640, 8, 36, 36), (4096, 8, 4, 1), (3000, 5, 8, 2),
                                                         (2000, 12, 8, 8), (300, 2, 32, 8)])
-@pytest.mark.parametrize("exact,rows,loads", [(1, -1, -1), (1, 8, 3), (1, 8, 6), (1, 16, 6), (1, 32, -1),
-                                               (0, -1, -1)])
+@pytest.mark.parametrize("exact,rows,loads", [(1, -1, -1), (1, 8, 2), (1, 8, 3), (1, 8, 6), (1, 16, 6), (1, 32, -1),
+                                               (0, -1, -1), (0, 8, 2)])
 def test_attention_matmul_add_equals_attention_then_matmul(gpu, visible, splits, n_head, n_kv, exact, rows, loads):
     """q8_attention_matmul_add: the partials combined in the output
     projection's GEMV prologue (or, past eight splits, the two calls it makes
     instead) give y bit-identical to q8_attention with the same splits then
     q8_matmul with y as the residual; and the attention alone is within the
-    f32 bar of the oracle.  rows/loads: the row-slice kernels q8_gemv_rc{8,16}
-    _l{3,6} (-1: the tactic's choice), where fewer threads than x has float4s
+    f32 bar of the oracle.  rows/loads: the row-slice kernels q8_gemv_rc8_l{2,3,6}
+    and q8_gemv_rc16_l{3,6} (-1: the tactic's choice), where fewer threads than x has float4s
     build the rest of x in turn, or the tile kernel (32).  Only splits > 8
     (the 12-split case) leave the folded combine for the two calls."""
     gpu.set_option("gemv.exact", exact)

@@ -323,7 +323,7 @@ def test_gemv_launch_shapes_agree(gpu, slices, waves, pairs, exact):
     gpu.release(w)
 
 
-ROW_SLICES = [(8, 3), (8, 6), (16, 3), (16, 6)]
+ROW_SLICES = [(8, 2), (8, 3), (8, 6), (16, 3), (16, 6)]
 
 
 @pytest.mark.parametrize("exact", [1, 0])

@@ -195,3 +195,30 @@ def test_two_tokens_gemv_and_gemm(gpu, out, k):
     for b in (xb, ya, yb, yc):
         b.free()
     gpu.release(w)
+
+
+@pytest.mark.parametrize("rows,loads", [(8, 2), (8, 3), (8, 6), (16, 3), (16, 6)])
+@pytest.mark.parametrize("out,k", [(5760, 2304), (200, 1056), (33, 96)])
+def test_every_slice_shape(gpu, rows, loads, out, k):
+    """Each built quantized-x kernel (q8_gemv_q8x{1,2}_r{8,16}_l{2,3,6}, the
+    slice shape taken from the f32 GEMV's options), one and two tokens,
+    within the n >= 2 bar of the reference."""
+    gpu.set_option("gemv.rows", rows)
+    gpu.set_option("gemv.loads", loads)
+    try:
+        r = rng(600 + rows + loads + out)
+        w = weight(r, out, k)
+        x = oracle.make_activations(r, 2, k, outlier_rate=0.01)
+        print(f"\nq8_matmul_q8 rows={rows} loads={loads} {out}x{k}", flush=True)
+        got1 = run_q8(gpu, w, x[0], 1)[0]
+        qx, sx = oracle.quantize_q8_0(x[0])
+        assert_parity(got1, oracle_one(w, x[0]),
+                      exact_at(w.data, k, out, quants=qx.reshape(1, k), scales=sx.reshape(1, -1)),
+                      f"q8_matmul_q8 n=1 rows={rows} loads={loads} {out}x{k}")
+        got2 = run_q8(gpu, w, x, 2)
+        assert_parity(got2, oracle.matmul(w.data, k, out, x, 2), exact_at(w.data, k, out, x, 2),
+                      f"q8_matmul_q8 n=2 rows={rows} loads={loads} {out}x{k}")
+        gpu.release(w)
+    finally:
+        gpu.set_option("gemv.rows", -1)
+        gpu.set_option("gemv.loads", -1)
