@@ -1199,7 +1199,7 @@ static __device__ __forceinline__ void gemv_q8x_body(const Q8GemvArgs &a) {
                 isum = (int)(sw[0] + sw[1]);
             }
             // the scale read stays unconditional: sunk under the bu < b_end
-            // select it became an exec-masked branch per load (measured slower)
+            // select it becomes an exec-masked branch around each LDS read
             float xs = xd[t * nb + b];
             asm volatile("" : "+v"(xs));
             const float v = (dw * xs) * (float)isum;
