@@ -235,6 +235,20 @@ static __device__ __forceinline__ void kernarg_lines() {
     asm volatile("" ::"s"(v[0]), "s"(v[1]), "s"(v[2]), "s"(v[3]), "s"(v[4]), "s"(v[5]), "s"(v[6]), "s"(v[7]), "s"(gs));
 }
 
+// Buffer loads over one wave-uniform stream: the stream's base and length in
+// a descriptor (SGPRs), the lane's constant offset in a VGPR and the block's
+// offset in an SGPR, so a load in a loop needs no vector address arithmetic
+// (a global load's 64-bit address is one v_lshl_add_u64 per load).  Reads
+// past `bytes` return 0 instead of touching memory.
+typedef __amdgpu_buffer_rsrc_t q8_stream_t;
+#define Q8_BUFFER_WORD3 0x00020000  // gfx9 raw buffer: 32-bit data, no swizzle
+static __device__ __forceinline__ q8_stream_t q8_stream(const void *base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, bytes, Q8_BUFFER_WORD3);
+}
+static __device__ __forceinline__ i32x4 q8_load16(q8_stream_t s, int lane_off, int block_off) {
+    return __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(s, lane_off, block_off, 0));
+}
+
 // The same butterfly step on an f64 (the folded norm's sums of squares): both
 // 32-bit halves move with the same DPP or row swap.
 template <int M>
@@ -1774,6 +1788,14 @@ static __device__ __forceinline__ void gemm_body(const Q8GemmArgs &a) {
         xsc[t] = a.xs + (size_t)ttc * nb * Q8_TILE_TOKENS;
     }
     const int lo = lane * 16;
+    const q8_stream_t wr = q8_stream(wq, nb * Q8_UNIT_BYTES);
+    const q8_stream_t wsr = q8_stream(wsc, nb * Q8_TILE_ROWS * 2);
+    q8_stream_t xr[TPW], xsr[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; t++) {
+        xr[t] = q8_stream(xq[t], nb * Q8_UNIT_BYTES);
+        xsr[t] = q8_stream(xsc[t], nb * Q8_TILE_TOKENS * 4);
+    }
 
     // this wave's block pairs: slice range split over the kw waves
     const int npairs = (nb + 1) >> 1;
@@ -1794,29 +1816,33 @@ static __device__ __forceinline__ void gemm_body(const Q8GemmArgs &a) {
     // Loads of the full pair (b, b+1): lane L's scale slot (b + h, r) is
     // element b*32 + L of the scale stream.
     auto load_full = [&](GemmOps<TPW> &q, int b) {
-        const size_t u0 = (size_t)b * Q8_UNIT_BYTES;
-        q.w0 = *(const i32x4 *)(wq + u0 + lo);
-        q.w1 = *(const i32x4 *)(wq + u0 + Q8_UNIT_BYTES + lo);
-        q.dw = wsc[(size_t)b * Q8_TILE_ROWS + lane];
+        const int u0 = b * Q8_UNIT_BYTES;
+        q.w0 = q8_load16(wr, lo, u0);
+        q.w1 = q8_load16(wr, lo, u0 + Q8_UNIT_BYTES);
+        q.dw = __builtin_amdgcn_raw_buffer_load_b16(wsr, 2 * lane, b * Q8_TILE_ROWS * 2, 0);
 #pragma unroll
         for (int t = 0; t < TPW; t++) {
-            q.x0[t] = *(const i32x4 *)(xq[t] + u0 + lo);
-            q.x1[t] = *(const i32x4 *)(xq[t] + u0 + Q8_UNIT_BYTES + lo);
-            q.sx[t] = xsc[t][(size_t)b * Q8_TILE_TOKENS + lane];
+            q.x0[t] = q8_load16(xr[t], lo, u0);
+            q.x1[t] = q8_load16(xr[t], lo, u0 + Q8_UNIT_BYTES);
+            q.sx[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xsr[t], 4 * lane,
+                                                                                     b * Q8_TILE_TOKENS * 4, 0));
         }
     };
     // The odd last block of an odd nb: the absent block repeats block b with
     // zero scales, so it adds 0 * 0.
     auto load_last = [&](GemmOps<TPW> &q, int b) {
-        const size_t u0 = (size_t)b * Q8_UNIT_BYTES;
-        q.w0 = *(const i32x4 *)(wq + u0 + lo);
+        const int u0 = b * Q8_UNIT_BYTES;
+        q.w0 = q8_load16(wr, lo, u0);
         q.w1 = q.w0;
-        q.dw = h ? 0u : (unsigned)wsc[(size_t)b * Q8_TILE_ROWS + r];
+        const unsigned dwr = __builtin_amdgcn_raw_buffer_load_b16(wsr, 2 * r, b * Q8_TILE_ROWS * 2, 0);
+        q.dw = h ? 0u : dwr;
 #pragma unroll
         for (int t = 0; t < TPW; t++) {
-            q.x0[t] = *(const i32x4 *)(xq[t] + u0 + lo);
+            q.x0[t] = q8_load16(xr[t], lo, u0);
             q.x1[t] = q.x0[t];
-            q.sx[t] = h ? 0.0f : xsc[t][(size_t)b * Q8_TILE_TOKENS + r];
+            const float sxr = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xsr[t], 4 * r,
+                                                                                            b * Q8_TILE_TOKENS * 4, 0));
+            q.sx[t] = h ? 0.0f : sxr;
         }
     };
     // One block pair of one token tile: the scale products first (the
@@ -2015,30 +2041,36 @@ extern "C" __global__ __launch_bounds__(512) void q8_gemm_silu(Q8GemmArgs a) {
     f32x16 ag = {}, au = {};
     const i32x16 izero = {};
     const f32x32 fzero = {};
+    const q8_stream_t wr = q8_stream(wq, nb * Q8_UNIT_BYTES), ur = q8_stream(uq, nb * Q8_UNIT_BYTES);
+    const q8_stream_t wsr = q8_stream(wsc, nb * Q8_TILE_ROWS * 2), usr = q8_stream(usc, nb * Q8_TILE_ROWS * 2);
+    const q8_stream_t xr = q8_stream(xq, nb * Q8_UNIT_BYTES), xsr = q8_stream(xsc, nb * Q8_TILE_TOKENS * 4);
     auto load_full = [&](SiluOps &q, int b) {
-        const size_t u0 = (size_t)b * Q8_UNIT_BYTES;
-        q.w0 = *(const i32x4 *)(wq + u0 + lo);
-        q.w1 = *(const i32x4 *)(wq + u0 + Q8_UNIT_BYTES + lo);
-        q.u0 = *(const i32x4 *)(uq + u0 + lo);
-        q.u1 = *(const i32x4 *)(uq + u0 + Q8_UNIT_BYTES + lo);
-        q.dw = wsc[(size_t)b * Q8_TILE_ROWS + lane];
-        q.du = usc[(size_t)b * Q8_TILE_ROWS + lane];
-        q.x0 = *(const i32x4 *)(xq + u0 + lo);
-        q.x1 = *(const i32x4 *)(xq + u0 + Q8_UNIT_BYTES + lo);
-        q.sx = xsc[(size_t)b * Q8_TILE_TOKENS + lane];
+        const int u0 = b * Q8_UNIT_BYTES;
+        q.w0 = q8_load16(wr, lo, u0);
+        q.w1 = q8_load16(wr, lo, u0 + Q8_UNIT_BYTES);
+        q.u0 = q8_load16(ur, lo, u0);
+        q.u1 = q8_load16(ur, lo, u0 + Q8_UNIT_BYTES);
+        q.dw = __builtin_amdgcn_raw_buffer_load_b16(wsr, 2 * lane, b * Q8_TILE_ROWS * 2, 0);
+        q.du = __builtin_amdgcn_raw_buffer_load_b16(usr, 2 * lane, b * Q8_TILE_ROWS * 2, 0);
+        q.x0 = q8_load16(xr, lo, u0);
+        q.x1 = q8_load16(xr, lo, u0 + Q8_UNIT_BYTES);
+        q.sx = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xsr, 4 * lane, b * Q8_TILE_TOKENS * 4, 0));
     };
     // the odd last block of an odd nb: the absent block repeats block b with zero scales
     auto load_last = [&](SiluOps &q, int b) {
-        const size_t u0 = (size_t)b * Q8_UNIT_BYTES;
-        q.w0 = *(const i32x4 *)(wq + u0 + lo);
+        const int u0 = b * Q8_UNIT_BYTES;
+        q.w0 = q8_load16(wr, lo, u0);
         q.w1 = q.w0;
-        q.u0 = *(const i32x4 *)(uq + u0 + lo);
+        q.u0 = q8_load16(ur, lo, u0);
         q.u1 = q.u0;
-        q.dw = h ? 0u : (unsigned)wsc[(size_t)b * Q8_TILE_ROWS + r];
-        q.du = h ? 0u : (unsigned)usc[(size_t)b * Q8_TILE_ROWS + r];
-        q.x0 = *(const i32x4 *)(xq + u0 + lo);
+        const unsigned dwr = __builtin_amdgcn_raw_buffer_load_b16(wsr, 2 * r, b * Q8_TILE_ROWS * 2, 0);
+        const unsigned dur = __builtin_amdgcn_raw_buffer_load_b16(usr, 2 * r, b * Q8_TILE_ROWS * 2, 0);
+        q.dw = h ? 0u : dwr;
+        q.du = h ? 0u : dur;
+        q.x0 = q8_load16(xr, lo, u0);
         q.x1 = q.x0;
-        q.sx = h ? 0.0f : xsc[(size_t)b * Q8_TILE_TOKENS + r];
+        const float sxr = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xsr, 4 * r, b * Q8_TILE_TOKENS * 4, 0));
+        q.sx = h ? 0.0f : sxr;
     };
     auto step = [&](const SiluOps &q, bool two) {
         {
