@@ -142,7 +142,10 @@ void *q8_stream(q8_ctx *ctx);
  * "gemm.smode", "gemm.tpw", "gemm.twaves", "gemm.xcd_remap", "gemm.kwaves",
  * "gemm.slices", "gemm.rwaves", "gemm.pipe", "gemm.lds", "gemm.silu",
  * "gemm.f16" (0: int8 prepared activations and the int8-MFMA GEMM for every
- * n; 1: f16 and the f16-MFMA GEMM for every n >= 2). */
+ * n; 1: f16 and the f16-MFMA GEMM for every n >= 2), "gemm.small_gemv" (0:
+ * n = 2 on f32 x takes the GEMM), "gemm.stream" (0: a one-token-tile GEMM
+ * reads its weights with the default cache policy instead of non-temporally;
+ * the results are the same bits either way). */
 int q8_set_option(q8_ctx *ctx, const char *name, int value);
 
 /* ---- device memory: Gpu::alloc / upload / download (cuda/mod.rs:530-567) ---- */

@@ -258,8 +258,10 @@ typedef __amdgpu_buffer_rsrc_t q8_stream_t;
 static __device__ __forceinline__ q8_stream_t q8_stream(const void *base, int bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, bytes, Q8_BUFFER_WORD3);
 }
+// NT: the non-temporal policy (the stream is read once, as q8_weight_load)
+template <bool NT = false>
 static __device__ __forceinline__ i32x4 q8_load16(q8_stream_t s, int lane_off, int block_off) {
-    return __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(s, lane_off, block_off, 0));
+    return __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(s, lane_off, block_off, NT ? 2 : 0));
 }
 
 // The same butterfly step on an f64 (the folded norm's sums of squares): both
@@ -1756,7 +1758,11 @@ struct GemmOps {
     float sx[TPW];
 };
 
-template <int SMODE, int TPW>
+// NT: the weight quants are read non-temporally, for launches where one wave
+// covers every token tile of its row tile, so each weight byte is read once
+// (one token tile: configs[1] n = 8, 10.15 -> 9.74 us; with more token groups
+// the re-reads want the caches: n = 512 142 -> 148 us).
+template <int SMODE, int TPW, bool NT = false>
 static __device__ __forceinline__ void gemm_body(const Q8GemmArgs &a) {
     extern __shared__ __attribute__((aligned(16))) float gsm[];  // [kwaves-1][twaves][TPW][64][16]
     __shared__ int last_flag;
@@ -1830,8 +1836,8 @@ static __device__ __forceinline__ void gemm_body(const Q8GemmArgs &a) {
     // element b*32 + L of the scale stream.
     auto load_full = [&](GemmOps<TPW> &q, int b) {
         const int u0 = b * Q8_UNIT_BYTES;
-        q.w0 = q8_load16(wr, lo, u0);
-        q.w1 = q8_load16(wr, lo, u0 + Q8_UNIT_BYTES);
+        q.w0 = q8_load16<NT>(wr, lo, u0);
+        q.w1 = q8_load16<NT>(wr, lo, u0 + Q8_UNIT_BYTES);
         q.dw = __builtin_amdgcn_raw_buffer_load_b16(wsr, 2 * lane, b * Q8_TILE_ROWS * 2, 0);
 #pragma unroll
         for (int t = 0; t < TPW; t++) {
@@ -1845,7 +1851,7 @@ static __device__ __forceinline__ void gemm_body(const Q8GemmArgs &a) {
     // zero scales, so it adds 0 * 0.
     auto load_last = [&](GemmOps<TPW> &q, int b) {
         const int u0 = b * Q8_UNIT_BYTES;
-        q.w0 = q8_load16(wr, lo, u0);
+        q.w0 = q8_load16<NT>(wr, lo, u0);
         q.w1 = q.w0;
         const unsigned dwr = __builtin_amdgcn_raw_buffer_load_b16(wsr, 2 * r, b * Q8_TILE_ROWS * 2, 0);
         q.dw = h ? 0u : dwr;
@@ -2638,6 +2644,7 @@ extern "C" __global__ __launch_bounds__(512) void q8_gemm_p_t2(Q8GemmArgs a) { g
 
 extern "C" __global__ __launch_bounds__(1024) void q8_gemm_s0_t1(Q8GemmArgs a) { gemm_body<0, 1>(a); }
 extern "C" __global__ __launch_bounds__(1024) void q8_gemm_s1_t1(Q8GemmArgs a) { gemm_body<1, 1>(a); }
+extern "C" __global__ __launch_bounds__(1024) void q8_gemm_s1_t1s(Q8GemmArgs a) { gemm_body<1, 1, true>(a); }
 extern "C" __global__ __launch_bounds__(512) void q8_gemm_s1_t2(Q8GemmArgs a) { gemm_body<1, 2>(a); }
 extern "C" __global__ __launch_bounds__(512) void q8_gemm_s1_t4(Q8GemmArgs a) { gemm_body<1, 4>(a); }
 

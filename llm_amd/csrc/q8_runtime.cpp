@@ -80,6 +80,7 @@ enum Fn {
     F_GEMV_Q8X1_8_3, F_GEMV_Q8X1_8_6, F_GEMV_Q8X1_16_3, F_GEMV_Q8X1_16_6,
     F_GEMV_Q8X2_8_3, F_GEMV_Q8X2_8_6, F_GEMV_Q8X2_16_3, F_GEMV_Q8X2_16_6,
     F_GEMV_R8_2, F_GEMV_RC8_2, F_GEMV_R8_2_E0, F_GEMV_RC8_2_E0, F_GEMV_Q8X1_8_2, F_GEMV_Q8X2_8_2,
+    F_GEMM_S1_T1S,
     F_QUANTIZE,
     F_GEMM_S0_T1, F_GEMM_S1_T1, F_GEMM_S1_T2, F_GEMM_S1_T4,
     F_GEMM_H_T1_R4, F_GEMM_H_T2_R2, F_GEMM_H_T2_R4,
@@ -115,6 +116,7 @@ const char *const kFnNames[F_COUNT] = {
     "q8_gemv_q8x2_r8_l3", "q8_gemv_q8x2_r8_l6", "q8_gemv_q8x2_r16_l3", "q8_gemv_q8x2_r16_l6",
     "q8_gemv_r8_l2", "q8_gemv_rc8_l2", "q8_gemv_r8_l2_e0", "q8_gemv_rc8_l2_e0", "q8_gemv_q8x1_r8_l2",
     "q8_gemv_q8x2_r8_l2",
+    "q8_gemm_s1_t1s",
     "q8_quantize",
     "q8_gemm_s0_t1", "q8_gemm_s1_t1", "q8_gemm_s1_t2", "q8_gemm_s1_t4",
     "q8_gemm_h_t1_r4", "q8_gemm_h_t2_r2", "q8_gemm_h_t2_r4",
@@ -808,8 +810,11 @@ int run_gemm(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n,
     const int max_threads = (tpw == 1 && !pipe) ? 1024 : 512;
     if (threads > max_threads) return fail(Q8_ERR_UNSUPPORTED, "gemm: %d threads per workgroup", threads);
     const unsigned lds = (unsigned)((kwaves - 1) * a.twaves * tpw * 64 * 16 * sizeof(float));
-    const Fn f = pipe ? (tpw == 2 ? F_GEMM_P_T2 : F_GEMM_P_T1)
-                      : !t.smode ? F_GEMM_S0_T1 : tpw == 4 ? F_GEMM_S1_T4 : tpw == 2 ? F_GEMM_S1_T2 : F_GEMM_S1_T1;
+    Fn f = pipe ? (tpw == 2 ? F_GEMM_P_T2 : F_GEMM_P_T1)
+                : !t.smode ? F_GEMM_S0_T1 : tpw == 4 ? F_GEMM_S1_T4 : tpw == 2 ? F_GEMM_S1_T2 : F_GEMM_S1_T1;
+    // one token tile: every weight byte is read by one wave, once (option
+    // gemm.stream = 0 keeps the default cache policy)
+    if (f == F_GEMM_S1_T1 && a.ttiles == 1 && option(c, "gemm.stream", 1)) f = F_GEMM_S1_T1S;
     return launch(c, f, (unsigned)nwg, (unsigned)threads, lds, &a, sizeof a);
 }
 
@@ -1166,7 +1171,7 @@ int q8_set_option(q8_ctx *c, const char *name, int value) {
                                         "gemv.group_loads",
                                         "gemm.smode", "gemm.tpw",    "gemm.twaves",    "gemm.xcd_remap",
                                         "gemm.kwaves", "gemm.slices", "gemm.rwaves",    "gemm.f16",
-                                        "gemm.pipe",  "gemm.lds",      "gemm.silu",      "gemm.small_gemv"};
+                                        "gemm.pipe",  "gemm.lds",      "gemm.silu",      "gemm.small_gemv", "gemm.stream"};
     bool ok = false;
     for (const char *k : known) ok = ok || std::strcmp(k, name) == 0;
     if (!ok) return fail(Q8_ERR_INVALID, "unknown option %s", name);

@@ -24,7 +24,7 @@ SEED = 0x5EED
 J = [[0, 4, 1, 5], [2, 6, 3, 7]]
 OPTIONS = ("gemv.exact", "gemv.waves", "gemv.pairs", "gemv.slices", "gemv.rows", "gemv.loads", "gemv.xcd_order", "gemm.smode", "gemm.tpw", "gemm.twaves",
            "gemm.xcd_remap", "gemm.kwaves", "gemm.slices", "gemm.rwaves", "gemm.f16", "gemm.pipe", "gemm.lds",
-           "gemm.silu", "gemm.small_gemv")
+           "gemm.silu", "gemm.small_gemv", "gemm.stream")
 
 
 def assert_close(got, ref, what):
@@ -1059,4 +1059,25 @@ def test_graph_replay_matches_eager(gpu):
         gpu.graph_destroy(graph)
     for b in (b1, bn, y1, yn):
         b.free()
+    gpu.release(w)
+
+
+@pytest.mark.parametrize("n,out,k", [(8, 5760, 2304), (1 + 31, 200, 96), (3, 64, 5760), (33, 2304, 2304)])
+def test_gemm_streamed_weights_are_the_same_bits(gpu, n, out, k):
+    """One token tile (n <= 32): the GEMM reads its weights non-temporally
+    (q8_gemm_s1_t1s); option gemm.stream = 0 keeps the default cache policy.
+    Same bits either way (the policy is not arithmetic), within the n >= 2
+    bar of the reference; n = 33 (two token tiles) is the plain kernel."""
+    r = rng(900 + n + out + k)
+    w = weight(r, out, k)
+    x = oracle.make_activations(r, n, k, outlier_rate=0.01)
+    try:
+        got = run_matmul(gpu, w, x, n).reshape(n, out)
+        gpu.set_option("gemm.stream", 0)
+        plain = run_matmul(gpu, w, x, n).reshape(n, out)
+    finally:
+        gpu.set_option("gemm.stream", -1)
+    assert_bits(got, plain, f"streamed weights n={n} {out}x{k}")
+    assert_parity(got, oracle.matmul(w.data, k, out, x, n), exact_at(w.data, k, out, x, n),
+                  f"streamed weights n={n} {out}x{k}")
     gpu.release(w)
