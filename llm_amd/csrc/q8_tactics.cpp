@@ -87,25 +87,27 @@ void q8_gemv_shape(int out, int k, int cu_count, int slots, q8_tactic *t) {
     // nb adds per row at the end of the kernel (configs[0]: 5.48 vs 5.26 us).
     t->exact = 0;
     // A single matrix with fewer tiles than CUs runs in row slices (whole K
-    // per workgroup): 8-row slices (four per tile, three loads per lane) when
-    // 16-row slices would already fill every CU, else 16-row slices with as
-    // many waves as fit 16 at three loads per lane, else six.  Measured
+    // per workgroup): 8-row slices (four per tile) when 16-row slices would
+    // already fill every CU and the 8-row workgroups fit (below), else
+    // 16-row slices with as many waves as fit 16 at three loads per lane,
+    // else six.  Measured
     // MALL-cold on gfx950 (tile kernel -> slices): configs[0] 5760 x 2304
     // 5.50 -> 5.36 us (16-row slices 5.50), O 2304 x 2304 4.98 -> 3.95 us
     // (8-row 4.29), down 2304 x 5760 8.25 -> 6.2 us (8-row 6.84); the lm_head
     // (3840 tiles) keeps the tile kernel (51.5 us either way).
     t->row_slice = Q8_TILE_ROWS;
     t->slice_loads = 0;
-    if (slots == 1 && tiles < cus && 2 * tiles >= cus && ceil_div(nb, 3 * 4) <= 16) {
+    // 8-row slices take two loads per lane (eight blocks a wave, more and
+    // shorter waves) and only where every workgroup is resident at once, 32
+    // waves a CU (eight per SIMD): configs[0] 5.13 -> 4.94 us against three
+    // loads, 4096 x 2304 4.43 -> 4.22 us.  Where they would need a second
+    // round of workgroups the 16-row slices win (6912 x 2304 with
+    // non-temporal weight loads: 16-row 5.22 us, 8-row 5.37 at two loads and
+    // 5.54 at three).
+    const int w2 = ceil_div(nb, 2 * 4);
+    if (slots == 1 && tiles < cus && 2 * tiles >= cus && w2 <= 16 && 4 * tiles <= cus * (32 / w2)) {
         t->row_slice = 8;
-        t->slice_loads = 3;
-        // Two loads per lane (eight blocks a wave, more and shorter waves)
-        // where every workgroup is resident at once, 32 waves a CU (eight per
-        // SIMD): configs[0] 5.13 -> 4.94 us, 4096 x 2304 4.43 -> 4.22 us; where
-        // a second round of workgroups would be needed it loses (6912 x 2304:
-        // 5.60 against 5.76 at three loads, 5.43 in 16-row slices).
-        const int w2 = ceil_div(nb, 2 * 4);
-        if (w2 <= 16 && 4 * tiles <= cus * (32 / w2)) t->slice_loads = 2;
+        t->slice_loads = 2;
     } else if (slots == 1 && tiles < cus) {
         if (ceil_div(nb, 3 * 2) <= 16) {
             t->row_slice = 16;

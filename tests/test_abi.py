@@ -84,15 +84,14 @@ def test_tactic_table_invariants():
 
 
 @pytest.mark.parametrize("out,k,rows,loads", [(2304, 2304, 16, 3), (2304, 5760, 16, 6), (5760, 2304, 8, 2),
-                                              (4096, 4096, 8, 2), (6912, 2304, 8, 3), (4096, 8192, 32, 0),
+                                              (4096, 4096, 8, 2), (6912, 2304, 16, 3), (4096, 8192, 32, 0),
                                               (122880, 2304, 32, 0), (64, 12288, 32, 0)])
 def test_plan_row_slices_follow_the_measured_rule(out, k, rows, loads):
     """Single-matrix GEMVs with fewer 32-row tiles than CUs run in row
-    slices: 8 rows where 16-row slices would already fill the CUs (and K
-    fits 16 waves of three loads) -- two loads per lane where every
-    workgroup of nine or more waves is resident at once, else three -- else
-    16 rows (three loads per lane when K fits 16 waves, else six); the
-    lm_head and K beyond 16 waves keep the tile kernel."""
+    slices: 8 rows at two loads per lane where 16-row slices would already
+    fill the CUs and every 8-row workgroup is resident at once, else 16 rows
+    (three loads per lane when K fits 16 waves, else six); the lm_head and K
+    beyond 16 waves keep the tile kernel."""
     t = llm_amd.plan(1, out, k)
     assert (t["row_slice"], t["slice_loads"]) == (rows, loads)
 
