@@ -405,13 +405,22 @@ def bench_decode_layer(gpu, steps, warmup, rng):
     h = summary(rotating_trials(gpu, lambda i: gpu.matmul(wl, xb, 0, 1, logits, 0), 1, 20, 2), per, 1e-9)
     t0 = time.perf_counter()
     best = gpu.lm_head_argmax(wl, xb, 0, logits, 0)
-    log(f"lm_head 122880x2304: {h['median_us']:.1f} us, {h['value']:.0f} GB/s")
+    call_us = round((time.perf_counter() - t0) * 1e6, 1)
+    # the argmax check: the folded argmax against the first maximum of the
+    # logits it wrote, and the top-2 logit gap (how far the winner stands clear)
+    lv = logits.download(np.float32, VOCAB)
+    order = np.argsort(lv, kind="stable")[::-1]
+    first = int(np.flatnonzero(lv == lv[order[0]])[0])
+    top2_gap = float(lv[order[0]] - lv[order[1]])
+    log(f"lm_head 122880x2304: {h['median_us']:.1f} us, {h['value']:.0f} GB/s; argmax {best} "
+        f"(first max of the logits {first}), top-2 gap {top2_gap:.3g}")
     gpu.release(wl)
     for b in (xb, qkv, hb, act, logits):
         b.free()
     return ({"us": s["median_us"], "weight_bytes": wbytes, "gbs": round(s["value"], 1), "copies": copies},
             {"us": h["median_us"], "gbs": round(h["value"], 1), "bytes": per, "argmax": best,
-             "argmax_call_us_host": round((time.perf_counter() - t0) * 1e6, 1)})
+             "argmax_matches_logits": best == first, "top2_logit_gap": top2_gap,
+             "top2_logits": [float(lv[order[0]]), float(lv[order[1]])], "argmax_call_us_host": call_us})
 
 
 # ---------------------------------------------------------------------------

@@ -31,7 +31,8 @@ const Q8TacticRow kRows[] = {
      "buffers cost ~130 VGPRs, two waves per SIMD instead of three; gate|up n=512 57 us vs 51 us"},
     {"matmul.gemm_mfma_i8_lds_staged", Q8_KERNEL_GEMM, 2, Q8_MAX_TOKENS, Q8_MATURITY_REJECTED, 0,
      "int8 activations staged once per workgroup in LDS with global_load_lds and shared by row-tile "
-     "waves (option gemm.lds), cutting L2 reads (the plain kernel keeps the L2 79% busy): one "
+     "waves (option gemm.lds), cutting L2 reads (the plain kernel reads both operands from L2 at "
+     "86-92% hit rates, its HBM fetch 1.4-3.4x the weight bytes: the activations once per XCD): one "
      "workgroup barrier per block pair costs more; gate|up n=512 56 us vs 51 us"},
     {"matmul.gemm_f32_small_n", Q8_KERNEL_GEMM, 2, 7, Q8_MATURITY_REJECTED, 0,
      "the reference GPU's f32-activation path for 2 <= n <= 7 (cuda/mod.rs:883-891) disagrees with "
