@@ -2847,8 +2847,15 @@ extern "C" __global__ __launch_bounds__(256) void q8_rmsnorm(Q8NormArgs a) {
 // The f64 sum is the same set of f32 terms as there, in another order.  The
 // prepared Q8_0 output uses that kernel's per-half-block element layout and
 // quantizer; rows from n up to the token-tile boundary are written as zeros.
+// Prepared output: the normalized row goes through LDS once ([block][36]
+// floats: the pad keeps the half-block reads at most two-way bank-conflicted)
+// so each thread takes its half-block in the quantizer's element order from
+// there; the row's x and w are read from memory only as the float4s of the
+// sum of squares.  The values are the same products (x * scale) * w as the
+// f32 output, so the prepared bytes are the f32 row's quantization.
 extern "C" __global__ __launch_bounds__(256) void q8_rmsnorm_row(Q8NormArgs a) {
     __shared__ double part[4];
+    extern __shared__ __attribute__((aligned(16))) float nrow[];  // [nb][Q8_NORM_LDS_PITCH], prepared output only
     const int tid = threadIdx.x;
     const int t = blockIdx.x;
     const int k = a.k;
@@ -2857,37 +2864,17 @@ extern "C" __global__ __launch_bounds__(256) void q8_rmsnorm_row(Q8NormArgs a) {
     const float *xrow = a.x + (size_t)min(t, a.n - 1) * k;
     const f32x4 *xr = (const f32x4 *)xrow;
     const f32x4 *wr = (const f32x4 *)a.w;
+    const bool need_w = a.out != nullptr || a.xq != nullptr;
     f32x4 xv[Q8_NORM_ROW_VEC], wv[Q8_NORM_ROW_VEC];
 #pragma unroll
     for (int j = 0; j < Q8_NORM_ROW_VEC; j++) {
-        const int i = tid + 256 * j;
-        const int ic = min(i, nv - 1);  // clamped in-bounds address; the value is unused past nv
-        xv[j] = xr[ic];
-        if (a.out) wv[j] = wr[ic];
-    }
-    // Prepared output: thread tid takes half tid % 2 of blocks tid / 2 + 128 g
-    // (the wave-per-row kernel's element layout per half-block), its x and w
-    // loaded with the rest, before the reduction.
-    const int nb = k / 32;
-    const int h = tid & 1;
-    float qx[2][4][4], qw[2][4][4];
-    if (a.xq) {
-#pragma unroll
-        for (int g = 0; g < 2; g++) {
-            const int b = min(128 * g + (tid >> 1), nb - 1);
-            const size_t base = (size_t)b * 32 + 2 * h;
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const size_t i0 = base + 8 * c, i1 = base + 8 * c + 4;
-                qx[g][c][0] = xrow[i0];
-                qx[g][c][1] = xrow[i0 + 1];
-                qx[g][c][2] = xrow[i1];
-                qx[g][c][3] = xrow[i1 + 1];
-                qw[g][c][0] = a.w[i0];
-                qw[g][c][1] = a.w[i0 + 1];
-                qw[g][c][2] = a.w[i1];
-                qw[g][c][3] = a.w[i1 + 1];
-            }
+        xv[j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        wv[j] = xv[j];
+        if (256 * j < nv) {  // workgroup-uniform
+            const int i = tid + 256 * j;
+            const int ic = min(i, nv - 1);  // clamped in-bounds address; the value is unused past nv
+            xv[j] = xr[ic];
+            if (need_w) wv[j] = wr[ic];
         }
     }
     double ss = 0.0;
@@ -2919,18 +2906,36 @@ extern "C" __global__ __launch_bounds__(256) void q8_rmsnorm_row(Q8NormArgs a) {
         }
     }
     if (a.xq) {
+        const int nb = k / 32;
+#pragma unroll
+        for (int j = 0; j < Q8_NORM_ROW_VEC; j++) {
+            const int i = tid + 256 * j;
+            if (i < nv) {
+                f32x4 o;
+#pragma unroll
+                for (int e = 0; e < 4; e++) o[e] = live ? (xv[j][e] * scale) * wv[j][e] : 0.0f;
+                *(f32x4 *)(nrow + (i >> 3) * Q8_NORM_LDS_PITCH + 4 * (i & 7)) = o;
+            }
+        }
+        __syncthreads();
+        // thread tid takes half tid % 2 of blocks tid / 2 + 128 g (the
+        // quantizer's element layout per half-block)
         const int tt = t >> 5;
+        const int h = tid & 1;
 #pragma unroll
         for (int g = 0; g < 2; g++) {
             if (128 * g >= nb) break;  // workgroup-uniform
             const int b = min(128 * g + (tid >> 1), nb - 1);  // clamped: every lane joins the shuffle
+            const float *src = nrow + b * Q8_NORM_LDS_PITCH + 2 * h;
             float e[4][4];
 #pragma unroll
             for (int c = 0; c < 4; c++) {
-                e[0][c] = live ? (qx[g][c][0] * scale) * qw[g][c][0] : 0.0f;  // J[h][0] = 2h
-                e[2][c] = live ? (qx[g][c][1] * scale) * qw[g][c][1] : 0.0f;  // J[h][2] = 2h + 1
-                e[1][c] = live ? (qx[g][c][2] * scale) * qw[g][c][2] : 0.0f;  // J[h][1] = 4 + 2h
-                e[3][c] = live ? (qx[g][c][3] * scale) * qw[g][c][3] : 0.0f;  // J[h][3] = 5 + 2h
+                const float2 lo = *(const float2 *)(src + 8 * c);      // elements 8c + 2h, +1
+                const float2 hi = *(const float2 *)(src + 8 * c + 4);  // elements 8c + 4 + 2h, +1
+                e[0][c] = lo.x;  // J[h][0] = 2h
+                e[2][c] = lo.y;  // J[h][2] = 2h + 1
+                e[1][c] = hi.x;  // J[h][1] = 4 + 2h
+                e[3][c] = hi.y;  // J[h][3] = 5 + 2h
             }
             float peak = half_peak(e);
             peak = fmaxf(peak, __shfl_xor(peak, 1));

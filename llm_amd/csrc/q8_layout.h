@@ -153,6 +153,9 @@ typedef struct {
 
 /* float4s per thread of the 256-thread row RMSNorm (k <= 1024 * this). */
 #define Q8_NORM_ROW_VEC 8
+// floats per block of the normalized row q8_rmsnorm_row stages in LDS for its
+// prepared output (a block's 32 plus a pad against bank conflicts)
+#define Q8_NORM_LDS_PITCH 36
 
 typedef struct {
     const float *x;    /* [n][k] f32 (mode 0) */

@@ -893,7 +893,7 @@ def test_rmsnorm_rows_match_the_reference_bit_for_bit(gpu, rows, k):
     ob.free()
 
 
-@pytest.mark.parametrize("rows,k", [(1, 2304), (2, 64), (33, 2304), (130, 5760), (512, 2304)])
+@pytest.mark.parametrize("rows,k", [(1, 2304), (2, 64), (33, 2304), (130, 5760), (512, 2304), (3, 8192)])
 @pytest.mark.parametrize("f16", [-1, 1])
 def test_norm_prepare_is_quantize_of_rmsnorm(gpu, rows, k, f16):
     """Gpu::rmsnorm_prepare: the quantized bytes and scales are the
