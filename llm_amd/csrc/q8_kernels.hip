@@ -1576,52 +1576,61 @@ static __device__ __forceinline__ void quant_store(const float (&e)[4][4], float
     if (write_scale) xs[u * Q8_TILE_TOKENS + (slot & 31)] = scale;
 }
 
-// One wave per (32-token tile, block) unit: lane L = 32h + t owns half h of
-// token t's block, i.e. AVX2 lanes J[h][0..3] across the four chunks -- as
-// eight float2 loads (elements 8c + {j, j+1}) -- and writes it as one 16-byte
-// store, so the wave's stores are one contiguous 1 KB unit.  The block peak
-// is the max of the two halves' peaks (one v_permlane32_swap).
+// One wave per (32-token tile, block) unit.  The unit's 32 token rows of 32
+// elements are read as whole 128-byte pieces (lane L takes float4 L % 8 of
+// rows L / 8 + 8u, u = 0..3: each load instruction covers eight rows) into a
+// wave-private LDS tile of 36 floats a row; then lane L = 32h + t takes half
+// h of token t's block in the AVX2 lane order J[h][0..3] across the four
+// chunks and writes it as one 16-byte store, so the wave's stores are one
+// contiguous 1 KB unit.  The block peak is the max of the two halves' peaks
+// (one v_permlane32_swap).
 // ---------------------------------------------------------------------------
 extern "C" __global__ __launch_bounds__(256) void q8_quantize(Q8QuantArgs a) {
+    __shared__ __attribute__((aligned(16))) float qtile[4][32 * Q8_NORM_LDS_PITCH];
     const int lane = threadIdx.x & 63;
-    const int unit = blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int unit = blockIdx.x * (blockDim.x >> 6) + wv;
     const int nb = a.nb;
     if (unit >= a.ttiles * nb) return;  // whole waves
     const int tt = unit / nb;
     const int b = unit - tt * nb;
+    float *tile = qtile[wv];
+    {
+        const int f8 = lane & 7;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int row = (lane >> 3) + 8 * u;
+            const int t = tt * Q8_TILE_TOKENS + row;
+            const size_t off = (size_t)min(t, a.n - 1) * nb * 32 + (size_t)b * 32 + 4 * f8;
+            f32x4 v;
+            if (a.mode == 0) {
+                v = *(const f32x4 *)(a.x + off);
+            } else {
+                const f32x4 g = *(const f32x4 *)(a.gate + off);
+                const f32x4 up = *(const f32x4 *)(a.up + off);
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[e] = silu_f32(g[e]) * up[e];
+            }
+            if (t >= a.n) v = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};  // tokens past n quantize as zeros
+            *(f32x4 *)(tile + row * Q8_NORM_LDS_PITCH + 4 * f8) = v;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const int h = lane >> 5;
     const int tl = lane & 31;
-    const int t = tt * Q8_TILE_TOKENS + tl;
-    // v[2i], v[2i+1] = elements 8*(i>>1)... laid out per dword: dword q holds
-    // elements 8c + J[h][q] for c = 0..3; J[h] = {2h, 4+2h, 1+2h, 5+2h}, so the
-    // pairs (2h, 2h+1) and (4+2h, 5+2h) of each chunk c cover all four dwords.
+    // chunk c: elements 8c + 2h, +1 (dwords 0, 2) and 8c + 4 + 2h, +1 (dwords 1, 3)
+    const float *src = tile + tl * Q8_NORM_LDS_PITCH + 2 * h;
     float e[4][4];  // e[q][c]
 #pragma unroll
-    for (int q = 0; q < 4; q++)
-#pragma unroll
-        for (int c = 0; c < 4; c++) e[q][c] = 0.0f;
-    if (t < a.n) {
-        const size_t base = (size_t)t * nb * 32 + (size_t)b * 32 + 2 * h;
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            // chunk c: elements 8c + 2h, 8c + 2h + 1 (dwords 0, 2) and 8c + 4 + 2h, +1 (dwords 1, 3)
-            float2 lo, hi;
-            if (a.mode == 0) {
-                lo = *(const float2 *)(a.x + base + 8 * c);
-                hi = *(const float2 *)(a.x + base + 8 * c + 4);
-            } else {
-                const float2 g0 = *(const float2 *)(a.gate + base + 8 * c);
-                const float2 u0 = *(const float2 *)(a.up + base + 8 * c);
-                const float2 g1 = *(const float2 *)(a.gate + base + 8 * c + 4);
-                const float2 u1 = *(const float2 *)(a.up + base + 8 * c + 4);
-                lo = make_float2(silu_f32(g0.x) * u0.x, silu_f32(g0.y) * u0.y);
-                hi = make_float2(silu_f32(g1.x) * u1.x, silu_f32(g1.y) * u1.y);
-            }
-            e[0][c] = lo.x;  // J[h][0] = 2h
-            e[2][c] = lo.y;  // J[h][2] = 2h + 1
-            e[1][c] = hi.x;  // J[h][1] = 4 + 2h
-            e[3][c] = hi.y;  // J[h][3] = 5 + 2h
-        }
+    for (int c = 0; c < 4; c++) {
+        const float2 lo = *(const float2 *)(src + 8 * c);
+        const float2 hi = *(const float2 *)(src + 8 * c + 4);
+        e[0][c] = lo.x;  // J[h][0] = 2h
+        e[2][c] = lo.y;  // J[h][2] = 2h + 1
+        e[1][c] = hi.x;  // J[h][1] = 4 + 2h
+        e[3][c] = hi.y;  // J[h][3] = 5 + 2h
     }
     float peak = half_peak(e);
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(peak), __float_as_uint(peak), false, false);
@@ -2857,7 +2866,17 @@ extern "C" __global__ __launch_bounds__(256) void q8_rmsnorm_row(Q8NormArgs a) {
     __shared__ double part[4];
     extern __shared__ __attribute__((aligned(16))) float nrow[];  // [nb][Q8_NORM_LDS_PITCH], prepared output only
     const int tid = threadIdx.x;
-    const int t = blockIdx.x;
+    // Prepared output: the eight rows whose 16-byte slots share a 128-byte
+    // line of a unit (tokens 8m .. 8m + 7) go to workgroups 8 apart, which
+    // round-robin dispatch places on one XCD, so each line is written from
+    // one L2; the grid is then a multiple of 64 rows and rows past the
+    // token-tile boundary return.
+    int t = blockIdx.x;
+    if (a.xq) {
+        const int q = t >> 3;
+        t = 8 * (8 * (q >> 3) + (t & 7)) + (q & 7);
+        if (t >= a.rows_launched) return;  // whole workgroup, before any barrier
+    }
     const int k = a.k;
     const int nv = k >> 2;
     const bool live = t < a.n;  // rows from n to the token-tile boundary quantize as zeros

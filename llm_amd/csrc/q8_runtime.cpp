@@ -971,7 +971,7 @@ int run_rmsnorm(q8_ctx *c, const float *x, int rows, int k, const float *w, floa
     // a workgroup per row, the row loaded once (k <= 8192, four floats per
     // thread per step); prepared output: rows to the token-tile boundary
     if (k <= 256 * 4 * Q8_NORM_ROW_VEC)
-        return launch(c, F_RMSNORM_ROW, (unsigned)a.rows_launched, 256,
+        return launch(c, F_RMSNORM_ROW, a.xq ? (unsigned)align_up((size_t)a.rows_launched, 64) : (unsigned)a.rows_launched, 256,
                       a.xq ? (unsigned)((k / 32) * Q8_NORM_LDS_PITCH * sizeof(float)) : 0u, &a, sizeof a);
     return launch(c, F_RMSNORM, (unsigned)ceil_div(a.rows_launched, 4), 256, 0, &a, sizeof a);
 }
