@@ -330,6 +330,12 @@ def bench_layer_n512(gpu, steps, warmup, rng, n=512):
         piece_us[name] = round(statistics.median(rotating_trials(gpu, fn, copies, max(steps // 2, copies), 2)) * 1e3,
                                2)
     piece_tops = {nm: round(ops[nm] / (piece_us[nm] * 1e-6) / 1e12, 1) for nm in ("qkv", "o", "gate_up", "down")}
+    # a piece rotates only its own weights over the copies: where those are
+    # smaller than the Infinity Cache, the piece runs MALL-warm, the layer set not
+    piece_w = {"qkv": ("q", "k", "v"), "o": ("o",), "gate_up": ("gate", "up"), "gate_up_silu": ("gate", "up"),
+               "down": ("down",)}
+    piece_mall = {nm: ("warm" if copies * sum(base[w].data.size for w in ws) < MALL_BYTES else "cold")
+                  for nm, ws in piece_w.items()}
     log("n=512 pieces (us): " + ", ".join(f"{k} {v}" for k, v in piece_us.items()))
     for L in layers:
         for w in L.values():
@@ -338,7 +344,8 @@ def bench_layer_n512(gpu, steps, warmup, rng, n=512):
         b.free()
     return {"us": s["median_us"], "tops": s["value"], "trials_tops": s["trials"], "ops": total_ops,
             "frac": s["value"] / INT8_PEAK_TOPS, "ops_by_projection": ops, "copies": copies,
-            "quantize_us": piece_us["quantize_x"], "projections_us": piece_us, "projections_tops": piece_tops}
+            "quantize_us": piece_us["quantize_x"], "projections_us": piece_us, "projections_tops": piece_tops,
+            "projections_mall": piece_mall}
 
 
 # ---------------------------------------------------------------------------
