@@ -224,7 +224,11 @@ def bench_ceilings(gpu, steps, warmup, read_bytes):
             "read_us": {n: r["median_us"] for n, r in reads.items()},
             "ceiling_gbs": round(reads[best]["value"], 1), "ceiling_kernel": f"q8_probe_read_{best}",
             "empty_kernel_us_per_launch": round(empty_us, 3),
-            "mfma_i8_tops": round(mfma_tops, 1), "valu_ns_per_op_per_simd": round(valu_ns, 3),
+            "mfma_i8_tops": round(mfma_tops, 1),
+            # the nominal 5.03 POPS is 8192 int8 ops per clock per CU at 2.4 GHz:
+            # the clock at which the measured MFMA-only rate is that per-CU rate
+            "mfma_implied_sclk_ghz": round(mfma_tops * 1e12 / (cus * 8192) / 1e9, 3),
+            "valu_ns_per_op_per_simd": round(valu_ns, 3),
             "tile_block_mix_ns_per_simd": round(mix_ns, 2), "tile_block_mix_tops": round(mix_tops, 1),
             "tile_block_mix_f16_ns_per_simd": round(mix16_ns, 2)}
 
@@ -336,6 +340,16 @@ def bench_layer_n512(gpu, steps, warmup, rng, n=512):
                "down": ("down",)}
     piece_mall = {nm: ("warm" if copies * sum(base[w].data.size for w in ws) < MALL_BYTES else "cold")
                   for nm, ws in piece_w.items()}
+    # the compulsory-traffic bound of each projection: weights + Q8_0 X + f32 Y
+    # once each, at 8 TB/s, against its ops at the 5.0 POPS int8 peak
+    dims = {"qkv": (3 * HID, HID), "o": (HID, HID), "gate_up": (2 * FFN, HID), "down": (HID, FFN)}
+    bound = {}
+    for nm, (m_, k_) in dims.items():
+        nbytes = m_ * k_ // 32 * 34 + n * k_ * 9 // 8 + 4 * n * m_
+        t_hbm, t_mfma = nbytes / (HBM_PEAK_GBS * 1e3), ops[nm] / (INT8_PEAK_TOPS * 1e6)
+        bound[nm] = {"bytes": nbytes, "t_hbm_us": round(t_hbm, 2), "t_mfma_us": round(t_mfma, 2),
+                     "max_frac_of_mfma_peak": round(t_mfma / max(t_hbm, t_mfma), 3),
+                     "attained_frac": round(piece_tops[nm] / INT8_PEAK_TOPS, 4)}
     log("n=512 pieces (us): " + ", ".join(f"{k} {v}" for k, v in piece_us.items()))
     for L in layers:
         for w in L.values():
@@ -345,7 +359,7 @@ def bench_layer_n512(gpu, steps, warmup, rng, n=512):
     return {"us": s["median_us"], "tops": s["value"], "trials_tops": s["trials"], "ops": total_ops,
             "frac": s["value"] / INT8_PEAK_TOPS, "ops_by_projection": ops, "copies": copies,
             "quantize_us": piece_us["quantize_x"], "projections_us": piece_us, "projections_tops": piece_tops,
-            "projections_mall": piece_mall}
+            "projections_mall": piece_mall, "projections_traffic_bound": bound}
 
 
 # ---------------------------------------------------------------------------
@@ -681,7 +695,9 @@ def main():
                       "mfma_ceiling_tops": ceil.get("mfma_i8_tops"),
                       "tile_block_ceiling_tops": ceil.get("tile_block_mix_tops"),
                       "quantize_us": gemm.get("quantize_us"), "projections_us": gemm.get("projections_us"),
-                      "projections_tops": gemm.get("projections_tops")},
+                      "projections_tops": gemm.get("projections_tops"),
+                      "projections_mall": gemm.get("projections_mall"),
+                      "projections_traffic_bound": gemm.get("projections_traffic_bound")},
         "ceilings": ceil,
         "extras": extras,
         "decoder_configs4": decoder,
