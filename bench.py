@@ -182,32 +182,52 @@ def bench_gemv(gpu, m, k, steps, warmup, rng):
             "q8x_gbs": round(qs["value"], 1), "q8x_us": qs["median_us"], "q8x_trials_gbs": qs["trials"]}
 
 
-def bench_ceilings(gpu, steps, warmup, read_bytes):
-    """The plain-read ceiling at the GEMV's byte count, an empty kernel, and
-    the MFMA / VALU / tile-block-mix rates."""
-    from llm_amd import q8
-    nbytes = (read_bytes + 15) // 16 * 16
-    copies = copies_for(nbytes)
-    stride = (nbytes + 4095) // 4096 * 4096
+# the read probe's shapes: 16-byte loads per lane, cache policy, threads per
+# workgroup (576 = nine waves, the configs[0] GEMV's row-slice workgroups,
+# whose weight loads are non-temporal)
+READ_SHAPES = [(loads, nt, threads) for threads in (256, 576, 1024) for nt in (False, True) for loads in (2, 4, 8, 16)]
+
+
+def best_read(gpu, pr, nbytes, copies, steps, warmup):
+    """The fastest plain read of nbytes over `copies` rotating copies, over
+    READ_SHAPES: (us, shape name, {shape: us})."""
+    nb = (nbytes + 15) // 16 * 16
+    stride = (nb + 4095) // 4096 * 4096
     buf = gpu.alloc(stride * copies)
-    reads = {}
-    for which, name in ((q8.PROBE_READ_L4, "l4"), (q8.PROBE_READ_L8, "l8"), (q8.PROBE_READ_L16, "l16")):
-        ms = rotating_trials(gpu, lambda i, w=which: gpu.probe(w, buf, nbytes, src_offset=i * stride), copies, steps,
-                             warmup)
-        reads[name] = summary(ms, read_bytes, 1e-9)
-    best = max(reads, key=lambda n: reads[n]["value"])
-    log("plain read of " + f"{read_bytes} B, MALL-cold: " +
-        ", ".join(f"{n} {r['median_us']:.2f} us ({r['value']:.0f} GB/s)" for n, r in reads.items()))
+    table = {}
+    for loads, nt, threads in READ_SHAPES:
+        name = f"l{loads}{'_nt' if nt else ''}_t{threads}"
+        ms = rotating_trials(gpu, lambda i, l=loads, n=nt, t=threads: pr.read(buf, nb, l, n, t, src_offset=i * stride),
+                             copies, steps, warmup)
+        table[name] = statistics.median(ms) * 1e3
     buf.free()
-    empty = rotating_trials(gpu, lambda i: gpu.probe(q8.PROBE_EMPTY), 1, 200, 20)
+    best = min(table, key=table.get)
+    return table[best], best, table
+
+
+def bench_ceilings(gpu, steps, warmup, read_bytes):
+    """The plain-read ceiling at the GEMV's byte count (best of the read
+    shapes, the GEMV's own non-temporal nine-wave shape among them), an empty
+    kernel, the MFMA / VALU / tile-block-mix rates, and the co-resident split
+    probes: an int8-MFMA role and a VALU role on the same SIMDs, timed alone
+    and together (together = the larger of the two if their pipes overlap,
+    the sum if they share one)."""
+    from llm_amd import probes
+    pr = probes.Probes(gpu)
+    copies = copies_for(read_bytes)
+    best_us, best_name, table = best_read(gpu, pr, read_bytes, copies, steps, warmup)
+    log(f"plain read of {read_bytes} B, MALL-cold: best {best_name} {best_us:.2f} us "
+        f"({read_bytes / (best_us * 1e-6) / 1e9:.0f} GB/s); " +
+        ", ".join(f"{n} {u:.2f}" for n, u in sorted(table.items(), key=lambda kv: kv[1])[:6]))
+    empty = rotating_trials(gpu, lambda i: pr.probe(probes.EMPTY), 1, 200, 20)
     empty_us = statistics.median(empty) * 1e3
     cus = gpu.info()["cu_count"]
     wgs = 4 * cus  # four 4-wave workgroups a CU: four waves a SIMD
     rates = {}
-    for which, name, per_iter in ((q8.PROBE_MFMA, "mfma", 4), (q8.PROBE_VALU, "valu", 1), (q8.PROBE_MIX, "mix", 2),
-                                  (q8.PROBE_MIX_F16, "mix_f16", 2)):
-        iters = 2048 if which != q8.PROBE_VALU else 8192
-        ms = rotating_trials(gpu, lambda i, w=which, it=iters: gpu.probe(w, iters=it, workgroups=wgs), 1, 3, 1)
+    for which, name, per_iter in ((probes.MFMA, "mfma", 4), (probes.VALU, "valu", 1), (probes.MIX, "mix", 2),
+                                  (probes.MIX_F16, "mix_f16", 2)):
+        iters = 2048 if which != probes.VALU else 8192
+        ms = rotating_trials(gpu, lambda i, w=which, it=iters: pr.probe(w, iters=it, workgroups=wgs), 1, 3, 1)
         t = statistics.median(ms) * 1e-3
         units = wgs * 4 * iters * per_iter  # per wave: MFMAs (mfma), 32-VALU groups (valu), tile-blocks (mix)
         rates[name] = {"units_per_s": units / t, "seconds": t}
@@ -217,12 +237,28 @@ def bench_ceilings(gpu, steps, warmup, read_bytes):
     mix_ns = simds / rates["mix"]["units_per_s"] * 1e9            # ns per tile-block per SIMD
     mix_tops = rates["mix"]["units_per_s"] * 65536 / 1e12
     mix16_ns = simds / rates["mix_f16"]["units_per_s"] * 1e9
+    # co-resident roles: 2 eight-wave workgroups a CU = one wave of each role on every SIMD, twice
+    split = {}
+    for which, name in ((probes.SPLIT_I8_VALU, "i8_mfma|cvt+fma"), (probes.SPLIT_I8_FMA, "i8_mfma|fma"),
+                        (probes.SPLIT_F32_VALU, "f32_outer_mfma|cvt+fma")):
+        t = {}
+        for mask, part in ((1, "a"), (2, "b"), (3, "both")):
+            ms = rotating_trials(gpu, lambda i, w=which, m=mask: pr.probe(w, iters=4096, workgroups=2 * cus, mask=m),
+                                 1, 3, 1)
+            t[part] = statistics.median(ms) * 1e3
+        lo, hi = min(t["a"], t["b"]), max(t["a"], t["b"])
+        split[name] = {"a_us": round(t["a"], 1), "b_us": round(t["b"], 1), "both_us": round(t["both"], 1),
+                       "both_over_sum": round(t["both"] / (t["a"] + t["b"]), 3),
+                       "overlapped_frac_of_shorter": round((t["a"] + t["b"] - t["both"]) / lo, 3),
+                       "both_over_max": round(t["both"] / hi, 3)}
+    pr.close()
     log(f"empty kernel {empty_us:.2f} us/launch; int8 MFMA only {mfma_tops:.0f} TOPS; VALU {valu_ns:.2f} ns/op/SIMD; "
-        f"GEMM tile-block mix {mix_ns:.1f} ns/SIMD = {mix_tops:.0f} TOPS (f16-MFMA family's mix {mix16_ns:.1f} ns)")
+        f"GEMM tile-block mix {mix_ns:.1f} ns/SIMD = {mix_tops:.0f} TOPS (f16-MFMA family's mix {mix16_ns:.1f} ns); "
+        "co-resident split (both / sum): " + ", ".join(f"{k} {v['both_over_sum']}" for k, v in split.items()))
     return {"read_bytes": read_bytes, "read_copies": copies,
-            "read_gbs": {n: round(r["value"], 1) for n, r in reads.items()},
-            "read_us": {n: r["median_us"] for n, r in reads.items()},
-            "ceiling_gbs": round(reads[best]["value"], 1), "ceiling_kernel": f"q8_probe_read_{best}",
+            "read_us_by_shape": {n: round(u, 3) for n, u in table.items()},
+            "ceiling_gbs": round(read_bytes / (best_us * 1e-6) / 1e9, 1), "ceiling_us": round(best_us, 3),
+            "ceiling_kernel": f"q8_probe_read ({best_name})",
             "empty_kernel_us_per_launch": round(empty_us, 3),
             "mfma_i8_tops": round(mfma_tops, 1),
             # the nominal 5.03 POPS is 8192 int8 ops per clock per CU at 2.4 GHz:
@@ -230,33 +266,28 @@ def bench_ceilings(gpu, steps, warmup, read_bytes):
             "mfma_implied_sclk_ghz": round(mfma_tops * 1e12 / (cus * 8192) / 1e9, 3),
             "valu_ns_per_op_per_simd": round(valu_ns, 3),
             "tile_block_mix_ns_per_simd": round(mix_ns, 2), "tile_block_mix_tops": round(mix_tops, 1),
-            "tile_block_mix_f16_ns_per_simd": round(mix16_ns, 2)}
+            "tile_block_mix_f16_ns_per_simd": round(mix16_ns, 2),
+            "coresident_split": split}
 
 
 def bench_launch_reads(gpu, steps, warmup):
     """The plain-read ceiling at the byte counts of the decode step's
     launches (weights only): what one launch of that size can read on this
-    box.  Its own section: a rocprofv3 kernel trace of it died on the host
-    inside hipGraphLaunch, so traced runs leave it out."""
-    from llm_amd import q8
+    box, best of the read shapes.  Its own section: a rocprofv3 kernel trace
+    of it died on the host inside hipGraphLaunch, so traced runs leave it out."""
+    from llm_amd import probes
+    pr = probes.Probes(gpu)
     decode_reads = {}
     for name, nb in (("o", HID * HID // 32 * 34), ("qkv", 3 * HID * HID // 32 * 34),
                      ("down", FFN * HID // 32 * 34), ("gate_up", 2 * FFN * HID // 32 * 34),
                      ("lm_head", VOCAB * HID // 32 * 34)):
-        nbr = (nb + 15) // 16 * 16
-        cp = copies_for(nbr)
-        st = (nbr + 4095) // 4096 * 4096
-        rb = gpu.alloc(st * cp)
-        best_us = None
-        for which in (q8.PROBE_READ_L4, q8.PROBE_READ_L8, q8.PROBE_READ_L16):
-            ms = rotating_trials(gpu, lambda i, w=which: gpu.probe(w, rb, nbr, src_offset=i * st), cp,
-                                 max(cp, min(steps, 100)), min(warmup, 10))
-            us = statistics.median(ms) * 1e3
-            best_us = us if best_us is None else min(best_us, us)
-        rb.free()
-        decode_reads[name] = {"bytes": nb, "us": round(best_us, 3), "gbs": round(nb / (best_us * 1e-6) / 1e9, 1)}
+        cp = copies_for(nb)
+        us, shape, _ = best_read(gpu, pr, nb, cp, max(cp, min(steps, 100)), min(warmup, 10))
+        decode_reads[name] = {"bytes": nb, "us": round(us, 3), "gbs": round(nb / (us * 1e-6) / 1e9, 1),
+                              "shape": shape}
+    pr.close()
     log("plain reads at the decode launches' sizes, MALL-cold: " +
-        ", ".join(f"{n} {v['bytes'] / 1e6:.1f} MB {v['us']:.2f} us" for n, v in decode_reads.items()))
+        ", ".join(f"{n} {v['bytes'] / 1e6:.1f} MB {v['us']:.2f} us ({v['shape']})" for n, v in decode_reads.items()))
     return decode_reads
 
 
@@ -467,10 +498,17 @@ def bench_decoder(gpu, rng, prompt=512, steps=128, reps=5):
     resets the context, prefills `prompt` random ids (pp) and decodes `steps`
     greedy tokens (tg); tok/s mean and sample std over `reps` repeats, after
     one eager pass and one capture pass.  Host wall clock around calls that
-    end in a wait."""
+    end in a wait.
+
+    The model has an output head of its own (a GGUF with output.weight,
+    model.rs:519-524: the same 122880 x 2304 Q8_0 bytes per token as the tied
+    head) and embedding rows at scale std 4: with the head tied to a 0.02
+    embedding the last hidden state barely depends on the current token and
+    greedy decode repeats one token, so the fed-back token path would run on
+    one value; here the tokens vary (distinct_tokens)."""
     from llm_amd import decoder as dm
     cfg = dm.config(n_layer=42, n_embd=HID, n_ff=FFN, n_head=36, n_head_kv=36, head_dim=64, n_vocab=VOCAB,
-                    capacity=4096, max_batch=prompt)
+                    capacity=4096, max_batch=prompt, untied_output=1, embd_std=4.0)
     t0 = time.perf_counter()
     dec = dm.Decoder(gpu, cfg, seed=0x5EED)
     log(f"decoder: 42 layers generated on the device in {time.perf_counter() - t0:.1f} s")

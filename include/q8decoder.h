@@ -159,16 +159,20 @@ int q8_weight_synthetic(q8_ctx *ctx, int k, int out, uint64_t seed, float scale_
 typedef struct q8_decoder q8_decoder;
 
 /* Geometry of a dense llama-style decoder (Config, model.rs:20-180): separate
- * q, k, v projections, SiLU-gated feed-forward, RMSNorm before each block,
- * token embedding tied to the output projection (model.rs:519-524). */
+ * q, k, v projections, SiLU-gated feed-forward, RMSNorm before each block.
+ * The output projection is the token embedding (a file without
+ * `output.weight`) or a matrix of its own (a file with one): the two cases
+ * model.rs:519-524 loads. */
 typedef struct {
     int n_layer, n_embd, n_ff, n_head, n_head_kv, head_dim, n_rot, n_vocab;
     int capacity;   /* KV cache positions */
     int max_batch;  /* most tokens one forward takes (<= Q8_MAX_TOKENS) */
     float eps, rope_base;
+    int untied_output; /* 0: the embedding is the output head; 1: a random output.weight of its own */
+    float embd_std;    /* scale std of the random embedding rows (0: 0.02, as every other matrix) */
 } q8_decoder_config;
 
-enum { Q8_DEC_Q = 0, Q8_DEC_K, Q8_DEC_V, Q8_DEC_O, Q8_DEC_GATE, Q8_DEC_UP, Q8_DEC_DOWN };
+enum { Q8_DEC_Q = 0, Q8_DEC_K, Q8_DEC_V, Q8_DEC_O, Q8_DEC_GATE, Q8_DEC_UP, Q8_DEC_DOWN, Q8_DEC_OUTPUT };
 
 /* Random-init weights on the device (q8_weight_synthetic, one seed per
  * matrix), norm weights near 1, an f16 KV cache of `capacity` positions.
@@ -199,8 +203,9 @@ int q8_decoder_generate(q8_decoder *dec, int steps, uint32_t *out);
 
 /* The logits of the last forward or step (n_vocab f32, waits). */
 int q8_decoder_logits(q8_decoder *dec, float *host, size_t len);
-/* Weights for the CPU checks: layer < 0 is the tied embedding / output
- * matrix; `which` is Q8_DEC_*.  Norms: which 0 attention, 1 feed-forward;
+/* Weights for the CPU checks: layer < 0 is the token embedding, or with
+ * which = Q8_DEC_OUTPUT the output head (the embedding when tied); `which`
+ * is Q8_DEC_*.  Norms: which 0 attention, 1 feed-forward;
  * layer < 0 the output norm (host pointer of n_embd floats). */
 int q8_decoder_weight(const q8_decoder *dec, int layer, int which, const q8_weight **weight);
 int q8_decoder_norm(const q8_decoder *dec, int layer, int which, const float **weight);

@@ -28,9 +28,14 @@
  *
  * Numerics (the reference CPU kernels are the oracle, apps/engine/src/quant.rs):
  *  - n == 1: f32 activations, no quantization (tensor.rs:96-101).  Each block
- *    is evaluated in the AVX2 order of dot_q8_0 (quant.rs:54-78); with option
- *    "gemv.exact" = 1 (the default) the cross-block sum is also left-to-right,
- *    so y is bit-identical to the reference's AVX2 path.
+ *    value is the reference's AVX2 order of dot_q8_0 (quant.rs:54-78), bit
+ *    for bit.  By default the block values of a row are then summed in a
+ *    fixed tree (per lane, the two halves, then the waves): deterministic and
+ *    within 2e-6 + 1e-5 |ref| of the reference, not bit-identical to it.
+ *    With option "gemv.exact" = 1 the cross-block sum is the reference's
+ *    left-to-right sum, so y is bit-identical to its AVX2 path (pinned by the
+ *    exact-mode tests in tests/test_gpu_q8.py; about 0.4 us slower at
+ *    configs[0]).
  *  - n >= 2: activations are quantized to Q8_0 exactly as quantize_q8_0 does
  *    (round half away from zero, saturating), then int8 x int8 per 32-block
  *    on v_mfma_i32_32x32x32_i8 (exact int32), f32 scale d_w*s_x per block.
@@ -247,8 +252,11 @@ int q8_matmul_q8(q8_ctx *ctx, const q8_weight *weight, q8_dptr x, size_t x_offse
  * scratch (Q8_ERR_UNSUPPORTED if its K would be split).  Results equal
  * q8_matmul's within the n >= 2 parity bar (bit-identical where q8_matmul
  * does not split K).  Every call on one GPU shares that GPU's array, which
- * keeps the last call's bytes (each call rewrites all it reads); calls that
- * overlap on one GPU (several streams or processes) race on it. */
+ * keeps the last call's bytes (each call rewrites all it reads).  Within one
+ * process the first context that uses a GPU's array holds it until q8_close,
+ * and a call from any other context on that GPU is Q8_ERR_UNSUPPORTED, so two
+ * contexts' streams never share it; calls of the holding context are ordered
+ * on its stream.  Several processes on one GPU each have their own copy. */
 int q8_matmul_noalloc(q8_ctx *ctx, const q8_weight *weight, q8_dptr x, size_t x_offset, int n, q8_dptr y,
                       size_t y_offset, q8_dptr bias, size_t bias_offset);
 
@@ -349,33 +357,34 @@ int q8_argmax(q8_ctx *ctx, q8_dptr values, size_t offset, size_t len, uint32_t *
 int q8_embeddings(q8_ctx *ctx, const q8_weight *weight, const uint32_t *tokens, size_t n, q8_dptr out,
                   size_t out_offset);
 
-/* ---- measurement kernels (no counterpart in the reference) ----
- * The ceilings the benchmark quotes the hot-path kernels against, run on the
- * context's stream like any launch (time them with events or graphs):
- *   Q8_PROBE_READ_L{4,8,16}  a plain streaming read of `bytes` at `src`
- *                            (16-byte aligned, a multiple of 16), L 16-byte
- *                            loads per lane, one pass;
- *   Q8_PROBE_EMPTY           a one-wave kernel that does nothing;
- *   Q8_PROBE_MFMA            `iters` x 4 v_mfma_i32_32x32x32_i8 per wave;
- *   Q8_PROBE_VALU            `iters` x 32 VALU (16 cvt + 16 fma) per wave;
- *   Q8_PROBE_MIX             `iters` GEMM tile-blocks per wave with operands
- *                            in registers: an int8 MFMA, half an f32
- *                            outer-product MFMA and 32 VALU each;
- *   Q8_PROBE_MIX_F16         the same for the f16-MFMA family: two
- *                            v_mfma_f32_32x32x16_f16, half an outer-product
- *                            MFMA and 16 fma per tile-block;
- * the last four over `workgroups` workgroups of four waves (iters even). */
-enum {
-    Q8_PROBE_READ_L4 = 0,
-    Q8_PROBE_READ_L8 = 1,
-    Q8_PROBE_READ_L16 = 2,
-    Q8_PROBE_EMPTY = 3,
-    Q8_PROBE_MFMA = 4,
-    Q8_PROBE_VALU = 5,
-    Q8_PROBE_MIX = 6,
-    Q8_PROBE_MIX_F16 = 7
-};
-int q8_probe(q8_ctx *ctx, int which, q8_dptr src, size_t bytes, int iters, int workgroups);
+/* ---- kernel inspection and launch validation ----
+ * The reference inspects each kernel at load -- registers, shared memory,
+ * occupancy -- and refuses launch shapes the kernel cannot take
+ * (cuda/mod.rs:229-283); debug builds also check a launch's argument count
+ * against the kernel (cuda/mod.rs:1835-1848).  Here every kernel's metadata
+ * comes from the code object's AMDGPU note at build time, and every launch
+ * the library makes passes q8_launch_check's rules before it is enqueued. */
+typedef struct {
+    uint32_t args_bytes;     /* explicit kernel arguments (one struct by value) */
+    uint32_t kernarg_bytes;  /* the whole kernarg segment, hidden arguments included */
+    uint32_t vgprs;          /* architected VGPRs per lane */
+    uint32_t agprs;          /* accumulation VGPRs per lane */
+    uint32_t sgprs;
+    uint32_t static_lds;     /* bytes of LDS the kernel declares statically */
+    uint32_t max_workgroup;  /* largest workgroup the kernel was compiled for (threads) */
+    uint32_t private_bytes;  /* scratch (spills) per lane */
+} q8_kernel_info_t;
+
+/* The metadata of kernel `name` of this build; Q8_ERR_INVALID for a name the
+ * code object does not hold. */
+int q8_kernel_info(const char *name, q8_kernel_info_t *info);
+/* Q8_OK when a launch of `name` with an argument block of args_bytes, `block`
+ * threads per workgroup and dynamic_lds bytes of dynamic LDS fits the kernel
+ * and a device of lds_limit bytes of LDS per workgroup: the block equals the
+ * kernel's explicit arguments, the workgroup is a whole number of 64-lane
+ * waves within the kernel's bound (else Q8_ERR_INVALID), static + dynamic
+ * LDS <= lds_limit (else Q8_ERR_UNSUPPORTED).  Host-only: needs no device. */
+int q8_launch_check(const char *name, size_t args_bytes, unsigned block, size_t dynamic_lds, size_t lds_limit);
 
 /* ---- tactics: the shape-keyed plan (tactics.rs:229-347, for gfx950) ---- */
 

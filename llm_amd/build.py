@@ -33,9 +33,13 @@ LIB = os.path.join(HERE, "libq8mi.so")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
-KERNEL_SOURCES = ["q8_kernels.hip", "q8_attn.hip", "q8_probe.hip", "q8_layout.h"]
+KERNEL_SOURCES = ["q8_kernels.hip", "q8_attn.hip", "q8_layout.h"]
 HOST_SOURCES = ["q8_runtime.cpp", "q8_tactics.cpp", "q8_gguf.cpp", "q8_decoder.cpp", "q8_tactics.h", "q8_layout.h",
-                "q8_internal.h", "q8_noalloc.hip"]
+                "q8_internal.h", "q8_noalloc.hip", "q8_noalloc_owner.h"]
+# The measurement kernels live in a library of their own (libq8bench.so,
+# include/q8bench.h): the benchmark's ceilings, not part of the product ABI.
+BENCH_LIB = os.path.join(HERE, "libq8bench.so")
+BENCH_SOURCES = ["q8_probe.hip", "q8_bench_args.h", "q8_bench.cpp"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -70,6 +74,59 @@ def _kernel_symbols(code_object: str) -> list[str]:
     return names
 
 
+def _kernel_meta(code_object: str) -> list[dict]:
+    """Each kernel's launch-relevant metadata from the code object's AMDGPU
+    metadata note (our own build): bytes of explicit arguments (the extent of
+    the non-hidden .args), the whole kernarg segment, VGPRs, AGPRs, SGPRs,
+    static LDS, the largest workgroup the kernel was compiled for and its
+    private (spill) bytes per lane.  The runtime checks every launch against
+    it, as the reference inspects its kernels at load (cuda/mod.rs:229-283)."""
+    import yaml
+    readelf = os.path.join(ROCM, "llvm", "bin", "llvm-readelf")
+    out = _run([readelf, "--notes", code_object])
+    start = out.index("---")
+    end = out.find("\n...", start)
+    doc = yaml.safe_load(out[start:end if end >= 0 else len(out)])
+    meta = []
+    for k in doc["amdhsa.kernels"]:
+        explicit = [a for a in k.get(".args", []) if not a[".value_kind"].startswith("hidden_")]
+        meta.append({
+            "name": k[".name"],
+            "args": max((a[".offset"] + a[".size"] for a in explicit), default=0),
+            "kernarg": k[".kernarg_segment_size"],
+            "vgpr": k[".vgpr_count"],
+            "agpr": k.get(".agpr_count", 0),
+            "sgpr": k[".sgpr_count"],
+            "lds": k[".group_segment_fixed_size"],
+            "max_wg": k[".max_flat_workgroup_size"],
+            "private": k[".private_segment_fixed_size"],
+        })
+    return sorted(meta, key=lambda m: m["name"])
+
+
+def _meta_table(meta: list[dict], macro: str) -> str:
+    """The metadata as a C initializer list (q8i::KernelMeta, q8_internal.h)."""
+    rows = ",\\\n    ".join(
+        f'{{"{m["name"]}", {m["args"]}u, {m["kernarg"]}u, {m["vgpr"]}u, {m["agpr"]}u, {m["sgpr"]}u, {m["lds"]}u, '
+        f'{m["max_wg"]}u, {m["private"]}u}}' for m in meta)
+    return f"#define {macro} \\\n    {rows}\n#define {macro}_COUNT {len(meta)}\n"
+
+
+def _embed(asm_path: str, symbol: str, blob: str):
+    """An assembly file that carries `blob` (a code object) as `symbol`."""
+    with open(asm_path, "w") as f:
+        f.write(
+            "    .section .rodata\n"
+            "    .p2align 12\n"
+            f"    .globl {symbol}\n"
+            f"{symbol}:\n"
+            f"    .incbin \"{blob}\"\n"
+            f"    .globl {symbol}_end\n"
+            f"{symbol}_end:\n"
+            "    .byte 0\n"
+            "    .section .note.GNU-stack,\"\",@progbits\n")
+
+
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     hipcc = os.path.join(ROCM, "bin", "hipcc")
@@ -93,17 +150,8 @@ def build(verbose: bool = False) -> str:
     with open(os.path.join(BUILD, "q8_manifest.h"), "w") as f:
         f.write("/* generated by llm_amd/build.py */\n")
         f.write("#define Q8_BUILD_INFO " + json.dumps(manifest) + "\n")
-    with open(os.path.join(BUILD, "q8_blob.S"), "w") as f:
-        f.write(
-            "    .section .rodata\n"
-            "    .p2align 12\n"
-            "    .globl q8_code_object\n"
-            "q8_code_object:\n"
-            f"    .incbin \"{hsaco}\"\n"
-            "    .globl q8_code_object_end\n"
-            "q8_code_object_end:\n"
-            "    .byte 0\n"
-            "    .section .note.GNU-stack,\"\",@progbits\n")
+        f.write(_meta_table(_kernel_meta(hsaco), "Q8_KERNEL_META"))
+    _embed(os.path.join(BUILD, "q8_blob.S"), "q8_code_object", hsaco)
 
     # the static device scratch of q8_matmul_noalloc: host + device code in
     # the library's own fat binary (registered when the library loads)
@@ -124,9 +172,37 @@ def build(verbose: bool = False) -> str:
         "-o", tmp,
     ])
     os.replace(tmp, LIB)
+    build_bench(hipcc)
     if verbose:
-        print(f"built {LIB} ({len(info['kernels'])} kernels, code object {info['code_object_sha256'][:12]})")
+        print(f"built {LIB} ({len(info['kernels'])} kernels, code object {info['code_object_sha256'][:12]}) "
+              f"and {BENCH_LIB}")
     return LIB
+
+
+def build_bench(hipcc: str) -> str:
+    """libq8bench.so: the measurement kernels (q8_probe.hip) as a code object
+    of their own, embedded like the product's, and their host launcher
+    (q8_bench.cpp, include/q8bench.h)."""
+    hsaco = os.path.join(BUILD, "q8_probe.hsaco")
+    _run([hipcc, *HIPCC_FLAGS, "--genco", "--no-gpu-bundle-output", "-I", CSRC, "-o", hsaco,
+          os.path.join(CSRC, "q8_probe.hip")])
+    info = {"arch": ARCH, "code_object_sha256": _sha256(hsaco), "kernels": _kernel_symbols(hsaco),
+            "source_sha256": hashlib.sha256(
+                b"".join(open(os.path.join(CSRC, s), "rb").read() for s in BENCH_SOURCES)).hexdigest()}
+    with open(os.path.join(BUILD, "q8_bench_manifest.h"), "w") as f:
+        f.write("/* generated by llm_amd/build.py */\n")
+        f.write("#define Q8_BENCH_BUILD_INFO " + json.dumps(json.dumps(info, sort_keys=True)) + "\n")
+    _embed(os.path.join(BUILD, "q8_bench_blob.S"), "q8_bench_code_object", hsaco)
+    tmp = BENCH_LIB + ".tmp"
+    _run([
+        "g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wextra", "-Wno-unused-parameter",
+        "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROCM, "include"), "-I", CSRC, "-I", BUILD, "-I", INCLUDE,
+        os.path.join(CSRC, "q8_bench.cpp"), os.path.join(BUILD, "q8_bench_blob.S"),
+        "-L", os.path.join(ROCM, "lib"), "-lamdhip64", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}",
+        "-o", tmp,
+    ])
+    os.replace(tmp, BENCH_LIB)
+    return BENCH_LIB
 
 
 if __name__ == "__main__":

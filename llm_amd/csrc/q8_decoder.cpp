@@ -72,6 +72,7 @@ struct q8_decoder {
     q8_decoder_config cfg{};
     std::vector<Layer> layers;
     const q8_weight *embd = nullptr;
+    const q8_weight *output = nullptr;  // the output head: embd when tied
     std::vector<float> output_norm;
     q8_dptr x = 0, q = 0, act = 0, logits = 0;
     q8_dptr pos = 0, tokens = 0;
@@ -134,12 +135,14 @@ int check_config(const q8_decoder_config &g) {
     if (g.n_layer < 1 || g.n_embd < 32 || g.n_embd % 32 || g.n_ff < 32 || g.n_ff % 32 || g.n_head < 1 ||
         g.n_head_kv < 1 || g.n_head % g.n_head_kv || g.head_dim != Q8_ATTN_HEAD_DIM ||
         g.n_head * g.head_dim != g.n_embd || g.n_rot < 0 || g.n_rot > g.head_dim || g.n_rot % 2 || g.n_vocab < 1 ||
-        g.capacity < 1 || g.max_batch < 1 || g.max_batch > Q8_MAX_TOKENS || !(g.eps > 0.0f))
+        g.capacity < 1 || g.max_batch < 1 || g.max_batch > Q8_MAX_TOKENS || !(g.eps > 0.0f) ||
+        (g.untied_output != 0 && g.untied_output != 1) || !(g.embd_std >= 0.0f) || g.embd_std > 1e3f)
         return set_error(Q8_ERR_INVALID,
                          "decoder config: layers %d, embd %d, ff %d, heads %d/%d x %d, rot %d, vocab %d, capacity %d, "
-                         "batch %d (head_dim must be 64, heads x head_dim = embd, dims multiples of 32)",
+                         "batch %d, untied %d, embd_std %g (head_dim must be 64, heads x head_dim = embd, dims "
+                         "multiples of 32, untied 0 or 1, 0 <= embd_std <= 1000)",
                          g.n_layer, g.n_embd, g.n_ff, g.n_head, g.n_head_kv, g.head_dim, g.n_rot, g.n_vocab, g.capacity,
-                         g.max_batch);
+                         g.max_batch, g.untied_output, (double)g.embd_std);
     return Q8_OK;
 }
 
@@ -186,7 +189,7 @@ int q8_decoder::body(int n, int splits) {
         }
     }
     // output norm of the last row, lm_head, greedy choice into the token slot
-    DEC_TRY(q8_norm_lm_head_argmax(c, output_norm.data(), g.eps, embd, x, (size_t)(n - 1) * E, logits, 0, tokens));
+    DEC_TRY(q8_norm_lm_head_argmax(c, output_norm.data(), g.eps, output, x, (size_t)(n - 1) * E, logits, 0, tokens));
     return q8_advance_position(c, pos, n);
 }
 
@@ -266,8 +269,13 @@ int q8_decoder_create_synthetic(q8_ctx *c, const q8_decoder_config *config, uint
         q8_decoder_destroy(d);
         return rc;
     };
-    int rc = q8_weight_synthetic(c, E, g.n_vocab, mix(seed), std_w, &d->embd);
+    int rc = q8_weight_synthetic(c, E, g.n_vocab, mix(seed), g.embd_std > 0.0f ? g.embd_std : std_w, &d->embd);
     if (rc) return fail(rc);
+    d->output = d->embd;
+    if (g.untied_output) {
+        rc = q8_weight_synthetic(c, E, g.n_vocab, mix(seed ^ 0x6f75747075742e77ull), std_w, &d->output);
+        if (rc) return fail(rc);
+    }
     d->output_norm = norm_weights(mix(seed ^ 0x6f75747075746e6full), E);
     d->layers.resize(g.n_layer);
     for (int l = 0; l < g.n_layer; l++) {
@@ -301,6 +309,7 @@ void q8_decoder_destroy(q8_decoder *d) {
     for (Layer &L : d->layers)
         for (const q8_weight *w : L.w)
             if (w) q8_weight_release(d->c, w);
+    if (d->output && d->output != d->embd) q8_weight_release(d->c, d->output);
     if (d->embd) q8_weight_release(d->c, d->embd);
     // the norm vectors' device copies are cached by host address: drop them
     // before the host vectors are freed and their addresses reused
@@ -380,7 +389,7 @@ int q8_decoder_logits(q8_decoder *d, float *host, size_t len) {
 int q8_decoder_weight(const q8_decoder *d, int layer, int which, const q8_weight **weight) {
     if (!d || !weight) return set_error(Q8_ERR_INVALID, "q8_decoder_weight: bad arguments");
     if (layer < 0) {
-        *weight = d->embd;
+        *weight = which == Q8_DEC_OUTPUT ? d->output : d->embd;
         return Q8_OK;
     }
     if (layer >= (int)d->layers.size() || which < 0 || which > Q8_DEC_DOWN)

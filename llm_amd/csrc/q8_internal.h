@@ -6,6 +6,14 @@
 struct q8_ctx;
 
 namespace q8i {
+// One kernel's metadata as the code object's AMDGPU note records it
+// (llm_amd/build.py writes the table into q8_manifest.h): the bytes of its
+// explicit arguments, the whole kernarg segment, VGPRs, AGPRs, SGPRs, static
+// LDS, the largest workgroup it was compiled for and its private bytes per lane.
+struct KernelMeta {
+    const char *name;
+    unsigned args, kernarg, vgpr, agpr, sgpr, lds, max_wg, priv;
+};
 // Record `fmt` as the calling thread's q8_last_error() message; returns code.
 __attribute__((visibility("hidden"), format(printf, 2, 3))) int set_error(int code, const char *fmt, ...);
 // Changes whenever the context reallocates a workspace; a graph captured
@@ -17,6 +25,11 @@ __attribute__((visibility("hidden"))) int attention_split_rows();
 // The device address of q8_matmul_noalloc's static scratch on `device`, which
 // must be the current device (q8_noalloc.hip); status code.
 __attribute__((visibility("hidden"))) int noalloc_scratch(int device, void **out);
+// Whether context `ctx` holds `device`'s no-allocation scratch: the first
+// context to ask takes it and keeps it until noalloc_release (q8_close);
+// another context on the same device is refused (q8_noalloc_owner.h).
+__attribute__((visibility("hidden"))) bool noalloc_claim(int device, const q8_ctx *ctx);
+__attribute__((visibility("hidden"))) void noalloc_release(const q8_ctx *ctx);
 }  // namespace q8i
 
 #endif

@@ -834,7 +834,9 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
             }
         }
     } else {
-        const float out = mbias ? sums[0] + mbias[row] : sums[0];
+        // the residual is read for live rows only: padding rows of the last
+        // tile lie past the end of a bias of mrows floats
+        const float out = (mbias && row < mrows) ? sums[0] + mbias[row] : sums[0];
         if (row < mrows) my[row] = out;
         if (a.amax_value) {
             // this tile's greedy-argmax candidate: the best (value, lowest
@@ -2970,4 +2972,3 @@ extern "C" __global__ __launch_bounds__(256) void q8_silu_mul(Q8EltArgs a) {
 }
 
 #include "q8_attn.hip"
-#include "q8_probe.hip"

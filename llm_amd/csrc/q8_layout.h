@@ -308,15 +308,5 @@ typedef struct {
     int advance;
 } Q8AdvanceArgs;
 
-/* Measurement kernels (q8_probe.hip): the ceilings the benchmark reports its
- * kernels against.  `sink` is written only if a result equals `never`, which
- * the host makes impossible, so nothing is stored but nothing is dead code. */
-typedef struct {
-    const uint8_t *src;     /* read_*: bytes to stream, 16-byte aligned */
-    long long bytes;        /* a multiple of 16 */
-    int iters;              /* mfma/valu/mix: loop trips per wave */
-    unsigned never;
-    unsigned *sink;
-} Q8ProbeArgs;
 
 #endif

@@ -14,13 +14,15 @@
 
 #include "../../include/q8mi.h"
 #include "q8_internal.h"
+#include "q8_noalloc_owner.h"
 
 static __device__ __align__(256) unsigned char scratch[Q8_NOALLOC_SCRATCH_BYTES];
 
 namespace {
-constexpr int kMaxDevices = 64;
+constexpr int kMaxDevices = q8i::NoallocOwners::kMaxDevices;
 std::mutex g_mu;
 void *g_ptr[kMaxDevices] = {};
+q8i::NoallocOwners g_owners;
 }  // namespace
 
 namespace q8i {
@@ -42,5 +44,9 @@ int noalloc_scratch(int device, void **out) {
     *out = g_ptr[device];
     return Q8_OK;
 }
+
+bool noalloc_claim(int device, const q8_ctx *ctx) { return g_owners.claim(device, ctx); }
+
+void noalloc_release(const q8_ctx *ctx) { g_owners.release(ctx); }
 
 }  // namespace q8i

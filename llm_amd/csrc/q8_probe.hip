@@ -1,13 +1,13 @@
-// q8_probe.hip -- measurement kernels: the ceilings the benchmark quotes its
-// hot-path kernels against (no counterpart in the reference; included at the
-// end of q8_kernels.hip, so they share its code object and build flags).
+// q8_probe.hip -- the benchmark's measurement kernels (libq8bench.so,
+// include/q8bench.h): the ceilings the benchmark quotes the hot-path kernels
+// against.  No counterpart in the reference, and not part of the product
+// code object: built by llm_amd/build.py into a code object of its own.
 //
-//   q8_probe_read_l{4,8,16}  a plain streaming read of `bytes`: 256 threads a
-//                            workgroup, L 16-byte loads per lane all issued
-//                            before any is used, one pass (grid = bytes /
-//                            (4096 L)); the best L at a given size is the
-//                            "what can a single kernel read" ceiling of an
-//                            HBM-bound launch of that size;
+//   q8_probe_read_l{2,4,8,16}[_nt]  a plain streaming read of `bytes`: L
+//                            16-byte loads per lane all issued before any is
+//                            used, one pass; default or non-temporal policy
+//                            (the GEMV's weight loads are non-temporal), any
+//                            workgroup size (the launcher passes the GEMV's);
 //   q8_probe_empty           a kernel that does nothing (per-launch cost);
 //   q8_probe_mfma            int8 MFMA only: 4 independent accumulator chains
 //                            of v_mfma_i32_32x32x32_i8 per wave;
@@ -22,18 +22,38 @@
 //   q8_probe_mix_f16         the same tile-blocks for the f16-MFMA family:
 //                            two v_mfma_f32_32x32x16_f16 per block (the exact
 //                            integer dot, already f32), half a scale-product
-//                            MFMA and 16 fma (no converts).
+//                            MFMA and 16 fma (no converts);
+//   q8_probe_split_*         two roles on the same SIMDs: in an 8-wave
+//                            workgroup waves w and w + 4 share a SIMD (the
+//                            dispatcher gives the waves of a workgroup to the
+//                            four SIMDs in turn), so waves 0-3 run role A and
+//                            waves 4-7 role B on every SIMD at once; `mask`
+//                            switches each role on or off, so the time of A
+//                            alone, B alone and both is measured at the same
+//                            launch shape: both = the larger of the two when
+//                            their pipes overlap, their sum when they share one.
 // Results feed `sink` only when equal to `never` (the host passes a value no
 // result takes), so no work is dead and nothing is written.
+#include <hip/hip_runtime.h>
 
-template <int L>
+#include "q8_bench_args.h"
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x32 __attribute__((ext_vector_type(32)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+template <int L, bool NT>
 static __device__ __forceinline__ void probe_read(const Q8ProbeArgs &a) {
-    const long long base = (long long)blockIdx.x * (256 * 16 * L) + threadIdx.x * 16;
+    const int threads = blockDim.x;
+    const long long base = (long long)blockIdx.x * threads * 16 * L + threadIdx.x * 16;
     i32x4 v[L];
 #pragma unroll
     for (int i = 0; i < L; i++) {
-        const long long off = min(base + (long long)i * 256 * 16, a.bytes - 16);
-        v[i] = *(const i32x4 *)(a.src + off);
+        const long long off = min(base + (long long)i * threads * 16, a.bytes - 16);
+        const i32x4 *p = (const i32x4 *)(a.src + off);
+        v[i] = NT ? __builtin_nontemporal_load(p) : *p;
     }
     unsigned acc = 0;
 #pragma unroll
@@ -41,9 +61,17 @@ static __device__ __forceinline__ void probe_read(const Q8ProbeArgs &a) {
     if (acc == a.never) a.sink[0] = acc;
 }
 
-extern "C" __global__ __launch_bounds__(256) void q8_probe_read_l4(Q8ProbeArgs a) { probe_read<4>(a); }
-extern "C" __global__ __launch_bounds__(256) void q8_probe_read_l8(Q8ProbeArgs a) { probe_read<8>(a); }
-extern "C" __global__ __launch_bounds__(256) void q8_probe_read_l16(Q8ProbeArgs a) { probe_read<16>(a); }
+#define Q8_PROBE_READ(L)                                                                                    \
+    extern "C" __global__ __launch_bounds__(1024) void q8_probe_read_l##L(Q8ProbeArgs a) {                \
+        probe_read<L, false>(a);                                                                           \
+    }                                                                                                      \
+    extern "C" __global__ __launch_bounds__(1024) void q8_probe_read_l##L##_nt(Q8ProbeArgs a) {           \
+        probe_read<L, true>(a);                                                                            \
+    }
+Q8_PROBE_READ(2)
+Q8_PROBE_READ(4)
+Q8_PROBE_READ(8)
+Q8_PROBE_READ(16)
 
 extern "C" __global__ __launch_bounds__(64) void q8_probe_empty(Q8ProbeArgs a) {
     if (threadIdx.x == 1024) a.sink[0] = a.never;
@@ -181,3 +209,78 @@ extern "C" __global__ __launch_bounds__(256) void q8_probe_mix_f16(Q8ProbeArgs a
     for (int i = 0; i < 16; i++) s += acc[i];
     if (__float_as_uint(s) == a.never) a.sink[0] = 1u;
 }
+
+
+// ---- co-resident roles (q8_probe_split_*) ----
+// A: int8 MFMA, four independent chains (4 MFMAs a trip)
+static __device__ __forceinline__ void role_i8(const Q8ProbeArgs &a) {
+    const int lane = threadIdx.x & 63;
+    const i32x4 x = {lane, lane + 1, lane + 2, lane + 3};
+    const i32x4 w = {3 * lane, lane ^ 5, lane * 7, 11};
+    i32x16 c0 = {}, c1 = {}, c2 = {}, c3 = {};
+    for (int it = 0; it < a.iters; it++) {
+        c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(x, w, c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(w, x, c1, 0, 0, 0);
+        c2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(x, x, c2, 0, 0, 0);
+        c3 = __builtin_amdgcn_mfma_i32_32x32x32_i8(w, w, c3, 0, 0, 0);
+    }
+    unsigned acc = 0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) acc ^= (unsigned)(c0[i] + c1[i] + c2[i] + c3[i]);
+    if (acc == a.never) a.sink[0] = acc;
+}
+// A: f32 outer-product scale MFMA, two chains (2 MFMAs a trip: four tile-blocks' scale products)
+static __device__ __forceinline__ void role_f32(const Q8ProbeArgs &a) {
+    const int lane = threadIdx.x & 63;
+    const float sx = 1e-3f * (float)(lane + 1), dw = 2e-3f * (float)(64 - lane);
+    f32x32 c0 = {}, c1 = {};
+    for (int it = 0; it < a.iters; it++) {
+        c0 = __builtin_amdgcn_mfma_f32_32x32x1f32(sx, dw, c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_f32_32x32x1f32(dw, sx, c1, 0, 0, 0);
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) s += c0[i] + c1[i];
+    if (__float_as_uint(s) == a.never) a.sink[0] = 1u;
+}
+// B: the block-scale VALU (CVT = 1: 16 cvt + 16 fma a trip; CVT = 0: 32 fma a trip)
+template <int CVT>
+static __device__ __forceinline__ void role_valu(const Q8ProbeArgs &a) {
+    const int lane = threadIdx.x & 63;
+    i32x16 iv;
+    f32x16 sc, acc = {}, acc2 = {};
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        iv[i] = lane * 37 + i;
+        sc[i] = 1e-3f * (float)(i + 1);
+    }
+    for (int it = 0; it < a.iters; it++) {
+        asm volatile("" : "+v"(iv), "+v"(sc));
+        if (CVT) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[i] = __builtin_fmaf((float)iv[i], sc[i], acc[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                acc[i] = __builtin_fmaf(sc[i], sc[i], acc[i]);
+                acc2[i] = __builtin_fmaf(acc[i], sc[i], acc2[i]);
+            }
+        }
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) s += acc[i] + acc2[i];
+    if (__float_as_uint(s) == a.never) a.sink[0] = 1u;
+}
+
+#define Q8_PROBE_SPLIT(NAME, ROLE_A, ROLE_B)                                                    \
+    extern "C" __global__ __launch_bounds__(512) void q8_probe_split_##NAME(Q8ProbeArgs a) {  \
+        if ((threadIdx.x >> 6) < 4) {                                                          \
+            if (a.mask & 1) ROLE_A(a);                                                         \
+        } else {                                                                               \
+            if (a.mask & 2) ROLE_B(a);                                                         \
+        }                                                                                      \
+    }
+Q8_PROBE_SPLIT(i8_valu, role_i8, role_valu<1>)
+Q8_PROBE_SPLIT(i8_fma, role_i8, role_valu<0>)
+Q8_PROBE_SPLIT(f32_valu, role_f32, role_valu<1>)

@@ -93,8 +93,6 @@ enum Fn {
     F_COPY,
     F_EMBED,
     F_ROPE, F_ATTN_DECODE, F_ATTN_DECODE_W4, F_ATTN_PREFILL, F_SYNTH, F_ADVANCE,
-    F_PROBE_READ_L4, F_PROBE_READ_L8, F_PROBE_READ_L16, F_PROBE_EMPTY, F_PROBE_MFMA, F_PROBE_VALU, F_PROBE_MIX,
-    F_PROBE_MIX_F16,
     F_COUNT
 };
 
@@ -129,9 +127,38 @@ const char *const kFnNames[F_COUNT] = {
     "q8_copy",
     "q8_embed",
     "q8_rope_append", "q8_attn_decode", "q8_attn_decode_w4", "q8_attn_prefill", "q8_synth", "q8_advance",
-    "q8_probe_read_l4", "q8_probe_read_l8", "q8_probe_read_l16", "q8_probe_empty", "q8_probe_mfma",
-    "q8_probe_valu", "q8_probe_mix", "q8_probe_mix_f16",
 };
+
+// Every kernel of the code object with its metadata (q8_manifest.h, from the
+// code object's AMDGPU note at build time).
+const q8i::KernelMeta kKernelMeta[] = {Q8_KERNEL_META};
+
+const q8i::KernelMeta *find_meta(const char *name) {
+    for (const q8i::KernelMeta &m : kKernelMeta)
+        if (std::strcmp(m.name, name) == 0) return &m;
+    return nullptr;
+}
+
+// A launch the kernel cannot take is refused before it reaches the device,
+// as the reference refuses launch shapes its kernels' attributes do not
+// allow (cuda/mod.rs:229-283) and checks a launch's argument count against
+// the kernel (cuda/mod.rs:1835-1848): the host's argument block must be
+// exactly the kernel's explicit arguments (every kernel here takes one
+// struct by value), the workgroup a whole number of waves within the
+// kernel's compiled bound, and static plus dynamic LDS within the device's.
+int check_launch(const q8i::KernelMeta &m, size_t args_size, unsigned block, size_t dynamic_lds,
+                 size_t lds_limit) {
+    if (args_size != m.args)
+        return fail(Q8_ERR_INVALID, "launch of %s: a %zu-byte argument block for %u bytes of kernel arguments",
+                    m.name, args_size, m.args);
+    if (block == 0 || block % 64 != 0 || block > m.max_wg)
+        return fail(Q8_ERR_INVALID, "launch of %s: %u threads per workgroup (whole waves, at most %u)", m.name, block,
+                    m.max_wg);
+    if (m.lds + dynamic_lds > lds_limit)
+        return fail(Q8_ERR_UNSUPPORTED, "launch of %s: %u + %zu bytes of LDS, the device allows %zu", m.name, m.lds,
+                    dynamic_lds, lds_limit);
+    return Q8_OK;
+}
 
 constexpr int kArgmaxParts = 1024;
 // Partials the argmax workspace holds: the lm_head GEMV writes one per 32-row
@@ -169,6 +196,7 @@ struct q8_ctx {
     hipStream_t stream = nullptr;
     hipModule_t module = nullptr;
     hipFunction_t fn[F_COUNT] = {};
+    const q8i::KernelMeta *meta[F_COUNT] = {};
     std::recursive_mutex mu;
     std::map<std::pair<uintptr_t, size_t>, q8_weight *> weights;
     std::map<std::pair<uintptr_t, size_t>, float *> vectors;  // resident f32 norm weights, by host identity
@@ -183,7 +211,6 @@ struct q8_ctx {
     void *norm_ws = nullptr;             // rmsnorm(x) when a norm cannot fold into the decode GEMV
     size_t norm_ws_bytes = 0;
     void *argmax_ws = nullptr;           // per-workgroup partials + result
-    unsigned *probe_sink = nullptr;      // the measurement kernels' never-written result slot
     void *noalloc = nullptr;             // this device's static scratch of q8_matmul_noalloc (not owned)
     float *split_ws = nullptr;           // partial results of split-K workgroups
     unsigned *counters = nullptr;        // split-K arrival counters (kernels reset them to 0)
@@ -235,10 +262,7 @@ int option(q8_ctx *c, const char *name, int fallback) {
 
 int launch(q8_ctx *c, Fn f, unsigned grid, unsigned block, unsigned lds, void *args, size_t args_size) {
     if (grid == 0) return Q8_OK;
-    if (lds > c->max_lds)
-        return fail(Q8_ERR_UNSUPPORTED, "%s needs %u bytes of LDS, the device allows %zu", kFnNames[f], lds,
-                    c->max_lds);
-    (void)args_size;
+    Q8_TRY(check_launch(*c->meta[f], args_size, block, lds, c->max_lds));
     void *params[] = {args};  // every kernel takes one argument block by value
     HIP_TRY(hipModuleLaunchKernel(c->fn[f], grid, 1, 1, block, 1, 1, lds, c->stream, params, nullptr),
             kFnNames[f]);
@@ -1059,6 +1083,21 @@ const char *q8_last_error(void) { return g_last_error.c_str(); }
 
 const char *q8_build_info(void) { return Q8_BUILD_INFO; }
 
+int q8_kernel_info(const char *name, q8_kernel_info_t *out) {
+    if (!name || !out) return fail(Q8_ERR_INVALID, "q8_kernel_info: bad arguments");
+    const q8i::KernelMeta *m = find_meta(name);
+    if (!m) return fail(Q8_ERR_INVALID, "q8_kernel_info: no kernel %s in this build", name);
+    *out = q8_kernel_info_t{m->args, m->kernarg, m->vgpr, m->agpr, m->sgpr, m->lds, m->max_wg, m->priv};
+    return Q8_OK;
+}
+
+int q8_launch_check(const char *name, size_t args_size, unsigned block, size_t dynamic_lds, size_t lds_limit) {
+    if (!name) return fail(Q8_ERR_INVALID, "q8_launch_check: null kernel name");
+    const q8i::KernelMeta *m = find_meta(name);
+    if (!m) return fail(Q8_ERR_INVALID, "q8_launch_check: no kernel %s in this build", name);
+    return check_launch(*m, args_size, block, dynamic_lds, lds_limit);
+}
+
 int q8_open(int device, q8_ctx **out) {
     if (!out) return fail(Q8_ERR_INVALID, "q8_open: null output");
     *out = nullptr;
@@ -1094,12 +1133,13 @@ int q8_open(int device, q8_ctx **out) {
             if (he != hipSuccess)
                 rc = fail(Q8_ERR_NO_DEVICE, "hip: hipModuleGetFunction(%s) failed: %s", kFnNames[i],
                           hipGetErrorString(he));
+            c->meta[i] = find_meta(kFnNames[i]);
+            if (rc == Q8_OK && !c->meta[i])
+                rc = fail(Q8_ERR_NO_DEVICE, "kernel %s has no metadata in this build", kFnNames[i]);
         }
         if (rc != Q8_OK) break;
         he = dev_malloc(c, &c->argmax_ws, kArgmaxMaxParts * 8 + 256);
         if (he != hipSuccess) { rc = hip_fail(he, "hipMalloc(argmax)"); break; }
-        he = dev_malloc(c, (void **)&c->probe_sink, 256);
-        if (he != hipSuccess) { rc = hip_fail(he, "hipMalloc(probe sink)"); break; }
         rc = q8i::noalloc_scratch(device, &c->noalloc);  // the device is current (hipSetDevice above)
         if (rc != Q8_OK) break;
         he = dev_malloc(c, (void **)&c->split_ws, kSplitBytes);
@@ -1122,6 +1162,7 @@ void q8_close(q8_ctx *c) {
     if (!c) return;
     hipSetDevice(c->device);
     if (c->stream) hipStreamSynchronize(c->stream);
+    q8i::noalloc_release(c);
     for (auto &kv : c->weights) {
         hipFree(kv.second->base);
         delete kv.second;
@@ -1133,7 +1174,6 @@ void q8_close(q8_ctx *c) {
         if (w && !in_arena(c, w)) hipFree(w);
     if (c->arena) hipFree(c->arena);
     if (c->argmax_ws) hipFree(c->argmax_ws);
-    if (c->probe_sink) hipFree(c->probe_sink);
     if (c->split_ws) hipFree(c->split_ws);
     if (c->counters) hipFree(c->counters);
     for (q8_weight *w : c->owned) {
@@ -1676,6 +1716,9 @@ int q8_matmul_noalloc(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset,
         if (rc != Q8_ERR_UNSUPPORTED) return rc;
     }
     if (!c->noalloc) return fail(Q8_ERR_NO_DEVICE, "q8_matmul_noalloc: no device scratch");
+    if (!q8i::noalloc_claim(c->device, c))
+        return fail(Q8_ERR_UNSUPPORTED, "q8_matmul_noalloc: device %d's scratch is held by another context (the "
+                                        "first context to use it keeps it until q8_close)", c->device);
     const size_t need = prepared_bytes(n, k, Q8_PREPARED_I8, nullptr);
     if (need > Q8_NOALLOC_SCRATCH_BYTES)
         return fail(Q8_ERR_UNSUPPORTED, "q8_matmul_noalloc: %d tokens of k = %d need %zu bytes of quantized "
@@ -1858,47 +1901,6 @@ int q8_copy_device(q8_ctx *c, q8_dptr dst, q8_dptr src, size_t bytes) {
     a.bytes = (long long)bytes;
     a.blocks = (int)std::min<long long>(ceil_div((long long)(bytes / 16), 256), 8LL * c->cu_count);
     return launch(c, F_COPY, (unsigned)a.blocks, 256, 0, &a, sizeof a);
-}
-
-int q8_probe(q8_ctx *c, int which, q8_dptr src, size_t bytes, int iters, int workgroups) {
-    if (!c) return fail(Q8_ERR_INVALID, "q8_probe: null context");
-    std::lock_guard<std::recursive_mutex> lock(c->mu);
-    Q8ProbeArgs a{};
-    a.never = 0x7fc0dead;  // a NaN payload: no XOR of the data or float sum is compared equal by chance
-    a.sink = c->probe_sink;
-    switch (which) {
-    case Q8_PROBE_READ_L4:
-    case Q8_PROBE_READ_L8:
-    case Q8_PROBE_READ_L16: {
-        if (bytes == 0 || bytes % 16 != 0 || src % 16 != 0)
-            return fail(Q8_ERR_INVALID, "q8_probe: read needs a 16-byte aligned source and a multiple of 16 bytes");
-        Q8_TRY(check_span(c, src, bytes, "probe src"));
-        const int l = which == Q8_PROBE_READ_L4 ? 4 : which == Q8_PROBE_READ_L8 ? 8 : 16;
-        const long long grid = ceil_div((long long)bytes, 256LL * 16 * l);
-        if (grid > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "q8_probe: %zu bytes", bytes);
-        a.src = reinterpret_cast<const uint8_t *>(src);
-        a.bytes = (long long)bytes;
-        const Fn f = l == 4 ? F_PROBE_READ_L4 : l == 8 ? F_PROBE_READ_L8 : F_PROBE_READ_L16;
-        return launch(c, f, (unsigned)grid, 256, 0, &a, sizeof a);
-    }
-    case Q8_PROBE_EMPTY:
-        return launch(c, F_PROBE_EMPTY, 1, 64, 0, &a, sizeof a);
-    case Q8_PROBE_MFMA:
-    case Q8_PROBE_VALU:
-    case Q8_PROBE_MIX:
-    case Q8_PROBE_MIX_F16: {
-        if (iters < 2 || iters % 2 != 0 || workgroups < 1)
-            return fail(Q8_ERR_INVALID, "q8_probe: iters must be even and >= 2, workgroups >= 1");
-        a.iters = iters;
-        const Fn f = which == Q8_PROBE_MFMA ? F_PROBE_MFMA
-                     : which == Q8_PROBE_VALU ? F_PROBE_VALU
-                     : which == Q8_PROBE_MIX ? F_PROBE_MIX
-                                             : F_PROBE_MIX_F16;
-        return launch(c, f, (unsigned)workgroups, 256, 0, &a, sizeof a);
-    }
-    default:
-        return fail(Q8_ERR_INVALID, "q8_probe: unknown probe %d", which);
-    }
 }
 
 int q8_lm_head_argmax(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset, q8_dptr logits,

@@ -15,7 +15,7 @@ import numpy as np
 
 from .q8 import DecoderConfig, DecoderStats, DeviceWeight, Gpu, _check, lib
 
-Q, K, V, O, GATE, UP, DOWN = range(7)
+Q, K, V, O, GATE, UP, DOWN, OUTPUT = range(8)
 
 
 def config(**kw) -> DecoderConfig:

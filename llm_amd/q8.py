@@ -48,7 +48,8 @@ EXPORTS = (
     "q8_matmul", "q8_matmul_noalloc", "q8_matmul_q8", "q8_prepare", "q8_silu_mul_prepare", "q8_rmsnorm",
     "q8_norm_prepare", "q8_silu_mul",
     "q8_matmul_decode_group", "q8_matmul_prompt_group", "q8_gate_up_silu", "q8_gate_up_silu_prepared",
-    "q8_lm_head_argmax", "q8_argmax", "q8_copy_device", "q8_embeddings", "q8_probe",
+    "q8_lm_head_argmax", "q8_argmax", "q8_copy_device", "q8_embeddings",
+    "q8_kernel_info", "q8_launch_check",
     "q8_plan", "q8_tactic_count", "q8_tactic_row",
     "q8_event_create", "q8_event_record", "q8_event_elapsed_ms", "q8_event_destroy",
     "q8_graph_begin", "q8_graph_end", "q8_graph_launch", "q8_graph_destroy",
@@ -65,8 +66,6 @@ EXPORTS = (
     "q8_workspace_plan", "q8_workspace_query", "q8_workspace_region", "q8_vector_resident",
 )
 
-
-PROBE_READ_L4, PROBE_READ_L8, PROBE_READ_L16, PROBE_EMPTY, PROBE_MFMA, PROBE_VALU, PROBE_MIX, PROBE_MIX_F16 = range(8)
 
 
 class Q8Error(RuntimeError):
@@ -91,6 +90,25 @@ class Prepared(ctypes.Structure):
         return (self.n + 31) // 32 * (self.k // 32) * 32 * 4
 
 
+class KernelInfo(ctypes.Structure):
+    """q8_kernel_info_t: one kernel's metadata from the code object."""
+    _fields_ = [("args_bytes", ctypes.c_uint32), ("kernarg_bytes", ctypes.c_uint32), ("vgprs", ctypes.c_uint32),
+                ("agprs", ctypes.c_uint32), ("sgprs", ctypes.c_uint32), ("static_lds", ctypes.c_uint32),
+                ("max_workgroup", ctypes.c_uint32), ("private_bytes", ctypes.c_uint32)]
+
+
+def kernel_info(name: str) -> dict:
+    """q8_kernel_info as a dict."""
+    info = KernelInfo()
+    _check(lib().q8_kernel_info(name.encode(), ctypes.byref(info)))
+    return {f: getattr(info, f) for f, _ in info._fields_}
+
+
+def launch_check(name: str, args_bytes: int, block: int, dynamic_lds: int, lds_limit: int) -> int:
+    """q8_launch_check's status (no device needed)."""
+    return lib().q8_launch_check(name.encode(), args_bytes, block, dynamic_lds, lds_limit)
+
+
 class GgufTensorInfo(ctypes.Structure):
     """q8_gguf_tensor_info (include/q8gguf.h)."""
     _fields_ = [("name", ctypes.c_char_p), ("name_len", ctypes.c_uint64), ("n_dims", ctypes.c_uint32),
@@ -103,7 +121,8 @@ class DecoderConfig(ctypes.Structure):
     """q8_decoder_config (include/q8decoder.h)."""
     _fields_ = [(f, ctypes.c_int) for f in ("n_layer", "n_embd", "n_ff", "n_head", "n_head_kv", "head_dim",
                                             "n_rot", "n_vocab", "capacity", "max_batch")] + \
-               [("eps", ctypes.c_float), ("rope_base", ctypes.c_float)]
+               [("eps", ctypes.c_float), ("rope_base", ctypes.c_float), ("untied_output", ctypes.c_int),
+                ("embd_std", ctypes.c_float)]
 
 
 class WorkspaceShape(ctypes.Structure):
@@ -202,7 +221,8 @@ def lib():
         "q8_lm_head_argmax": (c_int, [vp, vp, u64, c_size, u64, c_size, ctypes.POINTER(ctypes.c_uint32)]),
         "q8_argmax": (c_int, [vp, u64, c_size, c_size, ctypes.POINTER(ctypes.c_uint32)]),
         "q8_copy_device": (c_int, [vp, u64, u64, c_size]),
-        "q8_probe": (c_int, [vp, c_int, u64, c_size, c_int, c_int]),
+        "q8_kernel_info": (c_int, [ctypes.c_char_p, ctypes.POINTER(KernelInfo)]),
+        "q8_launch_check": (c_int, [ctypes.c_char_p, c_size, ctypes.c_uint, c_size, c_size]),
         "q8_embeddings": (c_int, [vp, vp, ctypes.POINTER(ctypes.c_uint32), c_size, u64, c_size]),
         "q8_plan": (c_int, [vp, c_int, c_int, c_int, ctypes.POINTER(Tactic)]),
         "q8_tactic_count": (c_int, []),
@@ -661,11 +681,9 @@ class Gpu:
     def plan(self, n: int, out: int, k: int) -> dict:
         return plan(n, out, k, self)
 
-    def probe(self, which: int, src: "DeviceBuffer | None" = None, nbytes: int = 0, iters: int = 0,
-              workgroups: int = 0, src_offset: int = 0):
-        """Launch a measurement kernel (q8_probe, PROBE_* below)."""
-        ptr = src.ptr + src_offset if src is not None else 0
-        _check(lib().q8_probe(self.handle, which, ptr, nbytes, iters, workgroups))
+    def stream(self) -> int:
+        """The context's HIP stream (q8_stream)."""
+        return lib().q8_stream(self.handle)
 
     # ---- timing and graphs ----
     def event(self):

@@ -161,3 +161,111 @@ def test_weight_view_checks_its_byte_length():
         q8.Weight(np.zeros(33, np.uint8), 32, 1)
     w = q8.Weight(np.zeros(68, np.uint8), 32, 2)
     assert w.identity()[1] == 68
+
+
+# ---- kernel metadata and launch validation (cuda/mod.rs:229-283, 1835-1848) ----
+
+ARG_STRUCTS = {  # kernel name prefix -> the argument struct every kernel of that family takes
+    "q8_gemm_": "Q8GemmArgs", "q8_gemv": "Q8GemvArgs", "q8_quantize": "Q8QuantArgs", "q8_rmsnorm": "Q8NormArgs",
+    "q8_repack": "Q8RepackArgs", "q8_argmax": "Q8ArgmaxArgs", "q8_copy": "Q8CopyArgs", "q8_embed": "Q8EmbedArgs",
+    "q8_silu_mul": "Q8EltArgs", "q8_rope_append": "Q8RopeArgs", "q8_attn_decode": "Q8AttnDecodeArgs",
+    "q8_attn_prefill": "Q8AttnPrefillArgs", "q8_synth": "Q8SynthArgs", "q8_advance": "Q8AdvanceArgs",
+}
+
+
+def test_every_kernel_carries_its_metadata():
+    info = json.loads(llm_amd.build_info())
+    sizes = {}
+    for name in info["kernels"]:
+        meta = q8.kernel_info(name)
+        assert meta["args_bytes"] > 0, name
+        assert meta["kernarg_bytes"] >= meta["args_bytes"], name
+        assert meta["max_workgroup"] in (64, 128, 256, 512, 576, 1024), (name, meta["max_workgroup"])
+        assert meta["private_bytes"] == 0, f"{name} spills {meta['private_bytes']} bytes per lane"
+        assert 0 < meta["vgprs"] + meta["agprs"] <= 512, name
+        family = next(s for p, s in ARG_STRUCTS.items() if name.startswith(p))
+        sizes.setdefault(family, set()).add(meta["args_bytes"])
+    # every kernel of a family takes the same struct, so the same argument bytes
+    for family, seen in sizes.items():
+        assert len(seen) == 1, f"{family}: kernels disagree on the argument size {sorted(seen)}"
+    with pytest.raises(q8.Q8Error) as e:
+        q8.kernel_info("q8_no_such_kernel")
+    assert e.value.status == q8.Q8_ERR_INVALID
+
+
+def test_launch_check_refuses_what_a_kernel_cannot_take():
+    """The rules every launch of the library passes, host-only: the argument
+    block is exactly the kernel's explicit arguments, the workgroup whole
+    waves within the kernel's compiled bound, and static + dynamic LDS within
+    the device's."""
+    lds = 160 * 1024
+    for name in ("q8_gemm_s1_t2", "q8_gemv_r8_l2", "q8_quantize", "q8_attn_prefill"):
+        m = q8.kernel_info(name)
+        ok = q8.launch_check(name, m["args_bytes"], 64, 0, lds)
+        assert ok == q8.Q8_OK, (name, q8.lib().q8_last_error())
+        assert q8.launch_check(name, m["args_bytes"], m["max_workgroup"], lds - m["static_lds"], lds) == q8.Q8_OK
+        assert q8.launch_check(name, m["args_bytes"] + 8, 64, 0, lds) == q8.Q8_ERR_INVALID
+        assert "argument block" in q8.lib().q8_last_error().decode()
+        assert q8.launch_check(name, m["args_bytes"] - 4, 64, 0, lds) == q8.Q8_ERR_INVALID
+        assert q8.launch_check(name, m["args_bytes"], m["max_workgroup"] + 64, 0, lds) == q8.Q8_ERR_INVALID
+        assert q8.launch_check(name, m["args_bytes"], 96, 0, lds) == q8.Q8_ERR_INVALID   # not whole waves
+        assert q8.launch_check(name, m["args_bytes"], 0, 0, lds) == q8.Q8_ERR_INVALID
+        assert q8.launch_check(name, m["args_bytes"], 64, lds - m["static_lds"] + 1, lds) == q8.Q8_ERR_UNSUPPORTED
+    assert q8.launch_check("q8_no_such_kernel", 8, 64, 0, lds) == q8.Q8_ERR_INVALID
+
+
+# ---- the benchmark's probe library: outside the product boundary ----
+
+def test_bench_library_exports_exactly_its_header():
+    from llm_amd import probes
+    text = re.sub(r"/\*.*?\*/", "", open(os.path.join(ROOT, "include", "q8bench.h")).read(), flags=re.S)
+    declared = set(re.findall(r"\b(q8bench_[a-z0-9_]+)\s*\(", text))
+    out = subprocess.run(["nm", "-D", "--defined-only", probes.LIB_PATH], stdout=subprocess.PIPE, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    assert declared == {s for s in exported if s.startswith("q8bench_")}
+    assert declared == set(probes.EXPORTS)
+    assert not {s for s in exported if s.startswith("q8_")}, "the bench library exports product symbols"
+    product = json.loads(llm_amd.build_info())["kernels"]
+    assert not [k for k in product if "probe" in k], "measurement kernels in the product code object"
+    bench = json.loads(probes.lib().q8bench_build_info())
+    assert "q8_probe_split_i8_valu" in bench["kernels"] and "q8_probe_read_l2_nt" in bench["kernels"]
+
+
+# ---- the no-allocation scratch: one holding context per device ----
+
+def test_noalloc_scratch_ownership_rule(tmp_path):
+    """q8_noalloc_owner.h on its own (host code, g++): the first context to use
+    a device's scratch holds it, a second is refused until the first releases,
+    devices are independent, out-of-range devices are refused."""
+    src = tmp_path / "owner_test.cpp"
+    src.write_text(r'''
+#include "q8_noalloc_owner.h"
+#include <cstdio>
+#define CHECK(c) do { if (!(c)) { std::printf("failed: %s (line %d)\n", #c, __LINE__); return 1; } } while (0)
+int main() {
+    q8i::NoallocOwners o;
+    int a = 0, b = 0;
+    CHECK(o.claim(0, &a));            // first user takes device 0
+    CHECK(o.claim(0, &a));            // and keeps it
+    CHECK(!o.claim(0, &b));           // a second context is refused
+    CHECK(o.holder(0) == &a);
+    CHECK(o.claim(1, &b));            // another device is independent
+    CHECK(!o.claim(1, &a));
+    o.release(&a);                    // q8_close of the holder
+    CHECK(o.holder(0) == nullptr);
+    CHECK(o.claim(0, &b));            // now the second context may take it
+    CHECK(!o.claim(0, &a));
+    CHECK(!o.claim(-1, &a) && !o.claim(q8i::NoallocOwners::kMaxDevices, &a));
+    CHECK(!o.claim(2, nullptr));
+    o.release(&b);
+    CHECK(o.holder(0) == nullptr && o.holder(1) == nullptr);
+    std::printf("ok\n");
+    return 0;
+}
+''')
+    exe = tmp_path / "owner_test"
+    subprocess.run(["g++", "-std=c++17", "-O1", "-Wall", "-Werror", "-I", os.path.join(ROOT, "llm_amd", "csrc"),
+                    str(src), "-o", str(exe)], check=True)
+    res = subprocess.run([str(exe)], stdout=subprocess.PIPE, text=True)
+    assert res.returncode == 0 and res.stdout.strip() == "ok", res.stdout

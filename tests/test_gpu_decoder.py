@@ -632,6 +632,7 @@ class OracleDecoder:
         self.perturb = perturb
         if gpu is not None:
             self.embd = gpu.export(dec.weight(-1))
+            self.out = gpu.export(dec.weight(-1, dm.OUTPUT))  # the embedding itself when tied
             self.w = {(l, i): gpu.export(dec.weight(l, i)) for l in range(c.n_layer) for i in range(7)}
             self.norms = {(l, i): dec.norm(l, i) for l in range(c.n_layer) for i in range(2)}
             self.out_norm = dec.norm(-1)
@@ -643,7 +644,7 @@ class OracleDecoder:
     def twin(self, perturb):
         """A fresh oracle over the same weights (empty cache, position 0)."""
         t = OracleDecoder(None, SimpleNamespace(cfg=self.cfg), perturb)
-        t.embd, t.w, t.norms, t.out_norm = self.embd, self.w, self.norms, self.out_norm
+        t.embd, t.out, t.w, t.norms, t.out_norm = self.embd, self.out, self.w, self.norms, self.out_norm
         return t
 
     def mm(self, data, k, out, x):
@@ -679,7 +680,7 @@ class OracleDecoder:
             x = (x + self.mm(self.w[(l, dm.DOWN)], c.n_ff, E, act)).astype(np.float32)
         self.pos += n
         last = oracle.rmsnorm(x[-1], self.out_norm, c.eps)
-        return self.mm(self.embd, E, c.n_vocab, last[None])[0]
+        return self.mm(self.out, E, c.n_vocab, last[None])[0]
 
 
 def check_logits(got, ref, what, tol=None):
@@ -726,6 +727,41 @@ def test_decoder_prompt_and_decode_steps_match_the_oracle(gpu):
             if top2[1] - top2[0] > 2e-3 * np.abs(logits).max():
                 assert int(steps[i]) == oracle.argmax(logits), f"decode step {i}"
         check_logits(dec.logits(), logits, "last decode step logits")
+    finally:
+        dec.close()
+
+
+@pytest.mark.parametrize("embd_std", [1.0, 4.0])
+def test_decoder_greedy_feedback_varies_through_the_captured_graph(gpu, embd_std):
+    """Greedy decode whose tokens change from step to step, fed back on the
+    device through the captured step graph: a model with its own output head
+    (a GGUF with output.weight, model.rs:519-524) and an embedding scale at
+    which the current token shows in the last hidden state.  Each step's
+    logits against the oracle decoder fed the same tokens; the device's token
+    is the argmax of its logits, and the oracle's wherever the oracle's top-2
+    gap clears the bar; at least two distinct tokens over the steps."""
+    cfg = small_config()
+    cfg.untied_output = 1
+    cfg.embd_std = embd_std
+    dec = dm.Decoder(gpu, cfg, seed=21)
+    try:
+        ref = OracleDecoder(gpu, dec)
+        assert not np.array_equal(ref.out, ref.embd), "the output head is a matrix of its own"
+        prompt = np.random.default_rng(SEED + 5).integers(0, cfg.n_vocab, 24).astype(np.uint32)
+        print(f"\nuntied decoder, embd_std {embd_std}: prompt of 24, then 10 steps", flush=True)
+        tokens = [dec.forward(prompt)]
+        check_logits(dec.logits(), ref.forward(prompt), "untied prompt logits")
+        for i in range(10):  # one step a call: eager, then captured, then graph replays
+            t = int(dec.generate(1)[0])
+            got = dec.logits()
+            want = ref.forward([tokens[-1]])
+            check_logits(got, want, f"untied step {i}")
+            assert t == int(np.argmax(got)), f"step {i}: the token is the argmax of the step's logits"
+            tokens.append(t)
+        stats = dec.graph_stats()
+        print(f"tokens {tokens}, graphs {stats}", flush=True)
+        assert stats["captured"] >= 1 and stats["graphs"] >= 1, stats
+        assert len(set(tokens)) >= 2, f"greedy decode repeated one token: {tokens}"
     finally:
         dec.close()
 

@@ -962,6 +962,55 @@ def test_lm_head_argmax(gpu):
     gpu.release(w)
 
 
+@pytest.mark.parametrize("seed", [100, 101, 102])
+def test_lm_head_default_order_argmax(gpu, seed):
+    """The lm_head at the default block order (the tree sum, not the exact
+    AVX2 order): logits within the bar and the token the GEMV's folded argmax
+    returns equal to the greedy argmax of the oracle's logits
+    (sampler.rs:167-175, first index of the strictly greatest value)."""
+    gpu.set_option("gemv.exact", -1)
+    r = rng(seed)
+    vocab, k = 122880, 2304
+    w = weight(r, vocab, k)
+    x = r.standard_normal(k, dtype=np.float32)
+    ref = oracle.matmul(w.data, k, vocab, x, 1).reshape(-1)
+    xb, lb = gpu.alloc(4 * k), gpu.alloc(4 * vocab)
+    xb.upload(x)
+    best = gpu.lm_head_argmax(w, xb, 0, lb, 0)
+    got = lb.download(np.float32, vocab)
+    assert_close(got, ref, f"default-order lm_head logits seed {seed}")
+    top2 = np.sort(ref)[-2:]
+    gap = float(top2[1] - top2[0])
+    print(f"default order: argmax {best}, oracle {oracle.argmax(ref)}, top-2 gap {gap:.3e}", flush=True)
+    assert best == oracle.argmax(ref), f"seed {seed}: token {best} vs oracle {oracle.argmax(ref)} (gap {gap:.3e})"
+    assert best == oracle.argmax(got), "the folded argmax is the argmax of the logits it wrote"
+    xb.free()
+    lb.free()
+    gpu.release(w)
+
+
+@pytest.mark.parametrize("exact", [1, 0])
+@pytest.mark.parametrize("out", [1000, 40, 8])
+def test_gemv_tile_kernel_residual_at_ragged_rows(gpu, out, exact):
+    """The 32-row tile kernel (gemv.rows = 32) with a residual whose row count
+    is not a multiple of 32: the padding lanes of the last tile read no
+    residual (the bias buffer holds `out` floats) and write nothing."""
+    gpu.set_option("gemv.rows", 32)
+    gpu.set_option("gemv.exact", exact)
+    r = rng(110 + out + exact)
+    k = 2304
+    w = weight(r, out, k)
+    x = r.standard_normal(k, dtype=np.float32)
+    y0 = r.standard_normal(out, dtype=np.float32)
+    ref = y0 + oracle.matmul(w.data, k, out, x, 1).reshape(-1)
+    got = run_matmul(gpu, w, x, 1, bias=y0).reshape(-1)
+    what = f"tile gemv residual out={out} exact={exact}"
+    assert_close(got, ref, what)
+    if exact and oracle.simd_path() == "avx2+fma":
+        assert_bits(got, ref, what)
+    gpu.release(w)
+
+
 @pytest.mark.parametrize("values,expect", [
     ([1, 3, 3, 2], 1), ([-1, -1], 0), ([0, float("nan"), 5, 5], 2), ([float("nan"), 1, 9], 0),
     ([-0.0, 0.0], 0), ([float("-inf"), float("-inf")], 0), ([1, float("inf"), float("inf")], 1),

@@ -97,3 +97,53 @@ def test_noalloc_rejects_what_the_scratch_cannot_hold(gpu):
     xb.free()
     yb.free()
     gpu.release(w)
+
+
+def test_noalloc_scratch_is_held_by_one_context(gpu):
+    """Two contexts on one GPU each have a stream of their own, so their calls
+    could overlap on the one static array: the first context to use it holds
+    it until q8_close and a second context is refused (Q8_ERR_UNSUPPORTED,
+    nothing launched); calls that need no scratch (n = 1, the two-token GEMV)
+    still run.  The hand-over after q8_close is tested on the CPU
+    (tests/test_abi.py, q8_noalloc_owner.h)."""
+    r = np.random.default_rng(SEED + 3)
+    n, k, out = 64, 2304, 256
+    w = q8.Weight(oracle.make_q8_weight(r, out, k), k, out)
+    x = oracle.make_activations(r, n, k, outlier_rate=0.01)
+    xb, yb = gpu.alloc(4 * n * k), gpu.alloc(4 * n * out)
+    xb.upload(x)
+    noalloc(gpu, w, xb, n, yb)  # this module's context holds the scratch (if it did not already)
+    gpu.sync()
+    held = yb.download(np.float32, n * out)
+    other = q8.Gpu(0)
+    try:
+        xo, yo = other.alloc(4 * n * k), other.alloc(4 * n * out)
+        xo.upload(x)
+        yo.upload(np.zeros(n * out, np.float32))
+        print("\nsecond context on device 0: noalloc n=64 (refused), n=1 and n=2 (no scratch)", flush=True)
+        with pytest.raises(q8.Q8Error) as e:
+            noalloc(other, w, xo, n, yo)
+        assert e.value.status == q8.Q8_ERR_UNSUPPORTED and "held by another context" in e.value.message
+        other.sync()
+        assert not yo.download(np.float32, n * out).any()  # nothing was launched
+        for m in (1, 2):
+            noalloc(other, w, xo, m, yo)
+            other.sync()
+            want = oracle.matmul(w.data, k, out, x[:m], m)
+            got = yo.download(np.float32, m * out).reshape(m, out)
+            if m == 1:  # the GEMV on f32 x
+                assert_close(got, want, "second context noalloc n=1")
+            else:
+                assert_parity(got, want, exact_at(w.data, k, out, x[:m], m), f"second context noalloc n={m}")
+        xo.free()
+        yo.free()
+        other.release(w)
+    finally:
+        other.close()
+    # the holder's scratch was not touched by the refused call
+    noalloc(gpu, w, xb, n, yb)
+    gpu.sync()
+    assert_bits(yb.download(np.float32, n * out), held, "holder after the refusal")
+    xb.free()
+    yb.free()
+    gpu.release(w)
