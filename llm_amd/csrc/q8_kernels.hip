@@ -921,8 +921,14 @@ static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
     const int mrows = a.m[0].rows;
     const float *xg = a.x;
     const int nb = a.nb;
+    // the wave count comes from the arguments (the host launches
+    // waves_per_tile waves), read here with the rest: blockDim lives in the
+    // dispatch packet's hidden arguments, a cache line no earlier read
+    // fetched, and read after the barrier it cost every workgroup a scalar
+    // miss at its end (~0.04 us of a configs[0] GEMV)
+    const int nw = a.waves_per_tile;
     asm volatile("" ::"s"(mq), "s"(msc), "s"(my), "s"(mbias), "s"(mrows), "s"(xg), "s"(nb), "s"(a.xcd_order),
-                 "s"(a.total_tiles));
+                 "s"(a.total_tiles), "s"(nw));
     // the combine's partials in the same kernel-argument read: a second read
     // would wait ahead of the first partial and weight loads
     if constexpr (CMB) asm volatile("" ::"s"(a.attn_acc), "s"(a.attn_ms), "s"(a.attn_splits));
@@ -1058,7 +1064,6 @@ static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
     if constexpr (EX) {
         acc = chain_row(vbuf + r * vrow, nb);
     } else {
-        const int nw = (int)(blockDim.x >> 6);
         acc = vbuf[r];
         for (int w2 = 1; w2 < nw; w2++) acc = acc + vbuf[w2 * RS + r];
     }
@@ -1126,8 +1131,9 @@ static __device__ __forceinline__ void gemv_q8x_body(const Q8GemvArgs &a) {
     const float *xg = a.x;
     const int nb = a.nb;
     const int ntok = NT == 1 ? 1 : a.tokens;
+    const int nw = a.waves_per_tile;  // the launch's wave count, read with the rest (as gemv_rs_body)
     asm volatile("" ::"s"(mq), "s"(msc), "s"(my), "s"(mbias), "s"(mrows), "s"(xg), "s"(nb), "s"(a.xcd_order),
-                 "s"(a.total_tiles), "s"(ntok));
+                 "s"(a.total_tiles), "s"(ntok), "s"(nw));
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int j = lane / LPB;
@@ -1237,7 +1243,6 @@ static __device__ __forceinline__ void gemv_q8x_body(const Q8GemvArgs &a) {
             lsum[t] = bu < b_end ? lsum[t] + v : lsum[t];
         }
     }
-    const int nw = (int)(blockDim.x >> 6);
 #pragma unroll
     for (int t = 0; t < NT; t++) {
         float ls = lsum[t];
