@@ -254,9 +254,11 @@ int q8_matmul_q8(q8_ctx *ctx, const q8_weight *weight, q8_dptr x, size_t x_offse
  * does not split K).  Every call on one GPU shares that GPU's array, which
  * keeps the last call's bytes (each call rewrites all it reads).  Within one
  * process the first context that uses a GPU's array holds it until q8_close,
- * and a call from any other context on that GPU is Q8_ERR_UNSUPPORTED, so two
- * contexts' streams never share it; calls of the holding context are ordered
- * on its stream.  Several processes on one GPU each have their own copy. */
+ * and a call that needs the array (n >= 3) from any other context on that GPU
+ * is Q8_ERR_UNSUPPORTED before anything is launched (n = 1 and n = 2 need none
+ * and run), so two contexts' streams never share it; calls of the holding
+ * context are ordered on its stream.  Several processes on one GPU each have
+ * their own copy. */
 int q8_matmul_noalloc(q8_ctx *ctx, const q8_weight *weight, q8_dptr x, size_t x_offset, int n, q8_dptr y,
                       size_t y_offset, q8_dptr bias, size_t bias_offset);
 
