@@ -24,6 +24,10 @@ Also reported, each on its own rotation:
                 first, as configs[0]'s wording reads (q8_matmul_q8: the
                 n >= 2 arithmetic of tensor::matmul at n = 1, quantization
                 and int8 block dots in one launch);
+  configs0_sustained  the same rotation replayed back to back for
+                --sustained-seconds (default 6): GB/s over every replay and
+                the slowest replay against the fastest, i.e. whether the
+                figure holds under continuous load;
   ceilings      what one kernel of this size can do on this box: the best
                 plain streaming read of the configs[0] byte count (the
                 GEMV's achievable ceiling), an empty kernel's cost per graph
@@ -149,7 +153,42 @@ def summary(ms_list, work, unit_scale):
 # configs[0] GEMV (the headline) and its ceiling
 # ---------------------------------------------------------------------------
 
-def bench_gemv(gpu, m, k, steps, warmup, rng):
+def sustained_gemv(gpu, launch, copies, per, seconds, steps=2000):
+    """The same rotation replayed back to back for about `seconds`: one graph
+    of `steps` launches between two event nodes, replayed until the host
+    clock passes `seconds`; GB/s over every replay's event time, and the
+    slowest replay against the fastest (a throttling GPU would show it)."""
+    if seconds <= 0:
+        return None
+    pos = 0
+    e0, e1 = gpu.event(), gpu.event()
+    gpu.graph_begin()
+    gpu.record(e0)
+    for _ in range(steps):
+        launch(pos % copies)
+        pos += 1
+    gpu.record(e1)
+    g = gpu.graph_end()
+    per_replay = []
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        gpu.graph_launch(g)
+        per_replay.append(gpu.elapsed_ms(e0, e1))  # waits for the replay
+    wall = time.perf_counter() - t0
+    gpu.graph_destroy(g)
+    gpu.destroy_event(e0)
+    gpu.destroy_event(e1)
+    total_ms = sum(per_replay)
+    out = {"seconds": round(wall, 2), "replays": len(per_replay), "steps": steps * len(per_replay),
+           "gbs": round(per * steps * len(per_replay) / (total_ms * 1e-3) / 1e9, 1),
+           "us_per_step": round(total_ms * 1e3 / (steps * len(per_replay)), 3),
+           "slowest_over_fastest": round(max(per_replay) / min(per_replay), 3)}
+    log(f"configs[0] GEMV sustained: {out['gbs']:.0f} GB/s over {out['steps']} steps in {out['seconds']} s "
+        f"(slowest / fastest replay {out['slowest_over_fastest']})")
+    return out
+
+
+def bench_gemv(gpu, m, k, steps, warmup, rng, sustained_s=6.0):
     from llm_amd import q8
     base = make_weight(rng, m, k)
     per = gemv_bytes(m, k)
@@ -167,6 +206,7 @@ def bench_gemv(gpu, m, k, steps, warmup, rng):
     hot = rotating_trials(gpu, lambda i: gpu.matmul(base, xb, 0, 1, yb, 0), 1, max(steps, 50), warmup)
     hs = summary(hot, per, 1e-9)
     log(f"configs[0] GEMV MALL-hot: {hs['median_us']:.2f} us/step, {hs['value']:.0f} GB/s")
+    sustained = sustained_gemv(gpu, lambda i: gpu.matmul(weights[i], xb, 0, 1, yb, 0), copies, per, sustained_s)
     # x quantized to Q8_0 first, as the n >= 2 path does (q8_matmul_q8: one
     # launch quantizes x and takes the int8 block dots), same rotation
     q8x = rotating_trials(gpu, lambda i: gpu.matmul_q8(weights[i], xb, 0, 1, yb, 0), copies, steps, warmup)
@@ -179,7 +219,8 @@ def bench_gemv(gpu, m, k, steps, warmup, rng):
     yb.free()
     return {"us_per_step": s["median_us"], "gbs": s["value"], "trials_gbs": s["trials"], "bytes_per_step": per,
             "copies": copies, "mall_hot_gbs": round(hs["value"], 1), "mall_hot_us": hs["median_us"],
-            "q8x_gbs": round(qs["value"], 1), "q8x_us": qs["median_us"], "q8x_trials_gbs": qs["trials"]}
+            "q8x_gbs": round(qs["value"], 1), "q8x_us": qs["median_us"], "q8x_trials_gbs": qs["trials"],
+            "sustained": sustained}
 
 
 # the read probe's shapes: 16-byte loads per lane, cache policy, threads per
@@ -647,6 +688,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
+    ap.add_argument("--sustained-seconds", type=float, default=6.0,
+                    help="configs[0] GEMV replayed back to back for this long after its trials (0: skip)")
     ap.add_argument("--sections", default="all",
                     help="comma list of gemv,ceilings,reads,gemm,extras,decoder,cpu (default all); a profiler run "
                          "names one so each kernel's average covers one workload")
@@ -671,7 +714,7 @@ def main():
     m, k = 5760, HID
     gemv = {"gbs": None, "us_per_step": None, "bytes_per_step": gemv_bytes(m, k), "copies": None}
     if "gemv" in sections:
-        gemv = bench_gemv(gpu, m, k, steps, warmup, rng)
+        gemv = bench_gemv(gpu, m, k, steps, warmup, rng, args.sustained_seconds)
     ceil = bench_ceilings(gpu, steps, warmup, gemv_bytes(m, k)) if "ceilings" in sections else {}
     if "reads" in sections:
         ceil["decode_launch_reads"] = bench_launch_reads(gpu, steps, warmup)
@@ -725,6 +768,7 @@ def main():
                                  "trials_gbs": gemv.get("q8x_trials_gbs"), "entry": "q8_matmul_q8",
                                  "workload": "configs[0] with x quantized to Q8_0 per 32-block in the same launch "
                                              "(the n >= 2 arithmetic at n = 1), int8 block dots"},
+        "configs0_sustained": gemv.get("sustained"),
         "gemm_n512": {"value": r(gemm["tops"], 2), "unit": "TOPS", "peak": INT8_PEAK_TOPS,
                       "frac": round(gemm["frac"], 4) if gemm["frac"] is not None else None,
                       "us_per_layer": r(gemm["us"], 2), "ops_per_layer": gemm["ops"],
