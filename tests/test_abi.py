@@ -34,6 +34,27 @@ def test_library_loads():
     assert q8.lib() is not None
 
 
+def test_a_missing_library_fails_loudly(tmp_path):
+    """Without libq8mi.so the package raises on first use: there is no CPU
+    fallback for the matmul path (run in a fresh interpreter, so this
+    process keeps its loaded library)."""
+    code = (
+        "import sys; sys.path.insert(0, %r)\n"
+        "from llm_amd import q8\n"
+        "q8.LIB_PATH = %r\n"
+        "q8._lib = None\n"
+        "try:\n"
+        "    q8.Gpu(0)\n"
+        "except RuntimeError as e:\n"
+        "    print('raised:', e)\n"
+        "    sys.exit(0)\n"
+        "sys.exit(3)\n"
+    ) % (ROOT, str(tmp_path / "libq8mi.so"))
+    res = subprocess.run(["python3", "-c", code], stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    assert res.returncode == 0, res.stdout
+    assert "is missing" in res.stdout and "no CPU fallback" in res.stdout
+
+
 def test_every_declared_function_is_exported():
     declared = header_functions()
     exported = library_exports()
