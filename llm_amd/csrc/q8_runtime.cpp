@@ -1716,9 +1716,6 @@ int q8_matmul_noalloc(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset,
         if (rc != Q8_ERR_UNSUPPORTED) return rc;
     }
     if (!c->noalloc) return fail(Q8_ERR_NO_DEVICE, "q8_matmul_noalloc: no device scratch");
-    if (!q8i::noalloc_claim(c->device, c))
-        return fail(Q8_ERR_UNSUPPORTED, "q8_matmul_noalloc: device %d's scratch is held by another context (the "
-                                        "first context to use it keeps it until q8_close)", c->device);
     const size_t need = prepared_bytes(n, k, Q8_PREPARED_I8, nullptr);
     if (need > Q8_NOALLOC_SCRATCH_BYTES)
         return fail(Q8_ERR_UNSUPPORTED, "q8_matmul_noalloc: %d tokens of k = %d need %zu bytes of quantized "
@@ -1730,6 +1727,11 @@ int q8_matmul_noalloc(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset,
     Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)m.y, (size_t)n * w->out * 4, "noalloc y"));
     const float *b = fptr(bias, bias_offset);
     if (b) Q8_TRY(check_span(c, (q8_dptr)(uintptr_t)b, (size_t)n * w->out * 4, "noalloc bias"));
+    // claimed only by a call that passed every check and will use the array:
+    // a refused call leaves the scratch to whoever takes it next
+    if (!q8i::noalloc_claim(c->device, c))
+        return fail(Q8_ERR_UNSUPPORTED, "q8_matmul_noalloc: device %d's scratch is held by another context (the "
+                                        "first context to use it keeps it until q8_close)", c->device);
     q8_prepared p{};
     Q8_TRY(run_quantize(c, xp, 0, 0, n, k, Q8_PREPARED_I8, c->noalloc, &p));
     return run_gemm(c, &m, 1, &p, n, b, nullptr, true);

@@ -45,6 +45,47 @@ def run_both(gpu, w, x, n, residual=None):
     return got, want
 
 
+def test_a_refused_call_does_not_take_the_scratch():
+    """First in this module, before its shared context uses the array: a
+    call refused for its size holds nothing, so another context's call then
+    takes the array, and the refused context's next call is the one turned
+    away."""
+    r = np.random.default_rng(SEED + 4)
+    a, b = q8.Gpu(0), q8.Gpu(0)
+    try:
+        nb_, kb_, ob_ = 1024, 8192, 64  # 32 x 256 x 1152 bytes > 8 MiB
+        wbig = q8.Weight(oracle.make_q8_weight(r, ob_, kb_), kb_, ob_)
+        xa, ya = a.alloc(4 * nb_ * kb_), a.alloc(4 * nb_ * ob_)
+        print("\ncontext A: an oversized noalloc call (refused)", flush=True)
+        with pytest.raises(q8.Q8Error) as e:
+            noalloc(a, wbig, xa, nb_, ya)
+        assert e.value.status == q8.Q8_ERR_UNSUPPORTED and "more than" in e.value.message
+        n, k, out = 64, 2304, 256
+        w = q8.Weight(oracle.make_q8_weight(r, out, k), k, out)
+        x = oracle.make_activations(r, n, k, outlier_rate=0.01)
+        xb, yb = b.alloc(4 * n * k), b.alloc(4 * n * out)
+        xb.upload(x)
+        print("context B: noalloc n=64 (takes the array)", flush=True)
+        noalloc(b, w, xb, n, yb)
+        b.sync()
+        got = yb.download(np.float32, n * out).reshape(n, out)
+        assert_parity(got, oracle.matmul(w.data, k, out, x, n), exact_at(w.data, k, out, x, n), "context B noalloc")
+        xa2, ya2 = a.alloc(4 * n * k), a.alloc(4 * n * out)
+        xa2.upload(x)
+        print("context A: noalloc n=64 (refused: B holds the array)", flush=True)
+        with pytest.raises(q8.Q8Error) as e:
+            noalloc(a, w, xa2, n, ya2)
+        assert e.value.status == q8.Q8_ERR_UNSUPPORTED and "held by another context" in e.value.message
+        for buf in (xa, ya, xa2, ya2, xb, yb):
+            buf.free()
+        a.release(wbig)
+        a.release(w)
+        b.release(w)
+    finally:
+        b.close()
+        a.close()
+
+
 @pytest.mark.parametrize("first,second", [((512, 2304, 2304), (40, 2304, 576)), ((300, 5760, 2304), (33, 5760, 64)),
                                           ((1024, 2304, 1024), (2, 2304, 256))])
 def test_noalloc_matches_matmul_twice_second_smaller(gpu, first, second):
