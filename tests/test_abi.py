@@ -290,3 +290,53 @@ int main() {
                     str(src), "-o", str(exe)], check=True)
     res = subprocess.run([str(exe)], stdout=subprocess.PIPE, text=True)
     assert res.returncode == 0 and res.stdout.strip() == "ok", res.stdout
+
+
+def test_noalloc_scratch_owner_table_under_threads(tmp_path):
+    """The owner table under ThreadSanitizer (host code, g++): eight threads,
+    each a context of its own, claim device 0 and release it in a loop; at
+    most one holds it at any moment, every claim either succeeds for one
+    thread or is refused, and TSan sees no data race."""
+    src = tmp_path / "owner_threads.cpp"
+    src.write_text(r'''
+#include "q8_noalloc_owner.h"
+#include <atomic>
+#include <cstdio>
+#include <thread>
+#include <vector>
+int main() {
+    q8i::NoallocOwners o;
+    std::atomic<int> inside{0}, bad{0}, taken{0};
+    std::vector<std::thread> ts;
+    for (int t = 0; t < 8; t++) {
+        ts.emplace_back([&, t] {
+            int me = t;
+            for (int i = 0; i < 20000; i++) {
+                if (o.claim(0, &me)) {
+                    if (inside.fetch_add(1) != 0) bad++;
+                    if (o.holder(0) != &me) bad++;
+                    taken++;
+                    inside.fetch_sub(1);
+                    o.release(&me);
+                } else if (o.holder(0) == &me) {
+                    bad++;  // refused, yet recorded as the holder
+                }
+            }
+        });
+    }
+    for (auto &th : ts) th.join();
+    if (bad.load() != 0 || taken.load() == 0 || o.holder(0) != nullptr) {
+        std::printf("failed: bad %d taken %d\n", bad.load(), taken.load());
+        return 1;
+    }
+    std::printf("ok %d\n", taken.load());
+    return 0;
+}
+''')
+    exe = tmp_path / "owner_threads"
+    subprocess.run(["g++", "-std=c++17", "-O1", "-g", "-fsanitize=thread", "-Wall", "-Werror",
+                    "-I", os.path.join(ROOT, "llm_amd", "csrc"), str(src), "-o", str(exe), "-pthread"], check=True)
+    res = subprocess.run([str(exe)], stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True,
+                         env=dict(os.environ, TSAN_OPTIONS="halt_on_error=1"))
+    assert res.returncode == 0 and res.stdout.startswith("ok"), res.stdout[-3000:]
+    assert "ThreadSanitizer" not in res.stdout, res.stdout[-3000:]
