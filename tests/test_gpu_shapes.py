@@ -13,6 +13,8 @@ groups) meets the oracle under the bar of its path:
     2e-6 + 1e-5 |ref| of the reference (assert_parity, tensor.rs:104-148);
   * q8_matmul_q8 at n = 1: the n >= 2 arithmetic on one token, same bar.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -22,8 +24,10 @@ from test_gpu_q8 import assert_bits, assert_parity, exact_at
 
 pytestmark = pytest.mark.gpu
 
-SEED = 0x5EED + 0x5A5A
-CASES = 60
+# Q8_SHAPE_CASES / Q8_SHAPE_SEED draw a longer or a different sweep (the
+# committed run: 60 cases from the base seed)
+SEED = 0x5EED + 0x5A5A + int(os.environ.get("Q8_SHAPE_SEED", "0"))
+CASES = int(os.environ.get("Q8_SHAPE_CASES", "60"))
 
 
 def draw(i):
