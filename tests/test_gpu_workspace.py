@@ -147,3 +147,55 @@ def test_decoder_prefill_and_128_steps_allocate_nothing(gpu):
         assert stats["captured"] >= 2 and stats["graphs"] == stats["captured"]
     finally:
         dec.close()
+
+
+def test_decoders_and_contexts_give_back_their_device_memory():
+    """Device memory is returned, not leaked: decoders (weights, caches, graphs,
+    norm vectors) created and destroyed on one context, then whole contexts
+    opened, used and closed.  Read from a context of its own, the device's
+    free memory after the first cycle of each loop (which grows the context's
+    lasting workspaces) stays within a few MiB; a decoder of this size holds
+    about 30 MB, so a leak of any of it per cycle would show."""
+    tol = 16 << 20
+    probe = q8.Gpu(0)
+    try:
+        cfg = dm.config(n_layer=2, n_embd=1024, n_ff=2048, n_head=16, n_head_kv=16, head_dim=64, n_vocab=8000,
+                        capacity=256, max_batch=64)
+        prompt = np.random.default_rng(SEED + 9).integers(0, cfg.n_vocab, 20).astype(np.uint32)
+        host = q8.Gpu(0)
+        try:
+            levels = []
+            for cycle in range(4):
+                dec = dm.Decoder(host, cfg, seed=cycle + 1)
+                dec.forward(prompt)
+                dec.generate(4)  # eager, captured, replayed
+                dec.close()
+                host.sync()
+                levels.append(probe.info()["free_bytes"])
+            print("decoder cycles, free bytes:", levels)
+            assert max(levels[1:]) - min(levels[1:]) < tol, levels
+        finally:
+            host.close()
+        r = np.random.default_rng(SEED + 10)
+        w = q8.Weight(oracle.make_q8_weight(r, 2304, 2304), 2304, 2304)
+        x = oracle.make_activations(r, 64, 2304)
+        levels = []
+        for cycle in range(4):
+            g = q8.Gpu(0)
+            xb, yb = g.alloc(4 * 64 * 2304), g.alloc(4 * 64 * 2304)
+            xb.upload(x)
+            g.matmul(w, xb, 0, 64, yb, 0)
+            g.matmul(w, xb, 0, 1, yb, 0)
+            dec = dm.Decoder(g, cfg, seed=7)
+            dec.forward(prompt)
+            dec.generate(2)
+            dec.close()
+            xb.free()
+            yb.free()
+            g.close()
+            levels.append(probe.info()["free_bytes"])
+        print("context cycles, free bytes:", levels)
+        assert max(levels[1:]) - min(levels[1:]) < tol, levels
+        assert max(levels) - min(levels) < tol, levels  # a closed context keeps nothing
+    finally:
+        probe.close()
