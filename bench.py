@@ -41,7 +41,10 @@ Also reported, each on its own rotation:
                 O 2304 + residual, gate|up 2x5760 -> SiLU -> Q8_0, down
                 2304x5760 + residual) with the activation quantization, on
                 rotating copies of the layer (MALL-cold), int8 TOPS
-                (2*M*N*K) vs the 5.0 POPS dense peak; each piece alone too;
+                (2*M*N*K) vs the 5.0 POPS dense peak, each GEMM announcing
+                the next one's weights (q8_gemm_prefetch) as the decoder's
+                prefill does; the same layer without announcements, and
+                each piece alone, beside it;
   extras        configs[1] n = 8 / 64, configs[2] decode layer set (rotating
                 layer copies) and the 122880 x 2304 lm_head GEMV + argmax;
   decoder       configs[4]: the 42-layer synthetic decoder (hidden 2304, FFN
@@ -370,18 +373,29 @@ def bench_layer_n512(gpu, steps, warmup, rng, n=512):
            "down": 2 * n * HID * FFN}
     total_ops = sum(ops.values())
 
-    def layer_set(i):
-        L = layers[i]
-        p = gpu.prepare(xb, 0, n, HID)
-        gpu.matmul_prompt_group([(L["q"], qkv, 0), (L["k"], qkv, n * HID), (L["v"], qkv, 2 * n * HID)], p, n, HID)
-        gpu.matmul(L["o"], qkv, 0, n, hb, 0, bias=hb)                  # O with its residual
-        pd = gpu.gate_up_silu(L["gate"], L["up"], hb, 0, n, act, 0, want_prepared=True)
-        gpu.matmul(L["down"], act, 0, n, hb, 0, prepared=pd, bias=hb)  # down with its residual
+    def make_layer_set(announce):
+        def layer_set(i):
+            L, N = layers[i], layers[(i + 1) % copies]
+            hint = gpu.gemm_prefetch if announce else (lambda ws: None)
+            p = gpu.prepare(xb, 0, n, HID)
+            hint([L["o"]])  # read by the next GEMM launch's cache riders
+            gpu.matmul_prompt_group([(L["q"], qkv, 0), (L["k"], qkv, n * HID), (L["v"], qkv, 2 * n * HID)], p, n,
+                                    HID)
+            hint([L["gate"], L["up"]])
+            gpu.matmul(L["o"], qkv, 0, n, hb, 0, bias=hb)                  # O with its residual
+            hint([L["down"]])
+            pd = gpu.gate_up_silu(L["gate"], L["up"], hb, 0, n, act, 0, want_prepared=True)
+            hint([N["q"], N["k"], N["v"]])                                 # the next layer's
+            gpu.matmul(L["down"], act, 0, n, hb, 0, prepared=pd, bias=hb)  # down with its residual
+        return layer_set
 
-    ms = rotating_trials(gpu, layer_set, copies, max(steps // 4, copies), warmup)
+    ms = rotating_trials(gpu, make_layer_set(True), copies, max(steps // 4, copies), warmup)
     s = summary(ms, total_ops, 1e-12)
     log(f"n={n} layer set (MALL-cold, {copies} layer copies): {s['median_us']:.1f} us, {s['value']:.1f} TOPS "
         f"({s['value'] / INT8_PEAK_TOPS * 100:.1f}% of int8 peak); trials {s['trials']}")
+    ms_plain = rotating_trials(gpu, make_layer_set(False), copies, max(steps // 4, copies), warmup)
+    plain_us = statistics.median(ms_plain) * 1e3
+    log(f"n={n} layer set without weight announcements: {plain_us:.1f} us")
 
     # each piece alone on the same rotation; prepared operands copied into
     # buffers of our own (a Prepared views the one activation workspace)
@@ -429,6 +443,7 @@ def bench_layer_n512(gpu, steps, warmup, rng, n=512):
     for b in (xb, hb, qkv, act, gu, pbuf, pfbuf):
         b.free()
     return {"us": s["median_us"], "tops": s["value"], "trials_tops": s["trials"], "ops": total_ops,
+            "us_unannounced": round(plain_us, 2),
             "frac": s["value"] / INT8_PEAK_TOPS, "ops_by_projection": ops, "copies": copies,
             "quantize_us": piece_us["quantize_x"], "projections_us": piece_us, "projections_tops": piece_tops,
             "projections_mall": piece_mall, "projections_traffic_bound": bound}
@@ -772,6 +787,7 @@ def main():
         "gemm_n512": {"value": r(gemm["tops"], 2), "unit": "TOPS", "peak": INT8_PEAK_TOPS,
                       "frac": round(gemm["frac"], 4) if gemm["frac"] is not None else None,
                       "us_per_layer": r(gemm["us"], 2), "ops_per_layer": gemm["ops"],
+                      "us_per_layer_unannounced": gemm.get("us_unannounced"),
                       "mall": f"cold ({gemm.get('copies')} rotating layer copies)",
                       "trials_tops": gemm.get("trials_tops"),
                       "mfma_ceiling_tops": ceil.get("mfma_i8_tops"),

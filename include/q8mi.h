@@ -333,6 +333,18 @@ int q8_gate_up_silu(q8_ctx *ctx, const q8_weight *gate, const q8_weight *up, q8_
 int q8_gate_up_silu_prepared(q8_ctx *ctx, const q8_weight *gate, const q8_weight *up, const q8_prepared *x,
                              q8_prepared *out);
 
+/* Announces up to four resident weights that a later GEMM will read: the
+ * next launch of the int8 GEMM or the fused gate/up GEMM on this context
+ * (any entry point at n >= 2) appends cache riders to its grid, workgroups
+ * that only read these weights' device bytes once so that they sit in the
+ * Infinity Cache when their own GEMM runs.  That launch consumes the
+ * announcement; count = 0 withdraws it, and releasing an announced weight
+ * removes it.  Results never change.  No counterpart in the reference: its
+ * prefill GEMMs read MALL-cold weights as they come.  Meant for a caller that
+ * knows its next projection, such as a layer's prefill (q8_decoder_forward's
+ * prompt pass announces each next projection). */
+int q8_gemm_prefetch(q8_ctx *ctx, const q8_weight *const *weights, int count);
+
 /* lm_head GEMV on the last normed row plus the greedy argmax on the device:
  * model.rs:806-832 + sampler.rs:167-175.  Writes the logits and returns the
  * first index of the strictly greatest logit in *argmax (waits for it). */

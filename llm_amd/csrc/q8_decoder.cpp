@@ -154,7 +154,15 @@ int q8_decoder::body(int n, int splits) {
     const int E = g.n_embd;
     const float scale = 1.0f / std::sqrt((float)g.head_dim);
     DEC_TRY(q8_embeddings_device(c, embd, tokens, (size_t)n, x, 0));
-    for (Layer &L : layers) {
+    // A prompt's GEMMs are compute-bound and leave HBM mostly idle, so each
+    // announces the weights of the GEMM after it (q8_gemm_prefetch), whose
+    // launch then finds them in the Infinity Cache instead of HBM.
+    auto announce = [&](const q8_weight *a, const q8_weight *b = nullptr, const q8_weight *d = nullptr) {
+        const q8_weight *w[3] = {a, b, d};
+        return q8_gemm_prefetch(c, w, d ? 3 : b ? 2 : 1);
+    };
+    for (size_t li = 0; li < layers.size(); li++) {
+        Layer &L = layers[li];
         // attention block (dense_attention, model.rs:869-1043)
         if (n == 1) {  // norm, q/k/v and rope + KV append in one launch
             DEC_TRY(q8_norm_qkv_rope(c, L.attn_norm.data(), g.eps, L.w[Q8_DEC_Q], L.w[Q8_DEC_K], L.w[Q8_DEC_V], x, 0,
@@ -163,6 +171,7 @@ int q8_decoder::body(int n, int splits) {
         } else {
             q8_prepared p{};
             DEC_TRY(q8_norm_prepare(c, x, 0, L.attn_norm.data(), E, g.eps, n, &p));
+            DEC_TRY(announce(L.w[Q8_DEC_O]));
             DEC_TRY(q8_prompt_qkv_rope(c, L.w[Q8_DEC_Q], L.w[Q8_DEC_K], L.w[Q8_DEC_V], &p, n, q, 0, L.kcache,
                                        L.vcache, g.n_head, g.n_head_kv, g.head_dim, g.n_rot, g.rope_base,
                                        g.capacity, pos));
@@ -174,6 +183,7 @@ int q8_decoder::body(int n, int splits) {
             q8_prepared pa{};
             DEC_TRY(q8_attention_prepare(c, q, 0, L.kcache, L.vcache, n, g.n_head, g.n_head_kv, g.head_dim,
                                          g.capacity, scale, pos, &pa));
+            DEC_TRY(announce(L.w[Q8_DEC_GATE], L.w[Q8_DEC_UP]));
             DEC_TRY(q8_matmul(c, L.w[Q8_DEC_O], 0, 0, n, x, 0, &pa, x, 0));
         }
         // feed-forward block (feed_forward, model.rs:1162-1235)
@@ -184,7 +194,12 @@ int q8_decoder::body(int n, int splits) {
             q8_prepared p{};
             DEC_TRY(q8_norm_prepare(c, x, 0, L.ffn_norm.data(), E, g.eps, n, &p));
             q8_prepared pd{};
+            DEC_TRY(announce(L.w[Q8_DEC_DOWN]));
             DEC_TRY(q8_gate_up_silu_prepared(c, L.w[Q8_DEC_GATE], L.w[Q8_DEC_UP], &p, &pd));
+            if (li + 1 < layers.size()) {
+                const Layer &N = layers[li + 1];
+                DEC_TRY(announce(N.w[Q8_DEC_Q], N.w[Q8_DEC_K], N.w[Q8_DEC_V]));
+            }
             DEC_TRY(q8_matmul(c, L.w[Q8_DEC_DOWN], act, 0, n, x, 0, &pd, x, 0));
         }
     }

@@ -1766,6 +1766,58 @@ static __device__ __forceinline__ void store_tiles(const Q8GemmArgs &a, const Q8
 // in LDS in a fixed order, and optional K slices across workgroups by the
 // last workgroup to arrive.
 // ---------------------------------------------------------------------------
+// A cache rider (Q8GemmArgs::riders): rider workgroup `rider` of `riders`
+// reads its share of the rider weights' quants and scales, taken as one
+// sequence of 16-byte chunks (weight 0's quants, its scales, weight 1's ...),
+// in address order and in batches of 16 loads a lane, and keeps nothing: the
+// reads only leave the weights in the L2 and the Infinity Cache.
+static __device__ __forceinline__ void gemm_rider(const Q8GemmArgs &a, int rider) {
+    constexpr int BATCH = 16;
+    const int nt = blockDim.x;
+    const int t = threadIdx.x;
+    constexpr long long UNIT_CHUNKS = (Q8_UNIT_BYTES + Q8_TILE_ROWS * 2) / 16;
+    long long chunks = 0;
+    for (int i = 0; i < a.rider_count; i++) chunks += (long long)a.rider_units[i] * UNIT_CHUNKS;
+    const long long per = (chunks + a.riders - 1) / a.riders;
+    const long long c0 = (long long)rider * per;
+    const long long c1 = min(chunks, c0 + per);
+    long long off = 0;
+    for (int i = 0; i < 2 * a.rider_count; i++) {
+        const uint8_t *base = (i & 1) ? reinterpret_cast<const uint8_t *>(a.rider_s[i >> 1]) : a.rider_q[i >> 1];
+        const long long len = (long long)a.rider_units[i >> 1] * ((i & 1) ? Q8_TILE_ROWS * 2 : Q8_UNIT_BYTES) / 16;
+        const long long lo = max(c0, off) - off, hi = min(c1, off + len) - off;
+        for (long long c = lo; c < hi; c += (long long)nt * BATCH) {
+            i32x4 v[BATCH];
+#pragma unroll
+            for (int j = 0; j < BATCH; j++) {
+                const i32x4 *p = reinterpret_cast<const i32x4 *>(base) + min(c + t + (long long)nt * j, hi - 1);
+                v[j] = a.rider_nt ? __builtin_nontemporal_load(p) : *p;
+            }
+#pragma unroll
+            for (int j = 0; j < BATCH; j++) asm volatile("" ::"v"(v[j]));
+        }
+        off += len;
+    }
+}
+
+// The compute workgroup of grid workgroup `b`, or -1 for a cache rider (which
+// it has then run).
+static __device__ __forceinline__ int gemm_workgroup(const Q8GemmArgs &a, int b) {
+    if (a.riders) {
+        const int r = a.rider_first ? b : b - a.nwg;
+        if (r >= 0 && r < a.riders) {
+            gemm_rider(a, r);
+            return -1;
+        }
+        if (a.rider_first) b -= a.riders;
+    }
+    if (a.xcd_remap) {
+        const int per = a.nwg >> 3;
+        b = (b & 7) * per + (b >> 3);
+    }
+    return b;
+}
+
 template <int TPW>
 struct GemmOps {
     i32x4 w0, w1;
@@ -1789,11 +1841,8 @@ static __device__ __forceinline__ void gemm_body(const Q8GemmArgs &a) {
     const int tw = wave % TW;  // token-tile group of this wave
     const int kw = wave / TW;  // K-split wave
     const int S = a.kslices;
-    int wg = blockIdx.x;
-    if (a.xcd_remap) {
-        const int per = a.nwg >> 3;
-        wg = (wg & 7) * per + (wg >> 3);
-    }
+    const int wg = gemm_workgroup(a, blockIdx.x);
+    if (wg < 0) return;
     // workgroup -> (row tile, token group, K slice); slices of one tile are adjacent
     const int slice = wg % S;
     const int rtg = wg / S;
@@ -2050,11 +2099,8 @@ extern "C" __global__ __launch_bounds__(512) void q8_gemm_silu(Q8GemmArgs a) {
     const int lane = threadIdx.x & 63;
     const int kw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int KW = blockDim.x >> 6;
-    int wg = blockIdx.x;
-    if (a.xcd_remap) {
-        const int per = a.nwg >> 3;
-        wg = (wg & 7) * per + (wg >> 3);
-    }
+    const int wg = gemm_workgroup(a, blockIdx.x);
+    if (wg < 0) return;
     const int g = wg / a.ttiles;   // gate (and up) row tile = output feature block
     const int tt = wg - g * a.ttiles;
     const Q8GemmMember gm = a.m[0], um = a.m[1];

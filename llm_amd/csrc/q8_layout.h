@@ -57,6 +57,7 @@
 /* The int8-MFMA variant of the staged GEMM (q8_gemm_l): int8 activation units. */
 #define Q8_GEMM_L_BUF_BYTES(tpw, rw) Q8_GEMM_STAGED_BUF_BYTES(tpw, rw, Q8_UNIT_BYTES)
 #define Q8_GROUP_MAX 4 /* apps/engine/src/cuda/mod.rs:63 MMA_GROUP_MAX */
+#define Q8_RIDER_MAX 4 /* weights one GEMM launch's cache riders read */
 
 /* Q8_J[h][t]: the AVX2 lane held by dword t of half h. */
 #define Q8_J_INIT {{0, 4, 1, 5}, {2, 6, 3, 7}}
@@ -211,6 +212,19 @@ typedef struct {
     uint16_t *kcache;
     uint16_t *vcache;
     int head_dim, n_rot, capacity;
+    /* Cache riders (q8_gemm_s* and q8_gemm_silu): `riders` extra workgroups
+     * (a multiple of 8) that only read the weights in rider_q / rider_s once,
+     * in address order, and exit, so the weights sit in the L2 and the
+     * Infinity Cache when compute waves read them.  rider_first: the riders
+     * are the grid's first workgroups (compute workgroup w is riders + w),
+     * else its last (w is w).  rider_nt: non-temporal reads. */
+    int riders;
+    int rider_first;
+    int rider_nt;
+    int rider_count;                         /* weights in rider_q / rider_s */
+    const uint8_t *rider_q[Q8_RIDER_MAX];    /* quants of a resident weight */
+    const uint16_t *rider_s[Q8_RIDER_MAX];   /* its scales */
+    unsigned rider_units[Q8_RIDER_MAX];      /* row tiles x blocks of it */
 } Q8GemmArgs;
 
 typedef struct {

@@ -235,6 +235,7 @@ struct q8_ctx {
     size_t max_lds = 0;
     char name[256] = {};
     std::map<std::string, int> options;
+    std::vector<const q8_weight *> next_weights;  // q8_gemm_prefetch: read by the next GEMM's riders
 };
 
 namespace {
@@ -704,6 +705,39 @@ int run_norm_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, int s
 int run_gemm_h(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n, const float *bias,
                const GemvRope *rope = nullptr);
 
+// Cache riders of a GEMM launch (Q8GemmArgs::riders).  With weights
+// announced by q8_gemm_prefetch, the riders read those (and the announcement
+// is consumed); otherwise, with option gemm.riders > 0, the launch's own
+// members.  Counts are rounded down to a multiple of 8 so every compute
+// workgroup keeps its XCD.
+void set_riders(q8_ctx *c, Q8GemmArgs &a, const q8_weight *const *own, int own_count, int threads) {
+    a.riders = 0;
+    a.rider_count = 0;
+    const bool next = !c->next_weights.empty();
+    const q8_weight *const *w = next ? c->next_weights.data() : own;
+    const int count = next ? (int)c->next_weights.size() : own_count;
+    size_t bytes = 0;
+    for (int i = 0; i < count && i < Q8_RIDER_MAX; i++) {
+        a.rider_q[i] = w[i]->quants;
+        a.rider_s[i] = w[i]->scales;
+        a.rider_units[i] = (unsigned)((size_t)w[i]->tiles * w[i]->nb);
+        a.rider_count = i + 1;
+        bytes += (size_t)a.rider_units[i] * (Q8_UNIT_BYTES + Q8_TILE_ROWS * 2);
+    }
+    c->next_weights.clear();
+    if (next && !option(c, "gemm.prefetch", 1)) a.rider_count = 0;  // announcements switched off
+    long long riders = next ? option(c, "gemm.next_riders", 0) : option(c, "gemm.riders", 0);
+    if (next && riders == 0) {
+        // a rider wave per gemm.rider_wave_kib KiB of the announced weights
+        const long long per_wave = 1024LL * std::max(1, option(c, "gemm.rider_wave_kib", 32));
+        const long long waves = ceil_div((long long)bytes, per_wave);
+        riders = align_up(ceil_div(waves, std::max(1, threads / 64)), 8);
+    }
+    a.riders = a.rider_count ? (int)(std::min<long long>(std::max<long long>(riders, 0), 4096) & ~7LL) : 0;
+    a.rider_first = option(c, next ? "gemm.next_rider_first" : "gemm.rider_first", next ? 0 : 1) ? 1 : 0;
+    a.rider_nt = option(c, "gemm.rider_nt", 0) ? 1 : 0;
+}
+
 // Gate/up GEMM whose epilogue writes silu(gate) * up as prepared Q8_0
 // (q8_gemm_silu) into the second activation workspace: the input stays
 // readable in the first.  int8 prepared input only.
@@ -743,14 +777,16 @@ int run_gemm_silu(q8_ctx *c, const q8_weight *gate, const q8_weight *up, const q
     kw = (int)ceil_div(npairs, ppw);
     a.pairs_per_wave = ppw;
     const long long nwg = base;
-    if (nwg > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "gemm_silu: grid of %lld workgroups", nwg);
+    if (nwg > 0x7fffffffLL - 4096) return fail(Q8_ERR_UNSUPPORTED, "gemm_silu: grid of %lld workgroups", nwg);
     a.nwg = (int)nwg;
     a.xcd_remap = nwg % 8 == 0 ? 1 : 0;
     a.oq = static_cast<uint8_t *>(c->act2_ws);
     a.os = reinterpret_cast<float *>(static_cast<uint8_t *>(c->act2_ws) + align_up(qbytes, kAlign));
     a.of16 = fmt == Q8_PREPARED_F16 ? 1 : 0;
     const unsigned lds = (unsigned)std::max<size_t>((size_t)(kw - 1) * 2 * 64 * 16 * sizeof(float), 32 * 33 * sizeof(float));
-    Q8_TRY(launch(c, F_GEMM_SILU, (unsigned)nwg, (unsigned)(64 * kw), lds, &a, sizeof a));
+    const q8_weight *own[2] = {gate, up};
+    set_riders(c, a, own, 2, 64 * kw);
+    Q8_TRY(launch(c, F_GEMM_SILU, (unsigned)(nwg + a.riders), (unsigned)(64 * kw), lds, &a, sizeof a));
     out->quants = (q8_dptr)(uintptr_t)a.oq;
     out->scales = (q8_dptr)(uintptr_t)a.os;
     out->n = n;
@@ -826,7 +862,7 @@ int run_gemm(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n,
             return fail(Q8_ERR_UNSUPPORTED, "gemm: split-K needs %zu bytes of scratch", need);
     }
     const long long nwg = groups * a.kslices;
-    if (nwg > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "gemm: grid of %lld workgroups", nwg);
+    if (nwg > 0x7fffffffLL - 4096) return fail(Q8_ERR_UNSUPPORTED, "gemm: grid of %lld workgroups", nwg);
     a.nwg = (int)nwg;
     a.xcd_remap = (t.xcd_remap && nwg % 8 == 0) ? 1 : 0;
     const int threads = 64 * a.twaves * kwaves;
@@ -839,7 +875,12 @@ int run_gemm(q8_ctx *c, const Member *m, int count, const q8_prepared *p, int n,
     // one token tile: every weight byte is read by one wave, once (option
     // gemm.stream = 0 keeps the default cache policy)
     if (f == F_GEMM_S1_T1 && a.ttiles == 1 && option(c, "gemm.stream", 1)) f = F_GEMM_S1_T1S;
-    return launch(c, f, (unsigned)nwg, (unsigned)threads, lds, &a, sizeof a);
+    if (f != F_GEMM_P_T1 && f != F_GEMM_P_T2) {
+        const q8_weight *own[Q8_GROUP_MAX];
+        for (int i = 0; i < count; i++) own[i] = m[i].w;
+        set_riders(c, a, own, count, threads);
+    }
+    return launch(c, f, (unsigned)(nwg + a.riders), (unsigned)threads, lds, &a, sizeof a);
 }
 
 // The staged GEMMs (gemm_h_body): RW row-tile waves x KW K groups per
@@ -1212,7 +1253,9 @@ int q8_set_option(q8_ctx *c, const char *name, int value) {
                                         "gemv.group_loads",
                                         "gemm.smode", "gemm.tpw",    "gemm.twaves",    "gemm.xcd_remap",
                                         "gemm.kwaves", "gemm.slices", "gemm.rwaves",    "gemm.f16",
-                                        "gemm.pipe",  "gemm.lds",      "gemm.silu",      "gemm.small_gemv", "gemm.stream"};
+                                        "gemm.pipe",  "gemm.lds",      "gemm.silu",      "gemm.small_gemv", "gemm.stream",
+                                        "gemm.riders", "gemm.rider_nt", "gemm.rider_first", "gemm.next_riders",
+                                        "gemm.next_rider_first", "gemm.rider_wave_kib", "gemm.prefetch"};
     bool ok = false;
     for (const char *k : known) ok = ok || std::strcmp(k, name) == 0;
     if (!ok) return fail(Q8_ERR_INVALID, "unknown option %s", name);
@@ -1394,6 +1437,15 @@ int q8_download(q8_ctx *c, void *dst, q8_dptr src, size_t bytes) {
     return Q8_OK;
 }
 
+int q8_gemm_prefetch(q8_ctx *c, const q8_weight *const *weights, int count) {
+    if (!c || count < 0 || count > Q8_RIDER_MAX || (count > 0 && !weights))
+        return fail(Q8_ERR_INVALID, "q8_gemm_prefetch: bad arguments (count %d, at most %d)", count, Q8_RIDER_MAX);
+    for (int i = 0; i < count; i++) Q8_TRY(check_weight(c, weights[i]));
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    c->next_weights.assign(weights, weights + count);
+    return Q8_OK;
+}
+
 int q8_sync(q8_ctx *c) {
     if (!c) return fail(Q8_ERR_INVALID, "q8_sync: null context");
     HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
@@ -1463,6 +1515,9 @@ int q8_weight_release(q8_ctx *c, const q8_weight *w) {
     if (!c) return fail(Q8_ERR_INVALID, "q8_weight_release: null context");
     Q8_TRY(check_weight(c, w));
     std::lock_guard<std::recursive_mutex> lock(c->mu);
+    // a pending announcement of this weight (q8_gemm_prefetch) goes with it:
+    // no later launch may read its freed bytes
+    c->next_weights.erase(std::remove(c->next_weights.begin(), c->next_weights.end(), w), c->next_weights.end());
     auto own = std::find(c->owned.begin(), c->owned.end(), w);
     if (own != c->owned.end()) {  // generated on the device
         HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");

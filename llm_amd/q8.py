@@ -48,7 +48,7 @@ EXPORTS = (
     "q8_matmul", "q8_matmul_noalloc", "q8_matmul_q8", "q8_prepare", "q8_silu_mul_prepare", "q8_rmsnorm",
     "q8_norm_prepare", "q8_silu_mul",
     "q8_matmul_decode_group", "q8_matmul_prompt_group", "q8_gate_up_silu", "q8_gate_up_silu_prepared",
-    "q8_lm_head_argmax", "q8_argmax", "q8_copy_device", "q8_embeddings",
+    "q8_gemm_prefetch", "q8_lm_head_argmax", "q8_argmax", "q8_copy_device", "q8_embeddings",
     "q8_kernel_info", "q8_launch_check",
     "q8_plan", "q8_tactic_count", "q8_tactic_row",
     "q8_event_create", "q8_event_record", "q8_event_elapsed_ms", "q8_event_destroy",
@@ -211,6 +211,7 @@ def lib():
         "q8_matmul_prompt_group": (c_int, [vp, ctypes.POINTER(_GroupEntry), c_int, ctypes.POINTER(Prepared),
                                            c_int, c_int, u64, c_size]),
         "q8_gate_up_silu": (c_int, [vp, vp, vp, u64, c_size, c_int, u64, c_size, ctypes.POINTER(Prepared)]),
+        "q8_gemm_prefetch": (c_int, [vp, ctypes.POINTER(vp), c_int]),
         "q8_norm_matmul_decode_group": (c_int, [vp, vp, ctypes.c_float, ctypes.POINTER(_GroupEntry), c_int, u64,
                                                 c_size, c_int]),
         "q8_norm_gate_up_silu": (c_int, [vp, vp, ctypes.c_float, vp, vp, u64, c_size, u64, c_size]),
@@ -558,6 +559,12 @@ class Gpu:
         w = self._norm_weight(weight)
         _check(lib().q8_norm_gate_up_silu(self.handle, w.ctypes.data, float(eps), self.resident(gate),
                                           self.resident(up), x.ptr, x_offset, act.ptr, act_offset))
+
+    def gemm_prefetch(self, weights):
+        """q8_gemm_prefetch: the next n >= 2 GEMM launch reads these weights
+        (at most four) into the device caches beside its own work."""
+        arr = (ctypes.c_void_p * max(1, len(weights)))(*[self.resident(w) for w in weights])
+        _check(lib().q8_gemm_prefetch(self.handle, arr, len(weights)))
 
     def matmul_prompt_group(self, members, prepared: Prepared, n: int, k: int,
                             bias: DeviceBuffer | None = None, bias_offset: int = 0):

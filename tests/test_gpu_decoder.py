@@ -783,6 +783,31 @@ def test_decoder_graph_replays_are_bit_identical(gpu):
         dec.close()
 
 
+def test_prompt_weight_announcements_change_no_bits(gpu):
+    """A prompt pass announces each next projection's weights
+    (q8_gemm_prefetch: cache riders in the launch before); with the
+    announcements switched off (option gemm.prefetch = 0) the prompt's token
+    and logits are the same bits, eagerly and through the captured graph."""
+    prompt = np.arange(1, 41, dtype=np.uint32)
+    runs = []
+    try:
+        for pf in (0, 1):
+            gpu.set_option("gemm.prefetch", pf)
+            dec = dm.Decoder(gpu, small_config(), seed=12)
+            try:
+                for _ in range(3):  # eager, capture + replay, replay
+                    dec.reset()
+                    runs.append((pf, dec.forward(prompt), dec.logits()))
+                assert dec.graph_stats()["captured"] >= 1
+            finally:
+                dec.close()
+    finally:
+        gpu.set_option("gemm.prefetch", -1)
+    for pf, token, logits in runs[1:]:
+        assert token == runs[0][1], f"announcements {pf}: token {token} against {runs[0][1]}"
+        assert_bits(logits, runs[0][2], f"prompt logits, announcements {pf}")
+
+
 def test_decoders_in_turn_on_one_context_agree(gpu):
     """Two decoders with the same seed, one after the other on one context,
     give bit-identical tokens and logits (eager and replayed): the first one's
