@@ -63,6 +63,18 @@ int launch(q8bench *b, Kernel k, unsigned grid, unsigned block, Q8ProbeArgs &a) 
     return Q8_OK;
 }
 
+// A read probe: its arguments one by one, as the kernels declare them.
+int launch_read(q8bench *b, Kernel k, unsigned grid, unsigned block, const uint8_t *src, long long bytes) {
+    if (grid == 0) return Q8_OK;
+    int threads = (int)block;
+    unsigned never = 0x7fc0dead;
+    unsigned *sink = b->sink;
+    void *params[] = {&src, &bytes, &threads, &never, &sink};
+    const hipError_t e = hipModuleLaunchKernel(b->fn[k], grid, 1, 1, block, 1, 1, 0, b->stream, params, nullptr);
+    if (e != hipSuccess) return fail(Q8_ERR_HIP, "hip: launch of %s failed: %s", kNames[k], hipGetErrorString(e));
+    return Q8_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -123,10 +135,8 @@ int q8bench_read(q8bench *b, uint64_t src, size_t bytes, int loads, int nontempo
     const unsigned long long per = (unsigned long long)threads * 16 * loads;
     const unsigned long long grid = (bytes + per - 1) / per;
     if (grid > 0x7fffffffULL) return fail(Q8_ERR_UNSUPPORTED, "q8bench_read: %zu bytes", bytes);
-    Q8ProbeArgs a{};
-    a.src = reinterpret_cast<const uint8_t *>(src);
-    a.bytes = (long long)bytes;
-    return launch(b, static_cast<Kernel>(idx + (nontemporal ? 1 : 0)), (unsigned)grid, (unsigned)threads, a);
+    return launch_read(b, static_cast<Kernel>(idx + (nontemporal ? 1 : 0)), (unsigned)grid, (unsigned)threads,
+                       reinterpret_cast<const uint8_t *>(src), (long long)bytes);
 }
 
 int q8bench_probe(q8bench *b, int which, int iters, int workgroups, int mask) {

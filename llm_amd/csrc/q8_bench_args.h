@@ -9,8 +9,6 @@
 #include <stdint.h>
 
 typedef struct {
-    const uint8_t *src; /* read probes: bytes to stream, 16-byte aligned */
-    long long bytes;    /* a multiple of 16 */
     int iters;          /* compute probes: loop trips per wave */
     int mask;           /* split probes: bit 0 runs waves 0-3 (role A), bit 1 waves 4-7 (role B) */
     unsigned never;     /* a value no result takes: results feed `sink` only when equal to it */

@@ -906,31 +906,45 @@ Q8_GEMV_KERNEL(9, 1, 512)
 // and wave 0 adds the waves' row sums in wave order.  Deterministic, within
 // f32 rounding of the reference's left-to-right sum, and it drops the
 // serial 72-add chain and its LDS round trips from the end of the kernel.
+// The row-slice GEMV's hot values travel as its first kernel arguments, ahead
+// of the argument block: the code object is built with the first 13 argument
+// dwords preloaded into SGPRs at wave launch (gfx950 kernarg preload), so a
+// wave issues its weight loads without first reading the kernarg segment, a
+// scalar-cache miss of ~0.26 us on each CU's first wave (configs[0]: 4.72 ->
+// 4.49 us a launch, same bits).  nbw = nb | waves << 16, tiles_xo =
+// total_tiles | xcd_order << 31.
+struct RsHot {
+    const uint8_t *mq;
+    const uint16_t *msc;
+    float *my;
+    const float *mbias;
+    const float *xg;
+    int mrows, nbw, tiles_xo;
+};
+
 template <int RS, int NL, int CMB = 0, int EX = 1>
-static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
+static __device__ __forceinline__ void gemv_rs_body(const RsHot &hot, const Q8GemvArgs &a) {
     extern __shared__ __attribute__((aligned(16))) float smem[];
     constexpr int LPB = 2 * RS;               // lanes per block
     constexpr int BPL = 64 / LPB;             // blocks per wave load
     constexpr int SPT = Q8_TILE_ROWS / RS;    // slices per tile (power of two)
     constexpr int BPW = NL * BPL;             // blocks per wave
     static_assert(BPW * 8 <= 64 * Q8_GEMV_STAGE, "x range of a wave exceeds its staging registers");
-    const uint8_t *mq = a.m[0].quants;
-    const uint16_t *msc = a.m[0].scales;
-    float *my = a.m[0].y;
-    const float *mbias = a.m[0].bias;
-    const int mrows = a.m[0].rows;
-    const float *xg = a.x;
-    const int nb = a.nb;
-    // the wave count comes from the arguments (the host launches
-    // waves_per_tile waves), read here with the rest: blockDim lives in the
-    // dispatch packet's hidden arguments, a cache line no earlier read
-    // fetched, and read after the barrier it cost every workgroup a scalar
-    // miss at its end (~0.04 us of a configs[0] GEMV)
-    const int nw = a.waves_per_tile;
-    asm volatile("" ::"s"(mq), "s"(msc), "s"(my), "s"(mbias), "s"(mrows), "s"(xg), "s"(nb), "s"(a.xcd_order),
-                 "s"(a.total_tiles), "s"(nw));
-    // the combine's partials in the same kernel-argument read: a second read
-    // would wait ahead of the first partial and weight loads
+    const uint8_t *mq = hot.mq;
+    const uint16_t *msc = hot.msc;
+    float *my = hot.my;
+    const float *mbias = hot.mbias;
+    const int mrows = hot.mrows;
+    const float *xg = hot.xg;
+    const int nb = hot.nbw & 0xffff;
+    // the wave count comes from the arguments (the host launches that many
+    // waves), not blockDim: blockDim lives in the dispatch packet, a cache
+    // line nothing else reads
+    const int nw = hot.nbw >> 16;
+    const int total_tiles = hot.tiles_xo & 0x7fffffff;
+    const int xo = (int)((unsigned)hot.tiles_xo >> 31);
+    // the combine's partials come from the argument block, read at once: a
+    // second read would wait ahead of the first partial and weight loads
     if constexpr (CMB) asm volatile("" ::"s"(a.attn_acc), "s"(a.attn_ms), "s"(a.attn_splits));
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -942,10 +956,9 @@ static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
     // slices share one L2 (the 64-byte scale runs of a tile's blocks are
     // fetched once, not once per XCD).
     const int bx = blockIdx.x;
-    const int xo = a.xcd_order;
     const int tile = xo ? (bx / (8 * SPT)) * 8 + (bx & 7) : bx / SPT;
     const int slice = xo ? (bx >> 3) % SPT : bx % SPT;
-    if (tile >= a.total_tiles) return;  // padding of the XCD order, whole workgroup
+    if (tile >= total_tiles) return;  // padding of the XCD order, whole workgroup
     const int srow = slice * RS + r;  // row within the tile
     const int b_begin = wave * BPW;
     const int b_end = min(nb, b_begin + BPW);
@@ -1071,18 +1084,22 @@ static __device__ __forceinline__ void gemv_rs_body(const Q8GemvArgs &a) {
     if (row < mrows) my[row] = mbias ? acc + mbias[row] : acc;
 }
 
+#define Q8_RS_PARAMS                                                                                  \
+    const uint8_t *mq, const uint16_t *msc, float *my, const float *mbias, const float *xg, int mrows, \
+        int nbw, int tiles_xo, Q8GemvArgs a
+#define Q8_RS_HOT RsHot{mq, msc, my, mbias, xg, mrows, nbw, tiles_xo}
 #define Q8_GEMV_RS_KERNEL(RS, NL)                                                                      \
-    extern "C" __global__ __launch_bounds__(1024) void q8_gemv_r##RS##_l##NL(Q8GemvArgs a) {  \
-        gemv_rs_body<RS, NL>(a);                                                                       \
+    extern "C" __global__ __launch_bounds__(1024) void q8_gemv_r##RS##_l##NL(Q8_RS_PARAMS) {        \
+        gemv_rs_body<RS, NL>(Q8_RS_HOT, a);                                                            \
     }                                                                                                  \
-    extern "C" __global__ __launch_bounds__(1024) void q8_gemv_rc##RS##_l##NL(Q8GemvArgs a) { \
-        gemv_rs_body<RS, NL, 1>(a);                                                                    \
+    extern "C" __global__ __launch_bounds__(1024) void q8_gemv_rc##RS##_l##NL(Q8_RS_PARAMS) {       \
+        gemv_rs_body<RS, NL, 1>(Q8_RS_HOT, a);                                                         \
     }                                                                                                  \
-    extern "C" __global__ __launch_bounds__(1024) void q8_gemv_r##RS##_l##NL##_e0(Q8GemvArgs a) { \
-        gemv_rs_body<RS, NL, 0, 0>(a);                                                                 \
+    extern "C" __global__ __launch_bounds__(1024) void q8_gemv_r##RS##_l##NL##_e0(Q8_RS_PARAMS) {   \
+        gemv_rs_body<RS, NL, 0, 0>(Q8_RS_HOT, a);                                                      \
     }                                                                                                  \
-    extern "C" __global__ __launch_bounds__(1024) void q8_gemv_rc##RS##_l##NL##_e0(Q8GemvArgs a) { \
-        gemv_rs_body<RS, NL, 1, 0>(a);                                                                 \
+    extern "C" __global__ __launch_bounds__(1024) void q8_gemv_rc##RS##_l##NL##_e0(Q8_RS_PARAMS) {  \
+        gemv_rs_body<RS, NL, 1, 0>(Q8_RS_HOT, a);                                                      \
     }
 Q8_GEMV_RS_KERNEL(8, 2)
 Q8_GEMV_RS_KERNEL(8, 3)

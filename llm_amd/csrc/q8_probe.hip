@@ -44,29 +44,35 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x32 __attribute__((ext_vector_type(32)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
+// The read probes take their arguments as scalars, preloaded into SGPRs at
+// wave launch (the code object is built with kernarg preload), and the
+// workgroup size as an argument rather than from the dispatch packet: a wave
+// issues its loads without a scalar-cache miss first, as the row-slice GEMVs
+// they are the ceiling of do.
 template <int L, bool NT>
-static __device__ __forceinline__ void probe_read(const Q8ProbeArgs &a) {
-    const int threads = blockDim.x;
+static __device__ __forceinline__ void probe_read(const uint8_t *src, long long bytes, int threads, unsigned never,
+                                                  unsigned *sink) {
     const long long base = (long long)blockIdx.x * threads * 16 * L + threadIdx.x * 16;
     i32x4 v[L];
 #pragma unroll
     for (int i = 0; i < L; i++) {
-        const long long off = min(base + (long long)i * threads * 16, a.bytes - 16);
-        const i32x4 *p = (const i32x4 *)(a.src + off);
+        const long long off = min(base + (long long)i * threads * 16, bytes - 16);
+        const i32x4 *p = (const i32x4 *)(src + off);
         v[i] = NT ? __builtin_nontemporal_load(p) : *p;
     }
     unsigned acc = 0;
 #pragma unroll
     for (int i = 0; i < L; i++) acc ^= (unsigned)(v[i].x ^ v[i].y ^ v[i].z ^ v[i].w);
-    if (acc == a.never) a.sink[0] = acc;
+    if (acc == never) sink[0] = acc;
 }
 
+#define Q8_PROBE_READ_PARAMS const uint8_t *src, long long bytes, int threads, unsigned never, unsigned *sink
 #define Q8_PROBE_READ(L)                                                                                    \
-    extern "C" __global__ __launch_bounds__(1024) void q8_probe_read_l##L(Q8ProbeArgs a) {                \
-        probe_read<L, false>(a);                                                                           \
+    extern "C" __global__ __launch_bounds__(1024) void q8_probe_read_l##L(Q8_PROBE_READ_PARAMS) {         \
+        probe_read<L, false>(src, bytes, threads, never, sink);                                            \
     }                                                                                                      \
-    extern "C" __global__ __launch_bounds__(1024) void q8_probe_read_l##L##_nt(Q8ProbeArgs a) {           \
-        probe_read<L, true>(a);                                                                            \
+    extern "C" __global__ __launch_bounds__(1024) void q8_probe_read_l##L##_nt(Q8_PROBE_READ_PARAMS) {    \
+        probe_read<L, true>(src, bytes, threads, never, sink);                                             \
     }
 Q8_PROBE_READ(2)
 Q8_PROBE_READ(4)

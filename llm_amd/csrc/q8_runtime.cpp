@@ -261,10 +261,33 @@ int option(q8_ctx *c, const char *name, int fallback) {
     return (it == c->options.end() || it->second < 0) ? fallback : it->second;
 }
 
+// The row-slice GEMVs' leading scalar arguments, in the kernels' parameter
+// order (the RsHot the kernels rebuild from them), then the argument block at
+// the next 8-byte boundary: the kernel's explicit arguments span
+// sizeof(RsHead) + sizeof(Q8GemvArgs).
+struct RsHead {
+    const uint8_t *mq;
+    const uint16_t *msc;
+    float *my;
+    const float *mbias;
+    const float *xg;
+    int mrows, nbw, tiles_xo;
+};
+static_assert(sizeof(RsHead) == 56, "row-slice head: five pointers and three ints, padded to 8 bytes");
+
+int launch_rs(q8_ctx *c, Fn f, unsigned grid, unsigned block, unsigned lds, RsHead &h, Q8GemvArgs &a) {
+    if (grid == 0) return Q8_OK;
+    Q8_TRY(check_launch(*c->meta[f], sizeof(RsHead) + sizeof(Q8GemvArgs), block, lds, c->max_lds));
+    void *params[] = {&h.mq, &h.msc, &h.my, &h.mbias, &h.xg, &h.mrows, &h.nbw, &h.tiles_xo, &a};
+    HIP_TRY(hipModuleLaunchKernel(c->fn[f], grid, 1, 1, block, 1, 1, lds, c->stream, params, nullptr),
+            kFnNames[f]);
+    return Q8_OK;
+}
+
 int launch(q8_ctx *c, Fn f, unsigned grid, unsigned block, unsigned lds, void *args, size_t args_size) {
     if (grid == 0) return Q8_OK;
     Q8_TRY(check_launch(*c->meta[f], args_size, block, lds, c->max_lds));
-    void *params[] = {args};  // every kernel takes one argument block by value
+    void *params[] = {args};  // every other kernel takes one argument block by value
     HIP_TRY(hipModuleLaunchKernel(c->fn[f], grid, 1, 1, block, 1, 1, lds, c->stream, params, nullptr),
             kFnNames[f]);
     return Q8_OK;
@@ -499,7 +522,10 @@ int run_gemv_rs(q8_ctx *c, const q8_weight *w, float *y, q8_dptr x, const float 
         const int fi = (rs == 8 ? 0 : 2) + (nl == 3 ? 0 : 1);
         f = (Fn)((exact ? (comb ? F_GEMV_RC8_3 : F_GEMV_R8_3) : (comb ? F_GEMV_RC8_3_E0 : F_GEMV_R8_3_E0)) + fi);
     }
-    return launch(c, f, (unsigned)grid, (unsigned)(waves * 64), lds, &a, sizeof a);
+    if (nb > 0xffff || w->tiles > 0x7fffffff) return fail(Q8_ERR_UNSUPPORTED, "gemv: %d blocks a row", nb);
+    RsHead h{a.m[0].quants, a.m[0].scales, a.m[0].y, a.m[0].bias, a.x, a.m[0].rows, nb | (waves << 16),
+             (int)((unsigned)w->tiles | ((unsigned)a.xcd_order << 31))};
+    return launch_rs(c, f, (unsigned)grid, (unsigned)(waves * 64), lds, h, a);
 }
 
 // Row-slice shape of a multi-matrix decode launch (q8_gemv_g* for a group,
