@@ -80,6 +80,22 @@ static __device__ __forceinline__ float silu_f32(float v) {
 // ---------------------------------------------------------------------------
 // Repack: GGUF Q8_0 rows <-> tile layout.  One thread per (row slot, block).
 // ---------------------------------------------------------------------------
+// Slice-major copy of repacked quants (Q8SliceArgs): one thread per 16-byte
+// piece of the unit layout, read in order and written to its slice's run.
+extern "C" __global__ __launch_bounds__(256) void q8_slice_copy(Q8SliceArgs a) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long total = (long long)a.tiles * a.nb * 64;
+    if (i >= total) return;
+    const int lane = (int)(i & 63);           // 16-byte slot of its unit: 32 h + r
+    const long long unit = i >> 6;            // g * nb + b
+    const int b = (int)(unit % a.nb);
+    const long long g = unit / a.nb;
+    const int h = lane >> 5, r = lane & 31;
+    const int s = r / a.rs, rr = r % a.rs;
+    const long long dst = ((g * (Q8_TILE_ROWS / a.rs) + s) * a.nb + b) * (a.rs * 32) + (a.rs * h + rr) * 16;
+    *reinterpret_cast<i32x4 *>(a.dst + dst) = *reinterpret_cast<const i32x4 *>(a.src + i * 16);
+}
+
 extern "C" __global__ __launch_bounds__(256) void q8_repack(Q8RepackArgs a) {
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;  // < 2^31: the host checks
     const int nb = a.nb;
@@ -912,7 +928,8 @@ Q8_GEMV_KERNEL(9, 1, 512)
 // wave issues its weight loads without first reading the kernarg segment, a
 // scalar-cache miss of ~0.26 us on each CU's first wave (configs[0]: 4.72 ->
 // 4.49 us a launch, same bits).  nbw = nb | waves << 16, tiles_xo =
-// total_tiles | xcd_order << 31.
+// total_tiles | slice_major << 30 | xcd_order << 31; with slice_major, mq is
+// the weight's slice-major copy (Q8SliceArgs) and a wave load reads one run.
 struct RsHot {
     const uint8_t *mq;
     const uint16_t *msc;
@@ -941,7 +958,8 @@ static __device__ __forceinline__ void gemv_rs_body(const RsHot &hot, const Q8Ge
     // waves), not blockDim: blockDim lives in the dispatch packet, a cache
     // line nothing else reads
     const int nw = hot.nbw >> 16;
-    const int total_tiles = hot.tiles_xo & 0x7fffffff;
+    const int total_tiles = hot.tiles_xo & 0x3fffffff;
+    const bool slice_major = (hot.tiles_xo >> 30) & 1;
     const int xo = (int)((unsigned)hot.tiles_xo >> 31);
     // the combine's partials come from the argument block, read at once: a
     // second read would wait ahead of the first partial and weight loads
@@ -963,7 +981,12 @@ static __device__ __forceinline__ void gemv_rs_body(const RsHot &hot, const Q8Ge
     const int b_begin = wave * BPW;
     const int b_end = min(nb, b_begin + BPW);
     const int b_last = max(b_end - 1, 0);
-    const uint8_t *qbase = mq + (size_t)tile * nb * Q8_UNIT_BYTES + 16 * (32 * h + srow);
+    // unit layout: the lane's 16 bytes of each 1 KB unit, 1 KB a block;
+    // slice-major: lane % LPB = RS h + r of the slice's run, RS * 32 bytes a block
+    const uint8_t *qbase = slice_major
+                               ? mq + ((size_t)tile * SPT + slice) * nb * (RS * 32) + 16 * (lane % LPB)
+                               : mq + (size_t)tile * nb * Q8_UNIT_BYTES + 16 * (32 * h + srow);
+    const size_t qstride = slice_major ? (size_t)(RS * 32) : (size_t)Q8_UNIT_BYTES;
     const uint16_t *sbase = msc + (size_t)tile * nb * Q8_TILE_ROWS + srow;
     const int vrow = Q8_GEMV_VROW(nb);
     float *xs = smem;             // nb * 32 floats, permuted
@@ -1006,7 +1029,7 @@ static __device__ __forceinline__ void gemv_rs_body(const RsHot &hot, const Q8Ge
 #pragma unroll
     for (int i = 0; i < NL; i++) {
         const int b = min(b_begin + i * BPL + j, b_last);
-        qv[i] = q8_weight_load(qbase + (size_t)b * Q8_UNIT_BYTES);
+        qv[i] = q8_weight_load(qbase + (size_t)b * qstride);
         dd[i] = (unsigned)sbase[(size_t)b * Q8_TILE_ROWS];
     }
     __builtin_amdgcn_sched_barrier(0);

@@ -87,6 +87,23 @@ typedef struct {
     int inverse; /* 0: GGUF -> tile layout; 1: tile layout -> GGUF (test hook) */
 } Q8RepackArgs;
 
+/* Slice-major copy of a weight's quants, for the row-slice GEMVs: where a
+ * weight's one-token GEMV runs in slices of RS = 8 or 16 rows, its quants are
+ * also kept with each slice's bytes contiguous, so one 64-lane load reads
+ * 1 KB in a single run:
+ *   slice (g, s) of tile g, rows 32g + RS s .. + RS - 1, at
+ *     slices + (g * (32 / RS) + s) * nb * RS * 32;
+ *   block b of it at + b * RS * 32, row r' of half h at + (RS * h + r') * 16,
+ * the 16 bytes the unit layout holds at unit(g, b) + 16 * (32 h + RS s + r').
+ * Scales stay in the unit layout's plane. */
+typedef struct {
+    const uint8_t *src; /* unit-layout quants, tiles * nb units */
+    uint8_t *dst;       /* slice-major copy, the same byte count */
+    int nb;
+    int tiles;
+    int rs;             /* rows per slice: 8 or 16 */
+} Q8SliceArgs;
+
 typedef struct {
     const uint8_t *quants;   /* resident weight, tile layout */
     const uint16_t *scales;

@@ -93,6 +93,7 @@ enum Fn {
     F_COPY,
     F_EMBED,
     F_ROPE, F_ATTN_DECODE, F_ATTN_DECODE_W4, F_ATTN_PREFILL, F_SYNTH, F_ADVANCE,
+    F_SLICE_COPY,
     F_COUNT
 };
 
@@ -127,6 +128,7 @@ const char *const kFnNames[F_COUNT] = {
     "q8_copy",
     "q8_embed",
     "q8_rope_append", "q8_attn_decode", "q8_attn_decode_w4", "q8_attn_prefill", "q8_synth", "q8_advance",
+    "q8_slice_copy",
 };
 
 // Every kernel of the code object with its metadata (q8_manifest.h, from the
@@ -189,6 +191,8 @@ struct q8_weight {
     size_t device_bytes;
     uintptr_t id_ptr;
     size_t id_len;
+    uint8_t *slices = nullptr;  // slice-major copy of the quants (Q8SliceArgs), or none
+    int slice_rows = 0;         // its rows per slice: 8 or 16
 };
 
 struct q8_ctx {
@@ -522,9 +526,13 @@ int run_gemv_rs(q8_ctx *c, const q8_weight *w, float *y, q8_dptr x, const float 
         const int fi = (rs == 8 ? 0 : 2) + (nl == 3 ? 0 : 1);
         f = (Fn)((exact ? (comb ? F_GEMV_RC8_3 : F_GEMV_R8_3) : (comb ? F_GEMV_RC8_3_E0 : F_GEMV_R8_3_E0)) + fi);
     }
-    if (nb > 0xffff || w->tiles > 0x7fffffff) return fail(Q8_ERR_UNSUPPORTED, "gemv: %d blocks a row", nb);
-    RsHead h{a.m[0].quants, a.m[0].scales, a.m[0].y, a.m[0].bias, a.x, a.m[0].rows, nb | (waves << 16),
-             (int)((unsigned)w->tiles | ((unsigned)a.xcd_order << 31))};
+    if (nb > 0xffff || w->tiles > 0x3fffffff) return fail(Q8_ERR_UNSUPPORTED, "gemv: %d blocks a row", nb);
+    // the weight's slice-major copy where it has one for these slices
+    // (option gemv.slice_copy = 0 reads the unit layout instead)
+    const bool sm = w->slices && w->slice_rows == rs && option(c, "gemv.slice_copy", 1);
+    RsHead h{sm ? w->slices : a.m[0].quants, a.m[0].scales, a.m[0].y, a.m[0].bias, a.x, a.m[0].rows,
+             nb | (waves << 16),
+             (int)((unsigned)w->tiles | ((unsigned)sm << 30) | ((unsigned)a.xcd_order << 31))};
     return launch_rs(c, f, (unsigned)grid, (unsigned)(waves * 64), lds, h, a);
 }
 
@@ -1281,7 +1289,8 @@ int q8_set_option(q8_ctx *c, const char *name, int value) {
                                         "gemm.kwaves", "gemm.slices", "gemm.rwaves",    "gemm.f16",
                                         "gemm.pipe",  "gemm.lds",      "gemm.silu",      "gemm.small_gemv", "gemm.stream",
                                         "gemm.riders", "gemm.rider_nt", "gemm.rider_first", "gemm.next_riders",
-                                        "gemm.next_rider_first", "gemm.rider_wave_kib", "gemm.prefetch"};
+                                        "gemm.next_rider_first", "gemm.rider_wave_kib", "gemm.prefetch",
+                                        "gemv.slice_copy"};
     bool ok = false;
     for (const char *k : known) ok = ok || std::strcmp(k, name) == 0;
     if (!ok) return fail(Q8_ERR_INVALID, "unknown option %s", name);
@@ -1478,6 +1487,40 @@ int q8_sync(q8_ctx *c) {
     return Q8_OK;
 }
 
+// The device allocation of a weight: unit-layout quants, then the scales,
+// then, where the weight's one-token GEMV runs in row slices under the
+// default tactics, the slice-major copy of its quants (Q8SliceArgs): one more
+// copy of the quants for one contiguous run per slice and wave load
+// (configs[0] 4.50 -> 4.35 us a GEMV, down 2304 x 5760 5.25 -> 5.13 us).
+struct WeightAlloc {
+    size_t qbytes, sbytes, slices_off, total;
+    int slice_rows;
+};
+
+WeightAlloc weight_alloc(q8_ctx *c, int out, int k) {
+    WeightAlloc wa{};
+    const int nb = k / 32;
+    const int tiles = (int)ceil_div(out, Q8_TILE_ROWS);
+    wa.qbytes = (size_t)tiles * nb * Q8_UNIT_BYTES;
+    wa.sbytes = (size_t)tiles * nb * Q8_TILE_ROWS * 2;
+    q8_tactic t{};
+    q8_gemv_shape(out, k, c->cu_count, 1, &t);
+    // option gemv.slice_copy = 0: no copy (a context whose weights only ever
+    // run in groups or GEMMs saves the memory)
+    wa.slice_rows = ((t.row_slice == 8 || t.row_slice == 16) && option(c, "gemv.slice_copy", 1)) ? t.row_slice : 0;
+    wa.slices_off = align_up(align_up(wa.qbytes, kAlign) + wa.sbytes, kAlign);
+    wa.total = wa.slice_rows ? wa.slices_off + wa.qbytes : align_up(wa.qbytes, kAlign) + wa.sbytes;
+    return wa;
+}
+
+// The slice-major copy of repacked quants (enqueued on the context's stream).
+int slice_copy(q8_ctx *c, const uint8_t *quants, uint8_t *dst, int nb, int tiles, int rs) {
+    Q8SliceArgs a{quants, dst, nb, tiles, rs};
+    const long long threads = (long long)tiles * nb * 64;
+    if (ceil_div(threads, 256) > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "weight of %d tiles is too large", tiles);
+    return launch(c, F_SLICE_COPY, (unsigned)ceil_div(threads, 256), 256, 0, &a, sizeof a);
+}
+
 int q8_weight_resident(q8_ctx *c, const void *bytes, size_t nbytes, int k, int out, const q8_weight **weight) {
     if (!c || !bytes || !weight) return fail(Q8_ERR_INVALID, "q8_weight_resident: bad arguments");
     Q8_TRY(check_k(k));
@@ -1496,9 +1539,9 @@ int q8_weight_resident(q8_ctx *c, const void *bytes, size_t nbytes, int k, int o
         return Q8_OK;
     }
     const int tiles = (int)ceil_div(out, Q8_TILE_ROWS);
-    const size_t qbytes = (size_t)tiles * nb * Q8_UNIT_BYTES;
-    const size_t sbytes = (size_t)tiles * nb * Q8_TILE_ROWS * 2;
-    const size_t total = align_up(qbytes, kAlign) + sbytes;
+    const WeightAlloc wa = weight_alloc(c, out, k);
+    const size_t qbytes = wa.qbytes;
+    const size_t total = wa.total;
     void *base = nullptr, *staging = nullptr;
     HIP_TRY(dev_malloc(c, &base, total), "hipMalloc(weight)");
     hipError_t e = dev_malloc(c, &staging, nbytes);
@@ -1522,6 +1565,8 @@ int q8_weight_resident(q8_ctx *c, const void *bytes, size_t nbytes, int k, int o
         if (threads > 0x7fffffffLL) rc = fail(Q8_ERR_UNSUPPORTED, "weight of %lld blocks is too large", threads);
         if (rc == Q8_OK) rc = launch(c, F_REPACK, (unsigned)ceil_div(threads, 256), 256, 0, &a, sizeof a);
     }
+    uint8_t *slices = wa.slice_rows ? static_cast<uint8_t *>(base) + wa.slices_off : nullptr;
+    if (rc == Q8_OK && slices) rc = slice_copy(c, a.quants, slices, nb, tiles, wa.slice_rows);
     if (rc == Q8_OK) {
         e = hipStreamSynchronize(c->stream);
         if (e != hipSuccess) rc = hip_fail(e, "hipStreamSynchronize");
@@ -1532,6 +1577,8 @@ int q8_weight_resident(q8_ctx *c, const void *bytes, size_t nbytes, int k, int o
         return rc;
     }
     q8_weight *w = new q8_weight{c, base, a.quants, a.scales, k, out, nb, tiles, total, (uintptr_t)bytes, nbytes};
+    w->slices = slices;
+    w->slice_rows = wa.slice_rows;
     c->weights[key] = w;
     *weight = w;
     return Q8_OK;
@@ -2426,9 +2473,9 @@ int q8_weight_synthetic(q8_ctx *c, int k, int out, uint64_t seed, float scale_st
     const int nb = k / 32;
     const int tiles = (int)ceil_div(out, Q8_TILE_ROWS);
     const size_t nbytes = (size_t)out * nb * Q8_BLOCK_BYTES;
-    const size_t qbytes = (size_t)tiles * nb * Q8_UNIT_BYTES;
-    const size_t sbytes = (size_t)tiles * nb * Q8_TILE_ROWS * 2;
-    const size_t total = align_up(qbytes, kAlign) + sbytes;
+    const WeightAlloc wa = weight_alloc(c, out, k);
+    const size_t qbytes = wa.qbytes;
+    const size_t total = wa.total;
     const long long threads = (long long)tiles * Q8_TILE_ROWS * nb;
     if (threads > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "weight of %lld blocks is too large", threads);
     void *base = nullptr, *staging = nullptr;
@@ -2449,6 +2496,8 @@ int q8_weight_synthetic(q8_ctx *c, int k, int out, uint64_t seed, float scale_st
     a.inverse = 0;
     int rc = launch(c, F_SYNTH, (unsigned)std::min<long long>(ceil_div(sa.blocks, 256), 65536), 256, 0, &sa, sizeof sa);
     if (rc == Q8_OK) rc = launch(c, F_REPACK, (unsigned)ceil_div(threads, 256), 256, 0, &a, sizeof a);
+    uint8_t *slices = wa.slice_rows ? static_cast<uint8_t *>(base) + wa.slices_off : nullptr;
+    if (rc == Q8_OK && slices) rc = slice_copy(c, a.quants, slices, nb, tiles, wa.slice_rows);
     if (rc == Q8_OK) {
         e = hipStreamSynchronize(c->stream);
         if (e != hipSuccess) rc = hip_fail(e, "hipStreamSynchronize");
@@ -2459,6 +2508,8 @@ int q8_weight_synthetic(q8_ctx *c, int k, int out, uint64_t seed, float scale_st
         return rc;
     }
     q8_weight *w = new q8_weight{c, base, a.quants, a.scales, k, out, nb, tiles, total, 0, 0};
+    w->slices = slices;
+    w->slice_rows = wa.slice_rows;
     c->owned.push_back(w);
     *weight = w;
     return Q8_OK;

@@ -194,6 +194,7 @@ ARG_STRUCTS = {  # kernel name prefix -> the argument struct every kernel of tha
     "q8_repack": "Q8RepackArgs", "q8_argmax": "Q8ArgmaxArgs", "q8_copy": "Q8CopyArgs", "q8_embed": "Q8EmbedArgs",
     "q8_silu_mul": "Q8EltArgs", "q8_rope_append": "Q8RopeArgs", "q8_attn_decode": "Q8AttnDecodeArgs",
     "q8_attn_prefill": "Q8AttnPrefillArgs", "q8_synth": "Q8SynthArgs", "q8_advance": "Q8AdvanceArgs",
+    "q8_slice_copy": "Q8SliceArgs",
 }
 
 

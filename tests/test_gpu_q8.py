@@ -8,6 +8,7 @@ Bars (the path's parity targets):
     when the host oracle takes that order (it does on AVX2+FMA hosts);
   * lm_head: identical argmax.
 """
+import ctypes
 import math
 
 import numpy as np
@@ -24,7 +25,7 @@ SEED = 0x5EED
 J = [[0, 4, 1, 5], [2, 6, 3, 7]]
 OPTIONS = ("gemv.exact", "gemv.waves", "gemv.pairs", "gemv.slices", "gemv.rows", "gemv.loads", "gemv.xcd_order", "gemm.smode", "gemm.tpw", "gemm.twaves",
            "gemm.xcd_remap", "gemm.kwaves", "gemm.slices", "gemm.rwaves", "gemm.f16", "gemm.pipe", "gemm.lds",
-           "gemm.silu", "gemm.small_gemv", "gemm.stream")
+           "gemm.silu", "gemm.small_gemv", "gemm.stream", "gemv.slice_copy")
 
 
 def assert_close(got, ref, what):
@@ -351,6 +352,51 @@ def test_gemv_row_slices_match_the_reference(gpu, rows, loads, out, k, exact):
     if not exact:
         assert_bits(run_matmul(gpu, w, x, 1).reshape(-1), got, what + " rerun")
     gpu.release(w)
+
+
+def device_bytes(gpu, w):
+    k, out, nbytes = ctypes.c_int(), ctypes.c_int(), ctypes.c_size_t()
+    handle = gpu.resident(w)
+    assert q8.lib().q8_weight_shape(ctypes.c_void_p(handle), ctypes.byref(k), ctypes.byref(out),
+                                    ctypes.byref(nbytes)) == q8.Q8_OK
+    return nbytes.value
+
+
+@pytest.mark.parametrize("exact", [1, 0])
+@pytest.mark.parametrize("out,k,rows", [(5760, 2304, 8), (4096, 2304, 8), (2304, 5760, 16), (2304, 2304, 16),
+                                        (257, 2304, 16)])
+def test_gemv_slice_major_copy_matches_the_unit_layout(gpu, out, k, rows, exact):
+    """A weight whose one-token GEMV runs in row slices keeps a slice-major
+    copy of its quants (each slice's bytes in one run); the row-slice kernels
+    read it by default and the unit layout with option gemv.slice_copy = 0, and
+    give the same bits either way (residual included), within the bar of the
+    oracle.  A weight made resident with the option at 0 has no copy: its
+    device bytes are one copy of the quants fewer."""
+    r = rng(70 + out + k)
+    w = weight(r, out, k)
+    x = r.standard_normal(k, dtype=np.float32)
+    bias = r.standard_normal(out).astype(np.float32)
+    assert q8.plan(1, out, k, gpu)["row_slice"] == rows
+    gpu.set_option("gemv.exact", exact)
+    try:
+        got = run_matmul(gpu, w, x, 1, bias=bias).reshape(-1)
+        ref = oracle.matmul(w.data, k, out, x, 1).reshape(-1) + bias
+        assert_close(got, ref, f"slice-major {out}x{k} exact={exact}")
+        gpu.set_option("gemv.slice_copy", 0)
+        unit = run_matmul(gpu, w, x, 1, bias=bias).reshape(-1)
+        assert_bits(got, unit, f"slice-major against unit layout {out}x{k} exact={exact}")
+        with_copy = device_bytes(gpu, w)
+        bare = weight(r, out, k)  # resident while the option is 0
+        without = device_bytes(gpu, bare)
+        assert_bits(run_matmul(gpu, bare, x, 1, bias=bias).reshape(-1),
+                    run_matmul(gpu, bare, x, 1, bias=bias).reshape(-1), "no copy, rerun")
+        quants = (out + 31) // 32 * (k // 32) * 1024
+        assert quants <= with_copy - without < quants + 256, (with_copy, without, quants)
+        gpu.release(bare)
+    finally:
+        gpu.set_option("gemv.slice_copy", -1)
+        gpu.set_option("gemv.exact", -1)
+        gpu.release(w)
 
 
 @pytest.mark.parametrize("order,exact", [(0, 1), (1, 1), (1, 0)])
