@@ -298,7 +298,11 @@ int q8_decoder_create_synthetic(q8_ctx *c, const q8_decoder_config *config, uint
         const int dims[7][2] = {{E, g.n_head * g.head_dim}, {E, kv_dim},  {E, kv_dim}, {g.n_head * g.head_dim, E},
                                 {E, g.n_ff},                {E, g.n_ff}, {g.n_ff, E}};
         for (int i = 0; i < 7; i++) {
-            rc = q8_weight_synthetic(c, dims[i][0], dims[i][1], mix(seed + 1000003ull * (l + 1) + i), std_w, &L.w[i]);
+            // q/k/v and gate/up only run in groups (one launch over several
+            // matrices), so they need no slice-major copy; O and down run alone
+            const bool alone = i == Q8_DEC_O || i == Q8_DEC_DOWN;
+            rc = q8i::weight_synthetic(c, dims[i][0], dims[i][1], mix(seed + 1000003ull * (l + 1) + i), std_w, alone,
+                                       &L.w[i]);
             if (rc) return fail(rc);
         }
         L.attn_norm = norm_weights(mix(seed + 7919ull * (l + 1)), E);

@@ -30,6 +30,10 @@ __attribute__((visibility("hidden"))) int noalloc_scratch(int device, void **out
 // another context on the same device is refused (q8_noalloc_owner.h).
 __attribute__((visibility("hidden"))) bool noalloc_claim(int device, const q8_ctx *ctx);
 __attribute__((visibility("hidden"))) void noalloc_release(const q8_ctx *ctx);
+// q8_weight_synthetic, with slice_copy = false for a weight that only runs in
+// groups or GEMMs: no slice-major copy of its quants is built.
+__attribute__((visibility("hidden"))) int weight_synthetic(q8_ctx *c, int k, int out, uint64_t seed, float scale_std,
+                                                            bool slice_copy, const q8_weight **weight);
 }  // namespace q8i
 
 #endif

@@ -1497,7 +1497,7 @@ struct WeightAlloc {
     int slice_rows;
 };
 
-WeightAlloc weight_alloc(q8_ctx *c, int out, int k) {
+WeightAlloc weight_alloc(q8_ctx *c, int out, int k, bool allow_slices = true) {
     WeightAlloc wa{};
     const int nb = k / 32;
     const int tiles = (int)ceil_div(out, Q8_TILE_ROWS);
@@ -1507,7 +1507,8 @@ WeightAlloc weight_alloc(q8_ctx *c, int out, int k) {
     q8_gemv_shape(out, k, c->cu_count, 1, &t);
     // option gemv.slice_copy = 0: no copy (a context whose weights only ever
     // run in groups or GEMMs saves the memory)
-    wa.slice_rows = ((t.row_slice == 8 || t.row_slice == 16) && option(c, "gemv.slice_copy", 1)) ? t.row_slice : 0;
+    wa.slice_rows =
+        ((t.row_slice == 8 || t.row_slice == 16) && allow_slices && option(c, "gemv.slice_copy", 1)) ? t.row_slice : 0;
     wa.slices_off = align_up(align_up(wa.qbytes, kAlign) + wa.sbytes, kAlign);
     wa.total = wa.slice_rows ? wa.slices_off + wa.qbytes : align_up(wa.qbytes, kAlign) + wa.sbytes;
     return wa;
@@ -2465,6 +2466,13 @@ int q8_advance_position(q8_ctx *c, q8_dptr position, int by) {
 }
 
 int q8_weight_synthetic(q8_ctx *c, int k, int out, uint64_t seed, float scale_std, const q8_weight **weight) {
+    return q8i::weight_synthetic(c, k, out, seed, scale_std, true, weight);
+}
+
+}  // extern "C"
+
+int q8i::weight_synthetic(q8_ctx *c, int k, int out, uint64_t seed, float scale_std, bool with_slices,
+                          const q8_weight **weight) {
     if (!c || !weight) return fail(Q8_ERR_INVALID, "q8_weight_synthetic: bad arguments");
     Q8_TRY(check_k(k));
     if (out <= 0) return fail(Q8_ERR_INVALID, "weight has %d rows", out);
@@ -2473,7 +2481,7 @@ int q8_weight_synthetic(q8_ctx *c, int k, int out, uint64_t seed, float scale_st
     const int nb = k / 32;
     const int tiles = (int)ceil_div(out, Q8_TILE_ROWS);
     const size_t nbytes = (size_t)out * nb * Q8_BLOCK_BYTES;
-    const WeightAlloc wa = weight_alloc(c, out, k);
+    const WeightAlloc wa = weight_alloc(c, out, k, with_slices);
     const size_t qbytes = wa.qbytes;
     const size_t total = wa.total;
     const long long threads = (long long)tiles * Q8_TILE_ROWS * nb;
@@ -2514,6 +2522,8 @@ int q8_weight_synthetic(q8_ctx *c, int k, int out, uint64_t seed, float scale_st
     *weight = w;
     return Q8_OK;
 }
+
+extern "C" {
 
 int q8_argmax(q8_ctx *c, q8_dptr values, size_t offset, size_t len, uint32_t *argmax) {
     if (!c || !argmax) return fail(Q8_ERR_INVALID, "q8_argmax: bad arguments");
