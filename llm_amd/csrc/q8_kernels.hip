@@ -1154,8 +1154,10 @@ Q8_GEMV_RS_KERNEL(16, 6)
 // row are summed in gemv_rs_body's fixed tree, per token.  Tokens past
 // a.tokens (NT > n) re-read the last token and write nothing.
 // ---------------------------------------------------------------------------
+// The head (RsHot) as the row-slice GEMV takes it, with the token count in
+// the row count's top byte (mrows | tokens << 24).
 template <int RS, int NL, int NT>
-static __device__ __forceinline__ void gemv_q8x_body(const Q8GemvArgs &a) {
+static __device__ __forceinline__ void gemv_q8x_body(const RsHot &hot, const Q8GemvArgs &a) {
     extern __shared__ __attribute__((aligned(16))) float smem[];
     constexpr int LPB = 2 * RS;               // lanes per block
     constexpr int BPL = 64 / LPB;             // blocks per wave load
@@ -1163,32 +1165,36 @@ static __device__ __forceinline__ void gemv_q8x_body(const Q8GemvArgs &a) {
     constexpr int BPW = NL * BPL;             // blocks per wave
     constexpr int XS = (BPW * 8 + 63) / 64;   // x float4s a lane quantizes per token
     static_assert(BPW * 8 <= 64 * Q8_GEMV_STAGE, "x range of a wave exceeds its staging registers");
-    const uint8_t *mq = a.m[0].quants;
-    const uint16_t *msc = a.m[0].scales;
-    float *my = a.m[0].y;
-    const float *mbias = a.m[0].bias;
-    const int mrows = a.m[0].rows;
-    const float *xg = a.x;
-    const int nb = a.nb;
-    const int ntok = NT == 1 ? 1 : a.tokens;
-    const int nw = a.waves_per_tile;  // the launch's wave count, read with the rest (as gemv_rs_body)
-    asm volatile("" ::"s"(mq), "s"(msc), "s"(my), "s"(mbias), "s"(mrows), "s"(xg), "s"(nb), "s"(a.xcd_order),
-                 "s"(a.total_tiles), "s"(ntok), "s"(nw));
+    const uint8_t *mq = hot.mq;
+    const uint16_t *msc = hot.msc;
+    float *my = hot.my;
+    const float *mbias = hot.mbias;
+    const int mrows = hot.mrows & 0xffffff;
+    const float *xg = hot.xg;
+    const int nb = hot.nbw & 0xffff;
+    const int ntok = NT == 1 ? 1 : hot.mrows >> 24;
+    const int nw = hot.nbw >> 16;  // the launch's wave count (as gemv_rs_body)
+    const int total_tiles = hot.tiles_xo & 0x3fffffff;
+    const bool slice_major = (hot.tiles_xo >> 30) & 1;
+    const int xo = (int)((unsigned)hot.tiles_xo >> 31);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int j = lane / LPB;
     const int h = (lane / RS) & 1;
     const int r = lane % RS;
     const int bx = blockIdx.x;
-    const int xo = a.xcd_order;
     const int tile = xo ? (bx / (8 * SPT)) * 8 + (bx & 7) : bx / SPT;
     const int slice = xo ? (bx >> 3) % SPT : bx % SPT;
-    if (tile >= a.total_tiles) return;  // padding of the XCD order, whole workgroup
+    if (tile >= total_tiles) return;  // padding of the XCD order, whole workgroup
     const int srow = slice * RS + r;
     const int b_begin = wave * BPW;
     const int b_end = min(nb, b_begin + BPW);
     const int b_last = max(b_end - 1, 0);
-    const uint8_t *qbase = mq + (size_t)tile * nb * Q8_UNIT_BYTES + 16 * (32 * h + srow);
+    // the weight's slice-major copy where the head says so (as gemv_rs_body)
+    const uint8_t *qbase = slice_major
+                               ? mq + ((size_t)tile * SPT + slice) * nb * (RS * 32) + 16 * (lane % LPB)
+                               : mq + (size_t)tile * nb * Q8_UNIT_BYTES + 16 * (32 * h + srow);
+    const size_t qstride = slice_major ? (size_t)(RS * 32) : (size_t)Q8_UNIT_BYTES;
     const uint16_t *sbase = msc + (size_t)tile * nb * Q8_TILE_ROWS + srow;
     // the pad sits before the row sums so that no address of the quantize
     // step waits on the workgroup size (a second kernel-argument read ahead
@@ -1217,7 +1223,7 @@ static __device__ __forceinline__ void gemv_q8x_body(const Q8GemvArgs &a) {
 #pragma unroll
     for (int i = 0; i < NL; i++) {
         const int b = min(b_begin + i * BPL + j, b_last);
-        qv[i] = q8_weight_load(qbase + (size_t)b * Q8_UNIT_BYTES);
+        qv[i] = q8_weight_load(qbase + (size_t)b * qstride);
         dd[i] = (unsigned)sbase[(size_t)b * Q8_TILE_ROWS];
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -1305,8 +1311,8 @@ static __device__ __forceinline__ void gemv_q8x_body(const Q8GemvArgs &a) {
 }
 
 #define Q8_GEMV_Q8X_KERNEL(RS, NL, NT)                                                                   \
-    extern "C" __global__ __launch_bounds__(1024) void q8_gemv_q8x##NT##_r##RS##_l##NL(Q8GemvArgs a) { \
-        gemv_q8x_body<RS, NL, NT>(a);                                                                    \
+    extern "C" __global__ __launch_bounds__(1024) void q8_gemv_q8x##NT##_r##RS##_l##NL(Q8_RS_PARAMS) { \
+        gemv_q8x_body<RS, NL, NT>(Q8_RS_HOT, a);                                                         \
     }
 #define Q8_GEMV_Q8X_TOKENS(NT)                                                                          \
     Q8_GEMV_Q8X_KERNEL(8, 2, NT) Q8_GEMV_Q8X_KERNEL(8, 3, NT) Q8_GEMV_Q8X_KERNEL(8, 6, NT)                 \

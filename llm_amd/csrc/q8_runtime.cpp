@@ -1811,7 +1811,13 @@ int run_gemv_q8x(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset, int 
     if (grid > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "quantized-x GEMV: grid of %lld workgroups", grid);
     const Fn f = nl == 2 ? (nt == 1 ? F_GEMV_Q8X1_8_2 : F_GEMV_Q8X2_8_2)
                          : (Fn)(F_GEMV_Q8X1_8_3 + 4 * (nt - 1) + (rs == 8 ? 0 : 2) + (nl == 3 ? 0 : 1));
-    return launch(c, f, (unsigned)grid, (unsigned)(waves * 64), (unsigned)lds, &a, sizeof a);
+    if (nb > 0xffff || w->tiles > 0x3fffffff || w->out >= (1 << 24))
+        return fail(Q8_ERR_UNSUPPORTED, "quantized-x GEMV: %d x %d", w->out, k);
+    // the preloaded head of the row-slice GEMVs, the token count above the rows
+    const bool sm = w->slices && w->slice_rows == rs && option(c, "gemv.slice_copy", 1);
+    RsHead h{sm ? w->slices : w->quants, w->scales, y, bias, a.x, w->out | (nt << 24), nb | (waves << 16),
+             (int)((unsigned)w->tiles | ((unsigned)sm << 30) | ((unsigned)a.xcd_order << 31))};
+    return launch_rs(c, f, (unsigned)grid, (unsigned)(waves * 64), (unsigned)lds, h, a);
 }
 
 int q8_matmul_q8(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset, int n, q8_dptr y, size_t y_offset,

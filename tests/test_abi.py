@@ -190,6 +190,7 @@ ARG_STRUCTS = {  # kernel name prefix -> the argument struct every kernel of tha
     # the row-slice GEMVs: a preloadable scalar head (five pointers, three
     # ints, 56 bytes with padding), then the GEMV argument block
     "q8_gemv_r8_": "head + Q8GemvArgs", "q8_gemv_r16_": "head + Q8GemvArgs", "q8_gemv_rc": "head + Q8GemvArgs",
+    "q8_gemv_q8x": "head + Q8GemvArgs",
     "q8_gemm_": "Q8GemmArgs", "q8_gemv": "Q8GemvArgs", "q8_quantize": "Q8QuantArgs", "q8_rmsnorm": "Q8NormArgs",
     "q8_repack": "Q8RepackArgs", "q8_argmax": "Q8ArgmaxArgs", "q8_copy": "Q8CopyArgs", "q8_embed": "Q8EmbedArgs",
     "q8_silu_mul": "Q8EltArgs", "q8_rope_append": "Q8RopeArgs", "q8_attn_decode": "Q8AttnDecodeArgs",
@@ -214,7 +215,8 @@ def test_every_kernel_carries_its_metadata():
     for family, seen in sizes.items():
         assert len(seen) == 1, f"{family}: kernels disagree on the argument size {sorted(seen)}"
     assert sizes["head + Q8GemvArgs"] == {56 + min(sizes["Q8GemvArgs"])}, "the row-slice head is 56 bytes"
-    assert len([n for n in info["kernels"] if n.startswith(("q8_gemv_r8_", "q8_gemv_r16_", "q8_gemv_rc"))]) == 20
+    assert len([n for n in info["kernels"]
+                if n.startswith(("q8_gemv_r8_", "q8_gemv_r16_", "q8_gemv_rc", "q8_gemv_q8x"))]) == 30
     with pytest.raises(q8.Q8Error) as e:
         q8.kernel_info("q8_no_such_kernel")
     assert e.value.status == q8.Q8_ERR_INVALID

@@ -222,3 +222,34 @@ def test_every_slice_shape(gpu, rows, loads, out, k):
     finally:
         gpu.set_option("gemv.rows", -1)
         gpu.set_option("gemv.loads", -1)
+
+
+@pytest.mark.parametrize("out,k", [(5760, 2304), (2304, 5760), (257, 2304)])
+def test_slice_major_copy_matches_the_unit_layout(gpu, out, k):
+    """The quantized-x GEMV reads the weight's slice-major copy where it runs
+    the slice height the copy was built for, the unit layout with option
+    gemv.slice_copy = 0: the same bits at one token (q8_matmul_q8) and two
+    (q8_matmul's two-token GEMV), residual included."""
+    r = rng(300 + out + k)
+    w = weight(r, out, k)
+    x = oracle.make_activations(r, 2, k, outlier_rate=0.01)
+    bias = r.standard_normal(2 * out).astype(np.float32)
+    try:
+        one = run_q8(gpu, w, x[0], 1, bias=bias[:out])
+        xb, yb = gpu.alloc(4 * 2 * k), gpu.alloc(4 * 2 * out)
+        xb.upload(x)
+
+        def two():
+            yb.upload(bias)
+            gpu.matmul(w, xb, 0, 2, yb, 0, bias=yb)
+            return yb.download(np.float32, 2 * out)
+
+        pair = two()
+        gpu.set_option("gemv.slice_copy", 0)
+        assert_bits(run_q8(gpu, w, x[0], 1, bias=bias[:out]), one, f"one token {out}x{k}")
+        assert_bits(two(), pair, f"two tokens {out}x{k}")
+        xb.free()
+        yb.free()
+    finally:
+        gpu.set_option("gemv.slice_copy", -1)
+        gpu.release(w)
