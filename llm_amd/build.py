@@ -48,10 +48,10 @@ HIPCC_FLAGS = [
     "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-mllvm", "-amdgpu-mfma-vgpr-form=1",
-    # the first 13 argument dwords of a kernel whose leading arguments are
-    # scalars (the row-slice GEMVs) arrive preloaded in SGPRs; a kernel whose
-    # only argument is its argument block is unaffected
-    "-mllvm", "-amdgpu-kernarg-preload-count=13",
+    # the first 14 argument dwords of a kernel whose leading arguments are
+    # scalars (the row-slice GEMVs, the read probes) arrive preloaded in SGPRs;
+    # a kernel whose only argument is its argument block is unaffected
+    "-mllvm", "-amdgpu-kernarg-preload-count=14",
 ]
 
 

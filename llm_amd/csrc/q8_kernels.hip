@@ -401,18 +401,24 @@ struct CombineRegs {
     f32x2 ms[Q8_ATTN_COMBINE_MAX];  // (max, sum)
 };
 
-static __device__ __forceinline__ void combine_load_v(const Q8GemvArgs &a, int v, int ns, CombineRegs &c) {
+// Where the partials are: [heads][splits][64] sums and [heads][splits] (max, sum).
+struct CombineSrc {
+    const float *acc;
+    const float *ms;
+};
+
+static __device__ __forceinline__ void combine_load_v(const CombineSrc &a, int v, int ns, CombineRegs &c) {
     const int hs = (v >> 4) * ns;  // head * splits
 #pragma unroll
     for (int s = 0; s < Q8_ATTN_COMBINE_MAX; s++) {
         if (s < ns) {
-            c.ms[s] = *(const f32x2 *)(a.attn_ms + 2 * (hs + s));
-            c.acc[s] = *(const f32x4 *)(a.attn_acc + (size_t)(hs + s) * 64 + 4 * (v & 15));
+            c.ms[s] = *(const f32x2 *)(a.ms + 2 * (hs + s));
+            c.acc[s] = *(const f32x4 *)(a.acc + (size_t)(hs + s) * 64 + 4 * (v & 15));
         }
     }
 }
 
-static __device__ __forceinline__ void combine_load(const Q8GemvArgs &a, int nb, int ns, CombineRegs &c) {
+static __device__ __forceinline__ void combine_load(const CombineSrc &a, int nb, int ns, CombineRegs &c) {
     combine_load_v(a, min((int)threadIdx.x, nb * 8 - 1), ns, c);
 }
 
@@ -446,7 +452,7 @@ static __device__ __forceinline__ void combine_store(int nb, int ns, const Combi
 // The float4s of x past the workgroup's threads (a row-slice launch whose K
 // range needs fewer waves than x has float4s / 64): each thread builds them
 // in turn, v = tid + threads, tid + 2 threads, ..., with the same arithmetic.
-static __device__ __forceinline__ void combine_rest(const Q8GemvArgs &a, int nb, int ns, float *xs, float *pad) {
+static __device__ __forceinline__ void combine_rest(const CombineSrc &a, int nb, int ns, float *xs, float *pad) {
     for (int v = (int)(threadIdx.x + blockDim.x); v < nb * 8; v += (int)blockDim.x) {
         CombineRegs c;
         combine_load_v(a, v, ns, c);
@@ -574,7 +580,7 @@ static __device__ __forceinline__ void gemv_body(const Q8GemvArgs &a) {
     const int ns = comb ? a.attn_splits : 0;
     const bool comb_wave = comb && (int)(threadIdx.x & ~63u) < nb * 8;  // wave-uniform
     if constexpr (comb) {
-        if (comb_wave) combine_load(a, nb, ns, creg);
+        if (comb_wave) combine_load(CombineSrc{a.attn_acc, a.attn_ms}, nb, ns, creg);
     } else {
 #pragma unroll
         for (int u = 0; u < Q8_GEMV_STAGE; u++) {
@@ -923,13 +929,17 @@ Q8_GEMV_KERNEL(9, 1, 512)
 // f32 rounding of the reference's left-to-right sum, and it drops the
 // serial 72-add chain and its LDS round trips from the end of the kernel.
 // The row-slice GEMV's hot values travel as its first kernel arguments, ahead
-// of the argument block: the code object is built with the first 13 argument
+// of the argument block: the code object is built with the first 14 argument
 // dwords preloaded into SGPRs at wave launch (gfx950 kernarg preload), so a
 // wave issues its weight loads without first reading the kernarg segment, a
 // scalar-cache miss of ~0.26 us on each CU's first wave (configs[0]: 4.72 ->
 // 4.49 us a launch, same bits).  nbw = nb | waves << 16, tiles_xo =
 // total_tiles | slice_major << 30 | xcd_order << 31; with slice_major, mq is
 // the weight's slice-major copy (Q8SliceArgs) and a wave load reads one run.
+// The combine builds, whose x comes from the attention partials, take the
+// partial sums in xg, their (max, sum) plane at xg + ms_off and the split
+// count in mrows' top byte, so their prologue needs no argument-block read
+// either.
 struct RsHot {
     const uint8_t *mq;
     const uint16_t *msc;
@@ -937,6 +947,7 @@ struct RsHot {
     const float *mbias;
     const float *xg;
     int mrows, nbw, tiles_xo;
+    int ms_off;  // combine builds (q8_gemv_rc*): the (max, sum) plane's float offset from xg
 };
 
 template <int RS, int NL, int CMB = 0, int EX = 1>
@@ -951,7 +962,7 @@ static __device__ __forceinline__ void gemv_rs_body(const RsHot &hot, const Q8Ge
     const uint16_t *msc = hot.msc;
     float *my = hot.my;
     const float *mbias = hot.mbias;
-    const int mrows = hot.mrows;
+    const int mrows = hot.mrows & 0xffffff;
     const float *xg = hot.xg;
     const int nb = hot.nbw & 0xffff;
     // the wave count comes from the arguments (the host launches that many
@@ -961,9 +972,7 @@ static __device__ __forceinline__ void gemv_rs_body(const RsHot &hot, const Q8Ge
     const int total_tiles = hot.tiles_xo & 0x3fffffff;
     const bool slice_major = (hot.tiles_xo >> 30) & 1;
     const int xo = (int)((unsigned)hot.tiles_xo >> 31);
-    // the combine's partials come from the argument block, read at once: a
-    // second read would wait ahead of the first partial and weight loads
-    if constexpr (CMB) asm volatile("" ::"s"(a.attn_acc), "s"(a.attn_ms), "s"(a.attn_splits));
+    const CombineSrc csrc{xg, xg + hot.ms_off};
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int j = lane / LPB;
@@ -1008,12 +1017,12 @@ static __device__ __forceinline__ void gemv_rs_body(const RsHot &hot, const Q8Ge
     constexpr int XS = (BPW * 8 + 63) / 64;  // x float4s a lane stages
     f32x4 xv[Q8_GEMV_STAGE];
     CombineRegs creg;
-    const int ns = CMB ? a.attn_splits : 0;
+    const int ns = CMB ? hot.mrows >> 24 : 0;
     const int cmb_v = (lane < st_end - st_begin) ? st_begin + lane : nb * 8;  // CMBW: nb * 8 = the pad
     if constexpr (CMBW) {
-        combine_load_v(a, min(cmb_v, st_clamp), ns, creg);
+        combine_load_v(csrc, min(cmb_v, st_clamp), ns, creg);
     } else if constexpr (CMB) {
-        combine_load(a, nb, ns, creg);
+        combine_load(csrc, nb, ns, creg);
     } else {
 #pragma unroll
         for (int u = 0; u < XS; u++) {
@@ -1043,7 +1052,7 @@ static __device__ __forceinline__ void gemv_rs_body(const RsHot &hot, const Q8Ge
         combine_store_v(cmb_v, nb, ns, creg, xs, pad);
     } else if constexpr (CMB) {
         combine_store(nb, ns, creg, xs, pad);
-        combine_rest(a, nb, ns, xs, pad);
+        combine_rest(csrc, nb, ns, xs, pad);
         __syncthreads();
     }
     // stage x permuted (the tile kernel's order): float4 slot 8b + 4hh + t
@@ -1109,8 +1118,8 @@ static __device__ __forceinline__ void gemv_rs_body(const RsHot &hot, const Q8Ge
 
 #define Q8_RS_PARAMS                                                                                  \
     const uint8_t *mq, const uint16_t *msc, float *my, const float *mbias, const float *xg, int mrows, \
-        int nbw, int tiles_xo, Q8GemvArgs a
-#define Q8_RS_HOT RsHot{mq, msc, my, mbias, xg, mrows, nbw, tiles_xo}
+        int nbw, int tiles_xo, int ms_off, Q8GemvArgs a
+#define Q8_RS_HOT RsHot{mq, msc, my, mbias, xg, mrows, nbw, tiles_xo, ms_off}
 #define Q8_GEMV_RS_KERNEL(RS, NL)                                                                      \
     extern "C" __global__ __launch_bounds__(1024) void q8_gemv_r##RS##_l##NL(Q8_RS_PARAMS) {        \
         gemv_rs_body<RS, NL>(Q8_RS_HOT, a);                                                            \

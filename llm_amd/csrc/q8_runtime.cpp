@@ -275,14 +275,14 @@ struct RsHead {
     float *my;
     const float *mbias;
     const float *xg;
-    int mrows, nbw, tiles_xo;
+    int mrows, nbw, tiles_xo, ms_off;
 };
-static_assert(sizeof(RsHead) == 56, "row-slice head: five pointers and three ints, padded to 8 bytes");
+static_assert(sizeof(RsHead) == 56, "row-slice head: five pointers and four ints");
 
 int launch_rs(q8_ctx *c, Fn f, unsigned grid, unsigned block, unsigned lds, RsHead &h, Q8GemvArgs &a) {
     if (grid == 0) return Q8_OK;
     Q8_TRY(check_launch(*c->meta[f], sizeof(RsHead) + sizeof(Q8GemvArgs), block, lds, c->max_lds));
-    void *params[] = {&h.mq, &h.msc, &h.my, &h.mbias, &h.xg, &h.mrows, &h.nbw, &h.tiles_xo, &a};
+    void *params[] = {&h.mq, &h.msc, &h.my, &h.mbias, &h.xg, &h.mrows, &h.nbw, &h.tiles_xo, &h.ms_off, &a};
     HIP_TRY(hipModuleLaunchKernel(c->fn[f], grid, 1, 1, block, 1, 1, lds, c->stream, params, nullptr),
             kFnNames[f]);
     return Q8_OK;
@@ -530,9 +530,19 @@ int run_gemv_rs(q8_ctx *c, const q8_weight *w, float *y, q8_dptr x, const float 
     // the weight's slice-major copy where it has one for these slices
     // (option gemv.slice_copy = 0 reads the unit layout instead)
     const bool sm = w->slices && w->slice_rows == rs && option(c, "gemv.slice_copy", 1);
+    if (w->out >= (1 << 24)) return fail(Q8_ERR_UNSUPPORTED, "gemv: %d rows in row slices", w->out);
     RsHead h{sm ? w->slices : a.m[0].quants, a.m[0].scales, a.m[0].y, a.m[0].bias, a.x, a.m[0].rows,
              nb | (waves << 16),
-             (int)((unsigned)w->tiles | ((unsigned)sm << 30) | ((unsigned)a.xcd_order << 31))};
+             (int)((unsigned)w->tiles | ((unsigned)sm << 30) | ((unsigned)a.xcd_order << 31)), 0};
+    if (comb) {
+        // the combine's partials in the head: sums in xg, (max, sum) at xg + ms_off, splits above the rows
+        const long long off = comb->ms - comb->acc;
+        if (off < INT32_MIN || off > INT32_MAX)
+            return fail(Q8_ERR_UNSUPPORTED, "gemv: attention partials %lld floats apart", off);
+        h.xg = comb->acc;
+        h.ms_off = (int)off;
+        h.mrows |= comb->splits << 24;
+    }
     return launch_rs(c, f, (unsigned)grid, (unsigned)(waves * 64), lds, h, a);
 }
 
@@ -1816,7 +1826,7 @@ int run_gemv_q8x(q8_ctx *c, const q8_weight *w, q8_dptr x, size_t x_offset, int 
     // the preloaded head of the row-slice GEMVs, the token count above the rows
     const bool sm = w->slices && w->slice_rows == rs && option(c, "gemv.slice_copy", 1);
     RsHead h{sm ? w->slices : w->quants, w->scales, y, bias, a.x, w->out | (nt << 24), nb | (waves << 16),
-             (int)((unsigned)w->tiles | ((unsigned)sm << 30) | ((unsigned)a.xcd_order << 31))};
+             (int)((unsigned)w->tiles | ((unsigned)sm << 30) | ((unsigned)a.xcd_order << 31)), 0};
     return launch_rs(c, f, (unsigned)grid, (unsigned)(waves * 64), (unsigned)lds, h, a);
 }
 
