@@ -122,8 +122,22 @@ static __device__ __forceinline__ float wave_sum(float v) {
     return xor_add<1>(v);
 }
 
+// What the decode attention reads before its first key, as its leading
+// kernel arguments: preloaded into SGPRs at wave launch (the kernarg preload
+// the row-slice GEMVs use), so the cache position's load, the first dependent
+// read, issues at once.  dims = n_head | n_kv << 16; cap = capacity | defer <<
+// 31; the (max, sum) plane follows the partial sums (part_acc + heads * splits
+// * 64).  scale, out and counters stay in the argument block.
+struct AttnHead {
+    const float *q;
+    const uint16_t *kcache, *vcache;
+    const int *position;
+    float *part_acc;
+    int dims, splits, cap;
+};
+
 template <int W, int NP>
-static __device__ __forceinline__ void attn_decode_body(const Q8AttnDecodeArgs &a) {
+static __device__ __forceinline__ void attn_decode_body(const AttnHead &hd, const Q8AttnDecodeArgs &a) {
     constexpr int T = 64 * W;
     constexpr int HD = Q8_ATTN_HEAD_DIM;
     constexpr int RP = T / 8;  // rows per pass
@@ -131,18 +145,25 @@ static __device__ __forceinline__ void attn_decode_body(const Q8AttnDecodeArgs &
     __shared__ float lsum[W];
     __shared__ __attribute__((aligned(16))) float part[W][HD];
     __shared__ int last_flag;
-    const int position = *a.position;
-    const int head = blockIdx.x / a.splits;
-    const int split = blockIdx.x - head * a.splits;
-    const int kvh = head / (a.n_head / a.n_kv);
-    const int kv_dim = a.n_kv * HD;
+    const int n_head_ = hd.dims & 0xffff;
+    const int n_kv_ = hd.dims >> 16;
+    const int splits_ = hd.splits;
+    const int capacity_ = hd.cap & 0x7fffffff;
+    const int defer_ = (int)((unsigned)hd.cap >> 31);
+    float *const part_acc_ = hd.part_acc;
+    float *const part_ms_ = hd.part_acc + (size_t)n_head_ * splits_ * Q8_ATTN_HEAD_DIM;
+    const int position = *hd.position;
+    const int head = blockIdx.x / splits_;
+    const int split = blockIdx.x - head * splits_;
+    const int kvh = head / (n_head_ / n_kv_);
+    const int kv_dim = n_kv_ * HD;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int kc = tid & 7;     // dims 8 kc .. 8 kc + 7
     const int slot = tid >> 3;  // row slot of the pass
-    const uint16_t *kbase = a.kcache + kvh * HD + 8 * kc;
-    const uint16_t *vbase = a.vcache + kvh * HD + 8 * kc;
+    const uint16_t *kbase = hd.kcache + kvh * HD + 8 * kc;
+    const uint16_t *vbase = hd.vcache + kvh * HD + 8 * kc;
     float m = -INFINITY;  // running max, workgroup-uniform
     float l = 0.0f;       // this lane's weights summed over its rows
     float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
@@ -192,8 +213,8 @@ static __device__ __forceinline__ void attn_decode_body(const Q8AttnDecodeArgs &
         }
         m = mx;
     };
-    const int visible = min(position + 1, a.capacity);
-    const int per = (visible + a.splits - 1) / a.splits;
+    const int visible = min(position + 1, capacity_);
+    const int per = (visible + splits_ - 1) / splits_;
     const int begin = split * per;
     const int end = min(begin + per, visible);
     // A chunk's key and value rows, clamped to the last live row: rows past
@@ -211,8 +232,8 @@ static __device__ __forceinline__ void attn_decode_body(const Q8AttnDecodeArgs &
         }
     };
     if (begin < end) load_chunk(begin);
-    const f32x4 q0 = *(const f32x4 *)(a.q + (size_t)head * HD + 8 * kc);
-    const f32x4 q1 = *(const f32x4 *)(a.q + (size_t)head * HD + 8 * kc + 4);
+    const f32x4 q0 = *(const f32x4 *)(hd.q + (size_t)head * HD + 8 * kc);
+    const f32x4 q1 = *(const f32x4 *)(hd.q + (size_t)head * HD + 8 * kc + 4);
     __builtin_amdgcn_sched_barrier(0);
     for (int c0 = begin; c0 < end; c0 += RP * NP) {
         chunk(c0, end, q0, q1, ku, vu);
@@ -234,7 +255,7 @@ static __device__ __forceinline__ void attn_decode_body(const Q8AttnDecodeArgs &
     if (lane == 0) lsum[wave] = lw;
     __syncthreads();
     if (wave != 0) {
-        if (a.splits == 1 || a.defer) return;
+        if (splits_ == 1 || defer_) return;
     }
     float tot = 0.0f, sum = 0.0f;
     if (wave == 0) {
@@ -244,23 +265,23 @@ static __device__ __forceinline__ void attn_decode_body(const Q8AttnDecodeArgs &
         for (int w = 0; w < W; w++) sum += lsum[w];
     }
     const float mx = m;
-    const size_t base = (size_t)head * a.splits;
-    if (a.defer) {  // wave 0: the next kernel reads these after this one ends
-        a.part_acc[(base + split) * HD + lane] = tot;
+    const size_t base = (size_t)head * splits_;
+    if (defer_) {  // wave 0: the next kernel reads these after this one ends
+        part_acc_[(base + split) * HD + lane] = tot;
         if (lane == 0) {
-            *(f32x2 *)(a.part_ms + 2 * (base + split)) = (f32x2){mx, sum};
+            *(f32x2 *)(part_ms_ + 2 * (base + split)) = (f32x2){mx, sum};
         }
         return;
     }
-    if (a.splits == 1) {
+    if (splits_ == 1) {
         a.out[(size_t)head * HD + lane] = tot / sum;
         return;
     }
     if (wave == 0) {
-        store_agent(a.part_acc + (base + split) * HD + lane, tot);
+        store_agent(part_acc_ + (base + split) * HD + lane, tot);
         if (lane == 0) {
-            store_agent(a.part_ms + 2 * (base + split), mx);
-            store_agent(a.part_ms + 2 * (base + split) + 1, sum);
+            store_agent(part_ms_ + 2 * (base + split), mx);
+            store_agent(part_ms_ + 2 * (base + split) + 1, sum);
         }
     }
     // Release the partials at agent scope, count the arrival with an acq_rel
@@ -271,7 +292,7 @@ static __device__ __forceinline__ void attn_decode_body(const Q8AttnDecodeArgs &
     __syncthreads();
     if (tid == 0) {
         const unsigned old = __hip_atomic_fetch_add(&a.counters[head], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        last_flag = (old == (unsigned)(a.splits - 1));
+        last_flag = (old == (unsigned)(splits_ - 1));
     }
     __syncthreads();
     if (!last_flag) return;
@@ -279,18 +300,25 @@ static __device__ __forceinline__ void attn_decode_body(const Q8AttnDecodeArgs &
     if (tid == 0) __hip_atomic_store(&a.counters[head], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (wave != 0) return;
     float gmax = -INFINITY;
-    for (int s = 0; s < a.splits; s++) gmax = fmaxf(gmax, load_agent(a.part_ms + 2 * (base + s)));
+    for (int s = 0; s < splits_; s++) gmax = fmaxf(gmax, load_agent(part_ms_ + 2 * (base + s)));
     float num = 0.0f, den = 0.0f;
-    for (int s = 0; s < a.splits; s++) {
-        const float f = expf(load_agent(a.part_ms + 2 * (base + s)) - gmax);  // an empty split has max -inf: f = 0
-        den = __builtin_fmaf(load_agent(a.part_ms + 2 * (base + s) + 1), f, den);
-        num = __builtin_fmaf(load_agent(a.part_acc + (base + s) * HD + lane), f, num);
+    for (int s = 0; s < splits_; s++) {
+        const float f = expf(load_agent(part_ms_ + 2 * (base + s)) - gmax);  // an empty split has max -inf: f = 0
+        den = __builtin_fmaf(load_agent(part_ms_ + 2 * (base + s) + 1), f, den);
+        num = __builtin_fmaf(load_agent(part_acc_ + (base + s) * HD + lane), f, num);
     }
     a.out[(size_t)head * HD + lane] = num / den;
 }
 
-extern "C" __global__ __launch_bounds__(1024) void q8_attn_decode(Q8AttnDecodeArgs a) { attn_decode_body<16, 8>(a); }
-extern "C" __global__ __launch_bounds__(256) void q8_attn_decode_w4(Q8AttnDecodeArgs a) { attn_decode_body<4, 8>(a); }
+#define Q8_ATTN_PARAMS                                                                                     \
+    const float *q, const uint16_t *kcache, const uint16_t *vcache, const int *position, float *part_acc, int dims, \
+        int splits, int cap, Q8AttnDecodeArgs a
+extern "C" __global__ __launch_bounds__(1024) void q8_attn_decode(Q8_ATTN_PARAMS) {
+    attn_decode_body<16, 8>(AttnHead{q, kcache, vcache, position, part_acc, dims, splits, cap}, a);
+}
+extern "C" __global__ __launch_bounds__(256) void q8_attn_decode_w4(Q8_ATTN_PARAMS) {
+    attn_decode_body<4, 8>(AttnHead{q, kcache, vcache, position, part_acc, dims, splits, cap}, a);
+}
 
 // ---------------------------------------------------------------------------
 // Prefill attention: n query tokens at cache positions start .. start+n-1, each

@@ -2356,7 +2356,24 @@ int run_attn_decode(q8_ctx *c, const float *q, q8_dptr kcache, q8_dptr vcache, f
     a.scale = scale;
     a.defer = defer;
     const AttnShape sh = attn_shape(splits);
-    return launch(c, sh.fn, (unsigned)parts, sh.threads, 0, &a, sizeof a);
+    if (n_head > 0xffff || n_kv > 0xffff)
+        return fail(Q8_ERR_UNSUPPORTED, "attention: %d heads, %d key/value heads", n_head, n_kv);
+    // the kernel's preloaded head, then the argument block (scale, out, counters)
+    struct {
+        const float *q;
+        const uint16_t *kcache, *vcache;
+        const int *position;
+        float *part_acc;
+        int dims, splits, cap;
+    } h{a.q, a.kcache, a.vcache, a.position, a.part_acc, n_head | (n_kv << 16), splits,
+        (int)((unsigned)capacity | ((unsigned)(defer ? 1 : 0) << 31))};
+    static_assert(sizeof h == 56, "attention head: five pointers and three ints, padded to 8 bytes");
+    Q8_TRY(check_launch(*c->meta[sh.fn], sizeof h + sizeof a, sh.threads, 0, c->max_lds));
+    void *params[] = {&h.q, &h.kcache, &h.vcache, &h.position, &h.part_acc, &h.dims, &h.splits, &h.cap, &a};
+    HIP_TRY(hipModuleLaunchKernel(c->fn[sh.fn], (unsigned)parts, 1, 1, sh.threads, 1, 1, 0, c->stream, params,
+                                  nullptr),
+            kFnNames[sh.fn]);
+    return Q8_OK;
 }
 
 // Prompt attention (n >= 2): f32 rows into `out` and/or prepared Q8_0 into

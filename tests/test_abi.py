@@ -191,6 +191,8 @@ ARG_STRUCTS = {  # kernel name prefix -> the argument struct every kernel of tha
     # ints, 56 bytes with padding), then the GEMV argument block
     "q8_gemv_r8_": "head + Q8GemvArgs", "q8_gemv_r16_": "head + Q8GemvArgs", "q8_gemv_rc": "head + Q8GemvArgs",
     "q8_gemv_q8x": "head + Q8GemvArgs",
+    # the decode attention: a preloadable head (five pointers, three ints, 56 bytes), then its block
+    "q8_attn_decode": "head + Q8AttnDecodeArgs",
     "q8_gemm_": "Q8GemmArgs", "q8_gemv": "Q8GemvArgs", "q8_quantize": "Q8QuantArgs", "q8_rmsnorm": "Q8NormArgs",
     "q8_repack": "Q8RepackArgs", "q8_argmax": "Q8ArgmaxArgs", "q8_copy": "Q8CopyArgs", "q8_embed": "Q8EmbedArgs",
     "q8_silu_mul": "Q8EltArgs", "q8_rope_append": "Q8RopeArgs", "q8_attn_decode": "Q8AttnDecodeArgs",
