@@ -53,6 +53,11 @@ Also reported, each on its own rotation:
                 llama-bench does (apps/cli/src/bench.rs:83-229): pp512 and
                 tg128 tok/s, mean +- sample std over r = 5 repeats, with the
                 build's code object hash and the tactics its shapes run;
+  chain         (named only, not in the default set) the decoder's decode
+                step as its op chain launched eagerly, no graphs: 42 layers
+                of norm + q/k/v + RoPE, attention + O, norm + gate/up + SiLU,
+                down, then the head, 20 steps at 600 visible positions, for a
+                kernel trace of the launches the captured step replays;
   cpu_baseline  the oracle's C restatement of the reference rayon CPU path
                 (oracle/q8_oracle.c, AVX2 order) on this host's cores: the
                 configs[0] GEMV in GB/s and the configs[3] layer set in TOPS,
@@ -609,6 +614,53 @@ def bench_decoder(gpu, rng, prompt=512, steps=128, reps=5):
     return out
 
 
+def bench_decode_chain(gpu, steps=20, visible=600, splits=3):
+    """configs[4]'s decode step as its op chain launched eagerly (no graph): the
+    same calls q8_decoder_generate's captured step makes, for a kernel trace
+    (a kernel trace of the captured step itself aborted on the host; the
+    eager chain runs the same kernels, arguments and launch shapes).  Weights
+    generated on the device; returns the host time per step."""
+    heads, hd, cap, n_layer = 36, 64, 4096, 42
+    rng = np.random.default_rng(5)
+    names = (("q", HID, HID), ("k", HID, HID), ("v", HID, HID), ("o", HID, HID), ("g", HID, FFN), ("u", HID, FFN),
+             ("d", FFN, HID))
+    layers = []
+    for li in range(n_layer):
+        w = {n: gpu.weight_synthetic(k, out, 1000 * li + i) for i, (n, k, out) in enumerate(names)}
+        w["an"] = (1.0 + 0.1 * rng.standard_normal(HID)).astype(np.float32)
+        w["fn"] = (1.0 + 0.1 * rng.standard_normal(HID)).astype(np.float32)
+        w["kc"], w["vc"] = gpu.alloc(2 * cap * HID), gpu.alloc(2 * cap * HID)
+        layers.append(w)
+    head = gpu.weight_synthetic(HID, VOCAB, 77)
+    onorm = (1.0 + 0.1 * rng.standard_normal(HID)).astype(np.float32)
+    x, q, act = gpu.alloc(4 * HID), gpu.alloc(4 * HID), gpu.alloc(4 * FFN)
+    logits, tok, pos = gpu.alloc(4 * VOCAB), gpu.alloc(4), gpu.alloc(4)
+    x.upload(rng.standard_normal(HID).astype(np.float32))
+    pos.upload(np.array([visible - 1], np.int32))
+    scale = 1.0 / math.sqrt(hd)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        for w in layers:
+            gpu.norm_qkv_rope(w["an"], 1e-6, w["q"], w["k"], w["v"], x, 0, q, 0, w["kc"], w["vc"], heads, heads, hd,
+                              hd, 10000.0, cap, pos)
+            gpu.attention_matmul_add(q, w["kc"], w["vc"], heads, heads, hd, cap, scale, pos, splits, w["o"], x)
+            gpu.norm_gate_up_silu(w["fn"], 1e-6, w["g"], w["u"], x, 0, act, 0)
+            gpu.matmul(w["d"], act, 0, 1, x, 0, bias=x)
+        gpu.norm_lm_head_argmax(onorm, 1e-6, head, x, 0, logits, 0, tok)
+        gpu.sync()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    log(f"decode op chain, eager: {ms:.3f} ms a step (host clock; {steps} steps at {visible} positions)")
+    for w in layers:
+        for n, _, _ in names:
+            gpu.release_device(w[n])
+        w["kc"].free()
+        w["vc"].free()
+    gpu.release_device(head)
+    for b in (x, q, act, logits, tok, pos):
+        b.free()
+    return {"ms_per_step_host": round(ms, 3), "steps": steps, "visible": visible, "splits": splits}
+
+
 # ---------------------------------------------------------------------------
 # CPU baseline and counter calibration
 # ---------------------------------------------------------------------------
@@ -706,12 +758,12 @@ def main():
     ap.add_argument("--sustained-seconds", type=float, default=6.0,
                     help="configs[0] GEMV replayed back to back for this long after its trials (0: skip)")
     ap.add_argument("--sections", default="all",
-                    help="comma list of gemv,ceilings,reads,gemm,extras,decoder,cpu (default all); a profiler run "
-                         "names one so each kernel's average covers one workload")
+                    help="comma list of gemv,ceilings,reads,gemm,extras,decoder,cpu (default all) and chain (named "
+                         "only); a profiler run names one so each kernel's average covers one workload")
     args = ap.parse_args()
-    known = {"gemv", "ceilings", "reads", "gemm", "extras", "decoder", "cpu"}
-    sections = set(known) if args.sections == "all" else set(args.sections.split(","))
-    unknown = sections - known
+    default = {"gemv", "ceilings", "reads", "gemm", "extras", "decoder", "cpu"}
+    sections = set(default) if args.sections == "all" else set(args.sections.split(","))
+    unknown = sections - default - {"chain"}
     if unknown:
         ap.error(f"unknown sections {sorted(unknown)}")
     if args.gpus != 1:
@@ -744,6 +796,7 @@ def main():
         extras["configs2_decode_layer"] = layer
         extras["configs2_lm_head"] = head
     decoder = bench_decoder(gpu, rng) if "decoder" in sections else None
+    chain = bench_decode_chain(gpu) if "chain" in sections else None
     tactics = tactic_names(gpu)
     build = json.loads(q8.build_info())
     gpu.close()
@@ -799,6 +852,7 @@ def main():
         "ceilings": ceil,
         "extras": extras,
         "decoder_configs4": decoder,
+        "decode_chain": chain,
         "build": {"code_object_sha256": build["code_object_sha256"], "hipcc": build.get("hipcc"),
                   "tactics": tactics},
         "cpu_baseline": cpu,
