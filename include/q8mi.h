@@ -150,7 +150,10 @@ void *q8_stream(q8_ctx *ctx);
  * n; 1: f16 and the f16-MFMA GEMM for every n >= 2), "gemm.small_gemv" (0:
  * n = 2 on f32 x takes the GEMM), "gemm.stream" (0: a one-token-tile GEMM
  * reads its weights with the default cache policy instead of non-temporally;
- * the results are the same bits either way). */
+ * the results are the same bits either way), "gemv.group_hot" (0: the tile
+ * kernels for contiguous groups too), "gemv.group_pair" (0: a contiguous
+ * gate/up pair takes the two-slot row-slice kernel instead of its paired
+ * slices), "gemv.slice_copy" (0, set before residency: no slice-major copies). */
 int q8_set_option(q8_ctx *ctx, const char *name, int value);
 
 /* ---- device memory: Gpu::alloc / upload / download (cuda/mod.rs:530-567) ---- */
@@ -199,9 +202,32 @@ int q8_workspace_region(q8_ctx *ctx, int index, const char **name, uint64_t *off
  * repacks them on the device into the tile layout; cached by the host
  * identity (bytes, nbytes) exactly as `Weight::identity()` keys the
  * reference's cache (tensor.rs:40-42).  The handle lives until q8_close or
- * q8_weight_release. */
+ * q8_weight_release.  Where the weight's one-token GEMV runs in 8- or 16-row
+ * slices, the allocation also holds a slice-major copy of the quants (each
+ * slice's bytes in one run, read by that GEMV), so q8_weight_shape's
+ * device_bytes is then about twice the GGUF bytes; option gemv.slice_copy = 0
+ * (set before the upload) leaves the copy out. */
 int q8_weight_resident(q8_ctx *ctx, const void *gguf_bytes, size_t nbytes, int k, int out,
                        const q8_weight **weight);
+/* Weights of one k made resident together as a contiguous group (no
+ * counterpart in the reference, which uploads each tensor alone and groups
+ * them at call time: matmul_decode_group, compute.rs): the members' 32-row
+ * tiles lie back to back in one allocation, quants then scales, so an n = 1
+ * launch over the members in this order (q8_matmul_decode_group,
+ * q8_norm_matmul_decode_group, q8_norm_qkv_rope) loads from one set of bases
+ * its kernels take preloaded, in 16-row slices of a slice-major copy of the
+ * group.  pair = 1 (two members of one shape: gate, then up) builds the
+ * pair's paired copy instead -- slices of 8 gate rows and the same 8 up rows
+ * -- read by q8_gate_up_silu / q8_norm_gate_up_silu at n = 1.  Each member is
+ * a resident weight of its own, cached by its host identity (bytes[i],
+ * nbytes[i]) as q8_weight_resident caches it, usable alone and released one
+ * by one; the allocation goes with the last.  Q8_ERR_INVALID if a member is
+ * already resident.  Outputs equal those of separately resident weights bit
+ * for bit with "gemv.exact" = 1 and within 2e-6 + 1e-5 |ref| otherwise
+ * (another fixed summation order); option "gemv.group_hot" = 0 keeps the
+ * tile kernels for such groups. */
+int q8_weight_group_resident(q8_ctx *ctx, int count, const void *const *bytes, const size_t *nbytes, int k,
+                             const int *outs, int pair, const q8_weight **weights);
 int q8_weight_release(q8_ctx *ctx, const q8_weight *weight);
 int q8_weight_shape(const q8_weight *weight, int *k, int *out, size_t *device_bytes);
 /* Writes the resident weight back as GGUF bytes (inverse repack), so the

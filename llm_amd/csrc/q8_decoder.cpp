@@ -297,14 +297,30 @@ int q8_decoder_create_synthetic(q8_ctx *c, const q8_decoder_config *config, uint
         Layer &L = d->layers[l];
         const int dims[7][2] = {{E, g.n_head * g.head_dim}, {E, kv_dim},  {E, kv_dim}, {g.n_head * g.head_dim, E},
                                 {E, g.n_ff},                {E, g.n_ff}, {g.n_ff, E}};
-        for (int i = 0; i < 7; i++) {
-            // q/k/v and gate/up only run in groups (one launch over several
-            // matrices), so they need no slice-major copy; O and down run alone
-            const bool alone = i == Q8_DEC_O || i == Q8_DEC_DOWN;
-            rc = q8i::weight_synthetic(c, dims[i][0], dims[i][1], mix(seed + 1000003ull * (l + 1) + i), std_w, alone,
-                                       &L.w[i]);
+        auto wseed = [&](int i) { return mix(seed + 1000003ull * (l + 1) + i); };
+        // q/k/v and gate/up run as groups (one launch over several matrices):
+        // each is made a contiguous group, whose launches read one run of
+        // tiles from preloaded bases; O and down run alone, each with its
+        // slice-major copy
+        for (int i : {Q8_DEC_O, Q8_DEC_DOWN}) {
+            rc = q8i::weight_synthetic(c, dims[i][0], dims[i][1], wseed(i), std_w, true, &L.w[i]);
             if (rc) return fail(rc);
         }
+        const int qkv_rows[3] = {dims[Q8_DEC_Q][1], dims[Q8_DEC_K][1], dims[Q8_DEC_V][1]};
+        const uint64_t qkv_seeds[3] = {wseed(Q8_DEC_Q), wseed(Q8_DEC_K), wseed(Q8_DEC_V)};
+        const q8_weight *qkv[3] = {};
+        rc = q8i::weight_synthetic_group(c, E, 3, qkv_rows, qkv_seeds, std_w, q8i::group_slice_rows(c, E, 0), qkv);
+        if (rc) return fail(rc);
+        L.w[Q8_DEC_Q] = qkv[0];
+        L.w[Q8_DEC_K] = qkv[1];
+        L.w[Q8_DEC_V] = qkv[2];
+        const int ffn_rows[2] = {g.n_ff, g.n_ff};
+        const uint64_t ffn_seeds[2] = {wseed(Q8_DEC_GATE), wseed(Q8_DEC_UP)};
+        const q8_weight *ffn[2] = {};
+        rc = q8i::weight_synthetic_group(c, E, 2, ffn_rows, ffn_seeds, std_w, q8i::group_pair_slices(c, E), ffn);
+        if (rc) return fail(rc);
+        L.w[Q8_DEC_GATE] = ffn[0];
+        L.w[Q8_DEC_UP] = ffn[1];
         L.attn_norm = norm_weights(mix(seed + 7919ull * (l + 1)), E);
         L.ffn_norm = norm_weights(mix(seed + 104729ull * (l + 1)), E);
         const size_t cache = (size_t)g.capacity * kv_dim * 2;

@@ -91,8 +91,16 @@ extern "C" __global__ __launch_bounds__(256) void q8_slice_copy(Q8SliceArgs a) {
     const int b = (int)(unit % a.nb);
     const long long g = unit / a.nb;
     const int h = lane >> 5, r = lane & 31;
-    const int s = r / a.rs, rr = r % a.rs;
-    const long long dst = ((g * (Q8_TILE_ROWS / a.rs) + s) * a.nb + b) * (a.rs * 32) + (a.rs * h + rr) * 16;
+    long long dst;
+    if (a.pair_tiles) {  // gate rows 8s.. of tile t, then the same up rows
+        const int up = g >= a.pair_tiles;
+        const long long t = g - (up ? a.pair_tiles : 0);
+        const int s = r >> 3;
+        dst = ((t * 4 + s) * a.nb + b) * 512 + (16 * h + 8 * up + (r & 7)) * 16;
+    } else {
+        const int s = r / a.rs, rr = r % a.rs;
+        dst = ((g * (Q8_TILE_ROWS / a.rs) + s) * a.nb + b) * (a.rs * 32) + (a.rs * h + rr) * 16;
+    }
     *reinterpret_cast<i32x4 *>(a.dst + dst) = *reinterpret_cast<const i32x4 *>(a.src + i * 16);
 }
 
@@ -1341,9 +1349,33 @@ Q8_GEMV_Q8X_TOKENS(2)
 // selection, folded norm and epilogues.  In exact mode the outputs are
 // therefore bit-identical to the multi-matrix tile kernels' (q8_gemv_pb*_e1);
 // EX = 0 sums the block values in gemv_rs_body's fixed tree.
+//
+// HOT: the contiguous-group builds (q8_gemv_hg*, q8_gemv_hs*).  The members'
+// 32-row tiles lie back to back in one allocation -- their quants, their
+// scales and, where the group has one, its slice-major copy (Q8SliceArgs) --
+// so a wave's loads need only the group's bases: global tile t of the group
+// is tile t of one matrix, and the up member of a SILU pair starts up_off
+// tiles after the gate.  Those bases, x, the norm weight and the position
+// arrive as the kernel's first scalar arguments (RsgHot), which the code
+// object preloads into SGPRs, so the weight stream starts without reading
+// the argument block; the member selection of the epilogue reads the block
+// after the weight loads are out.  Same arithmetic and order as the other
+// builds, so the outputs are bit-identical to them.
 // ---------------------------------------------------------------------------
-template <int RS, int NL, int EX, int SILU>
-static __device__ __forceinline__ void gemv_rsg_body(const Q8GemvArgs &a) {
+struct RsgHot {
+    const uint8_t *mq;   // the group's slice-major copy (tiles_xo bit 30) or its unit-layout quants
+    const uint16_t *msc; // the group's scales
+    const float *xg;
+    const float *norm_w;  // folded RMSNorm weight, or null
+    const int *rope_pos;  // RoPE + KV append position, or null
+    int nbw;              // nb | waves per slot << 16
+    int tiles_xo;         // total tiles | slice_major << 30 | xcd_order << 31
+    int up_off;           // SILU: first tile of the up member
+    int hpad;
+};
+
+template <int RS, int NL, int EX, int SILU, int HOT = 0>
+static __device__ __forceinline__ void gemv_rsg_body(const RsgHot &hot, const Q8GemvArgs &a) {
     extern __shared__ __attribute__((aligned(16))) float smem[];
     constexpr int LPB = 2 * RS;
     constexpr int BPL = 64 / LPB;
@@ -1352,24 +1384,14 @@ static __device__ __forceinline__ void gemv_rsg_body(const Q8GemvArgs &a) {
     constexpr int XS = (BPW * 8 + 63) / 64;  // x float4s a lane stages
     constexpr int NSLOT = SILU ? 2 : 1;
     static_assert(BPW * 8 <= 64 * Q8_GEMV_STAGE, "x range of a wave exceeds its staging registers");
-    const int nb = a.nb;
-    const int members = a.members;
-    const int nw = a.waves_per_tile;  // waves per slot
-    const float *xg = a.x;
-    const uint8_t *q_[Q8_GROUP_MAX];
-    const uint16_t *sc_[Q8_GROUP_MAX];
-    float *y_[Q8_GROUP_MAX];
-    const float *bias_[Q8_GROUP_MAX];
-    int rows_[Q8_GROUP_MAX], tb_[Q8_GROUP_MAX];
-#pragma unroll
-    for (int i = 0; i < Q8_GROUP_MAX; i++) {
-        q_[i] = a.m[i].quants;
-        sc_[i] = a.m[i].scales;
-        y_[i] = a.m[i].y;
-        bias_[i] = a.m[i].bias;
-        rows_[i] = a.m[i].rows;
-        tb_[i] = a.m[i].tile_begin;
-    }
+    const int nb = HOT ? hot.nbw & 0xffff : a.nb;
+    const int nw = HOT ? hot.nbw >> 16 : a.waves_per_tile;  // waves per slot
+    const float *xg = HOT ? hot.xg : a.x;
+    const int total_tiles = HOT ? hot.tiles_xo & 0x3fffffff : a.total_tiles;
+    const int xo = HOT ? (int)((unsigned)hot.tiles_xo >> 31) : a.xcd_order;
+    const bool sm = HOT && ((hot.tiles_xo >> 30) & 1);
+    const float *norm_w = HOT ? hot.norm_w : a.norm_w;
+    const int *rope_pos = HOT ? hot.rope_pos : a.rope_pos;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int slot = (SILU && wave >= nw) ? 1 : 0;
@@ -1378,37 +1400,57 @@ static __device__ __forceinline__ void gemv_rsg_body(const Q8GemvArgs &a) {
     const int h = (lane / RS) & 1;
     const int r = lane % RS;
     const int bx = blockIdx.x;
-    const int xo = a.xcd_order;
     const int gtile = xo ? (bx / (8 * SPT)) * 8 + (bx & 7) : bx / SPT;
     const int slice = xo ? (bx >> 3) % SPT : bx % SPT;
-    if (gtile >= a.total_tiles) return;  // padding of the XCD order, whole workgroup
-    int by_tile = 0;
+    if (gtile >= total_tiles) return;  // padding of the XCD order, whole workgroup
+    // the member of this workgroup's rows (SILU: of this wave's slot)
+    int mi = 0, mrows = 0, mtb = 0;
+    const uint8_t *mq = nullptr;
+    const uint16_t *msc = nullptr;
+    float *my = nullptr;
+    const float *mbias = nullptr;
+    auto select_member = [&]() {
+        const int members = a.members;
+        int by_tile = 0;
 #pragma unroll
-    for (int i = 1; i < Q8_GROUP_MAX; i++) by_tile += (int)(i < members) & (int)(gtile >= tb_[i]);
-    const int mi = SILU ? slot : by_tile;
-    const uint8_t *mq = q_[0];
-    const uint16_t *msc = sc_[0];
-    float *my = y_[0];
-    const float *mbias = bias_[0];
-    int mrows = rows_[0];
-    int mtb = tb_[0];
+        for (int i = 1; i < Q8_GROUP_MAX; i++) by_tile += (int)(i < members) & (int)(gtile >= a.m[i].tile_begin);
+        mi = SILU ? slot : by_tile;
+        mq = a.m[0].quants;
+        msc = a.m[0].scales;
+        my = a.m[0].y;
+        mbias = a.m[0].bias;
+        mrows = a.m[0].rows;
+        mtb = a.m[0].tile_begin;
 #pragma unroll
-    for (int i = 1; i < Q8_GROUP_MAX; i++) {
-        const bool take = mi == i;
-        mq = take ? q_[i] : mq;
-        msc = take ? sc_[i] : msc;
-        my = take ? y_[i] : my;
-        mbias = take ? bias_[i] : mbias;
-        mrows = take ? rows_[i] : mrows;
-        mtb = take ? tb_[i] : mtb;
-    }
-    const int tile = SILU ? gtile : gtile - mtb;
+        for (int i = 1; i < Q8_GROUP_MAX; i++) {
+            const bool take = mi == i;
+            mq = take ? a.m[i].quants : mq;
+            msc = take ? a.m[i].scales : msc;
+            my = take ? a.m[i].y : my;
+            mbias = take ? a.m[i].bias : mbias;
+            mrows = take ? a.m[i].rows : mrows;
+            mtb = take ? a.m[i].tile_begin : mtb;
+        }
+    };
     const int srow = slice * RS + r;
     const int b_begin = w * BPW;
     const int b_end = min(nb, b_begin + BPW);
     const int b_last = max(b_end - 1, 0);
-    const uint8_t *qbase = mq + (size_t)tile * nb * Q8_UNIT_BYTES + 16 * (32 * h + srow);
-    const uint16_t *sbase = msc + (size_t)tile * nb * Q8_TILE_ROWS + srow;
+    const uint8_t *qbase;
+    const uint16_t *sbase;
+    size_t qstride = Q8_UNIT_BYTES;
+    if constexpr (HOT) {
+        const int lt = SILU ? gtile + slot * hot.up_off : gtile;  // the group's own tile
+        qbase = sm ? hot.mq + ((size_t)lt * SPT + slice) * nb * (RS * 32) + 16 * (lane % LPB)
+                   : hot.mq + (size_t)lt * nb * Q8_UNIT_BYTES + 16 * (32 * h + srow);
+        qstride = sm ? (size_t)(RS * 32) : (size_t)Q8_UNIT_BYTES;
+        sbase = hot.msc + (size_t)lt * nb * Q8_TILE_ROWS + srow;
+    } else {
+        select_member();
+        const int tile = SILU ? gtile : gtile - mtb;
+        qbase = mq + (size_t)tile * nb * Q8_UNIT_BYTES + 16 * (32 * h + srow);
+        sbase = msc + (size_t)tile * nb * Q8_TILE_ROWS + srow;
+    }
     const int vrow = Q8_GEMV_VROW(nb);
     float *xs = smem;              // nb * 32 floats, permuted
     float *vbuf = smem + nb * 32;  // EX: [NSLOT][RS][vrow] block values; else [NSLOT * nw][RS] wave sums
@@ -1427,19 +1469,19 @@ static __device__ __forceinline__ void gemv_rsg_body(const Q8GemvArgs &a) {
     // 0..255 from x loads issued before the weights and summed after; EX
     // stages (x * scale) * w after a barrier, bit-identical to the tile
     // kernel, else x * w with the scale applied to the row sums
-    const bool norm = a.norm_w != nullptr;  // kernel-uniform
-    const int rope_position = a.rope_pos ? *a.rope_pos : 0;
+    const bool norm = norm_w != nullptr;  // kernel-uniform
+    const int rope_position = rope_pos ? *rope_pos : 0;
     f32x4 wv[Q8_GEMV_STAGE];
-    f32x4 nx[Q8_NORM_ROW_VEC];
+    f32x4 nx[Q8_RSG_NORM_VEC];
     const int nv = nb * 8;
     if (norm) {
-        const f32x4 *nwp = reinterpret_cast<const f32x4 *>(a.norm_w);
+        const f32x4 *nwp = reinterpret_cast<const f32x4 *>(norm_w);
 #pragma unroll
         for (int u = 0; u < XS; u++) wv[u] = nwp[min(st_begin + lane + 64 * u, st_clamp)];
         if (threadIdx.x < 256) {
             const f32x4 *xr = reinterpret_cast<const f32x4 *>(xg);
 #pragma unroll
-            for (int jj = 0; jj < Q8_NORM_ROW_VEC; jj++) {  // only the float4s the sum takes
+            for (int jj = 0; jj < Q8_RSG_NORM_VEC; jj++) {  // only the float4s the sum takes
                 if ((int)threadIdx.x + 256 * jj < nv) nx[jj] = xr[threadIdx.x + 256 * jj];
             }
         }
@@ -1451,15 +1493,17 @@ static __device__ __forceinline__ void gemv_rsg_body(const Q8GemvArgs &a) {
 #pragma unroll
     for (int i = 0; i < NL; i++) {
         const int b = min(b_begin + i * BPL + j, b_last);
-        qv[i] = q8_weight_load(qbase + (size_t)b * Q8_UNIT_BYTES);
+        qv[i] = q8_weight_load(qbase + (size_t)b * qstride);
         dd[i] = (unsigned)sbase[(size_t)b * Q8_TILE_ROWS];
     }
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (HOT) select_member();  // the epilogue's member, read while the weights stream in
+    const int tile = SILU ? gtile : gtile - mtb;  // within the member
     __shared__ double npart[4];
     if (norm && threadIdx.x < 256) {
         double ss = 0.0;
 #pragma unroll
-        for (int jj = 0; jj < Q8_NORM_ROW_VEC; jj++) {
+        for (int jj = 0; jj < Q8_RSG_NORM_VEC; jj++) {
             if ((int)threadIdx.x + 256 * jj < nv) {
 #pragma unroll
                 for (int e = 0; e < 4; e++) ss += (double)(nx[jj][e] * nx[jj][e]);
@@ -1549,7 +1593,7 @@ static __device__ __forceinline__ void gemv_rsg_body(const Q8GemvArgs &a) {
     const int row = tile * Q8_TILE_ROWS + srow;
     if constexpr (SILU) {
         if (row < mrows) my[row] = silu_f32(sums[0]) * sums[1];
-    } else if (a.rope_pos) {
+    } else if (rope_pos) {
         // gemv_body's RoPE + KV append: rows 2i and 2i+1 of a head are lanes
         // r and r ^ 1 of wave 0 (RS is even, slices start at even rows)
         const float other = __shfl_xor(sums[0], 1);
@@ -1582,18 +1626,209 @@ static __device__ __forceinline__ void gemv_rsg_body(const Q8GemvArgs &a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Row-slice GEMV over a contiguous gate/up pair (q8_gemv_hp16_l*; SILU pair:
+// y = silu(gate . x) * (up . x)) reading the pair's paired copy
+// (Q8SliceArgs::pair_tiles): a workgroup owns slice s of tile t, i.e. gate
+// rows 32t + 8s .. + 7 and the same up rows, 16 rows a wave load as in
+// gemv_rs_body's 16-row slices, so it has the whole K range of both members
+// of each of its 8 outputs and no slot of idle waves.  Lane r < 8 of the
+// tail wave takes its up row from lane r + 8.  Without the copy (sm = 0) the
+// lanes read their rows from the unit layout.  The block values, their
+// order and the folded norm are gemv_rsg_body's, so exact mode matches the
+// tile kernels bit for bit.
+// ---------------------------------------------------------------------------
+template <int NL, int EX>
+static __device__ __forceinline__ void gemv_rsp_body(const RsgHot &hot, const Q8GemvArgs &a) {
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    constexpr int RS = 16;                  // rows a slice: 8 gate + 8 up
+    constexpr int LPB = 2 * RS;
+    constexpr int BPL = 64 / LPB;
+    constexpr int SPT = 4;                  // slices a tile pair
+    constexpr int BPW = NL * BPL;
+    constexpr int XS = (BPW * 8 + 63) / 64;
+    static_assert(BPW * 8 <= 64 * Q8_GEMV_STAGE, "x range of a wave exceeds its staging registers");
+    const int nb = hot.nbw & 0xffff;
+    const int nw = hot.nbw >> 16;
+    const float *xg = hot.xg;
+    const int total_tiles = hot.tiles_xo & 0x3fffffff;
+    const int xo = (int)((unsigned)hot.tiles_xo >> 31);
+    const bool sm = (hot.tiles_xo >> 30) & 1;
+    const float *norm_w = hot.norm_w;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int j = lane / LPB;
+    const int h = (lane / RS) & 1;
+    const int r = lane % RS;
+    const int bx = blockIdx.x;
+    const int tile = xo ? (bx / (8 * SPT)) * 8 + (bx & 7) : bx / SPT;
+    const int slice = xo ? (bx >> 3) % SPT : bx % SPT;
+    if (tile >= total_tiles) return;  // padding of the XCD order, whole workgroup
+    const int up = r >> 3;             // 0: a gate row, 1: an up row
+    const int mrow = 8 * slice + (r & 7);  // the row within its member's tile
+    const int mt = tile + (up ? hot.up_off : 0);
+    const int b_begin = wave * BPW;
+    const int b_end = min(nb, b_begin + BPW);
+    const int b_last = max(b_end - 1, 0);
+    const uint8_t *qbase = sm ? hot.mq + ((size_t)tile * SPT + slice) * nb * (RS * 32) + 16 * (lane % LPB)
+                              : hot.mq + (size_t)mt * nb * Q8_UNIT_BYTES + 16 * (32 * h + mrow);
+    const size_t qstride = sm ? (size_t)(RS * 32) : (size_t)Q8_UNIT_BYTES;
+    const uint16_t *sbase = hot.msc + (size_t)mt * nb * Q8_TILE_ROWS + mrow;
+    const int vrow = Q8_GEMV_VROW(nb);
+    float *xs = smem;              // nb * 32 floats, permuted
+    float *vbuf = smem + nb * 32;  // EX: [RS][vrow] block values; else [nw][RS] wave sums
+    float *pad = vbuf + (EX ? RS * vrow : nw * RS);
+
+    const int st_begin = 8 * b_begin;
+    const int st_end = 8 * b_end;
+    const int st_clamp = max(st_end - 1, 0);
+    f32x4 xv[Q8_GEMV_STAGE];
+#pragma unroll
+    for (int u = 0; u < XS; u++) {
+        const float *xp = xg + 4 * min(st_begin + lane + 64 * u, st_clamp);
+        xv[u] = (f32x4){xp[0], xp[1], xp[2], xp[3]};
+    }
+    // the folded norm, as gemv_rsg_body's
+    const bool norm = norm_w != nullptr;  // kernel-uniform
+    f32x4 wv[Q8_GEMV_STAGE];
+    f32x4 nx[Q8_RSG_NORM_VEC];
+    const int nv = nb * 8;
+    if (norm) {
+        const f32x4 *nwp = reinterpret_cast<const f32x4 *>(norm_w);
+#pragma unroll
+        for (int u = 0; u < XS; u++) wv[u] = nwp[min(st_begin + lane + 64 * u, st_clamp)];
+        if (threadIdx.x < 256) {
+            const f32x4 *xr = reinterpret_cast<const f32x4 *>(xg);
+#pragma unroll
+            for (int jj = 0; jj < Q8_RSG_NORM_VEC; jj++) {
+                if ((int)threadIdx.x + 256 * jj < nv) nx[jj] = xr[threadIdx.x + 256 * jj];
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    i32x4 qv[NL];
+    unsigned dd[NL];
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+        const int b = min(b_begin + i * BPL + j, b_last);
+        qv[i] = q8_weight_load(qbase + (size_t)b * qstride);
+        dd[i] = (unsigned)sbase[(size_t)b * Q8_TILE_ROWS];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __shared__ double npart[4];
+    if (norm && threadIdx.x < 256) {
+        double ss = 0.0;
+#pragma unroll
+        for (int jj = 0; jj < Q8_RSG_NORM_VEC; jj++) {
+            if ((int)threadIdx.x + 256 * jj < nv) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) ss += (double)(nx[jj][e] * nx[jj][e]);
+            }
+        }
+        ss = xor_add_f64<32>(ss);
+        ss = xor_add_f64<16>(ss);
+        ss = xor_add_f64<8>(ss);
+        ss = xor_add_f64<4>(ss);
+        ss = xor_add_f64<2>(ss);
+        ss = xor_add_f64<1>(ss);
+        if (lane == 0) npart[wave] = ss;
+    }
+    if (norm) {
+        float nscale = 1.0f;
+        if constexpr (EX) {
+            __syncthreads();
+            nscale = norm_scale(npart, nb * 32, a.norm_eps);
+        }
+#pragma unroll
+        for (int u = 0; u < XS; u++) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) xv[u][e] = EX ? (xv[u][e] * nscale) * wv[u][e] : xv[u][e] * wv[u][e];
+        }
+    }
+    if (EX && wave == 0 && lane < RS) {
+        for (int b = nb; b < ((nb + 3) & ~3); b++) vbuf[r * vrow + b] = 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < XS; u++) {
+        if (64 * u < st_end - st_begin) {
+            const int i = st_begin + lane + 64 * u;
+            float *d = i < st_end ? xs + (i >> 3) * 32 + ((i & 7) >> 1) + 4 * (i & 1) : pad;
+            d[0] = xv[u].x;
+            d[8] = xv[u].y;
+            d[16] = xv[u].z;
+            d[24] = xv[u].w;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    float lsum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+        const int bu = b_begin + i * BPL + j;
+        const int b = min(bu, b_last);
+        const float p = half_partial(qv[i], (const f32x4 *)(xs + b * 32 + h * 16));
+        const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(p), __float_as_uint(p), false, false);
+        const float s01 = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        const float v = f16_to_f32(dd[i]) * s01;
+        if constexpr (EX) {
+            *((h == 0 && bu < b_end) ? vbuf + r * vrow + bu : pad) = v;
+        } else {
+            lsum = bu < b_end ? lsum + v : lsum;
+        }
+    }
+    if constexpr (!EX) {
+        if constexpr (BPL >= 2) lsum = xor_add<32>(lsum);
+        if (lane < RS) vbuf[wave * RS + r] = lsum;
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    float sum = 0.0f;
+    if (lane < RS) {
+        if constexpr (EX) {
+            sum = chain_row(vbuf + r * vrow, nb);
+        } else {
+            sum = vbuf[r];
+            for (int w2 = 1; w2 < nw; w2++) sum = sum + vbuf[w2 * RS + r];
+        }
+        if (!EX && norm) sum *= norm_scale(npart, nb * 32, a.norm_eps);
+    }
+    const float upv = __shfl_down(sum, 8);  // lane r < 8: its up row's sum
+    const int row = tile * Q8_TILE_ROWS + mrow;
+    if (lane < 8 && row < a.m[0].rows) a.m[0].y[row] = silu_f32(sum) * upv;
+}
+
+#define Q8_RSG_PARAMS                                                                                   \
+    const uint8_t *mq, const uint16_t *msc, const float *xg, const float *norm_w, const int *rope_pos, int nbw, \
+        int tiles_xo, int up_off, int hpad, Q8GemvArgs a
 #define Q8_GEMV_RSG_KERNEL(KIND, SILU, RS, NL)                                                                  \
     extern "C" __global__ __launch_bounds__(1024) void q8_gemv_##KIND##RS##_l##NL(Q8GemvArgs a) {            \
-        gemv_rsg_body<RS, NL, 1, SILU>(a);                                                                     \
+        gemv_rsg_body<RS, NL, 1, SILU>(RsgHot{}, a);                                                           \
     }                                                                                                          \
     extern "C" __global__ __launch_bounds__(1024) void q8_gemv_##KIND##RS##_l##NL##_e0(Q8GemvArgs a) {       \
-        gemv_rsg_body<RS, NL, 0, SILU>(a);                                                                     \
+        gemv_rsg_body<RS, NL, 0, SILU>(RsgHot{}, a);                                                           \
+    }                                                                                                          \
+    extern "C" __global__ __launch_bounds__(1024) void q8_gemv_h##KIND##RS##_l##NL(Q8_RSG_PARAMS) {          \
+        gemv_rsg_body<RS, NL, 1, SILU, 1>(RsgHot{mq, msc, xg, norm_w, rope_pos, nbw, tiles_xo, up_off, hpad}, a); \
+    }                                                                                                          \
+    extern "C" __global__ __launch_bounds__(1024) void q8_gemv_h##KIND##RS##_l##NL##_e0(Q8_RSG_PARAMS) {     \
+        gemv_rsg_body<RS, NL, 0, SILU, 1>(RsgHot{mq, msc, xg, norm_w, rope_pos, nbw, tiles_xo, up_off, hpad}, a); \
     }
 Q8_GEMV_RSG_KERNEL(g, 0, 8, 3)
 Q8_GEMV_RSG_KERNEL(g, 0, 16, 3)
 Q8_GEMV_RSG_KERNEL(g, 0, 16, 6)
 Q8_GEMV_RSG_KERNEL(s, 1, 8, 3)
 Q8_GEMV_RSG_KERNEL(s, 1, 16, 6)
+#define Q8_GEMV_RSP_KERNEL(NL)                                                                     \
+    extern "C" __global__ __launch_bounds__(1024) void q8_gemv_hp16_l##NL(Q8_RSG_PARAMS) {      \
+        gemv_rsp_body<NL, 1>(RsgHot{mq, msc, xg, norm_w, rope_pos, nbw, tiles_xo, up_off, hpad}, a); \
+    }                                                                                              \
+    extern "C" __global__ __launch_bounds__(1024) void q8_gemv_hp16_l##NL##_e0(Q8_RSG_PARAMS) { \
+        gemv_rsp_body<NL, 0>(RsgHot{mq, msc, xg, norm_w, rope_pos, nbw, tiles_xo, up_off, hpad}, a); \
+    }
+Q8_GEMV_RSP_KERNEL(3)
+Q8_GEMV_RSP_KERNEL(6)
 
 // ---------------------------------------------------------------------------
 // Activation quantization (quant.rs:98-121), into the prepared tile layout.

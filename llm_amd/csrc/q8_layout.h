@@ -95,13 +95,20 @@ typedef struct {
  *     slices + (g * (32 / RS) + s) * nb * RS * 32;
  *   block b of it at + b * RS * 32, row r' of half h at + (RS * h + r') * 16,
  * the 16 bytes the unit layout holds at unit(g, b) + 16 * (32 h + RS s + r').
- * Scales stay in the unit layout's plane. */
+ * Scales stay in the unit layout's plane.
+ *
+ * The paired copy of a gate/up pair (pair_tiles = T: gate tiles 0 .. T - 1
+ * then up tiles T .. 2T - 1 in src, RS = 16): slice (t, s), s < 4, holds gate
+ * rows 32t + 8s .. + 7 as its rows 0..7 and the same up rows as its rows
+ * 8..15, at dst + (t * 4 + s) * nb * 512, block b at + b * 512, row r' of
+ * half h at + (16 h + r') * 16, so one wave holds a gate row and its up row. */
 typedef struct {
     const uint8_t *src; /* unit-layout quants, tiles * nb units */
     uint8_t *dst;       /* slice-major copy, the same byte count */
     int nb;
     int tiles;
     int rs;             /* rows per slice: 8 or 16 */
+    int pair_tiles;     /* 0, or T: the paired copy of a gate/up pair (tiles = 2T, rs = 16) */
 } Q8SliceArgs;
 
 typedef struct {
@@ -171,6 +178,9 @@ typedef struct {
 
 /* float4s per thread of the 256-thread row RMSNorm (k <= 1024 * this). */
 #define Q8_NORM_ROW_VEC 8
+/* The same for the norm folded into the group row-slice GEMVs, which hold
+ * these x float4s in registers across their weight loads: k <= 1024 * this. */
+#define Q8_RSG_NORM_VEC 3
 // floats per block of the normalized row q8_rmsnorm_row stages in LDS for its
 // prepared output (a block's 32 plus a pad against bank conflicts)
 #define Q8_NORM_LDS_PITCH 36

@@ -94,6 +94,9 @@ enum Fn {
     F_EMBED,
     F_ROPE, F_ATTN_DECODE, F_ATTN_DECODE_W4, F_ATTN_PREFILL, F_SYNTH, F_ADVANCE,
     F_SLICE_COPY,
+    F_GEMV_HG8_3, F_GEMV_HG16_3, F_GEMV_HG16_6, F_GEMV_HS8_3, F_GEMV_HS16_6,
+    F_GEMV_HG8_3_E0, F_GEMV_HG16_3_E0, F_GEMV_HG16_6_E0, F_GEMV_HS8_3_E0, F_GEMV_HS16_6_E0,
+    F_GEMV_HP16_3, F_GEMV_HP16_6, F_GEMV_HP16_3_E0, F_GEMV_HP16_6_E0,
     F_COUNT
 };
 
@@ -129,6 +132,9 @@ const char *const kFnNames[F_COUNT] = {
     "q8_embed",
     "q8_rope_append", "q8_attn_decode", "q8_attn_decode_w4", "q8_attn_prefill", "q8_synth", "q8_advance",
     "q8_slice_copy",
+    "q8_gemv_hg8_l3", "q8_gemv_hg16_l3", "q8_gemv_hg16_l6", "q8_gemv_hs8_l3", "q8_gemv_hs16_l6",
+    "q8_gemv_hg8_l3_e0", "q8_gemv_hg16_l3_e0", "q8_gemv_hg16_l6_e0", "q8_gemv_hs8_l3_e0", "q8_gemv_hs16_l6_e0",
+    "q8_gemv_hp16_l3", "q8_gemv_hp16_l6", "q8_gemv_hp16_l3_e0", "q8_gemv_hp16_l6_e0",
 };
 
 // Every kernel of the code object with its metadata (q8_manifest.h, from the
@@ -193,6 +199,8 @@ struct q8_weight {
     size_t id_len;
     uint8_t *slices = nullptr;  // slice-major copy of the quants (Q8SliceArgs), or none
     int slice_rows = 0;         // its rows per slice: 8 or 16
+    int *group_refs = nullptr;  // a member of a contiguous group: the members still holding `base`
+    uint8_t *pair_slices = nullptr;  // the gate of a contiguous gate/up pair: the pair's paired copy (Q8SliceArgs)
 };
 
 struct q8_ctx {
@@ -283,6 +291,29 @@ int launch_rs(q8_ctx *c, Fn f, unsigned grid, unsigned block, unsigned lds, RsHe
     if (grid == 0) return Q8_OK;
     Q8_TRY(check_launch(*c->meta[f], sizeof(RsHead) + sizeof(Q8GemvArgs), block, lds, c->max_lds));
     void *params[] = {&h.mq, &h.msc, &h.my, &h.mbias, &h.xg, &h.mrows, &h.nbw, &h.tiles_xo, &h.ms_off, &a};
+    HIP_TRY(hipModuleLaunchKernel(c->fn[f], grid, 1, 1, block, 1, 1, lds, c->stream, params, nullptr),
+            kFnNames[f]);
+    return Q8_OK;
+}
+
+// The contiguous-group row-slice GEMVs' preloaded head (RsgHot in
+// q8_kernels.hip): the group's load bases, x, the norm weight and the RoPE
+// position, then nb | waves per slot << 16, total tiles | slice_major << 30 |
+// xcd_order << 31 and the up member's first tile.
+struct RsgHead {
+    const uint8_t *mq;
+    const uint16_t *msc;
+    const float *xg;
+    const float *norm_w;
+    const int *rope_pos;
+    int nbw, tiles_xo, up_off, hpad;
+};
+static_assert(sizeof(RsgHead) == 56, "group row-slice head: five pointers and four ints");
+
+int launch_rsg(q8_ctx *c, Fn f, unsigned grid, unsigned block, unsigned lds, RsgHead &h, Q8GemvArgs &a) {
+    if (grid == 0) return Q8_OK;
+    Q8_TRY(check_launch(*c->meta[f], sizeof(RsgHead) + sizeof(Q8GemvArgs), block, lds, c->max_lds));
+    void *params[] = {&h.mq, &h.msc, &h.xg, &h.norm_w, &h.rope_pos, &h.nbw, &h.tiles_xo, &h.up_off, &h.hpad, &a};
     HIP_TRY(hipModuleLaunchKernel(c->fn[f], grid, 1, 1, block, 1, 1, lds, c->stream, params, nullptr),
             kFnNames[f]);
     return Q8_OK;
@@ -469,6 +500,39 @@ struct Member {
     float *y;
 };
 
+// weight_synthetic_group's slice_rows for a gate/up pair's paired copy.
+constexpr int kPairSlices = q8i::kGroupPairSlices;
+// Loads a lane of the paired gate/up kernels (q8_gemv_hp16_l3 / _l6) at nb
+// blocks a row, at most 16 waves; 0 where neither fits.
+int pair_loads(int nb) { return nb <= 96 ? 3 : nb <= 192 ? 6 : 0; }
+int build_group(q8_ctx *c, int k, int count, const int *outs, const void *const *bytes, const size_t *nbytes,
+                const uint64_t *seeds, float scale_std, int slice_rows, const q8_weight **weights);
+
+// Whether a launch's members lie back to back in one allocation (made by
+// group residency, q8i::weight_synthetic_group): member i's quants and
+// scales start where member i - 1's tiles end, and so does its slice-major
+// copy where every member has one of the same height (*slice_rows, else 0).
+// Such a group runs the contiguous-group row-slice kernels unless option
+// "gemv.group_hot" is 0.
+bool contiguous_group(q8_ctx *c, const Member *m, int count, int *slice_rows) {
+    if (count < 2 || !option(c, "gemv.group_hot", 1)) return false;
+    const q8_weight *w0 = m[0].w;
+    const uintptr_t q0 = (uintptr_t)w0->quants, s0 = (uintptr_t)w0->scales, l0 = (uintptr_t)w0->slices;
+    const size_t nb = (size_t)w0->nb;
+    size_t t = 0;
+    bool sl = w0->slices != nullptr;
+    for (int i = 0; i < count; i++) {
+        const q8_weight *w = m[i].w;
+        if (w->nb != w0->nb || (uintptr_t)w->quants != q0 + t * nb * Q8_UNIT_BYTES ||
+            (uintptr_t)w->scales != s0 + t * nb * Q8_TILE_ROWS * 2)
+            return false;
+        sl = sl && w->slices && w->slice_rows == w0->slice_rows && (uintptr_t)w->slices == l0 + t * nb * Q8_UNIT_BYTES;
+        t += (size_t)w->tiles;
+    }
+    *slice_rows = sl ? w0->slice_rows : 0;
+    return true;
+}
+
 // n = 1 over up to four weights sharing x; silu = 1 fuses silu(m0)*m1 into y of m0.
 // The RoPE + KV append epilogue of a q, k, v decode group.
 struct GemvRope {
@@ -552,8 +616,13 @@ int run_gemv_rs(q8_ctx *c, const q8_weight *w, float *y, q8_dptr x, const float 
 // which measured faster on the decode step's QKV and gate/up shapes) and
 // "gemv.group_loads".  False when no built variant fits: more than 16 waves, or a folded
 // norm without the 256 threads its reduction takes.
-bool rsg_shape(q8_ctx *c, int nb, int silu, bool norm, int *rs, int *nl, int *nw) {
-    const int rows = option(c, "gemv.group_rows", -1);
+// hot: a contiguous group (q8_gemv_hg*, q8_gemv_hs*), whose default is
+// 16-row slices: three loads a lane for a group, six for the SiLU pair
+// (its two slots share a workgroup); "gemv.group_rows" = 32 keeps the tile
+// kernel for it too.
+bool rsg_shape(q8_ctx *c, int nb, int silu, bool norm, int *rs, int *nl, int *nw, bool hot = false) {
+    int rows = option(c, "gemv.group_rows", -1);
+    if (hot && rows < 0) rows = 16;
     if (rows <= 0 || rows == 32) return false;  // default: the tile kernel (faster at the decode shapes)
     int r = rows;
     int l = option(c, "gemv.group_loads", -1);
@@ -565,7 +634,7 @@ bool rsg_shape(q8_ctx *c, int nb, int silu, bool norm, int *rs, int *nl, int *nw
     const int waves_slot = (int)ceil_div(nb, bpw);
     const int waves = waves_slot * (silu ? 2 : 1);
     if (waves > 16) return false;
-    if (norm && (waves * 64 < 256 || nb * 32 > 1024 * Q8_NORM_ROW_VEC)) return false;
+    if (norm && (waves * 64 < 256 || nb * 32 > 1024 * Q8_RSG_NORM_VEC)) return false;
     *rs = r;
     *nl = l;
     *nw = waves_slot;
@@ -611,7 +680,72 @@ int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const floa
         const int rc = run_gemv_rs(c, m[0].w, m[0].y, x, bias, t.row_slice, t.slice_loads, comb, t.exact);
         if (rc != Q8_ERR_UNSUPPORTED) return rc;
     }
-    int rs = 0, nl = 0, nw = 0;
+    int rs = 0, nl = 0, nw = 0, group_slices = 0;
+    if (silu && !comb && !amax && contiguous_group(c, m, count, &group_slices) && option(c, "gemv.group_pair", 1) &&
+        option(c, "gemv.group_rows", -1) < 0) {
+        // a contiguous gate/up pair: 16-row slices of 8 gate rows and the same
+        // 8 up rows (q8_gemv_hp16_*), from the pair's paired copy where it has one
+        const int pl = pair_loads(nb);
+        const int pw = pl ? (int)ceil_div(nb, 2 * pl) : 0;
+        const int total = m[0].w->tiles;
+        if (pl && (!norm_w || (pw * 64 >= 256 && nb * 32 <= 1024 * Q8_RSG_NORM_VEC)) && nb <= 0xffff &&
+            total <= 0x3fffffff) {
+            a.total_tiles = total;
+            a.x = reinterpret_cast<const float *>(x);
+            a.nb = nb;
+            a.waves_per_tile = pw;
+            a.silu_pair = 1;
+            a.kslices = 1;
+            a.norm_w = norm_w;
+            a.norm_eps = norm_eps;
+            a.xcd_order = option(c, "gemv.xcd_order", 1) ? 1 : 0;
+            const long long grid = (a.xcd_order ? ceil_div(total, 8) * 8 : (long long)total) * 4;
+            if (grid > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "gemv: grid of %lld workgroups", grid);
+            const unsigned lds =
+                (unsigned)((nb * 32 + (t.exact ? 16 * Q8_GEMV_VROW(nb) : pw * 16) + Q8_GEMV_PAD_FLOATS) * 4);
+            const Fn f = (Fn)((t.exact ? F_GEMV_HP16_3 : F_GEMV_HP16_3_E0) + (pl == 3 ? 0 : 1));
+            const bool sm = m[0].w->pair_slices && option(c, "gemv.slice_copy", 1);
+            RsgHead h{sm ? m[0].w->pair_slices : m[0].w->quants, m[0].w->scales, a.x, norm_w, nullptr, nb | (pw << 16),
+                      (int)((unsigned)total | ((unsigned)sm << 30) | ((unsigned)a.xcd_order << 31)), total, 0};
+            return launch_rsg(c, f, (unsigned)grid, (unsigned)(pw * 64), lds, h, a);
+        }
+    }
+    if ((count > 1 || silu) && !comb && !amax && contiguous_group(c, m, count, &group_slices) &&
+        rsg_shape(c, nb, silu, norm_w != nullptr, &rs, &nl, &nw, true)) {
+        // a contiguous group: the preloaded-head kernels, reading the group's
+        // slice-major copy where it has one of this height
+        const int total = silu ? m[0].w->tiles : tile;
+        if (nb > 0xffff || total > 0x3fffffff) return fail(Q8_ERR_UNSUPPORTED, "gemv: %d blocks a row", nb);
+        a.total_tiles = total;
+        a.x = reinterpret_cast<const float *>(x);
+        a.nb = nb;
+        a.waves_per_tile = nw;
+        a.silu_pair = silu;
+        a.kslices = 1;
+        a.norm_w = norm_w;
+        a.norm_eps = norm_eps;
+        if (rope) {
+            a.rope_pos = rope->position;
+            a.rope_freq = rope->freq;
+            a.kcache = rope->kcache;
+            a.vcache = rope->vcache;
+            a.head_dim = rope->head_dim;
+            a.n_rot = rope->n_rot;
+            a.capacity = rope->capacity;
+        }
+        a.xcd_order = option(c, "gemv.xcd_order", 1) ? 1 : 0;
+        const long long grid = (a.xcd_order ? ceil_div(total, 8) * 8 : (long long)total) * (Q8_TILE_ROWS / rs);
+        if (grid > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "gemv: grid of %lld workgroups", grid);
+        const unsigned lds = (unsigned)((nb * 32 + (t.exact ? slots * rs * Q8_GEMV_VROW(nb) : slots * nw * rs) +
+                                         Q8_GEMV_PAD_FLOATS) * 4);
+        const int vi = silu ? (rs == 8 ? 3 : 4) : (rs == 8 ? 0 : nl == 3 ? 1 : 2);
+        const Fn f = (Fn)((t.exact ? F_GEMV_HG8_3 : F_GEMV_HG8_3_E0) + vi);
+        const bool sm = group_slices == rs && option(c, "gemv.slice_copy", 1);
+        RsgHead h{sm ? m[0].w->slices : m[0].w->quants, m[0].w->scales, a.x, norm_w, a.rope_pos, nb | (nw << 16),
+                  (int)((unsigned)total | ((unsigned)sm << 30) | ((unsigned)a.xcd_order << 31)),
+                  silu ? m[0].w->tiles : 0, 0};
+        return launch_rsg(c, f, (unsigned)grid, (unsigned)(nw * slots * 64), lds, h, a);
+    }
     if ((count > 1 || silu) && !comb && rsg_shape(c, nb, silu, norm_w != nullptr, &rs, &nl, &nw)) {
         a.total_tiles = silu ? m[0].w->tiles : tile;
         a.x = reinterpret_cast<const float *>(x);
@@ -720,12 +854,13 @@ bool gemv_folds_combine(q8_ctx *c, const q8_weight *w, int splits) {
 // workgroup sees all of x), >= 256 threads (the row norm's reduction shape)
 // and k within the row norm's reach.
 bool gemv_folds_norm(q8_ctx *c, const Member *m, int count, int k, int silu) {
-    int rs = 0, nl = 0, nw = 0;
-    if ((count > 1 || silu) && rsg_shape(c, k / 32, silu, true, &rs, &nl, &nw)) return true;
+    int rs = 0, nl = 0, nw = 0, sl = 0;
     int rows_total = 0;
     for (int i = 0; i < count; i++) rows_total += m[i].w->out;
     const int slots = silu ? 2 : 1;
     const q8_tactic t = plan(c, 1, silu ? m[0].w->out : rows_total, k, slots);
+    if ((count > 1 || silu) && rsg_shape(c, k / 32, silu, true, &rs, &nl, &nw, contiguous_group(c, m, count, &sl)))
+        return true;
     const int pb = valid_pb(t.pairs_per_batch) ? t.pairs_per_batch : 5;
     const int waves = t.waves_per_tile * slots;
     return t.kslices == 1 && t.pairs_per_wave <= 12 && waves * 64 >= 256 && waves * 64 <= (pb == 9 ? 512 : 1024) &&
@@ -1248,10 +1383,15 @@ void q8_close(q8_ctx *c) {
     hipSetDevice(c->device);
     if (c->stream) hipStreamSynchronize(c->stream);
     q8i::noalloc_release(c);
-    for (auto &kv : c->weights) {
-        hipFree(kv.second->base);
-        delete kv.second;
-    }
+    // a group's allocation goes with its last member
+    auto drop = [](q8_weight *w) {
+        if (!w->group_refs || --*w->group_refs == 0) {
+            hipFree(w->base);
+            delete w->group_refs;
+        }
+        delete w;
+    };
+    for (auto &kv : c->weights) drop(kv.second);
     for (auto &kv : c->vectors) hipFree(kv.second);
     for (auto &kv : c->rope_freq) hipFree(kv.second);
     for (auto &kv : c->allocs) hipFree(reinterpret_cast<void *>(kv.first));
@@ -1261,10 +1401,7 @@ void q8_close(q8_ctx *c) {
     if (c->argmax_ws) hipFree(c->argmax_ws);
     if (c->split_ws) hipFree(c->split_ws);
     if (c->counters) hipFree(c->counters);
-    for (q8_weight *w : c->owned) {
-        hipFree(w->base);
-        delete w;
-    }
+    for (q8_weight *w : c->owned) drop(w);
     if (c->module) hipModuleUnload(c->module);
     if (c->stream) hipStreamDestroy(c->stream);
     delete c;
@@ -1300,7 +1437,7 @@ int q8_set_option(q8_ctx *c, const char *name, int value) {
                                         "gemm.pipe",  "gemm.lds",      "gemm.silu",      "gemm.small_gemv", "gemm.stream",
                                         "gemm.riders", "gemm.rider_nt", "gemm.rider_first", "gemm.next_riders",
                                         "gemm.next_rider_first", "gemm.rider_wave_kib", "gemm.prefetch",
-                                        "gemv.slice_copy"};
+                                        "gemv.slice_copy", "gemv.group_hot", "gemv.group_pair"};
     bool ok = false;
     for (const char *k : known) ok = ok || std::strcmp(k, name) == 0;
     if (!ok) return fail(Q8_ERR_INVALID, "unknown option %s", name);
@@ -1525,8 +1662,8 @@ WeightAlloc weight_alloc(q8_ctx *c, int out, int k, bool allow_slices = true) {
 }
 
 // The slice-major copy of repacked quants (enqueued on the context's stream).
-int slice_copy(q8_ctx *c, const uint8_t *quants, uint8_t *dst, int nb, int tiles, int rs) {
-    Q8SliceArgs a{quants, dst, nb, tiles, rs};
+int slice_copy(q8_ctx *c, const uint8_t *quants, uint8_t *dst, int nb, int tiles, int rs, int pair_tiles = 0) {
+    Q8SliceArgs a{quants, dst, nb, tiles, rs, pair_tiles};
     const long long threads = (long long)tiles * nb * 64;
     if (ceil_div(threads, 256) > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "weight of %d tiles is too large", tiles);
     return launch(c, F_SLICE_COPY, (unsigned)ceil_div(threads, 256), 256, 0, &a, sizeof a);
@@ -1595,6 +1732,18 @@ int q8_weight_resident(q8_ctx *c, const void *bytes, size_t nbytes, int k, int o
     return Q8_OK;
 }
 
+int q8_weight_group_resident(q8_ctx *c, int count, const void *const *bytes, const size_t *nbytes, int k,
+                             const int *outs, int pair, const q8_weight **weights) {
+    if (!c || !bytes || !nbytes || !outs || !weights || (pair != 0 && pair != 1))
+        return fail(Q8_ERR_INVALID, "q8_weight_group_resident: bad arguments");
+    if (count < 1 || count > Q8_GROUP_MAX) return fail(Q8_ERR_INVALID, "a weight group holds one to four matrices");
+    if (pair && (count != 2 || outs[0] != outs[1]))
+        return fail(Q8_ERR_INVALID, "a gate/up pair holds two matrices of one shape");
+    Q8_TRY(check_k(k));
+    const int slice_rows = pair ? q8i::group_pair_slices(c, k) : q8i::group_slice_rows(c, k, 0);
+    return build_group(c, k, count, outs, bytes, nbytes, nullptr, 0.0f, slice_rows, weights);
+}
+
 int q8_weight_release(q8_ctx *c, const q8_weight *w) {
     if (!c) return fail(Q8_ERR_INVALID, "q8_weight_release: null context");
     Q8_TRY(check_weight(c, w));
@@ -1605,7 +1754,11 @@ int q8_weight_release(q8_ctx *c, const q8_weight *w) {
     auto own = std::find(c->owned.begin(), c->owned.end(), w);
     if (own != c->owned.end()) {  // generated on the device
         HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-        hipFree(w->base);
+        // a group's allocation goes with its last member
+        if (!w->group_refs || --*w->group_refs == 0) {
+            hipFree(w->base);
+            delete w->group_refs;
+        }
         delete *own;
         c->owned.erase(own);
         return Q8_OK;
@@ -1613,7 +1766,10 @@ int q8_weight_release(q8_ctx *c, const q8_weight *w) {
     auto it = c->weights.find(std::make_pair(w->id_ptr, w->id_len));
     if (it == c->weights.end() || it->second != w) return fail(Q8_ERR_INVALID, "weight is not resident");
     HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-    hipFree(w->base);
+    if (!w->group_refs || --*w->group_refs == 0) {
+        hipFree(w->base);
+        delete w->group_refs;
+    }
     delete it->second;
     c->weights.erase(it);
     return Q8_OK;
@@ -2487,6 +2643,18 @@ int q8_attention_matmul_add(q8_ctx *c, q8_dptr q, size_t q_offset, q8_dptr kcach
 extern "C++" {
 namespace q8i {
 int attention_split_rows() { return attn_shape(2).rows; }
+int group_rows(q8_ctx *c, int k, int silu) {
+    int rs = 0, nl = 0, nw = 0;
+    if (!c || k < 32 || k % 32 || !option(c, "gemv.group_hot", 1)) return 0;
+    return rsg_shape(c, k / 32, silu, true, &rs, &nl, &nw, true) ? rs : 0;
+}
+int group_slice_rows(q8_ctx *c, int k, int silu) { return option(c, "gemv.slice_copy", 1) ? group_rows(c, k, silu) : 0; }
+int group_pair_slices(q8_ctx *c, int k) {
+    return (c && k >= 32 && k % 32 == 0 && option(c, "gemv.group_hot", 1) && option(c, "gemv.slice_copy", 1) &&
+            pair_loads(k / 32))
+               ? kGroupPairSlices
+               : 0;
+}
 }  // namespace q8i
 }
 
@@ -2554,6 +2722,137 @@ int q8i::weight_synthetic(q8_ctx *c, int k, int out, uint64_t seed, float scale_
     c->owned.push_back(w);
     *weight = w;
     return Q8_OK;
+}
+
+// Synthetic matrices of one K as a contiguous group: one allocation holds
+// every member's quants (their 32-row tiles back to back), then every
+// member's scales, then, with slice_rows 8 or 16, the slice-major copy of all
+// the tiles.  Each member is a weight of its own (the same bytes as
+// q8_weight_synthetic with its seed) whose pointers lie inside the group's
+// allocation; the allocation is freed with the last member released.  A
+// decode group or gate/up pair of such members runs the contiguous-group
+// row-slice GEMVs.
+namespace {
+
+// One contiguous group of `count` matrices of one k: one allocation holding
+// every member's quants (tiles back to back), then every member's scales,
+// then the slice-major copy of all the tiles (slice_rows 8 or 16) or a
+// gate/up pair's paired copy (kPairSlices).  Member i's GGUF bytes come from
+// the host (bytes[i]) or are synthesized on the device (seeds[i]).  Resident
+// members are cached by host identity, synthetic ones owned by the context.
+int build_group(q8_ctx *c, int k, int count, const int *outs, const void *const *bytes, const size_t *nbytes,
+                const uint64_t *seeds, float scale_std, int slice_rows, const q8_weight **weights) {
+    if (count < 1 || count > Q8_GROUP_MAX) return fail(Q8_ERR_INVALID, "a weight group holds one to four matrices");
+    const bool pair = slice_rows == kPairSlices;
+    if (pair && (count != 2 || outs[0] != outs[1]))
+        return fail(Q8_ERR_INVALID, "weight group: a paired copy belongs to a gate/up pair of one shape");
+    if (pair) slice_rows = 16;
+    if (slice_rows != 0 && slice_rows != 8 && slice_rows != 16)
+        return fail(Q8_ERR_INVALID, "weight group: slice rows %d (0, 8 or 16)", slice_rows);
+    Q8_TRY(check_k(k));
+    const int nb = k / 32;
+    int total_tiles = 0, most_rows = 0;
+    for (int i = 0; i < count; i++) {
+        if (outs[i] <= 0) return fail(Q8_ERR_INVALID, "weight has %d rows", outs[i]);
+        if (bytes) {
+            if (!bytes[i]) return fail(Q8_ERR_INVALID, "weight group: member %d has no bytes", i);
+            if (nbytes[i] != (size_t)outs[i] * nb * Q8_BLOCK_BYTES)
+                return fail(Q8_ERR_INVALID, "weight byte length mismatch: %zu bytes for %d x %d Q8_0", nbytes[i],
+                            outs[i], k);
+            for (int j2 = 0; j2 < i; j2++)
+                if (bytes[j2] == bytes[i] && nbytes[j2] == nbytes[i])
+                    return fail(Q8_ERR_INVALID, "weight group: member %d repeats member %d", i, j2);
+        }
+        total_tiles += (int)ceil_div(outs[i], Q8_TILE_ROWS);
+        most_rows = std::max(most_rows, outs[i]);
+    }
+    const long long threads = (long long)total_tiles * Q8_TILE_ROWS * nb;
+    if (threads > 0x7fffffffLL) return fail(Q8_ERR_UNSUPPORTED, "weight group of %lld blocks is too large", threads);
+    std::lock_guard<std::recursive_mutex> lock(c->mu);
+    if (bytes) {
+        for (int i = 0; i < count; i++)
+            if (c->weights.count(std::make_pair((uintptr_t)bytes[i], nbytes[i])))
+                return fail(Q8_ERR_INVALID, "weight group: member %d is already resident", i);
+    }
+    HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+    const size_t qbytes = (size_t)total_tiles * nb * Q8_UNIT_BYTES;
+    const size_t sbytes = (size_t)total_tiles * nb * Q8_TILE_ROWS * 2;
+    const size_t slices_off = align_up(align_up(qbytes, kAlign) + sbytes, kAlign);
+    const size_t total = slice_rows ? slices_off + qbytes : align_up(qbytes, kAlign) + sbytes;
+    void *base = nullptr, *staging = nullptr;
+    HIP_TRY(dev_malloc(c, &base, total), "hipMalloc(weight group)");
+    hipError_t e = dev_malloc(c, &staging, (size_t)most_rows * nb * Q8_BLOCK_BYTES);
+    if (e != hipSuccess) {
+        hipFree(base);
+        return hip_fail(e, "hipMalloc(weight staging)");
+    }
+    uint8_t *quants = static_cast<uint8_t *>(base);
+    uint16_t *scales = reinterpret_cast<uint16_t *>(quants + align_up(qbytes, kAlign));
+    int rc = Q8_OK;
+    int t0 = 0;
+    for (int i = 0; i < count && rc == Q8_OK; i++) {
+        const int tiles = (int)ceil_div(outs[i], Q8_TILE_ROWS);
+        if (bytes) {
+            e = hipMemcpyAsync(staging, bytes[i], nbytes[i], hipMemcpyHostToDevice, c->stream);
+            if (e != hipSuccess) rc = hip_fail(e, "hipMemcpyAsync(weight)");
+        } else {
+            Q8SynthArgs sa{static_cast<uint8_t *>(staging), (long long)outs[i] * nb, seeds[i], scale_std};
+            rc = launch(c, F_SYNTH, (unsigned)std::min<long long>(ceil_div(sa.blocks, 256), 65536), 256, 0, &sa,
+                        sizeof sa);
+        }
+        Q8RepackArgs a{};
+        a.src = static_cast<const uint8_t *>(staging);
+        a.quants = quants + (size_t)t0 * nb * Q8_UNIT_BYTES;
+        a.scales = scales + (size_t)t0 * nb * Q8_TILE_ROWS;
+        a.rows = outs[i];
+        a.nb = nb;
+        a.tiles = tiles;
+        a.inverse = 0;
+        const long long th = (long long)tiles * Q8_TILE_ROWS * nb;
+        if (rc == Q8_OK) rc = launch(c, F_REPACK, (unsigned)ceil_div(th, 256), 256, 0, &a, sizeof a);
+        t0 += tiles;
+    }
+    uint8_t *slices = slice_rows ? quants + slices_off : nullptr;
+    if (rc == Q8_OK && slices)
+        rc = slice_copy(c, quants, slices, nb, total_tiles, slice_rows, pair ? total_tiles / 2 : 0);
+    if (rc == Q8_OK) {  // the staging buffer is reused member by member and freed below
+        e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) rc = hip_fail(e, "hipStreamSynchronize");
+    }
+    hipFree(staging);
+    if (rc != Q8_OK) {
+        hipFree(base);
+        return rc;
+    }
+    int *refs = new int(count);
+    t0 = 0;
+    for (int i = 0; i < count; i++) {
+        const int tiles = (int)ceil_div(outs[i], Q8_TILE_ROWS);
+        const size_t off = (size_t)t0 * nb;
+        q8_weight *w = new q8_weight{c, base, quants + off * Q8_UNIT_BYTES, scales + off * Q8_TILE_ROWS, k, outs[i],
+                                     nb, tiles, total, bytes ? (uintptr_t)bytes[i] : 0, bytes ? nbytes[i] : 0};
+        // a paired copy serves the pair's launch only (the gate holds it); a
+        // member alone reads the unit layout
+        w->slices = (slices && !pair) ? slices + off * Q8_UNIT_BYTES : nullptr;
+        w->slice_rows = (slices && !pair) ? slice_rows : 0;
+        w->pair_slices = (pair && i == 0) ? slices : nullptr;
+        w->group_refs = refs;
+        if (bytes)
+            c->weights[std::make_pair(w->id_ptr, w->id_len)] = w;
+        else
+            c->owned.push_back(w);
+        weights[i] = w;
+        t0 += tiles;
+    }
+    return Q8_OK;
+}
+
+}  // namespace
+
+int q8i::weight_synthetic_group(q8_ctx *c, int k, int count, const int *outs, const uint64_t *seeds, float scale_std,
+                                int slice_rows, const q8_weight **weights) {
+    if (!c || !outs || !seeds || !weights) return fail(Q8_ERR_INVALID, "weight group: bad arguments");
+    return build_group(c, k, count, outs, nullptr, nullptr, seeds, scale_std, slice_rows, weights);
 }
 
 extern "C" {

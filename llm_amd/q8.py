@@ -44,7 +44,7 @@ EXPORTS = (
     "q8_status_string", "q8_last_error", "q8_build_info",
     "q8_open", "q8_close", "q8_device_name", "q8_device_info", "q8_stream", "q8_set_option",
     "q8_alloc", "q8_free", "q8_upload", "q8_download", "q8_sync",
-    "q8_weight_resident", "q8_weight_release", "q8_weight_shape", "q8_weight_export",
+    "q8_weight_resident", "q8_weight_group_resident", "q8_weight_release", "q8_weight_shape", "q8_weight_export",
     "q8_matmul", "q8_matmul_noalloc", "q8_matmul_q8", "q8_prepare", "q8_silu_mul_prepare", "q8_rmsnorm",
     "q8_norm_prepare", "q8_silu_mul",
     "q8_matmul_decode_group", "q8_matmul_prompt_group", "q8_gate_up_silu", "q8_gate_up_silu_prepared",
@@ -58,7 +58,7 @@ EXPORTS = (
     "q8_gguf_meta_f32", "q8_gguf_meta_bool", "q8_gguf_meta_str", "q8_gguf_has_key_prefix",
     "q8_gguf_meta_i32_array", "q8_gguf_meta_f32_array", "q8_gguf_meta_str_array", "q8_gguf_weight",
     "q8_rope_append", "q8_attention", "q8_attention_prepare", "q8_attention_matmul_add", "q8_prompt_qkv_rope", "q8_embeddings_device", "q8_argmax_device", "q8_advance_position",
-    "q8_norm_matmul_decode_group", "q8_norm_gate_up_silu", 
+    "q8_norm_matmul_decode_group", "q8_norm_gate_up_silu",
     "q8_vector_release", "q8_norm_qkv_rope",
     "q8_weight_synthetic", "q8_decoder_create_synthetic", "q8_decoder_destroy", "q8_decoder_reset",
     "q8_decoder_position", "q8_decoder_forward", "q8_decoder_generate", "q8_decoder_logits", "q8_decoder_weight",
@@ -196,6 +196,8 @@ def lib():
         "q8_download": (c_int, [vp, vp, u64, c_size]),
         "q8_sync": (c_int, [vp]),
         "q8_weight_resident": (c_int, [vp, vp, c_size, c_int, c_int, ctypes.POINTER(vp)]),
+        "q8_weight_group_resident": (c_int, [vp, c_int, ctypes.POINTER(vp), ctypes.POINTER(c_size), c_int,
+                                             ctypes.POINTER(c_int), c_int, ctypes.POINTER(vp)]),
         "q8_weight_release": (c_int, [vp, vp]),
         "q8_weight_shape": (c_int, [vp, ctypes.POINTER(c_int), ctypes.POINTER(c_int), ctypes.POINTER(c_size)]),
         "q8_weight_export": (c_int, [vp, vp, vp, c_size]),
@@ -455,6 +457,19 @@ class Gpu:
                                         weight.k, weight.out, ctypes.byref(h)))
         self._resident[weight.identity()] = weight  # keep the host bytes alive
         return h.value
+
+    def resident_group(self, weights, pair: bool = False):
+        """q8_weight_group_resident: the weights (one k) as one contiguous
+        group, each then resident on its own identity; pair = a gate/up pair."""
+        n = len(weights)
+        ptrs = (ctypes.c_void_p * n)(*[w.data.ctypes.data for w in weights])
+        sizes = (ctypes.c_size_t * n)(*[w.data.nbytes for w in weights])
+        outs = (ctypes.c_int * n)(*[w.out for w in weights])
+        hs = (ctypes.c_void_p * n)()
+        _check(lib().q8_weight_group_resident(self.handle, n, ptrs, sizes, weights[0].k, outs, int(pair), hs))
+        for w in weights:
+            self._resident[w.identity()] = w
+        return list(hs)
 
     def release(self, weight: Weight):
         h = self.resident(weight)

@@ -191,6 +191,10 @@ ARG_STRUCTS = {  # kernel name prefix -> the argument struct every kernel of tha
     # ints, 56 bytes with padding), then the GEMV argument block
     "q8_gemv_r8_": "head + Q8GemvArgs", "q8_gemv_r16_": "head + Q8GemvArgs", "q8_gemv_rc": "head + Q8GemvArgs",
     "q8_gemv_q8x": "head + Q8GemvArgs",
+    # the contiguous-group row-slice GEMVs: their own 56-byte head (five
+    # pointers, four ints), then the same block
+    "q8_gemv_hg": "head + Q8GemvArgs", "q8_gemv_hs": "head + Q8GemvArgs",
+    "q8_gemv_hp": "head + Q8GemvArgs",
     # the decode attention: a preloadable head (five pointers, three ints, 56 bytes), then its block
     "q8_attn_decode": "head + Q8AttnDecodeArgs",
     "q8_gemm_": "Q8GemmArgs", "q8_gemv": "Q8GemvArgs", "q8_quantize": "Q8QuantArgs", "q8_rmsnorm": "Q8NormArgs",
@@ -219,6 +223,8 @@ def test_every_kernel_carries_its_metadata():
     assert sizes["head + Q8GemvArgs"] == {56 + min(sizes["Q8GemvArgs"])}, "the row-slice head is 56 bytes"
     assert len([n for n in info["kernels"]
                 if n.startswith(("q8_gemv_r8_", "q8_gemv_r16_", "q8_gemv_rc", "q8_gemv_q8x"))]) == 30
+    assert len([n for n in info["kernels"] if n.startswith(("q8_gemv_hg", "q8_gemv_hs"))]) == 10
+    assert len([n for n in info["kernels"] if n.startswith("q8_gemv_hp")]) == 4
     with pytest.raises(q8.Q8Error) as e:
         q8.kernel_info("q8_no_such_kernel")
     assert e.value.status == q8.Q8_ERR_INVALID
