@@ -491,7 +491,11 @@ def bench_decode_layer(gpu, steps, warmup, rng):
     copies = copies_for(wbytes)
     layers = [base] + [[q8.Weight(w.data.copy(), w.k, w.out) for w in base] for _ in range(copies - 1)]
     for L in layers:
-        for w in L:
+        # q/k/v and gate/up as contiguous groups (q8_weight_group_resident),
+        # as a decoder keeps them; O and down alone
+        gpu.resident_group(L[0:3])
+        gpu.resident_group(L[4:6], pair=True)
+        for w in (L[3], L[6]):
             gpu.resident(w)
     x = rng.standard_normal(HID, dtype=np.float32)
     xb, qkv, hb, act = gpu.alloc(4 * HID), gpu.alloc(4 * 3 * HID), gpu.alloc(4 * HID), gpu.alloc(4 * FFN)

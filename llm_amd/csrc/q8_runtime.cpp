@@ -1650,8 +1650,9 @@ WeightAlloc weight_alloc(q8_ctx *c, int out, int k, bool allow_slices = true) {
     const int tiles = (int)ceil_div(out, Q8_TILE_ROWS);
     wa.qbytes = (size_t)tiles * nb * Q8_UNIT_BYTES;
     wa.sbytes = (size_t)tiles * nb * Q8_TILE_ROWS * 2;
-    q8_tactic t{};
-    q8_gemv_shape(out, k, c->cu_count, 1, &t);
+    // the slice height this context's one-token GEMV of the shape runs in
+    // (options gemv.rows / gemv.loads included, as they stand at residency)
+    const q8_tactic t = plan(c, 1, out, k);
     // option gemv.slice_copy = 0: no copy (a context whose weights only ever
     // run in groups or GEMMs saves the memory)
     wa.slice_rows =

@@ -97,15 +97,17 @@ CASES = [("qkv_rope", (2304, 2304, 2304), 2304), ("qkv_rope", (256, 128, 128), 2
          ("norm_gate_up", (2304, 2304), 5760)]
 
 
-@pytest.mark.parametrize("kind,outs,k", CASES)
-@pytest.mark.parametrize("variant", ["default", "unit_layout", "no_pair"])
+# no_pair concerns gate/up pairs only
+VARIANTS = [(kind, outs, k, v) for kind, outs, k in CASES for v in ("default", "unit_layout", "no_pair")
+            if v != "no_pair" or kind in ("gate_up", "norm_gate_up")]
+
+
+@pytest.mark.parametrize("kind,outs,k,variant", VARIANTS)
 @pytest.mark.parametrize("exact", [1, 0])
 def test_contiguous_group_equals_separate_weights(gpu, kind, outs, k, variant, exact):
     """unit_layout: the group built with gemv.slice_copy = 0 (its kernels read
     the unit layout); no_pair: a gate/up pair with gemv.group_pair = 0 (the
     two-slot row slices)."""
-    if variant == "no_pair" and kind not in ("gate_up", "norm_gate_up"):
-        pytest.skip("gemv.group_pair only concerns gate/up pairs")
     r = np.random.default_rng(SEED + sum(outs) + k + len(kind))
     datas = [oracle.make_q8_weight(r, o, k) for o in outs]
     sep = [q8.Weight(d.copy(), k, o) for d, o in zip(datas, outs)]
