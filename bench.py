@@ -622,20 +622,22 @@ def bench_decode_chain(gpu, steps=20, visible=600, splits=3):
     """configs[4]'s decode step as its op chain launched eagerly (no graph): the
     same calls q8_decoder_generate's captured step makes, for a kernel trace
     (a kernel trace of the captured step itself aborted on the host; the
-    eager chain runs the same kernels, arguments and launch shapes).  Weights
-    generated on the device; returns the host time per step."""
+    eager chain runs the same kernels, arguments and launch shapes).  The
+    weights are a synthetic decoder's (generated on the device, q/k/v and
+    gate/up as its contiguous groups); returns the host time per step."""
+    from llm_amd import decoder as dm
     heads, hd, cap, n_layer = 36, 64, 4096, 42
     rng = np.random.default_rng(5)
-    names = (("q", HID, HID), ("k", HID, HID), ("v", HID, HID), ("o", HID, HID), ("g", HID, FFN), ("u", HID, FFN),
-             ("d", FFN, HID))
+    dec = dm.Decoder(gpu, dm.config(n_layer=n_layer, n_embd=HID, n_ff=FFN, n_head=heads, head_dim=hd, n_vocab=VOCAB,
+                                    capacity=8, max_batch=1, untied_output=1), seed=5)
     layers = []
     for li in range(n_layer):
-        w = {n: gpu.weight_synthetic(k, out, 1000 * li + i) for i, (n, k, out) in enumerate(names)}
+        w = {n: dec.weight(li, i) for i, n in enumerate("qkvogud")}
         w["an"] = (1.0 + 0.1 * rng.standard_normal(HID)).astype(np.float32)
         w["fn"] = (1.0 + 0.1 * rng.standard_normal(HID)).astype(np.float32)
         w["kc"], w["vc"] = gpu.alloc(2 * cap * HID), gpu.alloc(2 * cap * HID)
         layers.append(w)
-    head = gpu.weight_synthetic(HID, VOCAB, 77)
+    head = dec.weight(-1, dm.OUTPUT)
     onorm = (1.0 + 0.1 * rng.standard_normal(HID)).astype(np.float32)
     x, q, act = gpu.alloc(4 * HID), gpu.alloc(4 * HID), gpu.alloc(4 * FFN)
     logits, tok, pos = gpu.alloc(4 * VOCAB), gpu.alloc(4), gpu.alloc(4)
@@ -655,11 +657,9 @@ def bench_decode_chain(gpu, steps=20, visible=600, splits=3):
     ms = (time.perf_counter() - t0) * 1e3 / steps
     log(f"decode op chain, eager: {ms:.3f} ms a step (host clock; {steps} steps at {visible} positions)")
     for w in layers:
-        for n, _, _ in names:
-            gpu.release_device(w[n])
         w["kc"].free()
         w["vc"].free()
-    gpu.release_device(head)
+    dec.close()
     for b in (x, q, act, logits, tok, pos):
         b.free()
     return {"ms_per_step_host": round(ms, 3), "steps": steps, "visible": visible, "splits": splits}
