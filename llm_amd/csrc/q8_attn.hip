@@ -319,6 +319,10 @@ extern "C" __global__ __launch_bounds__(1024) void q8_attn_decode(Q8_ATTN_PARAMS
 extern "C" __global__ __launch_bounds__(256) void q8_attn_decode_w4(Q8_ATTN_PARAMS) {
     attn_decode_body<4, 8>(AttnHead{q, kcache, vcache, position, part_acc, dims, splits, cap}, a);
 }
+// The split kernel's 256-row chunks over eight waves: four rows a lane instead of eight.
+extern "C" __global__ __launch_bounds__(512) void q8_attn_decode_w8(Q8_ATTN_PARAMS) {
+    attn_decode_body<8, 4>(AttnHead{q, kcache, vcache, position, part_acc, dims, splits, cap}, a);
+}
 
 // ---------------------------------------------------------------------------
 // Prefill attention: n query tokens at cache positions start .. start+n-1, each

@@ -97,6 +97,7 @@ enum Fn {
     F_GEMV_HG8_3, F_GEMV_HG16_3, F_GEMV_HG16_6, F_GEMV_HS8_3, F_GEMV_HS16_6,
     F_GEMV_HG8_3_E0, F_GEMV_HG16_3_E0, F_GEMV_HG16_6_E0, F_GEMV_HS8_3_E0, F_GEMV_HS16_6_E0,
     F_GEMV_HP16_3, F_GEMV_HP16_6, F_GEMV_HP16_3_E0, F_GEMV_HP16_6_E0,
+    F_ATTN_DECODE_W8,
     F_COUNT
 };
 
@@ -135,6 +136,7 @@ const char *const kFnNames[F_COUNT] = {
     "q8_gemv_hg8_l3", "q8_gemv_hg16_l3", "q8_gemv_hg16_l6", "q8_gemv_hs8_l3", "q8_gemv_hs16_l6",
     "q8_gemv_hg8_l3_e0", "q8_gemv_hg16_l3_e0", "q8_gemv_hg16_l6_e0", "q8_gemv_hs8_l3_e0", "q8_gemv_hs16_l6_e0",
     "q8_gemv_hp16_l3", "q8_gemv_hp16_l6", "q8_gemv_hp16_l3_e0", "q8_gemv_hp16_l6_e0",
+    "q8_attn_decode_w8",
 };
 
 // Every kernel of the code object with its metadata (q8_manifest.h, from the
@@ -1437,7 +1439,7 @@ int q8_set_option(q8_ctx *c, const char *name, int value) {
                                         "gemm.pipe",  "gemm.lds",      "gemm.silu",      "gemm.small_gemv", "gemm.stream",
                                         "gemm.riders", "gemm.rider_nt", "gemm.rider_first", "gemm.next_riders",
                                         "gemm.next_rider_first", "gemm.rider_wave_kib", "gemm.prefetch",
-                                        "gemv.slice_copy", "gemv.group_hot", "gemv.group_pair"};
+                                        "gemv.slice_copy", "gemv.group_hot", "gemv.group_pair", "attn.waves"};
     bool ok = false;
     for (const char *k : known) ok = ok || std::strcmp(k, name) == 0;
     if (!ok) return fail(Q8_ERR_INVALID, "unknown option %s", name);
@@ -1449,6 +1451,8 @@ int q8_set_option(q8_ctx *c, const char *name, int value) {
         return fail(Q8_ERR_INVALID, "gemv.loads must be 2 (8-row slices), 3 or 6");
     if (std::strcmp(name, "gemv.group_rows") == 0 && value > 0 && value != 8 && value != 16 && value != 32)
         return fail(Q8_ERR_INVALID, "gemv.group_rows must be 0 or 32 (the tile kernel), 8 or 16");
+    if (std::strcmp(name, "attn.waves") == 0 && value >= 0 && value != 4 && value != 8)
+        return fail(Q8_ERR_INVALID, "attn.waves must be 4 or 8 (the split attention's waves a workgroup)");
     if (std::strcmp(name, "gemv.group_loads") == 0 && value > 0 && value != 3 && value != 6)
         return fail(Q8_ERR_INVALID, "gemv.group_loads must be 3 or 6");
     std::lock_guard<std::recursive_mutex> lock(c->mu);
@@ -2480,8 +2484,16 @@ struct AttnShape {
     unsigned threads;
     int rows;  // positions per chunk
 };
-AttnShape attn_shape(int splits) {
+// With splits, the 256-row chunks run on eight waves (four rows a lane) while
+// the launch's workgroups fit one per CU, else on four: configs[4] decode,
+// attention + O at 600 positions 8.77 -> 8.53 us (3 splits), 2400 positions
+// 13.62 -> 12.69 us (5), but 4000 positions 18.02 -> 19.13 us (8 splits:
+// 288 workgroups, the heavier ones' second round); option "attn.waves"
+// = 4 or 8 forces one.
+AttnShape attn_shape(int splits, q8_ctx *c = nullptr, int n_head = 0) {
     if (splits == 1) return {F_ATTN_DECODE, 1024, 1024};
+    const int w = c ? option(c, "attn.waves", -1) : 4;
+    if (w == 8 || (w < 0 && (long long)n_head * splits <= c->cu_count)) return {F_ATTN_DECODE_W8, 512, 256};
     return {F_ATTN_DECODE_W4, 256, 256};
 }
 
@@ -2512,7 +2524,7 @@ int run_attn_decode(q8_ctx *c, const float *q, q8_dptr kcache, q8_dptr vcache, f
     a.capacity = capacity;
     a.scale = scale;
     a.defer = defer;
-    const AttnShape sh = attn_shape(splits);
+    const AttnShape sh = attn_shape(splits, c, n_head);
     if (n_head > 0xffff || n_kv > 0xffff)
         return fail(Q8_ERR_UNSUPPORTED, "attention: %d heads, %d key/value heads", n_head, n_kv);
     // the kernel's preloaded head, then the argument block (scale, out, counters)

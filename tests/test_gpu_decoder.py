@@ -380,9 +380,18 @@ def cache_pair(gpu, r, L, capacity, n_kv, hd=64):
     return k.astype(np.float32), v.astype(np.float32), kc, vc
 
 
-@pytest.mark.parametrize("visible,splits,n_head,n_kv", [(1, 1, 4, 2), (200, 1, 4, 2), (200, 3, 4, 4), (200, 7, 8, 2),
-                                                        (640, 10, 36, 36), (4096, 16, 4, 1)])
-def test_decode_attention_matches_the_oracle(gpu, visible, splits, n_head, n_kv):
+ATTN_CASES = [(1, 1, 4, 2), (200, 1, 4, 2), (200, 3, 4, 4), (200, 7, 8, 2), (640, 10, 36, 36), (4096, 16, 4, 1),
+              (600, 3, 36, 36), (2400, 5, 36, 36)]
+
+
+# waves: option attn.waves (-1 the default choice; 4 or 8 forced on the split kernel)
+@pytest.mark.parametrize("visible,splits,n_head,n_kv,waves",
+                         [c + (w,) for c in ATTN_CASES for w in (-1, 4, 8) if w < 0 or c[1] > 1])
+def test_decode_attention_matches_the_oracle(gpu, visible, splits, n_head, n_kv, waves):
+    """The split kernel's 256-row chunks over four or eight waves (by default
+    eight while heads x splits workgroups fit one per CU) and the one-split
+    16-wave kernel, against the exact attention formula."""
+    gpu.set_option("attn.waves", waves)
     r = np.random.default_rng(SEED + visible + splits)
     capacity = max(visible, 256)
     kf, vf, kc, vc = cache_pair(gpu, r, visible, capacity, n_kv)
@@ -391,8 +400,11 @@ def test_decode_attention_matches_the_oracle(gpu, visible, splits, n_head, n_kv)
     qb.upload(q)
     pos = int_buffer(gpu, visible - 1)
     print(f"\ndecode attention visible={visible} splits={splits} heads={n_head}/{n_kv}", flush=True)
-    gpu.attention(qb, kc, vc, out, 1, n_head, n_kv, 64, capacity, 0.125, pos, splits)
-    got = out.download(np.float32, q.size).reshape(q.shape)
+    try:
+        gpu.attention(qb, kc, vc, out, 1, n_head, n_kv, 64, capacity, 0.125, pos, splits)
+        got = out.download(np.float32, q.size).reshape(q.shape)
+    finally:
+        gpu.set_option("attn.waves", -1)
     assert_close(got, oracle.attention(q, kf, vf, visible - 1, 0.125), f"decode attention L={visible} s={splits}")
 
 
