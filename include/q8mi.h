@@ -231,6 +231,8 @@ int q8_weight_resident(q8_ctx *ctx, const void *gguf_bytes, size_t nbytes, int k
 int q8_weight_group_resident(q8_ctx *ctx, int count, const void *const *bytes, const size_t *nbytes, int k,
                              const int *outs, int pair, const q8_weight **weights);
 int q8_weight_release(q8_ctx *ctx, const q8_weight *weight);
+/* k, rows, and the bytes of the device allocation holding the weight (for a
+ * member of a contiguous group: the group's whole allocation). */
 int q8_weight_shape(const q8_weight *weight, int *k, int *out, size_t *device_bytes);
 /* Writes the resident weight back as GGUF bytes (inverse repack), so the
  * device layout can be checked byte-exactly against the upload. */
