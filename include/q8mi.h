@@ -153,7 +153,10 @@ void *q8_stream(q8_ctx *ctx);
  * the results are the same bits either way), "gemv.group_hot" (0: the tile
  * kernels for contiguous groups too), "gemv.group_pair" (0: a contiguous
  * gate/up pair takes the two-slot row-slice kernel instead of its paired
- * slices), "gemv.slice_copy" (0, set before residency: no slice-major copies),
+ * slices), "gemv.pair_loads" (3 or 6: the paired slices' loads a lane, so
+ * K / 32 / (2 * loads) waves a workgroup; by default 3 up to 96 blocks a row,
+ * else 6; a value that would need more than 16 waves is ignored),
+ * "gemv.slice_copy" (0, set before residency: no slice-major copies),
  * "attn.waves" (4 or 8: the split decode attention's waves a workgroup; by
  * default 8 while the heads x splits workgroups fit one per CU, else 4). */
 int q8_set_option(q8_ctx *ctx, const char *name, int value);

@@ -687,7 +687,9 @@ int run_gemv(q8_ctx *c, const Member *m, int count, q8_dptr x, int k, const floa
         option(c, "gemv.group_rows", -1) < 0) {
         // a contiguous gate/up pair: 16-row slices of 8 gate rows and the same
         // 8 up rows (q8_gemv_hp16_*), from the pair's paired copy where it has one
-        const int pl = pair_loads(nb);
+        int pl = pair_loads(nb);
+        const int po = option(c, "gemv.pair_loads", -1);
+        if (pl && po > 0 && ceil_div(nb, 2 * po) <= 16) pl = po;
         const int pw = pl ? (int)ceil_div(nb, 2 * pl) : 0;
         const int total = m[0].w->tiles;
         if (pl && (!norm_w || (pw * 64 >= 256 && nb * 32 <= 1024 * Q8_RSG_NORM_VEC)) && nb <= 0xffff &&
@@ -1439,7 +1441,8 @@ int q8_set_option(q8_ctx *c, const char *name, int value) {
                                         "gemm.pipe",  "gemm.lds",      "gemm.silu",      "gemm.small_gemv", "gemm.stream",
                                         "gemm.riders", "gemm.rider_nt", "gemm.rider_first", "gemm.next_riders",
                                         "gemm.next_rider_first", "gemm.rider_wave_kib", "gemm.prefetch",
-                                        "gemv.slice_copy", "gemv.group_hot", "gemv.group_pair", "attn.waves"};
+                                        "gemv.slice_copy", "gemv.group_hot", "gemv.group_pair", "gemv.pair_loads",
+                                        "attn.waves"};
     bool ok = false;
     for (const char *k : known) ok = ok || std::strcmp(k, name) == 0;
     if (!ok) return fail(Q8_ERR_INVALID, "unknown option %s", name);
@@ -1453,6 +1456,8 @@ int q8_set_option(q8_ctx *c, const char *name, int value) {
         return fail(Q8_ERR_INVALID, "gemv.group_rows must be 0 or 32 (the tile kernel), 8 or 16");
     if (std::strcmp(name, "attn.waves") == 0 && value >= 0 && value != 4 && value != 8)
         return fail(Q8_ERR_INVALID, "attn.waves must be 4 or 8 (the split attention's waves a workgroup)");
+    if (std::strcmp(name, "gemv.pair_loads") == 0 && value > 0 && value != 3 && value != 6)
+        return fail(Q8_ERR_INVALID, "gemv.pair_loads must be 3 or 6");
     if (std::strcmp(name, "gemv.group_loads") == 0 && value > 0 && value != 3 && value != 6)
         return fail(Q8_ERR_INVALID, "gemv.group_loads must be 3 or 6");
     std::lock_guard<std::recursive_mutex> lock(c->mu);

@@ -97,9 +97,10 @@ CASES = [("qkv_rope", (2304, 2304, 2304), 2304), ("qkv_rope", (256, 128, 128), 2
          ("norm_gate_up", (2304, 2304), 5760)]
 
 
-# no_pair concerns gate/up pairs only
-VARIANTS = [(kind, outs, k, v) for kind, outs, k in CASES for v in ("default", "unit_layout", "no_pair")
-            if v != "no_pair" or kind in ("gate_up", "norm_gate_up")]
+# no_pair and pair_l6 / pair_l3 concern gate/up pairs only
+VARIANTS = [(kind, outs, k, v) for kind, outs, k in CASES
+            for v in ("default", "unit_layout", "no_pair", "pair_l6", "pair_l3")
+            if v in ("default", "unit_layout") or kind in ("gate_up", "norm_gate_up")]
 
 
 @pytest.mark.parametrize("kind,outs,k,variant", VARIANTS)
@@ -107,7 +108,9 @@ VARIANTS = [(kind, outs, k, v) for kind, outs, k in CASES for v in ("default", "
 def test_contiguous_group_equals_separate_weights(gpu, kind, outs, k, variant, exact):
     """unit_layout: the group built with gemv.slice_copy = 0 (its kernels read
     the unit layout); no_pair: a gate/up pair with gemv.group_pair = 0 (the
-    two-slot row slices)."""
+    two-slot row slices); pair_l6 / pair_l3: the paired slices with six or
+    three loads a lane (gemv.pair_loads; three where K needs no more than 16
+    waves, else the default)."""
     r = np.random.default_rng(SEED + sum(outs) + k + len(kind))
     datas = [oracle.make_q8_weight(r, o, k) for o in outs]
     sep = [q8.Weight(d.copy(), k, o) for d, o in zip(datas, outs)]
@@ -143,6 +146,8 @@ def test_contiguous_group_equals_separate_weights(gpu, kind, outs, k, variant, e
         gpu.set_option("gemv.slice_copy", -1)
         if variant == "no_pair":
             gpu.set_option("gemv.group_pair", 0)
+        if variant.startswith("pair_l"):
+            gpu.set_option("gemv.pair_loads", int(variant[-1]))
         gpu.set_option("gemv.exact", exact)
         runs = []
         for _ in range(2):
@@ -184,7 +189,7 @@ def test_contiguous_group_equals_separate_weights(gpu, kind, outs, k, variant, e
                 assert_reordered(runs[0][0][i], oracle.matmul(d, k, o, xo, 1).reshape(-1), bounds[i],
                                  f"{kind} member {i} vs oracle")
     finally:
-        for name in ("gemv.exact", "gemv.group_pair", "gemv.slice_copy"):
+        for name in ("gemv.exact", "gemv.group_pair", "gemv.slice_copy", "gemv.pair_loads"):
             gpu.set_option(name, -1)
         for b in [xb] + ys + [c for c in caches if c is not None] + ([pos] if pos else []):
             b.free()
